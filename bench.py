@@ -1,0 +1,250 @@
+"""Benchmark of the fused mHC forward on one MI355X.
+
+Workload: 16384 tokens (B=16, T=1024), n=4 streams,
+C=768, bf16 streams with fp32 accumulation, phi [3072, 24] ~ N(0, 0.02),
+alpha 0.01, biases 0 / I, Sinkhorn 20 iterations, F replaced by a fixed
+seeded N(0, 1) tensor [16384, 768].  One step = the two kernels of one mHC
+connection: the fused pre phase (RMS + projection + gates + Sinkhorn +
+pre-aggregate) and the post phase (res-mix + post-expand).
+
+Timing: W untimed warmup steps, then K timed steps bracketed by
+torch.cuda.synchronize().  Every kernel launch is bracketed by HIP events on
+the stream it runs on, and a 1 GiB read-modify-write flush runs before each
+kernel so the 256 MB Infinity Cache cannot serve x to the post phase from the
+pre phase's read (a real model runs F in between).  value = tokens / (mean pre
++ mean post kernel time).  The same loop without flushes is reported as
+`unflushed`.
+
+Also printed in the JSON line: roofline of the dominant (post) kernel against
+8 TB/s, the CPU oracle baseline (bounded sample, host cores), and the e2e
+MiniMind-3-mHC prefill tokens/s (config 3).
+
+Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--no-e2e] [--no-cpu]
+"""
+from __future__ import annotations
+
+import argparse
+import json
+import os
+import sys
+import time
+from pathlib import Path
+
+ROOT = Path(__file__).resolve().parent
+for _p in (str(ROOT), str(ROOT / "minimind-mhc_amd")):
+    if _p not in sys.path:
+        sys.path.insert(0, _p)
+
+METRIC = "mHC fwd tokens/s + % HBM roofline (16k tok, n=4, C=768); e2e prefill tok/s"
+HBM_PEAK_GBS = 8000.0
+N_STREAMS, C_DIM, TOKENS, ITERS = 4, 768, 16384, 20
+
+
+def algorithmic_bytes(n: int, C: int, M: int, s: int = 2):
+    """Compulsory HBM bytes per launch (each byte of each operand once).
+
+    pre : read x (n*C) + phi once, write sublayer_in (C), h_post (n), h_res (n*n)
+    post: read x (n*C), F (C), h_post (n), h_res (n*n), write out (n*C)
+    Sum per token: 3*n*C*s + 2*C*s + 2*(n + n*n)*s  (+ phi once).
+    """
+    fd = 2 * n + n * n
+    pre = M * (n * C + C + n + n * n) * s + n * C * fd * s
+    post = M * (2 * n * C + C + n + n * n) * s
+    return pre, post
+
+
+def _sync():
+    import torch
+    torch.cuda.synchronize()
+
+
+def bench_mhc(steps: int, warmup: int):
+    import torch
+    from model import _hip as H, _ops
+
+    dev = torch.device("cuda:0")
+    n, C, M = N_STREAMS, C_DIM, TOKENS
+    g = torch.Generator().manual_seed(0)
+    x = torch.randn(1, M, n * C, generator=g).to(torch.bfloat16).to(dev)
+    f = torch.randn(M, C, generator=g).to(torch.bfloat16).to(dev)
+    phi = (torch.randn(n * C, 2 * n + n * n, generator=g) * 0.02).to(torch.bfloat16).to(dev)
+    a = torch.tensor(0.01, dtype=torch.bfloat16, device=dev)
+    b0 = torch.zeros(n, dtype=torch.bfloat16, device=dev)
+    br = torch.eye(n, dtype=torch.bfloat16, device=dev)
+    packed = _ops.PhiPack(H.MODE_FULL).get(phi, n, C)
+    assert packed is not None, "config 2 must take the MFMA kernel"
+    flush = torch.empty(256 * 1024 * 1024, dtype=torch.float32, device=dev)  # 1 GiB
+    flush.zero_()
+
+    def pre():
+        return _ops.pre_full(x, phi, packed, a, b0, a, b0, a, br, n, C, 2.0, 1e-6, 1e-6, ITERS, 1e-6)
+
+    def post(o):
+        return _ops.post(x, o["h_res"], o["h_post"], f, n, C)
+
+    def step(ev=None, do_flush=True):
+        if do_flush:
+            flush.add_(1.0)
+        if ev:
+            ev[0].record()
+        o = pre()
+        if ev:
+            ev[1].record()
+        if do_flush:
+            flush.add_(1.0)
+        if ev:
+            ev[2].record()
+        post(o)
+        if ev:
+            ev[3].record()
+
+    for _ in range(warmup):
+        step()
+    _sync()
+    evs = [[torch.cuda.Event(enable_timing=True) for _ in range(4)] for _ in range(steps)]
+    t0 = time.perf_counter()
+    for i in range(steps):
+        step(evs[i])
+    _sync()
+    wall_flushed = (time.perf_counter() - t0) / steps * 1e3
+    t_pre = [e[0].elapsed_time(e[1]) for e in evs]
+    t_post = [e[2].elapsed_time(e[3]) for e in evs]
+
+    # Same loop with no flush: back-to-back kernels, wall clock.
+    for _ in range(warmup):
+        step(do_flush=False)
+    _sync()
+    t0 = time.perf_counter()
+    for _ in range(steps):
+        step(do_flush=False)
+    _sync()
+    wall_unflushed = (time.perf_counter() - t0) / steps * 1e3
+    return dict(t_pre=sum(t_pre) / steps, t_post=sum(t_post) / steps,
+                t_pre_min=min(t_pre), t_post_min=min(t_post),
+                wall_flushed=wall_flushed, wall_unflushed=wall_unflushed)
+
+
+def cpu_baseline(budget_s: float = 12.0):
+    """The oracle (torch CPU restatement of the reference _forward_ref) on a
+    bounded sample of the config-2 workload: 512 tokens per call, bf16, F a
+    fixed tensor; repeated until ~budget_s of CPU time; median tokens/s."""
+    import torch
+    from oracle import mhc_ref as R
+    from tests._util import make_params
+
+    cores = min(16, os.cpu_count() or 1)
+    torch.set_num_threads(cores)
+    n, C, m = N_STREAMS, C_DIM, 512
+    g = torch.Generator().manual_seed(0)
+    x = torch.randn(1, m, n * C, generator=g).to(torch.bfloat16)
+    fz = torch.randn(1, m, C, generator=g).to(torch.bfloat16)
+    p = make_params("full", n, C, torch.bfloat16, g, stress=False)
+    times = []
+    t_end = time.perf_counter() + budget_s
+    with torch.inference_mode():
+        R.mhc_full_forward(x, p, lambda z: fz, n, C, sinkhorn_iters=ITERS)
+        while time.perf_counter() < t_end or len(times) < 3:
+            t0 = time.perf_counter()
+            R.mhc_full_forward(x, p, lambda z: fz, n, C, sinkhorn_iters=ITERS)
+            times.append(time.perf_counter() - t0)
+    times.sort()
+    med = times[len(times) // 2]
+    return {"value": round(m / med, 1), "unit": "tokens/s", "cores": cores, "kind": "port",
+            "sample": f"oracle mhc_full_forward (reference _forward_ref restated), bf16, "
+                      f"{m} tokens x n={n} x C={C}, F fixed, median of {len(times)} calls"}
+
+
+def e2e_prefill(steps: int = 5, warmup: int = 2):
+    """MiniMind-3-mHC, 8 layers, hidden 768, 8 q / 4 kv heads,
+    head_dim 96, SwiGLU 2048, vocab 6400, n=4, bf16, N(0, 0.02) init;
+    prefill B=8, T=1024 (logits for every position, as the reference forward)."""
+    import torch
+    from model.model_minimind import MiniMindConfig, MiniMindForCausalLM, init_normal_
+
+    dev = torch.device("cuda:0")
+    cfg = MiniMindConfig(hidden_size=768, num_hidden_layers=8, num_attention_heads=8,
+                         num_key_value_heads=4, head_dim=96, intermediate_size=2048,
+                         rope_theta=1e6, vocab_size=6400, use_mhc=1, mhc_residual_expansion=4,
+                         max_position_embeddings=4096)
+    torch.manual_seed(0)
+    model = init_normal_(MiniMindForCausalLM(cfg)).to(torch.bfloat16).to(dev).eval()
+    g = torch.Generator().manual_seed(1)
+    ids = torch.randint(0, 6400, (8, 1024), generator=g).to(dev)
+    with torch.inference_mode():
+        for _ in range(warmup):
+            model(ids)
+        _sync()
+        t0 = time.perf_counter()
+        for _ in range(steps):
+            model(ids)
+        _sync()
+    dt = (time.perf_counter() - t0) / steps
+    return {"value": round(ids.numel() / dt, 1), "unit": "tokens/s", "ms_per_forward": round(dt * 1e3, 3),
+            "config": "C3: 8 layers, hidden 768, 8q/4kv heads, head_dim 96, SwiGLU 2048, vocab 6400, "
+                      "n=4, bf16, B=8 T=1024, 16 mHC connections + StreamExpand + MHCHead"}
+
+
+def main():
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=50)
+    ap.add_argument("--warmup", type=int, default=10)
+    ap.add_argument("--no-e2e", action="store_true")
+    ap.add_argument("--no-cpu", action="store_true")
+    args = ap.parse_args()
+    if args.gpus != 1:
+        print(f"bench.py: this build measures one GPU only (the mHC forward is per-token and "
+              f"shards by tokens with no exchange); --gpus {args.gpus} is not run.", file=sys.stderr)
+        sys.exit(2)
+
+    import torch
+    if not torch.cuda.is_available():
+        print("bench.py: no ROCm GPU visible", file=sys.stderr)
+        sys.exit(1)
+
+    r = bench_mhc(args.steps, args.warmup)
+    pre_b, post_b = algorithmic_bytes(N_STREAMS, C_DIM, TOKENS)
+    step_ms = r["t_pre"] + r["t_post"]
+    value = TOKENS / (step_ms * 1e-3)
+    post_gbs = post_b / (r["t_post"] * 1e-3) / 1e9
+    pre_gbs = pre_b / (r["t_pre"] * 1e-3) / 1e9
+    total_gbs = (pre_b + post_b) / (step_ms * 1e-3) / 1e9
+    line = {
+        "metric": METRIC,
+        "value": round(value, 1),
+        "unit": "tokens/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(step_ms, 5),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "bf16",
+        "data": "synthetic",
+        "config": {"workload": "C2: isolated mHC fwd (pre+Sinkhorn kernel, post kernel), "
+                               "16384 tok (B=16,T=1024), n=4, C=768, bf16, F fixed N(0,1)",
+                   "tokens": TOKENS, "n": N_STREAMS, "C": C_DIM, "sinkhorn_iters": ITERS,
+                   "parallelism": "single GPU"},
+        "roofline": {"bound": "hbm", "kernel": "post_vec_kernel (res-mix + post-expand)",
+                     "achieved": round(post_gbs, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                     "frac": round(post_gbs / HBM_PEAK_GBS, 4), "traffic": None,
+                     "algorithmic_bytes_per_launch": post_b},
+        "step_roofline": {"achieved": round(total_gbs, 1), "frac": round(total_gbs / HBM_PEAK_GBS, 4),
+                          "algorithmic_bytes_per_step": pre_b + post_b},
+        "kernels": {"pre_ms": round(r["t_pre"], 5), "post_ms": round(r["t_post"], 5),
+                    "pre_min_ms": round(r["t_pre_min"], 5), "post_min_ms": round(r["t_post_min"], 5),
+                    "pre_GBps": round(pre_gbs, 1), "post_GBps": round(post_gbs, 1),
+                    "pre_bytes": pre_b, "post_bytes": post_b},
+        "unflushed": {"ms_per_step_wall": round(r["wall_unflushed"], 5),
+                      "tokens_per_s": round(TOKENS / (r["wall_unflushed"] * 1e-3), 1)},
+    }
+    if not args.no_e2e:
+        line["e2e_prefill"] = e2e_prefill()
+    if not args.no_cpu:
+        line["cpu_baseline"] = cpu_baseline()
+    print(json.dumps(line), flush=True)
+
+
+if __name__ == "__main__":
+    main()

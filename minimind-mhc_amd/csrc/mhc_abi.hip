@@ -1,0 +1,231 @@
+// extern "C" entry points declared in include/mhc_amd.h: argument checks,
+// kernel selection, error reporting.  No device allocation anywhere.
+#include <stdarg.h>
+#include <stdio.h>
+
+#include "mhc_amd.h"
+#include "mhc_internal.hpp"
+
+namespace {
+
+thread_local char g_err[512] = "";
+
+int fail(int code, const char* fmt, ...) {
+  va_list ap;
+  va_start(ap, fmt);
+  vsnprintf(g_err, sizeof(g_err), fmt, ap);
+  va_end(ap);
+  return code;
+}
+
+int hip_status(hipError_t e, const char* what) {
+  if (e == hipSuccess) return 0;
+  return fail((int)e, "%s: %s", what, hipGetErrorString(e));
+}
+
+bool dtype_ok(int dt) { return dt == mhc::kF32 || dt == mhc::kBF16 || dt == mhc::kF16; }
+bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15) == 0; }
+
+constexpr int kMaxN = 16;
+constexpr int64_t kMaxBlocks = 0x7fffffff;
+
+// Shared checks for the three pre-phase style entry points.
+int check_pre(const mhc::PreArgs& a, const char* fn) {
+  if (a.M < 0) return fail(hipErrorInvalidValue, "%s: M must be >= 0 (got %lld)", fn, (long long)a.M);
+  if (a.n < 1 || a.n > kMaxN) return fail(hipErrorInvalidValue, "%s: n must be in [1, %d] (got %d)", fn, kMaxN, a.n);
+  if (a.C < 1) return fail(hipErrorInvalidValue, "%s: C must be >= 1 (got %d)", fn, a.C);
+  if (!dtype_ok(a.x_dtype)) return fail(hipErrorInvalidValue, "%s: bad x dtype %d", fn, a.x_dtype);
+  if (a.M > kMaxBlocks) return fail(hipErrorInvalidValue, "%s: M too large", fn);
+  if (!a.x || !a.sub_in) return fail(hipErrorInvalidValue, "%s: x and the main output are required", fn);
+  if (a.mode != mhc::kRms) {
+    if (!a.phi) return fail(hipErrorInvalidValue, "%s: phi is required", fn);
+    if (!dtype_ok(a.phi_dtype)) return fail(hipErrorInvalidValue, "%s: bad phi dtype %d", fn, a.phi_dtype);
+    if (!dtype_ok(a.param_dtype)) return fail(hipErrorInvalidValue, "%s: bad param dtype %d", fn, a.param_dtype);
+    if (!a.alpha[0] || !a.bias[0]) return fail(hipErrorInvalidValue, "%s: alpha/bias are required", fn);
+  }
+  if ((a.mode == mhc::kFull || a.mode == mhc::kNoHres) && (!a.h_post || !a.alpha[1] || !a.bias[1]))
+    return fail(hipErrorInvalidValue, "%s: h_post, alpha_post and bias_post are required", fn);
+  if (a.mode == mhc::kFull && (!a.alpha[2] || !a.bias[2]))
+    return fail(hipErrorInvalidValue, "%s: alpha_res and bias_res are required", fn);
+  return 0;
+}
+
+int run_pre(mhc::PreArgs& a, hipStream_t stream, const char* fn) {
+  if (int rc = check_pre(a, fn)) return rc;
+  if (a.M == 0) return 0;
+  const bool mfma = a.phi_packed && a.mode != mhc::kRms &&
+                    mhc::mfma_supported(a.x_dtype, a.phi_dtype, a.n, a.C, a.mode) &&
+                    aligned16(a.x) && aligned16(a.sub_in) && aligned16(a.phi_packed);
+  if (!mfma) a.phi_packed = nullptr;
+  return hip_status(mfma ? mhc::launch_pre_mfma(a, stream) : mhc::launch_pre_generic(a, stream), fn);
+}
+
+}  // namespace
+
+extern "C" {
+
+int mhc_abi_version(void) { return 1; }
+
+const char* mhc_last_error(void) { return g_err; }
+
+int64_t mhc_phi_packed_bytes(int n, int C, int mode) { return mhc::mfma_packed_bytes(n, C, mode); }
+
+int mhc_phi_pack(const void* phi, int phi_dtype, void* packed, int n, int C, int mode,
+                 hipStream_t stream) {
+  const int64_t bytes = mhc::mfma_packed_bytes(n, C, mode);
+  if (bytes <= 0) return fail(hipErrorInvalidValue, "mhc_phi_pack: no MFMA layout for n=%d C=%d mode=%d", n, C, mode);
+  if (phi_dtype != mhc::kBF16) return fail(hipErrorInvalidValue, "mhc_phi_pack: phi must be bf16");
+  if (!phi || !packed) return fail(hipErrorInvalidValue, "mhc_phi_pack: null pointer");
+  return hip_status(mhc::launch_phi_pack(phi, phi_dtype, packed, n, C, mode, stream), "mhc_phi_pack");
+}
+
+int mhc_pre_fwd(const void* x, int x_dtype, const void* phi, int phi_dtype, const void* phi_packed,
+                const void* alpha_pre, const void* bias_pre, const void* alpha_post,
+                const void* bias_post, const void* alpha_res, const void* bias_res,
+                int param_dtype, void* sublayer_in, void* h_pre, void* h_post, void* h_res_raw,
+                void* h_res, float* inv_rms, float* mixes_raw, int64_t M, int n, int C,
+                float post_mult, float pre_eps, float rms_eps, int sinkhorn_iters,
+                float sinkhorn_eps, hipStream_t stream) {
+  mhc::PreArgs a{};
+  a.x = x;
+  a.phi = phi;
+  a.phi_packed = phi_packed;
+  a.alpha[0] = alpha_pre;
+  a.alpha[1] = alpha_post;
+  a.alpha[2] = alpha_res;
+  a.bias[0] = bias_pre;
+  a.bias[1] = bias_post;
+  a.bias[2] = bias_res;
+  a.sub_in = sublayer_in;
+  a.h_pre = h_pre;
+  a.h_post = h_post;
+  a.h_res_raw = h_res_raw;
+  a.h_res = h_res;
+  a.inv_rms = inv_rms;
+  a.mixes_raw = mixes_raw;
+  a.M = M;
+  a.n = n;
+  a.C = C;
+  a.mode = mhc::kFull;
+  a.x_dtype = x_dtype;
+  a.phi_dtype = phi_dtype;
+  a.param_dtype = param_dtype;
+  a.post_mult = post_mult;
+  a.pre_eps = pre_eps;
+  a.rms_eps = rms_eps;
+  a.sk_iters = sinkhorn_iters;
+  a.sk_eps = sinkhorn_eps;
+  return run_pre(a, stream, "mhc_pre_fwd");
+}
+
+int mhc_pre_nohres_fwd(const void* x, int x_dtype, const void* phi, int phi_dtype,
+                       const void* phi_packed, const void* alpha_pre, const void* bias_pre,
+                       const void* alpha_post, const void* bias_post, int param_dtype,
+                       void* sublayer_in, void* h_pre, void* h_post, float* inv_rms,
+                       float* mixes_raw, int64_t M, int n, int C, float post_mult, float pre_eps,
+                       float rms_eps, hipStream_t stream) {
+  mhc::PreArgs a{};
+  a.x = x;
+  a.phi = phi;
+  a.phi_packed = phi_packed;
+  a.alpha[0] = alpha_pre;
+  a.alpha[1] = alpha_post;
+  a.bias[0] = bias_pre;
+  a.bias[1] = bias_post;
+  a.sub_in = sublayer_in;
+  a.h_pre = h_pre;
+  a.h_post = h_post;
+  a.inv_rms = inv_rms;
+  a.mixes_raw = mixes_raw;
+  a.M = M;
+  a.n = n;
+  a.C = C;
+  a.mode = mhc::kNoHres;
+  a.x_dtype = x_dtype;
+  a.phi_dtype = phi_dtype;
+  a.param_dtype = param_dtype;
+  a.post_mult = post_mult;
+  a.pre_eps = pre_eps;
+  a.rms_eps = rms_eps;
+  return run_pre(a, stream, "mhc_pre_nohres_fwd");
+}
+
+int mhc_head_fwd(const void* x, int x_dtype, const void* phi, int phi_dtype,
+                 const void* phi_packed, const void* alpha, const void* bias, int param_dtype,
+                 void* out, float* inv_rms, float* mix_raw, int64_t M, int n, int C, float pre_eps,
+                 float rms_eps, hipStream_t stream) {
+  mhc::PreArgs a{};
+  a.x = x;
+  a.phi = phi;
+  a.phi_packed = phi_packed;
+  a.alpha[0] = alpha;
+  a.bias[0] = bias;
+  a.sub_in = out;
+  a.inv_rms = inv_rms;
+  a.mixes_raw = n == 1 ? nullptr : mix_raw;
+  a.M = M;
+  a.n = n;
+  a.C = C;
+  a.mode = n == 1 ? mhc::kRms : mhc::kHead;
+  a.x_dtype = x_dtype;
+  a.phi_dtype = phi_dtype;
+  a.param_dtype = param_dtype;
+  a.pre_eps = pre_eps;
+  a.rms_eps = rms_eps;
+  return run_pre(a, stream, "mhc_head_fwd");
+}
+
+static int run_post(mhc::PostArgs& a, hipStream_t stream, const char* fn) {
+  if (a.M < 0) return fail(hipErrorInvalidValue, "%s: M must be >= 0", fn);
+  if (a.n < 1 || a.n > kMaxN) return fail(hipErrorInvalidValue, "%s: n must be in [1, %d] (got %d)", fn, kMaxN, a.n);
+  if (a.C < 1) return fail(hipErrorInvalidValue, "%s: C must be >= 1", fn);
+  if (!dtype_ok(a.x_dtype) || !dtype_ok(a.h_dtype) || !dtype_ok(a.f_dtype))
+    return fail(hipErrorInvalidValue, "%s: bad dtype", fn);
+  if (!a.x || !a.h_post || !a.f_out || !a.out) return fail(hipErrorInvalidValue, "%s: null pointer", fn);
+  if (a.out == a.x) return fail(hipErrorInvalidValue, "%s: out must not alias x", fn);
+  if (a.M * a.n * (int64_t)a.C / 256 + 1 > kMaxBlocks) return fail(hipErrorInvalidValue, "%s: problem too large", fn);
+  if (a.M == 0) return 0;
+  return hip_status(mhc::launch_post(a, stream), fn);
+}
+
+int mhc_post_fwd(const void* x, int x_dtype, const void* h_res, const void* h_post, int h_dtype,
+                 const void* f_out, int f_dtype, void* out, int64_t M, int n, int C,
+                 hipStream_t stream) {
+  if (!h_res) return fail(hipErrorInvalidValue, "mhc_post_fwd: h_res is required");
+  mhc::PostArgs a{x, h_res, h_post, f_out, out, M, n, C, x_dtype, h_dtype, f_dtype};
+  return run_post(a, stream, "mhc_post_fwd");
+}
+
+int mhc_post_nohres_fwd(const void* x, int x_dtype, const void* h_post, int h_dtype,
+                        const void* f_out, int f_dtype, void* out, int64_t M, int n, int C,
+                        hipStream_t stream) {
+  mhc::PostArgs a{x, nullptr, h_post, f_out, out, M, n, C, x_dtype, h_dtype, f_dtype};
+  return run_post(a, stream, "mhc_post_nohres_fwd");
+}
+
+int mhc_sinkhorn_fwd(const void* m_in, void* m_out, int dtype, int64_t batch, int n, int iters,
+                     float eps, hipStream_t stream) {
+  if (batch < 0) return fail(hipErrorInvalidValue, "mhc_sinkhorn_fwd: batch must be >= 0");
+  if (n < 1 || n > 32) return fail(hipErrorInvalidValue, "mhc_sinkhorn_fwd: n must be in [1, 32] (got %d)", n);
+  if (!dtype_ok(dtype)) return fail(hipErrorInvalidValue, "mhc_sinkhorn_fwd: bad dtype %d", dtype);
+  if (!m_in || !m_out) return fail(hipErrorInvalidValue, "mhc_sinkhorn_fwd: null pointer");
+  if (batch > kMaxBlocks) return fail(hipErrorInvalidValue, "mhc_sinkhorn_fwd: batch too large");
+  if (batch == 0) return 0;
+  return hip_status(mhc::launch_sinkhorn(m_in, m_out, dtype, batch, n, iters, eps, stream),
+                    "mhc_sinkhorn_fwd");
+}
+
+int mhc_stream_expand_fwd(const void* x, void* out, int elem_bytes, int64_t M, int n, int C,
+                          hipStream_t stream) {
+  if (elem_bytes != 2 && elem_bytes != 4)
+    return fail(hipErrorInvalidValue, "mhc_stream_expand_fwd: elem_bytes must be 2 or 4");
+  if (M < 0 || n < 1 || C < 1) return fail(hipErrorInvalidValue, "mhc_stream_expand_fwd: bad shape");
+  if (!x || !out) return fail(hipErrorInvalidValue, "mhc_stream_expand_fwd: null pointer");
+  if (M * n * (int64_t)C / 256 + 1 > kMaxBlocks)
+    return fail(hipErrorInvalidValue, "mhc_stream_expand_fwd: problem too large");
+  if (M == 0) return 0;
+  return hip_status(mhc::launch_stream_expand(x, out, elem_bytes, M, n, C, stream),
+                    "mhc_stream_expand_fwd");
+}
+
+}  // extern "C"

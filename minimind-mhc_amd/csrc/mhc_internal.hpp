@@ -1,0 +1,82 @@
+// Host-side declarations shared between the kernel translation units and the
+// C-ABI layer.  Nothing here is exported; the public surface is include/mhc_amd.h.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+#include "mhc_device.hpp"
+
+namespace mhc {
+
+// Which slice of the reference's fused projection a pre-phase launch computes.
+//   kFull   : [pre n | post n | res n*n]   (MHCConnection_Fused)
+//   kNoHres : [pre n | post n]             (MHCConnection_FusedNoHres)
+//   kHead   : [mix n]                      (MHCHead)
+//   kRms    : no projection, out = x * inv_rms (MHCHead with n == 1)
+enum Mode : int { kFull = 0, kNoHres = 1, kHead = 2, kRms = 3 };
+
+__host__ __device__ inline int mode_fd(int mode, int n) {
+  switch (mode) {
+    case kFull: return 2 * n + n * n;
+    case kNoHres: return 2 * n;
+    case kHead: return n;
+    default: return 0;
+  }
+}
+
+// Everything one pre-phase launch reads and writes.  Optional outputs are null
+// when the caller does not want them.
+struct PreArgs {
+  const void* x;          // [M, n*C]   x_dtype
+  const void* phi;        // [n*C, FD]  phi_dtype, reference row-major layout
+  const void* phi_packed; // MFMA B-operand image of phi (bf16), or null
+  const void* alpha[3];   // pre, post, res scalars (param_dtype)
+  const void* bias[3];    // pre [n], post [n], res [n*n] (param_dtype)
+  void* sub_in;           // [M, C]     x_dtype  (MHCHead: the head output)
+  void* h_pre;            // [M, n]     x_dtype  optional
+  void* h_post;           // [M, n]     x_dtype
+  void* h_res_raw;        // [M, n, n]  x_dtype  optional
+  void* h_res;            // [M, n, n]  x_dtype  (Sinkhorn output; null = skip)
+  float* inv_rms;         // [M]        optional
+  float* mixes_raw;       // [M, FD]    optional
+  int64_t M;
+  int n, C, mode;
+  int x_dtype, phi_dtype, param_dtype;
+  float post_mult, pre_eps, rms_eps;
+  int sk_iters;
+  float sk_eps;
+};
+
+struct PostArgs {
+  const void* x;       // [M, n*C]
+  const void* h_res;   // [M, n, n] or null (identity, use_mhc = 2)
+  const void* h_post;  // [M, n]
+  const void* f_out;   // [M, C]
+  void* out;           // [M, n*C]
+  int64_t M;
+  int n, C;
+  int x_dtype, h_dtype, f_dtype;
+};
+
+// Launchers: return hipSuccess or the launch error.
+hipError_t launch_pre_mfma(const PreArgs& a, hipStream_t s);   // requires mfma_supported()
+hipError_t launch_pre_generic(const PreArgs& a, hipStream_t s);
+hipError_t launch_post(const PostArgs& a, hipStream_t s);
+hipError_t launch_sinkhorn(const void* in, void* out, int dtype, int64_t batch, int n,
+                           int iters, float eps, hipStream_t s);
+hipError_t launch_stream_expand(const void* x, void* out, int elem_bytes, int64_t M, int n,
+                                int C, hipStream_t s);
+hipError_t launch_phi_pack(const void* phi, int phi_dtype, void* packed, int n, int C, int mode,
+                           hipStream_t s);
+
+// MFMA pre-phase geometry: 16 tokens per workgroup, c-blocks of 32 columns.
+constexpr int kTokTile = 16;
+constexpr int kCBlock = 32;
+
+// Packed size in bytes of phi for the MFMA path, or 0 when (n, C, mode) has no
+// MFMA instance (the generic kernel then serves the call).
+int64_t mfma_packed_bytes(int n, int C, int mode);
+bool mfma_supported(int x_dtype, int phi_dtype, int n, int C, int mode);
+
+}  // namespace mhc

@@ -1,0 +1,131 @@
+// Standalone Sinkhorn-Knopp (sinkhorn_normalize) and StreamExpand.
+#include "mhc_internal.hpp"
+
+namespace mhc {
+
+// ------------------------------------------------------------- Sinkhorn-Knopp
+// Batched n x n projection onto the doubly-stochastic set, fp32 arithmetic,
+// output in the input dtype (model/mhc_fused.py:61-93, :111-128; schedule
+// :47-56).  n in {1, 2, 4, 8}: one element per lane, lane-group shuffles.
+
+template <int N>
+__global__ __launch_bounds__(256) void sinkhorn_lane_kernel(const void* __restrict__ in,
+                                                            void* __restrict__ out, int dt,
+                                                            int64_t total, int iters, float eps) {
+  const int64_t e = (int64_t)blockIdx.x * 256 + threadIdx.x;
+  const bool ok = e < total;  // total is a multiple of N*N, and 256 % (N*N) == 0
+  float v = ok ? ld_any(in, e, dt) : 0.f;
+  v = sinkhorn_lane<N>(v, iters, eps);
+  if (ok) st_any(out, e, dt, v);
+}
+
+// Any n <= 32: one workgroup per matrix, thread i owns row i / column i, the
+// matrix lives in LDS.
+constexpr int kSkMaxN = 32;
+
+__global__ __launch_bounds__(64) void sinkhorn_lds_kernel(const void* __restrict__ in,
+                                                          void* __restrict__ out, int dt, int n,
+                                                          int iters, float eps) {
+  __shared__ float s[kSkMaxN * kSkMaxN];
+  const int tid = threadIdx.x;
+  const int64_t base = (int64_t)blockIdx.x * n * n;
+  for (int e = tid; e < n * n; e += 64) s[e] = ld_any(in, base + e, dt);
+  __syncthreads();
+  if (tid < n) {
+    float* row = s + tid * n;
+    float mx = row[0];
+    for (int j = 1; j < n; ++j) mx = fmaxf(mx, row[j]);
+    float sum = 0.f;
+    for (int j = 0; j < n; ++j) {
+      row[j] = expf(row[j] - mx);
+      sum += row[j];
+    }
+    for (int j = 0; j < n; ++j) row[j] = __fadd_rn(__fdiv_rn(row[j], sum), eps);
+  }
+  __syncthreads();
+  for (int it = 0; it < iters || it == 0; ++it) {
+    if (it > 0) {
+      if (tid < n) {
+        float* row = s + tid * n;
+        float sum = 0.f;
+        for (int j = 0; j < n; ++j) sum += row[j];
+        const float d = __fadd_rn(sum, eps);
+        for (int j = 0; j < n; ++j) row[j] = __fdiv_rn(row[j], d);
+      }
+      __syncthreads();
+    }
+    if (tid < n) {
+      float sum = 0.f;
+      for (int i = 0; i < n; ++i) sum += s[i * n + tid];
+      const float d = __fadd_rn(sum, eps);
+      for (int i = 0; i < n; ++i) s[i * n + tid] = __fdiv_rn(s[i * n + tid], d);
+    }
+    __syncthreads();
+  }
+  for (int e = tid; e < n * n; e += 64) st_any(out, base + e, dt, s[e]);
+}
+
+hipError_t launch_sinkhorn(const void* in, void* out, int dtype, int64_t batch, int n, int iters,
+                           float eps, hipStream_t s) {
+  const int64_t total = batch * n * n;
+  const int64_t blocks = (total + 255) / 256;
+  switch (n) {
+    case 1:
+      hipLaunchKernelGGL(sinkhorn_lane_kernel<1>, dim3((unsigned)blocks), dim3(256), 0, s, in, out, dtype, total, iters, eps);
+      break;
+    case 2:
+      hipLaunchKernelGGL(sinkhorn_lane_kernel<2>, dim3((unsigned)blocks), dim3(256), 0, s, in, out, dtype, total, iters, eps);
+      break;
+    case 4:
+      hipLaunchKernelGGL(sinkhorn_lane_kernel<4>, dim3((unsigned)blocks), dim3(256), 0, s, in, out, dtype, total, iters, eps);
+      break;
+    case 8:
+      hipLaunchKernelGGL(sinkhorn_lane_kernel<8>, dim3((unsigned)blocks), dim3(256), 0, s, in, out, dtype, total, iters, eps);
+      break;
+    default:
+      if (n > kSkMaxN) return hipErrorInvalidValue;
+      hipLaunchKernelGGL(sinkhorn_lds_kernel, dim3((unsigned)batch), dim3(64), 0, s, in, out, dtype, n, iters, eps);
+      break;
+  }
+  return hipGetLastError();
+}
+
+// --------------------------------------------------------------- StreamExpand
+// out[t, i*C + c] = x[t, c] for i < n (model/mhc_common.py:115-119); a pure
+// byte copy, so it is written over units of U (16, 4 or 2 bytes).
+
+template <typename U>
+__global__ __launch_bounds__(256) void expand_kernel(const U* __restrict__ x, U* __restrict__ out,
+                                                     int64_t total, int n, int cu) {
+  const int64_t gid = (int64_t)blockIdx.x * 256 + threadIdx.x;
+  if (gid >= total) return;
+  const int64_t per_tok = (int64_t)n * cu;
+  const int64_t tok = gid / per_tok;
+  const int c = (int)((gid - tok * per_tok) % cu);
+  out[gid] = x[tok * cu + c];
+}
+
+hipError_t launch_stream_expand(const void* x, void* out, int elem_bytes, int64_t M, int n, int C,
+                                hipStream_t s) {
+  const int64_t row_bytes = (int64_t)elem_bytes * C;
+  const uintptr_t align = reinterpret_cast<uintptr_t>(x) | reinterpret_cast<uintptr_t>(out);
+  if (row_bytes % 16 == 0 && align % 16 == 0) {
+    const int cu = (int)(row_bytes / 16);
+    const int64_t total = M * n * cu;
+    hipLaunchKernelGGL(expand_kernel<U32x4>, dim3((unsigned)((total + 255) / 256)), dim3(256), 0, s,
+                       static_cast<const U32x4*>(x), static_cast<U32x4*>(out), total, n, cu);
+  } else if (row_bytes % 4 == 0 && align % 4 == 0) {
+    const int cu = (int)(row_bytes / 4);
+    const int64_t total = M * n * cu;
+    hipLaunchKernelGGL(expand_kernel<uint32_t>, dim3((unsigned)((total + 255) / 256)), dim3(256), 0, s,
+                       static_cast<const uint32_t*>(x), static_cast<uint32_t*>(out), total, n, cu);
+  } else {
+    const int cu = (int)(row_bytes / 2);
+    const int64_t total = M * n * cu;
+    hipLaunchKernelGGL(expand_kernel<uint16_t>, dim3((unsigned)((total + 255) / 256)), dim3(256), 0, s,
+                       static_cast<const uint16_t*>(x), static_cast<uint16_t*>(out), total, n, cu);
+  }
+  return hipGetLastError();
+}
+
+}  // namespace mhc

@@ -1,0 +1,172 @@
+// Post phase: res-mix + post-expand, one read-n / write-n streaming pass.
+//
+//   out[t, i, c] = sum_j H_res[t, i, j] * x[t, j, c] + H_post[t, i] * F[t, c]
+//   (use_mhc = 2, H_res = I:  out[t, i, c] = x[t, i, c] + H_post[t, i] * F[t, c])
+//
+// Reference: model/mhc_fused.py:416-459 (fused kernel), :562-568 (ref),
+// model/mhc_fused_no_hres.py:284-316, :389-394.  fp32 arithmetic, one rounding
+// at the store, like the reference's fused kernel.
+//
+// Work split: one thread per (token, V-column chunk), V = 16 bytes of x.  The
+// thread reads the n chunks of x at that column, the F chunk, and the token's
+// n*n + n gate values (broadcast within the token's threads), and writes n
+// chunks of out.  Every byte of x, F and out moves exactly once.
+#include "mhc_internal.hpp"
+
+namespace mhc {
+
+template <typename T>
+struct Elem;
+template <>
+struct Elem<float> {
+  __device__ static float get(float v) { return v; }
+  __device__ static float put(float v) { return v; }
+};
+template <>
+struct Elem<__bf16> {
+  __device__ static float get(__bf16 v) { return bf16_bits_to_f32(__builtin_bit_cast(uint16_t, v)); }
+  __device__ static __bf16 put(float v) { return (__bf16)v; }
+};
+template <>
+struct Elem<_Float16> {
+  __device__ static float get(_Float16 v) { return (float)v; }
+  __device__ static _Float16 put(float v) { return (_Float16)v; }
+};
+
+// K contiguous elements moved as one aligned aggregate (K * sizeof(T) is a power
+// of two, so the compiler emits the widest vector load/store that fits).
+template <typename T, int K>
+struct alignas(K * sizeof(T) >= 16 ? 16 : K * sizeof(T)) Pack {
+  T v[K];
+};
+
+template <typename T, int K>
+__device__ __forceinline__ void load_pack(const T* p, float (&o)[K]) {
+  const Pack<T, K> pk = *reinterpret_cast<const Pack<T, K>*>(p);
+#pragma unroll
+  for (int k = 0; k < K; ++k) o[k] = Elem<T>::get(pk.v[k]);
+}
+
+template <typename T, int K>
+__device__ __forceinline__ void store_pack(T* p, const float (&o)[K]) {
+  Pack<T, K> pk;
+#pragma unroll
+  for (int k = 0; k < K; ++k) pk.v[k] = Elem<T>::put(o[k]);
+  *reinterpret_cast<Pack<T, K>*>(p) = pk;
+}
+
+template <typename XT, typename FT, int N, bool RES>
+__global__ __launch_bounds__(256) void post_vec_kernel(PostArgs a) {
+  constexpr int V = 16 / sizeof(XT);
+  const int C = a.C;
+  const int CV = C / V;
+  const int64_t gid = (int64_t)blockIdx.x * 256 + threadIdx.x;
+  const int64_t tok = gid / CV;
+  if (tok >= a.M) return;
+  const int c = (int)(gid - tok * CV) * V;
+  const int64_t NC = (int64_t)N * C;
+  const XT* __restrict__ x = static_cast<const XT*>(a.x) + tok * NC + c;
+  XT* __restrict__ out = static_cast<XT*>(a.out) + tok * NC + c;
+
+  float xv[N][V];
+#pragma unroll
+  for (int j = 0; j < N; ++j) load_pack<XT, V>(x + (int64_t)j * C, xv[j]);
+  float fv[V];
+  load_pack<FT, V>(static_cast<const FT*>(a.f_out) + tok * C + c, fv);
+  float hp[N];
+  load_pack<XT, N>(static_cast<const XT*>(a.h_post) + tok * N, hp);
+  float hr[RES ? N * N : 1];
+  if constexpr (RES) load_pack<XT, N * N>(static_cast<const XT*>(a.h_res) + tok * N * N, hr);
+
+#pragma unroll
+  for (int i = 0; i < N; ++i) {
+    float o[V];
+#pragma unroll
+    for (int v = 0; v < V; ++v) {
+      float acc;
+      if constexpr (RES) {
+        acc = 0.f;
+#pragma unroll
+        for (int j = 0; j < N; ++j) acc = fmaf(hr[i * N + j], xv[j][v], acc);
+      } else {
+        acc = xv[i][v];
+      }
+      o[v] = fmaf(hp[i], fv[v], acc);
+    }
+    store_pack<XT, V>(out + (int64_t)i * C, o);
+  }
+}
+
+// Any dtype mix, any C: one thread per output element.
+__global__ __launch_bounds__(256) void post_generic_kernel(PostArgs a) {
+  const int64_t gid = (int64_t)blockIdx.x * 256 + threadIdx.x;
+  const int n = a.n;
+  const int C = a.C;
+  const int64_t per_tok = (int64_t)n * C;
+  const int64_t tok = gid / per_tok;
+  if (tok >= a.M) return;
+  const int64_t rem = gid - tok * per_tok;
+  const int i = (int)(rem / C);
+  const int c = (int)(rem - (int64_t)i * C);
+  const int64_t xb = tok * per_tok;
+  float acc;
+  if (a.h_res) {
+    acc = 0.f;
+    for (int j = 0; j < n; ++j)
+      acc = fmaf(ld_any(a.h_res, tok * n * n + i * n + j, a.h_dtype),
+                 ld_any(a.x, xb + (int64_t)j * C + c, a.x_dtype), acc);
+  } else {
+    acc = ld_any(a.x, xb + (int64_t)i * C + c, a.x_dtype);
+  }
+  const float r = fmaf(ld_any(a.h_post, tok * n + i, a.h_dtype),
+                       ld_any(a.f_out, tok * C + c, a.f_dtype), acc);
+  st_any(a.out, xb + (int64_t)i * C + c, a.x_dtype, r);
+}
+
+template <typename XT, typename FT, int N>
+static hipError_t launch_vec(const PostArgs& a, hipStream_t s) {
+  constexpr int V = 16 / sizeof(XT);
+  const int64_t threads = a.M * (a.C / V);
+  const int64_t blocks = (threads + 255) / 256;
+  if (a.h_res)
+    hipLaunchKernelGGL((post_vec_kernel<XT, FT, N, true>), dim3((unsigned)blocks), dim3(256), 0, s, a);
+  else
+    hipLaunchKernelGGL((post_vec_kernel<XT, FT, N, false>), dim3((unsigned)blocks), dim3(256), 0, s, a);
+  return hipGetLastError();
+}
+
+template <typename XT, typename FT>
+static hipError_t launch_vec_n(const PostArgs& a, hipStream_t s) {
+  switch (a.n) {
+    case 1: return launch_vec<XT, FT, 1>(a, s);
+    case 2: return launch_vec<XT, FT, 2>(a, s);
+    case 4: return launch_vec<XT, FT, 4>(a, s);
+    case 8: return launch_vec<XT, FT, 8>(a, s);
+    default: return hipErrorInvalidValue;
+  }
+}
+
+static bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15) == 0; }
+
+hipError_t launch_post(const PostArgs& a, hipStream_t s) {
+  const int xb = dtype_bytes(a.x_dtype);
+  const int V = 16 / xb;
+  // n == 16 would hold 256 gate values per thread; it takes the generic kernel.
+  const bool pow2n = a.n == 1 || a.n == 2 || a.n == 4 || a.n == 8;
+  const bool vec_ok = pow2n && a.h_dtype == a.x_dtype && a.C % V == 0 && aligned16(a.x) &&
+                      aligned16(a.out) && aligned16(a.f_out) &&
+                      (reinterpret_cast<uintptr_t>(a.h_post) % (a.n * xb > 16 ? 16 : a.n * xb)) == 0 &&
+                      (!a.h_res ||
+                       (reinterpret_cast<uintptr_t>(a.h_res) % (a.n * a.n * xb > 16 ? 16 : a.n * a.n * xb)) == 0);
+  if (vec_ok) {
+    if (a.x_dtype == kBF16 && a.f_dtype == kBF16) return launch_vec_n<__bf16, __bf16>(a, s);
+    if (a.x_dtype == kF32 && a.f_dtype == kF32) return launch_vec_n<float, float>(a, s);
+    if (a.x_dtype == kF16 && a.f_dtype == kF16) return launch_vec_n<_Float16, _Float16>(a, s);
+  }
+  const int64_t total = a.M * a.n * (int64_t)a.C;
+  const int64_t blocks = (total + 255) / 256;
+  hipLaunchKernelGGL(post_generic_kernel, dim3((unsigned)blocks), dim3(256), 0, s, a);
+  return hipGetLastError();
+}
+
+}  // namespace mhc

@@ -1,0 +1,237 @@
+// Pre phase: MFMA dispatch, phi packing, and the generic VALU kernel.
+//
+// The generic kernel serves every (dtype, n, C) the MFMA instances do not:
+// fp32 / fp16 streams, fp32 phi, n == 16, C > 1024 or C % 8 != 0, and the
+// n == 1 MHCHead (plain RMSNorm).  One 256-thread workgroup per token; it is a
+// correctness path, not a tuned one.  Its arithmetic follows the reference's
+// fused kernel: x_norm = x * inv_rms in fp32, fp32 projection, gates in fp32,
+// outputs rounded once to the stream dtype (model/mhc_fused.py:205-268,
+// model/mhc_fused_no_hres.py:48-145, model/mhc_common.py:128-195).
+#include "mhc_pre_mfma.hpp"
+
+namespace mhc {
+
+// ------------------------------------------------------------------ packing
+
+// packed[((i*NCB + cb)*NT + nt)*64 + lane][s] =
+//     phi[i*C + cb*32 + (lane/16)*8 + s, nt*16 + lane%16]   (0 outside [C, FD))
+// so that lane `lane` of the wave reading column block cb of stream i finds its
+// MFMA B operand (8 consecutive k for output column lane%16) as one 16-byte load.
+__global__ __launch_bounds__(256) void phi_pack_kernel(const void* __restrict__ phi, int dt,
+                                                       uint16_t* __restrict__ packed, int C,
+                                                       int FD, int NCB, int NT, int64_t total) {
+  const int64_t idx = (int64_t)blockIdx.x * 256 + threadIdx.x;
+  if (idx >= total) return;
+  const int s = (int)(idx & 7);
+  const int lane = (int)((idx >> 3) & 63);
+  int64_t rest = idx >> 9;
+  const int nt = (int)(rest % NT);
+  rest /= NT;
+  const int cb = (int)(rest % NCB);
+  const int i = (int)(rest / NCB);
+  const int c = cb * kCBlock + (lane >> 4) * 8 + s;
+  const int f = nt * 16 + (lane & 15);
+  float v = 0.f;
+  if (c < C && f < FD) v = ld_any(phi, ((int64_t)i * C + c) * FD + f, dt);
+  packed[idx] = f32_to_bf16_bits(v);
+}
+
+int64_t mfma_packed_bytes(int n, int C, int mode) {
+  if (!(n == 1 || n == 2 || n == 4 || n == 8)) return 0;
+  if (mode != kFull && mode != kNoHres && mode != kHead) return 0;
+  if (mode == kHead && n == 1) return 0;
+  if (C <= 0 || C % 8 != 0) return 0;
+  if (pre_mfma_kb_needed(n, C) > pre_mfma_kb_max(n)) return 0;
+  const int fd = mode_fd(mode, n);
+  const int nt = (fd + 15) / 16;
+  const int ncb = (C + kCBlock - 1) / kCBlock;
+  return (int64_t)n * ncb * nt * 64 * 8 * 2;
+}
+
+bool mfma_supported(int x_dtype, int phi_dtype, int n, int C, int mode) {
+  return x_dtype == kBF16 && phi_dtype == kBF16 && mfma_packed_bytes(n, C, mode) > 0;
+}
+
+hipError_t launch_phi_pack(const void* phi, int phi_dtype, void* packed, int n, int C, int mode,
+                           hipStream_t s) {
+  const int fd = mode_fd(mode, n);
+  const int nt = (fd + 15) / 16;
+  const int ncb = (C + kCBlock - 1) / kCBlock;
+  const int64_t total = (int64_t)n * ncb * nt * 64 * 8;
+  const int64_t blocks = (total + 255) / 256;
+  hipLaunchKernelGGL(phi_pack_kernel, dim3((unsigned)blocks), dim3(256), 0, s, phi, phi_dtype,
+                     static_cast<uint16_t*>(packed), C, fd, ncb, nt, total);
+  return hipGetLastError();
+}
+
+hipError_t launch_pre_mfma(const PreArgs& a, hipStream_t s) {
+  const int kb = pre_mfma_kb_needed(a.n, a.C);
+  switch (a.n) {
+    case 1: return launch_pre_mfma_n1(a, kb, s);
+    case 2: return launch_pre_mfma_n2(a, kb, s);
+    case 4: return launch_pre_mfma_n4(a, kb, s);
+    case 8: return launch_pre_mfma_n8(a, kb, s);
+    default: return hipErrorInvalidValue;
+  }
+}
+
+// ------------------------------------------------------------ generic kernel
+
+constexpr int kGenThreads = 256;
+constexpr int kGenMaxN = 16;
+constexpr int kGenMaxFD = 2 * kGenMaxN + kGenMaxN * kGenMaxN;
+constexpr int kGenChunk = 16;  // features reduced per block-wide reduction
+
+__device__ __forceinline__ float wave_sum(float v) {
+#pragma unroll
+  for (int m = 1; m < 64; m <<= 1) v += __shfl_xor(v, m, 64);
+  return v;
+}
+
+__global__ __launch_bounds__(kGenThreads) void pre_generic_kernel(PreArgs a) {
+  __shared__ float s_red[kGenThreads / 64][kGenChunk];
+  __shared__ float s_mix[kGenMaxFD];
+  __shared__ float s_hpre[kGenMaxN];
+  __shared__ float s_mat[kGenMaxN * kGenMaxN];
+  __shared__ float s_inv;
+
+  const int tid = threadIdx.x;
+  const int lane = tid & 63;
+  const int wave = tid >> 6;
+  const int64_t tok = blockIdx.x;
+  const int n = a.n;
+  const int C = a.C;
+  const int mode = a.mode;
+  const int FD = mode_fd(mode, n);
+  const int64_t NC = (int64_t)n * C;
+  const int xdt = a.x_dtype;
+  const int64_t xb = tok * NC;
+
+  // sum of squares over the whole n*C row
+  float ss = 0.f;
+  for (int64_t k = tid; k < NC; k += kGenThreads) {
+    const float v = ld_any(a.x, xb + k, xdt);
+    ss = fmaf(v, v, ss);
+  }
+  ss = wave_sum(ss);
+  if (lane == 0) s_red[wave][0] = ss;
+  __syncthreads();
+  if (tid == 0) {
+    float t = 0.f;
+    for (int w = 0; w < kGenThreads / 64; ++w) t += s_red[w][0];
+    const float inv = 1.0f / sqrtf(t / (float)NC + a.rms_eps);
+    s_inv = inv;
+    if (a.inv_rms) a.inv_rms[tok] = inv;
+  }
+  __syncthreads();
+  const float inv = s_inv;
+
+  if (mode == kRms) {  // MHCHead with n == 1 (model/mhc_common.py:438-442)
+    for (int64_t k = tid; k < NC; k += kGenThreads)
+      st_any(a.sub_in, tok * NC + k, xdt, ld_any(a.x, xb + k, xdt) * inv);
+    return;
+  }
+
+  // projection, kGenChunk output features per block reduction
+  for (int f0 = 0; f0 < FD; f0 += kGenChunk) {
+    float p[kGenChunk];
+#pragma unroll
+    for (int j = 0; j < kGenChunk; ++j) p[j] = 0.f;
+    for (int64_t k = tid; k < NC; k += kGenThreads) {
+      const float xn = ld_any(a.x, xb + k, xdt) * inv;
+      const int64_t wb = k * FD + f0;
+#pragma unroll
+      for (int j = 0; j < kGenChunk; ++j)
+        if (f0 + j < FD) p[j] = fmaf(xn, ld_any(a.phi, wb + j, a.phi_dtype), p[j]);
+    }
+    __syncthreads();  // s_red reuse
+#pragma unroll
+    for (int j = 0; j < kGenChunk; ++j) {
+      const float v = wave_sum(p[j]);
+      if (lane == 0) s_red[wave][j] = v;
+    }
+    __syncthreads();
+    if (tid < kGenChunk && f0 + tid < FD) {
+      float t = 0.f;
+      for (int w = 0; w < kGenThreads / 64; ++w) t += s_red[w][tid];
+      s_mix[f0 + tid] = t;
+      if (a.mixes_raw) a.mixes_raw[tok * FD + f0 + tid] = t;
+    }
+  }
+  __syncthreads();
+
+  // gates
+  const int pdt = a.param_dtype;
+  for (int f = tid; f < FD; f += kGenThreads) {
+    const float m = s_mix[f];
+    if (f < n) {
+      const float al = ld_any(a.alpha[0], 0, pdt);
+      const float h = __fadd_rn(sigmoid_f(affine_rn(m, al, ld_any(a.bias[0], f, pdt))), a.pre_eps);
+      s_hpre[f] = h;
+      if (a.h_pre) st_any(a.h_pre, tok * n + f, xdt, h);
+    } else if (f < 2 * n) {
+      const float al = ld_any(a.alpha[1], 0, pdt);
+      const float h =
+          __fmul_rn(sigmoid_f(affine_rn(m, al, ld_any(a.bias[1], f - n, pdt))), a.post_mult);
+      st_any(a.h_post, tok * n + (f - n), xdt, h);
+    } else {
+      const int e = f - 2 * n;
+      const float al = ld_any(a.alpha[2], 0, pdt);
+      const float h = round_to(affine_rn(m, al, ld_any(a.bias[2], e, pdt)), xdt);
+      s_mat[e] = h;
+      if (a.h_res_raw) st_any(a.h_res_raw, tok * n * n + e, xdt, h);
+    }
+  }
+  __syncthreads();
+
+  // Sinkhorn-Knopp (model/mhc_fused.py:47-56): thread i owns row i / column i.
+  if (mode == kFull && a.h_res) {
+    const float eps = a.sk_eps;
+    if (tid < n) {
+      float* row = s_mat + tid * n;
+      float mx = row[0];
+      for (int j = 1; j < n; ++j) mx = fmaxf(mx, row[j]);
+      float s = 0.f;
+      for (int j = 0; j < n; ++j) {
+        row[j] = expf(row[j] - mx);
+        s += row[j];
+      }
+      for (int j = 0; j < n; ++j) row[j] = __fadd_rn(__fdiv_rn(row[j], s), eps);
+    }
+    __syncthreads();
+    for (int it = 0; it < a.sk_iters || it == 0; ++it) {
+      if (it > 0) {
+        if (tid < n) {
+          float* row = s_mat + tid * n;
+          float s = 0.f;
+          for (int j = 0; j < n; ++j) s += row[j];
+          const float d = __fadd_rn(s, eps);
+          for (int j = 0; j < n; ++j) row[j] = __fdiv_rn(row[j], d);
+        }
+        __syncthreads();
+      }
+      if (tid < n) {
+        float s = 0.f;
+        for (int i = 0; i < n; ++i) s += s_mat[i * n + tid];
+        const float d = __fadd_rn(s, eps);
+        for (int i = 0; i < n; ++i) s_mat[i * n + tid] = __fdiv_rn(s_mat[i * n + tid], d);
+      }
+      __syncthreads();
+    }
+    for (int e = tid; e < n * n; e += kGenThreads) st_any(a.h_res, tok * n * n + e, xdt, s_mat[e]);
+  }
+
+  // pre-aggregate (or the MHCHead weighted reduce)
+  for (int c = tid; c < C; c += kGenThreads) {
+    float o = 0.f;
+    for (int i = 0; i < n; ++i) o = fmaf(s_hpre[i], ld_any(a.x, xb + (int64_t)i * C + c, xdt), o);
+    st_any(a.sub_in, tok * C + c, xdt, o);
+  }
+}
+
+hipError_t launch_pre_generic(const PreArgs& a, hipStream_t s) {
+  hipLaunchKernelGGL(pre_generic_kernel, dim3((unsigned)a.M), dim3(kGenThreads), 0, s, a);
+  return hipGetLastError();
+}
+
+}  // namespace mhc

@@ -1,0 +1,222 @@
+"""Tensor-level wrappers of the C-ABI entry points (forward kernels only).
+
+Each function validates shapes, allocates the outputs with torch.empty on the
+input's device (the library never allocates), and enqueues the kernel on the
+current stream.  Inputs are made contiguous, as the reference's Functions do
+(model/mhc_fused.py:585-586, :729-732).
+"""
+from __future__ import annotations
+
+import weakref
+from typing import Optional
+
+import torch
+
+from . import _hip as H
+
+
+class PhiPack:
+    """MFMA operand image of a projection weight, rebuilt when the weight changes.
+
+    The cache is valid for one weight tensor object (held by weak reference,
+    so a replaced parameter never aliases a freed one) at one value of its
+    version counter, which every in-place update (optimizer step,
+    load_state_dict, copy_) bumps.  Weights whose version is not tracked
+    (inference tensors) are repacked on every call.  No reference counterpart: the reference's kernels read the
+    row-major weight directly (model/mhc_fused.py:217-229).
+    """
+
+    def __init__(self, mode: int):
+        self.mode = mode
+        self._src = None
+        self._key = None
+        self._buf: Optional[torch.Tensor] = None
+
+    def get(self, phi: torch.Tensor, n: int, C: int) -> Optional[torch.Tensor]:
+        lib = H.load()
+        if phi.dtype != torch.bfloat16:
+            return None
+        nbytes = lib.mhc_phi_packed_bytes(n, C, self.mode)
+        if nbytes <= 0:
+            return None
+        try:
+            version = phi._version
+        except RuntimeError:
+            version = None
+        key = (phi.data_ptr(), version, phi.device, n, C)
+        src = self._src() if self._src is not None else None
+        if version is not None and src is phi and key == self._key and self._buf is not None:
+            return self._buf
+        w = phi.detach().contiguous()
+        buf = torch.empty(nbytes, dtype=torch.uint8, device=phi.device)
+        H.check(lib.mhc_phi_pack(w.data_ptr(), H.DTYPE_BF16, buf.data_ptr(), n, C, self.mode,
+                                 H.stream(phi.device)), "mhc_phi_pack")
+        self._src = weakref.ref(phi)
+        self._key = key if version is not None else None
+        self._buf = buf
+        return buf
+
+
+def _check_numel(name: str, t: torch.Tensor, want: int) -> None:
+    # The kernels index biases by stream / matrix element; a short tensor would be
+    # read out of bounds, so sizes are enforced here (the C ABI sees only pointers).
+    if t.numel() != want:
+        raise ValueError(f"mhc_amd: {name} has {t.numel()} elements, expected {want}")
+
+
+def _rows(x_flat: torch.Tensor, NC: int) -> torch.Tensor:
+    if x_flat.shape[-1] != NC:
+        raise ValueError(f"mhc_amd: last dim {x_flat.shape[-1]} != n*C = {NC}")
+    return x_flat.contiguous().view(-1, NC)
+
+
+def pre_full(x_flat, phi, packed, a_pre, b_pre, a_post, b_post, a_res, b_res, n, C,
+             post_mult, pre_eps, rms_eps, sk_iters, sk_eps, *, sinkhorn=True,
+             want_h_pre=False, want_raw=False, want_saved=False):
+    """Fused pre phase (+ Sinkhorn).  Returns a dict of [M, ...] tensors."""
+    dev = H.require_device(x_flat, phi, a_pre, b_pre, a_post, b_post, a_res, b_res)
+    NC = n * C
+    FD = 2 * n + n * n
+    if tuple(phi.shape) != (NC, FD):
+        raise ValueError(f"mhc_amd: phi_weight shape {tuple(phi.shape)} != ({NC}, {FD})")
+    x2 = _rows(x_flat, NC)
+    M = x2.shape[0]
+    phi_c = phi.detach().contiguous()
+    a_pre, b_pre, a_post, b_post, a_res, b_res = H.params_like(
+        x2, a_pre, b_pre, a_post, b_post, a_res, b_res)
+    for nm, tt, want in (("alpha_pre", a_pre, 1), ("alpha_post", a_post, 1), ("alpha_res", a_res, 1),
+                         ("bias_pre", b_pre, n), ("bias_post", b_post, n), ("bias_res", b_res, n * n)):
+        _check_numel(nm, tt, want)
+    kw = dict(dtype=x2.dtype, device=dev)
+    out = {
+        "sub_in": torch.empty(M, C, **kw),
+        "h_post": torch.empty(M, n, **kw),
+        "h_pre": torch.empty(M, n, **kw) if want_h_pre else None,
+        "h_res_raw": torch.empty(M, n, n, **kw) if want_raw else None,
+        "h_res": torch.empty(M, n, n, **kw) if sinkhorn else None,
+        "inv_rms": torch.empty(M, dtype=torch.float32, device=dev) if want_saved else None,
+        "mixes_raw": torch.empty(M, FD, dtype=torch.float32, device=dev) if want_saved else None,
+    }
+    rc = H.load().mhc_pre_fwd(
+        x2.data_ptr(), H.dtype_tag(x2), phi_c.data_ptr(), H.dtype_tag(phi_c), H.ptr(packed),
+        a_pre.data_ptr(), b_pre.data_ptr(), a_post.data_ptr(), b_post.data_ptr(),
+        a_res.data_ptr(), b_res.data_ptr(), H.dtype_tag(a_pre),
+        out["sub_in"].data_ptr(), H.ptr(out["h_pre"]), out["h_post"].data_ptr(),
+        H.ptr(out["h_res_raw"]), H.ptr(out["h_res"]), H.ptr(out["inv_rms"]),
+        H.ptr(out["mixes_raw"]), M, n, C, float(post_mult), float(pre_eps), float(rms_eps),
+        int(sk_iters), float(sk_eps), H.stream(dev))
+    H.check(rc, "mhc_pre_fwd")
+    return out
+
+
+def pre_nohres(x_flat, phi, packed, a_pre, b_pre, a_post, b_post, n, C, post_mult, pre_eps,
+               rms_eps, *, want_h_pre=False, want_saved=False):
+    dev = H.require_device(x_flat, phi, a_pre, b_pre, a_post, b_post)
+    NC = n * C
+    FD = 2 * n
+    if tuple(phi.shape) != (NC, FD):
+        raise ValueError(f"mhc_amd: phi_weight shape {tuple(phi.shape)} != ({NC}, {FD})")
+    x2 = _rows(x_flat, NC)
+    M = x2.shape[0]
+    phi_c = phi.detach().contiguous()
+    a_pre, b_pre, a_post, b_post = H.params_like(x2, a_pre, b_pre, a_post, b_post)
+    for nm, tt, want in (("alpha_pre", a_pre, 1), ("alpha_post", a_post, 1),
+                         ("bias_pre", b_pre, n), ("bias_post", b_post, n)):
+        _check_numel(nm, tt, want)
+    kw = dict(dtype=x2.dtype, device=dev)
+    out = {
+        "sub_in": torch.empty(M, C, **kw),
+        "h_post": torch.empty(M, n, **kw),
+        "h_pre": torch.empty(M, n, **kw) if want_h_pre else None,
+        "inv_rms": torch.empty(M, dtype=torch.float32, device=dev) if want_saved else None,
+        "mixes_raw": torch.empty(M, FD, dtype=torch.float32, device=dev) if want_saved else None,
+    }
+    rc = H.load().mhc_pre_nohres_fwd(
+        x2.data_ptr(), H.dtype_tag(x2), phi_c.data_ptr(), H.dtype_tag(phi_c), H.ptr(packed),
+        a_pre.data_ptr(), b_pre.data_ptr(), a_post.data_ptr(), b_post.data_ptr(),
+        H.dtype_tag(a_pre), out["sub_in"].data_ptr(), H.ptr(out["h_pre"]),
+        out["h_post"].data_ptr(), H.ptr(out["inv_rms"]), H.ptr(out["mixes_raw"]),
+        M, n, C, float(post_mult), float(pre_eps), float(rms_eps), H.stream(dev))
+    H.check(rc, "mhc_pre_nohres_fwd")
+    return out
+
+
+def head(x_flat, phi, packed, alpha, bias, n, C, pre_eps, rms_eps, *, want_saved=False):
+    """MHCHead forward; n == 1 is the plain RMSNorm (phi/alpha/bias unused)."""
+    NC = n * C
+    x2 = _rows(x_flat, NC)
+    M = x2.shape[0]
+    if n == 1:
+        dev = H.require_device(x_flat)
+        phi_p = a_p = b_p = None
+        phi_dt = pdt = H.DTYPE_F32
+    else:
+        dev = H.require_device(x_flat, phi, alpha, bias)
+        if tuple(phi.shape) != (NC, n):
+            raise ValueError(f"mhc_amd: phi_weight shape {tuple(phi.shape)} != ({NC}, {n})")
+        phi_c = phi.detach().contiguous()
+        alpha_c, bias_c = H.params_like(x2, alpha, bias)
+        _check_numel("alpha", alpha_c, 1)
+        _check_numel("bias", bias_c, n)
+        phi_p, a_p, b_p = phi_c.data_ptr(), alpha_c.data_ptr(), bias_c.data_ptr()
+        phi_dt, pdt = H.dtype_tag(phi_c), H.dtype_tag(alpha_c)
+    out = torch.empty(M, C, dtype=x2.dtype, device=dev)
+    inv = torch.empty(M, dtype=torch.float32, device=dev) if want_saved else None
+    mix = torch.empty(M, n, dtype=torch.float32, device=dev) if (want_saved and n > 1) else None
+    rc = H.load().mhc_head_fwd(
+        x2.data_ptr(), H.dtype_tag(x2), phi_p, phi_dt, H.ptr(packed), a_p, b_p, pdt,
+        out.data_ptr(), H.ptr(inv), H.ptr(mix), M, n, C, float(pre_eps), float(rms_eps),
+        H.stream(dev))
+    H.check(rc, "mhc_head_fwd")
+    return out, inv, mix
+
+
+def post(x_flat, h_res, h_post, f_out, n, C):
+    """out = H_res . x + H_post (x) F; h_res None means identity (use_mhc = 2)."""
+    dev = H.require_device(x_flat, h_res, h_post, f_out)
+    NC = n * C
+    x2 = _rows(x_flat, NC)
+    M = x2.shape[0]
+    hp = h_post.contiguous().view(M, n)
+    f2 = f_out.contiguous().view(M, C)
+    if hp.dtype != (h_res.dtype if h_res is not None else hp.dtype):
+        raise TypeError("mhc_amd: h_res and h_post must share a dtype")
+    out = torch.empty_like(x2)
+    lib = H.load()
+    if h_res is not None:
+        hr = h_res.contiguous().view(M, n, n)
+        rc = lib.mhc_post_fwd(x2.data_ptr(), H.dtype_tag(x2), hr.data_ptr(), hp.data_ptr(),
+                              H.dtype_tag(hp), f2.data_ptr(), H.dtype_tag(f2), out.data_ptr(),
+                              M, n, C, H.stream(dev))
+        H.check(rc, "mhc_post_fwd")
+    else:
+        rc = lib.mhc_post_nohres_fwd(x2.data_ptr(), H.dtype_tag(x2), hp.data_ptr(),
+                                     H.dtype_tag(hp), f2.data_ptr(), H.dtype_tag(f2),
+                                     out.data_ptr(), M, n, C, H.stream(dev))
+        H.check(rc, "mhc_post_nohres_fwd")
+    return out
+
+
+def sinkhorn(m: torch.Tensor, iters: int, eps: float) -> torch.Tensor:
+    dev = H.require_device(m)
+    N = m.shape[-1]
+    if m.dim() < 2 or m.shape[-2] != N:
+        raise ValueError(f"mhc_amd: last two dims must be square, got {tuple(m.shape)}")
+    mc = m.contiguous()
+    out = torch.empty_like(mc)
+    batch = mc.numel() // (N * N) if N > 0 else 0
+    rc = H.load().mhc_sinkhorn_fwd(mc.data_ptr(), out.data_ptr(), H.dtype_tag(mc), batch, N,
+                                   int(iters), float(eps), H.stream(dev))
+    H.check(rc, "mhc_sinkhorn_fwd")
+    return out
+
+
+def stream_expand(x: torch.Tensor, n: int) -> torch.Tensor:
+    dev = H.require_device(x)
+    B, L, D = x.shape
+    xc = x.contiguous()
+    out = torch.empty(B, L, n * D, dtype=x.dtype, device=dev)
+    rc = H.load().mhc_stream_expand_fwd(xc.data_ptr(), out.data_ptr(), xc.element_size(),
+                                        B * L, n, D, H.stream(dev))
+    H.check(rc, "mhc_stream_expand_fwd")
+    return out

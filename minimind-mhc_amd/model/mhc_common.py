@@ -1,0 +1,123 @@
+"""mHC stream entry / exit on MI355X HIP kernels.
+
+Drop-in for the reference module model/mhc_common.py:
+  StreamExpand(n, D) : (B, L, D)   -> (B, L, n*D)   model/mhc_common.py:104-119
+  MHCHead(n, D)      : (B, L, n*D) -> (B, L, D)     model/mhc_common.py:403-450
+Both run hand-written gfx950 kernels through libmhc_amd.so; there is no CPU
+or PyTorch forward path.
+"""
+from __future__ import annotations
+
+import math
+
+import torch
+import torch.nn as nn
+
+from . import _grad, _ops
+from . import _hip as H
+
+
+def _is_pow2(n: int) -> bool:
+    return n >= 1 and (n & (n - 1)) == 0
+
+
+class _StreamExpandFn(torch.autograd.Function):
+    @staticmethod
+    def forward(ctx, x, n):
+        ctx.n = n
+        return _ops.stream_expand(x, n)
+
+    @staticmethod
+    def backward(ctx, g):
+        B, L, ND = g.shape
+        return g.view(B, L, ctx.n, ND // ctx.n).sum(dim=2), None
+
+
+class StreamExpand(nn.Module):
+    """(B, L, D) -> (B, L, n*D): n identical copies of the stream (no parameters)."""
+
+    def __init__(self, n: int, dim: int):
+        super().__init__()
+        self.n = n
+        self.dim = dim
+
+    def forward(self, x: torch.Tensor) -> torch.Tensor:
+        if self.n == 1:
+            return x
+        return _StreamExpandFn.apply(x, self.n)
+
+
+class _MHCHeadFn(torch.autograd.Function):
+    """MHCHead forward on the HIP kernel (model/mhc_common.py:311-400)."""
+
+    @staticmethod
+    def forward(ctx, x_flat, w_phi, alpha, bias, pre_eps, rms_eps, n, c, packed=None):
+        B, L, NC = x_flat.shape
+        train = any(ctx.needs_input_grad)
+        out, inv, mix = _ops.head(x_flat, w_phi, packed, alpha, bias, n, c, pre_eps, rms_eps,
+                                  want_saved=train)
+        if train:
+            ctx.save_for_backward(x_flat.detach().contiguous().view(B * L, NC), w_phi, alpha,
+                                  bias, inv, mix)
+        ctx.cfg = (n, c, float(pre_eps), (B, L, NC))
+        return out.view(B, L, c)
+
+    @staticmethod
+    def backward(ctx, g_out):
+        x2, w, alpha, bias, inv, mix = ctx.saved_tensors
+        n, c, pre_eps, shape = ctx.cfg
+        g_x, g_w, g_a, g_b = _grad.head_backward(x2, w, alpha, bias, inv, mix, n, c, pre_eps,
+                                                 g_out)
+        return (g_x.to(x2.dtype).view(shape), g_w.to(w.dtype), g_a.to(alpha.dtype),
+                g_b.to(bias.dtype), None, None, None, None, None)
+
+
+class _RMSFn(torch.autograd.Function):
+    """y = x * rsqrt(mean(x^2) + eps), no gain (MHCHead with n == 1)."""
+
+    @staticmethod
+    def forward(ctx, x_flat, eps):
+        B, L, C = x_flat.shape
+        out, inv, _ = _ops.head(x_flat, None, None, None, None, 1, C, 0.0, eps,
+                                want_saved=any(ctx.needs_input_grad))
+        if inv is not None:
+            ctx.save_for_backward(x_flat.detach().contiguous().view(B * L, C), inv)
+        return out.view(B, L, C)
+
+    @staticmethod
+    def backward(ctx, g_out):
+        x2, inv = ctx.saved_tensors
+        return _grad.rms_backward(x2, inv, g_out).to(x2.dtype).view(g_out.shape), None
+
+
+class MHCHead(nn.Module):
+    """(B, L, n*D) -> (B, L, D): out = sum_i (sigmoid(alpha * (x_norm . phi)_i + beta_i) + eps) * x_i.
+
+    Same constructor and parameters as the reference (model/mhc_common.py:403-450):
+    phi_weight (n*dim, n), bias (n,), alpha of shape (1,).
+    """
+
+    def __init__(self, n: int, dim: int, alpha_init: float = 0.01,
+                 eps: float = 1e-6, pre_eps: float = 1e-6):
+        super().__init__()
+        assert _is_pow2(n) and n <= 16, f"n must be in {{1,2,4,8,16}}, got {n}"
+        self.n = n
+        self.dim = dim
+        self.nC = n * dim
+        self.eps = eps
+        self.pre_eps = pre_eps
+        self.phi_weight = nn.Parameter(torch.empty(self.nC, n))
+        nn.init.kaiming_uniform_(self.phi_weight, a=math.sqrt(5))
+        self.bias = nn.Parameter(torch.zeros(n))
+        self.alpha = nn.Parameter(torch.full((1,), alpha_init))
+        self._phi_pack = _ops.PhiPack(H.MODE_HEAD)
+
+    def extra_repr(self) -> str:
+        return f"n={self.n}, dim={self.dim}, backend=hip-gfx950"
+
+    def forward(self, x_flat: torch.Tensor) -> torch.Tensor:
+        if self.n == 1:
+            return _RMSFn.apply(x_flat, self.eps)
+        packed = self._phi_pack.get(self.phi_weight, self.n, self.dim) if x_flat.is_cuda else None
+        return _MHCHeadFn.apply(x_flat, self.phi_weight, self.alpha, self.bias,
+                                self.pre_eps, self.eps, self.n, self.dim, packed)

@@ -1,0 +1,118 @@
+"""mHC with H_res frozen to I_n (use_mhc = 2) on MI355X HIP kernels.
+
+Drop-in for the reference module model/mhc_fused_no_hres.py
+(MHCConnection_FusedNoHres, model/mhc_fused_no_hres.py:584-659): the same
+pre-phase kernel with FD = 2n and no Sinkhorn, and the post kernel with
+H_res = I, out = x + H_post (x) F.  No CPU or PyTorch forward path.
+"""
+from __future__ import annotations
+
+import math
+from typing import Callable
+
+import torch
+import torch.nn as nn
+
+from . import _grad, _ops
+from . import _hip as H
+
+
+def _is_pow2(n: int) -> bool:
+    return n >= 1 and (n & (n - 1)) == 0
+
+
+class _PrePhaseFn(torch.autograd.Function):
+    """Pre phase -> (sublayer_in, h_pre, h_post) (model/mhc_fused_no_hres.py:397-529)."""
+
+    @staticmethod
+    def forward(ctx, x_flat, w_phi, alpha_pre, bias_pre, alpha_post, bias_post,
+                post_mult, pre_eps, rms_eps, n, c, packed=None):
+        B, L, NC = x_flat.shape
+        train = any(ctx.needs_input_grad)
+        o = _ops.pre_nohres(x_flat, w_phi, packed, alpha_pre, bias_pre, alpha_post, bias_post,
+                            n, c, post_mult, pre_eps, rms_eps, want_h_pre=True, want_saved=train)
+        if train:
+            ctx.save_for_backward(x_flat.detach().contiguous().view(B * L, NC), w_phi,
+                                  alpha_pre, bias_pre, alpha_post, bias_post,
+                                  o["inv_rms"], o["mixes_raw"])
+        ctx.cfg = (n, c, float(post_mult), float(pre_eps), (B, L, NC))
+        return (o["sub_in"].view(B, L, c), o["h_pre"].view(B, L, n), o["h_post"].view(B, L, n))
+
+    @staticmethod
+    def backward(ctx, g_sub, g_hpre, g_hpost):
+        x2, w, a_pre, b_pre, a_post, b_post, inv, mixes = ctx.saved_tensors
+        n, c, post_mult, pre_eps, shape = ctx.cfg
+        g = _grad.pre_backward(x2, w, a_pre, b_pre, a_post, b_post, None, inv, mixes, n, c,
+                               post_mult, pre_eps, g_sub, g_hpre, g_hpost, None)
+        return (g[0].to(x2.dtype).view(shape), g[1].to(w.dtype),
+                g[2].to(a_pre.dtype).reshape(a_pre.shape), g[3].to(b_pre.dtype),
+                g[4].to(a_post.dtype).reshape(a_post.shape), g[5].to(b_post.dtype),
+                None, None, None, None, None, None)
+
+
+class _PostPhaseFn(torch.autograd.Function):
+    """out = x + H_post (x) F_out (model/mhc_fused_no_hres.py:532-581)."""
+
+    @staticmethod
+    def forward(ctx, x_flat, h_post, f_out, n, c):
+        B, L, NC = x_flat.shape
+        out = _ops.post(x_flat, None, h_post, f_out, n, c)
+        if any(ctx.needs_input_grad):
+            ctx.save_for_backward(h_post, f_out)
+        ctx.cfg = (n, c, (B, L, NC))
+        return out.view(B, L, NC)
+
+    @staticmethod
+    def backward(ctx, g_out):
+        h_post, f_out = ctx.saved_tensors
+        n, c, shape = ctx.cfg
+        M = shape[0] * shape[1]
+        g = g_out.float().reshape(M, n, c)
+        g_hp = torch.bmm(g, f_out.float().reshape(M, c, 1)).squeeze(-1)
+        g_f = torch.bmm(h_post.float().reshape(M, 1, n), g).squeeze(1)
+        return (g_out, g_hp.to(h_post.dtype).view(h_post.shape),
+                g_f.to(f_out.dtype).view(f_out.shape), None, None)
+
+
+class MHCConnection_FusedNoHres(nn.Module):
+    """mHC sublayer wrapper with H_res = I_n: x' = x + H_post (x) F(H_pre . x).
+
+    Same constructor and parameters as the reference
+    (model/mhc_fused_no_hres.py:584-659); phi_weight is (n*dim, 2n) row-major.
+    """
+
+    def __init__(self, n: int, dim: int, alpha_init: float = 0.01,
+                 post_mult_value: float = 2.0, eps: float = 1e-6,
+                 pre_eps: float = 1e-6):
+        super().__init__()
+        assert n >= 1 and isinstance(n, int)
+        assert _is_pow2(n) and n <= 16, f"n must be in {{1,2,4,8,16}}, got {n}"
+        assert post_mult_value > 1.0
+        self.n = n
+        self.dim = dim
+        self.nC = n * dim
+        self.fused_dim = 2 * n
+        self.post_mult_value = post_mult_value
+        self.pre_eps = pre_eps
+        self.eps = eps
+
+        self.phi_weight = nn.Parameter(torch.empty(self.nC, self.fused_dim))
+        nn.init.kaiming_uniform_(self.phi_weight, a=math.sqrt(5))
+        self.alpha_pre = nn.Parameter(torch.tensor(alpha_init))
+        self.bias_pre = nn.Parameter(torch.zeros(n))
+        self.alpha_post = nn.Parameter(torch.tensor(alpha_init))
+        self.bias_post = nn.Parameter(torch.zeros(n))
+        self._phi_pack = _ops.PhiPack(H.MODE_NOHRES)
+
+    def extra_repr(self) -> str:
+        return (f"n={self.n}, dim={self.dim}, fused_dim={self.fused_dim}, "
+                f"post_mult_value={self.post_mult_value}, backend=hip-gfx950")
+
+    def forward(self, x_flat: torch.Tensor, sublayer_fn: Callable) -> torch.Tensor:
+        packed = self._phi_pack.get(self.phi_weight, self.n, self.dim) if x_flat.is_cuda else None
+        sublayer_in, _h_pre, h_post = _PrePhaseFn.apply(
+            x_flat, self.phi_weight, self.alpha_pre, self.bias_pre,
+            self.alpha_post, self.bias_post,
+            self.post_mult_value, self.pre_eps, self.eps, self.n, self.dim, packed)
+        f_out = sublayer_fn(sublayer_in)
+        return _PostPhaseFn.apply(x_flat, h_post, f_out, self.n, self.dim)

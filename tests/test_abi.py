@@ -1,0 +1,74 @@
+"""C-ABI library checks that need no GPU: it loads, exports every symbol
+include/mhc_amd.h declares, and rejects bad arguments before any device work."""
+from __future__ import annotations
+
+import ctypes
+import re
+from pathlib import Path
+
+import pytest
+
+ROOT = Path(__file__).resolve().parent.parent
+HEADER = ROOT / "include" / "mhc_amd.h"
+
+
+@pytest.fixture(scope="module")
+def lib():
+    from model import _hip
+    if not _hip.LIB_PATH.exists():
+        import __graft_entry__
+        __graft_entry__.build()
+    return _hip.load()
+
+
+def declared_functions():
+    text = HEADER.read_text()
+    return sorted(set(re.findall(r"^\s*(?:const char\*|int64_t|int)\s+(mhc_\w+)\s*\(", text, re.M)))
+
+
+def test_header_declares_the_boundary():
+    names = declared_functions()
+    for fn in ("mhc_pre_fwd", "mhc_pre_nohres_fwd", "mhc_post_fwd", "mhc_post_nohres_fwd",
+               "mhc_head_fwd", "mhc_sinkhorn_fwd", "mhc_stream_expand_fwd", "mhc_phi_pack",
+               "mhc_phi_packed_bytes", "mhc_last_error", "mhc_abi_version"):
+        assert fn in names
+
+
+def test_library_exports_every_declared_symbol(lib):
+    raw = ctypes.CDLL(str(ROOT / "minimind-mhc_amd" / "libmhc_amd.so"))
+    for name in declared_functions():
+        assert hasattr(raw, name), name
+
+
+def test_binding_signatures_cover_header(lib):
+    from model import _hip
+    assert set(_hip._SIGNATURES) == set(declared_functions())
+
+
+def test_packed_sizes(lib):
+    # n=4, C=768, full: 4 streams x 24 column blocks x 2 tiles x 64 lanes x 16 B
+    assert lib.mhc_phi_packed_bytes(4, 768, 0) == 4 * 24 * 2 * 64 * 16
+    assert lib.mhc_phi_packed_bytes(8, 768, 0) == 8 * 24 * 5 * 64 * 16   # FD 80 -> 5 tiles
+    assert lib.mhc_phi_packed_bytes(4, 768, 1) == 4 * 24 * 1 * 64 * 16
+    assert lib.mhc_phi_packed_bytes(16, 768, 0) == 0                     # no MFMA instance
+    assert lib.mhc_phi_packed_bytes(4, 100, 0) == 0                      # C % 8 != 0
+    assert lib.mhc_phi_packed_bytes(4, 2048, 0) == 0                     # C > 1024
+    assert lib.mhc_phi_packed_bytes(1, 768, 2) == 0                      # head n=1 is RMSNorm
+
+
+def test_validation_errors_need_no_device(lib):
+    # n = 0 is rejected by argument checks, before any HIP call
+    rc = lib.mhc_pre_fwd(None, 1, None, 1, None, None, None, None, None, None, None, 1,
+                         None, None, None, None, None, None, None, 16, 0, 768,
+                         2.0, 1e-6, 1e-6, 20, 1e-6, None)
+    assert rc == 1
+    assert b"n must be in" in lib.mhc_last_error()
+    rc = lib.mhc_post_fwd(None, 1, None, None, 1, None, 1, None, 16, 4, 768, None)
+    assert rc == 1
+    rc = lib.mhc_sinkhorn_fwd(ctypes.c_void_p(16), ctypes.c_void_p(32), 0, 4, 64, 20, 1e-6, None)
+    assert rc == 1 and b"n must be" in lib.mhc_last_error()
+    rc = lib.mhc_stream_expand_fwd(ctypes.c_void_p(16), ctypes.c_void_p(32), 3, 4, 4, 8, None)
+    assert rc == 1
+    # empty problems succeed without launching
+    assert lib.mhc_sinkhorn_fwd(ctypes.c_void_p(16), ctypes.c_void_p(32), 0, 0, 4, 20, 1e-6, None) == 0
+    assert lib.mhc_phi_pack(None, 0, None, 4, 768, 0, None) == 1  # fp32 phi has no MFMA image

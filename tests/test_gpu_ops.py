@@ -1,0 +1,193 @@
+"""GPU parity of every HIP kernel against the CPU oracle, through the C ABI.
+
+Bars (BASELINE): max|ref-got|/max|ref| <= 1e-2 in bf16 and <= 1e-5 in fp32
+(the reference's comparator, model/mhc_fused.py:871-876); Sinkhorn H_res row
+and column sums within 1e-5 of the oracle's in fp32.
+"""
+from __future__ import annotations
+
+import pytest
+import torch
+
+from oracle import mhc_ref as R
+from tests._util import make_params, maxabs, maxrel, tol
+
+pytestmark = pytest.mark.gpu
+
+from model import _hip as H  # noqa: E402
+from model import _ops  # noqa: E402
+
+
+def _to(p, dev):
+    return {k: v.to(dev) for k, v in p.items()}
+
+
+def _pre_case(dev, n, C, M, dtype, stress, iters, use_pack, seed=0):
+    g = torch.Generator().manual_seed(seed + 31 * n + C + M)
+    x = torch.randn(1, M, n * C, generator=g).to(dtype)
+    p = make_params("full", n, C, dtype, g, stress)
+    pd = _to(p, dev)
+    packed = _ops.PhiPack(H.MODE_FULL).get(pd["phi_weight"], n, C) if use_pack else None
+    o = _ops.pre_full(x.to(dev), pd["phi_weight"], packed, pd["alpha_pre"], pd["bias_pre"],
+                      pd["alpha_post"], pd["bias_post"], pd["alpha_res"], pd["bias_res"], n, C,
+                      2.0, 1e-6, 1e-6, iters, 1e-6, sinkhorn=True, want_h_pre=True,
+                      want_raw=True, want_saved=True)
+    torch.cuda.synchronize()
+    sub, h_pre, h_post, h_raw, inv, mixes = R.pre_full(x, p, n, C)
+    h_res = R.sinkhorn(h_raw.float(), iters, 1e-6).to(dtype)
+    return o, dict(sub=sub[0], h_pre=h_pre[0], h_post=h_post[0], h_raw=h_raw[0],
+                   h_res=h_res[0], inv=inv[0], mixes=mixes[0]), packed
+
+
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float32])
+@pytest.mark.parametrize("n,C", [(4, 768), (4, 64), (8, 768), (2, 256), (1, 128), (16, 64),
+                                 (4, 104), (4, 100), (4, 2048)])
+@pytest.mark.parametrize("M", [1, 17, 64])
+def test_pre_full_vs_oracle(dev, dtype, n, C, M):
+    o, r, packed = _pre_case(dev, n, C, M, dtype, stress=True, iters=20, use_pack=True)
+    mfma = packed is not None
+    print(f"pre n={n} C={C} M={M} {dtype} mfma={mfma}", flush=True)
+    bar = tol(dtype)
+    assert maxrel(r["sub"], o["sub_in"]) <= bar
+    assert maxrel(r["h_pre"], o["h_pre"]) <= bar
+    assert maxrel(r["h_post"], o["h_post"]) <= bar
+    assert maxrel(r["h_raw"], o["h_res_raw"]) <= (2e-2 if dtype == torch.bfloat16 else 1e-5)
+    assert maxrel(r["inv"], o["inv_rms"]) <= 1e-5
+    # The oracle's projection rounds x_norm and mixes to bf16; the kernels keep fp32.
+    assert maxrel(r["mixes"], o["mixes_raw"]) <= (2e-2 if dtype == torch.bfloat16 else 1e-5)
+    assert maxabs(r["h_res"], o["h_res"]) <= (1e-2 if dtype == torch.bfloat16 else 1e-5)
+    if dtype == torch.float32:
+        for dim in (-1, -2):
+            assert maxabs(r["h_res"].sum(dim), o["h_res"].sum(dim)) <= 1e-5
+
+
+@pytest.mark.parametrize("n,C", [(4, 768), (8, 768), (2, 512)])
+def test_pre_mfma_matches_generic(dev, n, C):
+    """The MFMA kernel and the generic VALU kernel agree on the same bf16 input."""
+    a, _, packed = _pre_case(dev, n, C, 48, torch.bfloat16, True, 20, use_pack=True, seed=5)
+    b, _, _ = _pre_case(dev, n, C, 48, torch.bfloat16, True, 20, use_pack=False, seed=5)
+    assert packed is not None
+    assert maxrel(b["mixes_raw"], a["mixes_raw"]) <= 1e-5
+    assert maxrel(b["inv_rms"], a["inv_rms"]) <= 1e-6
+    for k in ("sub_in", "h_post", "h_res"):
+        assert maxrel(b[k], a[k]) <= 1e-2, k
+
+
+@pytest.mark.parametrize("iters", [0, 1, 10, 20])
+def test_pre_sinkhorn_iteration_counts(dev, iters):
+    o, r, _ = _pre_case(dev, 4, 768, 32, torch.float32, True, iters, use_pack=True)
+    assert maxabs(r["h_res"], o["h_res"]) <= 1e-5
+
+
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float32])
+@pytest.mark.parametrize("n,C", [(4, 768), (8, 768), (2, 64), (1, 96), (4, 100), (16, 32)])
+def test_pre_nohres_vs_oracle(dev, dtype, n, C):
+    g = torch.Generator().manual_seed(11 + n + C)
+    M = 40
+    x = torch.randn(1, M, n * C, generator=g).to(dtype)
+    p = make_params("nohres", n, C, dtype, g)
+    pd = _to(p, dev)
+    packed = _ops.PhiPack(H.MODE_NOHRES).get(pd["phi_weight"], n, C)
+    o = _ops.pre_nohres(x.to(dev), pd["phi_weight"], packed, pd["alpha_pre"], pd["bias_pre"],
+                        pd["alpha_post"], pd["bias_post"], n, C, 2.0, 1e-6, 1e-6, want_h_pre=True,
+                        want_saved=True)
+    sub, h_pre, h_post, inv, mixes = R.pre_nohres(x, p, n, C)
+    bar = tol(dtype)
+    assert maxrel(sub[0], o["sub_in"]) <= bar
+    assert maxrel(h_pre[0], o["h_pre"]) <= bar
+    assert maxrel(h_post[0], o["h_post"]) <= bar
+
+
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float32])
+@pytest.mark.parametrize("n,C", [(4, 768), (8, 768), (2, 64), (1, 768), (4, 100), (16, 32)])
+def test_head_vs_oracle(dev, dtype, n, C):
+    g = torch.Generator().manual_seed(17 + n + C)
+    M = 33
+    x = torch.randn(1, M, n * C, generator=g).to(dtype)
+    p = make_params("head", n, C, dtype, g, phi_std=0.05)
+    pd = _to(p, dev)
+    packed = _ops.PhiPack(H.MODE_HEAD).get(pd["phi_weight"], n, C) if n > 1 else None
+    out, inv, mix = _ops.head(x.to(dev), pd["phi_weight"], packed, pd["alpha"], pd["bias"], n, C,
+                              1e-6, 1e-6, want_saved=True)
+    ref = R.head(x, p, n, C)
+    assert maxrel(ref[0], out) <= tol(dtype)
+
+
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float32])
+@pytest.mark.parametrize("n,C", [(4, 768), (8, 768), (2, 64), (1, 64), (4, 100), (16, 32)])
+@pytest.mark.parametrize("res", [True, False])
+def test_post_vs_oracle(dev, dtype, n, C, res):
+    g = torch.Generator().manual_seed(23 + n + C)
+    M = 70
+    x = torch.randn(1, M, n * C, generator=g).to(dtype)
+    h_res = R.sinkhorn(torch.randn(1, M, n, n, generator=g), 10, 1e-6).to(dtype)
+    h_post = (torch.rand(1, M, n, generator=g) * 2).to(dtype)
+    f = torch.randn(1, M, C, generator=g).to(dtype)
+    got = _ops.post(x.to(dev), h_res.to(dev) if res else None, h_post.to(dev), f.to(dev), n, C)
+    ref = R.post_full(x, h_res, h_post, f, n, C) if res else R.post_nohres(x, h_post, f, n, C)
+    assert maxrel(ref[0], got) <= tol(dtype)
+
+
+def test_post_mixed_dtypes(dev):
+    """Autocast training keeps the stream fp32 while F returns bf16
+    (model/mhc_fused.py:733, :441): the generic kernel casts on load."""
+    n, C, M = 4, 64, 20
+    g = torch.Generator().manual_seed(3)
+    x = torch.randn(1, M, n * C, generator=g)
+    h_res = R.sinkhorn(torch.randn(1, M, n, n, generator=g), 10, 1e-6)
+    h_post = torch.rand(1, M, n, generator=g) * 2
+    f = torch.randn(1, M, C, generator=g).to(torch.bfloat16)
+    got = _ops.post(x.to(dev), h_res.to(dev), h_post.to(dev), f.to(dev), n, C)
+    ref = R.post_full(x, h_res, h_post, f.float(), n, C)
+    assert got.dtype == torch.float32
+    assert maxrel(ref[0], got) <= 1e-5
+
+
+@pytest.mark.parametrize("n", [1, 2, 3, 4, 5, 8, 16])
+@pytest.mark.parametrize("iters", [0, 1, 10, 20])
+def test_sinkhorn_vs_oracle(dev, n, iters):
+    g = torch.Generator().manual_seed(n * 7 + iters)
+    M = torch.randn(3, 37, n, n, generator=g)
+    got = _ops.sinkhorn(M.to(dev), iters, 1e-6)
+    ref = R.sinkhorn(M, iters, 1e-6)
+    assert maxabs(ref, got) <= 1e-5
+    for dim in (-1, -2):
+        assert maxabs(ref.sum(dim), got.sum(dim)) <= 1e-5
+
+
+def test_sinkhorn_bf16_io(dev):
+    g = torch.Generator().manual_seed(1)
+    M = torch.randn(100, 4, 4, generator=g).to(torch.bfloat16)
+    got = _ops.sinkhorn(M.to(dev), 20, 1e-6)
+    assert got.dtype == torch.bfloat16
+    ref = R.sinkhorn(M.float(), 20, 1e-6).to(torch.bfloat16)  # fp32 math, bf16 store
+    assert maxabs(ref, got) <= 2 ** -8
+
+
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float32])
+@pytest.mark.parametrize("n,C", [(4, 768), (8, 100), (2, 3)])
+def test_stream_expand_exact(dev, dtype, n, C):
+    x = torch.randn(2, 9, C).to(dtype)
+    got = _ops.stream_expand(x.to(dev), n)
+    assert torch.equal(got.cpu(), R.stream_expand(x, n))
+
+
+def test_empty_batch(dev):
+    n, C = 4, 768
+    g = torch.Generator().manual_seed(0)
+    p = _to(make_params("full", n, C, torch.bfloat16, g), dev)
+    x = torch.empty(1, 0, n * C, dtype=torch.bfloat16, device=dev)
+    o = _ops.pre_full(x, p["phi_weight"], None, p["alpha_pre"], p["bias_pre"], p["alpha_post"],
+                      p["bias_post"], p["alpha_res"], p["bias_res"], n, C, 2.0, 1e-6, 1e-6, 20, 1e-6)
+    assert o["sub_in"].shape == (0, C)
+    out = _ops.post(x, o["h_res"].view(1, 0, n, n), o["h_post"].view(1, 0, n),
+                    torch.empty(1, 0, C, dtype=torch.bfloat16, device=dev), n, C)
+    assert out.shape == (0, n * C)
+
+
+def test_bad_arguments_raise(dev):
+    x = torch.randn(1, 4, 4 * 64, device=dev)
+    with pytest.raises(ValueError):
+        _ops.post(x, None, torch.rand(1, 4, 4, device=dev), torch.randn(1, 4, 64, device=dev), 4, 32)
+    with pytest.raises(RuntimeError, match="n must be"):
+        _ops.sinkhorn(torch.randn(2, 40, 40, device=dev), 3, 1e-6)
