@@ -36,6 +36,7 @@ int check_pre(const mhc::PreArgs& a, const char* fn) {
   if (a.C < 1) return fail(hipErrorInvalidValue, "%s: C must be >= 1 (got %d)", fn, a.C);
   if (!dtype_ok(a.x_dtype)) return fail(hipErrorInvalidValue, "%s: bad x dtype %d", fn, a.x_dtype);
   if (a.M > kMaxBlocks) return fail(hipErrorInvalidValue, "%s: M too large", fn);
+  if (a.M == 0) return 0;  // empty batch: nothing to read or write (pointers may be null)
   if (!a.x || !a.sub_in) return fail(hipErrorInvalidValue, "%s: x and the main output are required", fn);
   if (a.mode != mhc::kRms) {
     if (!a.phi) return fail(hipErrorInvalidValue, "%s: phi is required", fn);
@@ -181,17 +182,17 @@ static int run_post(mhc::PostArgs& a, hipStream_t stream, const char* fn) {
   if (a.C < 1) return fail(hipErrorInvalidValue, "%s: C must be >= 1", fn);
   if (!dtype_ok(a.x_dtype) || !dtype_ok(a.h_dtype) || !dtype_ok(a.f_dtype))
     return fail(hipErrorInvalidValue, "%s: bad dtype", fn);
-  if (!a.x || !a.h_post || !a.f_out || !a.out) return fail(hipErrorInvalidValue, "%s: null pointer", fn);
-  if (a.out == a.x) return fail(hipErrorInvalidValue, "%s: out must not alias x", fn);
   if (a.M * a.n * (int64_t)a.C / 256 + 1 > kMaxBlocks) return fail(hipErrorInvalidValue, "%s: problem too large", fn);
   if (a.M == 0) return 0;
+  if (!a.x || !a.h_post || !a.f_out || !a.out) return fail(hipErrorInvalidValue, "%s: null pointer", fn);
+  if (a.out == a.x) return fail(hipErrorInvalidValue, "%s: out must not alias x", fn);
   return hip_status(mhc::launch_post(a, stream), fn);
 }
 
 int mhc_post_fwd(const void* x, int x_dtype, const void* h_res, const void* h_post, int h_dtype,
                  const void* f_out, int f_dtype, void* out, int64_t M, int n, int C,
                  hipStream_t stream) {
-  if (!h_res) return fail(hipErrorInvalidValue, "mhc_post_fwd: h_res is required");
+  if (!h_res && M != 0) return fail(hipErrorInvalidValue, "mhc_post_fwd: h_res is required");
   mhc::PostArgs a{x, h_res, h_post, f_out, out, M, n, C, x_dtype, h_dtype, f_dtype};
   return run_post(a, stream, "mhc_post_fwd");
 }
@@ -208,9 +209,9 @@ int mhc_sinkhorn_fwd(const void* m_in, void* m_out, int dtype, int64_t batch, in
   if (batch < 0) return fail(hipErrorInvalidValue, "mhc_sinkhorn_fwd: batch must be >= 0");
   if (n < 1 || n > 32) return fail(hipErrorInvalidValue, "mhc_sinkhorn_fwd: n must be in [1, 32] (got %d)", n);
   if (!dtype_ok(dtype)) return fail(hipErrorInvalidValue, "mhc_sinkhorn_fwd: bad dtype %d", dtype);
-  if (!m_in || !m_out) return fail(hipErrorInvalidValue, "mhc_sinkhorn_fwd: null pointer");
   if (batch > kMaxBlocks) return fail(hipErrorInvalidValue, "mhc_sinkhorn_fwd: batch too large");
   if (batch == 0) return 0;
+  if (!m_in || !m_out) return fail(hipErrorInvalidValue, "mhc_sinkhorn_fwd: null pointer");
   return hip_status(mhc::launch_sinkhorn(m_in, m_out, dtype, batch, n, iters, eps, stream),
                     "mhc_sinkhorn_fwd");
 }
@@ -220,10 +221,10 @@ int mhc_stream_expand_fwd(const void* x, void* out, int elem_bytes, int64_t M, i
   if (elem_bytes != 2 && elem_bytes != 4)
     return fail(hipErrorInvalidValue, "mhc_stream_expand_fwd: elem_bytes must be 2 or 4");
   if (M < 0 || n < 1 || C < 1) return fail(hipErrorInvalidValue, "mhc_stream_expand_fwd: bad shape");
-  if (!x || !out) return fail(hipErrorInvalidValue, "mhc_stream_expand_fwd: null pointer");
   if (M * n * (int64_t)C / 256 + 1 > kMaxBlocks)
     return fail(hipErrorInvalidValue, "mhc_stream_expand_fwd: problem too large");
   if (M == 0) return 0;
+  if (!x || !out) return fail(hipErrorInvalidValue, "mhc_stream_expand_fwd: null pointer");
   return hip_status(mhc::launch_stream_expand(x, out, elem_bytes, M, n, C, stream),
                     "mhc_stream_expand_fwd");
 }

@@ -15,11 +15,35 @@ enum Dtype : int { kF32 = 0, kBF16 = 1, kF16 = 2 };
 __host__ __device__ inline int dtype_bytes(int dt) { return dt == kF32 ? 4 : 2; }
 
 typedef __attribute__((__vector_size__(8 * sizeof(__bf16)))) __bf16 bf16x8_t;
+typedef __attribute__((__vector_size__(2 * sizeof(__bf16)))) __bf16 bf16x2_t;
 typedef __attribute__((__vector_size__(4 * sizeof(float)))) float f32x4_t;
 
 struct alignas(16) U32x4 {
   uint32_t v[4];
 };
+
+// ------------------------------------------------------------ buffer access
+// Raw buffer loads/stores bounded by a descriptor's byte count: an offset past
+// the end reads zeros / drops the write in hardware.  Masking through the
+// descriptor instead of a branch keeps every lane's load unconditional, so the
+// compiler can count outstanding loads exactly (s_waitcnt vmcnt(N) rather than
+// vmcnt(0)) and prefetched data stays in flight.
+typedef unsigned int u32x4_t __attribute__((ext_vector_type(4)));
+constexpr int kBufDword3 = 0x00020000;   // raw buffer, gfx9-family dword 3
+constexpr uint32_t kBufOob = 0x7FFFFFF0u; // an offset past any descriptor used here
+
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t make_rsrc(const void* base, uint32_t bytes) {
+  return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), (short)0, (int)bytes,
+                                           kBufDword3);
+}
+
+__device__ __forceinline__ U32x4 buf_load16(__amdgpu_buffer_rsrc_t r, uint32_t off) {
+  return __builtin_bit_cast(U32x4, __builtin_amdgcn_raw_buffer_load_b128(r, (int)off, 0, 0));
+}
+
+__device__ __forceinline__ void buf_store16(__amdgpu_buffer_rsrc_t r, uint32_t off, const U32x4& v) {
+  __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(u32x4_t, v), r, (int)off, 0, 0);
+}
 
 // ---------------------------------------------------------------- conversions
 
@@ -87,46 +111,156 @@ __device__ __forceinline__ float affine_rn(float s, float alpha, float beta) {
   return __fadd_rn(__fmul_rn(s, alpha), beta);
 }
 
-// ------------------------------------------------------ lane-group reductions
-// Butterfly reductions over xor-partners: every lane of the group ends with the
-// bit-identical result, so all lanes of one Sinkhorn row see the same sum.
+// ---------------------------------------------- reference rounding points
+// The reference's PyTorch path evaluates the gates as separate torch ops on
+// tensors of the stream dtype (model/mhc_fused.py:846-854): the projection
+// output mixes is a stream-dtype tensor, then (m * alpha), (+ bias),
+// sigmoid, and (+ pre_eps) / (* post_mult) each round to that dtype.  These
+// helpers apply the same roundings (all no-ops for fp32 streams).
 
-template <int MASK_LO, int MASK_HI>
-__device__ __forceinline__ float xor_sum(float v) {
+// sigmoid(alpha * m + bias) with the reference's roundings.
+__device__ __forceinline__ float gate_sigmoid(float m, float alpha, float bias, int dt) {
+  const float mq = round_to(m, dt);
+  const float z = round_to(__fadd_rn(round_to(__fmul_rn(mq, alpha), dt), bias), dt);
+  return round_to(sigmoid_f(z), dt);
+}
+
+// h_pre (and the MHCHead mix): sigmoid(...) + pre_eps
+__device__ __forceinline__ float gate_pre(float m, float alpha, float bias, float pre_eps, int dt) {
+  return round_to(__fadd_rn(gate_sigmoid(m, alpha, bias, dt), pre_eps), dt);
+}
+
+// h_post: sigmoid(...) * post_mult
+__device__ __forceinline__ float gate_post(float m, float alpha, float bias, float post_mult, int dt) {
+  return round_to(__fmul_rn(gate_sigmoid(m, alpha, bias, dt), post_mult), dt);
+}
+
+// h_res_raw: alpha * m + bias (Sinkhorn then runs in fp32 on this value)
+__device__ __forceinline__ float gate_res(float m, float alpha, float bias, int dt) {
+  return round_to(__fadd_rn(round_to(__fmul_rn(round_to(m, dt), alpha), dt), bias), dt);
+}
+
+// ------------------------------------------- pre-aggregate on packed bf16
+// sub_in[c] = bf16( sum_i bf16(h_i * x_i[c]) ) for one 16-byte chunk (8
+// columns) of each of the N streams, with the reference's rounding points
+// (model/mhc_fused.py:859: each product is a bf16 tensor element, the sum over
+// streams accumulates in fp32).  v_dot2c_f32_bf16 forms each product exactly
+// from the packed pair (h_i is bf16, so h_i * x is exact in fp32) with no
+// unpacking: (x_lo, x_hi) . (h, 0) and (x_lo, x_hi) . (0, h).  Two streams'
+// rounded products share one packed register and one dot2 with (1, 1) adds
+// both into the fp32 sum.
+__device__ __forceinline__ float dot2_bf16(uint32_t a, uint32_t b, float c) {
+  return __builtin_amdgcn_fdot2_f32_bf16(__builtin_bit_cast(bf16x2_t, a),
+                                         __builtin_bit_cast(bf16x2_t, b), c, false);
+}
+
+template <int N>
+__device__ __forceinline__ U32x4 preagg_chunk(const U32x4 (&x)[N], const uint32_t (&hlo)[N],
+                                             const uint32_t (&hhi)[N]) {
+  constexpr uint32_t kOnes = 0x3F803F80u;  // bf16 (1.0, 1.0)
+  U32x4 out;
 #pragma unroll
-  for (int m = MASK_LO; m < MASK_HI; m <<= 1) v = __fadd_rn(v, __shfl_xor(v, m, 64));
+  for (int j = 0; j < 4; ++j) {
+    float plo[N];
+    float phi_[N];
+#pragma unroll
+    for (int i = 0; i < N; ++i) {
+      plo[i] = dot2_bf16(x[i].v[j], hlo[i], 0.f);
+      phi_[i] = dot2_bf16(x[i].v[j], hhi[i], 0.f);
+    }
+    float slo;
+    float shi;
+    if constexpr (N == 1) {
+      slo = plo[0];
+      shi = phi_[0];
+    } else {
+      slo = 0.f;
+      shi = 0.f;
+#pragma unroll
+      for (int i = 0; i < N; i += 2) {
+        slo = dot2_bf16(pack_bf16x2(plo[i], plo[i + 1]), kOnes, slo);
+        shi = dot2_bf16(pack_bf16x2(phi_[i], phi_[i + 1]), kOnes, shi);
+      }
+    }
+    out.v[j] = pack_bf16x2(slo, shi);
+  }
+  return out;
+}
+
+// (h, 0) and (0, h) packed bf16 pairs for preagg_chunk; h must be bf16-exact.
+__device__ __forceinline__ uint32_t pack_lo(float h) { return (uint32_t)f32_to_bf16_bits(h); }
+__device__ __forceinline__ uint32_t pack_hi(float h) { return (uint32_t)f32_to_bf16_bits(h) << 16; }
+
+// ------------------------------------------------------ lane-group reductions
+// Sinkhorn keeps one matrix element per lane; row and column sums are
+// butterflies over lane groups.  Within 16-lane rows they use DPP (fused into
+// v_add_f32_dpp): quad_perm for lane xor 1 / 2, row_ror:8 for xor 8, and
+// row_ror:4 / row_half_mirror for xor 4 once the value is already symmetric
+// under xor 8 / within quads (so every lane of a group ends with the
+// bit-identical sum).  Partners 16 and 32 lanes apart use ds_swizzle/bpermute.
+
+template <int CTRL>
+__device__ __forceinline__ float dpp_f(float v) {
+  return __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, v), CTRL,
+                                                               0xF, 0xF, true));
+}
+
+constexpr int kDppXor1 = 0xB1;        // quad_perm [1,0,3,2]
+constexpr int kDppXor2 = 0x4E;        // quad_perm [2,3,0,1]
+constexpr int kDppRor4 = 0x124;       // row_ror:4
+constexpr int kDppRor8 = 0x128;       // row_ror:8  (== lane xor 8 inside a row)
+constexpr int kDppHalfMirror = 0x141; // row_half_mirror (lane i <-> 7-i in each 8)
+
+struct OpAdd {
+  __device__ static float f(float a, float b) { return a + b; }
+};
+struct OpMax {
+  __device__ static float f(float a, float b) { return fmaxf(a, b); }
+};
+
+// Reduce over the N consecutive lanes of one matrix row (N in {1, 2, 4, 8}).
+template <int N, typename Op>
+__device__ __forceinline__ float row_reduce(float v) {
+  if constexpr (N >= 2) v = Op::f(v, dpp_f<kDppXor1>(v));
+  if constexpr (N >= 4) v = Op::f(v, dpp_f<kDppXor2>(v));
+  if constexpr (N >= 8) v = Op::f(v, dpp_f<kDppHalfMirror>(v));
   return v;
 }
 
-template <int MASK_LO, int MASK_HI>
-__device__ __forceinline__ float xor_max(float v) {
-#pragma unroll
-  for (int m = MASK_LO; m < MASK_HI; m <<= 1) v = fmaxf(v, __shfl_xor(v, m, 64));
+// Reduce over the N lanes of one matrix column (stride N inside N*N lanes).
+template <int N>
+__device__ __forceinline__ float col_sum(float v) {
+  if constexpr (N == 2) {
+    v = v + dpp_f<kDppXor2>(v);
+  } else if constexpr (N == 4) {
+    v = v + dpp_f<kDppRor8>(v);
+    v = v + dpp_f<kDppRor4>(v);
+  } else if constexpr (N == 8) {
+    v = v + dpp_f<kDppRor8>(v);
+    v = v + __shfl_xor(v, 16, 64);
+    v = v + __shfl_xor(v, 32, 64);
+  }
   return v;
 }
 
 // Sinkhorn-Knopp projection of one n x n matrix held one element per lane.
 // The group is N*N consecutive lanes (N a power of two, N*N <= 64); lane e of
-// the group holds element (row = e / N, col = e % N).  Row partners differ in
-// the low log2(N) lane bits, column partners in the next log2(N) bits.
+// the group holds element (row = e / N, col = e % N).
 //
 // Schedule (model/mhc_fused.py:47-56): softmax over each row, + eps, one column
 // normalisation, then (iters - 1) x (row, column) normalisations, each dividing
-// by (sum + eps).
+// by (sum + eps).  Divisions use the hardware reciprocal (<= 1 ulp) and a
+// multiply; sums are fp32 butterflies.
 template <int N>
 __device__ __forceinline__ float sinkhorn_lane(float v, int iters, float eps) {
-  constexpr int NN = N * N;
-  float mx = xor_max<1, N>(v);
-  float e = expf(v - mx);
-  float s = xor_sum<1, N>(e);
-  v = __fadd_rn(__fdiv_rn(e, s), eps);
-  float cs = xor_sum<N, NN>(v);
-  v = __fdiv_rn(v, __fadd_rn(cs, eps));
+  const float mx = row_reduce<N, OpMax>(v);
+  const float e = expf(v - mx);
+  const float s = row_reduce<N, OpAdd>(e);
+  v = e * __builtin_amdgcn_rcpf(s) + eps;
+  v = v * __builtin_amdgcn_rcpf(col_sum<N>(v) + eps);
   for (int it = 1; it < iters; ++it) {
-    float rs = xor_sum<1, N>(v);
-    v = __fdiv_rn(v, __fadd_rn(rs, eps));
-    cs = xor_sum<N, NN>(v);
-    v = __fdiv_rn(v, __fadd_rn(cs, eps));
+    v = v * __builtin_amdgcn_rcpf(row_reduce<N, OpAdd>(v) + eps);
+    v = v * __builtin_amdgcn_rcpf(col_sum<N>(v) + eps);
   }
   return v;
 }

@@ -5,7 +5,7 @@
 //
 // Reference: model/mhc_fused.py:416-459 (fused kernel), :562-568 (ref),
 // model/mhc_fused_no_hres.py:284-316, :389-394.  fp32 arithmetic, one rounding
-// at the store, like the reference's fused kernel.
+// at each point where the reference's torch ops round (see post_vec_kernel).
 //
 // Work split: one thread per (token, V-column chunk), V = 16 bytes of x.  The
 // thread reads the n chunks of x at that column, the F chunk, and the token's
@@ -55,6 +55,15 @@ __device__ __forceinline__ void store_pack(T* p, const float (&o)[K]) {
   *reinterpret_cast<Pack<T, K>*>(p) = pk;
 }
 
+// Value after a store to / reload from element type T.
+template <typename T>
+__device__ __forceinline__ float rnd(float v) {
+  return Elem<T>::get(Elem<T>::put(v));
+}
+
+// Rounding points follow the reference's torch ops (model/mhc_fused.py:861-863):
+// the einsum result, the H_post * F product and their sum are each a tensor of
+// the stream dtype.
 template <typename XT, typename FT, int N, bool RES>
 __global__ __launch_bounds__(256) void post_vec_kernel(PostArgs a) {
   constexpr int V = 16 / sizeof(XT);
@@ -88,10 +97,11 @@ __global__ __launch_bounds__(256) void post_vec_kernel(PostArgs a) {
         acc = 0.f;
 #pragma unroll
         for (int j = 0; j < N; ++j) acc = fmaf(hr[i * N + j], xv[j][v], acc);
+        acc = rnd<XT>(acc);
       } else {
         acc = xv[i][v];
       }
-      o[v] = fmaf(hp[i], fv[v], acc);
+      o[v] = __fadd_rn(acc, rnd<XT>(__fmul_rn(hp[i], fv[v])));
     }
     store_pack<XT, V>(out + (int64_t)i * C, o);
   }
@@ -109,18 +119,20 @@ __global__ __launch_bounds__(256) void post_generic_kernel(PostArgs a) {
   const int i = (int)(rem / C);
   const int c = (int)(rem - (int64_t)i * C);
   const int64_t xb = tok * per_tok;
+  const int xdt = a.x_dtype;
   float acc;
   if (a.h_res) {
     acc = 0.f;
     for (int j = 0; j < n; ++j)
       acc = fmaf(ld_any(a.h_res, tok * n * n + i * n + j, a.h_dtype),
-                 ld_any(a.x, xb + (int64_t)j * C + c, a.x_dtype), acc);
+                 ld_any(a.x, xb + (int64_t)j * C + c, xdt), acc);
+    acc = round_to(acc, xdt);
   } else {
-    acc = ld_any(a.x, xb + (int64_t)i * C + c, a.x_dtype);
+    acc = ld_any(a.x, xb + (int64_t)i * C + c, xdt);
   }
-  const float r = fmaf(ld_any(a.h_post, tok * n + i, a.h_dtype),
-                       ld_any(a.f_out, tok * C + c, a.f_dtype), acc);
-  st_any(a.out, xb + (int64_t)i * C + c, a.x_dtype, r);
+  const float wb = round_to(__fmul_rn(ld_any(a.h_post, tok * n + i, a.h_dtype),
+                                      ld_any(a.f_out, tok * C + c, a.f_dtype)), xdt);
+  st_any(a.out, xb + (int64_t)i * C + c, xdt, __fadd_rn(acc, wb));
 }
 
 template <typename XT, typename FT, int N>

@@ -3,11 +3,11 @@
 // The generic kernel serves every (dtype, n, C) the MFMA instances do not:
 // fp32 / fp16 streams, fp32 phi, n == 16, C > 1024 or C % 8 != 0, and the
 // n == 1 MHCHead (plain RMSNorm).  One 256-thread workgroup per token; it is a
-// correctness path, not a tuned one.  Its arithmetic follows the reference's
-// fused kernel: x_norm = x * inv_rms in fp32, fp32 projection, gates in fp32,
-// outputs rounded once to the stream dtype (model/mhc_fused.py:205-268,
-// model/mhc_fused_no_hres.py:48-145, model/mhc_common.py:128-195).
-#include "mhc_pre_mfma.hpp"
+// correctness path, not a tuned one.  x_norm = x * inv_rms and the projection
+// are fp32; the gates and the pre-aggregate round where the reference's torch
+// ops round (model/mhc_fused.py:843-859, model/mhc_fused_no_hres.py:364-386,
+// model/mhc_common.py:298-308).
+#include "mhc_pre_persist.hpp"
 
 namespace mhc {
 
@@ -64,7 +64,31 @@ hipError_t launch_phi_pack(const void* phi, int phi_dtype, void* packed, int n, 
   return hipGetLastError();
 }
 
+// Compute units of the current device (cached; one persistent workgroup each).
+static int device_cus() {
+  static int cache[64] = {0};
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess) dev = 0;
+  if (dev >= 0 && dev < 64 && cache[dev] > 0) return cache[dev];
+  int cus = 0;
+  if (hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || cus <= 0)
+    cus = 256;
+  if (dev >= 0 && dev < 64) cache[dev] = cus;
+  return cus;
+}
+
 hipError_t launch_pre_mfma(const PreArgs& a, hipStream_t s) {
+  // n <= 4: persistent workgroups with the x tile double-buffered in registers.
+  if (a.n <= 4) {
+    const int kb = persist_kb_needed(a.C);
+    const int cus = device_cus();
+    switch (a.n) {
+      case 1: return launch_pre_persist_n1(a, kb, cus, s);
+      case 2: return launch_pre_persist_n2(a, kb, cus, s);
+      case 4: return launch_pre_persist_n4(a, kb, cus, s);
+      default: break;
+    }
+  }
   const int kb = pre_mfma_kb_needed(a.n, a.C);
   switch (a.n) {
     case 1: return launch_pre_mfma_n1(a, kb, s);
@@ -165,19 +189,16 @@ __global__ __launch_bounds__(kGenThreads) void pre_generic_kernel(PreArgs a) {
   for (int f = tid; f < FD; f += kGenThreads) {
     const float m = s_mix[f];
     if (f < n) {
-      const float al = ld_any(a.alpha[0], 0, pdt);
-      const float h = __fadd_rn(sigmoid_f(affine_rn(m, al, ld_any(a.bias[0], f, pdt))), a.pre_eps);
+      const float h = gate_pre(m, ld_any(a.alpha[0], 0, pdt), ld_any(a.bias[0], f, pdt), a.pre_eps, xdt);
       s_hpre[f] = h;
       if (a.h_pre) st_any(a.h_pre, tok * n + f, xdt, h);
     } else if (f < 2 * n) {
-      const float al = ld_any(a.alpha[1], 0, pdt);
-      const float h =
-          __fmul_rn(sigmoid_f(affine_rn(m, al, ld_any(a.bias[1], f - n, pdt))), a.post_mult);
+      const float h = gate_post(m, ld_any(a.alpha[1], 0, pdt), ld_any(a.bias[1], f - n, pdt),
+                                a.post_mult, xdt);
       st_any(a.h_post, tok * n + (f - n), xdt, h);
     } else {
       const int e = f - 2 * n;
-      const float al = ld_any(a.alpha[2], 0, pdt);
-      const float h = round_to(affine_rn(m, al, ld_any(a.bias[2], e, pdt)), xdt);
+      const float h = gate_res(m, ld_any(a.alpha[2], 0, pdt), ld_any(a.bias[2], e, pdt), xdt);
       s_mat[e] = h;
       if (a.h_res_raw) st_any(a.h_res_raw, tok * n * n + e, xdt, h);
     }
@@ -221,10 +242,13 @@ __global__ __launch_bounds__(kGenThreads) void pre_generic_kernel(PreArgs a) {
     for (int e = tid; e < n * n; e += kGenThreads) st_any(a.h_res, tok * n * n + e, xdt, s_mat[e]);
   }
 
-  // pre-aggregate (or the MHCHead weighted reduce)
+  // pre-aggregate (or the MHCHead weighted reduce): each h_pre[i] * x_i product
+  // rounds to the stream dtype, the sum over streams accumulates in fp32
+  // (model/mhc_fused.py:859, model/mhc_common.py:308).
   for (int c = tid; c < C; c += kGenThreads) {
     float o = 0.f;
-    for (int i = 0; i < n; ++i) o = fmaf(s_hpre[i], ld_any(a.x, xb + (int64_t)i * C + c, xdt), o);
+    for (int i = 0; i < n; ++i)
+      o += round_to(s_hpre[i] * ld_any(a.x, xb + (int64_t)i * C + c, xdt), xdt);
     st_any(a.sub_in, tok * C + c, xdt, o);
   }
 }

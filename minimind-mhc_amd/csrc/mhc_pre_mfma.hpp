@@ -14,10 +14,10 @@
 //   mixes[f]  = acc[f] * inv_rms                (== (x * inv_rms) @ phi)
 //   gates     h_pre = sigmoid(a_pre*m + b_pre) + pre_eps
 //             h_post = 2*sigmoid(a_post*m + b_post)   (post_mult)
-//             h_res_raw = a_res*m + b_res   (rounded to bf16, as both reference
-//                                            paths feed Sinkhorn a bf16 tensor)
-//   h_res     = Sinkhorn(h_res_raw)          (one matrix element per lane)
-//   sub_in[c] = sum_i h_pre[i] * x[i*C + c]
+//             h_res_raw = a_res*m + b_res
+//             each op rounded to bf16 as the reference's torch ops round it
+//   h_res     = Sinkhorn(h_res_raw) in fp32     (one matrix element per lane)
+//   sub_in[c] = sum_i bf16(h_pre[i] * x[i*C + c])
 // Reference semantics: model/mhc_fused.py:163-268 (fused kernel),
 // :533-559 (_pre_phase_full_ref), :47-56 (Sinkhorn), :820-830 (module flow);
 // model/mhc_fused_no_hres.py:48-145; model/mhc_common.py:128-195 (head).
@@ -166,16 +166,15 @@ __global__ __launch_bounds__(pre_threads(N)) void pre_mfma_kernel(PreArgs a) {
       const bool ok = tk < M;
       const float m = s_mix[idx];
       if (f < N) {
-        const float h = __fadd_rn(sigmoid_f(affine_rn(m, al0, ld_any(a.bias[0], f, pdt))), a.pre_eps);
+        const float h = gate_pre(m, al0, ld_any(a.bias[0], f, pdt), a.pre_eps, kBF16);
         s_hpre[tt][f] = h;
         if (ok && a.h_pre) st_any(a.h_pre, tk * N + f, kBF16, h);
       } else if (f < 2 * N) {
-        const float h = __fmul_rn(sigmoid_f(affine_rn(m, al1, ld_any(a.bias[1], f - N, pdt))),
-                                  a.post_mult);
+        const float h = gate_post(m, al1, ld_any(a.bias[1], f - N, pdt), a.post_mult, kBF16);
         if (ok) st_any(a.h_post, tk * N + (f - N), kBF16, h);
       } else {
         const int e = f - 2 * N;
-        const float h = round_to(affine_rn(m, al2, ld_any(a.bias[2], e, pdt)), kBF16);
+        const float h = gate_res(m, al2, ld_any(a.bias[2], e, pdt), kBF16);
         if constexpr (MODE == kFull) s_hres[tt * G + e] = h;
         if (ok && a.h_res_raw) st_any(a.h_res_raw, tk * G + e, kBF16, h);
       }
@@ -198,29 +197,19 @@ __global__ __launch_bounds__(pre_threads(N)) void pre_mfma_kernel(PreArgs a) {
   }
 
   // ---- 6. pre-aggregate from the held x registers ------------------------------
-  float hp[N];
+  uint32_t hlo[N];
+  uint32_t hhi[N];
 #pragma unroll
-  for (int i = 0; i < N; ++i) hp[i] = s_hpre[r][i];
+  for (int i = 0; i < N; ++i) {
+    hlo[i] = pack_lo(s_hpre[r][i]);
+    hhi[i] = pack_hi(s_hpre[r][i]);
+  }
   uint16_t* __restrict__ sub = static_cast<uint16_t*>(a.sub_in);
 #pragma unroll
   for (int q = 0; q < KB; ++q) {
     const int c = (wave + WAVES * q) * kCBlock + g * 8;
     if (tok_ok && c < C) {
-      float o[8];
-#pragma unroll
-      for (int k = 0; k < 8; ++k) o[k] = 0.f;
-#pragma unroll
-      for (int i = 0; i < N; ++i) {
-        const U32x4 v = xr[q][i];
-#pragma unroll
-        for (int j = 0; j < 4; ++j) {
-          o[2 * j] = fmaf(hp[i], bf16lo(v.v[j]), o[2 * j]);
-          o[2 * j + 1] = fmaf(hp[i], bf16hi(v.v[j]), o[2 * j + 1]);
-        }
-      }
-      U32x4 pk;
-#pragma unroll
-      for (int j = 0; j < 4; ++j) pk.v[j] = pack_bf16x2(o[2 * j], o[2 * j + 1]);
+      const U32x4 pk = preagg_chunk<N>(xr[q], hlo, hhi);
       *reinterpret_cast<U32x4*>(sub + tok * C + c) = pk;
     }
   }

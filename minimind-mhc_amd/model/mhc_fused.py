@@ -118,7 +118,7 @@ class _PreSinkhornFn(torch.autograd.Function):
         n, c, post_mult, pre_eps, shape, iters, sk_eps = ctx.cfg
         g_raw = None
         if g_hres is not None:
-            g_raw = _grad.sinkhorn_backward(raw, iters, sk_eps, g_hres)
+            g_raw = _grad.sinkhorn_backward(raw, iters, sk_eps, g_hres.reshape(raw.shape))
         g = _grad.pre_backward(x2, w, a_pre, b_pre, a_post, b_post, a_res, inv, mixes, n, c,
                                post_mult, pre_eps, g_sub, None, g_hpost, g_raw)
         return (g[0].to(x2.dtype).view(shape), g[1].to(w.dtype), None,
