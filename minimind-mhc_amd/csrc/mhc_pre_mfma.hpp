@@ -60,7 +60,7 @@ __global__ __launch_bounds__(pre_threads(N)) void pre_mfma_kernel(PreArgs a) {
 
   const int tid = threadIdx.x;
   const int lane = tid & 63;
-  const int wave = tid >> 6;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);  // wave-uniform (SGPR)
   const int r = lane & 15;   // token row inside the tile (MFMA M index)
   const int g = lane >> 4;   // 8-column group inside a 32-column block
   const int64_t M = a.M;

@@ -4,24 +4,34 @@
 //   * one 8-wave workgroup per CU walks the 16-token tiles blockIdx.x,
 //     blockIdx.x + gridDim.x, ... until the tiles run out;
 //   * wave w owns the 32-column blocks cb = w, w + 8, ... of every stream;
-//   * phi stays resident for the workgroup's lifetime, as MFMA B operands: the
+//   * phi stays resident for the workgroup's lifetime as MFMA B operands: the
 //     first NREG 16-column tiles in registers, the next NLDS tiles in LDS (the
 //     last, partial tile stored compactly: lanes past its real columns read a
-//     shared zero block), any rest re-read from L2 per tile;
-//   * x tiles are DEPTH-buffered in registers: DEPTH - 1 tiles are in flight
-//     while one runs its MFMAs, cross-wave reduction, gates, Sinkhorn and
-//     pre-aggregate.  Loaded HBM latency on MI355X is several microseconds,
-//     so one tile (96 KiB per CU at n=4, C=768) in flight cannot keep HBM
-//     busy; DEPTH = 3 keeps two.
+//     shared zero block), any rest re-read from L2 per tile.  At n=4, C=768
+//     all of phi (96 VGPRs a lane) lives in registers and the MFMAs read no
+//     memory at all;
+//   * x tiles are DEPTH-buffered in registers.  The loads of tile t+DEPTH go
+//     out chunk by chunk while tile t's pre-aggregate frees its registers, so
+//     load issue overlaps the VALU work instead of stalling all waves at once;
 //   * x loads and sub_in stores are raw buffer ops bounded by a per-tile
 //     descriptor: missing tokens / columns are zero-filled (or dropped) by
 //     hardware, so no load sits behind a branch and the compiler waits only
 //     for the tile it is about to use;
 //   * the tile loop issues no other global load: the vector-memory counter
 //     retires in order, so waiting on any load issued after a prefetch would
-//     also wait for the prefetch.  Gate scalars and biases are read once, before
-//     the first x load, and kept in LDS as fp32.
-// Per tile: two workgroup barriers (partials written; gates written).
+//     also wait for the prefetch.  Gate scalars and biases are read once, with
+//     branch-free loads issued before everything else, and kept in LDS as fp32.
+//
+// Per tile, two workgroup barriers split three phases:
+//   1. all waves: sum of squares + MFMA partial projections -> LDS;
+//   2. waves SK_WAVES..7: reduce partials, inv_rms, gates (h_pre to LDS, h_res
+//      logits to one of two LDS slots); meanwhile waves 0..SK_WAVES-1 run the
+//      Sinkhorn-Knopp iterations of the PREVIOUS tile from the other slot.  The
+//      Sinkhorn is a ~20-step dependent chain; running it one tile behind, in
+//      parallel with the gates, takes it off the per-tile critical path;
+//   3. all waves: pre-aggregate from the held x registers, store sub_in, issue
+//      the next loads.
+// The last tile's Sinkhorn runs after the loop.
 //
 // Reference semantics: model/mhc_fused.py:163-268, :533-559, :47-56,
 // :820-830; model/mhc_fused_no_hres.py:48-145; model/mhc_common.py:128-195.
@@ -50,7 +60,7 @@ struct PersistShared {
   float acc[kPersistWaves][kTokTile][FD];  // per-wave partial projections
   float ss[kPersistWaves][kTokTile];       // per-wave partial sums of squares
   float hpre[kTokTile][N];
-  float hres[kTokTile * N * N];
+  float hres[2][kTokTile * N * N];         // h_res logits, two tiles in flight
   U32x4 zero;                              // B operand of padding columns
 };
 
@@ -61,9 +71,12 @@ struct PersistPlan {
   static constexpr int NT = S::NT;
   static constexpr int G = N * N;
   static constexpr int LAST_COLS = FD - 16 * (NT - 1);  // real columns of the last tile
-  // registers: x buffers first, then whole phi tiles
-  static constexpr int kRegBudget = 160;
+  // Registers for x buffers and resident phi tiles (the rest of the 256 is
+  // working set).  Bytes in flight set the streaming rate, so x gets three
+  // buffers whenever they fit and phi takes what is left; phi tiles that do
+  // not fit in registers are read from LDS each tile.
   static constexpr int XTILE = KB * N * 4;  // VGPRs of one x tile (and of one phi tile)
+  static constexpr int kRegBudget = 160;
   static constexpr int DEPTH = 3 * XTILE <= kRegBudget ? 3 : 2;
   static constexpr int REG_LEFT = kRegBudget - DEPTH * XTILE;
   static constexpr int REG_FIT = REG_LEFT > 0 ? REG_LEFT / XTILE : 0;
@@ -90,6 +103,16 @@ struct PersistPlan {
   }
   static constexpr int LDS_W = lds_base(NREG + NLDS) > 0 ? lds_base(NREG + NLDS) : 16;
   static constexpr int WR = NREG > 0 ? NREG : 1;  // register array extent (>= 1)
+  // x buffers whose loads go out before the LDS phi tiles are written (the
+  // staging registers of those tiles must fit beside them); the rest follow
+  // the LDS writes.
+  static constexpr int X_FIT = 224 / XTILE - NREG - NLDS;
+  static constexpr int X_EARLY = X_FIT < 0 ? 0 : (X_FIT > DEPTH ? DEPTH : X_FIT);
+  // Waves that run the Sinkhorn (whole waves covering a tile's TM*G elements);
+  // the gates run on the others.  Without h_res every wave runs the gates.
+  static constexpr int SK_WAVES = MODE == kFull ? (kTokTile * G + 63) / 64 : 0;
+  static_assert(SK_WAVES < kPersistWaves, "gates need at least one wave");
+  static_assert(kPersistWaves * kTokTile * FD * 4 >= 64 * 16, "partials area doubles as a write sink");
 };
 
 // Tokens of a tile that exist (0 for a tile past the end).
@@ -99,24 +122,37 @@ __device__ __forceinline__ int tile_tokens(int64_t tile, int64_t ntiles, int64_t
   return left < kTokTile ? (int)left : kTokTile;
 }
 
-// Load this lane's x chunks of one tile.  The descriptor covers the tile's
-// existing tokens (valid * n*C * 2 bytes); a lane whose token is missing has a
-// lane offset past that bound and a column past C gets kBufOob, so either
-// reads zeros.  The per-(stream, block) part of the offset is wave-uniform
-// and travels in the scalar offset.
+// Buffer descriptor over one tile's x rows: valid * n*C * 2 bytes (no records
+// for a tile past the end, so its loads read zeros without touching memory).
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t x_tile_rsrc(const uint16_t* __restrict__ x,
+                                                              int64_t tile, int64_t ntiles,
+                                                              int64_t M, int NC) {
+  const int valid = tile_tokens(tile, ntiles, M);
+  return make_rsrc(x + (valid > 0 ? tile * kTokTile * (int64_t)NC : 0),
+                   (uint32_t)valid * (uint32_t)NC * 2u);
+}
+
+// Column part of the lane offset for column block q of this wave: lane (r, g)
+// reads row r, columns c0 + 8g .. c0 + 8g + 7 (the row part is added by the
+// caller).  A column block past C gets kBufOob (reads zeros).  For loads the
+// per-stream offset travels in the scalar offset.
+__device__ __forceinline__ uint32_t x_lane_off(int q, int wave, int g, int C) {
+  const int c0 = (wave + kPersistWaves * q) * kCBlock;
+  return c0 + g * 8 < C ? (uint32_t)g * 16u : kBufOob;
+}
+
 template <int N, int KB>
 __device__ __forceinline__ void persist_load_tile(U32x4 (&xr)[KB][N], const uint16_t* __restrict__ x,
                                                   int64_t tile, int64_t ntiles, int64_t M, int C,
                                                   int wave, int r, int g) {
   const int NC = N * C;
-  const int valid = tile_tokens(tile, ntiles, M);
-  const auto rsrc = make_rsrc(x + (valid > 0 ? tile * kTokTile * (int64_t)NC : 0),
-                              (uint32_t)valid * (uint32_t)NC * 2u);
-  const uint32_t lane_off = (uint32_t)(r * NC + g * 8) * 2u;
+  const auto rsrc = x_tile_rsrc(x, tile, ntiles, M, NC);
+  const uint32_t row_off = (uint32_t)(r * NC) * 2u;
 #pragma unroll
   for (int q = 0; q < KB; ++q) {
     const int c0 = (wave + kPersistWaves * q) * kCBlock;
-    const uint32_t voff = c0 + g * 8 < C ? lane_off : kBufOob;
+    const uint32_t lo = x_lane_off(q, wave, g, C);
+    const uint32_t voff = lo == kBufOob ? kBufOob : row_off + lo;
 #pragma unroll
     for (int i = 0; i < N; ++i) {
       const int soff = (i * C + c0) * 2;
@@ -126,59 +162,54 @@ __device__ __forceinline__ void persist_load_tile(U32x4 (&xr)[KB][N], const uint
   }
 }
 
+// ---- phase 1: sum of squares (bf16 dot2) + projection partials (MFMA) -> LDS
 template <int N, int MODE, int KB>
-__device__ __forceinline__ void persist_tile(
+__device__ __forceinline__ void persist_partials(
     const PreArgs& a, PersistShared<N, PersistPlan<N, MODE, KB>::FD>& sh, const U32x4 (&xr)[KB][N],
     const bf16x8_t (&wreg)[KB][N][PersistPlan<N, MODE, KB>::WR], const unsigned char* lds_w,
-    int64_t tile, int tid, int lane, int wave) {
+    int lane, int wave) {
   using P = PersistPlan<N, MODE, KB>;
-  using GP = GateParams<N>;
   constexpr int FD = P::FD;
   constexpr int NT = P::NT;
-  constexpr int G = P::G;
-  constexpr int T = kPersistWaves * 64;
-  constexpr int TM = kTokTile;
   const int r = lane & 15;
   const int g = lane >> 4;
-  const int64_t M = a.M;
-  const int C = a.C;
-  const int NCB = (C + kCBlock - 1) / kCBlock;
-  const int64_t NC = (int64_t)N * C;
-  const int64_t t0 = tile * TM;
+  const int NCB = (a.C + kCBlock - 1) / kCBlock;
 
-  // ---- sum of squares (bf16 dot2) + projection (MFMA) ----------------------
   f32x4_t acc[NT];
 #pragma unroll
   for (int nt = 0; nt < NT; ++nt) acc[nt] = f32x4_t{0.f, 0.f, 0.f, 0.f};
   float ss = 0.f;
-  const bf16x8_t* __restrict__ wp = static_cast<const bf16x8_t*>(a.phi_packed);
+  // Column blocks past C hold zeros in x and in every phi copy (registers, LDS,
+  // and the bounded L2 reads below), so every block runs unconditionally: no
+  // branch splits the waits on the x buffers.
+  const auto wr = make_rsrc(a.phi_packed, (uint32_t)(N * NCB * NT) * 64u * 16u);
 #pragma unroll
   for (int q = 0; q < KB; ++q) {
     const int cb = wave + kPersistWaves * q;
-    if (cb < NCB) {
 #pragma unroll
-      for (int i = 0; i < N; ++i) {
-        const U32x4 v = xr[q][i];
+    for (int i = 0; i < N; ++i) {
+      const U32x4 v = xr[q][i];
 #pragma unroll
-        for (int j = 0; j < 4; ++j) ss = dot2_bf16(v.v[j], v.v[j], ss);
-        const bf16x8_t av = __builtin_bit_cast(bf16x8_t, v);
+      for (int j = 0; j < 4; ++j) ss = dot2_bf16(v.v[j], v.v[j], ss);
+      const bf16x8_t av = __builtin_bit_cast(bf16x8_t, v);
 #pragma unroll
-        for (int nt = 0; nt < NT; ++nt) {
-          bf16x8_t bv;
-          if (nt < P::NREG) {  // compile-time after unrolling
-            bv = wreg[q][i][nt < P::NREG ? nt : 0];
-          } else if (nt < P::NREG + P::NLDS) {
-            const int cols = P::cols(nt);
-            const unsigned char* src =
-                r < cols ? lds_w + P::lds_base(nt) +
-                               ((((wave * KB + q) * N + i) * 4 + g) * cols + r) * 16
-                         : reinterpret_cast<const unsigned char*>(&sh.zero);
-            bv = *reinterpret_cast<const bf16x8_t*>(src);
-          } else {
-            bv = wp[((int64_t)(i * NCB + cb) * NT + nt) * 64 + lane];
-          }
-          acc[nt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(av, bv, acc[nt], 0, 0, 0);
+      for (int nt = 0; nt < NT; ++nt) {
+        bf16x8_t bv;
+        if (nt < P::NREG) {  // compile-time after unrolling
+          bv = wreg[q][i][nt < P::NREG ? nt : 0];
+        } else if (nt < P::NREG + P::NLDS) {
+          const int cols = P::cols(nt);
+          const unsigned char* src =
+              r < cols ? lds_w + P::lds_base(nt) +
+                             ((((wave * KB + q) * N + i) * 4 + g) * cols + r) * 16
+                       : reinterpret_cast<const unsigned char*>(&sh.zero);
+          bv = *reinterpret_cast<const bf16x8_t*>(src);
+        } else {
+          const uint32_t off =
+              cb < NCB ? (uint32_t)(((i * NCB + cb) * NT + nt) * 64 + lane) * 16u : kBufOob;
+          bv = __builtin_bit_cast(bf16x8_t, buf_load16(wr, off));
         }
+        acc[nt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(av, bv, acc[nt], 0, 0, 0);
       }
     }
   }
@@ -191,10 +222,22 @@ __device__ __forceinline__ void persist_tile(
 #pragma unroll
       for (int j = 0; j < 4; ++j) sh.acc[wave][4 * g + j][nt * 16 + r] = acc[nt][j];
   if (g == 0) sh.ss[wave][r] = ss;
-  __syncthreads();
+}
 
-  // ---- reduce partials, inv_rms, gates -----------------------------------------
-  for (int idx = tid; idx < TM * FD; idx += T) {
+// ---- phase 2a: reduce partials, inv_rms, gates (threads idx0, idx0 + step, ...)
+template <int N, int MODE, int KB>
+__device__ __forceinline__ void persist_gates(const PreArgs& a,
+                                              PersistShared<N, PersistPlan<N, MODE, KB>::FD>& sh,
+                                              int64_t tile, int slot, int idx0, int step) {
+  using P = PersistPlan<N, MODE, KB>;
+  using GP = GateParams<N>;
+  constexpr int FD = P::FD;
+  constexpr int G = P::G;
+  constexpr int TM = kTokTile;
+  const int64_t M = a.M;
+  const int64_t NC = (int64_t)N * a.C;
+  const int64_t t0 = tile * TM;
+  for (int idx = idx0; idx < TM * FD; idx += step) {
     const int tt = idx / FD;
     const int f = idx - tt * FD;
     float sq = 0.f;
@@ -222,23 +265,40 @@ __device__ __forceinline__ void persist_tile(
     } else {
       const int e = f - 2 * N;
       const float h = gate_res(m, sh.prm[2], sh.prm[GP::kBiasRes + e], kBF16);
-      if constexpr (MODE == kFull) sh.hres[tt * G + e] = h;
+      if constexpr (MODE == kFull) sh.hres[slot][tt * G + e] = h;
       if (ok && a.h_res_raw) st_any(a.h_res_raw, tk * G + e, kBF16, h);
     }
   }
-  __syncthreads();
+}
 
-  // ---- Sinkhorn-Knopp, one matrix element per lane -----------------------------
-  if constexpr (MODE == kFull) {
-    if (a.h_res && wave * 64 < TM * G) {  // wave-uniform: whole groups only
-      const int e = tid;
-      float v = e < TM * G ? sh.hres[e] : 0.f;
-      v = sinkhorn_lane<N>(v, a.sk_iters, a.sk_eps);
-      if (e < TM * G && t0 + e / G < M) st_any(a.h_res, t0 * G + e, kBF16, v);
-    }
-  }
+// ---- phase 2b: Sinkhorn-Knopp of tile `tile` from LDS slot `slot`, one matrix
+// element per lane (waves 0..SK_WAVES-1).
+template <int N>
+__device__ __forceinline__ void persist_sinkhorn(const PreArgs& a, const float* hres, int64_t tile,
+                                                 int tid) {
+  constexpr int G = N * N;
+  constexpr int TM = kTokTile;
+  const int64_t t0 = tile * TM;
+  const int e = tid;
+  float v = e < TM * G ? hres[e] : 0.f;
+  v = sinkhorn_lane<N>(v, a.sk_iters, a.sk_eps);
+  if (e < TM * G && t0 + e / G < a.M) st_any(a.h_res, t0 * G + e, kBF16, v);
+}
 
-  // ---- pre-aggregate from the held x registers ---------------------------------
+// ---- phase 3: pre-aggregate from the held x registers; as each column block
+// is done its registers take the loads of tile `next`.
+template <int N, int MODE, int KB>
+__device__ __forceinline__ void persist_preagg(const PreArgs& a,
+                                               const PersistShared<N, PersistPlan<N, MODE, KB>::FD>& sh,
+                                               U32x4 (&xr)[KB][N], int64_t tile, int64_t next,
+                                               int64_t ntiles, int lane, int wave) {
+  constexpr int TM = kTokTile;
+  const int r = lane & 15;
+  const int g = lane >> 4;
+  const int64_t M = a.M;
+  const int C = a.C;
+  const int NC = N * C;
+  const int64_t t0 = tile * TM;
   uint32_t hlo[N];
   uint32_t hhi[N];
 #pragma unroll
@@ -248,14 +308,93 @@ __device__ __forceinline__ void persist_tile(
   }
   const int valid = (int)(M - t0 < TM ? M - t0 : TM);
   const auto rsub = make_rsrc(static_cast<uint16_t*>(a.sub_in) + t0 * C, (uint32_t)valid * C * 2u);
-  const uint32_t lane_off = (uint32_t)(r * C + g * 8) * 2u;
+  const uint32_t sub_row = (uint32_t)(r * C) * 2u;
+  const auto rnext = x_tile_rsrc(static_cast<const uint16_t*>(a.x), next, ntiles, M, NC);
+  const uint32_t x_row = (uint32_t)(r * NC) * 2u;
 #pragma unroll
   for (int q = 0; q < KB; ++q) {
     const int c0 = (wave + kPersistWaves * q) * kCBlock;
+    const uint32_t lo = x_lane_off(q, wave, g, C);
     const U32x4 pk = preagg_chunk<N>(xr[q], hlo, hhi);
-    __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(u32x4_t, pk), rsub,
-                                           (int)(c0 + g * 8 < C ? lane_off : kBufOob), c0 * 2, 0);
+    // The whole offset travels in the vector offset, the scalar offset stays
+    // the literal 0: a 128-bit store reads its data registers after issue, and
+    // the compiler only keeps the next VALU write off those registers for
+    // stores of that form.  With a register soffset it reused the first data
+    // register at once and some lanes stored the new value.
+    buf_store16(rsub, lo == kBufOob ? kBufOob : sub_row + lo + (uint32_t)c0 * 2u, pk);
+    const uint32_t voff = lo == kBufOob ? kBufOob : x_row + lo;
+#pragma unroll
+    for (int i = 0; i < N; ++i)
+      xr[q][i] = __builtin_bit_cast(
+          U32x4, __builtin_amdgcn_raw_buffer_load_b128(rnext, (int)voff, (i * C + c0) * 2, 0));
   }
+}
+
+// One tile: partials, barrier, gates || Sinkhorn(prev), barrier, pre-aggregate.
+template <int N, int MODE, int KB>
+__device__ __forceinline__ void persist_step(
+    const PreArgs& a, PersistShared<N, PersistPlan<N, MODE, KB>::FD>& sh, U32x4 (&xr)[KB][N],
+    const bf16x8_t (&wreg)[KB][N][PersistPlan<N, MODE, KB>::WR], const unsigned char* lds_w,
+    int64_t tile, int64_t prev, int64_t next, int64_t ntiles, int slot, int tid, int lane, int wave) {
+  using P = PersistPlan<N, MODE, KB>;
+  persist_partials<N, MODE, KB>(a, sh, xr, wreg, lds_w, lane, wave);
+  __syncthreads();
+  if constexpr (MODE == kFull) {
+    if (wave < P::SK_WAVES) {
+      if (prev >= 0 && a.h_res) persist_sinkhorn<N>(a, sh.hres[slot ^ 1], prev, tid);
+    } else {
+      persist_gates<N, MODE, KB>(a, sh, tile, slot, tid - P::SK_WAVES * 64,
+                                 (kPersistWaves - P::SK_WAVES) * 64);
+    }
+  } else {
+    persist_gates<N, MODE, KB>(a, sh, tile, slot, tid, kPersistWaves * 64);
+  }
+  __syncthreads();
+  persist_preagg<N, MODE, KB>(a, sh, xr, tile, next, ntiles, lane, wave);
+}
+
+// Gate parameter of thread tid (raw bits; converted once the streaming loads
+// are out).  Branch-free: threads without a parameter read alpha_pre[0].
+struct RawParam {
+  uint32_t lo, hi;
+  bool used;
+};
+
+template <int N, int MODE>
+__device__ __forceinline__ RawParam load_gate_param(const PreArgs& a, int tid) {
+  using GP = GateParams<N>;
+  int which = 5;
+  int idx = tid - GP::kBiasRes;
+  if (tid < GP::kBiasRes) { which = 4; idx = tid - GP::kBiasPost; }
+  if (tid < GP::kBiasPost) { which = 3; idx = tid - GP::kBiasPre; }
+  if (tid < 3) { which = tid; idx = 0; }
+  const bool used = tid < GP::kCount &&
+                    (which == 0 || which == 3 ||
+                     (MODE != kHead && (which == 1 || which == 4)) ||
+                     (MODE == kFull && (which == 2 || which == 5)));
+  const void* p = a.alpha[0];
+  p = which == 1 ? a.alpha[1] : p;
+  p = which == 2 ? a.alpha[2] : p;
+  p = which == 3 ? a.bias[0] : p;
+  p = which == 4 ? a.bias[1] : p;
+  p = which == 5 ? a.bias[2] : p;
+  p = used ? p : a.alpha[0];
+  idx = used ? idx : 0;
+  const int es = a.param_dtype == kF32 ? 4 : 2;
+  const unsigned char* b = static_cast<const unsigned char*>(p) + (int64_t)idx * es;
+  RawParam rp;
+  rp.lo = *reinterpret_cast<const uint16_t*>(b);
+  rp.hi = *reinterpret_cast<const uint16_t*>(b + (es == 4 ? 2 : 0));
+  rp.used = used;
+  return rp;
+}
+
+__device__ __forceinline__ float convert_param(const RawParam& rp, int dt) {
+  const float f32 = __uint_as_float(rp.lo | (rp.hi << 16));
+  const float bf = __uint_as_float(rp.lo << 16);
+  const float f16 = f16_bits_to_f32((uint16_t)rp.lo);
+  const float v = dt == kF32 ? f32 : (dt == kBF16 ? bf : f16);
+  return rp.used ? v : 0.f;
 }
 
 template <int N, int MODE, int KB>
@@ -267,93 +406,103 @@ __global__ __launch_bounds__(kPersistWaves * 64) void pre_persist_kernel(PreArgs
 
   const int tid = threadIdx.x;
   const int lane = tid & 63;
-  const int wave = tid >> 6;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);  // wave-uniform (SGPR)
   const int r = lane & 15;
   const int g = lane >> 4;
   const int C = a.C;
   const int NCB = (C + kCBlock - 1) / kCBlock;
   const uint16_t* __restrict__ x = static_cast<const uint16_t*>(a.x);
   const int64_t step = gridDim.x;
+  int64_t tile = blockIdx.x;
 
-  // Gate parameters first, so the waits for them never cover a streaming load.
-  using GP = GateParams<N>;
-  float prm = 0.f;
-  if (tid < GP::kCount) {
-    const int pdt = a.param_dtype;
-    if (tid < 3) {
-      const bool used = tid == 0 || (tid == 1 && MODE != kHead) || (tid == 2 && MODE == kFull);
-      if (used) prm = ld_any(a.alpha[tid], 0, pdt);
-    } else if (tid < GP::kBiasPost) {
-      prm = ld_any(a.bias[0], tid - GP::kBiasPre, pdt);
-    } else if (tid < GP::kBiasRes) {
-      if (MODE != kHead) prm = ld_any(a.bias[1], tid - GP::kBiasPost, pdt);
-    } else {
-      if (MODE == kFull) prm = ld_any(a.bias[2], tid - GP::kBiasRes, pdt);
-    }
-  }
+  // Issue order: gate parameters, register phi tiles, LDS phi tiles (staged in
+  // registers), the x buffers that fit beside that staging, then -- after the
+  // LDS writes, which wait only for phi -- the other x buffers.  Padding lanes
+  // of a compact phi tile write into the (not yet used) partials area.
+  const RawParam rp = load_gate_param<N, MODE>(a, tid);
 
-  // phi, resident for the workgroup's lifetime (unconditional buffer loads:
-  // column blocks past C read zeros).  Issued before the x loads so that
-  // waiting for it (to fill LDS) does not wait for x.
-  if (tid == 0) sh.zero = U32x4{{0u, 0u, 0u, 0u}};
+  const uint32_t wbytes = (uint32_t)(N * NCB * P::NT) * 64u * 16u;
+  const auto wr = make_rsrc(a.phi_packed, wbytes);
+  auto phi_off = [&](int nt, int q, int i) -> uint32_t {
+    const int cb = wave + kPersistWaves * q;
+    return cb < NCB ? (uint32_t)(((i * NCB + cb) * P::NT + nt) * 64 + lane) * 16u : kBufOob;
+  };
   bf16x8_t wreg[KB][N][P::WR];
-  {
-    const uint32_t wbytes = (uint32_t)(N * NCB * P::NT) * 64u * 16u;
-    const auto wr = make_rsrc(a.phi_packed, wbytes);
 #pragma unroll
-    for (int nt = 0; nt < P::NREG + P::NLDS; ++nt) {
+  for (int nt = 0; nt < P::NREG; ++nt)
 #pragma unroll
-      for (int q = 0; q < KB; ++q) {
-        const int cb = wave + kPersistWaves * q;
+    for (int q = 0; q < KB; ++q)
 #pragma unroll
-        for (int i = 0; i < N; ++i) {
-          const uint32_t off = cb < NCB
-              ? (uint32_t)(((i * NCB + cb) * P::NT + nt) * 64 + lane) * 16u : kBufOob;
-          const U32x4 w = buf_load16(wr, off);
-          if (nt < P::NREG) {
-            wreg[q][i][nt < P::NREG ? nt : 0] = __builtin_bit_cast(bf16x8_t, w);
-          } else {
-            const int cols = P::cols(nt);
-            if (r < cols)
-              *reinterpret_cast<U32x4*>(lds_w + P::lds_base(nt) +
-                                        ((((wave * KB + q) * N + i) * 4 + g) * cols + r) * 16) = w;
-          }
-        }
-      }
-    }
-  }
-  if (tid < GP::kCount) sh.prm[tid] = prm;
+      for (int i = 0; i < N; ++i)
+        wreg[q][i][nt] = __builtin_bit_cast(bf16x8_t, buf_load16(wr, phi_off(nt, q, i)));
 
   U32x4 xa[KB][N];
   U32x4 xb[KB][N];
   U32x4 xc[P::DEPTH == 3 ? KB : 1][N];
-  int64_t tile = blockIdx.x;
-  persist_load_tile<N, KB>(xa, x, tile, ntiles, a.M, C, wave, r, g);
-  persist_load_tile<N, KB>(xb, x, tile + step, ntiles, a.M, C, wave, r, g);
+  // x buffer b (0 = xa, 1 = xb, 2 = xc) holds tile blockIdx.x + b * step.
+  auto load_x = [&](int first, int last) {
+    if (first <= 0 && 0 < last) persist_load_tile<N, KB>(xa, x, tile, ntiles, a.M, C, wave, r, g);
+    if (first <= 1 && 1 < last) persist_load_tile<N, KB>(xb, x, tile + step, ntiles, a.M, C, wave, r, g);
+    if constexpr (P::DEPTH == 3)
+      if (first <= 2 && 2 < last)
+        persist_load_tile<N, KB>(xc, x, tile + 2 * step, ntiles, a.M, C, wave, r, g);
+  };
+  constexpr int NST = P::NLDS > 0 ? P::NLDS : 1;
+  U32x4 st[NST][KB][N];  // LDS phi tiles, staged
+#pragma unroll
+  for (int t = 0; t < P::NLDS; ++t)
+#pragma unroll
+    for (int q = 0; q < KB; ++q)
+#pragma unroll
+      for (int i = 0; i < N; ++i) st[t][q][i] = buf_load16(wr, phi_off(P::NREG + t, q, i));
+  load_x(0, P::X_EARLY);
+#pragma unroll
+  for (int t = 0; t < P::NLDS; ++t) {
+    const int nt = P::NREG + t;
+    const int cols = P::cols(nt);
+#pragma unroll
+    for (int q = 0; q < KB; ++q)
+#pragma unroll
+      for (int i = 0; i < N; ++i) {
+        unsigned char* dst = r < cols ? lds_w + P::lds_base(nt) +
+                                            ((((wave * KB + q) * N + i) * 4 + g) * cols + r) * 16
+                                      : reinterpret_cast<unsigned char*>(&sh.acc[0][0][0]) + lane * 16;
+        *reinterpret_cast<U32x4*>(dst) = st[t][q][i];
+      }
+  }
+  load_x(P::X_EARLY, P::DEPTH);
+
+  if (tid == 0) sh.zero = U32x4{{0u, 0u, 0u, 0u}};
+  if (tid < GateParams<N>::kCount) sh.prm[tid] = convert_param(rp, a.param_dtype);
   __syncthreads();  // gate parameters, zero block and phi tiles visible
 
-  if constexpr (P::DEPTH == 3) {
-    while (tile < ntiles) {  // uniform across the workgroup
-      persist_load_tile<N, KB>(xc, x, tile + 2 * step, ntiles, a.M, C, wave, r, g);
-      persist_tile<N, MODE, KB>(a, sh, xa, wreg, lds_w, tile, tid, lane, wave);
-      if (tile + step >= ntiles) break;
-      persist_load_tile<N, KB>(xa, x, tile + 3 * step, ntiles, a.M, C, wave, r, g);
-      persist_tile<N, MODE, KB>(a, sh, xb, wreg, lds_w, tile + step, tid, lane, wave);
-      if (tile + 2 * step >= ntiles) break;
-      persist_load_tile<N, KB>(xb, x, tile + 4 * step, ntiles, a.M, C, wave, r, g);
-      persist_tile<N, MODE, KB>(a, sh, xc, wreg, lds_w, tile + 2 * step, tid, lane, wave);
-      tile += 3 * step;
-    }
-  } else {
-    while (tile < ntiles) {
-      persist_tile<N, MODE, KB>(a, sh, xa, wreg, lds_w, tile, tid, lane, wave);
-      if (tile + step >= ntiles) break;
-      persist_load_tile<N, KB>(xa, x, tile + 2 * step, ntiles, a.M, C, wave, r, g);
-      persist_tile<N, MODE, KB>(a, sh, xb, wreg, lds_w, tile + step, tid, lane, wave);
-      if (tile + 2 * step >= ntiles) break;
-      persist_load_tile<N, KB>(xb, x, tile + 3 * step, ntiles, a.M, C, wave, r, g);
-      tile += 2 * step;
-    }
+  // Whole rounds of DEPTH steps, then the 0..DEPTH-1 leftover steps.  The
+  // loop body has no exit between its steps: an exit there leaves the compiler
+  // a path into the loop header on which the prefetch order differs, and the
+  // header then waits for every load in flight.
+  const int64_t my_tiles = (ntiles - blockIdx.x + step - 1) / step;
+  int64_t prev = -1;
+  int slot = 0;
+  auto run = [&](U32x4 (&xr)[KB][N]) {
+    persist_step<N, MODE, KB>(a, sh, xr, wreg, lds_w, tile, prev, tile + P::DEPTH * step, ntiles,
+                              slot, tid, lane, wave);
+    prev = tile;
+    slot ^= 1;
+    tile += step;
+  };
+  int64_t k = 0;
+  for (; k + P::DEPTH <= my_tiles; k += P::DEPTH) {  // uniform across the workgroup
+    run(xa);
+    run(xb);
+    if constexpr (P::DEPTH == 3) run(xc);
+  }
+  if (k < my_tiles) {
+    run(xa);
+    if (k + 1 < my_tiles) run(xb);
+  }
+  // The last tile's Sinkhorn (its logits were published by the final barrier).
+  if constexpr (MODE == kFull) {
+    if (wave < P::SK_WAVES && a.h_res) persist_sinkhorn<N>(a, sh.hres[slot ^ 1], prev, tid);
   }
 }
 

@@ -73,6 +73,32 @@ def test_pre_mfma_matches_generic(dev, n, C):
         assert maxrel(b[k], a[k]) <= 1e-2, k
 
 
+@pytest.mark.parametrize("n,C,M", [(4, 768, 4096), (2, 512, 4096), (4, 768, 20000)])
+def test_pre_mfma_many_workgroups_repeat(dev, n, C, M):
+    """Every CU busy, one or more tiles per workgroup, several launches: the
+    persistent kernel's output must equal the generic kernel's within bf16
+    rounding on every launch and be bit-identical between launches.  (A store
+    whose data registers were overwritten before the store read them left
+    zeros in a few lanes only under this kind of load.)"""
+    g = torch.Generator().manual_seed(7 + n + M)
+    x = torch.randn(M, n * C, generator=g).to(torch.bfloat16).to(dev)
+    p = _to(make_params("full", n, C, torch.bfloat16, g), dev)
+    packed = _ops.PhiPack(H.MODE_FULL).get(p["phi_weight"], n, C)
+    assert packed is not None
+    args = (p["alpha_pre"], p["bias_pre"], p["alpha_post"], p["bias_post"], p["alpha_res"],
+            p["bias_res"], n, C, 2.0, 1e-6, 1e-6, 20, 1e-6)
+    ref = _ops.pre_full(x, p["phi_weight"], None, *args)
+    first = None
+    for rep in range(4):
+        o = _ops.pre_full(x, p["phi_weight"], packed, *args)
+        torch.cuda.synchronize()
+        for k in ("sub_in", "h_post", "h_res"):
+            assert maxrel(ref[k], o[k]) <= 1e-2, (rep, k)
+            if first is not None:
+                assert torch.equal(first[k], o[k]), (rep, k)
+        first = first or o
+
+
 @pytest.mark.parametrize("iters", [0, 1, 10, 20])
 def test_pre_sinkhorn_iteration_counts(dev, iters):
     o, r, _ = _pre_case(dev, 4, 768, 32, torch.float32, True, iters, use_pack=True)
