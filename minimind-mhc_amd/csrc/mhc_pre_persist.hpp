@@ -71,13 +71,13 @@ struct PersistPlan {
   static constexpr int NT = S::NT;
   static constexpr int G = N * N;
   static constexpr int LAST_COLS = FD - 16 * (NT - 1);  // real columns of the last tile
-  // Registers for x buffers and resident phi tiles (the rest of the 256 is
-  // working set).  Bytes in flight set the streaming rate, so x gets three
-  // buffers whenever they fit and phi takes what is left; phi tiles that do
-  // not fit in registers are read from LDS each tile.
+  // Registers: two x buffers (the tile being computed and the next one, whose
+  // loads go out in small batches during the current step) and as many whole
+  // phi tiles as fit in the rest of the budget (the other ~60 VGPRs are
+  // working set); phi tiles that do not fit are read from LDS each tile.
   static constexpr int XTILE = KB * N * 4;  // VGPRs of one x tile (and of one phi tile)
-  static constexpr int kRegBudget = 160;
-  static constexpr int DEPTH = 3 * XTILE <= kRegBudget ? 3 : 2;
+  static constexpr int kRegBudget = XTILE <= 48 ? 192 : 160;
+  static constexpr int DEPTH = 2;
   static constexpr int REG_LEFT = kRegBudget - DEPTH * XTILE;
   static constexpr int REG_FIT = REG_LEFT > 0 ? REG_LEFT / XTILE : 0;
   static constexpr int NREG = REG_FIT < NT ? REG_FIT : NT;
@@ -103,15 +103,21 @@ struct PersistPlan {
   }
   static constexpr int LDS_W = lds_base(NREG + NLDS) > 0 ? lds_base(NREG + NLDS) : 16;
   static constexpr int WR = NREG > 0 ? NREG : 1;  // register array extent (>= 1)
-  // x buffers whose loads go out before the LDS phi tiles are written (the
-  // staging registers of those tiles must fit beside them); the rest follow
-  // the LDS writes.
-  static constexpr int X_FIT = 224 / XTILE - NREG - NLDS;
-  static constexpr int X_EARLY = X_FIT < 0 ? 0 : (X_FIT > DEPTH ? DEPTH : X_FIT);
+  // The first x tile's loads go out before the LDS phi tiles are written when
+  // the staging registers of those tiles fit beside it.
+  static constexpr bool X_EARLY = (NREG + NLDS + 1) * XTILE <= 224;
+  // Column blocks of the next tile loaded at the three points of a step:
+  // [0, B1) at its start, [B1, B2) after the first barrier, [B2, KB) after the
+  // second.  Spreading the loads keeps a steady ~32 KiB per CU in flight; a
+  // whole tile issued at once overflows the CU's request queue and stalls the
+  // issuing waves.
+  static constexpr int B1 = (KB + 2) / 3;
+  static constexpr int B2 = (2 * KB + 2) / 3;
   // Waves that run the Sinkhorn (whole waves covering a tile's TM*G elements);
   // the gates run on the others.  Without h_res every wave runs the gates.
   static constexpr int SK_WAVES = MODE == kFull ? (kTokTile * G + 63) / 64 : 0;
   static_assert(SK_WAVES < kPersistWaves, "gates need at least one wave");
+  static_assert(FD <= 32, "gates map at most two features to a thread");
   static_assert(kPersistWaves * kTokTile * FD * 4 >= 64 * 16, "partials area doubles as a write sink");
 };
 
@@ -141,24 +147,20 @@ __device__ __forceinline__ uint32_t x_lane_off(int q, int wave, int g, int C) {
   return c0 + g * 8 < C ? (uint32_t)g * 16u : kBufOob;
 }
 
-template <int N, int KB>
-__device__ __forceinline__ void persist_load_tile(U32x4 (&xr)[KB][N], const uint16_t* __restrict__ x,
-                                                  int64_t tile, int64_t ntiles, int64_t M, int C,
-                                                  int wave, int r, int g) {
-  const int NC = N * C;
-  const auto rsrc = x_tile_rsrc(x, tile, ntiles, M, NC);
-  const uint32_t row_off = (uint32_t)(r * NC) * 2u;
+// Load column blocks [Q0, Q1) of this lane's x chunks of one tile.
+template <int N, int KB, int Q0, int Q1>
+__device__ __forceinline__ void persist_load_part(U32x4 (&xr)[KB][N], __amdgpu_buffer_rsrc_t rsrc,
+                                                  int C, int wave, int r, int g) {
+  const uint32_t row_off = (uint32_t)(r * N * C) * 2u;
 #pragma unroll
-  for (int q = 0; q < KB; ++q) {
+  for (int q = Q0; q < Q1; ++q) {
     const int c0 = (wave + kPersistWaves * q) * kCBlock;
     const uint32_t lo = x_lane_off(q, wave, g, C);
     const uint32_t voff = lo == kBufOob ? kBufOob : row_off + lo;
 #pragma unroll
-    for (int i = 0; i < N; ++i) {
-      const int soff = (i * C + c0) * 2;
-      xr[q][i] = __builtin_bit_cast(U32x4,
-                                    __builtin_amdgcn_raw_buffer_load_b128(rsrc, (int)voff, soff, 0));
-    }
+    for (int i = 0; i < N; ++i)
+      xr[q][i] = __builtin_bit_cast(
+          U32x4, __builtin_amdgcn_raw_buffer_load_b128(rsrc, (int)voff, (i * C + c0) * 2, 0));
   }
 }
 
@@ -237,36 +239,38 @@ __device__ __forceinline__ void persist_gates(const PreArgs& a,
   const int64_t M = a.M;
   const int64_t NC = (int64_t)N * a.C;
   const int64_t t0 = tile * TM;
-  for (int idx = idx0; idx < TM * FD; idx += step) {
-    const int tt = idx / FD;
-    const int f = idx - tt * FD;
+  // 16 threads per token: thread (tt, f0) computes the token's inv_rms and
+  // features f0 and f0 + 16.
+  for (int idx = idx0; idx < TM * 16; idx += step) {
+    const int tt = idx >> 4;
+    const int f0 = idx & 15;
     float sq = 0.f;
-    float sum = 0.f;
 #pragma unroll
-    for (int w = 0; w < kPersistWaves; ++w) {
-      sq += sh.ss[w][tt];
-      sum += sh.acc[w][tt][f];
-    }
+    for (int w = 0; w < kPersistWaves; ++w) sq += sh.ss[w][tt];
     const float inv = 1.0f / sqrtf(sq / (float)NC + a.rms_eps);
-    const float m = sum * inv;
     const int64_t tk = t0 + tt;
     const bool ok = tk < M;
-    if (ok) {
-      if (a.mixes_raw) a.mixes_raw[tk * FD + f] = m;
-      if (a.inv_rms && f == 0) a.inv_rms[tk] = inv;
-    }
-    if (f < N) {
-      const float h = gate_pre(m, sh.prm[0], sh.prm[GP::kBiasPre + f], a.pre_eps, kBF16);
-      sh.hpre[tt][f] = h;
-      if (ok && a.h_pre) st_any(a.h_pre, tk * N + f, kBF16, h);
-    } else if (f < 2 * N) {
-      const float h = gate_post(m, sh.prm[1], sh.prm[GP::kBiasPost + f - N], a.post_mult, kBF16);
-      if (ok) st_any(a.h_post, tk * N + (f - N), kBF16, h);
-    } else {
-      const int e = f - 2 * N;
-      const float h = gate_res(m, sh.prm[2], sh.prm[GP::kBiasRes + e], kBF16);
-      if constexpr (MODE == kFull) sh.hres[slot][tt * G + e] = h;
-      if (ok && a.h_res_raw) st_any(a.h_res_raw, tk * G + e, kBF16, h);
+    if (ok && a.inv_rms && f0 == 0) a.inv_rms[tk] = inv;
+#pragma unroll
+    for (int f = f0; f < FD; f += 16) {
+      float sum = 0.f;
+#pragma unroll
+      for (int w = 0; w < kPersistWaves; ++w) sum += sh.acc[w][tt][f];
+      const float m = sum * inv;
+      if (ok && a.mixes_raw) a.mixes_raw[tk * FD + f] = m;
+      if (f < N) {
+        const float h = gate_pre(m, sh.prm[0], sh.prm[GP::kBiasPre + f], a.pre_eps, kBF16);
+        sh.hpre[tt][f] = h;
+        if (ok && a.h_pre) st_any(a.h_pre, tk * N + f, kBF16, h);
+      } else if (f < 2 * N) {
+        const float h = gate_post(m, sh.prm[1], sh.prm[GP::kBiasPost + f - N], a.post_mult, kBF16);
+        if (ok) st_any(a.h_post, tk * N + (f - N), kBF16, h);
+      } else {
+        const int e = f - 2 * N;
+        const float h = gate_res(m, sh.prm[2], sh.prm[GP::kBiasRes + e], kBF16);
+        if constexpr (MODE == kFull) sh.hres[slot][tt * G + e] = h;
+        if (ok && a.h_res_raw) st_any(a.h_res_raw, tk * G + e, kBF16, h);
+      }
     }
   }
 }
@@ -285,19 +289,17 @@ __device__ __forceinline__ void persist_sinkhorn(const PreArgs& a, const float* 
   if (e < TM * G && t0 + e / G < a.M) st_any(a.h_res, t0 * G + e, kBF16, v);
 }
 
-// ---- phase 3: pre-aggregate from the held x registers; as each column block
-// is done its registers take the loads of tile `next`.
+// ---- phase 3: pre-aggregate from the held x registers.
 template <int N, int MODE, int KB>
 __device__ __forceinline__ void persist_preagg(const PreArgs& a,
                                                const PersistShared<N, PersistPlan<N, MODE, KB>::FD>& sh,
-                                               U32x4 (&xr)[KB][N], int64_t tile, int64_t next,
-                                               int64_t ntiles, int lane, int wave) {
+                                               const U32x4 (&xr)[KB][N], int64_t tile, int lane,
+                                               int wave) {
   constexpr int TM = kTokTile;
   const int r = lane & 15;
   const int g = lane >> 4;
   const int64_t M = a.M;
   const int C = a.C;
-  const int NC = N * C;
   const int64_t t0 = tile * TM;
   uint32_t hlo[N];
   uint32_t hhi[N];
@@ -309,8 +311,6 @@ __device__ __forceinline__ void persist_preagg(const PreArgs& a,
   const int valid = (int)(M - t0 < TM ? M - t0 : TM);
   const auto rsub = make_rsrc(static_cast<uint16_t*>(a.sub_in) + t0 * C, (uint32_t)valid * C * 2u);
   const uint32_t sub_row = (uint32_t)(r * C) * 2u;
-  const auto rnext = x_tile_rsrc(static_cast<const uint16_t*>(a.x), next, ntiles, M, NC);
-  const uint32_t x_row = (uint32_t)(r * NC) * 2u;
 #pragma unroll
   for (int q = 0; q < KB; ++q) {
     const int c0 = (wave + kPersistWaves * q) * kCBlock;
@@ -322,23 +322,26 @@ __device__ __forceinline__ void persist_preagg(const PreArgs& a,
     // stores of that form.  With a register soffset it reused the first data
     // register at once and some lanes stored the new value.
     buf_store16(rsub, lo == kBufOob ? kBufOob : sub_row + lo + (uint32_t)c0 * 2u, pk);
-    const uint32_t voff = lo == kBufOob ? kBufOob : x_row + lo;
-#pragma unroll
-    for (int i = 0; i < N; ++i)
-      xr[q][i] = __builtin_bit_cast(
-          U32x4, __builtin_amdgcn_raw_buffer_load_b128(rnext, (int)voff, (i * C + c0) * 2, 0));
   }
 }
 
-// One tile: partials, barrier, gates || Sinkhorn(prev), barrier, pre-aggregate.
+// One tile: partials, barrier, gates || Sinkhorn(prev), barrier, pre-aggregate;
+// the next tile's loads go into xn in three batches along the way.
 template <int N, int MODE, int KB>
 __device__ __forceinline__ void persist_step(
-    const PreArgs& a, PersistShared<N, PersistPlan<N, MODE, KB>::FD>& sh, U32x4 (&xr)[KB][N],
-    const bf16x8_t (&wreg)[KB][N][PersistPlan<N, MODE, KB>::WR], const unsigned char* lds_w,
-    int64_t tile, int64_t prev, int64_t next, int64_t ntiles, int slot, int tid, int lane, int wave) {
+    const PreArgs& a, PersistShared<N, PersistPlan<N, MODE, KB>::FD>& sh, const U32x4 (&xr)[KB][N],
+    U32x4 (&xn)[KB][N], const bf16x8_t (&wreg)[KB][N][PersistPlan<N, MODE, KB>::WR],
+    const unsigned char* lds_w, int64_t tile, int64_t prev, int64_t ntiles, int slot, int tid,
+    int lane, int wave) {
   using P = PersistPlan<N, MODE, KB>;
+  const int r = lane & 15;
+  const int g = lane >> 4;
+  const auto rn = x_tile_rsrc(static_cast<const uint16_t*>(a.x), tile + gridDim.x, ntiles, a.M,
+                              N * a.C);
+  persist_load_part<N, KB, 0, P::B1>(xn, rn, a.C, wave, r, g);
   persist_partials<N, MODE, KB>(a, sh, xr, wreg, lds_w, lane, wave);
   __syncthreads();
+  persist_load_part<N, KB, P::B1, P::B2>(xn, rn, a.C, wave, r, g);
   if constexpr (MODE == kFull) {
     if (wave < P::SK_WAVES) {
       if (prev >= 0 && a.h_res) persist_sinkhorn<N>(a, sh.hres[slot ^ 1], prev, tid);
@@ -350,7 +353,8 @@ __device__ __forceinline__ void persist_step(
     persist_gates<N, MODE, KB>(a, sh, tile, slot, tid, kPersistWaves * 64);
   }
   __syncthreads();
-  persist_preagg<N, MODE, KB>(a, sh, xr, tile, next, ntiles, lane, wave);
+  persist_load_part<N, KB, P::B2, KB>(xn, rn, a.C, wave, r, g);
+  persist_preagg<N, MODE, KB>(a, sh, xr, tile, lane, wave);
 }
 
 // Gate parameter of thread tid (raw bits; converted once the streaming loads
@@ -415,10 +419,11 @@ __global__ __launch_bounds__(kPersistWaves * 64) void pre_persist_kernel(PreArgs
   const int64_t step = gridDim.x;
   int64_t tile = blockIdx.x;
 
-  // Issue order: gate parameters, register phi tiles, LDS phi tiles (staged in
-  // registers), the x buffers that fit beside that staging, then -- after the
-  // LDS writes, which wait only for phi -- the other x buffers.  Padding lanes
-  // of a compact phi tile write into the (not yet used) partials area.
+  // Issue order: gate parameters, register phi tiles, the first x tile (when
+  // it fits beside the LDS phi staging), LDS phi tiles, the first x tile
+  // otherwise.  The LDS writes wait only for phi.  Padding lanes of a compact
+  // phi tile write into the (not yet used) partials area.  The second tile's
+  // loads go out during the first step.
   const RawParam rp = load_gate_param<N, MODE>(a, tid);
 
   const uint32_t wbytes = (uint32_t)(N * NCB * P::NT) * 64u * 16u;
@@ -438,15 +443,8 @@ __global__ __launch_bounds__(kPersistWaves * 64) void pre_persist_kernel(PreArgs
 
   U32x4 xa[KB][N];
   U32x4 xb[KB][N];
-  U32x4 xc[P::DEPTH == 3 ? KB : 1][N];
-  // x buffer b (0 = xa, 1 = xb, 2 = xc) holds tile blockIdx.x + b * step.
-  auto load_x = [&](int first, int last) {
-    if (first <= 0 && 0 < last) persist_load_tile<N, KB>(xa, x, tile, ntiles, a.M, C, wave, r, g);
-    if (first <= 1 && 1 < last) persist_load_tile<N, KB>(xb, x, tile + step, ntiles, a.M, C, wave, r, g);
-    if constexpr (P::DEPTH == 3)
-      if (first <= 2 && 2 < last)
-        persist_load_tile<N, KB>(xc, x, tile + 2 * step, ntiles, a.M, C, wave, r, g);
-  };
+  const auto r0 = x_tile_rsrc(x, tile, ntiles, a.M, N * C);
+  if constexpr (P::X_EARLY) persist_load_part<N, KB, 0, KB>(xa, r0, C, wave, r, g);
   constexpr int NST = P::NLDS > 0 ? P::NLDS : 1;
   U32x4 st[NST][KB][N];  // LDS phi tiles, staged
 #pragma unroll
@@ -455,7 +453,6 @@ __global__ __launch_bounds__(kPersistWaves * 64) void pre_persist_kernel(PreArgs
     for (int q = 0; q < KB; ++q)
 #pragma unroll
       for (int i = 0; i < N; ++i) st[t][q][i] = buf_load16(wr, phi_off(P::NREG + t, q, i));
-  load_x(0, P::X_EARLY);
 #pragma unroll
   for (int t = 0; t < P::NLDS; ++t) {
     const int nt = P::NREG + t;
@@ -470,35 +467,35 @@ __global__ __launch_bounds__(kPersistWaves * 64) void pre_persist_kernel(PreArgs
         *reinterpret_cast<U32x4*>(dst) = st[t][q][i];
       }
   }
-  load_x(P::X_EARLY, P::DEPTH);
+  if constexpr (!P::X_EARLY) persist_load_part<N, KB, 0, KB>(xa, r0, C, wave, r, g);
 
   if (tid == 0) sh.zero = U32x4{{0u, 0u, 0u, 0u}};
   if (tid < GateParams<N>::kCount) sh.prm[tid] = convert_param(rp, a.param_dtype);
   __syncthreads();  // gate parameters, zero block and phi tiles visible
 
-  // Whole rounds of DEPTH steps, then the 0..DEPTH-1 leftover steps.  The
-  // loop body has no exit between its steps: an exit there leaves the compiler
-  // a path into the loop header on which the prefetch order differs, and the
-  // header then waits for every load in flight.
+  // Pairs of steps (xa computes while xb loads, then the reverse), then the
+  // leftover step.  The loop body has no exit between its steps: an exit
+  // there leaves the compiler a path into the loop header on which the
+  // prefetch order differs, and the header then waits for every load in
+  // flight.
   const int64_t my_tiles = (ntiles - blockIdx.x + step - 1) / step;
   int64_t prev = -1;
   int slot = 0;
-  auto run = [&](U32x4 (&xr)[KB][N]) {
-    persist_step<N, MODE, KB>(a, sh, xr, wreg, lds_w, tile, prev, tile + P::DEPTH * step, ntiles,
-                              slot, tid, lane, wave);
+  int64_t k = 0;
+  for (; k + 2 <= my_tiles; k += 2) {  // uniform across the workgroup
+    persist_step<N, MODE, KB>(a, sh, xa, xb, wreg, lds_w, tile, prev, ntiles, slot, tid, lane, wave);
     prev = tile;
     slot ^= 1;
     tile += step;
-  };
-  int64_t k = 0;
-  for (; k + P::DEPTH <= my_tiles; k += P::DEPTH) {  // uniform across the workgroup
-    run(xa);
-    run(xb);
-    if constexpr (P::DEPTH == 3) run(xc);
+    persist_step<N, MODE, KB>(a, sh, xb, xa, wreg, lds_w, tile, prev, ntiles, slot, tid, lane, wave);
+    prev = tile;
+    slot ^= 1;
+    tile += step;
   }
   if (k < my_tiles) {
-    run(xa);
-    if (k + 1 < my_tiles) run(xb);
+    persist_step<N, MODE, KB>(a, sh, xa, xb, wreg, lds_w, tile, prev, ntiles, slot, tid, lane, wave);
+    prev = tile;
+    slot ^= 1;
   }
   // The last tile's Sinkhorn (its logits were published by the final barrier).
   if constexpr (MODE == kFull) {
