@@ -22,16 +22,22 @@
 //     also wait for the prefetch.  Gate scalars and biases are read once, with
 //     branch-free loads issued before everything else, and kept in LDS as fp32.
 //
-// Per tile, two workgroup barriers split three phases:
-//   1. all waves: sum of squares + MFMA partial projections -> LDS;
-//   2. waves SK_WAVES..7: reduce partials, inv_rms, gates (h_pre to LDS, h_res
-//      logits to one of two LDS slots); meanwhile waves 0..SK_WAVES-1 run the
-//      Sinkhorn-Knopp iterations of the PREVIOUS tile from the other slot.  The
-//      Sinkhorn is a ~20-step dependent chain; running it one tile behind, in
-//      parallel with the gates, takes it off the per-tile critical path;
-//   3. all waves: pre-aggregate from the held x registers, store sub_in, issue
-//      the next loads.
-// The last tile's Sinkhorn runs after the loop.
+// Per tile, one workgroup barrier:
+//   1. all waves: sum of squares + MFMA partial projections -> LDS (two slots,
+//      alternating per tile, so a fast wave may start the next tile's partials
+//      while others still read this tile's);
+//   -- barrier --
+//   2. waves 0..SK_WAVES-1 first run the Sinkhorn-Knopp iterations of the
+//      PREVIOUS tile (h_res logits from the other LDS slot): a ~20-step
+//      dependent chain that overlaps the VALU-heavy pre-aggregate of the wave
+//      sharing the SIMD;
+//   3. every wave computes the tile's h_pre itself (one (token, stream) per
+//      lane, straight from the partials, then spread to the lanes that use it)
+//      and runs its pre-aggregate; one wave also writes h_post / h_pre /
+//      inv_rms, and the gate waves write the h_res logits (one per lane) for
+//      the next tile's Sinkhorn.
+// The next tile's x loads go out in three batches along the way.  The last
+// tile's Sinkhorn runs after the loop.
 //
 // Reference semantics: model/mhc_fused.py:163-268, :533-559, :47-56,
 // :820-830; model/mhc_fused_no_hres.py:48-145; model/mhc_common.py:128-195.
@@ -57,11 +63,10 @@ struct GateParams {
 template <int N, int FD>
 struct PersistShared {
   float prm[GateParams<N>::kCount];
-  float acc[kPersistWaves][kTokTile][FD];  // per-wave partial projections
-  float ss[kPersistWaves][kTokTile];       // per-wave partial sums of squares
-  float hpre[kTokTile][N];
-  float hres[2][kTokTile * N * N];         // h_res logits, two tiles in flight
-  U32x4 zero;                              // B operand of padding columns
+  float acc[2][kPersistWaves][kTokTile][FD];  // per-wave partial projections, 2 slots
+  float ss[2][kPersistWaves][kTokTile];       // per-wave partial sums of squares
+  float hres[2][kTokTile * N * N];            // h_res logits, two tiles in flight
+  U32x4 zero;                                 // B operand of padding columns
 };
 
 template <int N, int MODE, int KB>
@@ -116,9 +121,12 @@ struct PersistPlan {
   // Waves that run the Sinkhorn (whole waves covering a tile's TM*G elements);
   // the gates run on the others.  Without h_res every wave runs the gates.
   static constexpr int SK_WAVES = MODE == kFull ? (kTokTile * G + 63) / 64 : 0;
+  static constexpr int GATE_LANES = (kPersistWaves - SK_WAVES) * 64;
   static_assert(SK_WAVES < kPersistWaves, "gates need at least one wave");
-  static_assert(FD <= 32, "gates map at most two features to a thread");
+  static_assert(kTokTile * N <= 64, "one wave holds a tile's h_pre, one per lane");
   static_assert(kPersistWaves * kTokTile * FD * 4 >= 64 * 16, "partials area doubles as a write sink");
+  // Wave that writes h_post (and h_pre / inv_rms when asked for).
+  static constexpr int POST_WAVE = kPersistWaves - 1;
 };
 
 // Tokens of a tile that exist (0 for a tile past the end).
@@ -169,7 +177,7 @@ template <int N, int MODE, int KB>
 __device__ __forceinline__ void persist_partials(
     const PreArgs& a, PersistShared<N, PersistPlan<N, MODE, KB>::FD>& sh, const U32x4 (&xr)[KB][N],
     const bf16x8_t (&wreg)[KB][N][PersistPlan<N, MODE, KB>::WR], const unsigned char* lds_w,
-    int lane, int wave) {
+    int slot, int lane, int wave) {
   using P = PersistPlan<N, MODE, KB>;
   constexpr int FD = P::FD;
   constexpr int NT = P::NT;
@@ -222,55 +230,90 @@ __device__ __forceinline__ void persist_partials(
   for (int nt = 0; nt < NT; ++nt)
     if (nt * 16 + r < FD)
 #pragma unroll
-      for (int j = 0; j < 4; ++j) sh.acc[wave][4 * g + j][nt * 16 + r] = acc[nt][j];
-  if (g == 0) sh.ss[wave][r] = ss;
+      for (int j = 0; j < 4; ++j) sh.acc[slot][wave][4 * g + j][nt * 16 + r] = acc[nt][j];
+  if (g == 0) sh.ss[slot][wave][r] = ss;
 }
 
-// ---- phase 2a: reduce partials, inv_rms, gates (threads idx0, idx0 + step, ...)
+// ---- gates ---------------------------------------------------------------
+// inv_rms of token tt and the reduced projection m = (sum_w partial) * inv of
+// feature f, from partials slot `slot`.
+template <int N, int FD>
+__device__ __forceinline__ float persist_inv_rms(const PersistShared<N, FD>& sh, int slot, int tt,
+                                                 float nc, float eps) {
+  float sq = 0.f;
+#pragma unroll
+  for (int w = 0; w < kPersistWaves; ++w) sq += sh.ss[slot][w][tt];
+  return 1.0f / sqrtf(sq / nc + eps);
+}
+
+template <int N, int FD>
+__device__ __forceinline__ float persist_mix(const PersistShared<N, FD>& sh, int slot, int tt, int f,
+                                             float inv) {
+  float sum = 0.f;
+#pragma unroll
+  for (int w = 0; w < kPersistWaves; ++w) sum += sh.acc[slot][w][tt][f];
+  return sum * inv;
+}
+
+// h_pre of (token lane / N, stream lane % N) for every wave (lanes past TM*N
+// return 0); wave POST_WAVE also writes h_post, h_pre, inv_rms and the
+// pre/post mixes when asked for.
 template <int N, int MODE, int KB>
-__device__ __forceinline__ void persist_gates(const PreArgs& a,
-                                              PersistShared<N, PersistPlan<N, MODE, KB>::FD>& sh,
-                                              int64_t tile, int slot, int idx0, int step) {
+__device__ __forceinline__ float persist_pre_post(const PreArgs& a,
+                                                  const PersistShared<N, PersistPlan<N, MODE, KB>::FD>& sh,
+                                                  int64_t tile, int slot, int lane, int wave) {
+  using P = PersistPlan<N, MODE, KB>;
+  using GP = GateParams<N>;
+  constexpr int FD = P::FD;
+  float hp = 0.f;
+  if (lane < kTokTile * N) {
+    const int tt = lane / N;
+    const int i = lane % N;
+    const float inv = persist_inv_rms(sh, slot, tt, (float)(N * a.C), a.rms_eps);
+    const float m = persist_mix(sh, slot, tt, i, inv);
+    hp = gate_pre(m, sh.prm[0], sh.prm[GP::kBiasPre + i], a.pre_eps, kBF16);
+    if (wave == P::POST_WAVE) {
+      const int64_t tk = tile * kTokTile + tt;
+      const bool ok = tk < a.M;
+      if (ok) {
+        if (a.h_pre) st_any(a.h_pre, tk * N + i, kBF16, hp);
+        if (a.inv_rms && i == 0) a.inv_rms[tk] = inv;
+        if (a.mixes_raw) a.mixes_raw[tk * FD + i] = m;
+      }
+      if constexpr (MODE != kHead) {
+        const float mp = persist_mix(sh, slot, tt, N + i, inv);
+        const float hq = gate_post(mp, sh.prm[1], sh.prm[GP::kBiasPost + i], a.post_mult, kBF16);
+        if (ok) {
+          st_any(a.h_post, tk * N + i, kBF16, hq);
+          if (a.mixes_raw) a.mixes_raw[tk * FD + N + i] = mp;
+        }
+      }
+    }
+  }
+  return hp;
+}
+
+// h_res logits of the tile, one (token, element) per lane of the gate waves,
+// into LDS slot `slot` for the next step's Sinkhorn.
+template <int N, int MODE, int KB>
+__device__ __forceinline__ void persist_res_gates(const PreArgs& a,
+                                                  PersistShared<N, PersistPlan<N, MODE, KB>::FD>& sh,
+                                                  int64_t tile, int slot, int idx0) {
   using P = PersistPlan<N, MODE, KB>;
   using GP = GateParams<N>;
   constexpr int FD = P::FD;
   constexpr int G = P::G;
-  constexpr int TM = kTokTile;
-  const int64_t M = a.M;
-  const int64_t NC = (int64_t)N * a.C;
-  const int64_t t0 = tile * TM;
-  // 16 threads per token: thread (tt, f0) computes the token's inv_rms and
-  // features f0 and f0 + 16.
-  for (int idx = idx0; idx < TM * 16; idx += step) {
-    const int tt = idx >> 4;
-    const int f0 = idx & 15;
-    float sq = 0.f;
-#pragma unroll
-    for (int w = 0; w < kPersistWaves; ++w) sq += sh.ss[w][tt];
-    const float inv = 1.0f / sqrtf(sq / (float)NC + a.rms_eps);
-    const int64_t tk = t0 + tt;
-    const bool ok = tk < M;
-    if (ok && a.inv_rms && f0 == 0) a.inv_rms[tk] = inv;
-#pragma unroll
-    for (int f = f0; f < FD; f += 16) {
-      float sum = 0.f;
-#pragma unroll
-      for (int w = 0; w < kPersistWaves; ++w) sum += sh.acc[w][tt][f];
-      const float m = sum * inv;
-      if (ok && a.mixes_raw) a.mixes_raw[tk * FD + f] = m;
-      if (f < N) {
-        const float h = gate_pre(m, sh.prm[0], sh.prm[GP::kBiasPre + f], a.pre_eps, kBF16);
-        sh.hpre[tt][f] = h;
-        if (ok && a.h_pre) st_any(a.h_pre, tk * N + f, kBF16, h);
-      } else if (f < 2 * N) {
-        const float h = gate_post(m, sh.prm[1], sh.prm[GP::kBiasPost + f - N], a.post_mult, kBF16);
-        if (ok) st_any(a.h_post, tk * N + (f - N), kBF16, h);
-      } else {
-        const int e = f - 2 * N;
-        const float h = gate_res(m, sh.prm[2], sh.prm[GP::kBiasRes + e], kBF16);
-        if constexpr (MODE == kFull) sh.hres[slot][tt * G + e] = h;
-        if (ok && a.h_res_raw) st_any(a.h_res_raw, tk * G + e, kBF16, h);
-      }
+  for (int idx = idx0; idx < kTokTile * G; idx += P::GATE_LANES) {
+    const int tt = idx / G;
+    const int e = idx % G;
+    const float inv = persist_inv_rms(sh, slot, tt, (float)(N * a.C), a.rms_eps);
+    const float m = persist_mix(sh, slot, tt, 2 * N + e, inv);
+    const float h = gate_res(m, sh.prm[2], sh.prm[GP::kBiasRes + e], kBF16);
+    sh.hres[slot][idx] = h;
+    const int64_t tk = tile * kTokTile + tt;
+    if (tk < a.M) {
+      if (a.h_res_raw) st_any(a.h_res_raw, tk * G + e, kBF16, h);
+      if (a.mixes_raw) a.mixes_raw[tk * FD + 2 * N + e] = m;
     }
   }
 }
@@ -290,24 +333,16 @@ __device__ __forceinline__ void persist_sinkhorn(const PreArgs& a, const float* 
 }
 
 // ---- phase 3: pre-aggregate from the held x registers.
-template <int N, int MODE, int KB>
-__device__ __forceinline__ void persist_preagg(const PreArgs& a,
-                                               const PersistShared<N, PersistPlan<N, MODE, KB>::FD>& sh,
-                                               const U32x4 (&xr)[KB][N], int64_t tile, int lane,
-                                               int wave) {
+template <int N, int KB>
+__device__ __forceinline__ void persist_preagg(const PreArgs& a, const U32x4 (&xr)[KB][N],
+                                               const uint32_t (&hlo)[N], const uint32_t (&hhi)[N],
+                                               int64_t tile, int lane, int wave) {
   constexpr int TM = kTokTile;
   const int r = lane & 15;
   const int g = lane >> 4;
   const int64_t M = a.M;
   const int C = a.C;
   const int64_t t0 = tile * TM;
-  uint32_t hlo[N];
-  uint32_t hhi[N];
-#pragma unroll
-  for (int i = 0; i < N; ++i) {
-    hlo[i] = pack_lo(sh.hpre[r][i]);
-    hhi[i] = pack_hi(sh.hpre[r][i]);
-  }
   const int valid = (int)(M - t0 < TM ? M - t0 : TM);
   const auto rsub = make_rsrc(static_cast<uint16_t*>(a.sub_in) + t0 * C, (uint32_t)valid * C * 2u);
   const uint32_t sub_row = (uint32_t)(r * C) * 2u;
@@ -325,8 +360,8 @@ __device__ __forceinline__ void persist_preagg(const PreArgs& a,
   }
 }
 
-// One tile: partials, barrier, gates || Sinkhorn(prev), barrier, pre-aggregate;
-// the next tile's loads go into xn in three batches along the way.
+// One tile (partials slot and h_res slot `slot`); the next tile's loads go
+// into xn in three batches along the way.
 template <int N, int MODE, int KB>
 __device__ __forceinline__ void persist_step(
     const PreArgs& a, PersistShared<N, PersistPlan<N, MODE, KB>::FD>& sh, const U32x4 (&xr)[KB][N],
@@ -339,22 +374,27 @@ __device__ __forceinline__ void persist_step(
   const auto rn = x_tile_rsrc(static_cast<const uint16_t*>(a.x), tile + gridDim.x, ntiles, a.M,
                               N * a.C);
   persist_load_part<N, KB, 0, P::B1>(xn, rn, a.C, wave, r, g);
-  persist_partials<N, MODE, KB>(a, sh, xr, wreg, lds_w, lane, wave);
+  persist_partials<N, MODE, KB>(a, sh, xr, wreg, lds_w, slot, lane, wave);
   __syncthreads();
   persist_load_part<N, KB, P::B1, P::B2>(xn, rn, a.C, wave, r, g);
   if constexpr (MODE == kFull) {
-    if (wave < P::SK_WAVES) {
-      if (prev >= 0 && a.h_res) persist_sinkhorn<N>(a, sh.hres[slot ^ 1], prev, tid);
-    } else {
-      persist_gates<N, MODE, KB>(a, sh, tile, slot, tid - P::SK_WAVES * 64,
-                                 (kPersistWaves - P::SK_WAVES) * 64);
-    }
-  } else {
-    persist_gates<N, MODE, KB>(a, sh, tile, slot, tid, kPersistWaves * 64);
+    if (wave < P::SK_WAVES && prev >= 0 && a.h_res)
+      persist_sinkhorn<N>(a, sh.hres[slot ^ 1], prev, tid);
   }
-  __syncthreads();
+  const float hp = persist_pre_post<N, MODE, KB>(a, sh, tile, slot, lane, wave);
+  if constexpr (MODE == kFull) {
+    if (wave >= P::SK_WAVES) persist_res_gates<N, MODE, KB>(a, sh, tile, slot, tid - P::SK_WAVES * 64);
+  }
+  uint32_t hlo[N];
+  uint32_t hhi[N];
+#pragma unroll
+  for (int i = 0; i < N; ++i) {  // h_pre of this lane's token r, stream i
+    const float h = __shfl(hp, r * N + i, 64);
+    hlo[i] = pack_lo(h);
+    hhi[i] = pack_hi(h);
+  }
+  persist_preagg<N, KB>(a, xr, hlo, hhi, tile, lane, wave);
   persist_load_part<N, KB, P::B2, KB>(xn, rn, a.C, wave, r, g);
-  persist_preagg<N, MODE, KB>(a, sh, xr, tile, lane, wave);
 }
 
 // Gate parameter of thread tid (raw bits; converted once the streaming loads
@@ -497,8 +537,9 @@ __global__ __launch_bounds__(kPersistWaves * 64) void pre_persist_kernel(PreArgs
     prev = tile;
     slot ^= 1;
   }
-  // The last tile's Sinkhorn (its logits were published by the final barrier).
+  // The last tile's Sinkhorn, once every gate wave has written its logits.
   if constexpr (MODE == kFull) {
+    __syncthreads();
     if (wave < P::SK_WAVES && a.h_res) persist_sinkhorn<N>(a, sh.hres[slot ^ 1], prev, tid);
   }
 }
