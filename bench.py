@@ -9,9 +9,9 @@ pre-aggregate) and the post phase (res-mix + post-expand).
 
 Timing: W untimed warmup steps, then K timed steps bracketed by
 torch.cuda.synchronize().  A step runs the pre kernel on 4 distinct input
-sets, then the post kernel on the same 4 sets (see bench_mhc for why), each
-launch bracketed by HIP events on the stream it runs on; value = tokens /
-(mean pre + mean post kernel time).  A cold-cache measurement (read-only
+sets, then the post kernel on the same 4 sets (see bench_mhc for why); each
+group of 4 back-to-back launches of one kernel is bracketed by HIP events on
+the stream it runs on; value = tokens / (mean pre + mean post launch time).  A cold-cache measurement (read-only
 flush before each kernel) and plain torch copy / sum kernels over 1 GiB
 (`hbm_calibration`) are reported beside it.
 
@@ -19,7 +19,15 @@ Also printed in the JSON line: roofline of the dominant (post) kernel against
 8 TB/s, the CPU oracle baseline (bounded sample, host cores), and the e2e
 MiniMind-3-mHC prefill tokens/s (config 3).
 
+`roofline.traffic` is the measured HBM traffic of that kernel per launch:
+FETCH_SIZE + WRITE_SIZE from two rocprofv3 --pmc passes over `--traffic`
+(a 1 GiB copy of known size, then one pre and one post launch at config 2),
+each scaled by the copy kernel's bytes / counter ratio.  The figures are read
+from profiles/traffic_mhc_fwd_c2.txt (the rocprofv3 summary committed beside
+the kernel-trace summary); traffic is null when that file is absent.
+
 Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--no-e2e] [--no-cpu]
+       python bench.py --traffic     (counter passes only; prints nothing)
 """
 from __future__ import annotations
 
@@ -103,19 +111,18 @@ def bench_mhc(steps: int, warmup: int, sets: int = 4):
         return torch.cuda.Event(enable_timing=True)
 
     def step(rec):
-        outs = []
+        # one event pair around the `sets` back-to-back launches of each
+        # kernel: per-launch time = elapsed / sets (bracketing every launch
+        # would add the event packets' own dispatch latency to each one)
+        e0, e1, e2 = ev(), ev(), ev()
+        e0.record()
+        outs = [pre(s) for s in range(sets)]
+        e1.record()
         for s in range(sets):
-            e0, e1 = ev(), ev()
-            e0.record()
-            outs.append(pre(s))
-            e1.record()
-            rec["pre"].append((e0, e1))
-        for s in range(sets):
-            e0, e1 = ev(), ev()
-            e0.record()
             post(s, outs[s])
-            e1.record()
-            rec["post"].append((e0, e1))
+        e2.record()
+        rec["pre"].append((e0, e1))
+        rec["post"].append((e1, e2))
 
     for _ in range(warmup):
         step({"pre": [], "post": []})
@@ -127,8 +134,8 @@ def bench_mhc(steps: int, warmup: int, sets: int = 4):
         step(rec)
     _sync()
     wall = (time.perf_counter() - t0) / (steps * sets) * 1e3
-    t_pre = [a_.elapsed_time(b_) for a_, b_ in rec["pre"]]
-    t_post = [a_.elapsed_time(b_) for a_, b_ in rec["post"]]
+    t_pre = [a_.elapsed_time(b_) / sets for a_, b_ in rec["pre"]]
+    t_post = [a_.elapsed_time(b_) / sets for a_, b_ in rec["post"]]
     steady = dict(t_pre=sum(t_pre) / len(t_pre), t_post=sum(t_post) / len(t_post),
                   t_pre_min=min(t_pre), t_post_min=min(t_post), wall=wall)
 
@@ -155,6 +162,56 @@ def bench_mhc(steps: int, warmup: int, sets: int = 4):
     c_post = [a_.elapsed_time(b_) for a_, b_ in cold["post"]]
     del flush
     return steady, dict(t_pre=sum(c_pre) / len(c_pre), t_post=sum(c_post) / len(c_post))
+
+
+TRAFFIC_FILE = ROOT / "profiles" / "traffic_mhc_fwd_c2.txt"
+
+
+def read_traffic():
+    """Measured bytes per launch from the committed counter summary:
+    lines `<key>: <bytes>` for pre_fetch, pre_write, post_fetch, post_write
+    (already scaled by the copy-kernel calibration)."""
+    if not TRAFFIC_FILE.exists():
+        return None
+    vals = {}
+    for ln in TRAFFIC_FILE.read_text().splitlines():
+        k, sep, v = ln.partition(":")
+        if sep and k.strip() in ("pre_fetch", "pre_write", "post_fetch", "post_write"):
+            try:
+                vals[k.strip()] = float(v.split()[0])
+            except (ValueError, IndexError):
+                pass
+    return vals if len(vals) == 4 else None
+
+
+def traffic_passes():
+    """What the FETCH_SIZE / WRITE_SIZE counter passes run: a plain copy of
+    1 GiB -> 1 GiB and a plain sum over 1 GiB (known bytes, to calibrate the
+    counters), then one pre and one post launch at config 2 on fresh data."""
+    import torch
+    from model import _hip as H, _ops
+
+    dev = torch.device("cuda:0")
+    src = torch.ones(256 * 1024 * 1024, dtype=torch.float32, device=dev)
+    dst = torch.empty_like(src)
+    sink = torch.empty((), dtype=torch.float32, device=dev)
+    dst.copy_(src)
+    torch.sum(src, dim=0, out=sink)
+    _sync()
+    del src, dst
+    n, C, M = N_STREAMS, C_DIM, TOKENS
+    g = torch.Generator().manual_seed(0)
+    x = torch.randn(1, M, n * C, generator=g).to(torch.bfloat16).to(dev)
+    f = torch.randn(M, C, generator=g).to(torch.bfloat16).to(dev)
+    phi = (torch.randn(n * C, 2 * n + n * n, generator=g) * 0.02).to(torch.bfloat16).to(dev)
+    a = torch.tensor(0.01, dtype=torch.bfloat16, device=dev)
+    b0 = torch.zeros(n, dtype=torch.bfloat16, device=dev)
+    br = torch.eye(n, dtype=torch.bfloat16, device=dev)
+    packed = _ops.PhiPack(H.MODE_FULL).get(phi, n, C)
+    _sync()
+    o = _ops.pre_full(x, phi, packed, a, b0, a, b0, a, br, n, C, 2.0, 1e-6, 1e-6, ITERS, 1e-6)
+    _ops.post(x, o["h_res"], o["h_post"], f, n, C)
+    _sync()
 
 
 def hbm_calibration(reps: int = 10):
@@ -247,6 +304,8 @@ def main():
     ap.add_argument("--warmup", type=int, default=10)
     ap.add_argument("--no-e2e", action="store_true")
     ap.add_argument("--no-cpu", action="store_true")
+    ap.add_argument("--traffic", action="store_true",
+                    help="run the counter-calibration and config-2 launches once, print nothing")
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py: this build measures one GPU only (the mHC forward is per-token and "
@@ -258,6 +317,10 @@ def main():
         print("bench.py: no ROCm GPU visible", file=sys.stderr)
         sys.exit(1)
 
+    if args.traffic:
+        traffic_passes()
+        return
+
     r, rc = bench_mhc(args.steps, args.warmup)
     pre_b, post_b = algorithmic_bytes(N_STREAMS, C_DIM, TOKENS)
     step_ms = r["t_pre"] + r["t_post"]
@@ -266,6 +329,7 @@ def main():
     pre_gbs = pre_b / (r["t_pre"] * 1e-3) / 1e9
     total_gbs = (pre_b + post_b) / (step_ms * 1e-3) / 1e9
     c_ms = rc["t_pre"] + rc["t_post"]
+    tr = read_traffic()
     line = {
         "metric": METRIC,
         "value": round(value, 1),
@@ -286,8 +350,15 @@ def main():
                    "timing": "steady state over 4 rotating input sets, HIP events per kernel"},
         "roofline": {"bound": "hbm", "kernel": "post_vec_kernel (res-mix + post-expand)",
                      "achieved": round(post_gbs, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
-                     "frac": round(post_gbs / HBM_PEAK_GBS, 4), "traffic": None,
+                     "frac": round(post_gbs / HBM_PEAK_GBS, 4),
+                     "traffic": round(tr["post_fetch"] + tr["post_write"]) if tr else None,
                      "algorithmic_bytes_per_launch": post_b},
+        "pre_roofline": {"bound": "hbm", "kernel": "pre_persist_kernel (RMS + projection + gates "
+                                                   "+ Sinkhorn + pre-aggregate)",
+                         "achieved": round(pre_gbs, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                         "frac": round(pre_gbs / HBM_PEAK_GBS, 4),
+                         "traffic": round(tr["pre_fetch"] + tr["pre_write"]) if tr else None,
+                         "algorithmic_bytes_per_launch": pre_b},
         "step_roofline": {"achieved": round(total_gbs, 1), "frac": round(total_gbs / HBM_PEAK_GBS, 4),
                           "algorithmic_bytes_per_step": pre_b + post_b},
         "kernels": {"pre_ms": round(r["t_pre"], 5), "post_ms": round(r["t_post"], 5),
