@@ -184,7 +184,7 @@ def read_traffic():
     return vals if len(vals) == 4 else None
 
 
-def traffic_passes():
+def traffic_passes(vector_pre: bool = False):
     """What the FETCH_SIZE / WRITE_SIZE counter passes run: a plain copy of
     1 GiB -> 1 GiB and a plain sum over 1 GiB (known bytes, to calibrate the
     counters), then one pre and one post launch at config 2 on fresh data."""
@@ -212,6 +212,11 @@ def traffic_passes():
     o = _ops.pre_full(x, phi, packed, a, b0, a, b0, a, br, n, C, 2.0, 1e-6, 1e-6, ITERS, 1e-6)
     _ops.post(x, o["h_res"], o["h_post"], f, n, C)
     _sync()
+    if vector_pre:
+        # the same pre phase on the generic VALU kernel (projection as fp32
+        # FMAs, no MFMA), for the MFMA-vs-VALU comparison
+        _ops.pre_full(x, phi, None, a, b0, a, b0, a, br, n, C, 2.0, 1e-6, 1e-6, ITERS, 1e-6)
+        _sync()
 
 
 def hbm_calibration(reps: int = 10):
@@ -306,6 +311,8 @@ def main():
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--traffic", action="store_true",
                     help="run the counter-calibration and config-2 launches once, print nothing")
+    ap.add_argument("--vector-pre", action="store_true",
+                    help="with --traffic: also run the pre phase on the generic VALU kernel")
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py: this build measures one GPU only (the mHC forward is per-token and "
@@ -318,7 +325,7 @@ def main():
         sys.exit(1)
 
     if args.traffic:
-        traffic_passes()
+        traffic_passes(args.vector_pre)
         return
 
     r, rc = bench_mhc(args.steps, args.warmup)
