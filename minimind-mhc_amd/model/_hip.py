@@ -7,12 +7,16 @@ fallback: a missing library, a CPU tensor or an unsupported dtype raises.
 from __future__ import annotations
 
 import ctypes
+import os
 from pathlib import Path
 from typing import Optional
 
 import torch
 
-LIB_PATH = Path(__file__).resolve().parent.parent / "libmhc_amd.so"
+# The library built next to this package, unless MHC_AMD_LIB names another path
+# (for a checkout that copies these modules into its own package).
+LIB_PATH = Path(os.environ.get("MHC_AMD_LIB") or
+                Path(__file__).resolve().parent.parent / "libmhc_amd.so")
 
 DTYPE_F32, DTYPE_BF16, DTYPE_F16 = 0, 1, 2
 MODE_FULL, MODE_NOHRES, MODE_HEAD = 0, 1, 2

@@ -180,3 +180,37 @@ def test_head_backward_vs_oracle_autograd(dev):
     assert maxrel(xr.grad, xd.grad) <= 1e-4
     for k in p:
         assert maxrel(pr[k].grad, getattr(mod, k).grad) <= 1e-4, k
+
+
+def test_integration_ctypes_stub(dev, monkeypatch):
+    """The ctypes binding shown in INTEGRATION.md, executed as written, gives
+    the same outputs as the package's own ops (it calls the same C ABI)."""
+    import re
+    from pathlib import Path
+
+    from model import _hip as H, _ops
+
+    text = (Path(__file__).resolve().parent.parent / "INTEGRATION.md").read_text()
+    sec = text[text.index("## 2."):]
+    code = re.search(r"```python\n(.*?)```", sec, re.S).group(1)
+    monkeypatch.setenv("MHC_AMD_LIB", str(H.LIB_PATH))
+    ns = {}
+    exec(compile(code, "INTEGRATION.md", "exec"), ns)
+
+    n, C, M = 4, 768, 80
+    g = torch.Generator().manual_seed(3)
+    x = torch.randn(2, M // 2, n * C, generator=g).to(torch.bfloat16).to(dev)
+    f = torch.randn(2, M // 2, C, generator=g).to(torch.bfloat16).to(dev)
+    p = {k: v.to(dev) for k, v in make_params("full", n, C, torch.bfloat16, g).items()}
+    packed = _ops.PhiPack(H.MODE_FULL).get(p["phi_weight"], n, C)
+    args = (p["alpha_pre"], p["bias_pre"], p["alpha_post"], p["bias_post"], p["alpha_res"],
+            p["bias_res"])
+    sub, h_post, h_res = ns["mhc_pre_sinkhorn"](x, p["phi_weight"], *args, 2.0, 1e-6, 1e-6, n, C,
+                                               20, 1e-6, packed=packed)
+    o = _ops.pre_full(x, p["phi_weight"], packed, *args, n, C, 2.0, 1e-6, 1e-6, 20, 1e-6)
+    assert torch.equal(sub.reshape(M, C), o["sub_in"])
+    assert torch.equal(h_post.reshape(M, n), o["h_post"])
+    assert torch.equal(h_res.reshape(M, n, n), o["h_res"])
+    out = ns["mhc_post"](x, h_res, h_post, f, n, C)
+    ref = _ops.post(x, o["h_res"], o["h_post"], f.reshape(M, C), n, C)
+    assert torch.equal(out.reshape(M, n * C), ref.reshape(M, n * C))
