@@ -227,6 +227,29 @@ __device__ __forceinline__ float row_reduce(float v) {
   return v;
 }
 
+// The value of the lane 16 (32) lanes away: v_permlane16_swap /
+// v_permlane32_swap exchange rows of two registers without going through LDS.
+// Fed two copies of v, the first result holds v of the even rows (halves) and
+// the second of the odd ones, so each lane's partner value is whichever of
+// the two is not its own.  The copy goes through an opaque move: given the
+// same value twice the compiler folds the two results into one.
+__device__ __forceinline__ float xor_lane16(float v) {
+  uint32_t a = __builtin_bit_cast(uint32_t, v);
+  uint32_t b;
+  asm volatile("v_mov_b32 %0, %1" : "=v"(b) : "v"(a));
+  const auto r = __builtin_amdgcn_permlane16_swap(a, b, false, false);
+  const bool odd_row = (__lane_id() >> 4) & 1;
+  return __builtin_bit_cast(float, odd_row ? r[0] : r[1]);
+}
+__device__ __forceinline__ float xor_lane32(float v) {
+  uint32_t a = __builtin_bit_cast(uint32_t, v);
+  uint32_t b;
+  asm volatile("v_mov_b32 %0, %1" : "=v"(b) : "v"(a));
+  const auto r = __builtin_amdgcn_permlane32_swap(a, b, false, false);
+  const bool upper = __lane_id() >= 32;
+  return __builtin_bit_cast(float, upper ? r[0] : r[1]);
+}
+
 // Reduce over the N lanes of one matrix column (stride N inside N*N lanes).
 template <int N>
 __device__ __forceinline__ float col_sum(float v) {
@@ -237,8 +260,8 @@ __device__ __forceinline__ float col_sum(float v) {
     v = v + dpp_f<kDppRor4>(v);
   } else if constexpr (N == 8) {
     v = v + dpp_f<kDppRor8>(v);
-    v = v + __shfl_xor(v, 16, 64);
-    v = v + __shfl_xor(v, 32, 64);
+    v = v + xor_lane16(v);
+    v = v + xor_lane32(v);
   }
   return v;
 }
@@ -263,6 +286,28 @@ __device__ __forceinline__ float sinkhorn_lane(float v, int iters, float eps) {
     v = v * __builtin_amdgcn_rcpf(col_sum<N>(v) + eps);
   }
   return v;
+}
+
+// K independent matrices per lane (one element of each), iterated together so
+// the K dependent chains interleave; per value the same operations in the same
+// order as sinkhorn_lane<N>.
+template <int N, int K>
+__device__ __forceinline__ void sinkhorn_lanes(float (&v)[K], int iters, float eps) {
+#pragma unroll
+  for (int k = 0; k < K; ++k) {
+    const float mx = row_reduce<N, OpMax>(v[k]);
+    const float e = expf(v[k] - mx);
+    const float s = row_reduce<N, OpAdd>(e);
+    v[k] = e * __builtin_amdgcn_rcpf(s) + eps;
+  }
+#pragma unroll
+  for (int k = 0; k < K; ++k) v[k] = v[k] * __builtin_amdgcn_rcpf(col_sum<N>(v[k]) + eps);
+  for (int it = 1; it < iters; ++it) {
+#pragma unroll
+    for (int k = 0; k < K; ++k) v[k] = v[k] * __builtin_amdgcn_rcpf(row_reduce<N, OpAdd>(v[k]) + eps);
+#pragma unroll
+    for (int k = 0; k < K; ++k) v[k] = v[k] * __builtin_amdgcn_rcpf(col_sum<N>(v[k]) + eps);
+  }
 }
 
 }  // namespace mhc

@@ -7,7 +7,7 @@
 // are fp32; the gates and the pre-aggregate round where the reference's torch
 // ops round (model/mhc_fused.py:843-859, model/mhc_fused_no_hres.py:364-386,
 // model/mhc_common.py:298-308).
-#include "mhc_pre_persist.hpp"
+#include "mhc_pre_kstream.hpp"
 
 namespace mhc {
 
@@ -89,6 +89,8 @@ hipError_t launch_pre_mfma(const PreArgs& a, hipStream_t s) {
       default: break;
     }
   }
+  // n = 8: phi (983 KB at C = 768) streams from L2 through a K-split MFMA loop.
+  if (a.n == 8) return launch_pre_kstream_n8(a, s);
   const int kb = pre_mfma_kb_needed(a.n, a.C);
   switch (a.n) {
     case 1: return launch_pre_mfma_n1(a, kb, s);

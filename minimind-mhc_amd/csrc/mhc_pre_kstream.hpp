@@ -1,0 +1,262 @@
+// Fused mHC pre phase for wide projections (n = 8): K-streamed MFMA.
+//
+// At n = 8, C = 768 the projection phi is [6144, 80] bf16 = 983 KB: it fits
+// neither in a workgroup's registers and LDS (as it does at n = 4) nor does a
+// 16-token x tile (192 KB) fit in registers next to it.  So phi streams from
+// L2 and its cost is spread over a 32-token tile:
+//   * one 8-wave workgroup per 32-token tile; wave w owns every 8th 32-column
+//     chunk of the n*C row (K split 8 ways) for both 16-token M-blocks, so
+//     each phi chunk is read once per tile and feeds two MFMAs;
+//   * the K loop keeps D chunks in flight per wave: each chunk is two 16-byte
+//     x loads (16 tokens x 32 columns per M-block, the MFMA A operands) and
+//     NT 16-byte phi loads (the packed B operands, 16 output columns each);
+//     v_mfma_f32_16x16x32_bf16 accumulates, bf16 dot2 forms the sum of
+//     squares;
+//   * the eight K-split partials meet in LDS; inv_rms, the gates and the
+//     Sinkhorn-Knopp iterations (four tokens per lane, interleaved) run from
+//     LDS;
+//   * the pre-aggregate re-reads the tile's x (192 KB, still in L2 / the
+//     Infinity Cache from the K loop) one 16-byte column chunk at a time.
+// Arithmetic and rounding points as pre_persist_kernel.
+//
+// Reference semantics: model/mhc_fused.py:163-268, :533-559, :47-56;
+// model/mhc_fused_no_hres.py:48-145; model/mhc_common.py:128-195.
+#pragma once
+
+#include "mhc_pre_persist.hpp"
+
+namespace mhc {
+
+constexpr int kKsWaves = 8;
+
+template <int N, int MODE>
+struct KsPlan {
+  using S = PreShape<N, MODE>;
+  static constexpr int FD = S::FD;
+  static constexpr int NT = S::NT;
+  static constexpr int G = N * N;
+  static constexpr int WAVES = kKsWaves;
+  static constexpr int MB = 2;             // 16-token M-blocks per tile (every wave)
+  static constexpr int TM = 16 * MB;       // tokens per tile
+  static constexpr int KS = WAVES;         // K split
+  static constexpr int D = 5;              // chunks in flight per wave
+  static constexpr int SKV = TM * G / (WAVES * 64);  // Sinkhorn values per lane
+  static_assert(MODE != kFull || SKV * WAVES * 64 == TM * G, "Sinkhorn covers the tile exactly");
+};
+
+template <int N, int MODE>
+struct KsShared {
+  using P = KsPlan<N, MODE>;
+  float prm[GateParams<N>::kCount];
+  float acc[P::KS][P::TM][P::FD];
+  float ss[P::KS][P::TM];
+  float inv[P::TM];
+  float hpre[P::TM][N];
+  float hres[MODE == kFull ? P::TM * P::G : 1];
+};
+
+template <int N, int MODE>
+__global__ __launch_bounds__(kKsWaves * 64) void pre_kstream_kernel(PreArgs a) {
+  using P = KsPlan<N, MODE>;
+  using GP = GateParams<N>;
+  constexpr int FD = P::FD;
+  constexpr int NT = P::NT;
+  constexpr int TM = P::TM;
+  constexpr int D = P::D;
+  constexpr int T = P::WAVES * 64;
+  __shared__ KsShared<N, MODE> sh;
+
+  const int tid = threadIdx.x;
+  const int lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int r = lane & 15;
+  const int g = lane >> 4;
+  const int kq = wave;
+  const int C = a.C;
+  const int NC = N * C;
+  const int NCB = (C + kCBlock - 1) / kCBlock;
+  const int NCH = N * NCB;                      // 32-column chunks in a row
+  const int NJ = (NCH + P::KS - 1) / P::KS;     // chunks per wave (last ones may be empty)
+  const int64_t M = a.M;
+  const int64_t t0 = (int64_t)blockIdx.x * TM;
+  const int valid = (int)(M - t0 < TM ? M - t0 : TM);
+
+  const RawParam rp = load_gate_param<N, MODE>(a, tid);
+
+  // ---- K loop -----------------------------------------------------------
+  const auto rx = make_rsrc(static_cast<const uint16_t*>(a.x) + t0 * NC, (uint32_t)valid * NC * 2u);
+  const auto rw = make_rsrc(a.phi_packed, (uint32_t)(NCH * NT) * 1024u);
+  const uint32_t xrow = (uint32_t)(r * NC) * 2u + (uint32_t)g * 16u;
+  const uint32_t xblk = (uint32_t)(16 * NC) * 2u;  // offset of M-block 1
+  U32x4 xs[D][P::MB];
+  U32x4 ws[D][NT];
+  // Workgroups walk their chunks in rotated orders, so the CUs of an XCD do
+  // not all read the same few phi lines from the same L2 channels at once.
+  const int rot = (int)(blockIdx.x % (unsigned)NJ);
+  auto issue = [&](int slot_j, U32x4 (&xd)[P::MB], U32x4 (&wd)[NT]) {
+    const int jr = slot_j < NJ ? (slot_j + rot < NJ ? slot_j + rot : slot_j + rot - NJ) : slot_j;
+    const int k = kq + P::KS * jr;              // uniform
+    const bool live = slot_j < NJ && k < NCH;
+    const int i = live ? k / NCB : 0;
+    const int cb = live ? k - i * NCB : 0;
+    const int c0 = cb * kCBlock;
+    const bool xl = live && c0 + g * 8 < C;
+#pragma unroll
+    for (int m = 0; m < P::MB; ++m)
+      xd[m] = __builtin_bit_cast(U32x4, __builtin_amdgcn_raw_buffer_load_b128(
+                                            rx, (int)(xl ? xrow + m * xblk : kBufOob), (i * C + c0) * 2, 0));
+    const uint32_t wo = live ? (uint32_t)lane * 16u : kBufOob;
+#pragma unroll
+    for (int nt = 0; nt < NT; ++nt)
+      wd[nt] = __builtin_bit_cast(
+          U32x4, __builtin_amdgcn_raw_buffer_load_b128(rw, (int)wo, (k * NT + nt) * 1024, 0));
+  };
+#pragma unroll
+  for (int d = 0; d < D; ++d) issue(d, xs[d], ws[d]);
+
+  f32x4_t acc[P::MB][NT];
+  float ss[P::MB];
+#pragma unroll
+  for (int m = 0; m < P::MB; ++m) {
+    ss[m] = 0.f;
+#pragma unroll
+    for (int nt = 0; nt < NT; ++nt) acc[m][nt] = f32x4_t{0.f, 0.f, 0.f, 0.f};
+  }
+  for (int j0 = 0; j0 < NJ; j0 += D) {   // uniform trip count
+#pragma unroll
+    for (int d = 0; d < D; ++d) {
+#pragma unroll
+      for (int m = 0; m < P::MB; ++m) {
+        const U32x4 v = xs[d][m];
+#pragma unroll
+        for (int q = 0; q < 4; ++q) ss[m] = dot2_bf16(v.v[q], v.v[q], ss[m]);
+        const bf16x8_t av = __builtin_bit_cast(bf16x8_t, v);
+#pragma unroll
+        for (int nt = 0; nt < NT; ++nt)
+          acc[m][nt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(
+              av, __builtin_bit_cast(bf16x8_t, ws[d][nt]), acc[m][nt], 0, 0, 0);
+      }
+      issue(j0 + d + D, xs[d], ws[d]);
+    }
+  }
+  // MFMA 16x16 result layout: lane l holds D[4*(l/16) + j][l % 16], j = 0..3.
+#pragma unroll
+  for (int m = 0; m < P::MB; ++m) {
+    ss[m] += __shfl_xor(ss[m], 16, 64);
+    ss[m] += __shfl_xor(ss[m], 32, 64);
+#pragma unroll
+    for (int nt = 0; nt < NT; ++nt)
+      if (nt * 16 + r < FD)
+#pragma unroll
+        for (int j = 0; j < 4; ++j) sh.acc[kq][m * 16 + 4 * g + j][nt * 16 + r] = acc[m][nt][j];
+    if (g == 0) sh.ss[kq][m * 16 + r] = ss[m];
+  }
+  if (tid < GP::kCount) sh.prm[tid] = convert_param(rp, a.param_dtype);
+  __syncthreads();
+
+  // ---- inv_rms, gates ----------------------------------------------------
+  if (tid < TM) {
+    float sq = 0.f;
+#pragma unroll
+    for (int w = 0; w < P::KS; ++w) sq += sh.ss[w][tid];
+    const float inv = 1.0f / sqrtf(sq / (float)NC + a.rms_eps);
+    sh.inv[tid] = inv;
+    if (a.inv_rms && tid < valid) a.inv_rms[t0 + tid] = inv;
+  }
+  __syncthreads();
+  for (int idx = tid; idx < TM * FD; idx += T) {
+    const int tt = idx / FD;
+    const int f = idx - tt * FD;
+    float sum = 0.f;
+#pragma unroll
+    for (int w = 0; w < P::KS; ++w) sum += sh.acc[w][tt][f];
+    const float m = sum * sh.inv[tt];
+    const int64_t tk = t0 + tt;
+    const bool ok = tt < valid;
+    if (ok && a.mixes_raw) a.mixes_raw[tk * FD + f] = m;
+    if (f < N) {
+      const float h = gate_pre(m, sh.prm[0], sh.prm[GP::kBiasPre + f], a.pre_eps, kBF16);
+      sh.hpre[tt][f] = h;
+      if (ok && a.h_pre) st_any(a.h_pre, tk * N + f, kBF16, h);
+    } else if (f < 2 * N) {
+      const float h = gate_post(m, sh.prm[1], sh.prm[GP::kBiasPost + f - N], a.post_mult, kBF16);
+      if (ok) st_any(a.h_post, tk * N + (f - N), kBF16, h);
+    } else {
+      const int e = f - 2 * N;
+      const float h = gate_res(m, sh.prm[2], sh.prm[GP::kBiasRes + e], kBF16);
+      if constexpr (MODE == kFull) sh.hres[tt * P::G + e] = h;
+      if (ok && a.h_res_raw) st_any(a.h_res_raw, tk * P::G + e, kBF16, h);
+    }
+  }
+  __syncthreads();
+
+  // ---- Sinkhorn-Knopp: SKV matrices per lane -------------------------------
+  if constexpr (MODE == kFull) {
+    if (a.h_res) {
+      float v[P::SKV];
+      int e0[P::SKV];
+#pragma unroll
+      for (int k = 0; k < P::SKV; ++k) {
+        e0[k] = (wave * P::SKV + k) * 64 + lane;  // element index inside the tile
+        v[k] = sh.hres[e0[k]];
+      }
+      sinkhorn_lanes<N, P::SKV>(v, a.sk_iters, a.sk_eps);
+#pragma unroll
+      for (int k = 0; k < P::SKV; ++k)
+        if (e0[k] / P::G < valid) st_any(a.h_res, t0 * P::G + e0[k], kBF16, v[k]);
+    }
+  }
+
+  // ---- pre-aggregate: one 16-byte column chunk of one token per step -------
+  // PB (token, chunk) pairs per round, all their loads issued before any is
+  // used, so each round pays one L2 / Infinity Cache latency.
+  constexpr int PB = 3;
+  const int C8 = C / 8;
+  const auto rsub = make_rsrc(static_cast<uint16_t*>(a.sub_in) + t0 * C, (uint32_t)valid * C * 2u);
+  for (int p0 = tid; p0 < TM * C8; p0 += PB * T) {
+    U32x4 xv[PB][N];
+    int tts[PB];
+    int cs[PB];
+#pragma unroll
+    for (int b = 0; b < PB; ++b) {
+      const int p = p0 + b * T;
+      const int tt = p < TM * C8 ? p / C8 : TM;
+      tts[b] = tt;
+      cs[b] = tt < TM ? (p - tt * C8) * 8 : 0;
+      const uint32_t xo = tt < valid ? (uint32_t)(tt * NC + cs[b]) * 2u : kBufOob;
+#pragma unroll
+      for (int i = 0; i < N; ++i)
+        xv[b][i] = __builtin_bit_cast(U32x4,
+                                      __builtin_amdgcn_raw_buffer_load_b128(rx, (int)xo, i * C * 2, 0));
+    }
+#pragma unroll
+    for (int b = 0; b < PB; ++b) {
+      const int tt = tts[b] < TM ? tts[b] : 0;
+      uint32_t hlo[N];
+      uint32_t hhi[N];
+#pragma unroll
+      for (int i = 0; i < N; ++i) {
+        hlo[i] = pack_lo(sh.hpre[tt][i]);
+        hhi[i] = pack_hi(sh.hpre[tt][i]);
+      }
+      const U32x4 pk = preagg_chunk<N>(xv[b], hlo, hhi);
+      // whole offset in the vector offset, scalar offset the literal 0 (see
+      // persist_preagg: a 128-bit store reads its data registers after issue)
+      buf_store16(rsub, tts[b] < valid ? (uint32_t)(tts[b] * C + cs[b]) * 2u : kBufOob, pk);
+    }
+  }
+}
+
+template <int N, int MODE>
+hipError_t launch_pre_kstream_inst(const PreArgs& a, hipStream_t s) {
+  constexpr int TM = KsPlan<N, MODE>::TM;
+  const int64_t tiles = (a.M + TM - 1) / TM;
+  hipLaunchKernelGGL((pre_kstream_kernel<N, MODE>), dim3((unsigned)tiles),
+                     dim3(KsPlan<N, MODE>::WAVES * 64), 0, s, a);
+  return hipGetLastError();
+}
+
+// n = 8 instances (mhc_pre_kstream_n8.hip).
+hipError_t launch_pre_kstream_n8(const PreArgs& a, hipStream_t s);
+
+}  // namespace mhc
