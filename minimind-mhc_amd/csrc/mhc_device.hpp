@@ -288,26 +288,59 @@ __device__ __forceinline__ float sinkhorn_lane(float v, int iters, float eps) {
   return v;
 }
 
-// K independent matrices per lane (one element of each), iterated together so
-// the K dependent chains interleave; per value the same operations in the same
-// order as sinkhorn_lane<N>.
-template <int N, int K>
-__device__ __forceinline__ void sinkhorn_lanes(float (&v)[K], int iters, float eps) {
+// ------------------------------------------ 8 x 8 Sinkhorn, half a row per lane
+// One matrix per 16 lanes: lane j of the group holds row (j & 7), columns
+// 4 * (j >> 3) .. + 3 in v[0..3].  A row sum is three in-lane adds and one DPP
+// add with the lane 8 away (the row's other half; the sum is commutative, so
+// both halves get the bit-identical value).  A column sum is the 8-lane
+// butterfly of row_reduce over the lanes of one half (rows 0..7).  Lane j
+// forms the reciprocal of only column (j & 3) of its half (its quad position)
+// and quad_perm broadcasts hand each lane the four it needs, so a column
+// step costs one v_rcp per lane instead of four.  The schedule and the
+// (sum + eps) divisors are those of sinkhorn_lane<8>; only the order of the
+// fp32 additions inside a sum differs.
+
+__device__ __forceinline__ float sk8_row_sum(const float (&v)[4]) {
+  const float s = (v[0] + v[1]) + (v[2] + v[3]);
+  return s + dpp_f<kDppRor8>(s);
+}
+
+__device__ __forceinline__ void sk8_row_norm(float (&v)[4], float eps) {
+  const float r = __builtin_amdgcn_rcpf(sk8_row_sum(v) + eps);
 #pragma unroll
-  for (int k = 0; k < K; ++k) {
-    const float mx = row_reduce<N, OpMax>(v[k]);
-    const float e = expf(v[k] - mx);
-    const float s = row_reduce<N, OpAdd>(e);
-    v[k] = e * __builtin_amdgcn_rcpf(s) + eps;
-  }
+  for (int q = 0; q < 4; ++q) v[q] = v[q] * r;
+}
+
+__device__ __forceinline__ void sk8_col_norm(float (&v)[4], float eps) {
+  float c[4];
 #pragma unroll
-  for (int k = 0; k < K; ++k) v[k] = v[k] * __builtin_amdgcn_rcpf(col_sum<N>(v[k]) + eps);
-  for (int it = 1; it < iters; ++it) {
+  for (int q = 0; q < 4; ++q) c[q] = row_reduce<8, OpAdd>(v[q]);
+  const int l = __lane_id();
+  const float lo = (l & 1) ? c[1] : c[0];
+  const float hi = (l & 1) ? c[3] : c[2];
+  const float r = __builtin_amdgcn_rcpf(((l & 2) ? hi : lo) + eps);
+  v[0] = v[0] * dpp_f<0x00>(r);  // quad_perm [0,0,0,0]
+  v[1] = v[1] * dpp_f<0x55>(r);  // quad_perm [1,1,1,1]
+  v[2] = v[2] * dpp_f<0xAA>(r);  // quad_perm [2,2,2,2]
+  v[3] = v[3] * dpp_f<0xFF>(r);  // quad_perm [3,3,3,3]
+}
+
+// Softmax over each row, + eps, then the first column normalisation.
+__device__ __forceinline__ void sk8_start(float (&v)[4], float eps) {
+  float mx = fmaxf(fmaxf(v[0], v[1]), fmaxf(v[2], v[3]));
+  mx = fmaxf(mx, dpp_f<kDppRor8>(mx));
 #pragma unroll
-    for (int k = 0; k < K; ++k) v[k] = v[k] * __builtin_amdgcn_rcpf(row_reduce<N, OpAdd>(v[k]) + eps);
+  for (int q = 0; q < 4; ++q) v[q] = expf(v[q] - mx);
+  const float r = __builtin_amdgcn_rcpf(sk8_row_sum(v));
 #pragma unroll
-    for (int k = 0; k < K; ++k) v[k] = v[k] * __builtin_amdgcn_rcpf(col_sum<N>(v[k]) + eps);
-  }
+  for (int q = 0; q < 4; ++q) v[q] = v[q] * r + eps;
+  sk8_col_norm(v, eps);
+}
+
+// One of the remaining (iters - 1) row + column normalisations.
+__device__ __forceinline__ void sk8_iter(float (&v)[4], float eps) {
+  sk8_row_norm(v, eps);
+  sk8_col_norm(v, eps);
 }
 
 }  // namespace mhc

@@ -12,11 +12,17 @@
 //     NT 16-byte phi loads (the packed B operands, 16 output columns each);
 //     v_mfma_f32_16x16x32_bf16 accumulates, bf16 dot2 forms the sum of
 //     squares;
-//   * the eight K-split partials meet in LDS; inv_rms, the gates and the
-//     Sinkhorn-Knopp iterations (four tokens per lane, interleaved) run from
-//     LDS;
-//   * the pre-aggregate re-reads the tile's x (192 KB, still in L2 / the
-//     Infinity Cache from the K loop) one 16-byte column chunk at a time.
+//   * the eight K-split partials meet in LDS.  The pre-aggregate's re-reads
+//     of the tile's x (393 KB, from the Infinity Cache: it has left L2 by
+//     then) need no result of the projection, so its first two rounds go out
+//     before the partials are summed;
+//   * 16 lanes per token then form inv_rms and the gates straight from the
+//     partials: lane j takes mix j (h_pre for j < 8, h_post for 8 <= j < 16)
+//     and the four h_res logits of row (j & 7), columns 4 * (j >> 3) .. + 3,
+//     which is the layout the Sinkhorn iterations (sk8_*) run in, so h_res
+//     never passes through LDS;
+//   * the Sinkhorn iterations are spread between the pre-aggregate rounds:
+//     VALU work while the next round's loads are in flight.
 // Arithmetic and rounding points as pre_persist_kernel.
 //
 // Reference semantics: model/mhc_fused.py:163-268, :533-559, :47-56;
@@ -26,6 +32,10 @@
 #include "mhc_pre_persist.hpp"
 
 namespace mhc {
+
+#ifndef KS_PB
+#define KS_PB 2
+#endif
 
 constexpr int kKsWaves = 8;
 
@@ -40,19 +50,18 @@ struct KsPlan {
   static constexpr int TM = 16 * MB;       // tokens per tile
   static constexpr int KS = WAVES;         // K split
   static constexpr int D = 5;              // chunks in flight per wave
-  static constexpr int SKV = TM * G / (WAVES * 64);  // Sinkhorn values per lane
-  static_assert(MODE != kFull || SKV * WAVES * 64 == TM * G, "Sinkhorn covers the tile exactly");
+  static constexpr int PB = KS_PB;         // pre-aggregate items per lane per round
+  static_assert(N == 8, "16 lanes per token: mixes 0..2N-1 and half an 8 x 8 row each");
+  static_assert(TM == WAVES * 4, "four tokens per wave");
 };
 
 template <int N, int MODE>
 struct KsShared {
   using P = KsPlan<N, MODE>;
-  float prm[GateParams<N>::kCount];
-  float acc[P::KS][P::TM][P::FD];
+  alignas(16) float acc[P::KS][P::TM][P::FD];  // 16-byte reads of four h_res logits
   float ss[P::KS][P::TM];
-  float inv[P::TM];
+  float prm[GateParams<N>::kCount];
   float hpre[P::TM][N];
-  float hres[MODE == kFull ? P::TM * P::G : 1];
 };
 
 template <int N, int MODE>
@@ -152,98 +161,132 @@ __global__ __launch_bounds__(kKsWaves * 64) void pre_kstream_kernel(PreArgs a) {
     if (g == 0) sh.ss[kq][m * 16 + r] = ss[m];
   }
   if (tid < GP::kCount) sh.prm[tid] = convert_param(rp, a.param_dtype);
-  __syncthreads();
 
-  // ---- inv_rms, gates ----------------------------------------------------
-  if (tid < TM) {
-    float sq = 0.f;
-#pragma unroll
-    for (int w = 0; w < P::KS; ++w) sq += sh.ss[w][tid];
-    const float inv = 1.0f / sqrtf(sq / (float)NC + a.rms_eps);
-    sh.inv[tid] = inv;
-    if (a.inv_rms && tid < valid) a.inv_rms[t0 + tid] = inv;
-  }
-  __syncthreads();
-  for (int idx = tid; idx < TM * FD; idx += T) {
-    const int tt = idx / FD;
-    const int f = idx - tt * FD;
-    float sum = 0.f;
-#pragma unroll
-    for (int w = 0; w < P::KS; ++w) sum += sh.acc[w][tt][f];
-    const float m = sum * sh.inv[tt];
-    const int64_t tk = t0 + tt;
-    const bool ok = tt < valid;
-    if (ok && a.mixes_raw) a.mixes_raw[tk * FD + f] = m;
-    if (f < N) {
-      const float h = gate_pre(m, sh.prm[0], sh.prm[GP::kBiasPre + f], a.pre_eps, kBF16);
-      sh.hpre[tt][f] = h;
-      if (ok && a.h_pre) st_any(a.h_pre, tk * N + f, kBF16, h);
-    } else if (f < 2 * N) {
-      const float h = gate_post(m, sh.prm[1], sh.prm[GP::kBiasPost + f - N], a.post_mult, kBF16);
-      if (ok) st_any(a.h_post, tk * N + (f - N), kBF16, h);
-    } else {
-      const int e = f - 2 * N;
-      const float h = gate_res(m, sh.prm[2], sh.prm[GP::kBiasRes + e], kBF16);
-      if constexpr (MODE == kFull) sh.hres[tt * P::G + e] = h;
-      if (ok && a.h_res_raw) st_any(a.h_res_raw, tk * P::G + e, kBF16, h);
-    }
-  }
-  __syncthreads();
-
-  // ---- Sinkhorn-Knopp: SKV matrices per lane -------------------------------
-  if constexpr (MODE == kFull) {
-    if (a.h_res) {
-      float v[P::SKV];
-      int e0[P::SKV];
-#pragma unroll
-      for (int k = 0; k < P::SKV; ++k) {
-        e0[k] = (wave * P::SKV + k) * 64 + lane;  // element index inside the tile
-        v[k] = sh.hres[e0[k]];
-      }
-      sinkhorn_lanes<N, P::SKV>(v, a.sk_iters, a.sk_eps);
-#pragma unroll
-      for (int k = 0; k < P::SKV; ++k)
-        if (e0[k] / P::G < valid) st_any(a.h_res, t0 * P::G + e0[k], kBF16, v[k]);
-    }
-  }
-
-  // ---- pre-aggregate: one 16-byte column chunk of one token per step -------
-  // PB (token, chunk) pairs per round, all their loads issued before any is
-  // used, so each round pays one L2 / Infinity Cache latency.
-  constexpr int PB = 3;
+  // ---- pre-aggregate rounds --------------------------------------------------
+  // Items are (token, 16-byte column chunk) pairs, PB per lane per round, in
+  // two register buffers: rounds 0 and 1 are issued here, round r + 2 as soon
+  // as round r is consumed.  A round past the end reads nothing (offsets out
+  // of the descriptor) and stores nothing.
+  constexpr int PB = P::PB;
   const int C8 = C / 8;
+  const int items = TM * C8;
+  const int nrounds = (items + PB * T - 1) / (PB * T);
   const auto rsub = make_rsrc(static_cast<uint16_t*>(a.sub_in) + t0 * C, (uint32_t)valid * C * 2u);
-  for (int p0 = tid; p0 < TM * C8; p0 += PB * T) {
-    U32x4 xv[PB][N];
-    int tts[PB];
-    int cs[PB];
+  auto pa_item = [&](int round, int b, int& tt, int& c) {
+    const int p = (round * PB + b) * T + tid;
+    tt = p < items ? p / C8 : TM;
+    c = tt < TM ? (p - tt * C8) * 8 : 0;
+  };
+  auto pa_issue = [&](int round, U32x4 (&xv)[PB][N]) {
 #pragma unroll
     for (int b = 0; b < PB; ++b) {
-      const int p = p0 + b * T;
-      const int tt = p < TM * C8 ? p / C8 : TM;
-      tts[b] = tt;
-      cs[b] = tt < TM ? (p - tt * C8) * 8 : 0;
-      const uint32_t xo = tt < valid ? (uint32_t)(tt * NC + cs[b]) * 2u : kBufOob;
+      int tt, c;
+      pa_item(round, b, tt, c);
+      const uint32_t xo = tt < valid ? (uint32_t)(tt * NC + c) * 2u : kBufOob;
 #pragma unroll
       for (int i = 0; i < N; ++i)
         xv[b][i] = __builtin_bit_cast(U32x4,
                                       __builtin_amdgcn_raw_buffer_load_b128(rx, (int)xo, i * C * 2, 0));
     }
+  };
+  auto pa_finish = [&](int round, const U32x4 (&xv)[PB][N]) {
 #pragma unroll
     for (int b = 0; b < PB; ++b) {
-      const int tt = tts[b] < TM ? tts[b] : 0;
+      int tt, c;
+      pa_item(round, b, tt, c);
+      const int ts = tt < TM ? tt : 0;
       uint32_t hlo[N];
       uint32_t hhi[N];
 #pragma unroll
       for (int i = 0; i < N; ++i) {
-        hlo[i] = pack_lo(sh.hpre[tt][i]);
-        hhi[i] = pack_hi(sh.hpre[tt][i]);
+        hlo[i] = pack_lo(sh.hpre[ts][i]);
+        hhi[i] = pack_hi(sh.hpre[ts][i]);
       }
       const U32x4 pk = preagg_chunk<N>(xv[b], hlo, hhi);
       // whole offset in the vector offset, scalar offset the literal 0 (see
       // persist_preagg: a 128-bit store reads its data registers after issue)
-      buf_store16(rsub, tts[b] < valid ? (uint32_t)(tts[b] * C + cs[b]) * 2u : kBufOob, pk);
+      buf_store16(rsub, tt < valid ? (uint32_t)(tt * C + c) * 2u : kBufOob, pk);
     }
+  };
+  U32x4 xa[PB][N];
+  U32x4 xb[PB][N];
+  pa_issue(0, xa);
+  pa_issue(1, xb);
+  __syncthreads();  // partials and gate parameters visible
+
+  // ---- inv_rms and gates: 16 lanes per token ----------------------------------
+  const int tt = wave * 4 + (lane >> 4);
+  const int jl = lane & 15;
+  const int64_t tk = t0 + tt;
+  const bool ok = tt < valid;
+  float sq = 0.f;
+#pragma unroll
+  for (int w = 0; w < P::KS; ++w) sq += sh.ss[w][tt];
+  const float inv = 1.0f / sqrtf(sq / (float)NC + a.rms_eps);
+  if (jl == 0 && ok && a.inv_rms) a.inv_rms[tk] = inv;
+  constexpr int NMIX = FD < 2 * N ? FD : 2 * N;  // pre (and post) mixes
+  if (jl < NMIX) {
+    float sum = 0.f;
+#pragma unroll
+    for (int w = 0; w < P::KS; ++w) sum += sh.acc[w][tt][jl];
+    const float m = sum * inv;
+    if (ok && a.mixes_raw) a.mixes_raw[tk * FD + jl] = m;
+    // bias_pre[j] and bias_post[j - N] are adjacent: GP::kBiasPre + j for both
+    const bool pre = jl < N;
+    const float gs = gate_sigmoid(m, sh.prm[pre ? 0 : 1], sh.prm[GP::kBiasPre + jl], kBF16);
+    const float h = pre ? round_to(__fadd_rn(gs, a.pre_eps), kBF16)   // gate_pre
+                        : round_to(__fmul_rn(gs, a.post_mult), kBF16);  // gate_post
+    if (pre) {
+      sh.hpre[tt][jl] = h;
+      if (ok && a.h_pre) st_any(a.h_pre, tk * N + jl, kBF16, h);
+    } else if (ok) {
+      st_any(a.h_post, tk * N + (jl - N), kBF16, h);
+    }
+  }
+  float v[4] = {0.f, 0.f, 0.f, 0.f};
+  const int e0 = (jl & 7) * N + 4 * (jl >> 3);  // first of this lane's h_res entries
+  if constexpr (MODE == kFull) {
+    float s4[4] = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+    for (int w = 0; w < P::KS; ++w) {
+      const float4 pw = *reinterpret_cast<const float4*>(&sh.acc[w][tt][2 * N + e0]);
+      s4[0] += pw.x;
+      s4[1] += pw.y;
+      s4[2] += pw.z;
+      s4[3] += pw.w;
+    }
+#pragma unroll
+    for (int q = 0; q < 4; ++q) {
+      const float m = s4[q] * inv;
+      if (ok && a.mixes_raw) a.mixes_raw[tk * FD + 2 * N + e0 + q] = m;
+      v[q] = gate_res(m, sh.prm[2], sh.prm[GP::kBiasRes + e0 + q], kBF16);
+      if (ok && a.h_res_raw) st_any(a.h_res_raw, tk * P::G + e0 + q, kBF16, v[q]);
+    }
+  }
+  __syncthreads();  // h_pre visible to every lane's pre-aggregate items
+
+  // ---- Sinkhorn iterations between the pre-aggregate rounds ------------------
+  const bool sk = MODE == kFull && a.h_res != nullptr;
+  const int slots = (nrounds + 1) & ~1;  // rounds run in pairs
+  const int sk_rest = a.sk_iters > 1 ? a.sk_iters - 1 : 0;
+  int sk_done = 0;
+  if (sk) sk8_start(v, a.sk_eps);
+  auto sk_share = [&](int slot) {  // iterations due before slot's round is consumed
+    if (!sk) return;
+    const int target = (sk_rest * (slot + 1) + slots - 1) / slots;
+    for (; sk_done < target; ++sk_done) sk8_iter(v, a.sk_eps);
+  };
+  for (int rd = 0; rd < nrounds; rd += 2) {  // uniform trip count, no exit between steps
+    sk_share(rd);
+    pa_finish(rd, xa);
+    pa_issue(rd + 2, xa);
+    sk_share(rd + 1);
+    pa_finish(rd + 1, xb);
+    pa_issue(rd + 3, xb);
+  }
+  if (sk && ok) {
+#pragma unroll
+    for (int q = 0; q < 4; ++q) st_any(a.h_res, tk * P::G + e0 + q, kBF16, v[q]);
   }
 }
 

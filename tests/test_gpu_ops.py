@@ -73,7 +73,8 @@ def test_pre_mfma_matches_generic(dev, n, C):
         assert maxrel(b[k], a[k]) <= 1e-2, k
 
 
-@pytest.mark.parametrize("n,C,M", [(4, 768, 4096), (2, 512, 4096), (4, 768, 20000)])
+@pytest.mark.parametrize("n,C,M", [(4, 768, 4096), (2, 512, 4096), (4, 768, 20000),
+                                   (8, 768, 8192), (8, 768, 8200)])
 def test_pre_mfma_many_workgroups_repeat(dev, n, C, M):
     """Every CU busy, one or more tiles per workgroup, several launches: the
     persistent kernel's output must equal the generic kernel's within bf16
@@ -103,6 +104,18 @@ def test_pre_mfma_many_workgroups_repeat(dev, n, C, M):
 def test_pre_sinkhorn_iteration_counts(dev, iters):
     o, r, _ = _pre_case(dev, 4, 768, 32, torch.float32, True, iters, use_pack=True)
     assert maxabs(r["h_res"], o["h_res"]) <= 1e-5
+
+
+@pytest.mark.parametrize("iters", [0, 1, 2, 7, 20])
+@pytest.mark.parametrize("M", [32, 45])
+def test_pre_n8_sinkhorn_iteration_counts(dev, iters, M):
+    """n = 8, bf16: the MFMA kernel spreads the Sinkhorn iterations over its
+    pre-aggregate rounds; every count (including 0 and 1) must give the
+    reference schedule."""
+    o, r, packed = _pre_case(dev, 8, 768, M, torch.bfloat16, True, iters, use_pack=True)
+    assert packed is not None
+    assert maxabs(r["h_res"], o["h_res"]) <= 1e-2
+    assert maxrel(r["sub"], o["sub_in"]) <= 1e-2
 
 
 @pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float32])
