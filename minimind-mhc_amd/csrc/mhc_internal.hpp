@@ -70,9 +70,12 @@ hipError_t launch_stream_expand(const void* x, void* out, int elem_bytes, int64_
 hipError_t launch_phi_pack(const void* phi, int phi_dtype, void* packed, int n, int C, int mode,
                            hipStream_t s);
 
-// MFMA pre-phase geometry: 16 tokens per workgroup, c-blocks of 32 columns.
+// MFMA pre-phase geometry: 16-token tiles, c-blocks of 32 columns.
 constexpr int kTokTile = 16;
 constexpr int kCBlock = 32;
+// Widest row the MFMA kernels take: 32 column blocks (C <= 1024), i.e. at most
+// four blocks per wave of the 8-wave persistent kernel.
+constexpr int kMfmaMaxColBlocks = 32;
 
 // Packed size in bytes of phi for the MFMA path, or 0 when (n, C, mode) has no
 // MFMA instance (the generic kernel then serves the call).

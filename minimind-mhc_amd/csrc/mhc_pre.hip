@@ -41,7 +41,7 @@ int64_t mfma_packed_bytes(int n, int C, int mode) {
   if (mode != kFull && mode != kNoHres && mode != kHead) return 0;
   if (mode == kHead && n == 1) return 0;
   if (C <= 0 || C % 8 != 0) return 0;
-  if (pre_mfma_kb_needed(n, C) > pre_mfma_kb_max(n)) return 0;
+  if ((C + kCBlock - 1) / kCBlock > kMfmaMaxColBlocks) return 0;  // C <= 1024
   const int fd = mode_fd(mode, n);
   const int nt = (fd + 15) / 16;
   const int ncb = (C + kCBlock - 1) / kCBlock;
@@ -91,14 +91,7 @@ hipError_t launch_pre_mfma(const PreArgs& a, hipStream_t s) {
   }
   // n = 8: phi (983 KB at C = 768) streams from L2 through a K-split MFMA loop.
   if (a.n == 8) return launch_pre_kstream_n8(a, s);
-  const int kb = pre_mfma_kb_needed(a.n, a.C);
-  switch (a.n) {
-    case 1: return launch_pre_mfma_n1(a, kb, s);
-    case 2: return launch_pre_mfma_n2(a, kb, s);
-    case 4: return launch_pre_mfma_n4(a, kb, s);
-    case 8: return launch_pre_mfma_n8(a, kb, s);
-    default: return hipErrorInvalidValue;
-  }
+  return hipErrorInvalidValue;
 }
 
 // ------------------------------------------------------------ generic kernel

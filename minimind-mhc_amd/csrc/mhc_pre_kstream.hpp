@@ -33,10 +33,6 @@
 
 namespace mhc {
 
-#ifndef KS_PB
-#define KS_PB 2
-#endif
-
 constexpr int kKsWaves = 8;
 
 template <int N, int MODE>
@@ -49,8 +45,8 @@ struct KsPlan {
   static constexpr int MB = 2;             // 16-token M-blocks per tile (every wave)
   static constexpr int TM = 16 * MB;       // tokens per tile
   static constexpr int KS = WAVES;         // K split
-  static constexpr int D = 5;              // chunks in flight per wave
-  static constexpr int PB = KS_PB;         // pre-aggregate items per lane per round
+  static constexpr int D = 3;              // chunks in flight per wave
+  static constexpr int PB = 2;             // pre-aggregate items per lane per round (two rounds in flight)
   static_assert(N == 8, "16 lanes per token: mixes 0..2N-1 and half an 8 x 8 row each");
   static_assert(TM == WAVES * 4, "four tokens per wave");
 };

@@ -1,6 +1,19 @@
 // Persistent fused mHC pre phase on MFMA, bf16 streams (gfx950).
 //
-// Same arithmetic as pre_mfma_kernel (mhc_pre_mfma.hpp), scheduled for HBM:
+// Per token, with x read from HBM exactly once:
+//   ss        = sum_k x[k]^2                    (fp32, bf16 dot2 on the held registers)
+//   acc[f]    = sum_k x[k] * phi[k, f]          (v_mfma_f32_16x16x32_bf16, fp32 accumulate)
+//   inv_rms   = 1 / sqrt(ss / (n*C) + rms_eps)
+//   mixes[f]  = acc[f] * inv_rms                (== (x * inv_rms) @ phi)
+//   gates     h_pre = sigmoid(a_pre*m + b_pre) + pre_eps
+//             h_post = post_mult * sigmoid(a_post*m + b_post)
+//             h_res_raw = a_res*m + b_res
+//             each op rounded to bf16 as the reference's torch ops round it
+//   h_res     = Sinkhorn(h_res_raw) in fp32     (one matrix element per lane)
+//   sub_in[c] = sum_i bf16(h_pre[i] * x[i*C + c])
+// The token tile's n*C row is split over the waves by 32-column blocks, so
+// each wave holds all n streams of its columns and the pre-aggregate (a sum
+// over streams at a fixed column) is wave-local.  Scheduled for HBM:
 //   * one 8-wave workgroup per CU walks the 16-token tiles blockIdx.x,
 //     blockIdx.x + gridDim.x, ... until the tiles run out;
 //   * wave w owns the 32-column blocks cb = w, w + 8, ... of every stream;
@@ -43,9 +56,16 @@
 // :820-830; model/mhc_fused_no_hres.py:48-145; model/mhc_common.py:128-195.
 #pragma once
 
-#include "mhc_pre_mfma.hpp"
+#include "mhc_internal.hpp"
 
 namespace mhc {
+
+// Projection width per mode and its 16-wide MFMA column tiles.
+template <int N, int MODE>
+struct PreShape {
+  static constexpr int FD = MODE == kFull ? 2 * N + N * N : (MODE == kNoHres ? 2 * N : N);
+  static constexpr int NT = (FD + 15) / 16;
+};
 
 constexpr int kPersistWaves = 8;
 constexpr int kLdsBytes = 163840;  // LDS per CU on gfx950
