@@ -1,11 +1,13 @@
 /*
- * mhc_amd.h -- C ABI of the MI355X (gfx950) mHC forward kernels.
+ * mhc_amd.h -- C ABI of the MI355X (gfx950) mHC forward and backward kernels.
  *
  * Every entry point takes raw device pointers, plain sizes and a hipStream_t,
  * enqueues its kernels on that stream and returns without synchronising.
  * The caller allocates every output (as the reference's autograd Functions do
  * with torch.empty); the library never allocates or frees device memory and
- * keeps no state between calls, so calls are re-entrant and capturable.
+ * keeps no state between calls, so calls are re-entrant and capturable.  One
+ * entry point (mhc_pre_bwd_weights) needs scratch for token-range partial
+ * sums; the caller passes it as a workspace argument.
  *
  * Return value: 0 on success.  Otherwise a hipError_t code
  * (hipErrorInvalidValue = 1 for bad arguments); mhc_last_error() then returns a
@@ -39,6 +41,7 @@ extern "C" {
 #define MHC_MODE_FULL 0   /* phi [n*C, 2n+n*n]: MHCConnection_Fused        */
 #define MHC_MODE_NOHRES 1 /* phi [n*C, 2n]:     MHCConnection_FusedNoHres  */
 #define MHC_MODE_HEAD 2   /* phi [n*C, n]:      MHCHead                    */
+#define MHC_MODE_RMS 3    /* no phi:            MHCHead with n == 1 (RMSNorm), backward only */
 
 /* ABI revision (bumped on any signature change). */
 int mhc_abi_version(void);
@@ -159,6 +162,92 @@ int mhc_sinkhorn_fwd(const void* m_in, void* m_out, int dtype, int64_t batch, in
  */
 int mhc_stream_expand_fwd(const void* x, void* out, int elem_bytes, int64_t M, int n, int C,
                           hipStream_t stream);
+
+/* ------------------------------------------------------------------ backward
+ * Gradients are computed in fp32 and rounded once at the store, as the
+ * reference's Triton backward kernels do.  Incoming gradients that are NULL
+ * count as zero.
+ */
+
+/*
+ * Post-phase backward, per token:
+ *   g_x[j,:] = sum_i h_res[i,j] * g_out[i,:],  g_h_res[i,j] = g_out[i,:] . x[j,:],
+ *   g_h_post[i] = g_out[i,:] . f_out,          g_f = sum_i h_post[i] * g_out[i,:].
+ * Replaces _PostPhaseFullFn.backward  model/mhc_fused.py:747-772
+ *          (its kernel                model/mhc_fused.py:462-526).
+ *   g_out, g_x [M, n*C] x_dtype; g_h_res [M, n, n], g_h_post [M, n] h_dtype;
+ *   g_f [M, C] f_dtype.  n <= 16.
+ */
+int mhc_post_bwd(const void* x, int x_dtype, const void* h_res, const void* h_post, int h_dtype,
+                 const void* f_out, int f_dtype, const void* g_out, void* g_x, void* g_h_res,
+                 void* g_h_post, void* g_f, int64_t M, int n, int C, hipStream_t stream);
+
+/*
+ * Post-phase backward without H_res (out = x + h_post (x) f_out): g_x = g_out,
+ * so g_x may be NULL (the caller reuses g_out).
+ * Replaces _PostPhaseFn.backward  model/mhc_fused_no_hres.py:559-580
+ *          (its kernel           model/mhc_fused_no_hres.py:321-360).
+ */
+int mhc_post_nohres_bwd(const void* h_post, int h_dtype, const void* f_out, int f_dtype,
+                        const void* g_out, int x_dtype, void* g_x, void* g_h_post, void* g_f,
+                        int64_t M, int n, int C, hipStream_t stream);
+
+/*
+ * Pre-phase backward, per token, recomputed from the saved inv_rms and
+ * mixes_raw:  g_x (x_dtype) and g_raw [M, FD] fp32, the gradient of each
+ * segment's alpha * m + bias (pre and post after the sigmoid derivative,
+ * res as given).  g_raw feeds mhc_pre_bwd_weights.
+ * mode MHC_MODE_FULL / MHC_MODE_NOHRES: the mHC pre phase; g_sub = d sublayer_in,
+ *   g_h_pre, g_h_post, g_h_res_raw as named.
+ * mode MHC_MODE_HEAD: MHCHead; g_sub = d out, the other gradients NULL.
+ * mode MHC_MODE_RMS: MHCHead with n == 1 (out = x * inv_rms); g_sub = d out,
+ *   phi / alphas / biases / mixes_raw / g_raw unused (may be NULL).
+ * Replaces _PrePhaseFullFn.backward's kernel  model/mhc_fused.py:271-413, :644-695
+ *          _PrePhaseFn.backward's kernel      model/mhc_fused_no_hres.py:150-281, :466-515
+ *          _MHCHeadFn.backward's kernel       model/mhc_common.py:200-295, :360-390
+ *          the n == 1 RMSNorm head's autograd  model/mhc_common.py:438-442.
+ *   bias_post and alpha_res may be NULL where the mode has no such segment;
+ *   the four incoming gradients share grad_dtype.
+ */
+int mhc_pre_bwd(const void* x, int x_dtype, const void* phi, int phi_dtype, const void* alpha_pre,
+                const void* bias_pre, const void* alpha_post, const void* bias_post,
+                const void* alpha_res, int param_dtype, const float* inv_rms,
+                const float* mixes_raw, const void* g_sub, const void* g_h_pre,
+                const void* g_h_post, const void* g_h_res_raw, int grad_dtype, void* g_x,
+                float* g_raw, int64_t M, int n, int C, int mode, float post_mult, float pre_eps,
+                hipStream_t stream);
+
+/* Workspace bytes mhc_pre_bwd_weights needs for (M, n, C, mode). */
+int64_t mhc_pre_bwd_weights_workspace_bytes(int64_t M, int n, int C, int mode);
+
+/*
+ * Weight gradients of the pre phase from mhc_pre_bwd's g_raw:
+ *   g_phi[k, f] = alpha_seg(f) * sum_t x[t, k] * inv_rms[t] * g_raw[t, f]   (phi_dtype)
+ *   g_bias_seg  = sum_t g_raw[t, seg]                                       (param_dtype)
+ *   g_alpha_seg = sum_t sum_{f in seg} g_raw[t, f] * mixes_raw[t, f]        (param_dtype)
+ * Deterministic: token-range partial sums in the workspace, then one
+ * reduction.  Any g_alpha_* / g_bias_* may be NULL (skipped).
+ * Replaces the grad_W GEMM and alpha / bias reductions of
+ *   _PrePhaseFullFn.backward  model/mhc_fused.py:696-711
+ *   _PrePhaseFn.backward      model/mhc_fused_no_hres.py:515-525
+ *   _MHCHeadFn.backward       model/mhc_common.py:390-398.
+ */
+int mhc_pre_bwd_weights(const void* x, int x_dtype, const float* inv_rms, const float* mixes_raw,
+                        const float* g_raw, const void* alpha_pre, const void* alpha_post,
+                        const void* alpha_res, int param_dtype, void* g_phi, int phi_dtype,
+                        void* g_alpha_pre, void* g_bias_pre, void* g_alpha_post,
+                        void* g_bias_post, void* g_alpha_res, void* g_bias_res, void* workspace,
+                        int64_t workspace_bytes, int64_t M, int n, int C, int mode,
+                        hipStream_t stream);
+
+/*
+ * Sinkhorn-Knopp backward: g_in = d output / d input of mhc_sinkhorn_fwd's
+ * schedule, by recomputing the forward iterates (fp32).  n <= 16,
+ * iters <= 64.
+ * Replaces _SinkhornFn.backward  model/mhc_fused.py:131-137.
+ */
+int mhc_sinkhorn_bwd(const void* m_in, int in_dtype, const void* g_out, int g_dtype, void* g_in,
+                     int gi_dtype, int64_t batch, int n, int iters, float eps, hipStream_t stream);
 
 #ifdef __cplusplus
 }

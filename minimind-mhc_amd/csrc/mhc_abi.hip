@@ -65,7 +65,7 @@ int run_pre(mhc::PreArgs& a, hipStream_t stream, const char* fn) {
 
 extern "C" {
 
-int mhc_abi_version(void) { return 1; }
+int mhc_abi_version(void) { return 2; }
 
 const char* mhc_last_error(void) { return g_err; }
 
@@ -227,6 +227,128 @@ int mhc_stream_expand_fwd(const void* x, void* out, int elem_bytes, int64_t M, i
   if (!x || !out) return fail(hipErrorInvalidValue, "mhc_stream_expand_fwd: null pointer");
   return hip_status(mhc::launch_stream_expand(x, out, elem_bytes, M, n, C, stream),
                     "mhc_stream_expand_fwd");
+}
+
+// ------------------------------------------------------------------ backward
+
+int mhc_post_bwd(const void* x, int x_dtype, const void* h_res, const void* h_post, int h_dtype,
+                 const void* f_out, int f_dtype, const void* g_out, void* g_x, void* g_h_res,
+                 void* g_h_post, void* g_f, int64_t M, int n, int C, hipStream_t stream) {
+  const char* fn = "mhc_post_bwd";
+  if (M < 0 || n < 1 || n > kMaxN || C < 1) return fail(hipErrorInvalidValue, "%s: bad shape (M=%lld n=%d C=%d)", fn, (long long)M, n, C);
+  if (!dtype_ok(x_dtype) || !dtype_ok(h_dtype) || !dtype_ok(f_dtype)) return fail(hipErrorInvalidValue, "%s: bad dtype", fn);
+  if (M > kMaxBlocks) return fail(hipErrorInvalidValue, "%s: M too large", fn);
+  if (M == 0) return 0;
+  if (!x || !h_res || !h_post || !f_out || !g_out || !g_x || !g_h_res || !g_h_post || !g_f)
+    return fail(hipErrorInvalidValue, "%s: null pointer", fn);
+  mhc::PostBwdArgs a{x, h_res, h_post, f_out, g_out, g_x, g_h_res, g_h_post, g_f, M, n, C, x_dtype, h_dtype, f_dtype};
+  return hip_status(mhc::launch_post_bwd(a, stream), fn);
+}
+
+int mhc_post_nohres_bwd(const void* h_post, int h_dtype, const void* f_out, int f_dtype,
+                        const void* g_out, int x_dtype, void* g_x, void* g_h_post, void* g_f,
+                        int64_t M, int n, int C, hipStream_t stream) {
+  const char* fn = "mhc_post_nohres_bwd";
+  if (M < 0 || n < 1 || n > kMaxN || C < 1) return fail(hipErrorInvalidValue, "%s: bad shape", fn);
+  if (!dtype_ok(x_dtype) || !dtype_ok(h_dtype) || !dtype_ok(f_dtype)) return fail(hipErrorInvalidValue, "%s: bad dtype", fn);
+  if (M > kMaxBlocks) return fail(hipErrorInvalidValue, "%s: M too large", fn);
+  if (M == 0) return 0;
+  if (!h_post || !f_out || !g_out || !g_h_post || !g_f) return fail(hipErrorInvalidValue, "%s: null pointer", fn);
+  if (g_x == g_out) g_x = nullptr;  // identity: nothing to copy
+  mhc::PostBwdArgs a{nullptr, nullptr, h_post, f_out, g_out, g_x, nullptr, g_h_post, g_f, M, n, C, x_dtype, h_dtype, f_dtype};
+  return hip_status(mhc::launch_post_bwd(a, stream), fn);
+}
+
+int mhc_pre_bwd(const void* x, int x_dtype, const void* phi, int phi_dtype, const void* alpha_pre,
+                const void* bias_pre, const void* alpha_post, const void* bias_post,
+                const void* alpha_res, int param_dtype, const float* inv_rms,
+                const float* mixes_raw, const void* g_sub, const void* g_h_pre,
+                const void* g_h_post, const void* g_h_res_raw, int grad_dtype, void* g_x,
+                float* g_raw, int64_t M, int n, int C, int mode, float post_mult, float pre_eps,
+                hipStream_t stream) {
+  const char* fn = "mhc_pre_bwd";
+  if (M < 0 || n < 1 || n > kMaxN || C < 1) return fail(hipErrorInvalidValue, "%s: bad shape (M=%lld n=%d C=%d)", fn, (long long)M, n, C);
+  if (mode != mhc::kFull && mode != mhc::kNoHres && mode != mhc::kHead && mode != mhc::kRms)
+    return fail(hipErrorInvalidValue, "%s: bad mode %d", fn, mode);
+  if (!dtype_ok(x_dtype) || !dtype_ok(grad_dtype)) return fail(hipErrorInvalidValue, "%s: bad dtype", fn);
+  if (M > kMaxBlocks) return fail(hipErrorInvalidValue, "%s: M too large", fn);
+  if (M == 0) return 0;
+  if (!x || !inv_rms || !g_x) return fail(hipErrorInvalidValue, "%s: x, inv_rms and g_x are required", fn);
+  if (mode == mhc::kRms) {
+    if (!g_sub) return fail(hipErrorInvalidValue, "%s: g_sub (d out) is required for the RMSNorm head", fn);
+  } else {
+    if (!phi || !mixes_raw || !alpha_pre || !bias_pre) return fail(hipErrorInvalidValue, "%s: phi, mixes_raw, alpha_pre and bias_pre are required", fn);
+    if (!dtype_ok(phi_dtype) || !dtype_ok(param_dtype)) return fail(hipErrorInvalidValue, "%s: bad phi / param dtype", fn);
+    if (mode != mhc::kHead && (!alpha_post || !bias_post)) return fail(hipErrorInvalidValue, "%s: alpha_post and bias_post are required", fn);
+    if (mode == mhc::kFull && !alpha_res) return fail(hipErrorInvalidValue, "%s: alpha_res is required", fn);
+    if (mode == mhc::kHead && n == 1) return fail(hipErrorInvalidValue, "%s: MHCHead with n == 1 is mode MHC_MODE_RMS", fn);
+  }
+  mhc::PreBwdArgs a{};
+  a.x = x; a.phi = phi;
+  a.alpha[0] = alpha_pre; a.alpha[1] = alpha_post; a.alpha[2] = alpha_res;
+  a.bias[0] = bias_pre; a.bias[1] = bias_post; a.bias[2] = nullptr;
+  a.inv_rms = inv_rms; a.mixes = mixes_raw;
+  a.g_sub = g_sub; a.g_hpre = g_h_pre; a.g_hpost = g_h_post; a.g_hres = mode == mhc::kFull ? g_h_res_raw : nullptr;
+  a.g_x = g_x; a.g_raw = mode == mhc::kRms ? nullptr : g_raw;
+  a.M = M; a.n = n; a.C = C; a.mode = mode;
+  a.x_dtype = x_dtype; a.phi_dtype = phi_dtype; a.param_dtype = param_dtype; a.grad_dtype = grad_dtype;
+  a.post_mult = post_mult; a.pre_eps = pre_eps;
+  return hip_status(mhc::launch_pre_bwd(a, stream), fn);
+}
+
+int64_t mhc_pre_bwd_weights_workspace_bytes(int64_t M, int n, int C, int mode) {
+  if (M < 1 || n < 1 || n > kMaxN || C < 1) return 0;
+  if (mode != mhc::kFull && mode != mhc::kNoHres && mode != mhc::kHead) return 0;
+  return mhc::weights_workspace_bytes(M, n, C, mode);
+}
+
+int mhc_pre_bwd_weights(const void* x, int x_dtype, const float* inv_rms, const float* mixes_raw,
+                        const float* g_raw, const void* alpha_pre, const void* alpha_post,
+                        const void* alpha_res, int param_dtype, void* g_phi, int phi_dtype,
+                        void* g_alpha_pre, void* g_bias_pre, void* g_alpha_post,
+                        void* g_bias_post, void* g_alpha_res, void* g_bias_res, void* workspace,
+                        int64_t workspace_bytes, int64_t M, int n, int C, int mode,
+                        hipStream_t stream) {
+  const char* fn = "mhc_pre_bwd_weights";
+  if (M < 0 || n < 1 || n > kMaxN || C < 1) return fail(hipErrorInvalidValue, "%s: bad shape", fn);
+  if (mode != mhc::kFull && mode != mhc::kNoHres && mode != mhc::kHead) return fail(hipErrorInvalidValue, "%s: bad mode %d", fn, mode);
+  if (!dtype_ok(x_dtype) || !dtype_ok(phi_dtype) || !dtype_ok(param_dtype)) return fail(hipErrorInvalidValue, "%s: bad dtype", fn);
+  if (M > kMaxBlocks) return fail(hipErrorInvalidValue, "%s: M too large", fn);
+  if (!g_phi) return fail(hipErrorInvalidValue, "%s: g_phi is required", fn);
+  if (M == 0) return fail(hipErrorInvalidValue, "%s: M == 0 leaves the gradients undefined; zero them instead", fn);
+  if (!x || !inv_rms || !mixes_raw || !g_raw || !alpha_pre) return fail(hipErrorInvalidValue, "%s: null pointer", fn);
+  if (mode != mhc::kHead && !alpha_post) return fail(hipErrorInvalidValue, "%s: alpha_post is required", fn);
+  if (mode == mhc::kFull && !alpha_res) return fail(hipErrorInvalidValue, "%s: alpha_res is required", fn);
+  const int64_t need = mhc::weights_workspace_bytes(M, n, C, mode);
+  if (!workspace || workspace_bytes < need)
+    return fail(hipErrorInvalidValue, "%s: workspace of %lld bytes needed (got %lld)", fn, (long long)need, (long long)workspace_bytes);
+  if ((reinterpret_cast<uintptr_t>(workspace) & 3) != 0) return fail(hipErrorInvalidValue, "%s: workspace must be 4-byte aligned", fn);
+  mhc::WeightsArgs a{};
+  a.x = x; a.inv_rms = inv_rms; a.mixes = mixes_raw; a.g_raw = g_raw;
+  a.alpha[0] = alpha_pre; a.alpha[1] = alpha_post; a.alpha[2] = alpha_res;
+  a.g_phi = g_phi;
+  a.g_alpha[0] = g_alpha_pre; a.g_alpha[1] = mode == mhc::kHead ? nullptr : g_alpha_post;
+  a.g_alpha[2] = mode == mhc::kFull ? g_alpha_res : nullptr;
+  a.g_bias[0] = g_bias_pre; a.g_bias[1] = mode == mhc::kHead ? nullptr : g_bias_post;
+  a.g_bias[2] = mode == mhc::kFull ? g_bias_res : nullptr;
+  a.work = static_cast<float*>(workspace);
+  a.M = M; a.n = n; a.C = C; a.mode = mode;
+  a.x_dtype = x_dtype; a.phi_dtype = phi_dtype; a.param_dtype = param_dtype;
+  return hip_status(mhc::launch_pre_bwd_weights(a, stream), fn);
+}
+
+int mhc_sinkhorn_bwd(const void* m_in, int in_dtype, const void* g_out, int g_dtype, void* g_in,
+                     int gi_dtype, int64_t batch, int n, int iters, float eps, hipStream_t stream) {
+  const char* fn = "mhc_sinkhorn_bwd";
+  if (batch < 0) return fail(hipErrorInvalidValue, "%s: batch must be >= 0", fn);
+  if (n < 1 || n > 16) return fail(hipErrorInvalidValue, "%s: n must be in [1, 16] (got %d)", fn, n);
+  if (iters > 64) return fail(hipErrorInvalidValue, "%s: iters must be <= 64 (got %d)", fn, iters);
+  if (!dtype_ok(in_dtype) || !dtype_ok(g_dtype) || !dtype_ok(gi_dtype)) return fail(hipErrorInvalidValue, "%s: bad dtype", fn);
+  if (batch > kMaxBlocks) return fail(hipErrorInvalidValue, "%s: batch too large", fn);
+  if (batch == 0) return 0;
+  if (!m_in || !g_out || !g_in) return fail(hipErrorInvalidValue, "%s: null pointer", fn);
+  return hip_status(mhc::launch_sinkhorn_bwd(m_in, in_dtype, g_out, g_dtype, g_in, gi_dtype, batch, n,
+                                             iters, eps, stream), fn);
 }
 
 }  // extern "C"

@@ -210,6 +210,7 @@ constexpr int kDppXor2 = 0x4E;        // quad_perm [2,3,0,1]
 constexpr int kDppRor4 = 0x124;       // row_ror:4
 constexpr int kDppRor8 = 0x128;       // row_ror:8  (== lane xor 8 inside a row)
 constexpr int kDppHalfMirror = 0x141; // row_half_mirror (lane i <-> 7-i in each 8)
+constexpr int kDppRowMirror = 0x140;  // row_mirror (lane i <-> 15-i in each 16)
 
 struct OpAdd {
   __device__ static float f(float a, float b) { return a + b; }
@@ -248,6 +249,18 @@ __device__ __forceinline__ float xor_lane32(float v) {
   const auto r = __builtin_amdgcn_permlane32_swap(a, b, false, false);
   const bool upper = __lane_id() >= 32;
   return __builtin_bit_cast(float, upper ? r[0] : r[1]);
+}
+
+// Sum over all 64 lanes of the wave; every lane ends with the bit-identical
+// total (each step adds a value and its partner's, a commutative pair).
+__device__ __forceinline__ float wave_sum(float v) {
+  v = v + dpp_f<kDppXor1>(v);
+  v = v + dpp_f<kDppXor2>(v);
+  v = v + dpp_f<kDppHalfMirror>(v);
+  v = v + dpp_f<kDppRowMirror>(v);
+  v = v + xor_lane16(v);
+  v = v + xor_lane32(v);
+  return v;
 }
 
 // Reduce over the N lanes of one matrix column (stride N inside N*N lanes).

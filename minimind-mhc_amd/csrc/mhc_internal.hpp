@@ -59,10 +59,76 @@ struct PostArgs {
   int x_dtype, h_dtype, f_dtype;
 };
 
+// Post-phase backward (model/mhc_fused.py:462-526, :747-772).  g_out, g_x
+// share x_dtype; g_h_res, g_h_post the h dtype; g_f the f dtype.
+struct PostBwdArgs {
+  const void* x;       // [M, n*C]   (read only with h_res)
+  const void* h_res;   // [M, n, n] or null (identity)
+  const void* h_post;  // [M, n]
+  const void* f_out;   // [M, C]
+  const void* g_out;   // [M, n*C]
+  void* g_x;           // [M, n*C]   (may be null without h_res: then g_x == g_out)
+  void* g_h_res;       // [M, n, n]  (with h_res)
+  void* g_h_post;      // [M, n]
+  void* g_f;           // [M, C]
+  int64_t M;
+  int n, C;
+  int x_dtype, h_dtype, f_dtype;
+};
+
+// Pre-phase backward, per token (model/mhc_fused.py:271-413, :644-717;
+// model/mhc_fused_no_hres.py:150-281; model/mhc_common.py:200-295).  The
+// incoming gradients share grad_dtype; any of them may be null (zero).
+struct PreBwdArgs {
+  const void* x;          // [M, n*C]
+  const void* phi;        // [n*C, FD]
+  const void* alpha[3];   // pre, post, res (0-dim)
+  const void* bias[3];    // pre [n], post [n] (the sigmoids are recomputed); res unused
+  const float* inv_rms;   // [M]
+  const float* mixes;     // [M, FD] fp32 projection (before alpha / bias)
+  const void* g_sub;      // [M, C]   d sublayer_in (or d out for MHCHead / RMSNorm)
+  const void* g_hpre;     // [M, n]
+  const void* g_hpost;    // [M, n]
+  const void* g_hres;     // [M, n*n] d h_res_raw
+  void* g_x;              // [M, n*C]  x_dtype
+  float* g_raw;           // [M, FD]   fp32: d(alpha*m + bias) per segment (null for kRms)
+  int64_t M;
+  int n, C, mode;
+  int x_dtype, phi_dtype, param_dtype, grad_dtype;
+  float post_mult, pre_eps;
+};
+
+// Weight gradients of the pre phase from the per-token g_raw:
+//   grad_phi[k, f] = alpha_seg(f) * sum_t x[t, k] * inv_rms[t] * g_raw[t, f]
+//   grad_bias[f]   = sum_t g_raw[t, f]
+//   grad_alpha[s]  = sum_t sum_{f in s} g_raw[t, f] * mixes[t, f]
+// (model/mhc_fused.py:696-711).  Token-range partials go to the workspace.
+struct WeightsArgs {
+  const void* x;          // [M, n*C]
+  const float* inv_rms;   // [M]
+  const float* mixes;     // [M, FD]
+  const float* g_raw;     // [M, FD]
+  const void* alpha[3];
+  void* g_phi;            // [n*C, FD] phi_dtype
+  void* g_alpha[3];       // 0-dim, param_dtype (null: skipped)
+  void* g_bias[3];        // param_dtype (null: skipped)
+  float* work;            // workspace
+  int64_t M;
+  int n, C, mode;
+  int x_dtype, phi_dtype, param_dtype;
+};
+
 // Launchers: return hipSuccess or the launch error.
 hipError_t launch_pre_mfma(const PreArgs& a, hipStream_t s);   // requires mfma_supported()
 hipError_t launch_pre_generic(const PreArgs& a, hipStream_t s);
 hipError_t launch_post(const PostArgs& a, hipStream_t s);
+hipError_t launch_post_bwd(const PostBwdArgs& a, hipStream_t s);
+hipError_t launch_pre_bwd(const PreBwdArgs& a, hipStream_t s);
+int64_t weights_workspace_bytes(int64_t M, int n, int C, int mode);
+hipError_t launch_pre_bwd_weights(const WeightsArgs& a, hipStream_t s);
+hipError_t launch_sinkhorn_bwd(const void* m_in, int in_dtype, const void* g_out, int g_dtype,
+                               void* g_in, int gi_dtype, int64_t batch, int n, int iters,
+                               float eps, hipStream_t s);
 hipError_t launch_sinkhorn(const void* in, void* out, int dtype, int64_t batch, int n,
                            int iters, float eps, hipStream_t s);
 hipError_t launch_stream_expand(const void* x, void* out, int elem_bytes, int64_t M, int n,

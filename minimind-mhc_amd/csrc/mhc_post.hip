@@ -181,4 +181,213 @@ hipError_t launch_post(const PostArgs& a, hipStream_t s) {
   return hipGetLastError();
 }
 
+// ============================================================ backward
+// Per token (model/mhc_fused.py:462-526):
+//   g_x[j, c]     = sum_i h_res[i, j] * g[i, c]       (g_x = g without h_res)
+//   g_h_res[i, j] = sum_c g[i, c] * x[j, c]
+//   g_h_post[i]   = sum_c g[i, c] * F[c]
+//   g_F[c]        = sum_i h_post[i] * g[i, c]
+// fp32 arithmetic, one rounding at each store (the reference kernel's
+// tl.store casts), as one wave per token: lanes stride over the token's
+// 16-byte column chunks, then wave_sum reduces the n^2 + n dot products.
+
+template <typename XT, int N, bool RES>
+__global__ __launch_bounds__(256) void post_bwd_vec_kernel(PostBwdArgs a) {
+  constexpr int V = 16 / sizeof(XT);
+  const int lane = threadIdx.x & 63;
+  const int64_t tok = (int64_t)blockIdx.x * 4 + __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  if (tok >= a.M) return;  // whole wave
+  const int C = a.C;
+  const int CV = C / V;
+  const int64_t NC = (int64_t)N * C;
+  const XT* __restrict__ x = static_cast<const XT*>(a.x) + tok * NC;
+  const XT* __restrict__ g = static_cast<const XT*>(a.g_out) + tok * NC;
+  const XT* __restrict__ f = static_cast<const XT*>(a.f_out) + tok * C;
+  XT* __restrict__ gx = a.g_x ? static_cast<XT*>(a.g_x) + tok * NC : nullptr;
+  XT* __restrict__ gf = static_cast<XT*>(a.g_f) + tok * C;
+
+  float hp[N];
+  load_pack<XT, N>(static_cast<const XT*>(a.h_post) + tok * N, hp);
+  float hr[RES ? N * N : 1];
+  if constexpr (RES) load_pack<XT, N * N>(static_cast<const XT*>(a.h_res) + tok * N * N, hr);
+  float ahr[RES ? N * N : 1];
+  float ahp[N];
+#pragma unroll
+  for (int k = 0; k < (RES ? N * N : 1); ++k) ahr[k] = 0.f;
+#pragma unroll
+  for (int i = 0; i < N; ++i) ahp[i] = 0.f;
+
+  for (int cv = lane; cv < CV; cv += 64) {
+    const int c = cv * V;
+    float gv[N][V];
+#pragma unroll
+    for (int i = 0; i < N; ++i) load_pack<XT, V>(g + (int64_t)i * C + c, gv[i]);
+    float fv[V];
+    load_pack<XT, V>(f + c, fv);
+    if constexpr (RES) {
+      float xv[N][V];
+#pragma unroll
+      for (int j = 0; j < N; ++j) load_pack<XT, V>(x + (int64_t)j * C + c, xv[j]);
+#pragma unroll
+      for (int j = 0; j < N; ++j) {
+        float o[V];
+#pragma unroll
+        for (int v = 0; v < V; ++v) {
+          float acc = 0.f;
+#pragma unroll
+          for (int i = 0; i < N; ++i) acc = fmaf(hr[i * N + j], gv[i][v], acc);
+          o[v] = acc;
+        }
+        store_pack<XT, V>(gx + (int64_t)j * C + c, o);
+      }
+#pragma unroll
+      for (int i = 0; i < N; ++i)
+#pragma unroll
+        for (int j = 0; j < N; ++j)
+#pragma unroll
+          for (int v = 0; v < V; ++v) ahr[i * N + j] = fmaf(gv[i][v], xv[j][v], ahr[i * N + j]);
+    } else if (gx) {
+#pragma unroll
+      for (int j = 0; j < N; ++j) store_pack<XT, V>(gx + (int64_t)j * C + c, gv[j]);
+    }
+    float o[V];
+#pragma unroll
+    for (int v = 0; v < V; ++v) {
+      float acc = 0.f;
+#pragma unroll
+      for (int i = 0; i < N; ++i) acc = fmaf(hp[i], gv[i][v], acc);
+      o[v] = acc;
+    }
+    store_pack<XT, V>(gf + c, o);
+#pragma unroll
+    for (int i = 0; i < N; ++i)
+#pragma unroll
+      for (int v = 0; v < V; ++v) ahp[i] = fmaf(gv[i][v], fv[v], ahp[i]);
+  }
+  // Reduce over the wave; lane k stores value k.
+  float mine_hr = 0.f;
+  if constexpr (RES) {
+#pragma unroll
+    for (int k = 0; k < N * N; ++k) {
+      const float t = wave_sum(ahr[k]);
+      mine_hr = lane == k ? t : mine_hr;
+    }
+  }
+  float mine_hp = 0.f;
+#pragma unroll
+  for (int i = 0; i < N; ++i) {
+    const float t = wave_sum(ahp[i]);
+    mine_hp = lane == i ? t : mine_hp;
+  }
+  if constexpr (RES) {
+    if (lane < N * N) static_cast<XT*>(a.g_h_res)[tok * N * N + lane] = Elem<XT>::put(mine_hr);
+  }
+  if (lane < N) static_cast<XT*>(a.g_h_post)[tok * N + lane] = Elem<XT>::put(mine_hp);
+}
+
+// Any dtypes, n <= 16, any C: one 256-thread workgroup per token.
+__device__ __forceinline__ float block_sum256(float v, float* red) {
+  v = wave_sum(v);
+  const int w = threadIdx.x >> 6;
+  __syncthreads();  // red is reused by consecutive calls
+  if ((threadIdx.x & 63) == 0) red[w] = v;
+  __syncthreads();
+  return (red[0] + red[1]) + (red[2] + red[3]);
+}
+
+__global__ __launch_bounds__(256) void post_bwd_generic_kernel(PostBwdArgs a) {
+  __shared__ float red[4];
+  const int64_t tok = blockIdx.x;
+  const int tid = threadIdx.x;
+  const int n = a.n;
+  const int C = a.C;
+  const int64_t NC = (int64_t)n * C;
+  const int64_t xb = tok * NC;
+  const int xdt = a.x_dtype, hdt = a.h_dtype, fdt = a.f_dtype;
+  const bool res = a.h_res != nullptr;
+  if (a.g_x) {
+    for (int64_t e = tid; e < NC; e += 256) {
+      const int j = (int)(e / C);
+      const int c = (int)(e - (int64_t)j * C);
+      float acc;
+      if (res) {
+        acc = 0.f;
+        for (int i = 0; i < n; ++i)
+          acc = fmaf(ld_any(a.h_res, tok * n * n + i * n + j, hdt),
+                     ld_any(a.g_out, xb + (int64_t)i * C + c, xdt), acc);
+      } else {
+        acc = ld_any(a.g_out, xb + e, xdt);
+      }
+      st_any(a.g_x, xb + e, xdt, acc);
+    }
+  }
+  for (int c = tid; c < C; c += 256) {
+    float acc = 0.f;
+    for (int i = 0; i < n; ++i)
+      acc = fmaf(ld_any(a.h_post, tok * n + i, hdt), ld_any(a.g_out, xb + (int64_t)i * C + c, xdt), acc);
+    st_any(a.g_f, tok * C + c, fdt, acc);
+  }
+  const int np = (res ? n * n : 0) + n;
+  for (int p = 0; p < np; ++p) {  // uniform
+    float acc = 0.f;
+    if (p < (res ? n * n : 0)) {
+      const int i = p / n;
+      const int j = p - i * n;
+      for (int c = tid; c < C; c += 256)
+        acc = fmaf(ld_any(a.g_out, xb + (int64_t)i * C + c, xdt), ld_any(a.x, xb + (int64_t)j * C + c, xdt), acc);
+    } else {
+      const int i = p - (res ? n * n : 0);
+      for (int c = tid; c < C; c += 256)
+        acc = fmaf(ld_any(a.g_out, xb + (int64_t)i * C + c, xdt), ld_any(a.f_out, tok * C + c, fdt), acc);
+    }
+    const float t = block_sum256(acc, red);
+    if (tid == 0) {
+      if (p < (res ? n * n : 0)) st_any(a.g_h_res, tok * n * n + p, hdt, t);
+      else st_any(a.g_h_post, tok * n + (p - (res ? n * n : 0)), hdt, t);
+    }
+  }
+}
+
+template <typename XT, int N>
+static hipError_t launch_bwd_vec(const PostBwdArgs& a, hipStream_t s) {
+  const int64_t blocks = (a.M + 3) / 4;
+  if (a.h_res)
+    hipLaunchKernelGGL((post_bwd_vec_kernel<XT, N, true>), dim3((unsigned)blocks), dim3(256), 0, s, a);
+  else
+    hipLaunchKernelGGL((post_bwd_vec_kernel<XT, N, false>), dim3((unsigned)blocks), dim3(256), 0, s, a);
+  return hipGetLastError();
+}
+
+template <typename XT>
+static hipError_t launch_bwd_vec_n(const PostBwdArgs& a, hipStream_t s) {
+  switch (a.n) {
+    case 1: return launch_bwd_vec<XT, 1>(a, s);
+    case 2: return launch_bwd_vec<XT, 2>(a, s);
+    case 4: return launch_bwd_vec<XT, 4>(a, s);
+    case 8: return launch_bwd_vec<XT, 8>(a, s);
+    default: return hipErrorInvalidValue;
+  }
+}
+
+hipError_t launch_post_bwd(const PostBwdArgs& a, hipStream_t s) {
+  const int xb = dtype_bytes(a.x_dtype);
+  const int V = 16 / xb;
+  const bool pow2n = a.n == 1 || a.n == 2 || a.n == 4 || a.n == 8;
+  auto small_ok = [&](const void* p, int elems) {
+    const int al = elems * xb > 16 ? 16 : elems * xb;
+    return p == nullptr || (reinterpret_cast<uintptr_t>(p) % al) == 0;
+  };
+  const bool vec_ok = pow2n && a.h_dtype == a.x_dtype && a.f_dtype == a.x_dtype && a.C % V == 0 &&
+                      aligned16(a.x) && aligned16(a.g_out) && aligned16(a.f_out) &&
+                      aligned16(a.g_f) && (a.g_x == nullptr || aligned16(a.g_x)) &&
+                      small_ok(a.h_post, a.n) && small_ok(a.h_res, a.n * a.n);
+  if (vec_ok) {
+    if (a.x_dtype == kBF16) return launch_bwd_vec_n<__bf16>(a, s);
+    if (a.x_dtype == kF32) return launch_bwd_vec_n<float>(a, s);
+    if (a.x_dtype == kF16) return launch_bwd_vec_n<_Float16>(a, s);
+  }
+  hipLaunchKernelGGL(post_bwd_generic_kernel, dim3((unsigned)a.M), dim3(256), 0, s, a);
+  return hipGetLastError();
+}
+
 }  // namespace mhc

@@ -101,12 +101,6 @@ constexpr int kGenMaxN = 16;
 constexpr int kGenMaxFD = 2 * kGenMaxN + kGenMaxN * kGenMaxN;
 constexpr int kGenChunk = 16;  // features reduced per block-wide reduction
 
-__device__ __forceinline__ float wave_sum(float v) {
-#pragma unroll
-  for (int m = 1; m < 64; m <<= 1) v += __shfl_xor(v, m, 64);
-  return v;
-}
-
 __global__ __launch_bounds__(kGenThreads) void pre_generic_kernel(PreArgs a) {
   __shared__ float s_red[kGenThreads / 64][kGenChunk];
   __shared__ float s_mix[kGenMaxFD];

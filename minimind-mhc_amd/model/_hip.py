@@ -19,7 +19,7 @@ LIB_PATH = Path(os.environ.get("MHC_AMD_LIB") or
                 Path(__file__).resolve().parent.parent / "libmhc_amd.so")
 
 DTYPE_F32, DTYPE_BF16, DTYPE_F16 = 0, 1, 2
-MODE_FULL, MODE_NOHRES, MODE_HEAD = 0, 1, 2
+MODE_FULL, MODE_NOHRES, MODE_HEAD, MODE_RMS = 0, 1, 2, 3
 _DTYPE_TAG = {torch.float32: DTYPE_F32, torch.bfloat16: DTYPE_BF16, torch.float16: DTYPE_F16}
 
 _P = ctypes.c_void_p
@@ -46,9 +46,25 @@ _SIGNATURES = {
     "mhc_head_fwd": (_I, [_P, _I, _P, _I, _P, _P, _P, _I, _P, _P, _P, _I64, _I, _I, _F, _F, _P]),
     "mhc_sinkhorn_fwd": (_I, [_P, _P, _I, _I64, _I, _I, _F, _P]),
     "mhc_stream_expand_fwd": (_I, [_P, _P, _I, _I64, _I, _I, _P]),
+    "mhc_post_bwd": (_I, [_P, _I, _P, _P, _I, _P, _I, _P, _P, _P, _P, _P, _I64, _I, _I, _P]),
+    "mhc_post_nohres_bwd": (_I, [_P, _I, _P, _I, _P, _I, _P, _P, _P, _I64, _I, _I, _P]),
+    "mhc_pre_bwd": (_I, [_P, _I, _P, _I,                  # x, x_dt, phi, phi_dt
+                         _P, _P, _P, _P, _P, _I,          # a_pre, b_pre, a_post, b_post, a_res, param_dt
+                         _P, _P,                          # inv_rms, mixes_raw
+                         _P, _P, _P, _P, _I,              # g_sub, g_h_pre, g_h_post, g_h_res_raw, grad_dt
+                         _P, _P,                          # g_x, g_raw
+                         _I64, _I, _I, _I, _F, _F, _P]),
+    "mhc_pre_bwd_weights_workspace_bytes": (_I64, [_I64, _I, _I, _I]),
+    "mhc_pre_bwd_weights": (_I, [_P, _I, _P, _P, _P,      # x, x_dt, inv, mixes, g_raw
+                                 _P, _P, _P, _I,          # alphas, param_dt
+                                 _P, _I,                  # g_phi, phi_dt
+                                 _P, _P, _P, _P, _P, _P,  # g_alpha/bias pre, post, res
+                                 _P, _I64,                # workspace, bytes
+                                 _I64, _I, _I, _I, _P]),
+    "mhc_sinkhorn_bwd": (_I, [_P, _I, _P, _I, _P, _I, _I64, _I, _I, _F, _P]),
 }
 
-ABI_VERSION = 1
+ABI_VERSION = 2
 _lib: Optional[ctypes.CDLL] = None
 
 

@@ -1,4 +1,4 @@
-"""Tensor-level wrappers of the C-ABI entry points (forward kernels only).
+"""Tensor-level wrappers of the C-ABI entry points.
 
 Each function validates shapes, allocates the outputs with torch.empty on the
 input's device (the library never allocates), and enqueues the kernel on the
@@ -219,4 +219,129 @@ def stream_expand(x: torch.Tensor, n: int) -> torch.Tensor:
     rc = H.load().mhc_stream_expand_fwd(xc.data_ptr(), out.data_ptr(), xc.element_size(),
                                         B * L, n, D, H.stream(dev))
     H.check(rc, "mhc_stream_expand_fwd")
+    return out
+
+
+# ------------------------------------------------------------------ backward
+# Gradients come back in the dtypes the reference's backward kernels store:
+# the forward inputs' dtypes, with the per-token g_raw in fp32.
+
+def post_bwd(x_flat, h_res, h_post, f_out, n, C, g_out):
+    """(g_x, g_h_res, g_h_post, g_f) of out = H_res . x + H_post (x) F.  With
+    h_res None (use_mhc = 2) g_x is g_out itself and g_h_res is None."""
+    dev = H.require_device(g_out, h_post, f_out, h_res, x_flat if h_res is not None else None)
+    NC = n * C
+    M = g_out.numel() // NC
+    hp = h_post.contiguous().view(M, n)
+    f2 = f_out.contiguous().view(M, C)
+    g_hp = torch.empty_like(hp)
+    g_f = torch.empty_like(f2)
+    lib = H.load()
+    if h_res is None:
+        g2 = _rows(g_out, NC)
+        rc = lib.mhc_post_nohres_bwd(hp.data_ptr(), H.dtype_tag(hp), f2.data_ptr(), H.dtype_tag(f2),
+                                     g2.data_ptr(), H.dtype_tag(g2), None, g_hp.data_ptr(),
+                                     g_f.data_ptr(), M, n, C, H.stream(dev))
+        H.check(rc, "mhc_post_nohres_bwd")
+        return g2, None, g_hp, g_f
+    x2 = _rows(x_flat, NC)
+    g2 = _rows(g_out, NC)
+    if g2.dtype != x2.dtype:
+        g2 = g2.to(x2.dtype)
+    hr = h_res.contiguous().view(M, n, n)
+    if hr.dtype != hp.dtype:
+        raise TypeError("mhc_amd: h_res and h_post must share a dtype")
+    g_x = torch.empty_like(x2)
+    g_hr = torch.empty_like(hr)
+    rc = lib.mhc_post_bwd(x2.data_ptr(), H.dtype_tag(x2), hr.data_ptr(), hp.data_ptr(),
+                          H.dtype_tag(hp), f2.data_ptr(), H.dtype_tag(f2), g2.data_ptr(),
+                          g_x.data_ptr(), g_hr.data_ptr(), g_hp.data_ptr(), g_f.data_ptr(),
+                          M, n, C, H.stream(dev))
+    H.check(rc, "mhc_post_bwd")
+    return g_x, g_hr, g_hp, g_f
+
+
+def pre_bwd(x2, phi, alphas, biases, inv_rms, mixes, n, C, mode, post_mult, pre_eps,
+            g_sub=None, g_hpre=None, g_hpost=None, g_hres=None):
+    """Per-token pre-phase backward.  alphas / biases: (pre, post, res) with
+    None for absent segments.  Returns (g_x [M, n*C] x dtype, g_raw [M, FD] fp32
+    or None for mode RMS)."""
+    grads = [g for g in (g_sub, g_hpre, g_hpost, g_hres) if g is not None]
+    dev = H.require_device(x2, inv_rms, *grads)
+    M = x2.shape[0]
+    gdt = grads[0].dtype if grads else x2.dtype
+    g_sub, g_hpre, g_hpost, g_hres = (None if g is None else g.to(gdt).contiguous()
+                                      for g in (g_sub, g_hpre, g_hpost, g_hres))
+    g_x = torch.empty_like(x2)
+    if mode == H.MODE_RMS:
+        phi_p = phi_dt = None
+        ps = [None] * 5
+        pdt = H.DTYPE_F32
+        g_raw = None
+    else:
+        FD = {H.MODE_FULL: 2 * n + n * n, H.MODE_NOHRES: 2 * n, H.MODE_HEAD: n}[mode]
+        phi_c = phi.detach().contiguous()
+        phi_p, phi_dt = phi_c.data_ptr(), H.dtype_tag(phi_c)
+        present = [p for p in (alphas[0], biases[0], alphas[1], biases[1], alphas[2]) if p is not None]
+        conv = iter(H.params_like(x2, *present))
+        ps = [None if p is None else next(conv)
+              for p in (alphas[0], biases[0], alphas[1], biases[1], alphas[2])]
+        pdt = H.dtype_tag(ps[0])
+        g_raw = torch.empty(M, FD, dtype=torch.float32, device=dev)
+    rc = H.load().mhc_pre_bwd(
+        x2.data_ptr(), H.dtype_tag(x2), phi_p, phi_dt if phi_dt is not None else H.DTYPE_F32,
+        *[H.ptr(p) for p in ps], pdt, inv_rms.data_ptr(), H.ptr(mixes),
+        H.ptr(g_sub), H.ptr(g_hpre), H.ptr(g_hpost), H.ptr(g_hres),
+        H.dtype_tag(g_sub if g_sub is not None else x2), g_x.data_ptr(), H.ptr(g_raw),
+        M, n, C, mode, float(post_mult), float(pre_eps), H.stream(dev))
+    H.check(rc, "mhc_pre_bwd")
+    return g_x, g_raw
+
+
+def pre_bwd_weights(x2, inv_rms, mixes, g_raw, phi, alphas, n, C, mode):
+    """(g_phi, [g_alpha_seg], [g_bias_seg]) from pre_bwd's g_raw; alphas as in
+    pre_bwd.  g_alpha_* are 0-dim, g_bias_* flat, all in the alphas' dtype."""
+    dev = H.require_device(x2, inv_rms, mixes, g_raw, phi)
+    M = x2.shape[0]
+    present = [a for a in alphas if a is not None]
+    conv = iter(H.params_like(x2, *present))
+    al = [None if a is None else next(conv) for a in alphas]
+    pdt = al[0].dtype
+    lib = H.load()
+    g_phi = torch.empty(phi.shape, dtype=phi.dtype, device=dev)
+    sizes = (n, n, n * n)
+    g_alpha = [None if a is None else torch.empty((), dtype=pdt, device=dev) for a in al]
+    g_bias = [None if a is None else torch.empty(sizes[i], dtype=pdt, device=dev)
+              for i, a in enumerate(al)]
+    if M == 0:
+        g_phi.zero_()
+        for t in g_alpha + g_bias:
+            if t is not None:
+                t.zero_()
+        return g_phi, g_alpha, g_bias
+    nbytes = lib.mhc_pre_bwd_weights_workspace_bytes(M, n, C, mode)
+    ws = torch.empty(nbytes, dtype=torch.uint8, device=dev)
+    rc = lib.mhc_pre_bwd_weights(
+        x2.data_ptr(), H.dtype_tag(x2), inv_rms.data_ptr(), mixes.data_ptr(), g_raw.data_ptr(),
+        *[H.ptr(a) for a in al], H.dtype_tag(al[0]), g_phi.data_ptr(), H.dtype_tag(g_phi),
+        H.ptr(g_alpha[0]), H.ptr(g_bias[0]), H.ptr(g_alpha[1]), H.ptr(g_bias[1]),
+        H.ptr(g_alpha[2]), H.ptr(g_bias[2]), ws.data_ptr(), nbytes, M, n, C, mode,
+        H.stream(dev))
+    H.check(rc, "mhc_pre_bwd_weights")
+    return g_phi, g_alpha, g_bias
+
+
+def sinkhorn_bwd(m: torch.Tensor, g: torch.Tensor, iters: int, eps: float,
+                 out_dtype=None) -> torch.Tensor:
+    """d sinkhorn(m) / d m applied to g, stored in out_dtype (default m's)."""
+    dev = H.require_device(m, g)
+    N = m.shape[-1]
+    mc = m.contiguous()
+    gc = g.contiguous()
+    out = torch.empty(mc.shape, dtype=out_dtype or mc.dtype, device=dev)
+    batch = mc.numel() // (N * N) if N > 0 else 0
+    rc = H.load().mhc_sinkhorn_bwd(mc.data_ptr(), H.dtype_tag(mc), gc.data_ptr(), H.dtype_tag(gc),
+                                   out.data_ptr(), H.dtype_tag(out), batch, N, int(iters),
+                                   float(eps), H.stream(dev))
+    H.check(rc, "mhc_sinkhorn_bwd")
     return out

@@ -13,7 +13,7 @@ import math
 import torch
 import torch.nn as nn
 
-from . import _grad, _ops
+from . import _ops
 from . import _hip as H
 
 
@@ -66,10 +66,12 @@ class _MHCHeadFn(torch.autograd.Function):
     def backward(ctx, g_out):
         x2, w, alpha, bias, inv, mix = ctx.saved_tensors
         n, c, pre_eps, shape = ctx.cfg
-        g_x, g_w, g_a, g_b = _grad.head_backward(x2, w, alpha, bias, inv, mix, n, c, pre_eps,
-                                                 g_out)
-        return (g_x.to(x2.dtype).view(shape), g_w.to(w.dtype), g_a.to(alpha.dtype),
-                g_b.to(bias.dtype), None, None, None, None, None)
+        alphas, biases = (alpha, None, None), (bias, None, None)
+        g_x, g_raw = _ops.pre_bwd(x2, w, alphas, biases, inv, mix, n, c, H.MODE_HEAD, 0.0,
+                                  pre_eps, g_sub=g_out)
+        g_w, g_a, g_b = _ops.pre_bwd_weights(x2, inv, mix, g_raw, w, alphas, n, c, H.MODE_HEAD)
+        return (g_x.view(shape), g_w, g_a[0].to(alpha.dtype).reshape(alpha.shape),
+                g_b[0].to(bias.dtype).view(bias.shape), None, None, None, None, None)
 
 
 class _RMSFn(torch.autograd.Function):
@@ -87,7 +89,10 @@ class _RMSFn(torch.autograd.Function):
     @staticmethod
     def backward(ctx, g_out):
         x2, inv = ctx.saved_tensors
-        return _grad.rms_backward(x2, inv, g_out).to(x2.dtype).view(g_out.shape), None
+        C = x2.shape[1]
+        g_x, _ = _ops.pre_bwd(x2, None, (None,) * 3, (None,) * 3, inv, None, 1, C, H.MODE_RMS,
+                              0.0, 0.0, g_sub=g_out)
+        return g_x.view(g_out.shape), None
 
 
 class MHCHead(nn.Module):

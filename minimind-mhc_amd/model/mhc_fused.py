@@ -9,8 +9,8 @@ gfx950 kernels through the C ABI of libmhc_amd.so:
   post : out = H_res . x + H_post (x) F(sublayer_in)
 
 There is no CPU or PyTorch forward path: tensors must be on a ROCm device and
-the library must be built.  The backward pass currently evaluates the
-reference's analytic gradients with fp32 torch ops (see _grad.py).
+the library must be built.  The backward pass runs the library's backward
+kernels (mhc_post_bwd, mhc_sinkhorn_bwd, mhc_pre_bwd, mhc_pre_bwd_weights).
 """
 from __future__ import annotations
 
@@ -20,7 +20,7 @@ from typing import Callable
 import torch
 import torch.nn as nn
 
-from . import _grad, _ops
+from . import _ops
 from . import _hip as H
 
 
@@ -44,7 +44,7 @@ class _SinkhornFn(torch.autograd.Function):
     @staticmethod
     def backward(ctx, dy):
         (M,) = ctx.saved_tensors
-        return _grad.sinkhorn_backward(M, ctx.iters, ctx.eps, dy).to(M.dtype), None, None
+        return _ops.sinkhorn_bwd(M, dy, ctx.iters, ctx.eps), None, None
 
 
 @torch.amp.autocast("cuda", enabled=False)
@@ -59,6 +59,19 @@ def sinkhorn_normalize(M: torch.Tensor, iters: int = 10, eps: float = 1e-6) -> t
 
 
 # --------------------------------------------------------- pre / post phases
+
+def _pre_full_grads(x2, w, alphas, biases, inv, mixes, n, c, post_mult, pre_eps, shape,
+                    g_sub, g_hpre, g_hpost, g_hres_raw):
+    """(g_x, g_phi, g_alpha_pre, g_bias_pre, g_alpha_post, g_bias_post, g_alpha_res,
+    g_bias_res) of the full pre phase, each in its forward input's dtype and shape."""
+    g_x, g_raw = _ops.pre_bwd(x2, w, alphas, biases, inv, mixes, n, c, H.MODE_FULL, post_mult,
+                              pre_eps, g_sub, g_hpre, g_hpost, g_hres_raw)
+    g_w, g_a, g_b = _ops.pre_bwd_weights(x2, inv, mixes, g_raw, w, alphas, n, c, H.MODE_FULL)
+    out = [g_x.view(shape), g_w]
+    for a, b, ga, gb in zip(alphas, biases, g_a, g_b):
+        out += [ga.to(a.dtype).reshape(a.shape), gb.to(b.dtype).view(b.shape)]
+    return out
+
 
 class _PrePhaseFullFn(torch.autograd.Function):
     """Pre phase -> (sublayer_in, h_pre, h_post, h_res_raw), h_res_raw before
@@ -82,12 +95,9 @@ class _PrePhaseFullFn(torch.autograd.Function):
     def backward(ctx, g_sub, g_hpre, g_hpost, g_hres_raw):
         x2, w, a_pre, b_pre, a_post, b_post, a_res, b_res, inv, mixes = ctx.saved_tensors
         n, c, post_mult, pre_eps, shape = ctx.cfg
-        g = _grad.pre_backward(x2, w, a_pre, b_pre, a_post, b_post, a_res, inv, mixes, n, c,
-                               post_mult, pre_eps, g_sub, g_hpre, g_hpost, g_hres_raw)
-        return (g[0].to(x2.dtype).view(shape), g[1].to(w.dtype),
-                g[2].to(a_pre.dtype).reshape(a_pre.shape), g[3].to(b_pre.dtype),
-                g[4].to(a_post.dtype).reshape(a_post.shape), g[5].to(b_post.dtype),
-                g[6].to(a_res.dtype).reshape(a_res.shape), g[7].to(b_res.dtype),
+        return (*_pre_full_grads(x2, w, (a_pre, a_post, a_res), (b_pre, b_post, b_res), inv,
+                                 mixes, n, c, post_mult, pre_eps, shape,
+                                 g_sub, g_hpre, g_hpost, g_hres_raw),
                 None, None, None, None, None)
 
 
@@ -118,14 +128,13 @@ class _PreSinkhornFn(torch.autograd.Function):
         n, c, post_mult, pre_eps, shape, iters, sk_eps = ctx.cfg
         g_raw = None
         if g_hres is not None:
-            g_raw = _grad.sinkhorn_backward(raw, iters, sk_eps, g_hres.reshape(raw.shape))
-        g = _grad.pre_backward(x2, w, a_pre, b_pre, a_post, b_post, a_res, inv, mixes, n, c,
-                               post_mult, pre_eps, g_sub, None, g_hpost, g_raw)
-        return (g[0].to(x2.dtype).view(shape), g[1].to(w.dtype), None,
-                g[2].to(a_pre.dtype).reshape(a_pre.shape), g[3].to(b_pre.dtype),
-                g[4].to(a_post.dtype).reshape(a_post.shape), g[5].to(b_post.dtype),
-                g[6].to(a_res.dtype).reshape(a_res.shape), g[7].to(b_res.dtype),
-                None, None, None, None, None, None, None)
+            # The reference runs Sinkhorn on h_res_raw.float() and casts back, so the
+            # gradient reaching the pre phase is rounded to the stream dtype.
+            g_raw = _ops.sinkhorn_bwd(raw, g_hres.reshape(raw.shape), iters, sk_eps,
+                                      out_dtype=x2.dtype)
+        g = _pre_full_grads(x2, w, (a_pre, a_post, a_res), (b_pre, b_post, b_res), inv, mixes,
+                            n, c, post_mult, pre_eps, shape, g_sub, None, g_hpost, g_raw)
+        return (g[0], g[1], None, *g[2:], None, None, None, None, None, None, None)
 
 
 class _PostPhaseFullFn(torch.autograd.Function):
@@ -145,10 +154,9 @@ class _PostPhaseFullFn(torch.autograd.Function):
     def backward(ctx, g_out):
         x2, h_res, h_post, f_out = ctx.saved_tensors
         n, c, shape = ctx.cfg
-        g_x, g_hr, g_hp, g_f = _grad.post_backward(x2, h_res, h_post, f_out, n, c, g_out)
-        return (g_x.to(x2.dtype).view(shape), g_hr.to(h_res.dtype).view(h_res.shape),
-                g_hp.to(h_post.dtype).view(h_post.shape), g_f.to(f_out.dtype).view(f_out.shape),
-                None, None)
+        g_x, g_hr, g_hp, g_f = _ops.post_bwd(x2, h_res, h_post, f_out, n, c, g_out)
+        return (g_x.view(shape), g_hr.view(h_res.shape), g_hp.view(h_post.shape),
+                g_f.to(f_out.dtype).view(f_out.shape), None, None)
 
 
 # ------------------------------------------------------------------- module

@@ -13,7 +13,7 @@ from typing import Callable
 import torch
 import torch.nn as nn
 
-from . import _grad, _ops
+from . import _ops
 from . import _hip as H
 
 
@@ -42,11 +42,14 @@ class _PrePhaseFn(torch.autograd.Function):
     def backward(ctx, g_sub, g_hpre, g_hpost):
         x2, w, a_pre, b_pre, a_post, b_post, inv, mixes = ctx.saved_tensors
         n, c, post_mult, pre_eps, shape = ctx.cfg
-        g = _grad.pre_backward(x2, w, a_pre, b_pre, a_post, b_post, None, inv, mixes, n, c,
-                               post_mult, pre_eps, g_sub, g_hpre, g_hpost, None)
-        return (g[0].to(x2.dtype).view(shape), g[1].to(w.dtype),
-                g[2].to(a_pre.dtype).reshape(a_pre.shape), g[3].to(b_pre.dtype),
-                g[4].to(a_post.dtype).reshape(a_post.shape), g[5].to(b_post.dtype),
+        alphas, biases = (a_pre, a_post, None), (b_pre, b_post, None)
+        g_x, g_raw = _ops.pre_bwd(x2, w, alphas, biases, inv, mixes, n, c, H.MODE_NOHRES,
+                                  post_mult, pre_eps, g_sub, g_hpre, g_hpost)
+        g_w, g_a, g_b = _ops.pre_bwd_weights(x2, inv, mixes, g_raw, w, alphas, n, c,
+                                             H.MODE_NOHRES)
+        return (g_x.view(shape), g_w,
+                g_a[0].to(a_pre.dtype).reshape(a_pre.shape), g_b[0].to(b_pre.dtype).view(b_pre.shape),
+                g_a[1].to(a_post.dtype).reshape(a_post.shape), g_b[1].to(b_post.dtype).view(b_post.shape),
                 None, None, None, None, None, None)
 
 
@@ -66,12 +69,8 @@ class _PostPhaseFn(torch.autograd.Function):
     def backward(ctx, g_out):
         h_post, f_out = ctx.saved_tensors
         n, c, shape = ctx.cfg
-        M = shape[0] * shape[1]
-        g = g_out.float().reshape(M, n, c)
-        g_hp = torch.bmm(g, f_out.float().reshape(M, c, 1)).squeeze(-1)
-        g_f = torch.bmm(h_post.float().reshape(M, 1, n), g).squeeze(1)
-        return (g_out, g_hp.to(h_post.dtype).view(h_post.shape),
-                g_f.to(f_out.dtype).view(f_out.shape), None, None)
+        g_x, _, g_hp, g_f = _ops.post_bwd(None, None, h_post, f_out, n, c, g_out)
+        return (g_x.view(shape), g_hp.view(h_post.shape), g_f.view(f_out.shape), None, None)
 
 
 class MHCConnection_FusedNoHres(nn.Module):
