@@ -114,7 +114,272 @@ __global__ __launch_bounds__(256) void pre_bwd_generic_kernel(PreBwdArgs a) {
   }
 }
 
+// ------------------------------------------------- pre phase, bf16 on MFMA
+// One workgroup of NW waves per 16-token tile.  The tile's n*C row is cut into
+// chunks of 32 columns of one stream (chunk k = stream k / NCB, column block
+// k % NCB); wave w owns chunks w, w + NW, ...  A lane (r, g) holds token r,
+// columns 8g .. 8g + 7 of each of its chunks (16 bytes of x), the layout of
+// the forward kernels.
+//   A: phi rows.  A-row j of the chunk's k-tile h (h = 0, 1) is column
+//      8*(j/4) + 4h + j%4 of the chunk, so the D tile's lane (token c, g),
+//      rows 4g .. 4g+3, covers columns 8g + 4h .. 8g + 4h + 3: the two tiles
+//      give the 8 columns the lane holds of x.
+//   B: (alpha * g_raw)[token][f] for 32 features per K-step, split into bf16
+//      hi + lo so the product keeps ~16 mantissa bits (phi is bf16-exact).
+// Reductions over a token's columns (gh and mean(xn * gxn)) go through the 4
+// lanes of a token (lane xor 16, 32), then per chunk / per wave through LDS
+// and are summed there in a fixed order (deterministic).  HOLD keeps the gxn
+// tiles in registers between the two passes; otherwise the second pass
+// recomputes them (phi re-read from L2).
+template <int N, int MODE, int NW, int KJ>
+__global__ __launch_bounds__(NW * 64) void pre_bwd_mfma_kernel(PreBwdArgs a) {
+  constexpr int FD = MODE == kFull ? 2 * N + N * N : (MODE == kNoHres ? 2 * N : N);
+  constexpr int KS = (FD + 31) / 32;  // 32-feature K-steps
+  constexpr int TM = 16;
+  constexpr bool HOLD = NW == 8 && KJ <= 12;
+  __shared__ float s_gp[NW * KJ][TM];   // per-chunk partials of gh
+  __shared__ float s_mp[NW][TM];         // per-wave partials of sum x * gxn
+  __shared__ float s_gm[TM][KS * 32];    // alpha * g_raw, zero padded
+  __shared__ float s_hp[TM][N];          // h_pre = sigmoid + pre_eps (fp32 recompute)
+
+  const int tid = threadIdx.x;
+  const int lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int r = lane & 15;
+  const int g = lane >> 4;
+  const int C = a.C;
+  const int NC = N * C;
+  const int NCB = (C + 31) / 32;
+  const int NCH = N * NCB;
+  const int64_t t0 = (int64_t)blockIdx.x * TM;
+  const int valid = (int)(a.M - t0 < TM ? a.M - t0 : TM);
+
+  const auto rx = make_rsrc(static_cast<const uint16_t*>(a.x) + t0 * NC, (uint32_t)valid * NC * 2u);
+  const auto rgs = make_rsrc(a.g_sub ? static_cast<const uint16_t*>(a.g_sub) + t0 * C : nullptr,
+                             a.g_sub ? (uint32_t)valid * C * 2u : 0u);
+  const auto rgx = make_rsrc(static_cast<uint16_t*>(a.g_x) + t0 * NC, (uint32_t)valid * NC * 2u);
+  const auto rphi = make_rsrc(a.phi, (uint32_t)NC * FD * 2u);
+
+  // chunk j of this wave: stream ci, first column c0; lane column c0 + 8g
+  auto chunk = [&](int j, int& ci, int& c0) {
+    const int k = wave + NW * j;
+    ci = k < NCH ? k / NCB : 0;
+    c0 = k < NCH ? (k - ci * NCB) * 32 : C;  // C: no columns (loads read zeros)
+  };
+  U32x4 xs[KJ];
+#pragma unroll
+  for (int j = 0; j < KJ; ++j) {
+    int ci, c0;
+    chunk(j, ci, c0);
+    const bool ok = c0 + 8 * g < C;
+    xs[j] = buf_load16(rx, ok ? (uint32_t)(r * NC + ci * C + c0 + 8 * g) * 2u : kBufOob);
+  }
+  const float inv = r < valid ? a.inv_rms[t0 + r] : 0.f;
+
+  // ---- gh partials per chunk: sum_c g_sub[c] * x[i][c]
+#pragma unroll
+  for (int j = 0; j < KJ; ++j) {
+    int ci, c0;
+    chunk(j, ci, c0);
+    const bool ok = c0 + 8 * g < C;
+    const U32x4 gv = buf_load16(rgs, ok ? (uint32_t)(r * C + c0 + 8 * g) * 2u : kBufOob);
+    float acc = 0.f;
+#pragma unroll
+    for (int e = 0; e < 4; ++e) acc = dot2_bf16(gv.v[e], xs[j].v[e], acc);
+    acc += xor_lane16(acc);
+    acc += xor_lane32(acc);
+    if (g == 0) s_gp[wave + NW * j][r] = acc;
+  }
+  __syncthreads();
+
+  // ---- gates: g_raw and alpha * g_raw per (token, feature)
+  const int pdt = a.param_dtype;
+  const int gdt = a.grad_dtype;
+  for (int idx = tid; idx < TM * KS * 32; idx += NW * 64) {
+    const int tt = idx / (KS * 32);
+    const int f = idx - tt * (KS * 32);
+    float gm = 0.f;
+    if (f < FD && tt < valid) {
+      const int64_t tk = t0 + tt;
+      const float m = a.mixes[tk * FD + f];
+      float graw;
+      float alpha;
+      if (f < N) {
+        float gh = a.g_hpre ? ld_any(a.g_hpre, tk * N + f, gdt) : 0.f;
+        for (int cb = 0; cb < NCB; ++cb) gh += s_gp[f * NCB + cb][tt];
+        alpha = ld_any(a.alpha[0], 0, pdt);
+        const float sg = sigmoid_f(fmaf(alpha, m, ld_any(a.bias[0], f, pdt)));
+        graw = gh * sg * (1.0f - sg);
+        s_hp[tt][f] = sg + a.pre_eps;
+      } else if (f < 2 * N) {
+        alpha = ld_any(a.alpha[1], 0, pdt);
+        const float sg = sigmoid_f(fmaf(alpha, m, ld_any(a.bias[1], f - N, pdt)));
+        const float gp = a.g_hpost ? ld_any(a.g_hpost, tk * N + (f - N), gdt) : 0.f;
+        graw = gp * sg * (1.0f - sg) * a.post_mult;
+      } else {
+        alpha = ld_any(a.alpha[2], 0, pdt);
+        graw = a.g_hres ? ld_any(a.g_hres, tk * N * N + (f - 2 * N), gdt) : 0.f;
+      }
+      a.g_raw[tk * FD + f] = graw;
+      gm = graw * alpha;
+    } else if (f < N) {
+      s_hp[tt][f] = 0.f;
+    }
+    s_gm[tt][f] = gm;
+  }
+  __syncthreads();
+
+  // ---- B operands: lane (token r, g) holds features 32s + 8g .. + 7, hi and lo
+  bf16x8_t bhi[KS];
+  bf16x8_t blo[KS];
+#pragma unroll
+  for (int ks = 0; ks < KS; ++ks) {
+    U32x4 h4, l4;
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+      const float v0 = s_gm[r][32 * ks + 8 * g + 2 * e];
+      const float v1 = s_gm[r][32 * ks + 8 * g + 2 * e + 1];
+      const uint32_t hp = pack_bf16x2(v0, v1);
+      h4.v[e] = hp;
+      l4.v[e] = pack_bf16x2(v0 - bf16lo(hp), v1 - bf16hi(hp));
+    }
+    bhi[ks] = __builtin_bit_cast(bf16x8_t, h4);
+    blo[ks] = __builtin_bit_cast(bf16x8_t, l4);
+  }
+
+  // ---- gxn = phi . (alpha * g_raw) on MFMA, and the partial of sum x * gxn
+  auto gxn_tile = [&](int j, int h) {
+    int ci, c0;
+    chunk(j, ci, c0);
+    const int col = c0 + 8 * (r >> 2) + 4 * h + (r & 3);  // A-row r of this k-tile
+    f32x4_t d = f32x4_t{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+    for (int ks = 0; ks < KS; ++ks) {
+      const bool ok = col < C && 32 * ks + 8 * g < FD;
+      const bf16x8_t av = __builtin_bit_cast(
+          bf16x8_t, buf_load16(rphi, ok ? (uint32_t)((ci * C + col) * FD + 32 * ks + 8 * g) * 2u : kBufOob));
+      d = __builtin_amdgcn_mfma_f32_16x16x32_bf16(av, bhi[ks], d, 0, 0, 0);
+      d = __builtin_amdgcn_mfma_f32_16x16x32_bf16(av, blo[ks], d, 0, 0, 0);
+    }
+    return d;
+  };
+  f32x4_t acc[HOLD ? KJ : 1][2];
+  float mp = 0.f;
+#pragma unroll
+  for (int j = 0; j < KJ; ++j)
+#pragma unroll
+    for (int h = 0; h < 2; ++h) {
+      const f32x4_t d = gxn_tile(j, h);
+      if constexpr (HOLD) acc[j][h] = d;
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        const uint32_t w2 = xs[j].v[2 * h + (e >> 1)];
+        mp = fmaf((e & 1) ? bf16hi(w2) : bf16lo(w2), d[e], mp);
+      }
+    }
+  mp += xor_lane16(mp);
+  mp += xor_lane32(mp);
+  if (g == 0) s_mp[wave][r] = mp;
+  __syncthreads();
+  float msum = 0.f;
+#pragma unroll
+  for (int w = 0; w < NW; ++w) msum += s_mp[w][r];
+  const float mean = inv * msum / (float)NC;  // mean_k(xn * gxn)
+
+  // ---- g_x = inv * (gxn - xn * mean) + h_pre[i] * g_sub
+#pragma unroll
+  for (int j = 0; j < KJ; ++j) {
+    int ci, c0;
+    chunk(j, ci, c0);
+    const bool ok = c0 + 8 * g < C;
+    f32x4_t d2[2];
+#pragma unroll
+    for (int h = 0; h < 2; ++h) {
+      if constexpr (HOLD) d2[h] = acc[j][h];
+      else d2[h] = gxn_tile(j, h);
+    }
+    const U32x4 gv = buf_load16(rgs, ok ? (uint32_t)(r * C + c0 + 8 * g) * 2u : kBufOob);
+    const float hp = s_hp[r][ci];
+    U32x4 o;
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+      float v[2];
+#pragma unroll
+      for (int b = 0; b < 2; ++b) {
+        const int cc = 2 * e + b;  // column 8g + cc
+        const float gx = d2[cc >> 2][cc & 3];
+        const float xv = b ? bf16hi(xs[j].v[e]) : bf16lo(xs[j].v[e]);
+        const float gsv = b ? bf16hi(gv.v[e]) : bf16lo(gv.v[e]);
+        v[b] = inv * (gx - xv * inv * mean) + hp * gsv;
+      }
+      o.v[e] = pack_bf16x2(v[0], v[1]);
+    }
+    // whole offset in the vector offset, scalar offset the literal 0 (a
+    // 128-bit store reads its data registers after issue)
+    buf_store16(rgx, ok ? (uint32_t)(r * NC + ci * C + c0 + 8 * g) * 2u : kBufOob, o);
+  }
+}
+
+// Chunks per wave instantiated: 2 .. 24 in steps that cover C <= 1024 for
+// n in {2, 4} (8 waves) and n = 8 (16 waves).
+template <int N, int MODE, int NW, int KJ>
+static hipError_t launch_pre_bwd_inst(const PreBwdArgs& a, hipStream_t s) {
+  hipLaunchKernelGGL((pre_bwd_mfma_kernel<N, MODE, NW, KJ>), dim3((unsigned)((a.M + 15) / 16)),
+                     dim3(NW * 64), 0, s, a);
+  return hipGetLastError();
+}
+
+template <int N, int MODE, int NW, int... KJS>
+static hipError_t launch_pre_bwd_mfma_kj(const PreBwdArgs& a, int kj, hipStream_t s) {
+  hipError_t r = hipErrorInvalidValue;
+  bool done = false;
+  ((!done && KJS >= kj ? (r = launch_pre_bwd_inst<N, MODE, NW, KJS>(a, s), done = true) : false), ...);
+  return r;
+}
+
+template <int N, int MODE>
+static hipError_t launch_pre_bwd_mfma_mode(const PreBwdArgs& a, hipStream_t s) {
+  constexpr int NW = N >= 8 ? 16 : 8;
+  const int nch = N * ((a.C + 31) / 32);
+  const int kj = (nch + NW - 1) / NW;
+  return launch_pre_bwd_mfma_kj<N, MODE, NW, 2, 4, 6, 8, 12, 16>(a, kj, s);
+}
+
+// Shapes with an MFMA kernel: bf16 x / phi / gradients, n in {2, 4, 8}, FD a
+// multiple of 8 (16-byte phi rows), C % 8 == 0 and C <= 1024, 16-byte aligned
+// x / g_sub / g_x / phi.
+static bool pre_bwd_mfma_ok(const PreBwdArgs& a) {
+  auto al = [](const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15) == 0; };
+  if (a.mode == kRms) return false;
+  if (a.x_dtype != kBF16 || a.phi_dtype != kBF16 || a.grad_dtype != kBF16) return false;
+  if (!(a.n == 2 || a.n == 4 || a.n == 8)) return false;
+  if (mode_fd(a.mode, a.n) % 8 != 0) return false;
+  if (a.C % 8 != 0 || a.C > 32 * kMfmaMaxColBlocks) return false;
+  if ((int64_t)a.n * a.C * mode_fd(a.mode, a.n) * 2 > 0x7fffffffLL) return false;
+  return al(a.x) && al(a.phi) && al(a.g_x) && (a.g_sub == nullptr || al(a.g_sub));
+}
+
+template <int N>
+static hipError_t launch_pre_bwd_mfma_n(const PreBwdArgs& a, hipStream_t s) {
+  switch (a.mode) {
+    case kFull: return launch_pre_bwd_mfma_mode<N, kFull>(a, s);
+    case kNoHres: return launch_pre_bwd_mfma_mode<N, kNoHres>(a, s);
+    case kHead:
+      if constexpr (N == 8) return launch_pre_bwd_mfma_mode<N, kHead>(a, s);
+      return hipErrorInvalidValue;
+    default: return hipErrorInvalidValue;
+  }
+}
+
 hipError_t launch_pre_bwd(const PreBwdArgs& a, hipStream_t s) {
+  if (pre_bwd_mfma_ok(a)) {
+    switch (a.n) {
+      case 2: return launch_pre_bwd_mfma_n<2>(a, s);
+      case 4: return launch_pre_bwd_mfma_n<4>(a, s);
+      case 8: return launch_pre_bwd_mfma_n<8>(a, s);
+      default: break;
+    }
+  }
   hipLaunchKernelGGL(pre_bwd_generic_kernel, dim3((unsigned)a.M), dim3(256), 0, s, a);
   return hipGetLastError();
 }
@@ -204,15 +469,172 @@ __global__ __launch_bounds__(256) void weights_reduce_kernel(WeightsArgs a, int 
   }
 }
 
+// bf16 x on MFMA.  Workgroup (k-slice of 128 columns, token range): per step
+// of 64 tokens the x tile is written to LDS transposed ([column][token], two
+// tokens per 32-bit write) and u = inv_rms * g_raw ([feature][token]) split
+// into bf16 hi + lo, then wave w accumulates
+//   D[16w + i][f] += sum_t x[t][k0 + 16w + i] * u[t][f]
+// with A = x^T rows (16-byte LDS reads of 8 tokens) and B = u columns.
+// Workgroups of k-slice 0 also sum g_raw and g_raw * mixes per feature over
+// their range (the alpha / bias partials).
+constexpr int kWTok = 64;                // tokens per step
+constexpr int kWCols = 128;              // columns per workgroup
+constexpr int kWRow = kWTok * 2 + 16;    // LDS row stride in bytes (64 bf16 + pad)
+
+template <int NTF>  // 16-wide feature tiles
+__global__ __launch_bounds__(512) void weights_mfma_kernel(WeightsArgs a, int64_t per) {
+  __shared__ __attribute__((aligned(16))) unsigned char s_x[kWCols * kWRow];
+  __shared__ __attribute__((aligned(16))) unsigned char s_uh[NTF * 16 * kWRow];
+  __shared__ __attribute__((aligned(16))) unsigned char s_ul[NTF * 16 * kWRow];
+  __shared__ float s_ab[2][kWTok / 2][NTF * 16];
+  const int FD = mode_fd(a.mode, a.n);
+  const int NC = a.n * a.C;
+  const int tid = threadIdx.x;
+  const int lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int r = lane & 15;
+  const int g = lane >> 4;
+  const int k0 = blockIdx.x * kWCols;
+  const int rng = blockIdx.y;
+  const int64_t tb = (int64_t)rng * per;
+  const int64_t te = tb + per < a.M ? tb + per : a.M;
+  const bool ab_slice = blockIdx.x == 0;
+
+  const int tp = tid & 31;  // token pair (tokens 2tp, 2tp + 1 of the step)
+  const int kc = tid >> 5;  // 8-column group (columns k0 + 8kc .. + 7)
+  const int col = k0 + 8 * kc;
+  constexpr int UPT = (kWTok / 2) * NTF * 16 / 512;  // u pairs per thread per step
+  float sb[UPT > 0 ? UPT : 1], sa[UPT > 0 ? UPT : 1];
+#pragma unroll
+  for (int u = 0; u < (UPT > 0 ? UPT : 1); ++u) { sb[u] = 0.f; sa[u] = 0.f; }
+
+  f32x4_t acc[NTF];
+#pragma unroll
+  for (int ft = 0; ft < NTF; ++ft) acc[ft] = f32x4_t{0.f, 0.f, 0.f, 0.f};
+
+  for (int64_t t = tb; t < te; t += kWTok) {
+    const int valid = (int)(te - t < kWTok ? te - t : kWTok);
+    const auto rs = make_rsrc(static_cast<const uint16_t*>(a.x) + t * NC, (uint32_t)valid * NC * 2u);
+    const bool okc = col < NC;
+    const U32x4 xa = buf_load16(rs, okc ? (uint32_t)((2 * tp) * NC + col) * 2u : kBufOob);
+    const U32x4 xb = buf_load16(rs, okc ? (uint32_t)((2 * tp + 1) * NC + col) * 2u : kBufOob);
+    // u = inv * g_raw for (token pair, feature), hi / lo bf16 pairs
+#pragma unroll
+    for (int u = 0; u < UPT; ++u) {
+      const int idx = tid + 512 * u;
+      const int pp = idx & 31;
+      const int f = idx >> 5;
+      float va = 0.f, vb = 0.f;
+      const int64_t ta = t + 2 * pp;
+      if (f < FD) {
+        if (ta < te) {
+          const float gr = a.g_raw[ta * FD + f];
+          va = a.inv_rms[ta] * gr;
+          if (ab_slice) { sb[u] += gr; sa[u] = fmaf(gr, a.mixes[ta * FD + f], sa[u]); }
+        }
+        if (ta + 1 < te) {
+          const float gr = a.g_raw[(ta + 1) * FD + f];
+          vb = a.inv_rms[ta + 1] * gr;
+          if (ab_slice) { sb[u] += gr; sa[u] = fmaf(gr, a.mixes[(ta + 1) * FD + f], sa[u]); }
+        }
+      }
+      const uint32_t hi = pack_bf16x2(va, vb);
+      *reinterpret_cast<uint32_t*>(s_uh + f * kWRow + pp * 4) = hi;
+      *reinterpret_cast<uint32_t*>(s_ul + f * kWRow + pp * 4) =
+          pack_bf16x2(va - bf16lo(hi), vb - bf16hi(hi));
+    }
+    // x tile transposed: column 8kc + e, tokens (2tp, 2tp + 1) in one dword
+#pragma unroll
+    for (int e = 0; e < 8; ++e) {
+      const uint32_t wa = xa.v[e >> 1];
+      const uint32_t wb = xb.v[e >> 1];
+      const uint32_t d = (e & 1) ? ((wa >> 16) | (wb & 0xffff0000u)) : ((wa & 0xffffu) | (wb << 16));
+      *reinterpret_cast<uint32_t*>(s_x + (8 * kc + e) * kWRow + tp * 4) = d;
+    }
+    __syncthreads();
+#pragma unroll
+    for (int ks = 0; ks < kWTok / 32; ++ks) {
+      const bf16x8_t av = *reinterpret_cast<const bf16x8_t*>(s_x + (16 * wave + r) * kWRow + (32 * ks + 8 * g) * 2);
+#pragma unroll
+      for (int ft = 0; ft < NTF; ++ft) {
+        const int off = (16 * ft + r) * kWRow + (32 * ks + 8 * g) * 2;
+        acc[ft] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(av, *reinterpret_cast<const bf16x8_t*>(s_uh + off), acc[ft], 0, 0, 0);
+        acc[ft] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(av, *reinterpret_cast<const bf16x8_t*>(s_ul + off), acc[ft], 0, 0, 0);
+      }
+    }
+    __syncthreads();
+  }
+  // partial W of this range: lane (feature column r, g) holds rows 4g .. 4g + 3
+  float* W = a.work + (int64_t)rng * NC * FD;
+#pragma unroll
+  for (int ft = 0; ft < NTF; ++ft)
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      const int k = k0 + 16 * wave + 4 * g + j;
+      const int f = 16 * ft + r;
+      if (k < NC && f < FD) W[(int64_t)k * FD + f] = acc[ft][j];
+    }
+  if (ab_slice) {  // alpha / bias partials: sum the 32 token-pair lanes of each feature
+#pragma unroll
+    for (int u = 0; u < UPT; ++u) {
+      const int idx = tid + 512 * u;
+      s_ab[0][idx & 31][idx >> 5] = sb[u];
+      s_ab[1][idx & 31][idx >> 5] = sa[u];
+    }
+    __syncthreads();
+    float* ab = a.work + (int64_t)gridDim.y * NC * FD + (int64_t)rng * 2 * FD;
+    for (int f = tid; f < FD; f += 512) {
+      float b = 0.f, al = 0.f;
+      for (int q = 0; q < kWTok / 2; ++q) {
+        b += s_ab[0][q][f];
+        al += s_ab[1][q][f];
+      }
+      ab[f] = b;
+      ab[FD + f] = al;
+    }
+  }
+}
+
+template <int NTF>
+static hipError_t launch_weights_mfma(const WeightsArgs& a, int R, int64_t per, hipStream_t s) {
+  const int NC = a.n * a.C;
+  hipLaunchKernelGGL((weights_mfma_kernel<NTF>), dim3((unsigned)((NC + kWCols - 1) / kWCols), (unsigned)R),
+                     dim3(512), 0, s, a, per);
+  return hipGetLastError();
+}
+
 hipError_t launch_pre_bwd_weights(const WeightsArgs& a, hipStream_t s) {
   const int FD = mode_fd(a.mode, a.n);
   const int64_t NC = (int64_t)a.n * a.C;
-  const int R = weight_ranges(a.M);
-  const int64_t per = (a.M + R - 1) / R;
   const int64_t qb = (NC * FD + 255) / 256;
-  hipLaunchKernelGGL(weights_partial_generic_kernel, dim3((unsigned)R, (unsigned)qb), dim3(256), 0, s,
-                     a, R, per);
-  if (hipError_t e = hipGetLastError(); e != hipSuccess) return e;
+  const int ntf = (FD + 15) / 16;
+  const bool mfma = a.x_dtype == kBF16 && NC % 8 == 0 &&
+                    (reinterpret_cast<uintptr_t>(a.x) & 15) == 0 &&
+                    (ntf == 1 || ntf == 2 || ntf == 3 || ntf == 5);  // FD <= 80 (LDS)
+  int R = weight_ranges(a.M);
+  hipError_t e;
+  if (mfma) {
+    // about two workgroups per CU, token ranges of whole 64-token steps
+    const int64_t slices = (NC + kWCols - 1) / kWCols;
+    int64_t want = (512 + slices - 1) / slices;
+    if (want < R) R = (int)want;
+    int64_t per = (a.M + R - 1) / R;
+    per = (per + kWTok - 1) / kWTok * kWTok;
+    R = (int)((a.M + per - 1) / per);
+    switch (ntf) {
+      case 1: e = launch_weights_mfma<1>(a, R, per, s); break;
+      case 2: e = launch_weights_mfma<2>(a, R, per, s); break;
+      case 3: e = launch_weights_mfma<3>(a, R, per, s); break;
+      case 5: e = launch_weights_mfma<5>(a, R, per, s); break;
+      default: e = launch_weights_mfma<5>(a, R, per, s); break;
+    }
+  } else {
+    const int64_t per = (a.M + R - 1) / R;
+    hipLaunchKernelGGL(weights_partial_generic_kernel, dim3((unsigned)R, (unsigned)qb), dim3(256), 0, s,
+                       a, R, per);
+    e = hipGetLastError();
+  }
+  if (e != hipSuccess) return e;
   hipLaunchKernelGGL(weights_reduce_kernel, dim3((unsigned)qb), dim3(256), 0, s, a, R);
   return hipGetLastError();
 }
