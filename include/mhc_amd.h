@@ -242,8 +242,8 @@ int mhc_pre_bwd_weights(const void* x, int x_dtype, const float* inv_rms, const 
 
 /*
  * Sinkhorn-Knopp backward: g_in = d output / d input of mhc_sinkhorn_fwd's
- * schedule, by recomputing the forward iterates (fp32).  n <= 16,
- * iters <= 64.
+ * schedule, by recomputing the forward iterates (fp32).  n <= 16;
+ * iters <= 64 for n in {2, 4, 8}, <= 30 otherwise (the iterates live in LDS).
  * Replaces _SinkhornFn.backward  model/mhc_fused.py:131-137.
  */
 int mhc_sinkhorn_bwd(const void* m_in, int in_dtype, const void* g_out, int g_dtype, void* g_in,

@@ -342,7 +342,9 @@ int mhc_sinkhorn_bwd(const void* m_in, int in_dtype, const void* g_out, int g_dt
   const char* fn = "mhc_sinkhorn_bwd";
   if (batch < 0) return fail(hipErrorInvalidValue, "%s: batch must be >= 0", fn);
   if (n < 1 || n > 16) return fail(hipErrorInvalidValue, "%s: n must be in [1, 16] (got %d)", fn, n);
-  if (iters > 64) return fail(hipErrorInvalidValue, "%s: iters must be <= 64 (got %d)", fn, iters);
+  const bool lanes = n == 2 || n == 4 || n == 8;  // trajectory in 64 KiB of LDS per wave
+  if (iters > (lanes ? 64 : 30))
+    return fail(hipErrorInvalidValue, "%s: iters must be <= %d for n = %d (got %d)", fn, lanes ? 64 : 30, n, iters);
   if (!dtype_ok(in_dtype) || !dtype_ok(g_dtype) || !dtype_ok(gi_dtype)) return fail(hipErrorInvalidValue, "%s: bad dtype", fn);
   if (batch > kMaxBlocks) return fail(hipErrorInvalidValue, "%s: batch too large", fn);
   if (batch == 0) return 0;

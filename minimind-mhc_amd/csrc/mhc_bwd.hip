@@ -719,9 +719,63 @@ __global__ __launch_bounds__(256) void sinkhorn_bwd_kernel(const void* __restric
   if (live) st_any(g_in, idx, gi_dt, gm);
 }
 
+// n in {2, 4, 8}: one wave per workgroup, one matrix element per lane
+// (64 / n^2 matrices per wave), row and column sums as DPP / permlane
+// butterflies inside the matrix's lanes (row_reduce / col_sum).  Each lane
+// keeps its own forward trajectory in private LDS slots (the iterate after
+// each step and that step's divisor), so no barrier is needed; divisions are
+// reciprocal * multiply, as in the forward kernels.
+template <int N>
+__global__ __launch_bounds__(64) void sinkhorn_bwd_lanes_kernel(const void* __restrict__ m_in, int in_dt,
+                                                                const void* __restrict__ g_out, int g_dt,
+                                                                void* __restrict__ g_in, int gi_dt,
+                                                                int64_t batch, int iters, float eps) {
+  extern __shared__ float lds[];
+  constexpr int G = N * N;
+  const int lane = threadIdx.x;
+  const int64_t idx = (int64_t)blockIdx.x * 64 + lane;  // element index (64 / G matrices per wave)
+  const bool live = idx < batch * G;
+  const int steps = 2 * (iters > 1 ? iters : 1);
+  float* Y = lds;                 // [steps][64] iterate after step s
+  float* D = lds + steps * 64;    // [steps][64] divisor of step s (1 for the softmax step)
+
+  const float v = live ? ld_any(m_in, idx, in_dt) : 0.f;
+  const float mx = row_reduce<N, OpMax>(v);
+  const float ex = expf(v - mx);
+  const float p = ex * __builtin_amdgcn_rcpf(row_reduce<N, OpAdd>(ex));
+  float t = p + eps;
+  Y[lane] = t;
+  for (int st = 1; st < steps; ++st) {  // odd: column step, even: row step
+    const float den = ((st & 1) ? col_sum<N>(t) : row_reduce<N, OpAdd>(t)) + eps;
+    t = t * __builtin_amdgcn_rcpf(den);
+    Y[st * 64 + lane] = t;
+    D[st * 64 + lane] = den;
+  }
+  float gr = live ? ld_any(g_out, idx, g_dt) : 0.f;
+  for (int st = steps - 1; st >= 1; --st) {
+    const float y = Y[st * 64 + lane];
+    const float gy = gr * y;
+    const float dot = (st & 1) ? col_sum<N>(gy) : row_reduce<N, OpAdd>(gy);
+    gr = (gr - dot) * __builtin_amdgcn_rcpf(D[st * 64 + lane]);
+  }
+  const float gm = p * (gr - row_reduce<N, OpAdd>(gr * p));
+  if (live) st_any(g_in, idx, gi_dt, gm);
+}
+
 hipError_t launch_sinkhorn_bwd(const void* m_in, int in_dtype, const void* g_out, int g_dtype,
                                void* g_in, int gi_dtype, int64_t batch, int n, int iters,
                                float eps, hipStream_t s) {
+  if (n == 2 || n == 4 || n == 8) {
+    const int steps = 2 * (iters > 1 ? iters : 1);
+    const size_t lds = (size_t)2 * steps * 64 * sizeof(float);
+    const int64_t blocks = (batch * n * n + 63) / 64;
+    switch (n) {
+      case 2: hipLaunchKernelGGL(sinkhorn_bwd_lanes_kernel<2>, dim3((unsigned)blocks), dim3(64), lds, s, m_in, in_dtype, g_out, g_dtype, g_in, gi_dtype, batch, iters, eps); break;
+      case 4: hipLaunchKernelGGL(sinkhorn_bwd_lanes_kernel<4>, dim3((unsigned)blocks), dim3(64), lds, s, m_in, in_dtype, g_out, g_dtype, g_in, gi_dtype, batch, iters, eps); break;
+      default: hipLaunchKernelGGL(sinkhorn_bwd_lanes_kernel<8>, dim3((unsigned)blocks), dim3(64), lds, s, m_in, in_dtype, g_out, g_dtype, g_in, gi_dtype, batch, iters, eps); break;
+    }
+    return hipGetLastError();
+  }
   const int G = n * n;
   const int per = 256 / G;
   const int64_t blocks = (batch + per - 1) / per;

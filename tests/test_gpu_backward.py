@@ -99,6 +99,22 @@ def test_sinkhorn_bwd_vs_autograd(dev, n, iters):
     assert maxrel(mr.grad.float(), got) <= 1e-4
 
 
+@pytest.mark.parametrize("n,iters", [(4, 64), (8, 40), (3, 30)])
+def test_sinkhorn_bwd_long_schedules(dev, n, iters):
+    g = torch.Generator().manual_seed(n + iters)
+    m = torch.randn(33, n, n, generator=g)
+    gy = torch.randn(33, n, n, generator=g)
+    mr = m.double().requires_grad_(True)
+    R.sinkhorn(mr, iters, 1e-6).backward(gy.double())
+    got = _ops.sinkhorn_bwd(m.to(dev), gy.to(dev), iters, 1e-6)
+    assert maxrel(mr.grad.float(), got) <= 1e-4
+
+
+def test_sinkhorn_bwd_iteration_limit(dev):
+    with pytest.raises(RuntimeError, match="iters must be"):
+        _ops.sinkhorn_bwd(torch.zeros(2, 3, 3, device=dev), torch.zeros(2, 3, 3, device=dev), 31, 1e-6)
+
+
 def test_sinkhorn_bwd_bf16_io(dev):
     g = torch.Generator().manual_seed(3)
     m = (torch.randn(300, 4, 4, generator=g) * 2).to(torch.bfloat16)
