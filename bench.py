@@ -16,8 +16,11 @@ flush before each kernel) and plain torch copy / sum kernels over 1 GiB
 (`hbm_calibration`) are reported beside it.
 
 Also printed in the JSON line: roofline of the dominant (post) kernel against
-8 TB/s, the CPU oracle baseline (bounded sample, host cores), and the e2e
-MiniMind-3-mHC prefill tokens/s (config 3).
+8 TB/s, the CPU oracle baseline (bounded sample, host cores), the e2e
+MiniMind-3-mHC prefill tokens/s (config 3), and `backward`: the four backward
+launches of one connection at config 2 (post, Sinkhorn, per-token pre phase,
+weight gradients), each against its algorithmic bytes, plus the fwd + bwd
+tokens/s of the connection (F excluded).
 
 `roofline.traffic` is the measured HBM traffic of that kernel per launch:
 FETCH_SIZE + WRITE_SIZE from two rocprofv3 --pmc passes over `--traffic`
@@ -162,6 +165,93 @@ def bench_mhc(steps: int, warmup: int, sets: int = 4):
     c_post = [a_.elapsed_time(b_) for a_, b_ in cold["post"]]
     del flush
     return steady, dict(t_pre=sum(c_pre) / len(c_pre), t_post=sum(c_post) / len(c_post))
+
+
+def backward_bytes(n: int, C: int, M: int, s: int = 2):
+    """Compulsory HBM bytes per backward launch (bf16 tensors, fp32 saved
+    inv_rms / mixes_raw / g_raw; FD = 2n + n*n):
+      post_bwd     read g_out, x (n*C each), F (C), h_post, h_res; write g_x (n*C), g_F (C),
+                   g_h_post, g_h_res
+      sinkhorn_bwd read h_res_raw, g_h_res (n*n each); write g_h_res_raw
+      pre_bwd      read x (n*C), g_sub (C), g_h_post, g_h_res_raw, inv_rms, mixes_raw (FD fp32),
+                   phi once; write g_x (n*C), g_raw (FD fp32)
+      weights      read x (n*C), inv_rms, mixes_raw, g_raw; write g_phi once"""
+    fd = 2 * n + n * n
+    h = n + n * n
+    post = M * ((3 * n * C + 2 * C) * s + 2 * h * s)
+    sk = M * 3 * n * n * s
+    pre = M * ((2 * n * C + C + h) * s + 4 + 8 * fd) + n * C * fd * s
+    wts = M * (n * C * s + 4 + 8 * fd) + n * C * fd * s
+    return {"post_bwd": post, "sinkhorn_bwd": sk, "pre_bwd": pre, "pre_bwd_weights": wts}
+
+
+def bench_backward(reps: int = 20, sets: int = 4):
+    """Steady-state times of the four backward launches of one mHC connection
+    at config 2 (bf16, 16384 tokens, n = 4, C = 768), rotating `sets` input
+    sets as bench_mhc does, with the saved tensors of a real forward."""
+    import torch
+    from model import _hip as H, _ops
+
+    dev = torch.device("cuda:0")
+    n, C, M = N_STREAMS, C_DIM, TOKENS
+    bf = torch.bfloat16
+    g = torch.Generator().manual_seed(2)
+    phi = (torch.randn(n * C, 2 * n + n * n, generator=g) * 0.02).to(bf).to(dev)
+    a = torch.tensor(0.01, dtype=bf, device=dev)
+    b0 = torch.zeros(n, dtype=bf, device=dev)
+    br = torch.eye(n, dtype=bf, device=dev)
+    packed = _ops.PhiPack(H.MODE_FULL).get(phi, n, C)
+    S = []
+    for _ in range(sets):
+        x = torch.randn(M, n * C, generator=g).to(bf).to(dev)
+        o = _ops.pre_full(x.view(1, M, n * C), phi, packed, a, b0, a, b0, a, br, n, C, 2.0, 1e-6,
+                          1e-6, ITERS, 1e-6, want_raw=True, want_saved=True)
+        f = torch.randn(M, C, generator=g).to(bf).to(dev)
+        gout = torch.randn(M, n * C, generator=g).to(bf).to(dev)
+        gsub = torch.randn(M, C, generator=g).to(bf).to(dev)
+        S.append(dict(x=x, o=o, f=f, gout=gout, gsub=gsub))
+    for s in S:  # the intermediate gradients each later kernel consumes
+        _, s["ghr"], s["ghp"], _ = _ops.post_bwd(s["x"], s["o"]["h_res"], s["o"]["h_post"], s["f"],
+                                                 n, C, s["gout"])
+        s["graw_res"] = _ops.sinkhorn_bwd(s["o"]["h_res_raw"], s["ghr"], ITERS, 1e-6, out_dtype=bf)
+        _, s["graw"] = _ops.pre_bwd(s["x"], phi, (a, a, a), (b0, b0, br), s["o"]["inv_rms"],
+                                    s["o"]["mixes_raw"], n, C, H.MODE_FULL, 2.0, 1e-6, s["gsub"],
+                                    None, s["ghp"], s["graw_res"])
+    ops = {
+        "post_bwd": lambda s: _ops.post_bwd(s["x"], s["o"]["h_res"], s["o"]["h_post"], s["f"], n,
+                                            C, s["gout"]),
+        "sinkhorn_bwd": lambda s: _ops.sinkhorn_bwd(s["o"]["h_res_raw"], s["ghr"], ITERS, 1e-6,
+                                                    out_dtype=bf),
+        "pre_bwd": lambda s: _ops.pre_bwd(s["x"], phi, (a, a, a), (b0, b0, br), s["o"]["inv_rms"],
+                                          s["o"]["mixes_raw"], n, C, H.MODE_FULL, 2.0, 1e-6,
+                                          s["gsub"], None, s["ghp"], s["graw_res"]),
+        "pre_bwd_weights": lambda s: _ops.pre_bwd_weights(s["x"], s["o"]["inv_rms"],
+                                                          s["o"]["mixes_raw"], s["graw"], phi,
+                                                          (a, a, a), n, C, H.MODE_FULL),
+    }
+    nbytes = backward_bytes(n, C, M)
+    out = {}
+    for name, fn in ops.items():
+        for s in S:
+            fn(s)
+        _sync()
+        e0 = torch.cuda.Event(enable_timing=True)
+        e1 = torch.cuda.Event(enable_timing=True)
+        _queue_ahead()
+        e0.record()
+        for _ in range(reps):
+            for s in S:
+                fn(s)
+        e1.record()
+        _sync()
+        ms = e0.elapsed_time(e1) / (reps * sets)
+        gbs = nbytes[name] / (ms * 1e-3) / 1e9
+        out[name] = {"ms": round(ms, 5), "GBps": round(gbs, 1), "frac": round(gbs / HBM_PEAK_GBS, 4),
+                     "algorithmic_bytes": nbytes[name]}
+    out["total_ms"] = round(sum(v["ms"] for v in out.values()), 5)
+    out["note"] = ("timings include each launch's own small torch allocations (outputs, "
+                   "workspace); the weights entry is two launches (partials + reduction)")
+    return out
 
 
 TRAFFIC_FILE = ROOT / "profiles" / "traffic_mhc_fwd_c2.txt"
@@ -377,6 +467,9 @@ def main():
                              "tokens_per_s": round(TOKENS / (c_ms * 1e-3), 1)},
         "hbm_calibration": hbm_calibration(),
     }
+    bw = bench_backward()
+    bw["fwd_bwd_tokens_per_s"] = round(TOKENS / ((step_ms + bw["total_ms"]) * 1e-3), 1)
+    line["backward"] = bw
     if not args.no_e2e:
         line["e2e_prefill"] = e2e_prefill()
     if not args.no_cpu:
