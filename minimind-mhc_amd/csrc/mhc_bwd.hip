@@ -483,10 +483,12 @@ constexpr int kWRow = kWTok * 2 + 16;    // LDS row stride in bytes (64 bf16 + p
 
 template <int NTF>  // 16-wide feature tiles
 __global__ __launch_bounds__(512) void weights_mfma_kernel(WeightsArgs a, int64_t per) {
+  constexpr int F16 = NTF * 16;
+  constexpr int UPT = F16 / 16;  // (token pair, feature) items per thread: 32 * F16 / 512
   __shared__ __attribute__((aligned(16))) unsigned char s_x[kWCols * kWRow];
-  __shared__ __attribute__((aligned(16))) unsigned char s_uh[NTF * 16 * kWRow];
-  __shared__ __attribute__((aligned(16))) unsigned char s_ul[NTF * 16 * kWRow];
-  __shared__ float s_ab[2][kWTok / 2][NTF * 16];
+  __shared__ __attribute__((aligned(16))) unsigned char s_uh[F16 * kWRow];
+  __shared__ __attribute__((aligned(16))) unsigned char s_ul[F16 * kWRow];
+  __shared__ float s_ab[2][kWTok / 2][F16];
   const int FD = mode_fd(a.mode, a.n);
   const int NC = a.n * a.C;
   const int tid = threadIdx.x;
@@ -500,58 +502,75 @@ __global__ __launch_bounds__(512) void weights_mfma_kernel(WeightsArgs a, int64_
   const int64_t te = tb + per < a.M ? tb + per : a.M;
   const bool ab_slice = blockIdx.x == 0;
 
-  const int tp = tid & 31;  // token pair (tokens 2tp, 2tp + 1 of the step)
-  const int kc = tid >> 5;  // 8-column group (columns k0 + 8kc .. + 7)
+  const int tp = tid & 31;  // x: token pair (tokens 2tp, 2tp + 1 of the step)
+  const int kc = tid >> 5;  // x: 8-column group (columns k0 + 8kc .. + 7)
   const int col = k0 + 8 * kc;
-  constexpr int UPT = (kWTok / 2) * NTF * 16 / 512;  // u pairs per thread per step
-  float sb[UPT > 0 ? UPT : 1], sa[UPT > 0 ? UPT : 1];
-#pragma unroll
-  for (int u = 0; u < (UPT > 0 ? UPT : 1); ++u) { sb[u] = 0.f; sa[u] = 0.f; }
+  const bool okc = col < NC;
 
+  // Everything one step reads from memory; the next step's copy is loaded
+  // while the current step's MFMAs run.
+  struct Step {
+    U32x4 xa, xb;
+    float ga[UPT], gb[UPT], ia[UPT], ib[UPT], ma[UPT], mb[UPT];
+  };
+  auto load_step = [&](int64_t t, Step& st) {
+    const int valid = t < te ? (int)(te - t < kWTok ? te - t : kWTok) : 0;
+    const auto rs = make_rsrc(static_cast<const uint16_t*>(a.x) + (t < te ? t : 0) * NC,
+                              (uint32_t)valid * NC * 2u);
+    st.xa = buf_load16(rs, okc ? (uint32_t)((2 * tp) * NC + col) * 2u : kBufOob);
+    st.xb = buf_load16(rs, okc ? (uint32_t)((2 * tp + 1) * NC + col) * 2u : kBufOob);
+#pragma unroll
+    for (int u = 0; u < UPT; ++u) {
+      const int idx = tid + 512 * u;
+      const int f = idx % F16;  // feature-major: consecutive threads read consecutive features
+      const int pp = idx / F16;
+      const int64_t ta = t + 2 * pp;
+      const bool fa = f < FD && ta < te;
+      const bool fb = f < FD && ta + 1 < te;
+      st.ga[u] = fa ? a.g_raw[ta * FD + f] : 0.f;
+      st.gb[u] = fb ? a.g_raw[(ta + 1) * FD + f] : 0.f;
+      st.ia[u] = fa ? a.inv_rms[ta] : 0.f;
+      st.ib[u] = fb ? a.inv_rms[ta + 1] : 0.f;
+      st.ma[u] = fa && ab_slice ? a.mixes[ta * FD + f] : 0.f;
+      st.mb[u] = fb && ab_slice ? a.mixes[(ta + 1) * FD + f] : 0.f;
+    }
+  };
+  float sb[UPT], sa[UPT];
+#pragma unroll
+  for (int u = 0; u < UPT; ++u) { sb[u] = 0.f; sa[u] = 0.f; }
   f32x4_t acc[NTF];
 #pragma unroll
   for (int ft = 0; ft < NTF; ++ft) acc[ft] = f32x4_t{0.f, 0.f, 0.f, 0.f};
 
+  Step cur;
+  load_step(tb, cur);
   for (int64_t t = tb; t < te; t += kWTok) {
-    const int valid = (int)(te - t < kWTok ? te - t : kWTok);
-    const auto rs = make_rsrc(static_cast<const uint16_t*>(a.x) + t * NC, (uint32_t)valid * NC * 2u);
-    const bool okc = col < NC;
-    const U32x4 xa = buf_load16(rs, okc ? (uint32_t)((2 * tp) * NC + col) * 2u : kBufOob);
-    const U32x4 xb = buf_load16(rs, okc ? (uint32_t)((2 * tp + 1) * NC + col) * 2u : kBufOob);
-    // u = inv * g_raw for (token pair, feature), hi / lo bf16 pairs
+    // u = inv * g_raw as hi / lo bf16 token pairs, [feature][token]
 #pragma unroll
     for (int u = 0; u < UPT; ++u) {
       const int idx = tid + 512 * u;
-      const int pp = idx & 31;
-      const int f = idx >> 5;
-      float va = 0.f, vb = 0.f;
-      const int64_t ta = t + 2 * pp;
-      if (f < FD) {
-        if (ta < te) {
-          const float gr = a.g_raw[ta * FD + f];
-          va = a.inv_rms[ta] * gr;
-          if (ab_slice) { sb[u] += gr; sa[u] = fmaf(gr, a.mixes[ta * FD + f], sa[u]); }
-        }
-        if (ta + 1 < te) {
-          const float gr = a.g_raw[(ta + 1) * FD + f];
-          vb = a.inv_rms[ta + 1] * gr;
-          if (ab_slice) { sb[u] += gr; sa[u] = fmaf(gr, a.mixes[(ta + 1) * FD + f], sa[u]); }
-        }
-      }
+      const int f = idx % F16;
+      const int pp = idx / F16;
+      const float va = cur.ia[u] * cur.ga[u];
+      const float vb = cur.ib[u] * cur.gb[u];
       const uint32_t hi = pack_bf16x2(va, vb);
       *reinterpret_cast<uint32_t*>(s_uh + f * kWRow + pp * 4) = hi;
-      *reinterpret_cast<uint32_t*>(s_ul + f * kWRow + pp * 4) =
-          pack_bf16x2(va - bf16lo(hi), vb - bf16hi(hi));
+      *reinterpret_cast<uint32_t*>(s_ul + f * kWRow + pp * 4) = pack_bf16x2(va - bf16lo(hi), vb - bf16hi(hi));
+      if (ab_slice) {
+        sb[u] += cur.ga[u] + cur.gb[u];
+        sa[u] = fmaf(cur.gb[u], cur.mb[u], fmaf(cur.ga[u], cur.ma[u], sa[u]));
+      }
     }
     // x tile transposed: column 8kc + e, tokens (2tp, 2tp + 1) in one dword
 #pragma unroll
     for (int e = 0; e < 8; ++e) {
-      const uint32_t wa = xa.v[e >> 1];
-      const uint32_t wb = xb.v[e >> 1];
+      const uint32_t wa = cur.xa.v[e >> 1];
+      const uint32_t wb = cur.xb.v[e >> 1];
       const uint32_t d = (e & 1) ? ((wa >> 16) | (wb & 0xffff0000u)) : ((wa & 0xffffu) | (wb << 16));
       *reinterpret_cast<uint32_t*>(s_x + (8 * kc + e) * kWRow + tp * 4) = d;
     }
     __syncthreads();
+    load_step(t + kWTok, cur);  // next step's loads fly over the MFMAs
 #pragma unroll
     for (int ks = 0; ks < kWTok / 32; ++ks) {
       const bf16x8_t av = *reinterpret_cast<const bf16x8_t*>(s_x + (16 * wave + r) * kWRow + (32 * ks + 8 * g) * 2);
@@ -574,12 +593,12 @@ __global__ __launch_bounds__(512) void weights_mfma_kernel(WeightsArgs a, int64_
       const int f = 16 * ft + r;
       if (k < NC && f < FD) W[(int64_t)k * FD + f] = acc[ft][j];
     }
-  if (ab_slice) {  // alpha / bias partials: sum the 32 token-pair lanes of each feature
+  if (ab_slice) {  // alpha / bias partials: sum the 32 token-pair slots of each feature
 #pragma unroll
     for (int u = 0; u < UPT; ++u) {
       const int idx = tid + 512 * u;
-      s_ab[0][idx & 31][idx >> 5] = sb[u];
-      s_ab[1][idx & 31][idx >> 5] = sa[u];
+      s_ab[0][idx / F16][idx % F16] = sb[u];
+      s_ab[1][idx / F16][idx % F16] = sa[u];
     }
     __syncthreads();
     float* ab = a.work + (int64_t)gridDim.y * NC * FD + (int64_t)rng * 2 * FD;
