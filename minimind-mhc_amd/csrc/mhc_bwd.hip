@@ -437,8 +437,18 @@ __global__ __launch_bounds__(256) void weights_reduce_kernel(WeightsArgs a, int 
   const int64_t q = (int64_t)blockIdx.x * 256 + threadIdx.x;
   if (q < NC * FD) {
     const int f = (int)(q % FD);
-    float acc = 0.f;
-    for (int r = 0; r < R; ++r) acc += a.work[(int64_t)r * NC * FD + q];
+    const int64_t stride = NC * FD;
+    // four independent partial sums keep four loads in flight
+    float s0 = 0.f, s1 = 0.f, s2 = 0.f, s3 = 0.f;
+    int r = 0;
+    for (; r + 4 <= R; r += 4) {
+      s0 += a.work[(int64_t)r * stride + q];
+      s1 += a.work[(int64_t)(r + 1) * stride + q];
+      s2 += a.work[(int64_t)(r + 2) * stride + q];
+      s3 += a.work[(int64_t)(r + 3) * stride + q];
+    }
+    for (; r < R; ++r) s0 += a.work[(int64_t)r * stride + q];
+    const float acc = (s0 + s1) + (s2 + s3);
     st_any(a.g_phi, q, a.phi_dtype, acc * ld_any(a.alpha[seg_of(f, n)], 0, a.param_dtype));
   }
   if (blockIdx.x == 0) {
