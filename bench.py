@@ -274,10 +274,11 @@ def read_traffic():
     return vals if len(vals) == 4 else None
 
 
-def traffic_passes(vector_pre: bool = False):
+def traffic_passes(vector_pre: bool = False, extra: bool = False):
     """What the FETCH_SIZE / WRITE_SIZE counter passes run: a plain copy of
     1 GiB -> 1 GiB and a plain sum over 1 GiB (known bytes, to calibrate the
-    counters), then one pre and one post launch at config 2 on fresh data."""
+    counters), then one pre and one post launch at config 2 on fresh data.
+    With `extra`, also one launch of each other MFMA kernel (see below)."""
     import torch
     from model import _hip as H, _ops
 
@@ -306,6 +307,31 @@ def traffic_passes(vector_pre: bool = False):
         # the same pre phase on the generic VALU kernel (projection as fp32
         # FMAs, no MFMA), for the MFMA-vs-VALU comparison
         _ops.pre_full(x, phi, None, a, b0, a, b0, a, br, n, C, 2.0, 1e-6, 1e-6, ITERS, 1e-6)
+        _sync()
+    if extra:
+        # one launch of each other MFMA kernel, for the MFMA counter pass:
+        # the config-2 backward (per-token pre phase, weight gradients) and
+        # the config-5 pre phase (n = 8, 8192 tokens)
+        o2 = _ops.pre_full(x, phi, packed, a, b0, a, b0, a, br, n, C, 2.0, 1e-6, 1e-6, ITERS, 1e-6,
+                           want_raw=True, want_saved=True)
+        gsub = torch.randn(M, C, generator=g).to(torch.bfloat16).to(dev)
+        ghp = torch.randn(M, n, generator=g).to(torch.bfloat16).to(dev)
+        ghr = torch.randn(M, n * n, generator=g).to(torch.bfloat16).to(dev)
+        x2 = x.view(M, n * C)
+        _, graw = _ops.pre_bwd(x2, phi, (a, a, a), (b0, b0, br), o2["inv_rms"], o2["mixes_raw"], n,
+                               C, H.MODE_FULL, 2.0, 1e-6, gsub, None, ghp, ghr)
+        _ops.pre_bwd_weights(x2, o2["inv_rms"], o2["mixes_raw"], graw, phi, (a, a, a), n, C,
+                             H.MODE_FULL)
+        _sync()
+        del x, x2, f, o, o2, gsub
+        n8, M8 = 8, 8192
+        x8 = torch.randn(1, M8, n8 * C, generator=g).to(torch.bfloat16).to(dev)
+        phi8 = (torch.randn(n8 * C, 2 * n8 + n8 * n8, generator=g) * 0.02).to(torch.bfloat16).to(dev)
+        b08 = torch.zeros(n8, dtype=torch.bfloat16, device=dev)
+        br8 = torch.eye(n8, dtype=torch.bfloat16, device=dev)
+        pk8 = _ops.PhiPack(H.MODE_FULL).get(phi8, n8, C)
+        _sync()
+        _ops.pre_full(x8, phi8, pk8, a, b08, a, b08, a, br8, n8, C, 2.0, 1e-6, 1e-6, ITERS, 1e-6)
         _sync()
 
 
@@ -403,6 +429,9 @@ def main():
                     help="run the counter-calibration and config-2 launches once, print nothing")
     ap.add_argument("--vector-pre", action="store_true",
                     help="with --traffic: also run the pre phase on the generic VALU kernel")
+    ap.add_argument("--mfma-kernels", action="store_true",
+                    help="with --traffic: also run the config-2 backward MFMA kernels and the "
+                         "config-5 (n = 8) pre phase once")
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py: this build measures one GPU only (the mHC forward is per-token and "
@@ -415,7 +444,7 @@ def main():
         sys.exit(1)
 
     if args.traffic:
-        traffic_passes(args.vector_pre)
+        traffic_passes(args.vector_pre, args.mfma_kernels)
         return
 
     r, rc = bench_mhc(args.steps, args.warmup)
@@ -456,6 +485,12 @@ def main():
                          "frac": round(pre_gbs / HBM_PEAK_GBS, 4),
                          "traffic": round(tr["pre_fetch"] + tr["pre_write"]) if tr else None,
                          "algorithmic_bytes_per_launch": pre_b},
+        "pre_mfma": {"flops_per_launch": 2 * TOKENS * N_STREAMS * C_DIM * 32,
+                     "achieved_tflops": round(2 * TOKENS * N_STREAMS * C_DIM * 32 / (r["t_pre"] * 1e-3) / 1e12, 1),
+                     "peak_tflops": 2500.0,
+                     "frac": round(2 * TOKENS * N_STREAMS * C_DIM * 32 / (r["t_pre"] * 1e-3) / 2.5e15, 4),
+                     "source": "flops from SQ_INSTS_VALU_MFMA_MOPS_BF16 x 512 "
+                               "(profiles/mfma_util_and_traffic.txt), time from this run"},
         "step_roofline": {"achieved": round(total_gbs, 1), "frac": round(total_gbs / HBM_PEAK_GBS, 4),
                           "algorithmic_bytes_per_step": pre_b + post_b},
         "kernels": {"pre_ms": round(r["t_pre"], 5), "post_ms": round(r["t_post"], 5),
