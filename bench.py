@@ -16,11 +16,14 @@ flush before each kernel) and plain torch copy / sum kernels over 1 GiB
 (`hbm_calibration`) are reported beside it.
 
 Also printed in the JSON line: roofline of the dominant (post) kernel against
-8 TB/s, the CPU oracle baseline (bounded sample, host cores), the e2e
-MiniMind-3-mHC prefill tokens/s (config 3), and `backward`: the four backward
-launches of one connection at config 2 (post, Sinkhorn, per-token pre phase,
-weight gradients), each against its algorithmic bytes, plus the fwd + bwd
-tokens/s of the connection (F excluded).
+8 TB/s, the CPU oracle baseline (bounded sample, host cores; config 1 and the
+fp32 sample beside it), `backward`: the four backward launches of one
+connection at config 2 (post, Sinkhorn, per-token pre phase, weight
+gradients), each against its algorithmic bytes, plus the fwd + bwd tokens/s of
+the connection (F excluded); `other_configs`: the same kernel pair at config
+5's n = 8 shape and config 4's 64-token shape; and the end-to-end model
+figures: `e2e_prefill` (config 3), `e2e_decode` (config 4, eager and
+HIP-graph replay) and `e2e_prefill_moe` (config 5).
 
 `roofline.traffic` is the measured HBM traffic of that kernel per launch:
 FETCH_SIZE + WRITE_SIZE from two rocprofv3 --pmc passes over `--traffic`
@@ -78,7 +81,8 @@ def _queue_ahead():
         torch.cuda._sleep(20_000_000)
 
 
-def bench_mhc(steps: int, warmup: int, sets: int = 4):
+def bench_mhc(steps: int, warmup: int, sets: int = 4, n: int = N_STREAMS, C: int = C_DIM,
+              M: int = TOKENS, cold: bool = True):
     """Steady-state kernel times over `sets` distinct input sets.
 
     Each step runs the pre kernel on every set, then the post kernel on every
@@ -92,7 +96,6 @@ def bench_mhc(steps: int, warmup: int, sets: int = 4):
     from model import _hip as H, _ops
 
     dev = torch.device("cuda:0")
-    n, C, M = N_STREAMS, C_DIM, TOKENS
     g = torch.Generator().manual_seed(0)
     xs = [torch.randn(1, M, n * C, generator=g).to(torch.bfloat16).to(dev) for _ in range(sets)]
     fs = [torch.randn(M, C, generator=g).to(torch.bfloat16).to(dev) for _ in range(sets)]
@@ -101,7 +104,7 @@ def bench_mhc(steps: int, warmup: int, sets: int = 4):
     b0 = torch.zeros(n, dtype=torch.bfloat16, device=dev)
     br = torch.eye(n, dtype=torch.bfloat16, device=dev)
     packed = _ops.PhiPack(H.MODE_FULL).get(phi, n, C)
-    assert packed is not None, "config 2 must take the MFMA kernel"
+    assert packed is not None, "configs 2, 4 and 5 take the MFMA kernels"
 
     def pre(s):
         return _ops.pre_full(xs[s], phi, packed, a, b0, a, b0, a, br, n, C, 2.0, 1e-6, 1e-6,
@@ -141,6 +144,8 @@ def bench_mhc(steps: int, warmup: int, sets: int = 4):
     t_post = [a_.elapsed_time(b_) / sets for a_, b_ in rec["post"]]
     steady = dict(t_pre=sum(t_pre) / len(t_pre), t_post=sum(t_post) / len(t_post),
                   t_pre_min=min(t_pre), t_post_min=min(t_post), wall=wall)
+    if not cold:
+        return steady, None
 
     # cold, clean cache: read-only 1 GiB flush before each kernel
     flush = torch.ones(256 * 1024 * 1024, dtype=torch.float32, device=dev)
@@ -358,34 +363,58 @@ def hbm_calibration(reps: int = 10):
     return out
 
 
+def _cpu_rate(fn, budget_s: float):
+    """Median seconds per call of fn over ~budget_s (at least 3 calls, after one warm-up)."""
+    fn()
+    times = []
+    t_end = time.perf_counter() + budget_s
+    while time.perf_counter() < t_end or len(times) < 3:
+        t0 = time.perf_counter()
+        fn()
+        times.append(time.perf_counter() - t0)
+    times.sort()
+    return times[len(times) // 2], len(times)
+
+
 def cpu_baseline(budget_s: float = 12.0):
-    """The oracle (torch CPU restatement of the reference _forward_ref) on a
-    bounded sample of the config-2 workload: 512 tokens per call, bf16, F a
-    fixed tensor; repeated until ~budget_s of CPU time; median tokens/s."""
+    """The oracle (torch CPU restatement of the reference _forward_ref) on the
+    host cores.  Headline: a bounded sample of the config-2 workload, 512
+    tokens per call, bf16, F a fixed tensor, repeated for ~budget_s; median
+    tokens/s.  Beside it, ~budget_s / 3 each: the same sample in fp32, and
+    config 1 itself (256 tokens, fp32, F = Linear(768, 768) with N(0, 0.02)
+    weights, inside the timed call), each with its algorithmic GB/s."""
     import torch
     from oracle import mhc_ref as R
     from tests._util import make_params
 
     cores = min(16, os.cpu_count() or 1)
     torch.set_num_threads(cores)
-    n, C, m = N_STREAMS, C_DIM, 512
+    n, C = N_STREAMS, C_DIM
     g = torch.Generator().manual_seed(0)
-    x = torch.randn(1, m, n * C, generator=g).to(torch.bfloat16)
-    fz = torch.randn(1, m, C, generator=g).to(torch.bfloat16)
-    p = make_params("full", n, C, torch.bfloat16, g, stress=False)
-    times = []
-    t_end = time.perf_counter() + budget_s
+    res = {}
     with torch.inference_mode():
-        R.mhc_full_forward(x, p, lambda z: fz, n, C, sinkhorn_iters=ITERS)
-        while time.perf_counter() < t_end or len(times) < 3:
-            t0 = time.perf_counter()
-            R.mhc_full_forward(x, p, lambda z: fz, n, C, sinkhorn_iters=ITERS)
-            times.append(time.perf_counter() - t0)
-    times.sort()
-    med = times[len(times) // 2]
-    return {"value": round(m / med, 1), "unit": "tokens/s", "cores": cores, "kind": "port",
+        for key, dt, m, budget in (("c2_sample_bf16", torch.bfloat16, 512, budget_s),
+                                   ("c2_sample_fp32", torch.float32, 512, budget_s / 3),
+                                   ("c1_fp32", torch.float32, 256, budget_s / 3)):
+            x = torch.randn(1, m, n * C, generator=g).to(dt)
+            p = make_params("full", n, C, dt, g, stress=False)
+            if key == "c1_fp32":
+                lin = torch.nn.Linear(C, C, bias=False)
+                torch.nn.init.normal_(lin.weight, 0.0, 0.02, generator=g)
+                f = lin
+            else:
+                fz = torch.randn(1, m, C, generator=g).to(dt)
+                f = (lambda z, fz=fz: fz)
+            med, calls = _cpu_rate(lambda: R.mhc_full_forward(x, p, f, n, C, sinkhorn_iters=ITERS),
+                                   budget)
+            nbytes = sum(algorithmic_bytes(n, C, m, s=x.element_size()))
+            res[key] = {"tokens_per_s": round(m / med, 1), "GBps": round(nbytes / med / 1e9, 2),
+                        "tokens": m, "calls": calls}
+    head = res["c2_sample_bf16"]
+    return {"value": head["tokens_per_s"], "unit": "tokens/s", "cores": cores, "kind": "port",
             "sample": f"oracle mhc_full_forward (reference _forward_ref restated), bf16, "
-                      f"{m} tokens x n={n} x C={C}, F fixed, median of {len(times)} calls"}
+                      f"512 tokens x n={n} x C={C}, F fixed, median of {head['calls']} calls",
+            "runs": res}
 
 
 def e2e_prefill(steps: int = 5, warmup: int = 2):
@@ -393,13 +422,10 @@ def e2e_prefill(steps: int = 5, warmup: int = 2):
     head_dim 96, SwiGLU 2048, vocab 6400, n=4, bf16, N(0, 0.02) init;
     prefill B=8, T=1024 (logits for every position, as the reference forward)."""
     import torch
-    from model.model_minimind import MiniMindConfig, MiniMindForCausalLM, init_normal_
+    from model.model_minimind import MiniMindForCausalLM, init_normal_
 
     dev = torch.device("cuda:0")
-    cfg = MiniMindConfig(hidden_size=768, num_hidden_layers=8, num_attention_heads=8,
-                         num_key_value_heads=4, head_dim=96, intermediate_size=2048,
-                         rope_theta=1e6, vocab_size=6400, use_mhc=1, mhc_residual_expansion=4,
-                         max_position_embeddings=4096)
+    cfg = _dense_config()
     torch.manual_seed(0)
     model = init_normal_(MiniMindForCausalLM(cfg)).to(torch.bfloat16).to(dev).eval()
     g = torch.Generator().manual_seed(1)
@@ -416,6 +442,151 @@ def e2e_prefill(steps: int = 5, warmup: int = 2):
     return {"value": round(ids.numel() / dt, 1), "unit": "tokens/s", "ms_per_forward": round(dt * 1e3, 3),
             "config": "C3: 8 layers, hidden 768, 8q/4kv heads, head_dim 96, SwiGLU 2048, vocab 6400, "
                       "n=4, bf16, B=8 T=1024, 16 mHC connections + StreamExpand + MHCHead"}
+
+
+def isolated_configs(steps: int, warmup: int):
+    """The isolated pre + post kernel pair at the other BASELINE shapes:
+    config 5's n = 8 connection (B=4, T=2048: 8192 tokens, phi [6144, 80],
+    8x8 Sinkhorn) and config 4's decode shape (64 tokens, n = 4), where the
+    pair is launch-bound; timed as bench_mhc times config 2."""
+    out = {}
+    for key, n, M, sets in (("c5_n8_M8192", 8, 8192, 4), ("c4_n4_M64", 4, 64, 8)):
+        r, _ = bench_mhc(steps, warmup, sets=sets, n=n, M=M, cold=False)
+        pre_b, post_b = algorithmic_bytes(n, C_DIM, M)
+        t = r["t_pre"] + r["t_post"]
+        out[key] = {"n": n, "C": C_DIM, "tokens": M,
+                    "pre_ms": round(r["t_pre"], 5), "post_ms": round(r["t_post"], 5),
+                    "pre_GBps": round(pre_b / (r["t_pre"] * 1e-3) / 1e9, 1),
+                    "post_GBps": round(post_b / (r["t_post"] * 1e-3) / 1e9, 1),
+                    "step_frac": round((pre_b + post_b) / (t * 1e-3) / 1e9 / HBM_PEAK_GBS, 4),
+                    "tokens_per_s": round(M / (t * 1e-3), 1)}
+    return out
+
+
+def _dense_config(**kw):
+    from model.model_minimind import MiniMindConfig
+    base = dict(hidden_size=768, num_hidden_layers=8, num_attention_heads=8, num_key_value_heads=4,
+                head_dim=96, intermediate_size=2048, rope_theta=1e6, vocab_size=6400, use_mhc=1,
+                mhc_residual_expansion=4, max_position_embeddings=4096)
+    base.update(kw)
+    return MiniMindConfig(**base)
+
+
+def e2e_decode(steps: int = 30, warmup: int = 5, batch: int = 64, kv_len: int = 2048):
+    """the config-3 model decoding one token per sequence
+    per step for 64 sequences over a KV cache of 2048 positions per layer,
+    filled with seeded N(0, 1) bf16.  Greedy: each step's ids are the argmax
+    of the previous step's logits, kept on the device (no host sync inside
+    the timed loop).  The cache is held at 2048 entries (each step's new K/V
+    is not appended), so every step does the same work.
+
+    Two timings: eager (one host launch per op) and the same step captured
+    once in a HIP graph and replayed (torch.cuda.CUDAGraph), which removes
+    the host launch cost that dominates at 64 tokens.  `graph_vs_eager`
+    compares the graph's ids and logits with the eager run's over the same
+    steps."""
+    import torch
+    from model.model_minimind import MiniMindForCausalLM, init_normal_
+
+    dev = torch.device("cuda:0")
+    cfg = _dense_config()
+    torch.manual_seed(0)
+    model = init_normal_(MiniMindForCausalLM(cfg)).to(torch.bfloat16).to(dev).eval()
+    g = torch.Generator().manual_seed(3)
+    kv = []
+    for _ in range(cfg.num_hidden_layers):
+        shape = (batch, kv_len, cfg.num_key_value_heads, cfg.head_dim)
+        kv.append((torch.randn(shape, generator=g).to(torch.bfloat16).to(dev),
+                   torch.randn(shape, generator=g).to(torch.bfloat16).to(dev)))
+    ids0 = torch.randint(0, cfg.vocab_size, (batch, 1), generator=g).to(dev)
+
+    def step(ids):
+        logits = model(ids, past_key_values=kv, use_cache=False).logits
+        return logits, logits[:, -1].argmax(-1, keepdim=True)
+
+    res = {}
+    with torch.inference_mode():
+        ids = ids0.clone()
+        for _ in range(warmup):
+            _, ids = step(ids)
+        _sync()
+        ids = ids0.clone()
+        eager_ids = []
+        t0 = time.perf_counter()
+        for _ in range(steps):
+            logits, ids = step(ids)
+            eager_ids.append(ids)
+        _sync()
+        dt = (time.perf_counter() - t0) / steps
+        eager_last = logits.float()
+        res["eager"] = {"ms_per_step": round(dt * 1e3, 4),
+                        "tokens_per_s": round(batch / dt, 1)}
+
+        static_ids = ids0.clone()
+        side = torch.cuda.Stream()
+        side.wait_stream(torch.cuda.current_stream())
+        with torch.cuda.stream(side):
+            for _ in range(3):
+                step(static_ids)
+        torch.cuda.current_stream().wait_stream(side)
+        graph = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(graph):
+            static_logits, nxt = step(static_ids)
+            static_ids.copy_(nxt)
+        static_ids.copy_(ids0)
+        for _ in range(warmup):
+            graph.replay()
+        _sync()
+        static_ids.copy_(ids0)
+        graph_ids = []
+        t0 = time.perf_counter()
+        for _ in range(steps):
+            graph.replay()
+            graph_ids.append(static_ids.clone())
+        _sync()
+        dt = (time.perf_counter() - t0) / steps
+        res["hip_graph"] = {"ms_per_step": round(dt * 1e3, 4),
+                            "tokens_per_s": round(batch / dt, 1)}
+        same = all(torch.equal(a_, b_) for a_, b_ in zip(eager_ids, graph_ids))
+        res["graph_vs_eager"] = {"ids_equal": bool(same),
+                                 "logits_max_abs_diff": float((static_logits.float()
+                                                               - eager_last).abs().max())}
+    res["value"] = res["hip_graph"]["tokens_per_s"]
+    res["unit"] = "tokens/s"
+    res["config"] = (f"C4: config-3 model, batch {batch}, 1 token per sequence per step, KV cache "
+                     f"{kv_len} per layer (N(0,1) bf16, held fixed), greedy ids on device")
+    return res
+
+
+def e2e_prefill_moe(steps: int = 3, warmup: int = 1):
+    """8 layers, hidden 768, n = 8 streams (phi [6144, 80],
+    8x8 Sinkhorn, 20 iterations), FFN = 8 routed SwiGLU experts of
+    intermediate 1024, top-2 softmax routing, no shared expert; N(0, 0.02)
+    init, bf16; prefill B=4, T=2048.  The expert dispatch is the reference's
+    own loop over experts (a host sync per expert), timed as is."""
+    import torch
+    from model.model_minimind import MiniMindForCausalLM, init_normal_
+
+    dev = torch.device("cuda:0")
+    cfg = _dense_config(mhc_residual_expansion=8, use_moe=True, num_experts=8,
+                        num_experts_per_tok=2, moe_intermediate_size=1024)
+    torch.manual_seed(0)
+    model = init_normal_(MiniMindForCausalLM(cfg)).to(torch.bfloat16).to(dev).eval()
+    g = torch.Generator().manual_seed(4)
+    ids = torch.randint(0, cfg.vocab_size, (4, 2048), generator=g).to(dev)
+    with torch.inference_mode():
+        for _ in range(warmup):
+            model(ids)
+        _sync()
+        t0 = time.perf_counter()
+        for _ in range(steps):
+            model(ids)
+        _sync()
+    dt = (time.perf_counter() - t0) / steps
+    return {"value": round(ids.numel() / dt, 1), "unit": "tokens/s",
+            "ms_per_forward": round(dt * 1e3, 3),
+            "config": "C5: 8 layers, hidden 768, 8q/4kv heads, head_dim 96, n=8, 8 experts top-2, "
+                      "expert intermediate 1024, vocab 6400, bf16, B=4 T=2048"}
 
 
 def main():
@@ -505,8 +676,11 @@ def main():
     bw = bench_backward()
     bw["fwd_bwd_tokens_per_s"] = round(TOKENS / ((step_ms + bw["total_ms"]) * 1e-3), 1)
     line["backward"] = bw
+    line["other_configs"] = isolated_configs(max(10, args.steps // 2), max(3, args.warmup // 2))
     if not args.no_e2e:
         line["e2e_prefill"] = e2e_prefill()
+        line["e2e_decode"] = e2e_decode()
+        line["e2e_prefill_moe"] = e2e_prefill_moe()
     if not args.no_cpu:
         line["cpu_baseline"] = cpu_baseline()
     print(json.dumps(line), flush=True)
