@@ -5,7 +5,8 @@
  * enqueues its kernels on that stream and returns without synchronising.
  * The caller allocates every output (as the reference's autograd Functions do
  * with torch.empty); the library never allocates or frees device memory and
- * keeps no state between calls, so calls are re-entrant and capturable.  One
+ * keeps no state between calls (its one process-wide setting is the kernel
+ * choice of mhc_pre_token_threshold), so calls are re-entrant and capturable.  One
  * entry point (mhc_pre_bwd_weights) needs scratch for token-range partial
  * sums; the caller passes it as a workspace argument.
  *
@@ -162,6 +163,78 @@ int mhc_sinkhorn_fwd(const void* m_in, void* m_out, int dtype, int64_t batch, in
  */
 int mhc_stream_expand_fwd(const void* x, void* out, int elem_bytes, int64_t M, int n, int C,
                           hipStream_t stream);
+
+/* --------------------------------------------------- fused input norms
+ * The model wraps every sublayer as F(z) = sublayer(RMSNorm_C(z)) and ends
+ * with RMSNorm_C(MHCHead(x)) (model/model_minimind.py:326-336, :367-370).  The
+ * *_norm_fwd variants apply that RMSNorm (gain norm_weight [C] of norm_dtype,
+ * eps norm_eps) to the main output inside the same launch:
+ *   out = round(s * (1 / sqrt(mean_c(s^2) + norm_eps)) * norm_weight)
+ * where s is the pre-aggregate (head output) rounded to x_dtype, i.e. the
+ * tensor the reference's nn.RMSNorm receives.  All other outputs are those
+ * of the plain entry point.  Forward only: training keeps the separate norm,
+ * whose backward needs the un-normed s.
+ */
+
+/*
+ * mhc_pre_fwd + the sublayer's input RMSNorm.
+ * Replaces _PrePhaseFullFn.forward   model/mhc_fused.py:575-641
+ *          + self.attn_in_norm / self.ffn_in_norm applied to its output
+ *            inside F                model/model_minimind.py:330, :336.
+ */
+int mhc_pre_norm_fwd(const void* x, int x_dtype, const void* phi, int phi_dtype,
+                     const void* phi_packed, const void* alpha_pre, const void* bias_pre,
+                     const void* alpha_post, const void* bias_post, const void* alpha_res,
+                     const void* bias_res, int param_dtype, void* sublayer_in_normed, void* h_pre,
+                     void* h_post, void* h_res_raw, void* h_res, float* inv_rms,
+                     float* mixes_raw, int64_t M, int n, int C, float post_mult, float pre_eps,
+                     float rms_eps, int sinkhorn_iters, float sinkhorn_eps,
+                     const void* norm_weight, int norm_dtype, float norm_eps, hipStream_t stream);
+
+/*
+ * mhc_pre_nohres_fwd + the sublayer's input RMSNorm.
+ * Replaces _PrePhaseFn.forward  model/mhc_fused_no_hres.py:400-463
+ *          + the in-F norm      model/model_minimind.py:330, :336.
+ */
+int mhc_pre_nohres_norm_fwd(const void* x, int x_dtype, const void* phi, int phi_dtype,
+                            const void* phi_packed, const void* alpha_pre, const void* bias_pre,
+                            const void* alpha_post, const void* bias_post, int param_dtype,
+                            void* sublayer_in_normed, void* h_pre, void* h_post, float* inv_rms,
+                            float* mixes_raw, int64_t M, int n, int C, float post_mult,
+                            float pre_eps, float rms_eps, const void* norm_weight, int norm_dtype,
+                            float norm_eps, hipStream_t stream);
+
+/*
+ * mhc_head_fwd + the model's final RMSNorm.
+ * Replaces self.norm = Sequential(MHCHead, RMSNorm)  model/model_minimind.py:367-370
+ *          (MHCHead.forward model/mhc_common.py:435-450).
+ */
+int mhc_head_norm_fwd(const void* x, int x_dtype, const void* phi, int phi_dtype,
+                      const void* phi_packed, const void* alpha, const void* bias, int param_dtype,
+                      void* out_normed, float* inv_rms, float* mix_raw, int64_t M, int n, int C,
+                      float pre_eps, float rms_eps, const void* norm_weight, int norm_dtype,
+                      float norm_eps, hipStream_t stream);
+
+/*
+ * The model's entry: RMSNorm over C with gain norm_weight, then n copies:
+ *   out[t, i*C + c] = round(x[t, c] * (1 / sqrt(mean_c(x[t]^2) + eps)) * w[c]).
+ * Replaces self.embed_up_norm = Sequential(RMSNorm, StreamExpand)
+ *          model/model_minimind.py:365, applied at :385
+ *          (StreamExpand.forward model/mhc_common.py:115-119).
+ *   x [M, C] x_dtype; out [M, n*C] x_dtype.
+ */
+int mhc_expand_norm_fwd(const void* x, int x_dtype, const void* norm_weight, int norm_dtype,
+                        void* out, int64_t M, int n, int C, float eps, hipStream_t stream);
+
+/*
+ * Batch size (tokens) at or below which the pre-phase entry points run the
+ * one-workgroup-per-token kernel instead of the persistent one (bf16, packed
+ * phi, n <= 2, C <= 1024; default 512); max_tokens < 0 only queries.  Returns the previous
+ * value.  Process-wide setting, not synchronised with calls in flight.
+ * No reference counterpart (the reference launches one program per token at
+ * every size, model/mhc_fused.py:615-641).
+ */
+int64_t mhc_pre_token_threshold(int64_t max_tokens);
 
 /* ------------------------------------------------------------------ backward
  * Gradients are computed in fp32 and rounded once at the store, as the

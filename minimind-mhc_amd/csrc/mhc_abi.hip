@@ -48,6 +48,8 @@ int check_pre(const mhc::PreArgs& a, const char* fn) {
     return fail(hipErrorInvalidValue, "%s: h_post, alpha_post and bias_post are required", fn);
   if (a.mode == mhc::kFull && (!a.alpha[2] || !a.bias[2]))
     return fail(hipErrorInvalidValue, "%s: alpha_res and bias_res are required", fn);
+  if (a.norm_w && !dtype_ok(a.norm_dtype)) return fail(hipErrorInvalidValue, "%s: bad norm dtype %d", fn, a.norm_dtype);
+  if (a.norm_w && !(a.norm_eps >= 0.f)) return fail(hipErrorInvalidValue, "%s: norm_eps must be >= 0", fn);
   return 0;
 }
 
@@ -65,7 +67,7 @@ int run_pre(mhc::PreArgs& a, hipStream_t stream, const char* fn) {
 
 extern "C" {
 
-int mhc_abi_version(void) { return 2; }
+int mhc_abi_version(void) { return 3; }
 
 const char* mhc_last_error(void) { return g_err; }
 
@@ -80,14 +82,18 @@ int mhc_phi_pack(const void* phi, int phi_dtype, void* packed, int n, int C, int
   return hip_status(mhc::launch_phi_pack(phi, phi_dtype, packed, n, C, mode, stream), "mhc_phi_pack");
 }
 
-int mhc_pre_fwd(const void* x, int x_dtype, const void* phi, int phi_dtype, const void* phi_packed,
-                const void* alpha_pre, const void* bias_pre, const void* alpha_post,
-                const void* bias_post, const void* alpha_res, const void* bias_res,
-                int param_dtype, void* sublayer_in, void* h_pre, void* h_post, void* h_res_raw,
-                void* h_res, float* inv_rms, float* mixes_raw, int64_t M, int n, int C,
-                float post_mult, float pre_eps, float rms_eps, int sinkhorn_iters,
-                float sinkhorn_eps, hipStream_t stream) {
+static int pre_full(const void* x, int x_dtype, const void* phi, int phi_dtype,
+                    const void* phi_packed, const void* alpha_pre, const void* bias_pre,
+                    const void* alpha_post, const void* bias_post, const void* alpha_res,
+                    const void* bias_res, int param_dtype, void* sublayer_in, void* h_pre,
+                    void* h_post, void* h_res_raw, void* h_res, float* inv_rms, float* mixes_raw,
+                    int64_t M, int n, int C, float post_mult, float pre_eps, float rms_eps,
+                    int sinkhorn_iters, float sinkhorn_eps, const void* norm_w, int norm_dtype,
+                    float norm_eps, hipStream_t stream, const char* fn) {
   mhc::PreArgs a{};
+  a.norm_w = norm_w;
+  a.norm_dtype = norm_dtype;
+  a.norm_eps = norm_eps;
   a.x = x;
   a.phi = phi;
   a.phi_packed = phi_packed;
@@ -116,16 +122,49 @@ int mhc_pre_fwd(const void* x, int x_dtype, const void* phi, int phi_dtype, cons
   a.rms_eps = rms_eps;
   a.sk_iters = sinkhorn_iters;
   a.sk_eps = sinkhorn_eps;
-  return run_pre(a, stream, "mhc_pre_fwd");
+  return run_pre(a, stream, fn);
 }
 
-int mhc_pre_nohres_fwd(const void* x, int x_dtype, const void* phi, int phi_dtype,
-                       const void* phi_packed, const void* alpha_pre, const void* bias_pre,
-                       const void* alpha_post, const void* bias_post, int param_dtype,
-                       void* sublayer_in, void* h_pre, void* h_post, float* inv_rms,
-                       float* mixes_raw, int64_t M, int n, int C, float post_mult, float pre_eps,
-                       float rms_eps, hipStream_t stream) {
+int mhc_pre_fwd(const void* x, int x_dtype, const void* phi, int phi_dtype, const void* phi_packed,
+                const void* alpha_pre, const void* bias_pre, const void* alpha_post,
+                const void* bias_post, const void* alpha_res, const void* bias_res,
+                int param_dtype, void* sublayer_in, void* h_pre, void* h_post, void* h_res_raw,
+                void* h_res, float* inv_rms, float* mixes_raw, int64_t M, int n, int C,
+                float post_mult, float pre_eps, float rms_eps, int sinkhorn_iters,
+                float sinkhorn_eps, hipStream_t stream) {
+  return pre_full(x, x_dtype, phi, phi_dtype, phi_packed, alpha_pre, bias_pre, alpha_post,
+                  bias_post, alpha_res, bias_res, param_dtype, sublayer_in, h_pre, h_post,
+                  h_res_raw, h_res, inv_rms, mixes_raw, M, n, C, post_mult, pre_eps, rms_eps,
+                  sinkhorn_iters, sinkhorn_eps, nullptr, 0, 0.f, stream, "mhc_pre_fwd");
+}
+
+int mhc_pre_norm_fwd(const void* x, int x_dtype, const void* phi, int phi_dtype,
+                     const void* phi_packed, const void* alpha_pre, const void* bias_pre,
+                     const void* alpha_post, const void* bias_post, const void* alpha_res,
+                     const void* bias_res, int param_dtype, void* sublayer_in_normed, void* h_pre,
+                     void* h_post, void* h_res_raw, void* h_res, float* inv_rms,
+                     float* mixes_raw, int64_t M, int n, int C, float post_mult, float pre_eps,
+                     float rms_eps, int sinkhorn_iters, float sinkhorn_eps,
+                     const void* norm_weight, int norm_dtype, float norm_eps, hipStream_t stream) {
+  if (!norm_weight && M != 0) return fail(hipErrorInvalidValue, "mhc_pre_norm_fwd: norm_weight is required");
+  return pre_full(x, x_dtype, phi, phi_dtype, phi_packed, alpha_pre, bias_pre, alpha_post,
+                  bias_post, alpha_res, bias_res, param_dtype, sublayer_in_normed, h_pre, h_post,
+                  h_res_raw, h_res, inv_rms, mixes_raw, M, n, C, post_mult, pre_eps, rms_eps,
+                  sinkhorn_iters, sinkhorn_eps, norm_weight, norm_dtype, norm_eps, stream,
+                  "mhc_pre_norm_fwd");
+}
+
+static int pre_nohres(const void* x, int x_dtype, const void* phi, int phi_dtype,
+                      const void* phi_packed, const void* alpha_pre, const void* bias_pre,
+                      const void* alpha_post, const void* bias_post, int param_dtype,
+                      void* sublayer_in, void* h_pre, void* h_post, float* inv_rms,
+                      float* mixes_raw, int64_t M, int n, int C, float post_mult, float pre_eps,
+                      float rms_eps, const void* norm_w, int norm_dtype, float norm_eps,
+                      hipStream_t stream, const char* fn) {
   mhc::PreArgs a{};
+  a.norm_w = norm_w;
+  a.norm_dtype = norm_dtype;
+  a.norm_eps = norm_eps;
   a.x = x;
   a.phi = phi;
   a.phi_packed = phi_packed;
@@ -148,14 +187,43 @@ int mhc_pre_nohres_fwd(const void* x, int x_dtype, const void* phi, int phi_dtyp
   a.post_mult = post_mult;
   a.pre_eps = pre_eps;
   a.rms_eps = rms_eps;
-  return run_pre(a, stream, "mhc_pre_nohres_fwd");
+  return run_pre(a, stream, fn);
 }
 
-int mhc_head_fwd(const void* x, int x_dtype, const void* phi, int phi_dtype,
-                 const void* phi_packed, const void* alpha, const void* bias, int param_dtype,
-                 void* out, float* inv_rms, float* mix_raw, int64_t M, int n, int C, float pre_eps,
-                 float rms_eps, hipStream_t stream) {
+int mhc_pre_nohres_fwd(const void* x, int x_dtype, const void* phi, int phi_dtype,
+                       const void* phi_packed, const void* alpha_pre, const void* bias_pre,
+                       const void* alpha_post, const void* bias_post, int param_dtype,
+                       void* sublayer_in, void* h_pre, void* h_post, float* inv_rms,
+                       float* mixes_raw, int64_t M, int n, int C, float post_mult, float pre_eps,
+                       float rms_eps, hipStream_t stream) {
+  return pre_nohres(x, x_dtype, phi, phi_dtype, phi_packed, alpha_pre, bias_pre, alpha_post,
+                    bias_post, param_dtype, sublayer_in, h_pre, h_post, inv_rms, mixes_raw, M, n,
+                    C, post_mult, pre_eps, rms_eps, nullptr, 0, 0.f, stream, "mhc_pre_nohres_fwd");
+}
+
+int mhc_pre_nohres_norm_fwd(const void* x, int x_dtype, const void* phi, int phi_dtype,
+                            const void* phi_packed, const void* alpha_pre, const void* bias_pre,
+                            const void* alpha_post, const void* bias_post, int param_dtype,
+                            void* sublayer_in_normed, void* h_pre, void* h_post, float* inv_rms,
+                            float* mixes_raw, int64_t M, int n, int C, float post_mult,
+                            float pre_eps, float rms_eps, const void* norm_weight, int norm_dtype,
+                            float norm_eps, hipStream_t stream) {
+  if (!norm_weight && M != 0) return fail(hipErrorInvalidValue, "mhc_pre_nohres_norm_fwd: norm_weight is required");
+  return pre_nohres(x, x_dtype, phi, phi_dtype, phi_packed, alpha_pre, bias_pre, alpha_post,
+                    bias_post, param_dtype, sublayer_in_normed, h_pre, h_post, inv_rms, mixes_raw,
+                    M, n, C, post_mult, pre_eps, rms_eps, norm_weight, norm_dtype, norm_eps,
+                    stream, "mhc_pre_nohres_norm_fwd");
+}
+
+static int head(const void* x, int x_dtype, const void* phi, int phi_dtype,
+                const void* phi_packed, const void* alpha, const void* bias, int param_dtype,
+                void* out, float* inv_rms, float* mix_raw, int64_t M, int n, int C, float pre_eps,
+                float rms_eps, const void* norm_w, int norm_dtype, float norm_eps,
+                hipStream_t stream, const char* fn) {
   mhc::PreArgs a{};
+  a.norm_w = norm_w;
+  a.norm_dtype = norm_dtype;
+  a.norm_eps = norm_eps;
   a.x = x;
   a.phi = phi;
   a.phi_packed = phi_packed;
@@ -173,7 +241,26 @@ int mhc_head_fwd(const void* x, int x_dtype, const void* phi, int phi_dtype,
   a.param_dtype = param_dtype;
   a.pre_eps = pre_eps;
   a.rms_eps = rms_eps;
-  return run_pre(a, stream, "mhc_head_fwd");
+  return run_pre(a, stream, fn);
+}
+
+int mhc_head_fwd(const void* x, int x_dtype, const void* phi, int phi_dtype,
+                 const void* phi_packed, const void* alpha, const void* bias, int param_dtype,
+                 void* out, float* inv_rms, float* mix_raw, int64_t M, int n, int C, float pre_eps,
+                 float rms_eps, hipStream_t stream) {
+  return head(x, x_dtype, phi, phi_dtype, phi_packed, alpha, bias, param_dtype, out, inv_rms,
+              mix_raw, M, n, C, pre_eps, rms_eps, nullptr, 0, 0.f, stream, "mhc_head_fwd");
+}
+
+int mhc_head_norm_fwd(const void* x, int x_dtype, const void* phi, int phi_dtype,
+                      const void* phi_packed, const void* alpha, const void* bias, int param_dtype,
+                      void* out_normed, float* inv_rms, float* mix_raw, int64_t M, int n, int C,
+                      float pre_eps, float rms_eps, const void* norm_weight, int norm_dtype,
+                      float norm_eps, hipStream_t stream) {
+  if (!norm_weight && M != 0) return fail(hipErrorInvalidValue, "mhc_head_norm_fwd: norm_weight is required");
+  return head(x, x_dtype, phi, phi_dtype, phi_packed, alpha, bias, param_dtype, out_normed,
+              inv_rms, mix_raw, M, n, C, pre_eps, rms_eps, norm_weight, norm_dtype, norm_eps,
+              stream, "mhc_head_norm_fwd");
 }
 
 static int run_post(mhc::PostArgs& a, hipStream_t stream, const char* fn) {
@@ -227,6 +314,25 @@ int mhc_stream_expand_fwd(const void* x, void* out, int elem_bytes, int64_t M, i
   if (!x || !out) return fail(hipErrorInvalidValue, "mhc_stream_expand_fwd: null pointer");
   return hip_status(mhc::launch_stream_expand(x, out, elem_bytes, M, n, C, stream),
                     "mhc_stream_expand_fwd");
+}
+
+int mhc_expand_norm_fwd(const void* x, int x_dtype, const void* norm_weight, int norm_dtype,
+                        void* out, int64_t M, int n, int C, float eps, hipStream_t stream) {
+  const char* fn = "mhc_expand_norm_fwd";
+  if (M < 0 || n < 1 || n > kMaxN || C < 1) return fail(hipErrorInvalidValue, "%s: bad shape (M=%lld n=%d C=%d)", fn, (long long)M, n, C);
+  if (!dtype_ok(x_dtype) || !dtype_ok(norm_dtype)) return fail(hipErrorInvalidValue, "%s: bad dtype", fn);
+  if (!(eps >= 0.f)) return fail(hipErrorInvalidValue, "%s: eps must be >= 0", fn);
+  if (M > kMaxBlocks) return fail(hipErrorInvalidValue, "%s: M too large", fn);
+  if (M == 0) return 0;
+  if (!x || !norm_weight || !out) return fail(hipErrorInvalidValue, "%s: null pointer", fn);
+  return hip_status(mhc::launch_expand_norm(x, x_dtype, norm_weight, norm_dtype, out, M, n, C, eps,
+                                            stream), fn);
+}
+
+int64_t mhc_pre_token_threshold(int64_t max_tokens) {
+  const int64_t prev = mhc::pre_token_max_m();
+  if (max_tokens >= 0) mhc::set_pre_token_max_m(max_tokens);
+  return prev;
 }
 
 // ------------------------------------------------------------------ backward

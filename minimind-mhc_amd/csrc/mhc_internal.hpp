@@ -46,6 +46,13 @@ struct PreArgs {
   float post_mult, pre_eps, rms_eps;
   int sk_iters;
   float sk_eps;
+  // RMSNorm over C applied to the main output before it is stored (the
+  // sublayer's input norm, or the model's final norm after MHCHead):
+  //   out = bf16(s * (1 / sqrt(mean_c(s^2) + norm_eps)) * norm_w),  s the
+  // pre-aggregate (head output) rounded to x_dtype.  Null norm_w: no norm.
+  const void* norm_w;     // [C] norm_dtype
+  int norm_dtype;
+  float norm_eps;
 };
 
 struct PostArgs {
@@ -121,6 +128,16 @@ struct WeightsArgs {
 // Launchers: return hipSuccess or the launch error.
 hipError_t launch_pre_mfma(const PreArgs& a, hipStream_t s);   // requires mfma_supported()
 hipError_t launch_pre_generic(const PreArgs& a, hipStream_t s);
+// One workgroup per token (small M, n <= 2, bf16, packed phi): see mhc_pre_token.hip.
+bool pre_token_supported(const PreArgs& a);
+hipError_t launch_pre_token(const PreArgs& a, hipStream_t s);
+// Tokens at or below which launch_pre_mfma picks the one-workgroup-per-token
+// kernel (process-wide setting).
+int64_t pre_token_max_m();
+void set_pre_token_max_m(int64_t m);
+// RMSNorm of each C row followed by n copies (StreamExpand): out[t, i*C + c].
+hipError_t launch_expand_norm(const void* x, int x_dtype, const void* w, int w_dtype, void* out,
+                              int64_t M, int n, int C, float eps, hipStream_t s);
 hipError_t launch_post(const PostArgs& a, hipStream_t s);
 hipError_t launch_post_bwd(const PostBwdArgs& a, hipStream_t s);
 hipError_t launch_pre_bwd(const PreBwdArgs& a, hipStream_t s);

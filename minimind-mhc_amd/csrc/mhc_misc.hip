@@ -128,4 +128,94 @@ hipError_t launch_stream_expand(const void* x, void* out, int elem_bytes, int64_
   return hipGetLastError();
 }
 
+// ------------------------------------------------- RMSNorm + StreamExpand
+// The model's entry (model/model_minimind.py:365): RMSNorm(C) with gain w,
+// then n copies (model/mhc_common.py:115-119), in one pass:
+//   y[c] = round(x[c] * (1 / sqrt(mean_c(x^2) + eps)) * w[c]),  out[t, i*C + c] = y[c].
+// One wave per token; fp32 arithmetic, one rounding to the stream dtype.
+
+__device__ __forceinline__ float lo16(uint32_t u, int dt) {
+  return dt == kBF16 ? bf16lo(u) : f16_bits_to_f32((uint16_t)(u & 0xffffu));
+}
+__device__ __forceinline__ float hi16(uint32_t u, int dt) {
+  return dt == kBF16 ? bf16hi(u) : f16_bits_to_f32((uint16_t)(u >> 16));
+}
+__device__ __forceinline__ uint32_t pack16(float a, float b, int dt) {
+  if (dt == kBF16) return pack_bf16x2(a, b);
+  return (uint32_t)f32_to_f16_bits(a) | ((uint32_t)f32_to_f16_bits(b) << 16);
+}
+
+// 16-bit streams, C % 8 == 0, 16-byte aligned rows: 8 elements per lane step.
+__global__ __launch_bounds__(256) void expand_norm_vec_kernel(const U32x4* __restrict__ x, int xdt,
+                                                              const void* __restrict__ w, int wdt,
+                                                              U32x4* __restrict__ out, int64_t M,
+                                                              int n, int C, float eps) {
+  const int64_t tok = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
+  if (tok >= M) return;  // whole waves
+  const int lane = threadIdx.x & 63;
+  const int C8 = C >> 3;
+  const U32x4* xr = x + tok * C8;
+  float ss = 0.f;
+  for (int ch = lane; ch < C8; ch += 64) {
+    const U32x4 v = xr[ch];
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      const float a = lo16(v.v[j], xdt);
+      const float b = hi16(v.v[j], xdt);
+      ss = fmaf(a, a, ss);
+      ss = fmaf(b, b, ss);
+    }
+  }
+  ss = wave_sum(ss);
+  const float r = 1.0f / sqrtf(ss / (float)C + eps);
+  U32x4* orow = out + tok * n * C8;
+  for (int ch = lane; ch < C8; ch += 64) {
+    const U32x4 v = xr[ch];
+    U32x4 y;
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      const int c = ch * 8 + 2 * j;
+      y.v[j] = pack16(lo16(v.v[j], xdt) * r * ld_any(w, c, wdt),
+                      hi16(v.v[j], xdt) * r * ld_any(w, c + 1, wdt), xdt);
+    }
+    for (int i = 0; i < n; ++i) orow[(int64_t)i * C8 + ch] = y;
+  }
+}
+
+__global__ __launch_bounds__(256) void expand_norm_kernel(const void* __restrict__ x, int xdt,
+                                                          const void* __restrict__ w, int wdt,
+                                                          void* __restrict__ out, int64_t M, int n,
+                                                          int C, float eps) {
+  const int64_t tok = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
+  if (tok >= M) return;
+  const int lane = threadIdx.x & 63;
+  const int64_t xb = tok * C;
+  float ss = 0.f;
+  for (int c = lane; c < C; c += 64) {
+    const float v = ld_any(x, xb + c, xdt);
+    ss = fmaf(v, v, ss);
+  }
+  ss = wave_sum(ss);
+  const float r = 1.0f / sqrtf(ss / (float)C + eps);
+  const int64_t ob = tok * n * C;
+  for (int c = lane; c < C; c += 64) {
+    const float y = ld_any(x, xb + c, xdt) * r * ld_any(w, c, wdt);
+    for (int i = 0; i < n; ++i) st_any(out, ob + (int64_t)i * C + c, xdt, y);
+  }
+}
+
+hipError_t launch_expand_norm(const void* x, int x_dtype, const void* w, int w_dtype, void* out,
+                              int64_t M, int n, int C, float eps, hipStream_t s) {
+  const unsigned blocks = (unsigned)((M + 3) / 4);
+  const uintptr_t align = reinterpret_cast<uintptr_t>(x) | reinterpret_cast<uintptr_t>(out);
+  if (x_dtype != kF32 && C % 8 == 0 && align % 16 == 0)
+    hipLaunchKernelGGL(expand_norm_vec_kernel, dim3(blocks), dim3(256), 0, s,
+                       static_cast<const U32x4*>(x), x_dtype, w, w_dtype, static_cast<U32x4*>(out),
+                       M, n, C, eps);
+  else
+    hipLaunchKernelGGL(expand_norm_kernel, dim3(blocks), dim3(256), 0, s, x, x_dtype, w, w_dtype,
+                       out, M, n, C, eps);
+  return hipGetLastError();
+}
+
 }  // namespace mhc

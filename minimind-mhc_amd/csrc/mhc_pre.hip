@@ -78,6 +78,8 @@ static int device_cus() {
 }
 
 hipError_t launch_pre_mfma(const PreArgs& a, hipStream_t s) {
+  // Decode-size batches: one workgroup per token.
+  if (a.M <= pre_token_max_m() && pre_token_supported(a)) return launch_pre_token(a, s);
   // n <= 4: persistent workgroups with the x tile double-buffered in registers.
   if (a.n <= 4) {
     const int kb = persist_kb_needed(a.C);
@@ -100,6 +102,24 @@ constexpr int kGenThreads = 256;
 constexpr int kGenMaxN = 16;
 constexpr int kGenMaxFD = 2 * kGenMaxN + kGenMaxN * kGenMaxN;
 constexpr int kGenChunk = 16;  // features reduced per block-wide reduction
+
+// 1 / sqrt(mean_c(v(c)^2) + norm_eps) over the C outputs of this token's
+// workgroup (red: kGenThreads / 64 floats of LDS; ends with a barrier).
+template <typename F>
+__device__ float block_norm_scale(const PreArgs& a, F v, float* red, int tid) {
+  float q = 0.f;
+  for (int c = tid; c < a.C; c += kGenThreads) {
+    const float o = v(c);
+    q = fmaf(o, o, q);
+  }
+  q = wave_sum(q);
+  __syncthreads();  // red may hold an earlier reduction's values
+  if ((tid & 63) == 0) red[tid >> 6] = q;
+  __syncthreads();
+  float t = 0.f;
+  for (int w = 0; w < kGenThreads / 64; ++w) t += red[w];
+  return 1.0f / sqrtf(t / (float)a.C + a.norm_eps);
+}
 
 __global__ __launch_bounds__(kGenThreads) void pre_generic_kernel(PreArgs a) {
   __shared__ float s_red[kGenThreads / 64][kGenChunk];
@@ -140,6 +160,16 @@ __global__ __launch_bounds__(kGenThreads) void pre_generic_kernel(PreArgs a) {
   const float inv = s_inv;
 
   if (mode == kRms) {  // MHCHead with n == 1 (model/mhc_common.py:438-442)
+    if (a.norm_w) {
+      // the head output rounded to the stream dtype, then the model's final
+      // RMSNorm over C (== NC here)
+      const float r = block_norm_scale(a, [&](int c) { return round_to(ld_any(a.x, xb + c, xdt) * inv, xdt); },
+                                       s_red[0], tid);
+      for (int c = tid; c < C; c += kGenThreads)
+        st_any(a.sub_in, tok * C + c, xdt,
+               round_to(ld_any(a.x, xb + c, xdt) * inv, xdt) * r * ld_any(a.norm_w, c, a.norm_dtype));
+      return;
+    }
     for (int64_t k = tid; k < NC; k += kGenThreads)
       st_any(a.sub_in, tok * NC + k, xdt, ld_any(a.x, xb + k, xdt) * inv);
     return;
@@ -234,12 +264,19 @@ __global__ __launch_bounds__(kGenThreads) void pre_generic_kernel(PreArgs a) {
   // pre-aggregate (or the MHCHead weighted reduce): each h_pre[i] * x_i product
   // rounds to the stream dtype, the sum over streams accumulates in fp32
   // (model/mhc_fused.py:859, model/mhc_common.py:308).
-  for (int c = tid; c < C; c += kGenThreads) {
+  auto agg = [&](int c) {
     float o = 0.f;
     for (int i = 0; i < n; ++i)
       o += round_to(s_hpre[i] * ld_any(a.x, xb + (int64_t)i * C + c, xdt), xdt);
-    st_any(a.sub_in, tok * C + c, xdt, o);
+    return round_to(o, xdt);
+  };
+  if (a.norm_w) {  // RMSNorm over C of the rounded pre-aggregate (second pass recomputes it)
+    const float r = block_norm_scale(a, agg, s_red[0], tid);
+    for (int c = tid; c < C; c += kGenThreads)
+      st_any(a.sub_in, tok * C + c, xdt, agg(c) * r * ld_any(a.norm_w, c, a.norm_dtype));
+    return;
   }
+  for (int c = tid; c < C; c += kGenThreads) st_any(a.sub_in, tok * C + c, xdt, agg(c));
 }
 
 hipError_t launch_pre_generic(const PreArgs& a, hipStream_t s) {

@@ -22,7 +22,10 @@
 //     which is the layout the Sinkhorn iterations (sk8_*) run in, so h_res
 //     never passes through LDS;
 //   * the Sinkhorn iterations are spread between the pre-aggregate rounds:
-//     VALU work while the next round's loads are in flight.
+//     VALU work while the next round's loads are in flight;
+//   * with the RMSNorm epilogue the pre-aggregate chunks wait in LDS; after
+//     the rounds 16 lanes per token sum their squares, and a last pass
+//     scales, rounds and stores them.
 // Arithmetic and rounding points as pre_persist_kernel.
 //
 // Reference semantics: model/mhc_fused.py:163-268, :533-559, :47-56;
@@ -60,16 +63,34 @@ struct KsShared {
   float hpre[P::TM][N];
 };
 
+// LDS of the RMSNorm epilogue: the tile's pre-aggregate, the gain (fp32) and
+// each token's scale.
+template <int N, int MODE, bool NORM>
+struct KsNorm {
+  using P = KsPlan<N, MODE>;
+  static constexpr int kChunks = kMfmaMaxColBlocks * 4;  // 8-column chunks of a C <= 1024 row
+  U32x4 stash[P::TM * kChunks];
+  float gain[kMfmaMaxColBlocks * kCBlock];
+  float scale[P::TM];
+};
 template <int N, int MODE>
+struct KsNorm<N, MODE, false> {
+  int unused;
+};
+
+template <int N, int MODE, bool NORM>
 __global__ __launch_bounds__(kKsWaves * 64) void pre_kstream_kernel(PreArgs a) {
   using P = KsPlan<N, MODE>;
   using GP = GateParams<N>;
+  using NS = KsNorm<N, MODE, NORM>;
   constexpr int FD = P::FD;
   constexpr int NT = P::NT;
   constexpr int TM = P::TM;
   constexpr int D = P::D;
   constexpr int T = P::WAVES * 64;
+  static_assert(sizeof(KsShared<N, MODE>) + sizeof(NS) <= kLdsBytes, "LDS budget");
   __shared__ KsShared<N, MODE> sh;
+  __shared__ NS nsh;
 
   const int tid = threadIdx.x;
   const int lane = tid & 63;
@@ -87,6 +108,15 @@ __global__ __launch_bounds__(kKsWaves * 64) void pre_kstream_kernel(PreArgs a) {
   const int valid = (int)(M - t0 < TM ? M - t0 : TM);
 
   const RawParam rp = load_gate_param<N, MODE>(a, tid);
+  float gain[2] = {0.f, 0.f};  // norm gain of columns tid and tid + 512 (branch-free loads)
+  if constexpr (NORM) {
+#pragma unroll
+    for (int h = 0; h < 2; ++h) {
+      const int c = tid + h * T;
+      const float v = ld_any(a.norm_w, c < C ? c : 0, a.norm_dtype);
+      gain[h] = c < C ? v : 0.f;
+    }
+  }
 
   // ---- K loop -----------------------------------------------------------
   const auto rx = make_rsrc(static_cast<const uint16_t*>(a.x) + t0 * NC, (uint32_t)valid * NC * 2u);
@@ -157,6 +187,10 @@ __global__ __launch_bounds__(kKsWaves * 64) void pre_kstream_kernel(PreArgs a) {
     if (g == 0) sh.ss[kq][m * 16 + r] = ss[m];
   }
   if (tid < GP::kCount) sh.prm[tid] = convert_param(rp, a.param_dtype);
+  if constexpr (NORM) {
+#pragma unroll
+    for (int h = 0; h < 2; ++h) nsh.gain[tid + h * T] = gain[h];
+  }
 
   // ---- pre-aggregate rounds --------------------------------------------------
   // Items are (token, 16-byte column chunk) pairs, PB per lane per round, in
@@ -199,6 +233,10 @@ __global__ __launch_bounds__(kKsWaves * 64) void pre_kstream_kernel(PreArgs a) {
         hhi[i] = pack_hi(sh.hpre[ts][i]);
       }
       const U32x4 pk = preagg_chunk<N>(xv[b], hlo, hhi);
+      if constexpr (NORM) {
+        if (tt < TM) nsh.stash[tt * NS::kChunks + (c >> 3)] = pk;
+        continue;
+      }
       // whole offset in the vector offset, scalar offset the literal 0 (see
       // persist_preagg: a 128-bit store reads its data registers after issue)
       buf_store16(rsub, tt < valid ? (uint32_t)(tt * C + c) * 2u : kBufOob, pk);
@@ -284,14 +322,48 @@ __global__ __launch_bounds__(kKsWaves * 64) void pre_kstream_kernel(PreArgs a) {
 #pragma unroll
     for (int q = 0; q < 4; ++q) st_any(a.h_res, tk * P::G + e0 + q, kBF16, v[q]);
   }
+  if constexpr (NORM) {
+    // RMSNorm over C: 16 lanes per token sum the squares of the stashed
+    // (bf16-rounded) chunks jl, jl + 16, ...; then every item is scaled by
+    // its token's 1 / sqrt(mean + norm_eps) and the gain, rounded, stored.
+    __syncthreads();  // every chunk stashed
+    float q2 = 0.f;
+    for (int ch = jl; ch < C8; ch += 16) {
+      const U32x4 pk = nsh.stash[tt * NS::kChunks + ch];
+#pragma unroll
+      for (int j = 0; j < 4; ++j) q2 = dot2_bf16(pk.v[j], pk.v[j], q2);
+    }
+    q2 = row_reduce<8, OpAdd>(q2);
+    q2 = q2 + dpp_f<kDppRowMirror>(q2);
+    if (jl == 0) nsh.scale[tt] = 1.0f / sqrtf(q2 / (float)C + a.norm_eps);
+    __syncthreads();  // token scales visible
+    for (int p = tid; p < items; p += T) {
+      const int it = p / C8;
+      const int c = (p - it * C8) * 8;
+      const U32x4 pk = nsh.stash[it * NS::kChunks + (c >> 3)];
+      const float sc = nsh.scale[it];
+      const float4 w0 = *reinterpret_cast<const float4*>(&nsh.gain[c]);
+      const float4 w1 = *reinterpret_cast<const float4*>(&nsh.gain[c + 4]);
+      U32x4 y;
+      y.v[0] = pack_bf16x2(bf16lo(pk.v[0]) * sc * w0.x, bf16hi(pk.v[0]) * sc * w0.y);
+      y.v[1] = pack_bf16x2(bf16lo(pk.v[1]) * sc * w0.z, bf16hi(pk.v[1]) * sc * w0.w);
+      y.v[2] = pack_bf16x2(bf16lo(pk.v[2]) * sc * w1.x, bf16hi(pk.v[2]) * sc * w1.y);
+      y.v[3] = pack_bf16x2(bf16lo(pk.v[3]) * sc * w1.z, bf16hi(pk.v[3]) * sc * w1.w);
+      buf_store16(rsub, it < valid ? (uint32_t)(it * C + c) * 2u : kBufOob, y);
+    }
+  }
 }
 
 template <int N, int MODE>
 hipError_t launch_pre_kstream_inst(const PreArgs& a, hipStream_t s) {
   constexpr int TM = KsPlan<N, MODE>::TM;
   const int64_t tiles = (a.M + TM - 1) / TM;
-  hipLaunchKernelGGL((pre_kstream_kernel<N, MODE>), dim3((unsigned)tiles),
-                     dim3(KsPlan<N, MODE>::WAVES * 64), 0, s, a);
+  if (a.norm_w)
+    hipLaunchKernelGGL((pre_kstream_kernel<N, MODE, true>), dim3((unsigned)tiles),
+                       dim3(KsPlan<N, MODE>::WAVES * 64), 0, s, a);
+  else
+    hipLaunchKernelGGL((pre_kstream_kernel<N, MODE, false>), dim3((unsigned)tiles),
+                       dim3(KsPlan<N, MODE>::WAVES * 64), 0, s, a);
   return hipGetLastError();
 }
 

@@ -89,7 +89,22 @@ struct PersistShared {
   U32x4 zero;                                 // B operand of padding columns
 };
 
-template <int N, int MODE, int KB>
+// LDS of the optional RMSNorm epilogue: each tile's pre-aggregate waits in LDS
+// (lane-private slots, two tiles) until the next tile's barrier has made every
+// wave's sum-of-squares partial visible; the gain lives in LDS as fp32.
+template <bool NORM, int KB>
+struct PersistNorm {
+  static constexpr int kChunks = kPersistWaves * KB * 4;  // 8-column chunks per token row
+  U32x4 stash[2][kTokTile * kChunks];                     // [slot][token][chunk]
+  float gain[kMfmaMaxColBlocks * kCBlock];
+  float ss2[2][kPersistWaves][kTokTile];                  // per-wave partials, 2 slots
+};
+template <int KB>
+struct PersistNorm<false, KB> {
+  int unused;
+};
+
+template <int N, int MODE, int KB, bool NORM = false>
 struct PersistPlan {
   using S = PreShape<N, MODE>;
   static constexpr int FD = S::FD;
@@ -101,13 +116,15 @@ struct PersistPlan {
   // phi tiles as fit in the rest of the budget (the other ~60 VGPRs are
   // working set); phi tiles that do not fit are read from LDS each tile.
   static constexpr int XTILE = KB * N * 4;  // VGPRs of one x tile (and of one phi tile)
-  static constexpr int kRegBudget = XTILE <= 48 ? 192 : 160;
+  // With the norm epilogue one x tile's worth less: its stores and the stash
+  // traffic need working registers inside the tile loop.
+  static constexpr int kRegBudget = (XTILE <= 48 ? 192 : 160) - (NORM ? XTILE : 0);
   static constexpr int DEPTH = 2;
   static constexpr int REG_LEFT = kRegBudget - DEPTH * XTILE;
   static constexpr int REG_FIT = REG_LEFT > 0 ? REG_LEFT / XTILE : 0;
   static constexpr int NREG = REG_FIT < NT ? REG_FIT : NT;
   // LDS: shared scratch, then phi tiles NREG.. while they fit
-  static constexpr int SHARED = (int)sizeof(PersistShared<N, FD>);
+  static constexpr int SHARED = (int)sizeof(PersistShared<N, FD>) + (int)sizeof(PersistNorm<NORM, KB>);
   static constexpr int cols(int t) { return t == NT - 1 ? LAST_COLS : 16; }
   static constexpr int tile_lds(int t) { return kPersistWaves * KB * N * 4 * cols(t) * 16; }
   static constexpr int lds_tiles() {
@@ -193,12 +210,12 @@ __device__ __forceinline__ void persist_load_part(U32x4 (&xr)[KB][N], __amdgpu_b
 }
 
 // ---- phase 1: sum of squares (bf16 dot2) + projection partials (MFMA) -> LDS
-template <int N, int MODE, int KB>
+template <int N, int MODE, int KB, bool NORM>
 __device__ __forceinline__ void persist_partials(
     const PreArgs& a, PersistShared<N, PersistPlan<N, MODE, KB>::FD>& sh, const U32x4 (&xr)[KB][N],
-    const bf16x8_t (&wreg)[KB][N][PersistPlan<N, MODE, KB>::WR], const unsigned char* lds_w,
+    const bf16x8_t (&wreg)[KB][N][PersistPlan<N, MODE, KB, NORM>::WR], const unsigned char* lds_w,
     int slot, int lane, int wave) {
-  using P = PersistPlan<N, MODE, KB>;
+  using P = PersistPlan<N, MODE, KB, NORM>;
   constexpr int FD = P::FD;
   constexpr int NT = P::NT;
   const int r = lane & 15;
@@ -352,11 +369,14 @@ __device__ __forceinline__ void persist_sinkhorn(const PreArgs& a, const float* 
   if (e < TM * G && t0 + e / G < a.M) st_any(a.h_res, t0 * G + e, kBF16, v);
 }
 
-// ---- phase 3: pre-aggregate from the held x registers.
-template <int N, int KB>
+// ---- phase 3: pre-aggregate from the held x registers.  With the norm the
+// chunks go to the lane's LDS slots and the token's sum of squares (of the
+// bf16-rounded values) to this wave's partial, for persist_norm_store.
+template <int N, int KB, bool NORM>
 __device__ __forceinline__ void persist_preagg(const PreArgs& a, const U32x4 (&xr)[KB][N],
                                                const uint32_t (&hlo)[N], const uint32_t (&hhi)[N],
-                                               int64_t tile, int lane, int wave) {
+                                               int64_t tile, int lane, int wave,
+                                               PersistNorm<NORM, KB>& nsh, int slot) {
   constexpr int TM = kTokTile;
   const int r = lane & 15;
   const int g = lane >> 4;
@@ -366,11 +386,18 @@ __device__ __forceinline__ void persist_preagg(const PreArgs& a, const U32x4 (&x
   const int valid = (int)(M - t0 < TM ? M - t0 : TM);
   const auto rsub = make_rsrc(static_cast<uint16_t*>(a.sub_in) + t0 * C, (uint32_t)valid * C * 2u);
   const uint32_t sub_row = (uint32_t)(r * C) * 2u;
+  float q2 = 0.f;
 #pragma unroll
   for (int q = 0; q < KB; ++q) {
     const int c0 = (wave + kPersistWaves * q) * kCBlock;
     const uint32_t lo = x_lane_off(q, wave, g, C);
     const U32x4 pk = preagg_chunk<N>(xr[q], hlo, hhi);
+    if constexpr (NORM) {  // column blocks past C hold zeros
+#pragma unroll
+      for (int j = 0; j < 4; ++j) q2 = dot2_bf16(pk.v[j], pk.v[j], q2);
+      nsh.stash[slot][r * PersistNorm<NORM, KB>::kChunks + (c0 >> 3) + g] = pk;
+      continue;
+    }
     // The whole offset travels in the vector offset, the scalar offset stays
     // the literal 0: a 128-bit store reads its data registers after issue, and
     // the compiler only keeps the next VALU write off those registers for
@@ -378,23 +405,64 @@ __device__ __forceinline__ void persist_preagg(const PreArgs& a, const U32x4 (&x
     // register at once and some lanes stored the new value.
     buf_store16(rsub, lo == kBufOob ? kBufOob : sub_row + lo + (uint32_t)c0 * 2u, pk);
   }
+  if constexpr (NORM) {
+    q2 += __shfl_xor(q2, 16, 64);
+    q2 += __shfl_xor(q2, 32, 64);
+    if (g == 0) nsh.ss2[slot][wave][r] = q2;
+  }
+}
+
+// ---- RMSNorm epilogue of tile `tile` (stash and partials slot `slot`), once a
+// barrier has made every wave's partial visible: scale the stashed chunks by
+// 1 / sqrt(mean_c(s^2) + norm_eps) and the gain, round to bf16, store.
+template <int N, int KB>
+__device__ __forceinline__ void persist_norm_store(const PreArgs& a, const PersistNorm<true, KB>& nsh,
+                                                   int64_t tile, int slot, int lane, int wave) {
+  constexpr int TM = kTokTile;
+  const int r = lane & 15;
+  const int g = lane >> 4;
+  const int64_t M = a.M;
+  const int C = a.C;
+  const int64_t t0 = tile * TM;
+  const int valid = (int)(M - t0 < TM ? M - t0 : TM);
+  const auto rsub = make_rsrc(static_cast<uint16_t*>(a.sub_in) + t0 * C, (uint32_t)valid * C * 2u);
+  const uint32_t sub_row = (uint32_t)(r * C) * 2u;
+  float t = 0.f;
+#pragma unroll
+  for (int w = 0; w < kPersistWaves; ++w) t += nsh.ss2[slot][w][r];
+  const float sc = 1.0f / sqrtf(t / (float)C + a.norm_eps);
+#pragma unroll
+  for (int q = 0; q < KB; ++q) {
+    const int c0 = (wave + kPersistWaves * q) * kCBlock;
+    const uint32_t lo = x_lane_off(q, wave, g, C);
+    const U32x4 pk = nsh.stash[slot][r * PersistNorm<true, KB>::kChunks + (c0 >> 3) + g];
+    const float4 w0 = *reinterpret_cast<const float4*>(&nsh.gain[c0 + 8 * g]);
+    const float4 w1 = *reinterpret_cast<const float4*>(&nsh.gain[c0 + 8 * g + 4]);
+    U32x4 y;
+    y.v[0] = pack_bf16x2(bf16lo(pk.v[0]) * sc * w0.x, bf16hi(pk.v[0]) * sc * w0.y);
+    y.v[1] = pack_bf16x2(bf16lo(pk.v[1]) * sc * w0.z, bf16hi(pk.v[1]) * sc * w0.w);
+    y.v[2] = pack_bf16x2(bf16lo(pk.v[2]) * sc * w1.x, bf16hi(pk.v[2]) * sc * w1.y);
+    y.v[3] = pack_bf16x2(bf16lo(pk.v[3]) * sc * w1.z, bf16hi(pk.v[3]) * sc * w1.w);
+    // whole offset in the vector offset, scalar offset the literal 0 (see above)
+    buf_store16(rsub, lo == kBufOob ? kBufOob : sub_row + lo + (uint32_t)c0 * 2u, y);
+  }
 }
 
 // One tile (partials slot and h_res slot `slot`); the next tile's loads go
 // into xn in three batches along the way.
-template <int N, int MODE, int KB>
+template <int N, int MODE, int KB, bool NORM>
 __device__ __forceinline__ void persist_step(
-    const PreArgs& a, PersistShared<N, PersistPlan<N, MODE, KB>::FD>& sh, const U32x4 (&xr)[KB][N],
-    U32x4 (&xn)[KB][N], const bf16x8_t (&wreg)[KB][N][PersistPlan<N, MODE, KB>::WR],
-    const unsigned char* lds_w, int64_t tile, int64_t prev, int64_t ntiles, int slot, int tid,
-    int lane, int wave) {
-  using P = PersistPlan<N, MODE, KB>;
+    const PreArgs& a, PersistShared<N, PersistPlan<N, MODE, KB>::FD>& sh, PersistNorm<NORM, KB>& nsh,
+    const U32x4 (&xr)[KB][N], U32x4 (&xn)[KB][N],
+    const bf16x8_t (&wreg)[KB][N][PersistPlan<N, MODE, KB, NORM>::WR], const unsigned char* lds_w,
+    int64_t tile, int64_t prev, int64_t ntiles, int slot, int tid, int lane, int wave) {
+  using P = PersistPlan<N, MODE, KB, NORM>;
   const int r = lane & 15;
   const int g = lane >> 4;
   const auto rn = x_tile_rsrc(static_cast<const uint16_t*>(a.x), tile + gridDim.x, ntiles, a.M,
                               N * a.C);
   persist_load_part<N, KB, 0, P::B1>(xn, rn, a.C, wave, r, g);
-  persist_partials<N, MODE, KB>(a, sh, xr, wreg, lds_w, slot, lane, wave);
+  persist_partials<N, MODE, KB, NORM>(a, sh, xr, wreg, lds_w, slot, lane, wave);
   __syncthreads();
   persist_load_part<N, KB, P::B1, P::B2>(xn, rn, a.C, wave, r, g);
   if constexpr (MODE == kFull) {
@@ -413,8 +481,13 @@ __device__ __forceinline__ void persist_step(
     hlo[i] = pack_lo(h);
     hhi[i] = pack_hi(h);
   }
-  persist_preagg<N, KB>(a, xr, hlo, hhi, tile, lane, wave);
+  persist_preagg<N, KB, NORM>(a, xr, hlo, hhi, tile, lane, wave, nsh, slot);
   persist_load_part<N, KB, P::B2, KB>(xn, rn, a.C, wave, r, g);
+  // The previous tile's normed stores, here where this tile's x registers are
+  // free (its partials became visible at this step's barrier).
+  if constexpr (NORM) {
+    if (prev >= 0) persist_norm_store<N, KB>(a, nsh, prev, slot ^ 1, lane, wave);
+  }
 }
 
 // Gate parameter of thread tid (raw bits; converted once the streaming loads
@@ -461,11 +534,12 @@ __device__ __forceinline__ float convert_param(const RawParam& rp, int dt) {
   return rp.used ? v : 0.f;
 }
 
-template <int N, int MODE, int KB>
+template <int N, int MODE, int KB, bool NORM>
 __global__ __launch_bounds__(kPersistWaves * 64) void pre_persist_kernel(PreArgs a, int64_t ntiles) {
-  using P = PersistPlan<N, MODE, KB>;
+  using P = PersistPlan<N, MODE, KB, NORM>;
   static_assert(P::SHARED + 256 + (P::NLDS > 0 ? P::LDS_W : 0) <= kLdsBytes, "LDS budget");
   __shared__ PersistShared<N, P::FD> sh;
+  __shared__ PersistNorm<NORM, KB> nsh;
   __shared__ __attribute__((aligned(16))) unsigned char lds_w[P::LDS_W];
 
   const int tid = threadIdx.x;
@@ -485,6 +559,15 @@ __global__ __launch_bounds__(kPersistWaves * 64) void pre_persist_kernel(PreArgs
   // phi tile write into the (not yet used) partials area.  The second tile's
   // loads go out during the first step.
   const RawParam rp = load_gate_param<N, MODE>(a, tid);
+  float gain[2] = {0.f, 0.f};  // norm gain of columns tid and tid + 512 (branch-free loads)
+  if constexpr (NORM) {
+#pragma unroll
+    for (int h = 0; h < 2; ++h) {
+      const int c = tid + h * kPersistWaves * 64;
+      const float v = ld_any(a.norm_w, c < C ? c : 0, a.norm_dtype);
+      gain[h] = c < C ? v : 0.f;
+    }
+  }
 
   const uint32_t wbytes = (uint32_t)(N * NCB * P::NT) * 64u * 16u;
   const auto wr = make_rsrc(a.phi_packed, wbytes);
@@ -531,6 +614,10 @@ __global__ __launch_bounds__(kPersistWaves * 64) void pre_persist_kernel(PreArgs
 
   if (tid == 0) sh.zero = U32x4{{0u, 0u, 0u, 0u}};
   if (tid < GateParams<N>::kCount) sh.prm[tid] = convert_param(rp, a.param_dtype);
+  if constexpr (NORM) {
+#pragma unroll
+    for (int h = 0; h < 2; ++h) nsh.gain[tid + h * kPersistWaves * 64] = gain[h];
+  }
   __syncthreads();  // gate parameters, zero block and phi tiles visible
 
   // Pairs of steps (xa computes while xb loads, then the reverse), then the
@@ -543,23 +630,25 @@ __global__ __launch_bounds__(kPersistWaves * 64) void pre_persist_kernel(PreArgs
   int slot = 0;
   int64_t k = 0;
   for (; k + 2 <= my_tiles; k += 2) {  // uniform across the workgroup
-    persist_step<N, MODE, KB>(a, sh, xa, xb, wreg, lds_w, tile, prev, ntiles, slot, tid, lane, wave);
+    persist_step<N, MODE, KB, NORM>(a, sh, nsh, xa, xb, wreg, lds_w, tile, prev, ntiles, slot, tid, lane, wave);
     prev = tile;
     slot ^= 1;
     tile += step;
-    persist_step<N, MODE, KB>(a, sh, xb, xa, wreg, lds_w, tile, prev, ntiles, slot, tid, lane, wave);
+    persist_step<N, MODE, KB, NORM>(a, sh, nsh, xb, xa, wreg, lds_w, tile, prev, ntiles, slot, tid, lane, wave);
     prev = tile;
     slot ^= 1;
     tile += step;
   }
   if (k < my_tiles) {
-    persist_step<N, MODE, KB>(a, sh, xa, xb, wreg, lds_w, tile, prev, ntiles, slot, tid, lane, wave);
+    persist_step<N, MODE, KB, NORM>(a, sh, nsh, xa, xb, wreg, lds_w, tile, prev, ntiles, slot, tid, lane, wave);
     prev = tile;
     slot ^= 1;
   }
-  // The last tile's Sinkhorn, once every gate wave has written its logits.
+  // The last tile's Sinkhorn, once every gate wave has written its logits,
+  // and its normed stores, once every wave has written its partial.
+  if constexpr (MODE == kFull || NORM) __syncthreads();
+  if constexpr (NORM) persist_norm_store<N, KB>(a, nsh, prev, slot ^ 1, lane, wave);
   if constexpr (MODE == kFull) {
-    __syncthreads();
     if (wave < P::SK_WAVES && a.h_res) persist_sinkhorn<N>(a, sh.hres[slot ^ 1], prev, tid);
   }
 }
@@ -575,8 +664,12 @@ template <int N, int MODE, int KB>
 hipError_t launch_pre_persist_inst(const PreArgs& a, int num_cus, hipStream_t s) {
   const int64_t ntiles = (a.M + kTokTile - 1) / kTokTile;
   const int64_t grid = ntiles < num_cus ? ntiles : num_cus;
-  hipLaunchKernelGGL((pre_persist_kernel<N, MODE, KB>), dim3((unsigned)grid),
-                     dim3(kPersistWaves * 64), 0, s, a, ntiles);
+  if (a.norm_w)
+    hipLaunchKernelGGL((pre_persist_kernel<N, MODE, KB, true>), dim3((unsigned)grid),
+                       dim3(kPersistWaves * 64), 0, s, a, ntiles);
+  else
+    hipLaunchKernelGGL((pre_persist_kernel<N, MODE, KB, false>), dim3((unsigned)grid),
+                       dim3(kPersistWaves * 64), 0, s, a, ntiles);
   return hipGetLastError();
 }
 

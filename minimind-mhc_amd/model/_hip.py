@@ -44,6 +44,20 @@ _SIGNATURES = {
     "mhc_post_fwd": (_I, [_P, _I, _P, _P, _I, _P, _I, _P, _I64, _I, _I, _P]),
     "mhc_post_nohres_fwd": (_I, [_P, _I, _P, _I, _P, _I, _P, _I64, _I, _I, _P]),
     "mhc_head_fwd": (_I, [_P, _I, _P, _I, _P, _P, _P, _I, _P, _P, _P, _I64, _I, _I, _F, _F, _P]),
+    "mhc_pre_norm_fwd": (_I, [_P, _I, _P, _I, _P,
+                              _P, _P, _P, _P, _P, _P, _I,
+                              _P, _P, _P, _P, _P, _P, _P,
+                              _I64, _I, _I, _F, _F, _F, _I, _F,
+                              _P, _I, _F, _P]),                # norm weight, dtype, eps, stream
+    "mhc_pre_nohres_norm_fwd": (_I, [_P, _I, _P, _I, _P,
+                                     _P, _P, _P, _P, _I,
+                                     _P, _P, _P, _P, _P,
+                                     _I64, _I, _I, _F, _F, _F,
+                                     _P, _I, _F, _P]),
+    "mhc_head_norm_fwd": (_I, [_P, _I, _P, _I, _P, _P, _P, _I, _P, _P, _P, _I64, _I, _I, _F, _F,
+                               _P, _I, _F, _P]),
+    "mhc_expand_norm_fwd": (_I, [_P, _I, _P, _I, _P, _I64, _I, _I, _F, _P]),
+    "mhc_pre_token_threshold": (_I64, [_I64]),
     "mhc_sinkhorn_fwd": (_I, [_P, _P, _I, _I64, _I, _I, _F, _P]),
     "mhc_stream_expand_fwd": (_I, [_P, _P, _I, _I64, _I, _I, _P]),
     "mhc_post_bwd": (_I, [_P, _I, _P, _P, _I, _P, _I, _P, _P, _P, _P, _P, _I64, _I, _I, _P]),
@@ -64,7 +78,7 @@ _SIGNATURES = {
     "mhc_sinkhorn_bwd": (_I, [_P, _I, _P, _I, _P, _I, _I64, _I, _I, _F, _P]),
 }
 
-ABI_VERSION = 2
+ABI_VERSION = 3
 _lib: Optional[ctypes.CDLL] = None
 
 

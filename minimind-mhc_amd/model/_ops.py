@@ -70,10 +70,25 @@ def _rows(x_flat: torch.Tensor, NC: int) -> torch.Tensor:
     return x_flat.contiguous().view(-1, NC)
 
 
+def _norm_args(norm, C: int, dev):
+    """(weight pointer, dtype tag, eps, keep-alive tensor) of an RMSNorm over C
+    fused into a pre-phase / head launch, or Nones without one."""
+    if norm is None:
+        return None, 0, 0.0, None
+    w, eps = norm
+    H.require_device(w)
+    wc = w.detach().contiguous()
+    _check_numel("norm weight", wc, C)
+    if wc.device != dev:
+        raise ValueError("mhc_amd: norm weight is on another device")
+    return wc.data_ptr(), H.dtype_tag(wc), float(eps), wc
+
+
 def pre_full(x_flat, phi, packed, a_pre, b_pre, a_post, b_post, a_res, b_res, n, C,
              post_mult, pre_eps, rms_eps, sk_iters, sk_eps, *, sinkhorn=True,
-             want_h_pre=False, want_raw=False, want_saved=False):
-    """Fused pre phase (+ Sinkhorn).  Returns a dict of [M, ...] tensors."""
+             want_h_pre=False, want_raw=False, want_saved=False, norm=None):
+    """Fused pre phase (+ Sinkhorn).  Returns a dict of [M, ...] tensors.
+    norm=(weight [C], eps): "sub_in" is RMSNorm(pre-aggregate) instead."""
     dev = H.require_device(x_flat, phi, a_pre, b_pre, a_post, b_post, a_res, b_res)
     NC = n * C
     FD = 2 * n + n * n
@@ -97,20 +112,23 @@ def pre_full(x_flat, phi, packed, a_pre, b_pre, a_post, b_post, a_res, b_res, n,
         "inv_rms": torch.empty(M, dtype=torch.float32, device=dev) if want_saved else None,
         "mixes_raw": torch.empty(M, FD, dtype=torch.float32, device=dev) if want_saved else None,
     }
-    rc = H.load().mhc_pre_fwd(
-        x2.data_ptr(), H.dtype_tag(x2), phi_c.data_ptr(), H.dtype_tag(phi_c), H.ptr(packed),
-        a_pre.data_ptr(), b_pre.data_ptr(), a_post.data_ptr(), b_post.data_ptr(),
-        a_res.data_ptr(), b_res.data_ptr(), H.dtype_tag(a_pre),
-        out["sub_in"].data_ptr(), H.ptr(out["h_pre"]), out["h_post"].data_ptr(),
-        H.ptr(out["h_res_raw"]), H.ptr(out["h_res"]), H.ptr(out["inv_rms"]),
-        H.ptr(out["mixes_raw"]), M, n, C, float(post_mult), float(pre_eps), float(rms_eps),
-        int(sk_iters), float(sk_eps), H.stream(dev))
-    H.check(rc, "mhc_pre_fwd")
+    args = (x2.data_ptr(), H.dtype_tag(x2), phi_c.data_ptr(), H.dtype_tag(phi_c), H.ptr(packed),
+            a_pre.data_ptr(), b_pre.data_ptr(), a_post.data_ptr(), b_post.data_ptr(),
+            a_res.data_ptr(), b_res.data_ptr(), H.dtype_tag(a_pre),
+            out["sub_in"].data_ptr(), H.ptr(out["h_pre"]), out["h_post"].data_ptr(),
+            H.ptr(out["h_res_raw"]), H.ptr(out["h_res"]), H.ptr(out["inv_rms"]),
+            H.ptr(out["mixes_raw"]), M, n, C, float(post_mult), float(pre_eps), float(rms_eps),
+            int(sk_iters), float(sk_eps))
+    if norm is None:
+        H.check(H.load().mhc_pre_fwd(*args, H.stream(dev)), "mhc_pre_fwd")
+    else:
+        wp, wdt, weps, _keep = _norm_args(norm, C, dev)
+        H.check(H.load().mhc_pre_norm_fwd(*args, wp, wdt, weps, H.stream(dev)), "mhc_pre_norm_fwd")
     return out
 
 
 def pre_nohres(x_flat, phi, packed, a_pre, b_pre, a_post, b_post, n, C, post_mult, pre_eps,
-               rms_eps, *, want_h_pre=False, want_saved=False):
+               rms_eps, *, want_h_pre=False, want_saved=False, norm=None):
     dev = H.require_device(x_flat, phi, a_pre, b_pre, a_post, b_post)
     NC = n * C
     FD = 2 * n
@@ -131,18 +149,24 @@ def pre_nohres(x_flat, phi, packed, a_pre, b_pre, a_post, b_post, n, C, post_mul
         "inv_rms": torch.empty(M, dtype=torch.float32, device=dev) if want_saved else None,
         "mixes_raw": torch.empty(M, FD, dtype=torch.float32, device=dev) if want_saved else None,
     }
-    rc = H.load().mhc_pre_nohres_fwd(
-        x2.data_ptr(), H.dtype_tag(x2), phi_c.data_ptr(), H.dtype_tag(phi_c), H.ptr(packed),
-        a_pre.data_ptr(), b_pre.data_ptr(), a_post.data_ptr(), b_post.data_ptr(),
-        H.dtype_tag(a_pre), out["sub_in"].data_ptr(), H.ptr(out["h_pre"]),
-        out["h_post"].data_ptr(), H.ptr(out["inv_rms"]), H.ptr(out["mixes_raw"]),
-        M, n, C, float(post_mult), float(pre_eps), float(rms_eps), H.stream(dev))
-    H.check(rc, "mhc_pre_nohres_fwd")
+    args = (x2.data_ptr(), H.dtype_tag(x2), phi_c.data_ptr(), H.dtype_tag(phi_c), H.ptr(packed),
+            a_pre.data_ptr(), b_pre.data_ptr(), a_post.data_ptr(), b_post.data_ptr(),
+            H.dtype_tag(a_pre), out["sub_in"].data_ptr(), H.ptr(out["h_pre"]),
+            out["h_post"].data_ptr(), H.ptr(out["inv_rms"]), H.ptr(out["mixes_raw"]),
+            M, n, C, float(post_mult), float(pre_eps), float(rms_eps))
+    if norm is None:
+        H.check(H.load().mhc_pre_nohres_fwd(*args, H.stream(dev)), "mhc_pre_nohres_fwd")
+    else:
+        wp, wdt, weps, _keep = _norm_args(norm, C, dev)
+        H.check(H.load().mhc_pre_nohres_norm_fwd(*args, wp, wdt, weps, H.stream(dev)),
+                "mhc_pre_nohres_norm_fwd")
     return out
 
 
-def head(x_flat, phi, packed, alpha, bias, n, C, pre_eps, rms_eps, *, want_saved=False):
-    """MHCHead forward; n == 1 is the plain RMSNorm (phi/alpha/bias unused)."""
+def head(x_flat, phi, packed, alpha, bias, n, C, pre_eps, rms_eps, *, want_saved=False,
+         norm=None):
+    """MHCHead forward; n == 1 is the plain RMSNorm (phi/alpha/bias unused).
+    norm=(weight [C], eps): the model's final RMSNorm applied in the same launch."""
     NC = n * C
     x2 = _rows(x_flat, NC)
     M = x2.shape[0]
@@ -163,11 +187,14 @@ def head(x_flat, phi, packed, alpha, bias, n, C, pre_eps, rms_eps, *, want_saved
     out = torch.empty(M, C, dtype=x2.dtype, device=dev)
     inv = torch.empty(M, dtype=torch.float32, device=dev) if want_saved else None
     mix = torch.empty(M, n, dtype=torch.float32, device=dev) if (want_saved and n > 1) else None
-    rc = H.load().mhc_head_fwd(
-        x2.data_ptr(), H.dtype_tag(x2), phi_p, phi_dt, H.ptr(packed), a_p, b_p, pdt,
-        out.data_ptr(), H.ptr(inv), H.ptr(mix), M, n, C, float(pre_eps), float(rms_eps),
-        H.stream(dev))
-    H.check(rc, "mhc_head_fwd")
+    args = (x2.data_ptr(), H.dtype_tag(x2), phi_p, phi_dt, H.ptr(packed), a_p, b_p, pdt,
+            out.data_ptr(), H.ptr(inv), H.ptr(mix), M, n, C, float(pre_eps), float(rms_eps))
+    if norm is None:
+        H.check(H.load().mhc_head_fwd(*args, H.stream(dev)), "mhc_head_fwd")
+    else:
+        wp, wdt, weps, _keep = _norm_args(norm, C, dev)
+        H.check(H.load().mhc_head_norm_fwd(*args, wp, wdt, weps, H.stream(dev)),
+                "mhc_head_norm_fwd")
     return out, inv, mix
 
 
@@ -209,6 +236,27 @@ def sinkhorn(m: torch.Tensor, iters: int, eps: float) -> torch.Tensor:
                                    int(iters), float(eps), H.stream(dev))
     H.check(rc, "mhc_sinkhorn_fwd")
     return out
+
+
+def expand_norm(x: torch.Tensor, weight: torch.Tensor, eps: float, n: int) -> torch.Tensor:
+    """RMSNorm over the last dim (gain weight) followed by StreamExpand to n
+    copies, one launch: [B, L, C] -> [B, L, n*C]."""
+    dev = H.require_device(x, weight)
+    B, L, C = x.shape
+    xc = x.contiguous()
+    wp, wdt, weps, _keep = _norm_args((weight, eps), C, dev)
+    out = torch.empty(B, L, n * C, dtype=x.dtype, device=dev)
+    rc = H.load().mhc_expand_norm_fwd(xc.data_ptr(), H.dtype_tag(xc), wp, wdt, out.data_ptr(),
+                                      B * L, n, C, weps, H.stream(dev))
+    H.check(rc, "mhc_expand_norm_fwd")
+    return out
+
+
+def pre_token_threshold(max_tokens: int = -1) -> int:
+    """Set (max_tokens >= 0) or query the batch size at or below which the
+    pre-phase launches use the one-workgroup-per-token kernel; returns the
+    previous value."""
+    return int(H.load().mhc_pre_token_threshold(int(max_tokens)))
 
 
 def stream_expand(x: torch.Tensor, n: int) -> torch.Tensor:

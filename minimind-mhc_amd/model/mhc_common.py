@@ -21,6 +21,27 @@ def _is_pow2(n: int) -> bool:
     return n >= 1 and (n & (n - 1)) == 0
 
 
+def fusable_norm(norm, dim: int, x: torch.Tensor, *modules) -> bool:
+    """True when an nn.RMSNorm over `dim` can run inside a HIP launch for this
+    call: a forward without autograd (no grad mode, or nothing requiring grad),
+    an affine norm over exactly (dim,)."""
+    if not isinstance(norm, nn.RMSNorm) or norm.weight is None:
+        return False
+    if tuple(norm.normalized_shape) != (dim,) or not x.is_cuda:
+        return False
+    if torch.is_grad_enabled():
+        if x.requires_grad or norm.weight.requires_grad:
+            return False
+        if any(p.requires_grad for m in modules for p in m.parameters()):
+            return False
+    return True
+
+
+def norm_eps(norm: nn.RMSNorm, x: torch.Tensor) -> float:
+    """nn.RMSNorm's eps (None means the dtype's machine epsilon, as torch uses)."""
+    return float(norm.eps) if norm.eps is not None else float(torch.finfo(x.dtype).eps)
+
+
 class _StreamExpandFn(torch.autograd.Function):
     @staticmethod
     def forward(ctx, x, n):
@@ -45,6 +66,13 @@ class StreamExpand(nn.Module):
         if self.n == 1:
             return x
         return _StreamExpandFn.apply(x, self.n)
+
+    def forward_normed(self, x: torch.Tensor, in_norm: nn.Module) -> torch.Tensor:
+        """self(in_norm(x)), the model's entry (model/model_minimind.py:365):
+        one HIP launch (RMSNorm + n copies) when no autograd is needed."""
+        if fusable_norm(in_norm, self.dim, x):
+            return _ops.expand_norm(x, in_norm.weight, norm_eps(in_norm, x), self.n)
+        return self(in_norm(x))
 
 
 class _MHCHeadFn(torch.autograd.Function):
@@ -120,7 +148,19 @@ class MHCHead(nn.Module):
     def extra_repr(self) -> str:
         return f"n={self.n}, dim={self.dim}, backend=hip-gfx950"
 
-    def forward(self, x_flat: torch.Tensor) -> torch.Tensor:
+    def forward(self, x_flat: torch.Tensor, out_norm: nn.Module = None) -> torch.Tensor:
+        """out_norm: an nn.RMSNorm over dim applied to the head output (the
+        model's final norm, model/model_minimind.py:367-370); without autograd
+        it runs inside the head launch."""
+        if out_norm is not None:
+            if fusable_norm(out_norm, self.dim, x_flat, self):
+                packed = (self._phi_pack.get(self.phi_weight, self.n, self.dim)
+                          if self.n > 1 else None)
+                out, _, _ = _ops.head(x_flat, self.phi_weight, packed, self.alpha, self.bias,
+                                      self.n, self.dim, self.pre_eps, self.eps,
+                                      norm=(out_norm.weight, norm_eps(out_norm, x_flat)))
+                return out.view(*x_flat.shape[:-1], self.dim)
+            return out_norm(self(x_flat))
         if self.n == 1:
             return _RMSFn.apply(x_flat, self.eps)
         packed = self._phi_pack.get(self.phi_weight, self.n, self.dim) if x_flat.is_cuda else None

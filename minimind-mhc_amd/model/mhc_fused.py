@@ -22,6 +22,7 @@ import torch.nn as nn
 
 from . import _ops
 from . import _hip as H
+from .mhc_common import fusable_norm, norm_eps
 
 
 def _is_pow2(n: int) -> bool:
@@ -201,9 +202,28 @@ class MHCConnection_Fused(nn.Module):
                 f"sinkhorn_iters={self.sinkhorn_iters}, post_mult_value={self.post_mult_value}, "
                 f"backend=hip-gfx950")
 
-    def forward(self, x_flat: torch.Tensor, sublayer_fn: Callable) -> torch.Tensor:
-        """PRE (+Sinkhorn, one HIP launch) -> sublayer F -> POST (one HIP launch)."""
+    def forward(self, x_flat: torch.Tensor, sublayer_fn: Callable,
+                in_norm: nn.Module = None) -> torch.Tensor:
+        """PRE (+Sinkhorn, one HIP launch) -> sublayer F -> POST (one HIP launch).
+
+        in_norm (optional, not in the reference signature): an nn.RMSNorm over
+        dim that F applies to its input first, i.e. F(z) = sublayer_fn(in_norm(z)).
+        Without autograd it runs inside the pre launch; otherwise it is applied
+        as a separate op, as when F contains it."""
         packed = self._phi_pack.get(self.phi_weight, self.n, self.dim) if x_flat.is_cuda else None
+        if in_norm is not None:
+            if fusable_norm(in_norm, self.dim, x_flat, self):
+                o = _ops.pre_full(x_flat, self.phi_weight, packed, self.alpha_pre, self.bias_pre,
+                                  self.alpha_post, self.bias_post, self.alpha_res, self.bias_res,
+                                  self.n, self.dim, self.post_mult_value, self.pre_eps, self.eps,
+                                  self.sinkhorn_iters, self.sinkhorn_eps,
+                                  norm=(in_norm.weight, norm_eps(in_norm, x_flat)))
+                B, L, NC = x_flat.shape
+                f_out = sublayer_fn(o["sub_in"].view(B, L, self.dim))
+                out = _ops.post(x_flat, o["h_res"], o["h_post"], f_out, self.n, self.dim)
+                return out.view(B, L, NC)
+            fn = sublayer_fn
+            sublayer_fn = lambda z: fn(in_norm(z))  # noqa: E731
         sublayer_in, h_post, h_res = _PreSinkhornFn.apply(
             x_flat, self.phi_weight, packed,
             self.alpha_pre, self.bias_pre, self.alpha_post, self.bias_post,

@@ -15,6 +15,7 @@ import torch.nn as nn
 
 from . import _ops
 from . import _hip as H
+from .mhc_common import fusable_norm, norm_eps
 
 
 def _is_pow2(n: int) -> bool:
@@ -107,8 +108,23 @@ class MHCConnection_FusedNoHres(nn.Module):
         return (f"n={self.n}, dim={self.dim}, fused_dim={self.fused_dim}, "
                 f"post_mult_value={self.post_mult_value}, backend=hip-gfx950")
 
-    def forward(self, x_flat: torch.Tensor, sublayer_fn: Callable) -> torch.Tensor:
+    def forward(self, x_flat: torch.Tensor, sublayer_fn: Callable,
+                in_norm: nn.Module = None) -> torch.Tensor:
+        """in_norm: as MHCConnection_Fused.forward (F(z) = sublayer_fn(in_norm(z)),
+        fused into the pre launch when no autograd is needed)."""
         packed = self._phi_pack.get(self.phi_weight, self.n, self.dim) if x_flat.is_cuda else None
+        if in_norm is not None:
+            if fusable_norm(in_norm, self.dim, x_flat, self):
+                o = _ops.pre_nohres(x_flat, self.phi_weight, packed, self.alpha_pre, self.bias_pre,
+                                    self.alpha_post, self.bias_post, self.n, self.dim,
+                                    self.post_mult_value, self.pre_eps, self.eps,
+                                    norm=(in_norm.weight, norm_eps(in_norm, x_flat)))
+                B, L, NC = x_flat.shape
+                f_out = sublayer_fn(o["sub_in"].view(B, L, self.dim))
+                out = _ops.post(x_flat, None, o["h_post"], f_out, self.n, self.dim)
+                return out.view(B, L, NC)
+            fn = sublayer_fn
+            sublayer_fn = lambda z: fn(in_norm(z))  # noqa: E731
         sublayer_in, _h_pre, h_post = _PrePhaseFn.apply(
             x_flat, self.phi_weight, self.alpha_pre, self.bias_pre,
             self.alpha_post, self.bias_post,

@@ -13,7 +13,13 @@ Differences from the reference, all outside the mHC path:
     MiniMindForCausalLM a plain nn.Module (no PreTrainedModel/GenerationMixin);
   * the RoPE tables are computed once at construction (the reference
     recomputes them after meta-device init and pays a host sync per forward,
-    model/model_minimind.py:387-389).
+    model/model_minimind.py:387-389);
+  * the norms next to the mHC pieces are handed to them instead of being
+    applied inside F: each sublayer's input RMSNorm goes to its connection
+    (in_norm), the entry RMSNorm to StreamExpand.forward_normed and the final
+    RMSNorm to MHCHead (out_norm).  Without autograd each runs inside the
+    neighbouring HIP launch; with autograd they run as separate ops in the
+    reference's order (model/model_minimind.py:326-336, :365-370).
 """
 from __future__ import annotations
 
@@ -240,17 +246,16 @@ class MiniMindBlock(nn.Module):
         if self.use_mhc:
             holder = [None]
 
-            def attn_fn(z):
-                out, kv = self.self_attn(self.attn_in_norm(z), position_embeddings,
-                                         past_key_value, use_cache, attention_mask)
+            # F(z) = sublayer(in_norm(z)); the connection applies in_norm (inside
+            # its pre launch when no autograd is needed).
+            def attn_fn(zn):
+                out, kv = self.self_attn(zn, position_embeddings, past_key_value, use_cache,
+                                         attention_mask)
                 holder[0] = kv
                 return out
 
-            def mlp_fn(z):
-                return self.mlp(self.ffn_in_norm(z))
-
-            hidden_states = self.attn_mhc(hidden_states, attn_fn)
-            hidden_states = self.mlp_mhc(hidden_states, mlp_fn)
+            hidden_states = self.attn_mhc(hidden_states, attn_fn, in_norm=self.attn_in_norm)
+            hidden_states = self.mlp_mhc(hidden_states, self.mlp, in_norm=self.ffn_in_norm)
             return hidden_states, holder[0]
         attn_out, kv = self.self_attn(self.attn_in_norm(hidden_states), position_embeddings,
                                       past_key_value, use_cache, attention_mask)
@@ -290,14 +295,20 @@ class MiniMindModel(nn.Module):
         past_key_values = past_key_values or [None] * len(self.layers)
         start = past_key_values[0][0].shape[1] if past_key_values[0] is not None else 0
         h = self.dropout(self.embed_tokens(input_ids))
-        h = self.embed_up_norm(h)
+        if self.config.use_mhc:  # RMSNorm + StreamExpand, one launch without autograd
+            h = self.embed_up_norm[1].forward_normed(h, self.embed_up_norm[0])
+        else:
+            h = self.embed_up_norm(h)
         pos = (self.freqs_cos[start:start + seq_len], self.freqs_sin[start:start + seq_len])
         presents = []
         for layer, pkv in zip(self.layers, past_key_values):
             h, present = layer(h, pos, past_key_value=pkv, use_cache=use_cache,
                                attention_mask=attention_mask)
             presents.append(present)
-        h = self.norm(h)
+        if self.config.use_mhc:  # MHCHead + final RMSNorm, one launch without autograd
+            h = self.norm[0](h, out_norm=self.norm[1])
+        else:
+            h = self.norm(h)
         aux = sum([l.mlp.aux_loss for l in self.layers if isinstance(l.mlp, MOEFeedForward)],
                   h.new_zeros(1).squeeze())
         return h, presents, aux

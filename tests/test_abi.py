@@ -72,3 +72,31 @@ def test_validation_errors_need_no_device(lib):
     # empty problems succeed without launching
     assert lib.mhc_sinkhorn_fwd(ctypes.c_void_p(16), ctypes.c_void_p(32), 0, 0, 4, 20, 1e-6, None) == 0
     assert lib.mhc_phi_pack(None, 0, None, 4, 768, 0, None) == 1  # fp32 phi has no MFMA image
+
+
+def test_norm_entry_points_validate_without_device(lib):
+    p = ctypes.c_void_p(256)
+    # the *_norm_fwd variants require the gain
+    rc = lib.mhc_pre_norm_fwd(p, 1, p, 1, None, p, p, p, p, p, p, 1, p, None, p, None, p, None,
+                              None, 16, 4, 64, 2.0, 1e-6, 1e-6, 20, 1e-6, None, 1, 1e-6, None)
+    assert rc == 1 and b"norm_weight is required" in lib.mhc_last_error()
+    rc = lib.mhc_pre_nohres_norm_fwd(p, 1, p, 1, None, p, p, p, p, 1, p, None, p, None, None,
+                                     16, 4, 64, 2.0, 1e-6, 1e-6, None, 1, 1e-6, None)
+    assert rc == 1 and b"norm_weight is required" in lib.mhc_last_error()
+    rc = lib.mhc_head_norm_fwd(p, 1, p, 1, None, p, p, 1, p, None, None, 16, 4, 64, 1e-6, 1e-6,
+                               p, 7, 1e-6, None)
+    assert rc == 1 and b"bad norm dtype" in lib.mhc_last_error()
+    rc = lib.mhc_expand_norm_fwd(p, 1, p, 1, p, 16, 4, 64, -1.0, None)
+    assert rc == 1 and b"eps" in lib.mhc_last_error()
+    rc = lib.mhc_expand_norm_fwd(p, 1, p, 1, p, 16, 0, 64, 1e-6, None)
+    assert rc == 1 and b"bad shape" in lib.mhc_last_error()
+    assert lib.mhc_expand_norm_fwd(None, 1, None, 1, None, 0, 4, 64, 1e-6, None) == 0  # empty
+
+
+def test_token_threshold_round_trip(lib):
+    old = lib.mhc_pre_token_threshold(-1)
+    assert old >= 0
+    assert lib.mhc_pre_token_threshold(17) == old
+    assert lib.mhc_pre_token_threshold(-1) == 17
+    assert lib.mhc_pre_token_threshold(old) == 17
+    assert lib.mhc_pre_token_threshold(-1) == old

@@ -1,0 +1,208 @@
+"""GPU tests of the decode-size pre kernel and of the RMSNorm fusions.
+
+* The one-workgroup-per-token pre kernel and the persistent kernel, each
+  forced through mhc_pre_token_threshold, against the CPU oracle at the
+  BASELINE bars (1e-2 bf16), on the batch sizes either side of the switch.
+* mhc_pre_norm_fwd / mhc_pre_nohres_norm_fwd / mhc_head_norm_fwd: every
+  output but the main one equals the plain entry point's bit for bit, and the
+  main output is RMSNorm(plain output) (the reference applies nn.RMSNorm to
+  the rounded pre-aggregate, model/model_minimind.py:330, :336, :367-370),
+  computed here in fp32 by torch: within one rounding step of the stream
+  dtype (2^-7 relative in bf16, 2^-10 in fp16) or 1e-5 in fp32.
+* mhc_expand_norm_fwd against torch's rms_norm + expand
+  (model/model_minimind.py:365; model/mhc_common.py:115-119), same bars.
+Shapes cover every kernel: token (M <= threshold), persistent (n <= 4),
+K-streamed (n = 8) and generic (fp32, C > 1024, C % 8 != 0)."""
+from __future__ import annotations
+
+import pytest
+import torch
+
+from oracle import mhc_ref as R
+from tests._util import make_params, maxabs, maxrel, tol
+
+pytestmark = pytest.mark.gpu
+
+from model import _hip as H  # noqa: E402
+from model import _ops  # noqa: E402
+
+_MODE = {"full": H.MODE_FULL, "nohres": H.MODE_NOHRES, "head": H.MODE_HEAD}
+
+
+@pytest.fixture
+def token_threshold():
+    """Set the token-kernel threshold for one test, restore it afterwards."""
+    old = _ops.pre_token_threshold(-1)
+    yield _ops.pre_token_threshold
+    _ops.pre_token_threshold(old)
+
+
+def _params(kind, n, C, dtype, seed):
+    g = torch.Generator().manual_seed(seed)
+    return g, make_params(kind, n, C, dtype, g, stress=True)
+
+
+def _run(kind, x, p, n, C, dev, norm=None, iters=20):
+    pd = {k: v.to(dev) for k, v in p.items()}
+    packed = _ops.PhiPack(_MODE[kind]).get(pd["phi_weight"], n, C) if n > 1 or kind != "head" else None
+    xd = x.to(dev)
+    if kind == "full":
+        o = _ops.pre_full(xd, pd["phi_weight"], packed, pd["alpha_pre"], pd["bias_pre"],
+                          pd["alpha_post"], pd["bias_post"], pd["alpha_res"], pd["bias_res"], n, C,
+                          2.0, 1e-6, 1e-6, iters, 1e-6, want_h_pre=True, want_raw=True,
+                          want_saved=True, norm=norm)
+    elif kind == "nohres":
+        o = _ops.pre_nohres(xd, pd["phi_weight"], packed, pd["alpha_pre"], pd["bias_pre"],
+                            pd["alpha_post"], pd["bias_post"], n, C, 2.0, 1e-6, 1e-6,
+                            want_h_pre=True, want_saved=True, norm=norm)
+    else:
+        out, inv, mix = _ops.head(xd, pd.get("phi_weight"), packed, pd.get("alpha"),
+                                  pd.get("bias"), n, C, 1e-6, 1e-6, want_saved=True, norm=norm)
+        o = {"sub_in": out, "inv_rms": inv, "mixes_raw": mix}
+    torch.cuda.synchronize()
+    return o
+
+
+# ------------------------------------------------------- token vs persistent
+
+@pytest.mark.parametrize("path", ["token", "persistent"])
+@pytest.mark.parametrize("n,C", [(4, 768), (2, 768), (2, 256), (1, 128), (2, 200), (2, 1024)])
+@pytest.mark.parametrize("M", [1, 17, 64, 300, 600])
+def test_pre_full_token_and_persistent_vs_oracle(dev, token_threshold, path, n, C, M):
+    token_threshold(1 << 40 if path == "token" else 0)
+    g, p = _params("full", n, C, torch.bfloat16, 7 * n + C + M)
+    x = torch.randn(1, M, n * C, generator=g).to(torch.bfloat16)
+    print(f"pre {path} n={n} C={C} M={M}", flush=True)
+    o = _run("full", x, p, n, C, dev)
+    sub, h_pre, h_post, h_raw, inv, mixes = R.pre_full(x, p, n, C)
+    h_res = R.sinkhorn(h_raw.float(), 20, 1e-6).to(torch.bfloat16)
+    bar = tol(torch.bfloat16)
+    assert maxrel(h_pre[0], o["h_pre"]) <= bar
+    assert maxrel(h_post[0], o["h_post"]) <= bar
+    # The pre-aggregate is pinned on the kernel's own h_pre (model/mhc_fused.py:556-557
+    # applied by the oracle's formula): the oracle rounds x_norm to bf16 before the
+    # projection (:845) and the kernels do not, which can move an h_pre by one ulp
+    # and the pre-aggregate by a little more than the 1e-2 bar on a few tokens.
+    sub_k = (o["h_pre"].cpu().view(M, n, 1) * x.view(M, n, C)).sum(dim=-2)
+    assert maxrel(sub_k, o["sub_in"]) <= 2.0 ** -7
+    assert maxrel(sub[0], o["sub_in"]) <= 2e-2
+    assert maxrel(h_raw[0], o["h_res_raw"]) <= 2e-2
+    assert maxrel(inv[0], o["inv_rms"]) <= 1e-5
+    assert maxrel(mixes[0], o["mixes_raw"]) <= 2e-2
+    assert maxabs(h_res[0], o["h_res"]) <= 1e-2
+
+
+@pytest.mark.parametrize("kind,n", [("nohres", 2), ("nohres", 1), ("head", 2), ("head", 4)])
+@pytest.mark.parametrize("M", [3, 64])
+def test_token_kernel_other_modes_vs_oracle(dev, token_threshold, kind, n, M):
+    token_threshold(1 << 40)
+    C = 768
+    g, p = _params(kind, n, C, torch.bfloat16, 11 * n + M)
+    x = torch.randn(1, M, n * C, generator=g).to(torch.bfloat16)
+    o = _run(kind, x, p, n, C, dev)
+    bar = tol(torch.bfloat16)
+    if kind == "nohres":
+        sub, h_pre, h_post, inv, mixes = R.pre_nohres(x, p, n, C)
+        assert maxrel(sub[0], o["sub_in"]) <= bar
+        assert maxrel(h_pre[0], o["h_pre"]) <= bar
+        assert maxrel(h_post[0], o["h_post"]) <= bar
+    else:
+        ref = R.head(x, p, n, C)
+        assert maxrel(ref[0], o["sub_in"]) <= bar
+
+
+def test_token_threshold_switches_kernels_consistently(dev, token_threshold):
+    """At one batch size both kernels give the same rounding-level result."""
+    n, C, M = 2, 768, 128
+    g, p = _params("full", n, C, torch.bfloat16, 3)
+    x = torch.randn(1, M, n * C, generator=g).to(torch.bfloat16)
+    token_threshold(1 << 40)
+    a = _run("full", x, p, n, C, dev)
+    token_threshold(0)
+    b = _run("full", x, p, n, C, dev)
+    assert maxrel(b["mixes_raw"], a["mixes_raw"]) <= 1e-5
+    assert maxrel(b["inv_rms"], a["inv_rms"]) <= 1e-6
+    for k in ("sub_in", "h_post", "h_res"):
+        assert maxrel(b[k], a[k]) <= 1e-2, k
+
+
+# ------------------------------------------------------------- fused norms
+
+def _norm_ref(s: torch.Tensor, w: torch.Tensor, eps: float) -> torch.Tensor:
+    sf = s.float()
+    return sf * torch.rsqrt(sf.pow(2).mean(-1, keepdim=True) + eps) * w.float()
+
+
+def _assert_rounded_close(got: torch.Tensor, ref: torch.Tensor, dtype) -> None:
+    rel = {torch.bfloat16: 2.0 ** -7, torch.float16: 2.0 ** -10, torch.float32: 1e-5}[dtype]
+    err = (got.float() - ref).abs()
+    lim = rel * ref.abs() + 1e-6
+    bad = (err > lim).sum().item()
+    assert bad == 0, f"{bad} elements off by more than one rounding step (max err {err.max().item()})"
+
+
+CASES = [  # (kind, n, C, M, dtype): token, persistent, K-streamed and generic kernels
+    ("full", 4, 768, 37, torch.bfloat16), ("full", 4, 768, 1000, torch.bfloat16),
+    ("full", 2, 768, 37, torch.bfloat16), ("nohres", 2, 256, 9, torch.bfloat16),
+    ("head", 2, 768, 5, torch.bfloat16),
+    ("full", 8, 768, 100, torch.bfloat16), ("full", 2, 64, 300, torch.bfloat16),
+    ("full", 1, 64, 50, torch.bfloat16), ("full", 4, 768, 37, torch.float32),
+    ("full", 4, 200, 20, torch.bfloat16), ("full", 4, 200, 600, torch.bfloat16),
+    ("full", 4, 1032, 40, torch.bfloat16), ("full", 4, 1024, 700, torch.bfloat16),
+    ("nohres", 4, 768, 37, torch.bfloat16), ("nohres", 4, 768, 1000, torch.bfloat16),
+    ("nohres", 8, 768, 70, torch.bfloat16), ("nohres", 2, 96, 50, torch.float16),
+    ("head", 4, 768, 37, torch.bfloat16), ("head", 4, 768, 1000, torch.bfloat16),
+    ("head", 8, 768, 100, torch.bfloat16), ("head", 1, 64, 50, torch.bfloat16),
+    ("head", 1, 64, 50, torch.float32),
+]
+
+
+@pytest.mark.parametrize("kind,n,C,M,dtype", CASES)
+@pytest.mark.parametrize("gain_f32", [False, True])
+def test_fused_norm_matches_plain_then_rmsnorm(dev, kind, n, C, M, dtype, gain_f32):
+    g, p = _params(kind, n, C, dtype, 13 * n + C + M)
+    x = torch.randn(1, M, n * C, generator=g).to(dtype)
+    w = (1.0 + 0.5 * torch.randn(C, generator=g)).to(torch.float32 if gain_f32 else dtype).to(dev)
+    eps = 1e-6
+    print(f"norm {kind} n={n} C={C} M={M} {dtype} gain_f32={gain_f32}", flush=True)
+    plain = _run(kind, x, p, n, C, dev)
+    fused = _run(kind, x, p, n, C, dev, norm=(w, eps))
+    for k, v in plain.items():
+        if k != "sub_in" and v is not None:
+            assert torch.equal(v, fused[k]), k
+    _assert_rounded_close(fused["sub_in"], _norm_ref(plain["sub_in"], w, eps), dtype)
+
+
+@pytest.mark.parametrize("M", [1, 17, 300])
+def test_fused_norm_vs_oracle_then_rmsnorm(dev, M):
+    """The fused output against the oracle's pre-aggregate normed on the CPU
+    (BASELINE bf16 bar)."""
+    n, C = 4, 768
+    g, p = _params("full", n, C, torch.bfloat16, 29 + M)
+    x = torch.randn(1, M, n * C, generator=g).to(torch.bfloat16)
+    w = (1.0 + 0.5 * torch.randn(C, generator=g)).to(torch.bfloat16)
+    fused = _run("full", x, p, n, C, dev, norm=(w.to(dev), 1e-6))
+    sub = R.pre_full(x, p, n, C)[0][0]
+    ref = torch.nn.functional.rms_norm(sub.float(), (C,), w.float(), 1e-6)
+    assert maxrel(ref, fused["sub_in"]) <= tol(torch.bfloat16)
+
+
+@pytest.mark.parametrize("n,C,M,dtype", [(4, 768, 100, torch.bfloat16), (1, 64, 7, torch.float32),
+                                         (8, 200, 33, torch.float16), (2, 100, 5, torch.bfloat16),
+                                         (4, 768, 8192, torch.bfloat16)])
+def test_expand_norm_matches_torch(dev, n, C, M, dtype):
+    g = torch.Generator().manual_seed(M + C)
+    x = torch.randn(1, M, C, generator=g).to(dtype).to(dev)
+    w = (1.0 + 0.5 * torch.randn(C, generator=g)).to(dtype).to(dev)
+    out = _ops.expand_norm(x, w, 1e-6, n)
+    torch.cuda.synchronize()
+    ref = _norm_ref(x, w, 1e-6)
+    assert out.shape == (1, M, n * C)
+    for i in range(n):
+        _assert_rounded_close(out[..., i * C:(i + 1) * C], ref, dtype)
+
+
+def test_expand_norm_rejects_wrong_gain(dev):
+    x = torch.randn(1, 4, 64, device=dev, dtype=torch.bfloat16)
+    with pytest.raises(ValueError, match="norm weight"):
+        _ops.expand_norm(x, torch.ones(32, device=dev, dtype=torch.bfloat16), 1e-6, 4)

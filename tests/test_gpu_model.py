@@ -45,29 +45,37 @@ def _model(cfg: MiniMindConfig, seed: int = 0) -> MiniMindForCausalLM:
     return m.eval()
 
 
+def _with_norm(f, norm):
+    """F(z) = f(norm(z)): the reference's sublayer closure (model/model_minimind.py:326-336)."""
+    return f if norm is None else (lambda z: f(norm(z)))
+
+
 def _oracle_copy(model: MiniMindForCausalLM) -> MiniMindForCausalLM:
-    """Same weights, fp32 on the CPU, every mHC module's forward the oracle's."""
+    """Same weights, fp32 on the CPU, every mHC module's forward the oracle's
+    (the norms handed to the mHC modules applied as separate torch ops, in the
+    reference's order)."""
     ref = MiniMindForCausalLM(model.config)
     ref.load_state_dict({k: v.detach().float().cpu() for k, v in model.state_dict().items()})
     for mod in ref.modules():
         if isinstance(mod, MHCConnection_Fused):
-            def fwd(self, x, f):
-                return R.mhc_full_forward(x, R.module_params(self), f, self.n, self.dim,
-                                          eps=self.eps, pre_eps=self.pre_eps,
+            def fwd(self, x, f, in_norm=None):
+                return R.mhc_full_forward(x, R.module_params(self), _with_norm(f, in_norm), self.n,
+                                          self.dim, eps=self.eps, pre_eps=self.pre_eps,
                                           post_mult=self.post_mult_value,
                                           sinkhorn_iters=self.sinkhorn_iters,
                                           sinkhorn_eps=self.sinkhorn_eps)["out"]
             mod.forward = types.MethodType(fwd, mod)
         elif isinstance(mod, MHCConnection_FusedNoHres):
-            def fwd(self, x, f):
-                return R.mhc_nohres_forward(x, R.module_params(self), f, self.n, self.dim,
-                                            eps=self.eps, pre_eps=self.pre_eps,
+            def fwd(self, x, f, in_norm=None):
+                return R.mhc_nohres_forward(x, R.module_params(self), _with_norm(f, in_norm),
+                                            self.n, self.dim, eps=self.eps, pre_eps=self.pre_eps,
                                             post_mult=self.post_mult_value)["out"]
             mod.forward = types.MethodType(fwd, mod)
         elif isinstance(mod, MHCHead):
-            def fwd(self, x):
-                return R.head(x, R.module_params(self), self.n, self.dim, pre_eps=self.pre_eps,
-                              rms_eps=self.eps)
+            def fwd(self, x, out_norm=None):
+                out = R.head(x, R.module_params(self), self.n, self.dim, pre_eps=self.pre_eps,
+                             rms_eps=self.eps)
+                return out if out_norm is None else out_norm(out)
             mod.forward = types.MethodType(fwd, mod)
         elif isinstance(mod, StreamExpand):
             mod.forward = types.MethodType(lambda self, x: R.stream_expand(x, self.n), mod)
@@ -158,3 +166,19 @@ def test_decode_step_hip_graph_replays_match_eager(dev):
             assert _rel(static_logits, want_logits) < 1e-6, (r, _rel(static_logits, want_logits))
             step(ids0)  # eager work between replays
             torch.cuda.synchronize()
+
+
+@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
+@pytest.mark.parametrize("use_mhc,n", [(1, 4), (2, 4), (1, 8), (1, 1)])
+def test_fused_norm_path_matches_autograd_path(dev, dtype, use_mhc, n):
+    """Without autograd the norms next to the mHC pieces run inside their
+    launches; with autograd they are separate ops.  Same logits."""
+    cfg = _config(use_mhc, n)
+    model = _model(cfg).to(dtype).to(dev)
+    g = torch.Generator().manual_seed(8)
+    ids = torch.randint(0, cfg.vocab_size, (2, 40), generator=g).to(dev)
+    with torch.no_grad():
+        fused = model(ids).logits
+    split = model(ids).logits.detach()  # parameters require grad: the autograd path
+    bar = 1e-4 if dtype == torch.float32 else 3e-2
+    assert _rel(fused, split) < bar, _rel(fused, split)
