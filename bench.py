@@ -34,6 +34,7 @@ the kernel-trace summary); traffic is null when that file is absent.
 
 Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--no-e2e] [--no-cpu]
        python bench.py --traffic     (counter passes only; prints nothing)
+       python bench.py --e2e-only [prefill|decode|moe]   (end-to-end model figures only)
 """
 from __future__ import annotations
 
@@ -600,6 +601,10 @@ def main():
                     help="run the counter-calibration and config-2 launches once, print nothing")
     ap.add_argument("--vector-pre", action="store_true",
                     help="with --traffic: also run the pre phase on the generic VALU kernel")
+    ap.add_argument("--e2e-only", nargs="?", const="all", default=None,
+                    choices=["all", "prefill", "decode", "moe"],
+                    help="run only the end-to-end model figures (configs 3, 4, 5, or one of "
+                         "them) and print them as one JSON line")
     ap.add_argument("--mfma-kernels", action="store_true",
                     help="with --traffic: also run the config-2 backward MFMA kernels and the "
                          "config-5 (n = 8) pre phase once")
@@ -616,6 +621,12 @@ def main():
 
     if args.traffic:
         traffic_passes(args.vector_pre, args.mfma_kernels)
+        return
+    if args.e2e_only:
+        runs = {"prefill": ("e2e_prefill", e2e_prefill), "decode": ("e2e_decode", e2e_decode),
+                "moe": ("e2e_prefill_moe", e2e_prefill_moe)}
+        keys = list(runs) if args.e2e_only == "all" else [args.e2e_only]
+        print(json.dumps({runs[k][0]: runs[k][1]() for k in keys}), flush=True)
         return
 
     r, rc = bench_mhc(args.steps, args.warmup)
