@@ -128,15 +128,17 @@ __global__ __launch_bounds__(256) void pre_bwd_generic_kernel(PreBwdArgs a) {
 //      hi + lo so the product keeps ~16 mantissa bits (phi is bf16-exact).
 // Reductions over a token's columns (gh and mean(xn * gxn)) go through the 4
 // lanes of a token (lane xor 16, 32), then per chunk / per wave through LDS
-// and are summed there in a fixed order (deterministic).  HOLD keeps the gxn
-// tiles in registers between the two passes; otherwise the second pass
-// recomputes them (phi re-read from L2).
+// and are summed there in a fixed order (deterministic).  With PHIREG the
+// phi A operands of the wave's chunks are loaded into registers at kernel
+// start, next to the x loads, so their L2 latency overlaps the gh partials
+// and the gates instead of following them, and both gxn passes (for the mean
+// and for g_x) run from registers; otherwise each pass reads phi from L2.
 template <int N, int MODE, int NW, int KJ>
 __global__ __launch_bounds__(NW * 64) void pre_bwd_mfma_kernel(PreBwdArgs a) {
   constexpr int FD = MODE == kFull ? 2 * N + N * N : (MODE == kNoHres ? 2 * N : N);
   constexpr int KS = (FD + 31) / 32;  // 32-feature K-steps
   constexpr int TM = 16;
-  constexpr bool HOLD = NW == 8 && KJ <= 12;
+  constexpr bool PHIREG = NW == 8 && KJ <= 12;
   __shared__ float s_gp[NW * KJ][TM];   // per-chunk partials of gh
   __shared__ float s_mp[NW][TM];         // per-wave partials of sum x * gxn
   __shared__ float s_gm[TM][KS * 32];    // alpha * g_raw, zero padded
@@ -158,7 +160,6 @@ __global__ __launch_bounds__(NW * 64) void pre_bwd_mfma_kernel(PreBwdArgs a) {
   const auto rgs = make_rsrc(a.g_sub ? static_cast<const uint16_t*>(a.g_sub) + t0 * C : nullptr,
                              a.g_sub ? (uint32_t)valid * C * 2u : 0u);
   const auto rgx = make_rsrc(static_cast<uint16_t*>(a.g_x) + t0 * NC, (uint32_t)valid * NC * 2u);
-  const auto rphi = make_rsrc(a.phi, (uint32_t)NC * FD * 2u);
 
   // chunk j of this wave: stream ci, first column c0; lane column c0 + 8g
   auto chunk = [&](int j, int& ci, int& c0) {
@@ -175,6 +176,58 @@ __global__ __launch_bounds__(NW * 64) void pre_bwd_mfma_kernel(PreBwdArgs a) {
     xs[j] = buf_load16(rx, ok ? (uint32_t)(r * NC + ci * C + c0 + 8 * g) * 2u : kBufOob);
   }
   const float inv = r < valid ? a.inv_rms[t0 + r] : 0.f;
+
+  // Gate inputs of this thread's (token, feature) items, loaded now so that
+  // their latency overlaps the x and g_sub loads instead of following a barrier.
+  constexpr int GI = TM * KS * 32;
+  constexpr int IPT = (GI + NW * 64 - 1) / (NW * 64);
+  const int pdt = a.param_dtype;
+  const int gdt = a.grad_dtype;
+  float pm[IPT], pg[IPT], pa[IPT], pb[IPT];
+#pragma unroll
+  for (int q = 0; q < IPT; ++q) {
+    const int idx = tid + q * NW * 64;
+    const int tt = idx / (KS * 32);
+    const int f = idx - tt * (KS * 32);
+    pm[q] = pg[q] = pa[q] = pb[q] = 0.f;
+    if (idx < GI && f < FD && tt < valid) {
+      const int64_t tk = t0 + tt;
+      pm[q] = a.mixes[tk * FD + f];
+      if (f < N) {
+        pg[q] = a.g_hpre ? ld_any(a.g_hpre, tk * N + f, gdt) : 0.f;
+        pa[q] = ld_any(a.alpha[0], 0, pdt);
+        pb[q] = ld_any(a.bias[0], f, pdt);
+      } else if (f < 2 * N) {
+        pg[q] = a.g_hpost ? ld_any(a.g_hpost, tk * N + (f - N), gdt) : 0.f;
+        pa[q] = ld_any(a.alpha[1], 0, pdt);
+        pb[q] = ld_any(a.bias[1], f - N, pdt);
+      } else {
+        pg[q] = a.g_hres ? ld_any(a.g_hres, tk * N * N + (f - 2 * N), gdt) : 0.f;
+        pa[q] = ld_any(a.alpha[2], 0, pdt);
+      }
+    }
+  }
+
+  const auto rphi = make_rsrc(a.phi, (uint32_t)NC * FD * 2u);
+  // phi A operand of chunk j, k-tile h, K-step ks: A-row r is column
+  // c0 + 8 (r / 4) + 4 h + r % 4 of the chunk, lane group g features 32 ks + 8g .. + 7
+  auto phi_op = [&](int j, int h, int ks) {
+    int ci, c0;
+    chunk(j, ci, c0);
+    const int col = c0 + 8 * (r >> 2) + 4 * h + (r & 3);
+    const bool ok = col < C && 32 * ks + 8 * g < FD;
+    return __builtin_bit_cast(
+        bf16x8_t, buf_load16(rphi, ok ? (uint32_t)((ci * C + col) * FD + 32 * ks + 8 * g) * 2u : kBufOob));
+  };
+  bf16x8_t wreg[PHIREG ? KJ : 1][2][PHIREG ? KS : 1];
+  if constexpr (PHIREG) {
+#pragma unroll
+    for (int j = 0; j < KJ; ++j)
+#pragma unroll
+      for (int h = 0; h < 2; ++h)
+#pragma unroll
+        for (int ks = 0; ks < KS; ++ks) wreg[j][h][ks] = phi_op(j, h, ks);
+  }
 
   // ---- gh partials per chunk: sum_c g_sub[c] * x[i][c]
 #pragma unroll
@@ -193,32 +246,29 @@ __global__ __launch_bounds__(NW * 64) void pre_bwd_mfma_kernel(PreBwdArgs a) {
   __syncthreads();
 
   // ---- gates: g_raw and alpha * g_raw per (token, feature)
-  const int pdt = a.param_dtype;
-  const int gdt = a.grad_dtype;
-  for (int idx = tid; idx < TM * KS * 32; idx += NW * 64) {
+#pragma unroll
+  for (int q = 0; q < IPT; ++q) {
+    const int idx = tid + q * NW * 64;
+    if (idx >= GI) break;
     const int tt = idx / (KS * 32);
     const int f = idx - tt * (KS * 32);
     float gm = 0.f;
     if (f < FD && tt < valid) {
       const int64_t tk = t0 + tt;
-      const float m = a.mixes[tk * FD + f];
+      const float m = pm[q];
+      const float alpha = pa[q];
       float graw;
-      float alpha;
       if (f < N) {
-        float gh = a.g_hpre ? ld_any(a.g_hpre, tk * N + f, gdt) : 0.f;
+        float gh = pg[q];
         for (int cb = 0; cb < NCB; ++cb) gh += s_gp[f * NCB + cb][tt];
-        alpha = ld_any(a.alpha[0], 0, pdt);
-        const float sg = sigmoid_f(fmaf(alpha, m, ld_any(a.bias[0], f, pdt)));
+        const float sg = sigmoid_f(fmaf(alpha, m, pb[q]));
         graw = gh * sg * (1.0f - sg);
         s_hp[tt][f] = sg + a.pre_eps;
       } else if (f < 2 * N) {
-        alpha = ld_any(a.alpha[1], 0, pdt);
-        const float sg = sigmoid_f(fmaf(alpha, m, ld_any(a.bias[1], f - N, pdt)));
-        const float gp = a.g_hpost ? ld_any(a.g_hpost, tk * N + (f - N), gdt) : 0.f;
-        graw = gp * sg * (1.0f - sg) * a.post_mult;
+        const float sg = sigmoid_f(fmaf(alpha, m, pb[q]));
+        graw = pg[q] * sg * (1.0f - sg) * a.post_mult;
       } else {
-        alpha = ld_any(a.alpha[2], 0, pdt);
-        graw = a.g_hres ? ld_any(a.g_hres, tk * N * N + (f - 2 * N), gdt) : 0.f;
+        graw = pg[q];
       }
       a.g_raw[tk * FD + f] = graw;
       gm = graw * alpha;
@@ -249,28 +299,23 @@ __global__ __launch_bounds__(NW * 64) void pre_bwd_mfma_kernel(PreBwdArgs a) {
 
   // ---- gxn = phi . (alpha * g_raw) on MFMA, and the partial of sum x * gxn
   auto gxn_tile = [&](int j, int h) {
-    int ci, c0;
-    chunk(j, ci, c0);
-    const int col = c0 + 8 * (r >> 2) + 4 * h + (r & 3);  // A-row r of this k-tile
     f32x4_t d = f32x4_t{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
     for (int ks = 0; ks < KS; ++ks) {
-      const bool ok = col < C && 32 * ks + 8 * g < FD;
-      const bf16x8_t av = __builtin_bit_cast(
-          bf16x8_t, buf_load16(rphi, ok ? (uint32_t)((ci * C + col) * FD + 32 * ks + 8 * g) * 2u : kBufOob));
+      bf16x8_t av;
+      if constexpr (PHIREG) av = wreg[j][h][ks];
+      else av = phi_op(j, h, ks);
       d = __builtin_amdgcn_mfma_f32_16x16x32_bf16(av, bhi[ks], d, 0, 0, 0);
       d = __builtin_amdgcn_mfma_f32_16x16x32_bf16(av, blo[ks], d, 0, 0, 0);
     }
     return d;
   };
-  f32x4_t acc[HOLD ? KJ : 1][2];
   float mp = 0.f;
 #pragma unroll
   for (int j = 0; j < KJ; ++j)
 #pragma unroll
     for (int h = 0; h < 2; ++h) {
       const f32x4_t d = gxn_tile(j, h);
-      if constexpr (HOLD) acc[j][h] = d;
 #pragma unroll
       for (int e = 0; e < 4; ++e) {
         const uint32_t w2 = xs[j].v[2 * h + (e >> 1)];
@@ -294,10 +339,7 @@ __global__ __launch_bounds__(NW * 64) void pre_bwd_mfma_kernel(PreBwdArgs a) {
     const bool ok = c0 + 8 * g < C;
     f32x4_t d2[2];
 #pragma unroll
-    for (int h = 0; h < 2; ++h) {
-      if constexpr (HOLD) d2[h] = acc[j][h];
-      else d2[h] = gxn_tile(j, h);
-    }
+    for (int h = 0; h < 2; ++h) d2[h] = gxn_tile(j, h);
     const U32x4 gv = buf_load16(rgs, ok ? (uint32_t)(r * C + c0 + 8 * g) * 2u : kBufOob);
     const float hp = s_hp[r][ci];
     U32x4 o;
