@@ -833,9 +833,62 @@ __global__ __launch_bounds__(64) void sinkhorn_bwd_lanes_kernel(const void* __re
   if (live) st_any(g_in, idx, gi_dt, gm);
 }
 
+// The same recurrence with the trajectory in registers, for schedules of at
+// most MAXS steps (2 * iters): no LDS, so occupancy is set by registers alone
+// and every access is a register read.  The steps run fully unrolled behind a
+// uniform bound on the real step count.
+template <int N, int MAXS>
+__global__ __launch_bounds__(256) void sinkhorn_bwd_regs_kernel(const void* __restrict__ m_in, int in_dt,
+                                                                const void* __restrict__ g_out, int g_dt,
+                                                                void* __restrict__ g_in, int gi_dt,
+                                                                int64_t batch, int iters, float eps) {
+  constexpr int G = N * N;
+  const int64_t idx = (int64_t)blockIdx.x * 256 + threadIdx.x;  // element index
+  const bool live = idx < batch * G;
+  const int steps = 2 * (iters > 1 ? iters : 1);
+  float Y[MAXS];
+  float R[MAXS];  // 1 / divisor of each step
+  const float v = live ? ld_any(m_in, idx, in_dt) : 0.f;
+  const float mx = row_reduce<N, OpMax>(v);
+  const float ex = expf(v - mx);
+  const float p = ex * __builtin_amdgcn_rcpf(row_reduce<N, OpAdd>(ex));
+  float t = p + eps;
+  Y[0] = t;
+  R[0] = 1.f;
+#pragma unroll
+  for (int st = 1; st < MAXS; ++st) {  // odd: column step, even: row step
+    if (st < steps) {                  // uniform
+      const float den = ((st & 1) ? col_sum<N>(t) : row_reduce<N, OpAdd>(t)) + eps;
+      R[st] = __builtin_amdgcn_rcpf(den);
+      t = t * R[st];
+      Y[st] = t;
+    }
+  }
+  float gr = live ? ld_any(g_out, idx, g_dt) : 0.f;
+#pragma unroll
+  for (int st = MAXS - 1; st >= 1; --st) {
+    if (st < steps) {
+      const float gy = gr * Y[st];
+      const float dot = (st & 1) ? col_sum<N>(gy) : row_reduce<N, OpAdd>(gy);
+      gr = (gr - dot) * R[st];
+    }
+  }
+  const float gm = p * (gr - row_reduce<N, OpAdd>(gr * p));
+  if (live) st_any(g_in, idx, gi_dt, gm);
+}
+
 hipError_t launch_sinkhorn_bwd(const void* m_in, int in_dtype, const void* g_out, int g_dtype,
                                void* g_in, int gi_dtype, int64_t batch, int n, int iters,
                                float eps, hipStream_t s) {
+  if ((n == 2 || n == 4 || n == 8) && iters <= 20) {
+    const int64_t blocks = (batch * n * n + 255) / 256;
+    switch (n) {
+      case 2: hipLaunchKernelGGL((sinkhorn_bwd_regs_kernel<2, 40>), dim3((unsigned)blocks), dim3(256), 0, s, m_in, in_dtype, g_out, g_dtype, g_in, gi_dtype, batch, iters, eps); break;
+      case 4: hipLaunchKernelGGL((sinkhorn_bwd_regs_kernel<4, 40>), dim3((unsigned)blocks), dim3(256), 0, s, m_in, in_dtype, g_out, g_dtype, g_in, gi_dtype, batch, iters, eps); break;
+      default: hipLaunchKernelGGL((sinkhorn_bwd_regs_kernel<8, 40>), dim3((unsigned)blocks), dim3(256), 0, s, m_in, in_dtype, g_out, g_dtype, g_in, gi_dtype, batch, iters, eps); break;
+    }
+    return hipGetLastError();
+  }
   if (n == 2 || n == 4 || n == 8) {
     const int steps = 2 * (iters > 1 ? iters : 1);
     const size_t lds = (size_t)2 * steps * 64 * sizeof(float);
