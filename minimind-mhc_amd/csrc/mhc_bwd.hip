@@ -480,17 +480,19 @@ __global__ __launch_bounds__(256) void weights_reduce_kernel(WeightsArgs a, int 
   if (q < NC * FD) {
     const int f = (int)(q % FD);
     const int64_t stride = NC * FD;
-    // four independent partial sums keep four loads in flight
-    float s0 = 0.f, s1 = 0.f, s2 = 0.f, s3 = 0.f;
+    // eight independent partial sums keep eight loads in flight
+    float sp[8];
+#pragma unroll
+    for (int u = 0; u < 8; ++u) sp[u] = 0.f;
     int r = 0;
-    for (; r + 4 <= R; r += 4) {
-      s0 += a.work[(int64_t)r * stride + q];
-      s1 += a.work[(int64_t)(r + 1) * stride + q];
-      s2 += a.work[(int64_t)(r + 2) * stride + q];
-      s3 += a.work[(int64_t)(r + 3) * stride + q];
+    for (; r + 8 <= R; r += 8) {
+#pragma unroll
+      for (int u = 0; u < 8; ++u) sp[u] += a.work[(int64_t)(r + u) * stride + q];
     }
-    for (; r < R; ++r) s0 += a.work[(int64_t)r * stride + q];
-    const float acc = (s0 + s1) + (s2 + s3);
+#pragma unroll
+    for (int u = 0; u < 7; ++u)
+      if (r + u < R) sp[u] += a.work[(int64_t)(r + u) * stride + q];
+    const float acc = ((sp[0] + sp[1]) + (sp[2] + sp[3])) + ((sp[4] + sp[5]) + (sp[6] + sp[7]));
     st_any(a.g_phi, q, a.phi_dtype, acc * ld_any(a.alpha[seg_of(f, n)], 0, a.param_dtype));
   }
   if (blockIdx.x == 0) {
