@@ -8,12 +8,14 @@
 //                s_* = sigmoid(alpha_* * mixes + bias_*)
 //   gxn[k]     = sum_f alpha_seg(f) g_raw[f] * phi[k, f]
 //   g_x[k]     = inv * (gxn[k] - xn[k] * mean_k(xn * gxn)) + (s_pre[i(k)] + pre_eps) * g_sub[c(k)]
+//   with mean_k(xn * gxn) = sum_f alpha_seg(f) g_raw[f] mixes_raw[f] / (n*C), since
+//   mixes_raw[f] = sum_k xn[k] phi[k, f] (the saved fp32 projection).
 // The per-token g_raw (fp32) feeds the weight gradients (model/mhc_fused.py:696-711):
 //   grad_phi = alpha_seg * (x * inv)^T @ g_raw,  grad_bias = sum_t g_raw,
 //   grad_alpha = sum_t sum_seg g_raw * mixes.
 // Sinkhorn backward: the reference recomputes the forward under autograd
 // (model/mhc_fused.py:131-137); here the forward iterates are recomputed into
-// LDS and the chain rule runs back through them.
+// registers (or LDS for long schedules) and the chain rule runs back through them.
 #include "mhc_internal.hpp"
 
 namespace mhc {
@@ -126,13 +128,14 @@ __global__ __launch_bounds__(256) void pre_bwd_generic_kernel(PreBwdArgs a) {
 //      give the 8 columns the lane holds of x.
 //   B: (alpha * g_raw)[token][f] for 32 features per K-step, split into bf16
 //      hi + lo so the product keeps ~16 mantissa bits (phi is bf16-exact).
-// Reductions over a token's columns (gh and mean(xn * gxn)) go through the 4
-// lanes of a token (lane xor 16, 32), then per chunk / per wave through LDS
-// and are summed there in a fixed order (deterministic).  With PHIREG the
+// The gh reductions over a token's columns go through the 4 lanes of a token
+// (lane xor 16, 32), then per chunk through LDS, summed there in a fixed
+// order (deterministic).  mean(xn * gxn) needs no pass over x: it equals
+// sum_f gm[f] mixes_raw[f] / NC (gm = alpha * g_raw), formed from LDS with the
+// B operands.  So gxn is computed once, straight into g_x.  With PHIREG the
 // phi A operands of the wave's chunks are loaded into registers at kernel
 // start, next to the x loads, so their L2 latency overlaps the gh partials
-// and the gates instead of following them, and both gxn passes (for the mean
-// and for g_x) run from registers; otherwise each pass reads phi from L2.
+// and the gates instead of following them.
 template <int N, int MODE, int NW, int KJ>
 __global__ __launch_bounds__(NW * 64) void pre_bwd_mfma_kernel(PreBwdArgs a) {
   constexpr int FD = MODE == kFull ? 2 * N + N * N : (MODE == kNoHres ? 2 * N : N);
@@ -140,7 +143,7 @@ __global__ __launch_bounds__(NW * 64) void pre_bwd_mfma_kernel(PreBwdArgs a) {
   constexpr int TM = 16;
   constexpr bool PHIREG = NW == 8 && KJ <= 12;
   __shared__ float s_gp[NW * KJ][TM];   // per-chunk partials of gh
-  __shared__ float s_mp[NW][TM];         // per-wave partials of sum x * gxn
+  __shared__ float s_mx[TM][KS * 32];    // mixes_raw, zero padded
   __shared__ float s_gm[TM][KS * 32];    // alpha * g_raw, zero padded
   __shared__ float s_hp[TM][N];          // h_pre = sigmoid + pre_eps (fp32 recompute)
 
@@ -276,12 +279,17 @@ __global__ __launch_bounds__(NW * 64) void pre_bwd_mfma_kernel(PreBwdArgs a) {
       s_hp[tt][f] = 0.f;
     }
     s_gm[tt][f] = gm;
+    s_mx[tt][f] = f < FD && tt < valid ? pm[q] : 0.f;
   }
   __syncthreads();
 
-  // ---- B operands: lane (token r, g) holds features 32s + 8g .. + 7, hi and lo
+  // ---- B operands: lane (token r, g) holds features 32s + 8g .. + 7, hi and lo.
+  // The same pass forms mean_k(xn * gxn) without touching x:
+  //   sum_k xn[k] gxn[k] = sum_f gm[f] sum_k xn[k] phi[k, f] = sum_f gm[f] mixes_raw[f],
+  // the forward's fp32 projection, saved for backward.
   bf16x8_t bhi[KS];
   bf16x8_t blo[KS];
+  float msum = 0.f;
 #pragma unroll
   for (int ks = 0; ks < KS; ++ks) {
     U32x4 h4, l4;
@@ -289,6 +297,8 @@ __global__ __launch_bounds__(NW * 64) void pre_bwd_mfma_kernel(PreBwdArgs a) {
     for (int e = 0; e < 4; ++e) {
       const float v0 = s_gm[r][32 * ks + 8 * g + 2 * e];
       const float v1 = s_gm[r][32 * ks + 8 * g + 2 * e + 1];
+      msum = fmaf(v0, s_mx[r][32 * ks + 8 * g + 2 * e], msum);
+      msum = fmaf(v1, s_mx[r][32 * ks + 8 * g + 2 * e + 1], msum);
       const uint32_t hp = pack_bf16x2(v0, v1);
       h4.v[e] = hp;
       l4.v[e] = pack_bf16x2(v0 - bf16lo(hp), v1 - bf16hi(hp));
@@ -297,7 +307,11 @@ __global__ __launch_bounds__(NW * 64) void pre_bwd_mfma_kernel(PreBwdArgs a) {
     blo[ks] = __builtin_bit_cast(bf16x8_t, l4);
   }
 
-  // ---- gxn = phi . (alpha * g_raw) on MFMA, and the partial of sum x * gxn
+  msum += xor_lane16(msum);
+  msum += xor_lane32(msum);
+  const float mean = msum / (float)NC;  // mean_k(xn * gxn)
+
+  // ---- gxn = phi . (alpha * g_raw) on MFMA
   auto gxn_tile = [&](int j, int h) {
     f32x4_t d = f32x4_t{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
@@ -310,26 +324,6 @@ __global__ __launch_bounds__(NW * 64) void pre_bwd_mfma_kernel(PreBwdArgs a) {
     }
     return d;
   };
-  float mp = 0.f;
-#pragma unroll
-  for (int j = 0; j < KJ; ++j)
-#pragma unroll
-    for (int h = 0; h < 2; ++h) {
-      const f32x4_t d = gxn_tile(j, h);
-#pragma unroll
-      for (int e = 0; e < 4; ++e) {
-        const uint32_t w2 = xs[j].v[2 * h + (e >> 1)];
-        mp = fmaf((e & 1) ? bf16hi(w2) : bf16lo(w2), d[e], mp);
-      }
-    }
-  mp += xor_lane16(mp);
-  mp += xor_lane32(mp);
-  if (g == 0) s_mp[wave][r] = mp;
-  __syncthreads();
-  float msum = 0.f;
-#pragma unroll
-  for (int w = 0; w < NW; ++w) msum += s_mp[w][r];
-  const float mean = inv * msum / (float)NC;  // mean_k(xn * gxn)
 
   // ---- g_x = inv * (gxn - xn * mean) + h_pre[i] * g_sub
 #pragma unroll
