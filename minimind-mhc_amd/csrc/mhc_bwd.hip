@@ -132,16 +132,15 @@ __global__ __launch_bounds__(256) void pre_bwd_generic_kernel(PreBwdArgs a) {
 // (lane xor 16, 32), then per chunk through LDS, summed there in a fixed
 // order (deterministic).  mean(xn * gxn) needs no pass over x: it equals
 // sum_f gm[f] mixes_raw[f] / NC (gm = alpha * g_raw), formed from LDS with the
-// B operands.  So gxn is computed once, straight into g_x.  With PHIREG the
-// phi A operands of the wave's chunks are loaded into registers at kernel
-// start, next to the x loads, so their L2 latency overlaps the gh partials
-// and the gates instead of following them.
+// B operands.  So gxn is computed once, straight into g_x, with phi's A
+// operands read from L2 as they are used.  That leaves ~90 VGPRs a lane at
+// n = 4 (amdgpu_waves_per_eu(4): two 8-wave workgroups per CU), so one
+// workgroup's loads overlap the other's gates and MFMAs.
 template <int N, int MODE, int NW, int KJ>
-__global__ __launch_bounds__(NW * 64) void pre_bwd_mfma_kernel(PreBwdArgs a) {
+__global__ __launch_bounds__(NW * 64) __attribute__((amdgpu_waves_per_eu(4))) void pre_bwd_mfma_kernel(PreBwdArgs a) {
   constexpr int FD = MODE == kFull ? 2 * N + N * N : (MODE == kNoHres ? 2 * N : N);
   constexpr int KS = (FD + 31) / 32;  // 32-feature K-steps
   constexpr int TM = 16;
-  constexpr bool PHIREG = NW == 8 && KJ <= 12;
   __shared__ float s_gp[NW * KJ][TM];   // per-chunk partials of gh
   __shared__ float s_mx[TM][KS * 32];    // mixes_raw, zero padded
   __shared__ float s_gm[TM][KS * 32];    // alpha * g_raw, zero padded
@@ -222,15 +221,6 @@ __global__ __launch_bounds__(NW * 64) void pre_bwd_mfma_kernel(PreBwdArgs a) {
     return __builtin_bit_cast(
         bf16x8_t, buf_load16(rphi, ok ? (uint32_t)((ci * C + col) * FD + 32 * ks + 8 * g) * 2u : kBufOob));
   };
-  bf16x8_t wreg[PHIREG ? KJ : 1][2][PHIREG ? KS : 1];
-  if constexpr (PHIREG) {
-#pragma unroll
-    for (int j = 0; j < KJ; ++j)
-#pragma unroll
-      for (int h = 0; h < 2; ++h)
-#pragma unroll
-        for (int ks = 0; ks < KS; ++ks) wreg[j][h][ks] = phi_op(j, h, ks);
-  }
 
   // ---- gh partials per chunk: sum_c g_sub[c] * x[i][c]
 #pragma unroll
@@ -316,9 +306,7 @@ __global__ __launch_bounds__(NW * 64) void pre_bwd_mfma_kernel(PreBwdArgs a) {
     f32x4_t d = f32x4_t{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
     for (int ks = 0; ks < KS; ++ks) {
-      bf16x8_t av;
-      if constexpr (PHIREG) av = wreg[j][h][ks];
-      else av = phi_op(j, h, ks);
+      const bf16x8_t av = phi_op(j, h, ks);
       d = __builtin_amdgcn_mfma_f32_16x16x32_bf16(av, bhi[ks], d, 0, 0, 0);
       d = __builtin_amdgcn_mfma_f32_16x16x32_bf16(av, blo[ks], d, 0, 0, 0);
     }
