@@ -191,15 +191,15 @@ def backward_bytes(n: int, C: int, M: int, s: int = 2):
     return {"post_bwd": post, "sinkhorn_bwd": sk, "pre_bwd": pre, "pre_bwd_weights": wts}
 
 
-def bench_backward(reps: int = 20, sets: int = 4):
+def bench_backward(reps: int = 20, sets: int = 4, n: int = N_STREAMS, M: int = TOKENS):
     """Steady-state times of the four backward launches of one mHC connection
-    at config 2 (bf16, 16384 tokens, n = 4, C = 768), rotating `sets` input
-    sets as bench_mhc does, with the saved tensors of a real forward."""
+    (bf16, C = 768; config 2 by default: 16384 tokens, n = 4), rotating `sets`
+    input sets as bench_mhc does, with the saved tensors of a real forward."""
     import torch
     from model import _hip as H, _ops
 
     dev = torch.device("cuda:0")
-    n, C, M = N_STREAMS, C_DIM, TOKENS
+    C = C_DIM
     bf = torch.bfloat16
     g = torch.Generator().manual_seed(2)
     phi = (torch.randn(n * C, 2 * n + n * n, generator=g) * 0.02).to(bf).to(dev)
@@ -687,6 +687,9 @@ def main():
     bw = bench_backward()
     bw["fwd_bwd_tokens_per_s"] = round(TOKENS / ((step_ms + bw["total_ms"]) * 1e-3), 1)
     line["backward"] = bw
+    bw5 = bench_backward(n=8, M=8192)
+    bw5["config"] = "C5 shape: 8192 tokens, n=8, C=768, bf16"
+    line["backward_c5"] = bw5
     line["other_configs"] = isolated_configs(max(10, args.steps // 2), max(3, args.warmup // 2))
     if not args.no_e2e:
         line["e2e_prefill"] = e2e_prefill()
