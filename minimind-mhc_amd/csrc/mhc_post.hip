@@ -192,7 +192,7 @@ hipError_t launch_post(const PostArgs& a, hipStream_t s) {
 // 16-byte column chunks, then wave_sum reduces the n^2 + n dot products.
 
 template <typename XT, int N, bool RES>
-__global__ __launch_bounds__(256) void post_bwd_vec_kernel(PostBwdArgs a) {
+__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(N >= 8 ? 2 : 1))) void post_bwd_vec_kernel(PostBwdArgs a) {
   constexpr int V = 16 / sizeof(XT);
   const int lane = threadIdx.x & 63;
   const int64_t tok = (int64_t)blockIdx.x * 4 + __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
