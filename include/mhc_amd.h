@@ -236,6 +236,17 @@ int mhc_expand_norm_fwd(const void* x, int x_dtype, const void* norm_weight, int
  */
 int64_t mhc_pre_token_threshold(int64_t max_tokens);
 
+/*
+ * Whether the persistent pre kernel loads x tiles as whole rows and stages
+ * them through LDS (C a multiple of 256, phi resident in registers, no fused
+ * norm; on by default) rather than loading the MFMA operand layout directly.
+ * Both give bit-identical results; the row loads stream faster on MI355X.
+ * on < 0 only queries; returns the previous setting (0 or 1).  Process-wide,
+ * not synchronised with calls in flight.  No reference counterpart (a
+ * scheduling choice of this implementation).
+ */
+int mhc_pre_row_staging(int on);
+
 /* ------------------------------------------------------------------ backward
  * Gradients are computed in fp32 and rounded once at the store, as the
  * reference's Triton backward kernels do.  Incoming gradients that are NULL

@@ -67,7 +67,7 @@ int run_pre(mhc::PreArgs& a, hipStream_t stream, const char* fn) {
 
 extern "C" {
 
-int mhc_abi_version(void) { return 3; }
+int mhc_abi_version(void) { return 4; }
 
 const char* mhc_last_error(void) { return g_err; }
 
@@ -332,6 +332,12 @@ int mhc_expand_norm_fwd(const void* x, int x_dtype, const void* norm_weight, int
 int64_t mhc_pre_token_threshold(int64_t max_tokens) {
   const int64_t prev = mhc::pre_token_max_m();
   if (max_tokens >= 0) mhc::set_pre_token_max_m(max_tokens);
+  return prev;
+}
+
+int mhc_pre_row_staging(int on) {
+  const int prev = mhc::pre_row_staging() ? 1 : 0;
+  if (on >= 0) mhc::set_pre_row_staging(on != 0);
   return prev;
 }
 

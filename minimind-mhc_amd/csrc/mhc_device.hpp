@@ -37,6 +37,16 @@ __device__ __forceinline__ __amdgpu_buffer_rsrc_t make_rsrc(const void* base, ui
                                            kBufDword3);
 }
 
+// A wave-uniform 64-bit value pinned to scalar registers.  Where the compiler
+// has also materialised a value in vector registers (per-lane addresses built
+// from it), a descriptor made from that copy costs a readfirstlane loop around
+// every buffer op; the caller asserts uniformity instead.
+__device__ __forceinline__ int64_t wave_uniform(int64_t v) {
+  const uint32_t lo = __builtin_amdgcn_readfirstlane((uint32_t)v);
+  const uint32_t hi = __builtin_amdgcn_readfirstlane((uint32_t)((uint64_t)v >> 32));
+  return (int64_t)(((uint64_t)hi << 32) | lo);
+}
+
 __device__ __forceinline__ U32x4 buf_load16(__amdgpu_buffer_rsrc_t r, uint32_t off) {
   return __builtin_bit_cast(U32x4, __builtin_amdgcn_raw_buffer_load_b128(r, (int)off, 0, 0));
 }

@@ -135,6 +135,11 @@ hipError_t launch_pre_token(const PreArgs& a, hipStream_t s);
 // kernel (process-wide setting).
 int64_t pre_token_max_m();
 void set_pre_token_max_m(int64_t m);
+// Whether the persistent pre kernel stages x tiles through LDS from row-
+// contiguous loads where the shape allows it (process-wide setting, on by
+// default).
+bool pre_row_staging();
+void set_pre_row_staging(bool on);
 // RMSNorm of each C row followed by n copies (StreamExpand): out[t, i*C + c].
 hipError_t launch_expand_norm(const void* x, int x_dtype, const void* w, int w_dtype, void* out,
                               int64_t M, int n, int C, float eps, hipStream_t s);

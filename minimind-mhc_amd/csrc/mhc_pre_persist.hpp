@@ -166,6 +166,80 @@ struct PersistPlan {
   static constexpr int POST_WAVE = kPersistWaves - 1;
 };
 
+// Row staging of x (C == 256 * KB, phi wholly in registers, no norm epilogue).
+// A 16-token tile is loaded with row-contiguous 1 KiB wave loads (lane l reads
+// 16 bytes at l * 16 of a 1 KiB piece of the tile), written to LDS, and read
+// back in the MFMA operand layout.  The operand layout's own loads put 16 rows
+// x 64 bytes in each wave instruction (every 128-byte line split between two
+// waves); on MI355X that pattern streams at ~4.8 TB/s where whole rows stream
+// at ~6.1 TB/s.  Wave w loads pieces w * PW .. w * PW + PW - 1 (PW = n * KB, as
+// many 16-byte chunks a lane as the operand layout holds), into the same
+// registers the operand layout used for the in-flight tile.
+template <int N, int MODE, int KB>
+struct PersistRow {
+  using P = PersistPlan<N, MODE, KB, false>;
+  static constexpr int NC = N * KB * 256;              // n * C
+  static constexpr int RCH = NC / 8;                   // 16-byte chunks of a token row
+  static constexpr int PW = N * KB;                    // 1 KiB pieces per wave
+  static constexpr int BYTES = kTokTile * NC * 2;      // the tile in LDS
+  static constexpr int R1 = (PW + 2) / 3;              // load batches [0,R1) [R1,R2) [R2,PW)
+  static constexpr int R2 = (2 * PW + 2) / 3;          // at three points of a step
+  static constexpr bool OK = P::NREG == P::NT && RCH % 16 == 0 &&
+                             P::SHARED + 256 + BYTES <= kLdsBytes;
+};
+
+// LDS byte of 16-byte chunk j of token row t.  The chunk index is XORed with
+// the row's low 4 bits: the operand-layout reads (16 rows at one column, the
+// rows 6 KiB apart) then hit 16 different 16-byte bank groups, and a row-
+// contiguous write still covers whole aligned 256-byte groups.
+template <int RCH>
+__device__ __forceinline__ uint32_t row_lds_off(int t, int j) {
+  return (uint32_t)(t * RCH + (j ^ (t & 15))) * 16u;
+}
+
+// Pieces [P0, P1) of this wave's share of a tile into xn (flat chunk p is
+// xn[p / N][p % N]).  A token past the end reads zeros (bounded descriptor).
+template <int N, int MODE, int KB, int P0, int P1>
+__device__ __forceinline__ void persist_load_row(U32x4 (&xn)[KB][N], __amdgpu_buffer_rsrc_t rsrc,
+                                                 int wave, int lane) {
+  using RW = PersistRow<N, MODE, KB>;
+#pragma unroll
+  for (int p = P0; p < P1; ++p)
+    xn[p / N][p % N] = __builtin_bit_cast(
+        U32x4, __builtin_amdgcn_raw_buffer_load_b128(rsrc, lane * 16, (wave * RW::PW + p) * 1024, 0));
+}
+
+// This wave's row pieces [P0, P1) of a tile -> LDS.
+template <int N, int MODE, int KB, int P0, int P1>
+__device__ __forceinline__ void persist_row_to_lds(unsigned char* xl, const U32x4 (&xn)[KB][N],
+                                                   int wave, int lane) {
+  using RW = PersistRow<N, MODE, KB>;
+#pragma unroll
+  for (int p = P0; p < P1; ++p) {
+    const int J = (wave * RW::PW + p) * 64 + lane;  // chunk of the tile
+    const int t = J / RW::RCH;
+    *reinterpret_cast<U32x4*>(xl + row_lds_off<RW::RCH>(t, J - t * RW::RCH)) = xn[p / N][p % N];
+  }
+}
+
+// The operand layout of this wave's column blocks from LDS: lane (r, g) of
+// block q, stream i holds row r, columns c0 + 8g .. c0 + 8g + 7.
+template <int N, int MODE, int KB>
+__device__ __forceinline__ void persist_lds_to_operands(const unsigned char* xl, U32x4 (&xr)[KB][N],
+                                                        int wave, int lane) {
+  using RW = PersistRow<N, MODE, KB>;
+  constexpr int C = KB * 256;
+  const int r = lane & 15;
+  const int g = lane >> 4;
+#pragma unroll
+  for (int q = 0; q < KB; ++q)
+#pragma unroll
+    for (int i = 0; i < N; ++i) {
+      const int j = (i * C + (wave + kPersistWaves * q) * kCBlock) / 8 + g;
+      xr[q][i] = *reinterpret_cast<const U32x4*>(xl + row_lds_off<RW::RCH>(r, j));
+    }
+}
+
 // Tokens of a tile that exist (0 for a tile past the end).
 __device__ __forceinline__ int tile_tokens(int64_t tile, int64_t ntiles, int64_t M) {
   if (tile >= ntiles) return 0;
@@ -382,7 +456,7 @@ __device__ __forceinline__ void persist_preagg(const PreArgs& a, const U32x4 (&x
   const int g = lane >> 4;
   const int64_t M = a.M;
   const int C = a.C;
-  const int64_t t0 = tile * TM;
+  const int64_t t0 = wave_uniform(tile * TM);
   const int valid = (int)(M - t0 < TM ? M - t0 : TM);
   const auto rsub = make_rsrc(static_cast<uint16_t*>(a.sub_in) + t0 * C, (uint32_t)valid * C * 2u);
   const uint32_t sub_row = (uint32_t)(r * C) * 2u;
@@ -423,7 +497,7 @@ __device__ __forceinline__ void persist_norm_store(const PreArgs& a, const Persi
   const int g = lane >> 4;
   const int64_t M = a.M;
   const int C = a.C;
-  const int64_t t0 = tile * TM;
+  const int64_t t0 = wave_uniform(tile * TM);
   const int valid = (int)(M - t0 < TM ? M - t0 : TM);
   const auto rsub = make_rsrc(static_cast<uint16_t*>(a.sub_in) + t0 * C, (uint32_t)valid * C * 2u);
   const uint32_t sub_row = (uint32_t)(r * C) * 2u;
@@ -490,6 +564,53 @@ __device__ __forceinline__ void persist_step(
   }
 }
 
+// One tile with row staging: xn holds the tile in row layout (its loads were
+// issued during the previous step); it goes to LDS, xn takes the next tile's
+// loads in three batches along the step (at its start, after the partials
+// barrier, after the pre-aggregate), and the operand registers xr are read
+// back from LDS.  A second barrier orders the LDS writes before the reads;
+// the previous step's partials barrier orders this step's writes after every
+// wave's previous reads.  (Overlapping two tiles' loads, with the LDS tile
+// taking the next tile's first batch once read, measured slower: the extra
+// loads in flight stall the issuing waves.)
+template <int N, int MODE, int KB>
+__device__ __forceinline__ void persist_step_row(
+    const PreArgs& a, PersistShared<N, PersistPlan<N, MODE, KB>::FD>& sh, PersistNorm<false, KB>& nsh,
+    unsigned char* xl, U32x4 (&xr)[KB][N], U32x4 (&xn)[KB][N],
+    const bf16x8_t (&wreg)[KB][N][PersistPlan<N, MODE, KB>::WR], const unsigned char* lds_w,
+    int64_t tile, int64_t prev, int64_t ntiles, int slot, int tid, int lane, int wave) {
+  using P = PersistPlan<N, MODE, KB>;
+  using RW = PersistRow<N, MODE, KB>;
+  const int r = lane & 15;
+  const auto rn = x_tile_rsrc(static_cast<const uint16_t*>(a.x), tile + gridDim.x, ntiles, a.M,
+                              N * a.C);
+  persist_row_to_lds<N, MODE, KB, 0, RW::PW>(xl, xn, wave, lane);
+  persist_load_row<N, MODE, KB, 0, RW::R1>(xn, rn, wave, lane);
+  __syncthreads();
+  persist_lds_to_operands<N, MODE, KB>(xl, xr, wave, lane);
+  persist_partials<N, MODE, KB, false>(a, sh, xr, wreg, lds_w, slot, lane, wave);
+  __syncthreads();
+  persist_load_row<N, MODE, KB, RW::R1, RW::R2>(xn, rn, wave, lane);
+  if constexpr (MODE == kFull) {
+    if (wave < P::SK_WAVES && prev >= 0 && a.h_res)
+      persist_sinkhorn<N>(a, sh.hres[slot ^ 1], prev, tid);
+  }
+  const float hp = persist_pre_post<N, MODE, KB>(a, sh, tile, slot, lane, wave);
+  if constexpr (MODE == kFull) {
+    if (wave >= P::SK_WAVES) persist_res_gates<N, MODE, KB>(a, sh, tile, slot, tid - P::SK_WAVES * 64);
+  }
+  uint32_t hlo[N];
+  uint32_t hhi[N];
+#pragma unroll
+  for (int i = 0; i < N; ++i) {  // h_pre of this lane's token r, stream i
+    const float h = __shfl(hp, r * N + i, 64);
+    hlo[i] = pack_lo(h);
+    hhi[i] = pack_hi(h);
+  }
+  persist_preagg<N, KB, false>(a, xr, hlo, hhi, tile, lane, wave, nsh, slot);
+  persist_load_row<N, MODE, KB, RW::R2, RW::PW>(xn, rn, wave, lane);
+}
+
 // Gate parameter of thread tid (raw bits; converted once the streaming loads
 // are out).  Branch-free: threads without a parameter read alpha_pre[0].
 struct RawParam {
@@ -534,13 +655,16 @@ __device__ __forceinline__ float convert_param(const RawParam& rp, int dt) {
   return rp.used ? v : 0.f;
 }
 
-template <int N, int MODE, int KB, bool NORM>
+template <int N, int MODE, int KB, bool NORM, bool ROW = false>
 __global__ __launch_bounds__(kPersistWaves * 64) void pre_persist_kernel(PreArgs a, int64_t ntiles) {
   using P = PersistPlan<N, MODE, KB, NORM>;
+  using RW = PersistRow<N, MODE, KB>;
   static_assert(P::SHARED + 256 + (P::NLDS > 0 ? P::LDS_W : 0) <= kLdsBytes, "LDS budget");
+  static_assert(!ROW || (RW::OK && !NORM), "row staging: C == 256 * KB, phi in registers, no norm");
   __shared__ PersistShared<N, P::FD> sh;
   __shared__ PersistNorm<NORM, KB> nsh;
   __shared__ __attribute__((aligned(16))) unsigned char lds_w[P::LDS_W];
+  __shared__ __attribute__((aligned(16))) unsigned char xl[ROW ? RW::BYTES : 16];
 
   const int tid = threadIdx.x;
   const int lane = tid & 63;
@@ -587,7 +711,8 @@ __global__ __launch_bounds__(kPersistWaves * 64) void pre_persist_kernel(PreArgs
   U32x4 xa[KB][N];
   U32x4 xb[KB][N];
   const auto r0 = x_tile_rsrc(x, tile, ntiles, a.M, N * C);
-  if constexpr (P::X_EARLY) persist_load_part<N, KB, 0, KB>(xa, r0, C, wave, r, g);
+  if constexpr (ROW) persist_load_row<N, MODE, KB, 0, RW::PW>(xa, r0, wave, lane);
+  else if constexpr (P::X_EARLY) persist_load_part<N, KB, 0, KB>(xa, r0, C, wave, r, g);
   constexpr int NST = P::NLDS > 0 ? P::NLDS : 1;
   U32x4 st[NST][KB][N];  // LDS phi tiles, staged
 #pragma unroll
@@ -610,7 +735,7 @@ __global__ __launch_bounds__(kPersistWaves * 64) void pre_persist_kernel(PreArgs
         *reinterpret_cast<U32x4*>(dst) = st[t][q][i];
       }
   }
-  if constexpr (!P::X_EARLY) persist_load_part<N, KB, 0, KB>(xa, r0, C, wave, r, g);
+  if constexpr (!P::X_EARLY && !ROW) persist_load_part<N, KB, 0, KB>(xa, r0, C, wave, r, g);
 
   if (tid == 0) sh.zero = U32x4{{0u, 0u, 0u, 0u}};
   if (tid < GateParams<N>::kCount) sh.prm[tid] = convert_param(rp, a.param_dtype);
@@ -629,7 +754,16 @@ __global__ __launch_bounds__(kPersistWaves * 64) void pre_persist_kernel(PreArgs
   int64_t prev = -1;
   int slot = 0;
   int64_t k = 0;
-  for (; k + 2 <= my_tiles; k += 2) {  // uniform across the workgroup
+  if constexpr (ROW) {  // fixed roles: xa in flight (row layout), xb the operands
+    for (; k < my_tiles; ++k) {
+      persist_step_row<N, MODE, KB>(a, sh, nsh, xl, xb, xa, wreg, lds_w, tile, prev, ntiles, slot,
+                                    tid, lane, wave);
+      prev = tile;
+      slot ^= 1;
+      tile += step;
+    }
+  }
+  for (; !ROW && k + 2 <= my_tiles; k += 2) {  // uniform across the workgroup
     persist_step<N, MODE, KB, NORM>(a, sh, nsh, xa, xb, wreg, lds_w, tile, prev, ntiles, slot, tid, lane, wave);
     prev = tile;
     slot ^= 1;
@@ -639,7 +773,7 @@ __global__ __launch_bounds__(kPersistWaves * 64) void pre_persist_kernel(PreArgs
     slot ^= 1;
     tile += step;
   }
-  if (k < my_tiles) {
+  if (!ROW && k < my_tiles) {
     persist_step<N, MODE, KB, NORM>(a, sh, nsh, xa, xb, wreg, lds_w, tile, prev, ntiles, slot, tid, lane, wave);
     prev = tile;
     slot ^= 1;
@@ -664,6 +798,13 @@ template <int N, int MODE, int KB>
 hipError_t launch_pre_persist_inst(const PreArgs& a, int num_cus, hipStream_t s) {
   const int64_t ntiles = (a.M + kTokTile - 1) / kTokTile;
   const int64_t grid = ntiles < num_cus ? ntiles : num_cus;
+  if constexpr (PersistRow<N, MODE, KB>::OK) {
+    if (!a.norm_w && a.C == 256 * KB && pre_row_staging()) {
+      hipLaunchKernelGGL((pre_persist_kernel<N, MODE, KB, false, true>), dim3((unsigned)grid),
+                         dim3(kPersistWaves * 64), 0, s, a, ntiles);
+      return hipGetLastError();
+    }
+  }
   if (a.norm_w)
     hipLaunchKernelGGL((pre_persist_kernel<N, MODE, KB, true>), dim3((unsigned)grid),
                        dim3(kPersistWaves * 64), 0, s, a, ntiles);

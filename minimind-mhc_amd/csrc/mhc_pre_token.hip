@@ -37,6 +37,13 @@ int64_t g_token_max_m = 512;
 int64_t pre_token_max_m() { return g_token_max_m; }
 void set_pre_token_max_m(int64_t m) { g_token_max_m = m; }
 
+namespace {
+bool g_row_staging = true;
+}  // namespace
+
+bool pre_row_staging() { return g_row_staging; }
+void set_pre_row_staging(bool on) { g_row_staging = on; }
+
 constexpr int kTokThreads = 128;  // 128 column groups of 8: C <= 1024
 
 template <int N, int MODE>

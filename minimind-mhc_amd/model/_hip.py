@@ -58,6 +58,7 @@ _SIGNATURES = {
                                _P, _I, _F, _P]),
     "mhc_expand_norm_fwd": (_I, [_P, _I, _P, _I, _P, _I64, _I, _I, _F, _P]),
     "mhc_pre_token_threshold": (_I64, [_I64]),
+    "mhc_pre_row_staging": (_I, [_I]),
     "mhc_sinkhorn_fwd": (_I, [_P, _P, _I, _I64, _I, _I, _F, _P]),
     "mhc_stream_expand_fwd": (_I, [_P, _P, _I, _I64, _I, _I, _P]),
     "mhc_post_bwd": (_I, [_P, _I, _P, _P, _I, _P, _I, _P, _P, _P, _P, _P, _I64, _I, _I, _P]),
@@ -78,7 +79,7 @@ _SIGNATURES = {
     "mhc_sinkhorn_bwd": (_I, [_P, _I, _P, _I, _P, _I, _I64, _I, _I, _F, _P]),
 }
 
-ABI_VERSION = 3
+ABI_VERSION = 4
 _lib: Optional[ctypes.CDLL] = None
 
 

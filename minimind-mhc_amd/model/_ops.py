@@ -259,6 +259,13 @@ def pre_token_threshold(max_tokens: int = -1) -> int:
     return int(H.load().mhc_pre_token_threshold(int(max_tokens)))
 
 
+def pre_row_staging(on: int = -1) -> int:
+    """Set (on >= 0) or query whether the persistent pre kernel loads x tiles
+    as whole rows staged through LDS where the shape allows; returns the
+    previous setting (0 or 1).  Results are bit-identical either way."""
+    return int(H.load().mhc_pre_row_staging(int(on)))
+
+
 def stream_expand(x: torch.Tensor, n: int) -> torch.Tensor:
     dev = H.require_device(x)
     B, L, D = x.shape

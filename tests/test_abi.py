@@ -93,6 +93,15 @@ def test_norm_entry_points_validate_without_device(lib):
     assert lib.mhc_expand_norm_fwd(None, 1, None, 1, None, 0, 4, 64, 1e-6, None) == 0  # empty
 
 
+def test_row_staging_round_trip(lib):
+    old = lib.mhc_pre_row_staging(-1)
+    assert old in (0, 1)
+    assert lib.mhc_pre_row_staging(1 - old) == old
+    assert lib.mhc_pre_row_staging(-1) == 1 - old
+    assert lib.mhc_pre_row_staging(old) == 1 - old
+    assert lib.mhc_pre_row_staging(-1) == old
+
+
 def test_token_threshold_round_trip(lib):
     old = lib.mhc_pre_token_threshold(-1)
     assert old >= 0
