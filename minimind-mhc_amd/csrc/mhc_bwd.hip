@@ -454,42 +454,56 @@ __global__ __launch_bounds__(256) void weights_partial_generic_kernel(WeightsArg
 
 __device__ __forceinline__ int seg_of(int f, int n) { return f < n ? 0 : (f < 2 * n ? 1 : 2); }
 
+// Sum of w[r * stride], r < R (R <= 64, at most 64 token ranges), in a fixed
+// order: batches of 32 independent loads (so a thread waits for one memory
+// round trip per batch, not one per range), each summed as a pairwise tree.
+// Indices past R re-read range R - 1 and are dropped: branch-free, in bounds.
+constexpr int kRangeBatch = 32;
+__device__ __forceinline__ float sum_ranges(const float* __restrict__ w, int64_t stride, int R) {
+  float total = 0.f;
+  for (int r0 = 0; r0 < R; r0 += kRangeBatch) {
+    float v[kRangeBatch];
+#pragma unroll
+    for (int u = 0; u < kRangeBatch; ++u) {
+      const int r = r0 + u;
+      const float t = w[(int64_t)(r < R ? r : R - 1) * stride];
+      v[u] = r < R ? t : 0.f;
+    }
+#pragma unroll
+    for (int h = kRangeBatch / 2; h > 0; h >>= 1)
+#pragma unroll
+      for (int u = 0; u < h; ++u) v[u] += v[u + h];
+    total += v[0];
+  }
+  return total;
+}
+
+// Grid: one thread per phi element, plus one last workgroup for the alpha /
+// bias sums (one thread per (feature, kind)).
 __global__ __launch_bounds__(256) void weights_reduce_kernel(WeightsArgs a, int R) {
   const int n = a.n;
   const int FD = mode_fd(a.mode, n);
   const int64_t NC = (int64_t)n * a.C;
   const int64_t q = (int64_t)blockIdx.x * 256 + threadIdx.x;
-  if (q < NC * FD) {
-    const int f = (int)(q % FD);
-    const int64_t stride = NC * FD;
-    // eight independent partial sums keep eight loads in flight
-    float sp[8];
-#pragma unroll
-    for (int u = 0; u < 8; ++u) sp[u] = 0.f;
-    int r = 0;
-    for (; r + 8 <= R; r += 8) {
-#pragma unroll
-      for (int u = 0; u < 8; ++u) sp[u] += a.work[(int64_t)(r + u) * stride + q];
+  if (blockIdx.x + 1 < gridDim.x) {
+    if (q < NC * FD) {
+      const int f = (int)(q % FD);
+      const float acc = sum_ranges(a.work + q, NC * FD, R);
+      st_any(a.g_phi, q, a.phi_dtype, acc * ld_any(a.alpha[seg_of(f, n)], 0, a.param_dtype));
     }
-#pragma unroll
-    for (int u = 0; u < 7; ++u)
-      if (r + u < R) sp[u] += a.work[(int64_t)(r + u) * stride + q];
-    const float acc = ((sp[0] + sp[1]) + (sp[2] + sp[3])) + ((sp[4] + sp[5]) + (sp[6] + sp[7]));
-    st_any(a.g_phi, q, a.phi_dtype, acc * ld_any(a.alpha[seg_of(f, n)], 0, a.param_dtype));
-  }
-  if (blockIdx.x == 0) {
+  } else {
     __shared__ float s_a[kMaxFD];
     const float* ab = a.work + (int64_t)R * NC * FD;
-    for (int f = threadIdx.x; f < FD; f += 256) {
-      float sb = 0.f, sa = 0.f;
-      for (int r = 0; r < R; ++r) {
-        sb += ab[(int64_t)r * 2 * FD + f];
-        sa += ab[(int64_t)r * 2 * FD + FD + f];
+    for (int t = threadIdx.x; t < 2 * FD; t += 256) {  // t < FD: bias (sum g_raw), else alpha
+      const int f = t < FD ? t : t - FD;               // (sum g_raw * mixes)
+      const float v = sum_ranges(ab + t, 2 * FD, R);
+      if (t < FD) {
+        const int sg = seg_of(f, n);
+        const int base = sg == 0 ? 0 : (sg == 1 ? n : 2 * n);
+        if (a.g_bias[sg]) st_any(a.g_bias[sg], f - base, a.param_dtype, v);
+      } else {
+        s_a[f] = v;
       }
-      const int sg = seg_of(f, n);
-      const int base = sg == 0 ? 0 : (sg == 1 ? n : 2 * n);
-      if (a.g_bias[sg]) st_any(a.g_bias[sg], f - base, a.param_dtype, sb);
-      s_a[f] = sa;
     }
     __syncthreads();
     if (threadIdx.x < 3) {
@@ -690,7 +704,7 @@ hipError_t launch_pre_bwd_weights(const WeightsArgs& a, hipStream_t s) {
     e = hipGetLastError();
   }
   if (e != hipSuccess) return e;
-  hipLaunchKernelGGL(weights_reduce_kernel, dim3((unsigned)qb), dim3(256), 0, s, a, R);
+  hipLaunchKernelGGL(weights_reduce_kernel, dim3((unsigned)(qb + 1)), dim3(256), 0, s, a, R);
   return hipGetLastError();
 }
 
