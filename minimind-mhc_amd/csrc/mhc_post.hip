@@ -285,6 +285,150 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(N >= 8 ? 2 
   if (lane < N) static_cast<XT*>(a.g_h_post)[tok * N + lane] = Elem<XT>::put(mine_hp);
 }
 
+// bf16 streams, n in {2, 4, 8}: the same one-wave-per-token split with
+// packed operands.  h_res and h_post are wave-uniform and sit in scalar
+// registers as bf16 pairs of adjacent streams, (h[2p][j], h[2p+1][j]); every
+// product runs on v_dot2_f32_bf16 (a bf16 x bf16 product is exact in fp32,
+// and each dot2 adds two of them to an fp32 accumulator):
+//   g_h_res[i][j] += g_i . x_j,  g_h_post[i] += g_i . F   (4 column pairs a chunk)
+//   g_x[j][c] = sum_p (h[2p][j], h[2p+1][j]) . (g[2p][c], g[2p+1][c])
+//   g_F[c]    = sum_p (hp[2p], hp[2p+1])     . (g[2p][c], g[2p+1][c])
+// with the stream pairs of each column built once per chunk by v_perm.  g and
+// x stay packed (4 VGPRs per 8 columns, not 8 fp32), so n = 8 fits three
+// waves per SIMD with no spills where the fp32 form needed more than 256
+// VGPRs.  Sums run in a different order than post_bwd_vec_kernel's fmaf
+// chains: results agree to fp32 rounding before the bf16 store.
+template <int N, bool RES>
+__global__ __launch_bounds__(256) void post_bwd_bf16_kernel(PostBwdArgs a) {
+  static_assert(N % 2 == 0, "pairs of streams");
+  constexpr int NP = N / 2;
+  const int lane = threadIdx.x & 63;
+  const int64_t tok = (int64_t)blockIdx.x * 4 + __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  if (tok >= a.M) return;  // whole wave
+  const int C = a.C;
+  const int CV = C / 8;
+  const int64_t NC = (int64_t)N * C;
+  const uint16_t* __restrict__ x = static_cast<const uint16_t*>(a.x) + tok * NC;
+  const uint16_t* __restrict__ g = static_cast<const uint16_t*>(a.g_out) + tok * NC;
+  const uint16_t* __restrict__ f = static_cast<const uint16_t*>(a.f_out) + tok * C;
+  uint16_t* __restrict__ gx = a.g_x ? static_cast<uint16_t*>(a.g_x) + tok * NC : nullptr;
+  uint16_t* __restrict__ gf = static_cast<uint16_t*>(a.g_f) + tok * C;
+
+  // Gate pairs: element (i, j) of the token's row-major gates is half (j & 1)
+  // of dword (i * N + j) / 2 (N even).
+  const uint32_t* __restrict__ hp32 =
+      reinterpret_cast<const uint32_t*>(static_cast<const uint16_t*>(a.h_post) + tok * N);
+  uint32_t hp2[NP];
+#pragma unroll
+  for (int p = 0; p < NP; ++p) hp2[p] = __builtin_amdgcn_readfirstlane(hp32[p]);
+  uint32_t hr2[RES ? NP * N : 1];
+  if constexpr (RES) {
+    const uint32_t* __restrict__ hr32 =
+        reinterpret_cast<const uint32_t*>(static_cast<const uint16_t*>(a.h_res) + tok * N * N);
+#pragma unroll
+    for (int p = 0; p < NP; ++p)
+#pragma unroll
+      for (int j = 0; j < N; ++j) {
+        const uint32_t w0 = hr32[(2 * p * N + j) >> 1];
+        const uint32_t w1 = hr32[((2 * p + 1) * N + j) >> 1];
+        const uint32_t v = (j & 1) ? ((w0 >> 16) | (w1 & 0xffff0000u)) : ((w0 & 0xffffu) | (w1 << 16));
+        hr2[p * N + j] = __builtin_amdgcn_readfirstlane(v);
+      }
+  }
+  float ahr[RES ? N * N : 1];
+  float ahp[N];
+#pragma unroll
+  for (int k = 0; k < (RES ? N * N : 1); ++k) ahr[k] = 0.f;
+#pragma unroll
+  for (int i = 0; i < N; ++i) ahp[i] = 0.f;
+
+  for (int cv = lane; cv < CV; cv += 64) {
+    const int c = cv * 8;
+    U32x4 gv[N];
+#pragma unroll
+    for (int i = 0; i < N; ++i) gv[i] = *reinterpret_cast<const U32x4*>(g + (int64_t)i * C + c);
+    const U32x4 fv = *reinterpret_cast<const U32x4*>(f + c);
+#pragma unroll
+    for (int i = 0; i < N; ++i)
+#pragma unroll
+      for (int k = 0; k < 4; ++k) ahp[i] = dot2_bf16(gv[i].v[k], fv.v[k], ahp[i]);
+    if constexpr (RES) {
+      U32x4 xv[N];
+#pragma unroll
+      for (int j = 0; j < N; ++j) xv[j] = *reinterpret_cast<const U32x4*>(x + (int64_t)j * C + c);
+#pragma unroll
+      for (int i = 0; i < N; ++i)
+#pragma unroll
+        for (int j = 0; j < N; ++j)
+#pragma unroll
+          for (int k = 0; k < 4; ++k) ahr[i * N + j] = dot2_bf16(gv[i].v[k], xv[j].v[k], ahr[i * N + j]);
+    } else if (gx) {
+#pragma unroll
+      for (int j = 0; j < N; ++j) *reinterpret_cast<U32x4*>(gx + (int64_t)j * C + c) = gv[j];
+    }
+    // (g[2p][c], g[2p+1][c]) for the low (even) and high (odd) column of each pair k
+    uint32_t glo[NP][4];
+    uint32_t ghi[NP][4];
+#pragma unroll
+    for (int p = 0; p < NP; ++p)
+#pragma unroll
+      for (int k = 0; k < 4; ++k) {
+        glo[p][k] = __builtin_amdgcn_perm(gv[2 * p + 1].v[k], gv[2 * p].v[k], 0x05040100u);
+        ghi[p][k] = __builtin_amdgcn_perm(gv[2 * p + 1].v[k], gv[2 * p].v[k], 0x07060302u);
+      }
+    U32x4 of;
+#pragma unroll
+    for (int k = 0; k < 4; ++k) {
+      float lo = 0.f;
+      float hi = 0.f;
+#pragma unroll
+      for (int p = 0; p < NP; ++p) {
+        lo = dot2_bf16(hp2[p], glo[p][k], lo);
+        hi = dot2_bf16(hp2[p], ghi[p][k], hi);
+      }
+      of.v[k] = pack_bf16x2(lo, hi);
+    }
+    *reinterpret_cast<U32x4*>(gf + c) = of;
+    if constexpr (RES) {
+#pragma unroll
+      for (int j = 0; j < N; ++j) {
+        U32x4 o;
+#pragma unroll
+        for (int k = 0; k < 4; ++k) {
+          float lo = 0.f;
+          float hi = 0.f;
+#pragma unroll
+          for (int p = 0; p < NP; ++p) {
+            lo = dot2_bf16(hr2[p * N + j], glo[p][k], lo);
+            hi = dot2_bf16(hr2[p * N + j], ghi[p][k], hi);
+          }
+          o.v[k] = pack_bf16x2(lo, hi);
+        }
+        if (gx) *reinterpret_cast<U32x4*>(gx + (int64_t)j * C + c) = o;
+      }
+    }
+  }
+  // Reduce over the wave; lane k stores value k.
+  float mine_hr = 0.f;
+  if constexpr (RES) {
+#pragma unroll
+    for (int k = 0; k < N * N; ++k) {
+      const float t = wave_sum(ahr[k]);
+      mine_hr = lane == k ? t : mine_hr;
+    }
+  }
+  float mine_hp = 0.f;
+#pragma unroll
+  for (int i = 0; i < N; ++i) {
+    const float t = wave_sum(ahp[i]);
+    mine_hp = lane == i ? t : mine_hp;
+  }
+  if constexpr (RES) {
+    if (lane < N * N) static_cast<__bf16*>(a.g_h_res)[tok * N * N + lane] = (__bf16)mine_hr;
+  }
+  if (lane < N) static_cast<__bf16*>(a.g_h_post)[tok * N + lane] = (__bf16)mine_hp;
+}
+
 // Any dtypes, n <= 16, any C: one 256-thread workgroup per token.
 __device__ __forceinline__ float block_sum256(float v, float* red) {
   v = wave_sum(v);
@@ -358,6 +502,27 @@ static hipError_t launch_bwd_vec(const PostBwdArgs& a, hipStream_t s) {
   return hipGetLastError();
 }
 
+template <int N>
+static hipError_t launch_bwd_bf16(const PostBwdArgs& a, hipStream_t s) {
+  const int64_t blocks = (a.M + 3) / 4;
+  if (a.h_res)
+    hipLaunchKernelGGL((post_bwd_bf16_kernel<N, true>), dim3((unsigned)blocks), dim3(256), 0, s, a);
+  else
+    hipLaunchKernelGGL((post_bwd_bf16_kernel<N, false>), dim3((unsigned)blocks), dim3(256), 0, s, a);
+  return hipGetLastError();
+}
+
+// bf16: the packed dot2 kernel for paired streams, the fp32 form at n = 1.
+static hipError_t launch_bwd_bf16_n(const PostBwdArgs& a, hipStream_t s) {
+  switch (a.n) {
+    case 1: return launch_bwd_vec<__bf16, 1>(a, s);
+    case 2: return launch_bwd_bf16<2>(a, s);
+    case 4: return launch_bwd_bf16<4>(a, s);
+    case 8: return launch_bwd_bf16<8>(a, s);
+    default: return hipErrorInvalidValue;
+  }
+}
+
 template <typename XT>
 static hipError_t launch_bwd_vec_n(const PostBwdArgs& a, hipStream_t s) {
   switch (a.n) {
@@ -382,7 +547,7 @@ hipError_t launch_post_bwd(const PostBwdArgs& a, hipStream_t s) {
                       aligned16(a.g_f) && (a.g_x == nullptr || aligned16(a.g_x)) &&
                       small_ok(a.h_post, a.n) && small_ok(a.h_res, a.n * a.n);
   if (vec_ok) {
-    if (a.x_dtype == kBF16) return launch_bwd_vec_n<__bf16>(a, s);
+    if (a.x_dtype == kBF16) return launch_bwd_bf16_n(a, s);
     if (a.x_dtype == kF32) return launch_bwd_vec_n<float>(a, s);
     if (a.x_dtype == kF16) return launch_bwd_vec_n<_Float16>(a, s);
   }
