@@ -552,10 +552,18 @@ __global__ __launch_bounds__(512) void weights_mfma_kernel(WeightsArgs a, int64_
   const int64_t te = tb + per < a.M ? tb + per : a.M;
   const bool ab_slice = blockIdx.x == 0;
 
-  const int tp = tid & 31;  // x: token pair (tokens 2tp, 2tp + 1 of the step)
-  const int kc = tid >> 5;  // x: 8-column group (columns k0 + 8kc .. + 7)
+  // x: 8-column group kc (columns k0 + 8kc .. + 7) of token pair tp (tokens
+  // 2tp, 2tp + 1 of the step).  Sixteen consecutive lanes cover a token's 256
+  // bytes of the slice, so each wave load reads whole 128-byte lines.
+  const int kc = tid & 15;
+  const int tp = tid >> 4;
   const int col = k0 + 8 * kc;
   const bool okc = col < NC;
+  // In s_x the 16-byte groups of token pairs (4 pairs = 8 tokens) of column
+  // group kc are XOR-permuted by kc & 7: the transposed writes of 16 column
+  // groups at one token pair then spread over 8 bank groups instead of one,
+  // and an MFMA read of 8 consecutive tokens stays one aligned 16-byte read.
+  auto tp_slot = [](int pair, int group) { return pair ^ (4 * (group & 7)); };
 
   // Everything one step reads from memory; the next step's copy is loaded
   // while the current step's MFMAs run.
@@ -617,13 +625,15 @@ __global__ __launch_bounds__(512) void weights_mfma_kernel(WeightsArgs a, int64_
       const uint32_t wa = cur.xa.v[e >> 1];
       const uint32_t wb = cur.xb.v[e >> 1];
       const uint32_t d = (e & 1) ? ((wa >> 16) | (wb & 0xffff0000u)) : ((wa & 0xffffu) | (wb << 16));
-      *reinterpret_cast<uint32_t*>(s_x + (8 * kc + e) * kWRow + tp * 4) = d;
+      *reinterpret_cast<uint32_t*>(s_x + (8 * kc + e) * kWRow + tp_slot(tp, kc) * 4) = d;
     }
     __syncthreads();
     load_step(t + kWTok, cur);  // next step's loads fly over the MFMAs
 #pragma unroll
     for (int ks = 0; ks < kWTok / 32; ++ks) {
-      const bf16x8_t av = *reinterpret_cast<const bf16x8_t*>(s_x + (16 * wave + r) * kWRow + (32 * ks + 8 * g) * 2);
+      const int xc = 16 * wave + r;  // column of the slice
+      const bf16x8_t av = *reinterpret_cast<const bf16x8_t*>(
+          s_x + xc * kWRow + tp_slot(16 * ks + 4 * g, xc >> 3) * 4);
 #pragma unroll
       for (int ft = 0; ft < NTF; ++ft) {
         const int off = (16 * ft + r) * kWRow + (32 * ks + 8 * g) * 2;
