@@ -222,19 +222,31 @@ __global__ __launch_bounds__(NW * 64) __attribute__((amdgpu_waves_per_eu(4))) vo
         bf16x8_t, buf_load16(rphi, ok ? (uint32_t)((ci * C + col) * FD + 32 * ks + 8 * g) * 2u : kBufOob));
   };
 
-  // ---- gh partials per chunk: sum_c g_sub[c] * x[i][c]
+  // ---- gh partials per chunk: sum_c g_sub[c] * x[i][c].  The g_sub loads go
+  // out in batches of GB independent loads (one register set each) before
+  // they are consumed; one reused register set would wait a round trip each.
+  constexpr int GB = KJ < 6 ? KJ : 6;
 #pragma unroll
-  for (int j = 0; j < KJ; ++j) {
-    int ci, c0;
-    chunk(j, ci, c0);
-    const bool ok = c0 + 8 * g < C;
-    const U32x4 gv = buf_load16(rgs, ok ? (uint32_t)(r * C + c0 + 8 * g) * 2u : kBufOob);
-    float acc = 0.f;
+  for (int j0 = 0; j0 < KJ; j0 += GB) {
+    U32x4 gvb[GB];
 #pragma unroll
-    for (int e = 0; e < 4; ++e) acc = dot2_bf16(gv.v[e], xs[j].v[e], acc);
-    acc += xor_lane16(acc);
-    acc += xor_lane32(acc);
-    if (g == 0) s_gp[wave + NW * j][r] = acc;
+    for (int u = 0; u < GB; ++u) {
+      int ci, c0;
+      chunk(j0 + u, ci, c0);
+      const bool ok = j0 + u < KJ && c0 + 8 * g < C;
+      gvb[u] = buf_load16(rgs, ok ? (uint32_t)(r * C + c0 + 8 * g) * 2u : kBufOob);
+    }
+#pragma unroll
+    for (int u = 0; u < GB; ++u) {
+      const int j = j0 + u;
+      if (j >= KJ) break;
+      float acc = 0.f;
+#pragma unroll
+      for (int e = 0; e < 4; ++e) acc = dot2_bf16(gvb[u].v[e], xs[j].v[e], acc);
+      acc += xor_lane16(acc);
+      acc += xor_lane32(acc);
+      if (g == 0) s_gp[wave + NW * j][r] = acc;
+    }
   }
   __syncthreads();
 
@@ -301,28 +313,52 @@ __global__ __launch_bounds__(NW * 64) __attribute__((amdgpu_waves_per_eu(4))) vo
   msum += xor_lane32(msum);
   const float mean = msum / (float)NC;  // mean_k(xn * gxn)
 
-  // ---- gxn = phi . (alpha * g_raw) on MFMA
-  auto gxn_tile = [&](int j, int h) {
-    f32x4_t d = f32x4_t{0.f, 0.f, 0.f, 0.f};
-#pragma unroll
-    for (int ks = 0; ks < KS; ++ks) {
-      const bf16x8_t av = phi_op(j, h, ks);
-      d = __builtin_amdgcn_mfma_f32_16x16x32_bf16(av, bhi[ks], d, 0, 0, 0);
-      d = __builtin_amdgcn_mfma_f32_16x16x32_bf16(av, blo[ks], d, 0, 0, 0);
-    }
-    return d;
+  // ---- gxn = phi . (alpha * g_raw) on MFMA, and
+  //      g_x = inv * (gxn - xn * mean) + h_pre[i] * g_sub.
+  // Where phi is one K-step wide (FD <= 32), a chunk's phi A operands and its
+  // g_sub go out one chunk ahead (two register sets), so the MFMAs and the
+  // g_x arithmetic of chunk j run while chunk j + 1's loads are in flight
+  // instead of each load being waited for in turn.  Wider phi (n = 8, full)
+  // keeps one set: two would spill.
+  constexpr bool PF = KS == 1;
+  struct ChunkIn {
+    bf16x8_t av[2][KS];
+    U32x4 gv;
   };
-
-  // ---- g_x = inv * (gxn - xn * mean) + h_pre[i] * g_sub
+  auto load_chunk = [&](int j, ChunkIn& in) {
+    int ci, c0;
+    chunk(j, ci, c0);
+#pragma unroll
+    for (int h = 0; h < 2; ++h)
+#pragma unroll
+      for (int ks = 0; ks < KS; ++ks) in.av[h][ks] = phi_op(j, h, ks);
+    const bool ok = c0 + 8 * g < C;
+    in.gv = buf_load16(rgs, ok ? (uint32_t)(r * C + c0 + 8 * g) * 2u : kBufOob);
+  };
+  ChunkIn cin[PF ? 2 : 1];
+  if constexpr (PF) load_chunk(0, cin[0]);
 #pragma unroll
   for (int j = 0; j < KJ; ++j) {
+    ChunkIn& cur = cin[PF ? (j & 1) : 0];
+    if constexpr (PF) {
+      if (j + 1 < KJ) load_chunk(j + 1, cin[(j + 1) & 1]);
+    }
     int ci, c0;
     chunk(j, ci, c0);
     const bool ok = c0 + 8 * g < C;
     f32x4_t d2[2];
 #pragma unroll
-    for (int h = 0; h < 2; ++h) d2[h] = gxn_tile(j, h);
-    const U32x4 gv = buf_load16(rgs, ok ? (uint32_t)(r * C + c0 + 8 * g) * 2u : kBufOob);
+    for (int h = 0; h < 2; ++h) {
+      f32x4_t d = f32x4_t{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+      for (int ks = 0; ks < KS; ++ks) {
+        const bf16x8_t av = PF ? cur.av[h][ks] : phi_op(j, h, ks);  // one operand live at a time
+        d = __builtin_amdgcn_mfma_f32_16x16x32_bf16(av, bhi[ks], d, 0, 0, 0);
+        d = __builtin_amdgcn_mfma_f32_16x16x32_bf16(av, blo[ks], d, 0, 0, 0);
+      }
+      d2[h] = d;
+    }
+    const U32x4 gv = PF ? cur.gv : buf_load16(rgs, ok ? (uint32_t)(r * C + c0 + 8 * g) * 2u : kBufOob);
     const float hp = s_hp[r][ci];
     U32x4 o;
 #pragma unroll
