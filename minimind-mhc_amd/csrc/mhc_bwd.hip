@@ -319,8 +319,11 @@ __global__ __launch_bounds__(NW * 64) __attribute__((amdgpu_waves_per_eu(4))) vo
   // g_sub go out one chunk ahead (two register sets), so the MFMAs and the
   // g_x arithmetic of chunk j run while chunk j + 1's loads are in flight
   // instead of each load being waited for in turn.  Wider phi (n = 8, full)
-  // keeps one set: two would spill.
+  // keeps one set, loaded at the start of its chunk (CH: one round trip a
+  // chunk) up to 12 chunks a wave, and operand by operand beyond that (the
+  // whole set would spill).
   constexpr bool PF = KS == 1;
+  constexpr bool CH = !PF && KJ <= 12;
   struct ChunkIn {
     bf16x8_t av[2][KS];
     U32x4 gv;
@@ -342,6 +345,8 @@ __global__ __launch_bounds__(NW * 64) __attribute__((amdgpu_waves_per_eu(4))) vo
     ChunkIn& cur = cin[PF ? (j & 1) : 0];
     if constexpr (PF) {
       if (j + 1 < KJ) load_chunk(j + 1, cin[(j + 1) & 1]);
+    } else if constexpr (CH) {
+      load_chunk(j, cur);
     }
     int ci, c0;
     chunk(j, ci, c0);
@@ -352,13 +357,13 @@ __global__ __launch_bounds__(NW * 64) __attribute__((amdgpu_waves_per_eu(4))) vo
       f32x4_t d = f32x4_t{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
       for (int ks = 0; ks < KS; ++ks) {
-        const bf16x8_t av = PF ? cur.av[h][ks] : phi_op(j, h, ks);  // one operand live at a time
+        const bf16x8_t av = PF || CH ? cur.av[h][ks] : phi_op(j, h, ks);
         d = __builtin_amdgcn_mfma_f32_16x16x32_bf16(av, bhi[ks], d, 0, 0, 0);
         d = __builtin_amdgcn_mfma_f32_16x16x32_bf16(av, blo[ks], d, 0, 0, 0);
       }
       d2[h] = d;
     }
-    const U32x4 gv = PF ? cur.gv : buf_load16(rgs, ok ? (uint32_t)(r * C + c0 + 8 * g) * 2u : kBufOob);
+    const U32x4 gv = PF || CH ? cur.gv : buf_load16(rgs, ok ? (uint32_t)(r * C + c0 + 8 * g) * 2u : kBufOob);
     const float hp = s_hp[r][ci];
     U32x4 o;
 #pragma unroll
