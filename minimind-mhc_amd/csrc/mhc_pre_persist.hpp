@@ -26,6 +26,12 @@
 //   * x tiles are DEPTH-buffered in registers.  The loads of tile t+DEPTH go
 //     out chunk by chunk while tile t's pre-aggregate frees its registers, so
 //     load issue overlaps the VALU work instead of stalling all waves at once;
+//   * with row staging (ROW; C == 256 * KB, phi in registers, no norm) the
+//     in-flight tile is loaded as whole-row 1 KiB pieces instead of in the
+//     MFMA operand layout, and at the start of its step goes through LDS
+//     (one more barrier a tile) into the operand registers: the operand
+//     layout's loads split every 128-byte line between two waves, which
+//     streams ~20% slower;
 //   * x loads and sub_in stores are raw buffer ops bounded by a per-tile
 //     descriptor: missing tokens / columns are zero-filled (or dropped) by
 //     hardware, so no load sits behind a branch and the compiler waits only
@@ -35,7 +41,7 @@
 //     also wait for the prefetch.  Gate scalars and biases are read once, with
 //     branch-free loads issued before everything else, and kept in LDS as fp32.
 //
-// Per tile, one workgroup barrier:
+// Per tile, one workgroup barrier (two with row staging):
 //   1. all waves: sum of squares + MFMA partial projections -> LDS (two slots,
 //      alternating per tile, so a fast wave may start the next tile's partials
 //      while others still read this tile's);
