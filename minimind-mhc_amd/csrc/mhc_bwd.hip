@@ -498,18 +498,14 @@ __device__ __forceinline__ int seg_of(int f, int n) { return f < n ? 0 : (f < 2 
 // Sum of w[r * stride], r < R (R <= 64, at most 64 token ranges), in a fixed
 // order: batches of 32 independent loads (so a thread waits for one memory
 // round trip per batch, not one per range), each summed as a pairwise tree.
-// Indices past R re-read range R - 1 and are dropped: branch-free, in bounds.
+// Slots past R load nothing (R is uniform: a scalar branch, no divergence).
 constexpr int kRangeBatch = 32;
 __device__ __forceinline__ float sum_ranges(const float* __restrict__ w, int64_t stride, int R) {
   float total = 0.f;
   for (int r0 = 0; r0 < R; r0 += kRangeBatch) {
     float v[kRangeBatch];
 #pragma unroll
-    for (int u = 0; u < kRangeBatch; ++u) {
-      const int r = r0 + u;
-      const float t = w[(int64_t)(r < R ? r : R - 1) * stride];
-      v[u] = r < R ? t : 0.f;
-    }
+    for (int u = 0; u < kRangeBatch; ++u) v[u] = r0 + u < R ? w[(int64_t)(r0 + u) * stride] : 0.f;
 #pragma unroll
     for (int h = kRangeBatch / 2; h > 0; h >>= 1)
 #pragma unroll
