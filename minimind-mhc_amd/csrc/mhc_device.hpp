@@ -47,6 +47,21 @@ __device__ __forceinline__ int64_t wave_uniform(int64_t v) {
   return (int64_t)(((uint64_t)hi << 32) | lo);
 }
 
+// Cache policy for data a launch streams exactly once (x in, outputs out): the
+// non-temporal bit.  With it the forward's x reads and stream-sized writes
+// stop displacing, and being displaced by, the previous launch's dirty lines;
+// measured on MI355X at 16384 tokens, n = 4, C = 768 (pre + post step, four
+// rotating input sets): 74.5 -> 65.5 us.
+constexpr int kNt = 2;
+
+__device__ __forceinline__ U32x4 buf_load16_nt(__amdgpu_buffer_rsrc_t r, uint32_t off, int soff) {
+  return __builtin_bit_cast(U32x4, __builtin_amdgcn_raw_buffer_load_b128(r, (int)off, soff, kNt));
+}
+
+__device__ __forceinline__ void buf_store16_nt(__amdgpu_buffer_rsrc_t r, uint32_t off, const U32x4& v) {
+  __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(u32x4_t, v), r, (int)off, 0, kNt);
+}
+
 __device__ __forceinline__ U32x4 buf_load16(__amdgpu_buffer_rsrc_t r, uint32_t off) {
   return __builtin_bit_cast(U32x4, __builtin_amdgcn_raw_buffer_load_b128(r, (int)off, 0, 0));
 }

@@ -47,6 +47,25 @@ __device__ __forceinline__ void load_pack(const T* p, float (&o)[K]) {
   for (int k = 0; k < K; ++k) o[k] = Elem<T>::get(pk.v[k]);
 }
 
+// 16-byte packs with the non-temporal cache policy (data streamed once).
+template <typename T, int K>
+__device__ __forceinline__ void load_pack_nt(const T* p, float (&o)[K]) {
+  static_assert(sizeof(Pack<T, K>) == 16, "16-byte packs");
+  const Pack<T, K> pk =
+      __builtin_bit_cast(Pack<T, K>, __builtin_nontemporal_load(reinterpret_cast<const u32x4_t*>(p)));
+#pragma unroll
+  for (int k = 0; k < K; ++k) o[k] = Elem<T>::get(pk.v[k]);
+}
+
+template <typename T, int K>
+__device__ __forceinline__ void store_pack_nt(T* p, const float (&o)[K]) {
+  static_assert(sizeof(Pack<T, K>) == 16, "16-byte packs");
+  Pack<T, K> pk;
+#pragma unroll
+  for (int k = 0; k < K; ++k) pk.v[k] = Elem<T>::put(o[k]);
+  __builtin_nontemporal_store(__builtin_bit_cast(u32x4_t, pk), reinterpret_cast<u32x4_t*>(p));
+}
+
 template <typename T, int K>
 __device__ __forceinline__ void store_pack(T* p, const float (&o)[K]) {
   Pack<T, K> pk;
@@ -63,7 +82,8 @@ __device__ __forceinline__ float rnd(float v) {
 
 // Rounding points follow the reference's torch ops (model/mhc_fused.py:861-863):
 // the einsum result, the H_post * F product and their sum are each a tensor of
-// the stream dtype.
+// the stream dtype.  x reads and out writes are non-temporal (each byte once per
+// launch); F keeps the default policy (measured slower non-temporal).
 template <typename XT, typename FT, int N, bool RES>
 __global__ __launch_bounds__(256) void post_vec_kernel(PostArgs a) {
   constexpr int V = 16 / sizeof(XT);
@@ -79,7 +99,7 @@ __global__ __launch_bounds__(256) void post_vec_kernel(PostArgs a) {
 
   float xv[N][V];
 #pragma unroll
-  for (int j = 0; j < N; ++j) load_pack<XT, V>(x + (int64_t)j * C, xv[j]);
+  for (int j = 0; j < N; ++j) load_pack_nt<XT, V>(x + (int64_t)j * C, xv[j]);
   float fv[V];
   load_pack<FT, V>(static_cast<const FT*>(a.f_out) + tok * C + c, fv);
   float hp[N];
@@ -103,7 +123,7 @@ __global__ __launch_bounds__(256) void post_vec_kernel(PostArgs a) {
       }
       o[v] = __fadd_rn(acc, rnd<XT>(__fmul_rn(hp[i], fv[v])));
     }
-    store_pack<XT, V>(out + (int64_t)i * C, o);
+    store_pack_nt<XT, V>(out + (int64_t)i * C, o);
   }
 }
 

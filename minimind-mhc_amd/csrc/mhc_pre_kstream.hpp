@@ -215,8 +215,7 @@ __global__ __launch_bounds__(kKsWaves * 64) void pre_kstream_kernel(PreArgs a) {
       const uint32_t xo = tt < valid ? (uint32_t)(tt * NC + c) * 2u : kBufOob;
 #pragma unroll
       for (int i = 0; i < N; ++i)
-        xv[b][i] = __builtin_bit_cast(U32x4,
-                                      __builtin_amdgcn_raw_buffer_load_b128(rx, (int)xo, i * C * 2, 0));
+        xv[b][i] = buf_load16_nt(rx, xo, i * C * 2);  // x's last use in this launch
     }
   };
   auto pa_finish = [&](int round, const U32x4 (&xv)[PB][N]) {
@@ -239,7 +238,7 @@ __global__ __launch_bounds__(kKsWaves * 64) void pre_kstream_kernel(PreArgs a) {
       }
       // whole offset in the vector offset, scalar offset the literal 0 (see
       // persist_preagg: a 128-bit store reads its data registers after issue)
-      buf_store16(rsub, tt < valid ? (uint32_t)(tt * C + c) * 2u : kBufOob, pk);
+      buf_store16_nt(rsub, tt < valid ? (uint32_t)(tt * C + c) * 2u : kBufOob, pk);
     }
   };
   U32x4 xa[PB][N];
@@ -349,7 +348,7 @@ __global__ __launch_bounds__(kKsWaves * 64) void pre_kstream_kernel(PreArgs a) {
       y.v[1] = pack_bf16x2(bf16lo(pk.v[1]) * sc * w0.z, bf16hi(pk.v[1]) * sc * w0.w);
       y.v[2] = pack_bf16x2(bf16lo(pk.v[2]) * sc * w1.x, bf16hi(pk.v[2]) * sc * w1.y);
       y.v[3] = pack_bf16x2(bf16lo(pk.v[3]) * sc * w1.z, bf16hi(pk.v[3]) * sc * w1.w);
-      buf_store16(rsub, it < valid ? (uint32_t)(it * C + c) * 2u : kBufOob, y);
+      buf_store16_nt(rsub, it < valid ? (uint32_t)(it * C + c) * 2u : kBufOob, y);
     }
   }
 }
