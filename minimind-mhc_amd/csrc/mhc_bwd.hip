@@ -603,7 +603,8 @@ __global__ __launch_bounds__(512) void weights_mfma_kernel(WeightsArgs a, int64_
   auto tp_slot = [](int pair, int group) { return pair ^ (4 * (group & 7)); };
 
   // Everything one step reads from memory; the next step's copy is loaded
-  // while the current step's MFMAs run.
+  // while the current step's MFMAs run.  x is read non-temporally (its last
+  // use in the backward).
   struct Step {
     U32x4 xa, xb;
     float ga[UPT], gb[UPT], ia[UPT], ib[UPT], ma[UPT], mb[UPT];
@@ -612,8 +613,8 @@ __global__ __launch_bounds__(512) void weights_mfma_kernel(WeightsArgs a, int64_
     const int valid = t < te ? (int)(te - t < kWTok ? te - t : kWTok) : 0;
     const auto rs = make_rsrc(static_cast<const uint16_t*>(a.x) + (t < te ? t : 0) * NC,
                               (uint32_t)valid * NC * 2u);
-    st.xa = buf_load16(rs, okc ? (uint32_t)((2 * tp) * NC + col) * 2u : kBufOob);
-    st.xb = buf_load16(rs, okc ? (uint32_t)((2 * tp + 1) * NC + col) * 2u : kBufOob);
+    st.xa = buf_load16_nt(rs, okc ? (uint32_t)((2 * tp) * NC + col) * 2u : kBufOob, 0);
+    st.xb = buf_load16_nt(rs, okc ? (uint32_t)((2 * tp + 1) * NC + col) * 2u : kBufOob, 0);
 #pragma unroll
     for (int u = 0; u < UPT; ++u) {
       const int idx = tid + 512 * u;

@@ -62,6 +62,15 @@ __device__ __forceinline__ void buf_store16_nt(__amdgpu_buffer_rsrc_t r, uint32_
   __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(u32x4_t, v), r, (int)off, 0, kNt);
 }
 
+// The same policy through a flat pointer (16 bytes, 16-byte aligned).
+__device__ __forceinline__ U32x4 ld16_nt(const void* p) {
+  return __builtin_bit_cast(U32x4, __builtin_nontemporal_load(static_cast<const u32x4_t*>(p)));
+}
+
+__device__ __forceinline__ void st16_nt(void* p, const U32x4& v) {
+  __builtin_nontemporal_store(__builtin_bit_cast(u32x4_t, v), static_cast<u32x4_t*>(p));
+}
+
 __device__ __forceinline__ U32x4 buf_load16(__amdgpu_buffer_rsrc_t r, uint32_t off) {
   return __builtin_bit_cast(U32x4, __builtin_amdgcn_raw_buffer_load_b128(r, (int)off, 0, 0));
 }

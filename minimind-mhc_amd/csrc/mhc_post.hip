@@ -317,7 +317,9 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(N >= 8 ? 2 
 // x stay packed (4 VGPRs per 8 columns, not 8 fp32), so n = 8 fits three
 // waves per SIMD with no spills where the fp32 form needed more than 256
 // VGPRs.  Sums run in a different order than post_bwd_vec_kernel's fmaf
-// chains: results agree to fp32 rounding before the bf16 store.
+// chains: results agree to fp32 rounding before the bf16 store.  g and x
+// reads and the g_x / g_F writes are non-temporal (68.7 -> 60.5 us at 16384
+// tokens, n = 4, C = 768 on MI355X); F keeps the default policy.
 template <int N, bool RES>
 __global__ __launch_bounds__(256) void post_bwd_bf16_kernel(PostBwdArgs a) {
   static_assert(N % 2 == 0, "pairs of streams");
@@ -366,7 +368,7 @@ __global__ __launch_bounds__(256) void post_bwd_bf16_kernel(PostBwdArgs a) {
     const int c = cv * 8;
     U32x4 gv[N];
 #pragma unroll
-    for (int i = 0; i < N; ++i) gv[i] = *reinterpret_cast<const U32x4*>(g + (int64_t)i * C + c);
+    for (int i = 0; i < N; ++i) gv[i] = ld16_nt(g + (int64_t)i * C + c);
     const U32x4 fv = *reinterpret_cast<const U32x4*>(f + c);
 #pragma unroll
     for (int i = 0; i < N; ++i)
@@ -375,7 +377,7 @@ __global__ __launch_bounds__(256) void post_bwd_bf16_kernel(PostBwdArgs a) {
     if constexpr (RES) {
       U32x4 xv[N];
 #pragma unroll
-      for (int j = 0; j < N; ++j) xv[j] = *reinterpret_cast<const U32x4*>(x + (int64_t)j * C + c);
+      for (int j = 0; j < N; ++j) xv[j] = ld16_nt(x + (int64_t)j * C + c);
 #pragma unroll
       for (int i = 0; i < N; ++i)
 #pragma unroll
@@ -408,7 +410,7 @@ __global__ __launch_bounds__(256) void post_bwd_bf16_kernel(PostBwdArgs a) {
       }
       of.v[k] = pack_bf16x2(lo, hi);
     }
-    *reinterpret_cast<U32x4*>(gf + c) = of;
+    st16_nt(gf + c, of);
     if constexpr (RES) {
 #pragma unroll
       for (int j = 0; j < N; ++j) {
@@ -424,7 +426,7 @@ __global__ __launch_bounds__(256) void post_bwd_bf16_kernel(PostBwdArgs a) {
           }
           o.v[k] = pack_bf16x2(lo, hi);
         }
-        if (gx) *reinterpret_cast<U32x4*>(gx + (int64_t)j * C + c) = o;
+        if (gx) st16_nt(gx + (int64_t)j * C + c, o);
       }
     }
   }
