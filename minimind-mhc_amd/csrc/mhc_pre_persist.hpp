@@ -190,8 +190,12 @@ struct PersistRow {
   static constexpr int RCH = NC / 8;                   // 16-byte chunks of a token row
   static constexpr int PW = N * KB;                    // 1 KiB pieces per wave
   static constexpr int BYTES = kTokTile * NC * 2;      // the tile in LDS
-  static constexpr int R1 = (PW + 2) / 3;              // load batches [0,R1) [R1,R2) [R2,PW)
-  static constexpr int R2 = (2 * PW + 2) / 3;          // at three points of a step
+  // Load batches [0,R1) [R1,R2) [R2,PW) at three points of a step.  The
+  // second (after the first barrier) carries half the tile: measured on MI355X
+  // at C2 (PW = 12), splits 4/8/12 -> 4/10/12 took the pre launch from
+  // 30.0-31.3 to 29.6 us; 4/9, 3/9 and 5/10 measured the same, 4/11 slower.
+  static constexpr int R1 = (PW + 2) / 3;
+  static constexpr int R2 = 5 * PW / 6;
   static constexpr bool OK = P::NREG == P::NT && RCH % 16 == 0 &&
                              P::SHARED + 256 + BYTES <= kLdsBytes;
 };
