@@ -53,13 +53,19 @@ __device__ __forceinline__ int64_t wave_uniform(int64_t v) {
 // measured on MI355X at 16384 tokens, n = 4, C = 768 (pre + post step, four
 // rotating input sets): 74.5 -> 65.5 us.
 constexpr int kNt = 2;
+// The same with the device-scope bit (sc1) as well: measured faster for the
+// persistent n <= 4 pre kernel (29.9 -> 29.0 us at C2) and slightly slower for
+// the n = 8 kernel and the weight kernel, which keep kNt.
+constexpr int kNtSc1 = kNt | 16;
 
+template <int POL = kNt>
 __device__ __forceinline__ U32x4 buf_load16_nt(__amdgpu_buffer_rsrc_t r, uint32_t off, int soff) {
-  return __builtin_bit_cast(U32x4, __builtin_amdgcn_raw_buffer_load_b128(r, (int)off, soff, kNt));
+  return __builtin_bit_cast(U32x4, __builtin_amdgcn_raw_buffer_load_b128(r, (int)off, soff, POL));
 }
 
+template <int POL = kNt>
 __device__ __forceinline__ void buf_store16_nt(__amdgpu_buffer_rsrc_t r, uint32_t off, const U32x4& v) {
-  __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(u32x4_t, v), r, (int)off, 0, kNt);
+  __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(u32x4_t, v), r, (int)off, 0, POL);
 }
 
 // The same policy through a flat pointer (16 bytes, 16-byte aligned).

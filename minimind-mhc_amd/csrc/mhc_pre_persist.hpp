@@ -36,8 +36,8 @@
 //     descriptor: missing tokens / columns are zero-filled (or dropped) by
 //     hardware, so no load sits behind a branch and the compiler waits only
 //     for the tile it is about to use;
-//   * x loads and sub_in stores carry the non-temporal cache policy (each
-//     byte is touched once per launch);
+//   * x loads and sub_in stores carry the non-temporal cache policy with the
+//     device-scope bit (each byte is touched once per launch);
 //   * the tile loop issues no other global load: the vector-memory counter
 //     retires in order, so waiting on any load issued after a prefetch would
 //     also wait for the prefetch.  Gate scalars and biases are read once, with
@@ -217,7 +217,7 @@ __device__ __forceinline__ void persist_load_row(U32x4 (&xn)[KB][N], __amdgpu_bu
   using RW = PersistRow<N, MODE, KB>;
 #pragma unroll
   for (int p = P0; p < P1; ++p)
-    xn[p / N][p % N] = buf_load16_nt(rsrc, (uint32_t)lane * 16u, (wave * RW::PW + p) * 1024);
+    xn[p / N][p % N] = buf_load16_nt<kNtSc1>(rsrc, (uint32_t)lane * 16u, (wave * RW::PW + p) * 1024);
 }
 
 // This wave's row pieces [P0, P1) of a tile -> LDS.
@@ -289,7 +289,7 @@ __device__ __forceinline__ void persist_load_part(U32x4 (&xr)[KB][N], __amdgpu_b
     const uint32_t voff = lo == kBufOob ? kBufOob : row_off + lo;
 #pragma unroll
     for (int i = 0; i < N; ++i)
-      xr[q][i] = buf_load16_nt(rsrc, voff, (i * C + c0) * 2);
+      xr[q][i] = buf_load16_nt<kNtSc1>(rsrc, voff, (i * C + c0) * 2);
   }
 }
 
@@ -487,7 +487,7 @@ __device__ __forceinline__ void persist_preagg(const PreArgs& a, const U32x4 (&x
     // the compiler only keeps the next VALU write off those registers for
     // stores of that form.  With a register soffset it reused the first data
     // register at once and some lanes stored the new value.
-    buf_store16_nt(rsub, lo == kBufOob ? kBufOob : sub_row + lo + (uint32_t)c0 * 2u, pk);
+    buf_store16_nt<kNtSc1>(rsub, lo == kBufOob ? kBufOob : sub_row + lo + (uint32_t)c0 * 2u, pk);
   }
   if constexpr (NORM) {
     q2 += __shfl_xor(q2, 16, 64);
@@ -528,7 +528,7 @@ __device__ __forceinline__ void persist_norm_store(const PreArgs& a, const Persi
     y.v[2] = pack_bf16x2(bf16lo(pk.v[2]) * sc * w1.x, bf16hi(pk.v[2]) * sc * w1.y);
     y.v[3] = pack_bf16x2(bf16lo(pk.v[3]) * sc * w1.z, bf16hi(pk.v[3]) * sc * w1.w);
     // whole offset in the vector offset, scalar offset the literal 0 (see above)
-    buf_store16_nt(rsub, lo == kBufOob ? kBufOob : sub_row + lo + (uint32_t)c0 * 2u, y);
+    buf_store16_nt<kNtSc1>(rsub, lo == kBufOob ? kBufOob : sub_row + lo + (uint32_t)c0 * 2u, y);
   }
 }
 
