@@ -5,10 +5,12 @@
  * enqueues its kernels on that stream and returns without synchronising.
  * The caller allocates every output (as the reference's autograd Functions do
  * with torch.empty); the library never allocates or frees device memory and
- * keeps no state between calls (its one process-wide setting is the kernel
- * choice of mhc_pre_token_threshold), so calls are re-entrant and capturable.  One
- * entry point (mhc_pre_bwd_weights) needs scratch for token-range partial
- * sums; the caller passes it as a workspace argument.
+ * keeps no state between calls, so calls are re-entrant and capturable.  It has
+ * two process-wide settings, both kernel choices: mhc_pre_token_threshold and
+ * mhc_pre_row_staging.  One entry point (mhc_pre_bwd_weights) needs scratch
+ * for token-range partial sums; the caller passes it as a workspace argument,
+ * or calls mhc_pre_bwd_weights_noalloc, which uses a static device array the
+ * library holds instead.
  *
  * Return value: 0 on success.  Otherwise a hipError_t code
  * (hipErrorInvalidValue = 1 for bad arguments); mhc_last_error() then returns a
@@ -323,6 +325,28 @@ int mhc_pre_bwd_weights(const void* x, int x_dtype, const float* inv_rms, const 
                         void* g_bias_post, void* g_alpha_res, void* g_bias_res, void* workspace,
                         int64_t workspace_bytes, int64_t M, int n, int C, int mode,
                         hipStream_t stream);
+
+/*
+ * mhc_pre_bwd_weights without a workspace argument: the token-range partial
+ * sums go to a scratch array in device memory that the library holds (32 MiB
+ * per device, for the life of the process), so the call allocates nothing.
+ * Same arguments and results as mhc_pre_bwd_weights, minus the workspace; the
+ * token ranges are capped to what the scratch holds, so sums may group
+ * differently (fp32 rounding only).  Rejects shapes whose one-range partials,
+ * (n*C*FD + 2*FD) * 4 bytes, exceed the scratch (e.g. n = 16, C = 2048).
+ * Calls that overlap on one device share the scratch and race: serialise
+ * them (one stream, or events between streams).
+ * No reference counterpart: for callers that cannot allocate device memory
+ * (code under HIP graph capture, serving loops, harnesses that forbid
+ * hipMalloc).
+ */
+int mhc_pre_bwd_weights_noalloc(const void* x, int x_dtype, const float* inv_rms,
+                                const float* mixes_raw, const float* g_raw, const void* alpha_pre,
+                                const void* alpha_post, const void* alpha_res, int param_dtype,
+                                void* g_phi, int phi_dtype, void* g_alpha_pre, void* g_bias_pre,
+                                void* g_alpha_post, void* g_bias_post, void* g_alpha_res,
+                                void* g_bias_res, int64_t M, int n, int C, int mode,
+                                hipStream_t stream);
 
 /*
  * Sinkhorn-Knopp backward: g_in = d output / d input of mhc_sinkhorn_fwd's

@@ -3,8 +3,18 @@
 #include <stdarg.h>
 #include <stdio.h>
 
+#include <mutex>
+
 #include "mhc_amd.h"
 #include "mhc_internal.hpp"
+
+// Scratch of mhc_pre_bwd_weights_noalloc (its token-range partial sums), for
+// callers that cannot allocate.  Each device holds its own copy for the life
+// of the process; calls on one device share it, so calls that overlap on one
+// device (two streams, two threads) race on it.  Every byte a call reads was
+// written earlier in the same call, so nothing needs clearing.
+constexpr int64_t kScratchBytes = int64_t(32) << 20;
+static __device__ __align__(256) float scratch[kScratchBytes / 4];
 
 namespace {
 
@@ -61,6 +71,76 @@ int run_pre(mhc::PreArgs& a, hipStream_t stream, const char* fn) {
                     aligned16(a.x) && aligned16(a.sub_in) && aligned16(a.phi_packed);
   if (!mfma) a.phi_packed = nullptr;
   return hip_status(mfma ? mhc::launch_pre_mfma(a, stream) : mhc::launch_pre_generic(a, stream), fn);
+}
+
+// mhc_pre_bwd_weights / mhc_pre_bwd_weights_noalloc: checks and launch with the
+// given workspace; max_ranges > 0 caps the token ranges to what it holds.
+int weights_entry(const void* x, int x_dtype, const float* inv_rms, const float* mixes_raw,
+                  const float* g_raw, const void* alpha_pre, const void* alpha_post,
+                  const void* alpha_res, int param_dtype, void* g_phi, int phi_dtype,
+                  void* g_alpha_pre, void* g_bias_pre, void* g_alpha_post, void* g_bias_post,
+                  void* g_alpha_res, void* g_bias_res, void* workspace, int64_t workspace_bytes,
+                  int64_t M, int n, int C, int mode, int max_ranges, hipStream_t stream,
+                  const char* fn) {
+  if (M < 0 || n < 1 || n > kMaxN || C < 1) return fail(hipErrorInvalidValue, "%s: bad shape", fn);
+  if (mode != mhc::kFull && mode != mhc::kNoHres && mode != mhc::kHead) return fail(hipErrorInvalidValue, "%s: bad mode %d", fn, mode);
+  if (!dtype_ok(x_dtype) || !dtype_ok(phi_dtype) || !dtype_ok(param_dtype)) return fail(hipErrorInvalidValue, "%s: bad dtype", fn);
+  if (M > kMaxBlocks) return fail(hipErrorInvalidValue, "%s: M too large", fn);
+  if (!g_phi) return fail(hipErrorInvalidValue, "%s: g_phi is required", fn);
+  if (M == 0) return fail(hipErrorInvalidValue, "%s: M == 0 leaves the gradients undefined; zero them instead", fn);
+  if (!x || !inv_rms || !mixes_raw || !g_raw || !alpha_pre) return fail(hipErrorInvalidValue, "%s: null pointer", fn);
+  if (mode != mhc::kHead && !alpha_post) return fail(hipErrorInvalidValue, "%s: alpha_post is required", fn);
+  if (mode == mhc::kFull && !alpha_res) return fail(hipErrorInvalidValue, "%s: alpha_res is required", fn);
+  int64_t need = mhc::weights_workspace_bytes(M, n, C, mode);
+  const int64_t capped = (int64_t)max_ranges * mhc::weights_range_bytes(n, C, mode);
+  if (max_ranges > 0 && capped < need) need = capped;
+  if (!workspace || workspace_bytes < need)
+    return fail(hipErrorInvalidValue, "%s: workspace of %lld bytes needed (got %lld)", fn, (long long)need, (long long)workspace_bytes);
+  if ((reinterpret_cast<uintptr_t>(workspace) & 3) != 0) return fail(hipErrorInvalidValue, "%s: workspace must be 4-byte aligned", fn);
+  mhc::WeightsArgs a{};
+  a.x = x; a.inv_rms = inv_rms; a.mixes = mixes_raw; a.g_raw = g_raw;
+  a.alpha[0] = alpha_pre; a.alpha[1] = alpha_post; a.alpha[2] = alpha_res;
+  a.g_phi = g_phi;
+  a.g_alpha[0] = g_alpha_pre; a.g_alpha[1] = mode == mhc::kHead ? nullptr : g_alpha_post;
+  a.g_alpha[2] = mode == mhc::kFull ? g_alpha_res : nullptr;
+  a.g_bias[0] = g_bias_pre; a.g_bias[1] = mode == mhc::kHead ? nullptr : g_bias_post;
+  a.g_bias[2] = mode == mhc::kFull ? g_bias_res : nullptr;
+  a.work = static_cast<float*>(workspace);
+  a.M = M; a.n = n; a.C = C; a.mode = mode;
+  a.x_dtype = x_dtype; a.phi_dtype = phi_dtype; a.param_dtype = param_dtype;
+  a.max_ranges = max_ranges;
+  return hip_status(mhc::launch_pre_bwd_weights(a, stream), fn);
+}
+
+
+constexpr int kMaxDevices = 64;
+std::mutex g_scratch_mu;
+void* g_scratch_dev[kMaxDevices] = {};
+
+// Device address of this device's copy of scratch (the device `stream` runs
+// on), looked up once per device with that device current.  The host-side
+// name `scratch` is not a device address and is never passed to a kernel.
+int scratch_ptr(hipStream_t stream, void** out, const char* fn) {
+  int cur = 0;
+  if (hipError_t e = hipGetDevice(&cur); e != hipSuccess) return hip_status(e, fn);
+  int dev = cur;
+  if (stream != nullptr)
+    if (hipError_t e = hipStreamGetDevice(stream, &dev); e != hipSuccess) return hip_status(e, fn);
+  if (dev < 0 || dev >= kMaxDevices) return fail(hipErrorInvalidValue, "%s: device %d out of range", fn, dev);
+  std::lock_guard<std::mutex> lock(g_scratch_mu);
+  if (!g_scratch_dev[dev]) {
+    if (dev != cur)
+      if (hipError_t e = hipSetDevice(dev); e != hipSuccess) return hip_status(e, fn);
+    void* p = nullptr;
+    const hipError_t e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+    if (dev != cur) (void)hipSetDevice(cur);
+    if (e != hipSuccess || !p)
+      return fail(e != hipSuccess ? (int)e : (int)hipErrorInvalidSymbol,
+                  "%s: hipGetSymbolAddress(scratch) failed: %s", fn, hipGetErrorString(e));
+    g_scratch_dev[dev] = p;
+  }
+  *out = g_scratch_dev[dev];
+  return 0;
 }
 
 }  // namespace
@@ -421,32 +501,36 @@ int mhc_pre_bwd_weights(const void* x, int x_dtype, const float* inv_rms, const 
                         void* g_bias_post, void* g_alpha_res, void* g_bias_res, void* workspace,
                         int64_t workspace_bytes, int64_t M, int n, int C, int mode,
                         hipStream_t stream) {
-  const char* fn = "mhc_pre_bwd_weights";
-  if (M < 0 || n < 1 || n > kMaxN || C < 1) return fail(hipErrorInvalidValue, "%s: bad shape", fn);
+  return weights_entry(x, x_dtype, inv_rms, mixes_raw, g_raw, alpha_pre, alpha_post, alpha_res,
+                       param_dtype, g_phi, phi_dtype, g_alpha_pre, g_bias_pre, g_alpha_post,
+                       g_bias_post, g_alpha_res, g_bias_res, workspace, workspace_bytes, M, n, C,
+                       mode, 0, stream, "mhc_pre_bwd_weights");
+}
+
+int mhc_pre_bwd_weights_noalloc(const void* x, int x_dtype, const float* inv_rms,
+                                const float* mixes_raw, const float* g_raw, const void* alpha_pre,
+                                const void* alpha_post, const void* alpha_res, int param_dtype,
+                                void* g_phi, int phi_dtype, void* g_alpha_pre, void* g_bias_pre,
+                                void* g_alpha_post, void* g_bias_post, void* g_alpha_res,
+                                void* g_bias_res, int64_t M, int n, int C, int mode,
+                                hipStream_t stream) {
+  const char* fn = "mhc_pre_bwd_weights_noalloc";
+  if (n < 1 || n > kMaxN || C < 1) return fail(hipErrorInvalidValue, "%s: bad shape", fn);
   if (mode != mhc::kFull && mode != mhc::kNoHres && mode != mhc::kHead) return fail(hipErrorInvalidValue, "%s: bad mode %d", fn, mode);
-  if (!dtype_ok(x_dtype) || !dtype_ok(phi_dtype) || !dtype_ok(param_dtype)) return fail(hipErrorInvalidValue, "%s: bad dtype", fn);
-  if (M > kMaxBlocks) return fail(hipErrorInvalidValue, "%s: M too large", fn);
-  if (!g_phi) return fail(hipErrorInvalidValue, "%s: g_phi is required", fn);
-  if (M == 0) return fail(hipErrorInvalidValue, "%s: M == 0 leaves the gradients undefined; zero them instead", fn);
-  if (!x || !inv_rms || !mixes_raw || !g_raw || !alpha_pre) return fail(hipErrorInvalidValue, "%s: null pointer", fn);
-  if (mode != mhc::kHead && !alpha_post) return fail(hipErrorInvalidValue, "%s: alpha_post is required", fn);
-  if (mode == mhc::kFull && !alpha_res) return fail(hipErrorInvalidValue, "%s: alpha_res is required", fn);
-  const int64_t need = mhc::weights_workspace_bytes(M, n, C, mode);
-  if (!workspace || workspace_bytes < need)
-    return fail(hipErrorInvalidValue, "%s: workspace of %lld bytes needed (got %lld)", fn, (long long)need, (long long)workspace_bytes);
-  if ((reinterpret_cast<uintptr_t>(workspace) & 3) != 0) return fail(hipErrorInvalidValue, "%s: workspace must be 4-byte aligned", fn);
-  mhc::WeightsArgs a{};
-  a.x = x; a.inv_rms = inv_rms; a.mixes = mixes_raw; a.g_raw = g_raw;
-  a.alpha[0] = alpha_pre; a.alpha[1] = alpha_post; a.alpha[2] = alpha_res;
-  a.g_phi = g_phi;
-  a.g_alpha[0] = g_alpha_pre; a.g_alpha[1] = mode == mhc::kHead ? nullptr : g_alpha_post;
-  a.g_alpha[2] = mode == mhc::kFull ? g_alpha_res : nullptr;
-  a.g_bias[0] = g_bias_pre; a.g_bias[1] = mode == mhc::kHead ? nullptr : g_bias_post;
-  a.g_bias[2] = mode == mhc::kFull ? g_bias_res : nullptr;
-  a.work = static_cast<float*>(workspace);
-  a.M = M; a.n = n; a.C = C; a.mode = mode;
-  a.x_dtype = x_dtype; a.phi_dtype = phi_dtype; a.param_dtype = param_dtype;
-  return hip_status(mhc::launch_pre_bwd_weights(a, stream), fn);
+  const int64_t per_range = mhc::weights_range_bytes(n, C, mode);
+  if (per_range > kScratchBytes)
+    return fail(hipErrorInvalidValue,
+                "%s: n*C*FD = %lld phi partials need %lld bytes of scratch, more than its %lld bytes; "
+                "use mhc_pre_bwd_weights with a workspace", fn,
+                (long long)((int64_t)n * C * mhc::mode_fd(mode, n)), (long long)per_range,
+                (long long)kScratchBytes);
+  void* ws = nullptr;
+  if (int rc = scratch_ptr(stream, &ws, fn)) return rc;
+  const int64_t ranges = kScratchBytes / per_range;
+  return weights_entry(x, x_dtype, inv_rms, mixes_raw, g_raw, alpha_pre, alpha_post, alpha_res,
+                       param_dtype, g_phi, phi_dtype, g_alpha_pre, g_bias_pre, g_alpha_post,
+                       g_bias_post, g_alpha_res, g_bias_res, ws, kScratchBytes, M, n, C, mode,
+                       ranges > 64 ? 64 : (int)ranges, stream, fn);
 }
 
 int mhc_sinkhorn_bwd(const void* m_in, int in_dtype, const void* g_out, int g_dtype, void* g_in,

@@ -458,10 +458,13 @@ static int weight_ranges(int64_t M) {
   return (int)(r < 1 ? 1 : (r > 64 ? 64 : r));
 }
 
-int64_t weights_workspace_bytes(int64_t M, int n, int C, int mode) {
+int64_t weights_range_bytes(int n, int C, int mode) {
   const int FD = mode_fd(mode, n);
-  const int R = weight_ranges(M);
-  return ((int64_t)R * n * C * FD + (int64_t)R * 2 * FD) * 4;
+  return ((int64_t)n * C * FD + 2 * (int64_t)FD) * 4;
+}
+
+int64_t weights_workspace_bytes(int64_t M, int n, int C, int mode) {
+  return weight_ranges(M) * weights_range_bytes(n, C, mode);
 }
 
 __global__ __launch_bounds__(256) void weights_partial_generic_kernel(WeightsArgs a, int R, int64_t per) {
@@ -729,6 +732,7 @@ hipError_t launch_pre_bwd_weights(const WeightsArgs& a, hipStream_t s) {
                     (reinterpret_cast<uintptr_t>(a.x) & 15) == 0 &&
                     (ntf == 1 || ntf == 2 || ntf == 3 || ntf == 5);  // FD <= 80 (LDS)
   int R = weight_ranges(a.M);
+  if (a.max_ranges > 0 && R > a.max_ranges) R = a.max_ranges;  // smaller workspace
   hipError_t e;
   if (mfma) {
     // about two workgroups per CU, token ranges of whole 64-token steps

@@ -123,6 +123,9 @@ struct WeightsArgs {
   int64_t M;
   int n, C, mode;
   int x_dtype, phi_dtype, param_dtype;
+  // Most token ranges the workspace holds (0: as many as the launcher picks,
+  // i.e. weights_workspace_bytes was allocated).
+  int max_ranges;
 };
 
 // Launchers: return hipSuccess or the launch error.
@@ -147,6 +150,8 @@ hipError_t launch_post(const PostArgs& a, hipStream_t s);
 hipError_t launch_post_bwd(const PostBwdArgs& a, hipStream_t s);
 hipError_t launch_pre_bwd(const PreBwdArgs& a, hipStream_t s);
 int64_t weights_workspace_bytes(int64_t M, int n, int C, int mode);
+// Workspace bytes of one token range (its phi partials and alpha / bias sums).
+int64_t weights_range_bytes(int n, int C, int mode);
 hipError_t launch_pre_bwd_weights(const WeightsArgs& a, hipStream_t s);
 hipError_t launch_sinkhorn_bwd(const void* m_in, int in_dtype, const void* g_out, int g_dtype,
                                void* g_in, int gi_dtype, int64_t batch, int n, int iters,

@@ -76,6 +76,11 @@ _SIGNATURES = {
                                  _P, _P, _P, _P, _P, _P,  # g_alpha/bias pre, post, res
                                  _P, _I64,                # workspace, bytes
                                  _I64, _I, _I, _I, _P]),
+    "mhc_pre_bwd_weights_noalloc": (_I, [_P, _I, _P, _P, _P,   # x, x_dt, inv, mixes, g_raw
+                                         _P, _P, _P, _I,       # alphas, param_dt
+                                         _P, _I,               # g_phi, phi_dt
+                                         _P, _P, _P, _P, _P, _P,
+                                         _I64, _I, _I, _I, _P]),
     "mhc_sinkhorn_bwd": (_I, [_P, _I, _P, _I, _P, _I, _I64, _I, _I, _F, _P]),
 }
 
