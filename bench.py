@@ -15,9 +15,11 @@ the stream it runs on; value = tokens / (mean pre + mean post launch time).  A c
 flush before each kernel) and plain torch copy / sum kernels over 1 GiB
 (`hbm_calibration`) are reported beside it.
 
-Also printed in the JSON line: roofline of the dominant (post) kernel against
-8 TB/s, the CPU oracle baseline (bounded sample, host cores; config 1 and the
-fp32 sample beside it), `backward`: the four backward launches of one
+Also printed in the JSON line: `roofline`, the step (pre + post launch, the
+two kernels of one connection) against 8 TB/s, with each kernel's own
+(`pre_roofline`, `post_roofline`) beside it; the CPU oracle baseline (the
+config-2 shape in bf16 on the host cores, with fp32 and config 1 beside it);
+`backward`: the four backward launches of one
 connection at config 2 (post, Sinkhorn, per-token pre phase, weight
 gradients), each against its algorithmic bytes, plus the fwd + bwd tokens/s of
 the connection (F excluded); `other_configs`: the same kernel pair at config
@@ -25,7 +27,7 @@ the connection (F excluded); `other_configs`: the same kernel pair at config
 figures: `e2e_prefill` (config 3), `e2e_decode` (config 4, eager and
 HIP-graph replay) and `e2e_prefill_moe` (config 5).
 
-`roofline.traffic` is the measured HBM traffic of that kernel per launch:
+`*roofline.traffic` is the measured HBM traffic per launch (per step for `roofline`):
 FETCH_SIZE + WRITE_SIZE from two rocprofv3 --pmc passes over `--traffic`
 (a 1 GiB copy of known size, then one pre and one post launch at config 2),
 each scaled by the copy kernel's bytes / counter ratio.  The figures are read
@@ -136,15 +138,13 @@ def bench_mhc(steps: int, warmup: int, sets: int = 4, n: int = N_STREAMS, C: int
     _sync()
     rec = {"pre": [], "post": []}
     _queue_ahead()
-    t0 = time.perf_counter()
     for _ in range(steps):
         step(rec)
     _sync()
-    wall = (time.perf_counter() - t0) / (steps * sets) * 1e3
     t_pre = [a_.elapsed_time(b_) / sets for a_, b_ in rec["pre"]]
     t_post = [a_.elapsed_time(b_) / sets for a_, b_ in rec["post"]]
     steady = dict(t_pre=sum(t_pre) / len(t_pre), t_post=sum(t_post) / len(t_post),
-                  t_pre_min=min(t_pre), t_post_min=min(t_post), wall=wall)
+                  t_pre_min=min(t_pre), t_post_min=min(t_post))
     if not cold:
         return steady, None
 
@@ -364,39 +364,61 @@ def hbm_calibration(reps: int = 10):
     return out
 
 
-def _cpu_rate(fn, budget_s: float):
-    """Median seconds per call of fn over ~budget_s (at least 3 calls, after one warm-up)."""
-    fn()
+def _cpu_median(fn, warmup: int = 3, reps: int = 10):
+    """Median seconds per call of fn over `reps` calls after `warmup` calls."""
+    for _ in range(warmup):
+        fn()
     times = []
-    t_end = time.perf_counter() + budget_s
-    while time.perf_counter() < t_end or len(times) < 3:
+    for _ in range(reps):
         t0 = time.perf_counter()
         fn()
         times.append(time.perf_counter() - t0)
     times.sort()
-    return times[len(times) // 2], len(times)
+    return times[len(times) // 2]
 
 
-def cpu_baseline(budget_s: float = 12.0):
+def _cpu_model() -> str:
+    try:
+        for line in Path("/proc/cpuinfo").read_text().splitlines():
+            if line.startswith("model name"):
+                return line.split(":", 1)[1].strip()
+    except OSError:
+        pass
+    return "unknown"
+
+
+def _cpu_threads() -> int:
+    """The host CPUs this process may use: its affinity set, capped at the 16
+    CPUs a one-GPU box allots to its job (OMP_NUM_THREADS there)."""
+    try:
+        avail = len(os.sched_getaffinity(0))
+    except AttributeError:
+        avail = os.cpu_count() or 1
+    return max(1, min(avail, 16))
+
+
+def cpu_baseline():
     """The oracle (torch CPU restatement of the reference _forward_ref) on the
-    host cores.  Headline: a bounded sample of the config-2 workload, 512
-    tokens per call, bf16, F a fixed tensor, repeated for ~budget_s; median
-    tokens/s.  Beside it, ~budget_s / 3 each: the same sample in fp32, and
-    config 1 itself (256 tokens, fp32, F = Linear(768, 768) with N(0, 0.02)
-    weights, inside the timed call), each with its algorithmic GB/s."""
+    host cores, under torch.inference_mode(), 3 warm-up calls then the median of
+    10:
+      c2_bf16 : the config-2 workload itself, 16384 tokens, bf16, F a fixed tensor
+                (the headline);
+      c2_fp32 : the same in fp32;
+      c1_fp32 : config 1, 256 tokens, fp32, F = Linear(768, 768) with N(0, 0.02)
+                weights inside the timed call;
+    each with its algorithmic GB/s (the GPU's byte formula)."""
     import torch
     from oracle import mhc_ref as R
     from tests._util import make_params
 
-    cores = min(16, os.cpu_count() or 1)
-    torch.set_num_threads(cores)
+    threads = _cpu_threads()
+    torch.set_num_threads(threads)
     n, C = N_STREAMS, C_DIM
     g = torch.Generator().manual_seed(0)
     res = {}
     with torch.inference_mode():
-        for key, dt, m, budget in (("c2_sample_bf16", torch.bfloat16, 512, budget_s),
-                                   ("c2_sample_fp32", torch.float32, 512, budget_s / 3),
-                                   ("c1_fp32", torch.float32, 256, budget_s / 3)):
+        for key, dt, m in (("c2_bf16", torch.bfloat16, TOKENS), ("c2_fp32", torch.float32, TOKENS),
+                           ("c1_fp32", torch.float32, 256)):
             x = torch.randn(1, m, n * C, generator=g).to(dt)
             p = make_params("full", n, C, dt, g, stress=False)
             if key == "c1_fp32":
@@ -406,15 +428,19 @@ def cpu_baseline(budget_s: float = 12.0):
             else:
                 fz = torch.randn(1, m, C, generator=g).to(dt)
                 f = (lambda z, fz=fz: fz)
-            med, calls = _cpu_rate(lambda: R.mhc_full_forward(x, p, f, n, C, sinkhorn_iters=ITERS),
-                                   budget)
+            med = _cpu_median(lambda: R.mhc_full_forward(x, p, f, n, C, sinkhorn_iters=ITERS))
             nbytes = sum(algorithmic_bytes(n, C, m, s=x.element_size()))
             res[key] = {"tokens_per_s": round(m / med, 1), "GBps": round(nbytes / med / 1e9, 2),
-                        "tokens": m, "calls": calls}
-    head = res["c2_sample_bf16"]
-    return {"value": head["tokens_per_s"], "unit": "tokens/s", "cores": cores, "kind": "port",
-            "sample": f"oracle mhc_full_forward (reference _forward_ref restated), bf16, "
-                      f"512 tokens x n={n} x C={C}, F fixed, median of {head['calls']} calls",
+                        "ms_per_call": round(med * 1e3, 2), "tokens": m}
+            del x, f
+    head = res["c2_bf16"]
+    return {"value": head["tokens_per_s"], "unit": "tokens/s", "cores": threads, "kind": "port",
+            "sample": f"oracle mhc_full_forward (reference _forward_ref restated) on the full "
+                      f"config-2 shape, {TOKENS} tokens x n={n} x C={C}, bf16, F fixed; "
+                      f"median of 10 calls after 3 warm-up",
+            "cpu_model": _cpu_model(), "os_cpu_count": os.cpu_count(),
+            "threads_note": "torch threads = this process's CPU affinity set, capped at the 16 "
+                            "CPUs a one-GPU box allots to its job",
             "runs": res}
 
 
@@ -656,11 +682,20 @@ def main():
                    "tokens": TOKENS, "n": N_STREAMS, "C": C_DIM, "sinkhorn_iters": ITERS,
                    "parallelism": "single GPU",
                    "timing": "steady state over 4 rotating input sets, HIP events per kernel"},
-        "roofline": {"bound": "hbm", "kernel": "post_vec_kernel (res-mix + post-expand)",
-                     "achieved": round(post_gbs, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
-                     "frac": round(post_gbs / HBM_PEAK_GBS, 4),
-                     "traffic": round(tr["post_fetch"] + tr["post_write"]) if tr else None,
-                     "algorithmic_bytes_per_launch": post_b},
+        "roofline": {"bound": "hbm",
+                     "kernel": "one mHC forward step: pre_persist_kernel (RMS + projection + gates "
+                               "+ Sinkhorn + pre-aggregate) then post_vec_kernel (res-mix + "
+                               "post-expand)",
+                     "achieved": round(total_gbs, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                     "frac": round(total_gbs / HBM_PEAK_GBS, 4),
+                     "traffic": (round(tr["pre_fetch"] + tr["pre_write"] + tr["post_fetch"]
+                                       + tr["post_write"]) if tr else None),
+                     "algorithmic_bytes_per_launch": pre_b + post_b},
+        "post_roofline": {"bound": "hbm", "kernel": "post_vec_kernel (res-mix + post-expand)",
+                          "achieved": round(post_gbs, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                          "frac": round(post_gbs / HBM_PEAK_GBS, 4),
+                          "traffic": round(tr["post_fetch"] + tr["post_write"]) if tr else None,
+                          "algorithmic_bytes_per_launch": post_b},
         "pre_roofline": {"bound": "hbm", "kernel": "pre_persist_kernel (RMS + projection + gates "
                                                    "+ Sinkhorn + pre-aggregate)",
                          "achieved": round(pre_gbs, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
@@ -673,13 +708,10 @@ def main():
                      "frac": round(2 * TOKENS * N_STREAMS * C_DIM * 32 / (r["t_pre"] * 1e-3) / 2.5e15, 4),
                      "source": "flops from SQ_INSTS_VALU_MFMA_MOPS_BF16 x 512 "
                                "(profiles/mfma_util_and_traffic.txt), time from this run"},
-        "step_roofline": {"achieved": round(total_gbs, 1), "frac": round(total_gbs / HBM_PEAK_GBS, 4),
-                          "algorithmic_bytes_per_step": pre_b + post_b},
         "kernels": {"pre_ms": round(r["t_pre"], 5), "post_ms": round(r["t_post"], 5),
                     "pre_min_ms": round(r["t_pre_min"], 5), "post_min_ms": round(r["t_post_min"], 5),
                     "pre_GBps": round(pre_gbs, 1), "post_GBps": round(post_gbs, 1),
-                    "pre_bytes": pre_b, "post_bytes": post_b,
-                    "wall_ms_per_kernel_pair": round(r["wall"], 5)},
+                    "pre_bytes": pre_b, "post_bytes": post_b},
         "cold_clean_cache": {"pre_ms": round(rc["t_pre"], 5), "post_ms": round(rc["t_post"], 5),
                              "tokens_per_s": round(TOKENS / (c_ms * 1e-3), 1)},
         "hbm_calibration": hbm_calibration(),

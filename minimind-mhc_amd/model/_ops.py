@@ -18,29 +18,55 @@ from . import _hip as H
 class PhiPack:
     """MFMA operand image of a projection weight, rebuilt when the weight changes.
 
-    The cache is valid for one weight tensor object (held by weak reference,
-    so a replaced parameter never aliases a freed one) at one value of its
-    version counter, which every in-place update (optimizer step,
-    load_state_dict, copy_) bumps.  Weights whose version is not tracked
-    (inference tensors) are repacked on every call.  No reference counterpart: the reference's kernels read the
-    row-major weight directly (model/mhc_fused.py:217-229).
+    Policy:
+      * A weight that trains (grad mode on and phi.requires_grad) is repacked
+        on every call.  Its values change every optimizer step, and in-place
+        writes through .data (p.data.copy_ / normal_) do not bump the version
+        counter, so no cache key could see them.  The pack is one small launch.
+      * Otherwise (inference, frozen weights) the image is cached for one weight
+        tensor object (held by weak reference, so a replaced parameter never
+        aliases a freed one) at one value of its version counter, which
+        optimizer steps, load_state_dict and copy_ bump.  A write through .data
+        is invisible to that key: call invalidate() after one.  Inference
+        tensors, which have no version counter, are repacked on every call.
+    The cache is not pickled or deep-copied; a copy rebuilds it lazily.
+    No reference counterpart: the reference's kernels read the row-major weight
+    directly (model/mhc_fused.py:217-229).
     """
 
     def __init__(self, mode: int):
         self.mode = mode
+        self.invalidate()
+
+    def invalidate(self) -> None:
+        """Drop the cached image; the next call repacks."""
         self._src = None
         self._key = None
         self._buf: Optional[torch.Tensor] = None
 
-    def get(self, phi: torch.Tensor, n: int, C: int) -> Optional[torch.Tensor]:
+    def __getstate__(self):
+        return {"mode": self.mode}
+
+    def __setstate__(self, state):
+        self.mode = state["mode"]
+        self.invalidate()
+
+    def get(self, phi: torch.Tensor, n: int, C: int,
+            training: Optional[bool] = None) -> Optional[torch.Tensor]:
+        """The image of phi (None when (n, C, dtype) has no MFMA kernel).
+        training: whether phi trains in this call; default grad mode and
+        phi.requires_grad (inside an autograd Function's forward, where grad
+        mode is off, pass ctx.needs_input_grad for phi)."""
         lib = H.load()
         if phi.dtype != torch.bfloat16:
             return None
         nbytes = lib.mhc_phi_packed_bytes(n, C, self.mode)
         if nbytes <= 0:
             return None
+        if training is None:
+            training = torch.is_grad_enabled() and phi.requires_grad
         try:
-            version = phi._version
+            version = None if training else phi._version
         except RuntimeError:
             version = None
         key = (phi.data_ptr(), version, phi.device, n, C)
@@ -51,10 +77,35 @@ class PhiPack:
         buf = torch.empty(nbytes, dtype=torch.uint8, device=phi.device)
         H.check(lib.mhc_phi_pack(w.data_ptr(), H.DTYPE_BF16, buf.data_ptr(), n, C, self.mode,
                                  H.stream(phi.device)), "mhc_phi_pack")
-        self._src = weakref.ref(phi)
-        self._key = key if version is not None else None
-        self._buf = buf
+        if version is None:
+            self.invalidate()
+        else:
+            self._src = weakref.ref(phi)
+            self._key = key
+            self._buf = buf
         return buf
+
+
+# Packs of weights that no module owns (the reference-style autograd Functions
+# called directly): id(phi), mode -> (weak reference to phi, PhiPack).
+_PACKS: dict = {}
+
+
+def packed_phi(phi: torch.Tensor, n: int, C: int, mode: int,
+               training: Optional[bool] = None) -> Optional[torch.Tensor]:
+    """MFMA image of phi for a caller without a PhiPack of its own (None when
+    the shape or dtype has no MFMA kernel); training as in PhiPack.get."""
+    if not phi.is_cuda:
+        return None
+    key = (id(phi), mode)
+    ent = _PACKS.get(key)
+    if ent is None or ent[0]() is not phi:
+        if len(_PACKS) >= 256:
+            for k in [k for k, (ref, _) in _PACKS.items() if ref() is None]:
+                del _PACKS[k]
+        ent = (weakref.ref(phi), PhiPack(mode))
+        _PACKS[key] = ent
+    return ent[1].get(phi, n, C, training)
 
 
 def _check_numel(name: str, t: torch.Tensor, want: int) -> None:

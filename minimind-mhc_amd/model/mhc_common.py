@@ -21,20 +21,18 @@ def _is_pow2(n: int) -> bool:
     return n >= 1 and (n & (n - 1)) == 0
 
 
-def fusable_norm(norm, dim: int, x: torch.Tensor, *modules) -> bool:
+def fusable_norm(norm, dim: int, x: torch.Tensor) -> bool:
     """True when an nn.RMSNorm over `dim` can run inside a HIP launch for this
-    call: a forward without autograd (no grad mode, or nothing requiring grad),
-    an affine norm over exactly (dim,)."""
+    call: grad mode off (torch.no_grad / inference_mode) and an affine norm
+    over exactly (dim,).  With grad mode on the norm stays a separate op even
+    when nothing visible here requires grad: the sublayer F is opaque, and the
+    fused launches record no autograd graph that gradients to F's parameters
+    could flow through."""
     if not isinstance(norm, nn.RMSNorm) or norm.weight is None:
         return False
     if tuple(norm.normalized_shape) != (dim,) or not x.is_cuda:
         return False
-    if torch.is_grad_enabled():
-        if x.requires_grad or norm.weight.requires_grad:
-            return False
-        if any(p.requires_grad for m in modules for p in m.parameters()):
-            return False
-    return True
+    return not torch.is_grad_enabled()
 
 
 def norm_eps(norm: nn.RMSNorm, x: torch.Tensor) -> float:
@@ -82,6 +80,8 @@ class _MHCHeadFn(torch.autograd.Function):
     def forward(ctx, x_flat, w_phi, alpha, bias, pre_eps, rms_eps, n, c, packed=None):
         B, L, NC = x_flat.shape
         train = any(ctx.needs_input_grad)
+        if packed is None and n > 1:  # called without the module's pack
+            packed = _ops.packed_phi(w_phi, n, c, H.MODE_HEAD, training=ctx.needs_input_grad[1])
         out, inv, mix = _ops.head(x_flat, w_phi, packed, alpha, bias, n, c, pre_eps, rms_eps,
                                   want_saved=train)
         if train:
@@ -153,7 +153,7 @@ class MHCHead(nn.Module):
         model's final norm, model/model_minimind.py:367-370); without autograd
         it runs inside the head launch."""
         if out_norm is not None:
-            if fusable_norm(out_norm, self.dim, x_flat, self):
+            if fusable_norm(out_norm, self.dim, x_flat):
                 packed = (self._phi_pack.get(self.phi_weight, self.n, self.dim)
                           if self.n > 1 else None)
                 out, _, _ = _ops.head(x_flat, self.phi_weight, packed, self.alpha, self.bias,

@@ -82,7 +82,8 @@ class _PrePhaseFullFn(torch.autograd.Function):
     def forward(ctx, x_flat, w_phi, alpha_pre, bias_pre, alpha_post, bias_post,
                 alpha_res, bias_res, post_mult, pre_eps, rms_eps, n, c):
         B, L, NC = x_flat.shape
-        o = _ops.pre_full(x_flat, w_phi, None, alpha_pre, bias_pre, alpha_post, bias_post,
+        packed = _ops.packed_phi(w_phi, n, c, H.MODE_FULL, training=ctx.needs_input_grad[1])
+        o = _ops.pre_full(x_flat, w_phi, packed, alpha_pre, bias_pre, alpha_post, bias_post,
                           alpha_res, bias_res, n, c, post_mult, pre_eps, rms_eps, 0, 0.0,
                           sinkhorn=False, want_h_pre=True, want_raw=True, want_saved=True)
         ctx.save_for_backward(x_flat.detach().contiguous().view(B * L, NC), w_phi, alpha_pre,
@@ -212,7 +213,7 @@ class MHCConnection_Fused(nn.Module):
         as a separate op, as when F contains it."""
         packed = self._phi_pack.get(self.phi_weight, self.n, self.dim) if x_flat.is_cuda else None
         if in_norm is not None:
-            if fusable_norm(in_norm, self.dim, x_flat, self):
+            if fusable_norm(in_norm, self.dim, x_flat):
                 o = _ops.pre_full(x_flat, self.phi_weight, packed, self.alpha_pre, self.bias_pre,
                                   self.alpha_post, self.bias_post, self.alpha_res, self.bias_res,
                                   self.n, self.dim, self.post_mult_value, self.pre_eps, self.eps,

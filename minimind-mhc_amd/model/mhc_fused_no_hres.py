@@ -30,6 +30,8 @@ class _PrePhaseFn(torch.autograd.Function):
                 post_mult, pre_eps, rms_eps, n, c, packed=None):
         B, L, NC = x_flat.shape
         train = any(ctx.needs_input_grad)
+        if packed is None:  # called as the reference's Function, without the module's pack
+            packed = _ops.packed_phi(w_phi, n, c, H.MODE_NOHRES, training=ctx.needs_input_grad[1])
         o = _ops.pre_nohres(x_flat, w_phi, packed, alpha_pre, bias_pre, alpha_post, bias_post,
                             n, c, post_mult, pre_eps, rms_eps, want_h_pre=True, want_saved=train)
         if train:
@@ -114,7 +116,7 @@ class MHCConnection_FusedNoHres(nn.Module):
         fused into the pre launch when no autograd is needed)."""
         packed = self._phi_pack.get(self.phi_weight, self.n, self.dim) if x_flat.is_cuda else None
         if in_norm is not None:
-            if fusable_norm(in_norm, self.dim, x_flat, self):
+            if fusable_norm(in_norm, self.dim, x_flat):
                 o = _ops.pre_nohres(x_flat, self.phi_weight, packed, self.alpha_pre, self.bias_pre,
                                     self.alpha_post, self.bias_post, self.n, self.dim,
                                     self.post_mult_value, self.pre_eps, self.eps,
