@@ -28,7 +28,16 @@ def load_golden(name: str):
 
 
 def golden_names():
-    return sorted(p.name for p in GOLDEN.glob("*.npz"))
+    """The fixtures that store their inputs (module forwards at small C); the
+    seeded ones of tests/golden/cases.py are listed by `seeded_names`."""
+    return sorted(p.name for p in GOLDEN.glob("*.npz")
+                  if p.name.startswith(("full_", "nohres_", "head_")))
+
+
+def seeded_names(kind=None):
+    """Names of the seeded fixtures (tests/golden/cases.py), optionally of one kind."""
+    from tests.golden import cases
+    return sorted(k for k, c in cases.CASES.items() if kind is None or c["kind"] == kind)
 
 
 def t(a, dtype) -> torch.Tensor:

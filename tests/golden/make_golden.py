@@ -3,11 +3,21 @@
 Why an import: no reference test, fixture or closed form pins the exact bf16
 rounding trajectory of MHCConnection_Fused._forward_ref
 (model/mhc_fused.py:836-864), MHCConnection_FusedNoHres._forward_ref
-(model/mhc_fused_no_hres.py:635-659) or _mhc_head_ref
-(model/mhc_common.py:298-308).  This script runs those reference functions on
-the CPU (their PyTorch branch; no GPU, no Triton launch), in this container
-only, and stores small seeded cases as .npz fixtures (inputs and outputs,
-no reference code).  fp32 cases are stored alongside as a cross-check.
+(model/mhc_fused_no_hres.py:635-659), _mhc_head_ref
+(model/mhc_common.py:298-308), or of the per-phase functions the oracle
+restates one by one: _pre_phase_full_ref / _post_phase_full_ref
+(model/mhc_fused.py:533-568), _sinkhorn_ref (:47-56), _pre_phase_ref /
+_post_phase_ref (model/mhc_fused_no_hres.py:364-394).  Closed forms and
+float64 loops pin their mathematics, not where torch rounds to bf16.  This
+script runs those reference functions on the CPU (their PyTorch branch; no
+GPU, no Triton launch), in this container only, and stores seeded cases as
+.npz fixtures (inputs and outputs, no reference code).
+
+Two formats:
+  * the small module cases below store their inputs and outputs;
+  * the cases of tests/golden/cases.py (function-level vectors and C = 768
+    module rows) store the outputs in their own dtype plus a digest of the
+    inputs, which cases.build_inputs draws again at test time.
 
 The reference checkout is never needed at test time: tests read the .npz
 files.  Re-run with:  python tests/golden/make_golden.py [/root/reference]
@@ -107,5 +117,58 @@ def main(ref_root: str) -> None:
         print(f"wrote {name}.npz  out{tuple(out.shape)}")
 
 
+def main_seeded(ref_root: str) -> None:
+    """The cases of tests/golden/cases.py, through the reference's functions."""
+    sys.path.insert(0, ref_root)
+    sys.path.insert(0, str(OUT_DIR))
+    import cases as K                                           # noqa: E402
+    from model import mhc_fused as RF                           # noqa: E402
+    from model import mhc_fused_no_hres as RN                   # noqa: E402
+
+    torch.set_num_threads(1)
+    for name, c in K.CASES.items():
+        inp = K.build_inputs(name)
+        kind, n = c["kind"], c["n"]
+        outs = {}
+        with torch.no_grad():
+            if kind == "sinkhorn":
+                outs["y"] = RF._sinkhorn_ref(inp["M"], c["iters"], 1e-6)
+            elif kind == "pre_full":
+                r = RF._pre_phase_full_ref(inp["x"], inp["phi_weight"], inp["alpha_pre"],
+                                           inp["bias_pre"], inp["alpha_post"], inp["bias_post"],
+                                           inp["alpha_res"], inp["bias_res"], 2.0, 1e-6, 1e-6,
+                                           n, c["C"])
+                outs.update(zip(("sub_in", "h_pre", "h_post", "h_res_raw", "inv_rms",
+                                 "mixes_raw"), r))
+            elif kind == "post_full":
+                outs["out"] = RF._post_phase_full_ref(inp["x"], inp["h_res"], inp["h_post"],
+                                                      inp["f_out"], n, c["C"])
+            elif kind == "pre_nohres":
+                r = RN._pre_phase_ref(inp["x"], inp["phi_weight"], inp["alpha_pre"],
+                                      inp["bias_pre"], inp["alpha_post"], inp["bias_post"], 2.0,
+                                      1e-6, 1e-6, n, c["C"])
+                outs.update(zip(("sub_in", "h_pre", "h_post", "inv_rms", "mixes_raw"), r))
+            elif kind == "post_nohres":
+                outs["out"] = RN._post_phase_ref(inp["x"], inp["h_post"], inp["f_out"], n,
+                                                 c["C"])
+            elif kind == "full":
+                mod = RF.MHCConnection_Fused(n, c["C"], sinkhorn_iters=c["iters"])
+                mod = mod.to(inp["x"].dtype)
+                for k in ("phi_weight", "alpha_pre", "bias_pre", "alpha_post", "bias_post",
+                          "alpha_res", "bias_res"):
+                    getattr(mod, k).copy_(inp[k])
+                fw = inp["f_weight"]
+                outs["out"] = mod._forward_ref(inp["x"], lambda z: z @ fw.t())
+            else:
+                raise ValueError(kind)
+        rec = {"input_sha256": np.array(K.digest(inp))}
+        rec.update({"out_" + k: K.to_store(v) for k, v in outs.items()})
+        np.savez_compressed(OUT_DIR / f"{name}.npz", **rec)
+        print(f"wrote {name}.npz  " + " ".join(f"{k}{tuple(v.shape)}" for k, v in outs.items()))
+
+
 if __name__ == "__main__":
-    main(sys.argv[1] if len(sys.argv) > 1 else "/root/reference")
+    root = next((a for a in sys.argv[1:] if not a.startswith("--")), "/root/reference")
+    if "--seeded-only" not in sys.argv:
+        main(root)
+    main_seeded(root)

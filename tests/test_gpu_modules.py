@@ -6,7 +6,8 @@ import torch
 import torch.nn as nn
 
 from oracle import mhc_ref as R
-from tests._util import golden_names, load_golden, make_params, maxabs, maxrel, t, tol
+from tests._util import (golden_names, load_golden, make_params, maxabs, maxrel, seeded_names, t,
+                         tol)
 
 pytestmark = pytest.mark.gpu
 
@@ -214,3 +215,30 @@ def test_integration_ctypes_stub(dev, monkeypatch):
     out = ns["mhc_post"](x, h_res, h_post, f, n, C)
     ref = _ops.post(x, o["h_res"], o["h_post"], f.reshape(M, C), n, C)
     assert torch.equal(out.reshape(M, n * C), ref.reshape(M, n * C))
+
+
+@pytest.mark.parametrize("name", [
+    "c1_full_n4_c768_it20_f32", "c1_full_n4_c768_it10_f32",
+    "c2_full_n4_c768_it20_stress_bf16", "c5_full_n8_c768_it20_stress_bf16"])
+def test_module_matches_reference_c768(dev, name):
+    """Reference _forward_ref rows at C = 768 (tests/golden/cases.py): config 1
+    itself (fp32, T = 256) at the 1e-5 bar, and bf16 rows of the config-2
+    (n = 4) and config-5 (n = 8) shapes with stress gates (alphas 0.6 / 0.4 /
+    0.8, random biases, so every gate follows the projection) at the 1e-2 bar.
+    The kernels keep x_norm and the projection in fp32, as the reference's
+    fused kernel does (model/mhc_fused.py:209-229), where _forward_ref rounds
+    x_norm to bf16 (:845): the layer output meets the bar either way."""
+    from tests.golden import cases as K
+    case, inp, ref = K.load(name)
+    assert name in seeded_names("full")
+    dtype = inp["x"].dtype
+    n, C = case["n"], case["C"]
+    p = {k: inp[k] for k in ("phi_weight", "alpha_pre", "bias_pre", "alpha_post", "bias_post",
+                             "alpha_res", "bias_res")}
+    mod = _load_module(MHCConnection_Fused(n, C, sinkhorn_iters=case["iters"]), p, dev, dtype)
+    fw = inp["f_weight"].t().contiguous().to(dev)
+    print(f"c768 module {name}", flush=True)
+    with torch.no_grad():
+        out = mod(inp["x"].to(dev), lambda z: z @ fw)
+    err = maxrel(ref["out"], out)
+    assert err <= tol(dtype), f"{name}: {err:.3e}"

@@ -10,7 +10,7 @@ import pytest
 import torch
 
 from oracle import mhc_ref as R
-from tests._util import make_params, maxabs, maxrel, tol
+from tests._util import make_params, maxabs, maxrel, seeded_names, tol
 
 pytestmark = pytest.mark.gpu
 
@@ -230,3 +230,72 @@ def test_bad_arguments_raise(dev):
         _ops.post(x, None, torch.rand(1, 4, 4, device=dev), torch.randn(1, 4, 64, device=dev), 4, 32)
     with pytest.raises(RuntimeError, match="n must be"):
         _ops.sinkhorn(torch.randn(2, 40, 40, device=dev), 3, 1e-6)
+
+
+# ------------------------------------------------ reference function vectors
+
+def _fixture(name):
+    from tests.golden import cases as K
+    case, inp, ref = K.load(name)
+    return case, {k: v for k, v in inp.items()}, ref
+
+
+@pytest.mark.parametrize("name", seeded_names("pre_full") + seeded_names("pre_nohres"))
+def test_pre_vs_reference_vectors(dev, name):
+    """HIP pre phase (MFMA kernels for bf16) against _pre_phase_full_ref /
+    _pre_phase_ref outputs (model/mhc_fused.py:533-559,
+    model/mhc_fused_no_hres.py:364-386) on the same inputs."""
+    case, inp, ref = _fixture(name)
+    n, C = case["n"], case["C"]
+    d = {k: v.to(dev) for k, v in inp.items()}
+    dtype = inp["x"].dtype
+    full = case["kind"] == "pre_full"
+    mode = H.MODE_FULL if full else H.MODE_NOHRES
+    packed = _ops.PhiPack(mode).get(d["phi_weight"], n, C)
+    print(f"pre vectors {name} mfma={packed is not None}", flush=True)
+    if full:
+        o = _ops.pre_full(d["x"], d["phi_weight"], packed, d["alpha_pre"], d["bias_pre"],
+                          d["alpha_post"], d["bias_post"], d["alpha_res"], d["bias_res"], n, C,
+                          2.0, 1e-6, 1e-6, 0, 0.0, sinkhorn=False, want_h_pre=True,
+                          want_raw=True, want_saved=True)
+    else:
+        o = _ops.pre_nohres(d["x"], d["phi_weight"], packed, d["alpha_pre"], d["bias_pre"],
+                            d["alpha_post"], d["bias_post"], n, C, 2.0, 1e-6, 1e-6,
+                            want_h_pre=True, want_saved=True)
+    ref = {k: v.reshape(o[k].shape) for k, v in ref.items()}
+    bar = tol(dtype)
+    # x_norm and the projection stay fp32 in the kernels (as in the reference's
+    # fused kernel, model/mhc_fused.py:209-229); _pre_phase_full_ref rounds both
+    # to bf16 (:545-546), so the raw projection and h_res_raw carry up to a bf16
+    # step of their largest entry (2**-8 relative).
+    raw_bar = 2e-2 if dtype == torch.bfloat16 else 1e-5
+    assert maxrel(ref["sub_in"], o["sub_in"]) <= bar
+    assert maxrel(ref["h_pre"], o["h_pre"]) <= bar
+    assert maxrel(ref["h_post"], o["h_post"]) <= bar
+    assert maxrel(ref["inv_rms"], o["inv_rms"]) <= 1e-5
+    assert maxrel(ref["mixes_raw"], o["mixes_raw"]) <= raw_bar
+    if full:
+        assert maxrel(ref["h_res_raw"], o["h_res_raw"]) <= raw_bar
+
+
+@pytest.mark.parametrize("name", seeded_names("post_full") + seeded_names("post_nohres"))
+def test_post_vs_reference_vectors(dev, name):
+    """HIP post phase against _post_phase_full_ref / _post_phase_ref outputs
+    (model/mhc_fused.py:562-568, model/mhc_fused_no_hres.py:389-394)."""
+    case, inp, ref = _fixture(name)
+    n, C = case["n"], case["C"]
+    d = {k: v.to(dev) for k, v in inp.items()}
+    out = _ops.post(d["x"], d.get("h_res"), d["h_post"], d["f_out"], n, C)
+    assert maxrel(ref["out"].reshape(out.shape), out) <= tol(inp["x"].dtype)
+
+
+@pytest.mark.parametrize("name", seeded_names("sinkhorn"))
+def test_sinkhorn_vs_reference_vectors(dev, name):
+    """mhc_sinkhorn_fwd against _sinkhorn_ref (model/mhc_fused.py:47-56):
+    entries and row / column sums within 1e-5 in fp32."""
+    case, inp, ref = _fixture(name)
+    y = _ops.sinkhorn(inp["M"].to(dev), case["iters"], 1e-6).cpu()
+    r = ref["y"]
+    assert maxabs(r, y) <= 1e-5
+    for dim in (-1, -2):
+        assert maxabs(r.sum(dim), y.sum(dim)) <= 1e-5

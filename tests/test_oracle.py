@@ -3,16 +3,21 @@
 How each oracle function is pinned:
   mhc_full_forward, mhc_nohres_forward, head (bf16 and fp32)
       -> golden vectors written by the reference's own _forward_ref /
-         _mhc_head_ref (tests/golden/make_golden.py), compared bit-exactly;
+         _mhc_head_ref (tests/golden/make_golden.py), compared bit-exactly,
+         at small C and, for mhc_full_forward, at C = 768 (config 1 itself,
+         and config-2 / config-5 rows with stress gates);
       -> float64 scalar-loop brute force (oracle/brute.py) on tiny inputs.
-  sinkhorn      -> brute force; closed forms (final column sums = s/(s+eps),
-                   non-negativity, circulant fixed point).
+  sinkhorn      -> reference vectors of _sinkhorn_ref (n 2..16, iters 1, 10,
+                   20), bit-exact; brute force; closed forms (final column
+                   sums = s/(s+eps), non-negativity, circulant fixed point).
   pre_full / post_full / pre_nohres / post_nohres
-      -> composition equals the golden-pinned module forward; closed forms
-         (phi = 0 gates, identical streams under a row-stochastic H_res,
-         H_post = 0 leaves the einsum, uniform h_pre gives the stream mean).
+      -> reference vectors of _pre_phase_full_ref / _post_phase_full_ref /
+         _pre_phase_ref / _post_phase_ref in bf16 and fp32, every output
+         bit-exact (C up to 768); closed forms (phi = 0 gates, identical
+         streams under a row-stochastic H_res, H_post = 0 leaves the einsum,
+         uniform h_pre gives the stream mean).
   stream_expand -> definition (every copy equals the input).
-A planted-mistake test shows that a transposed H_res, a dropped eps or a
+Planted-mistake tests show that a transposed H_res, a dropped eps or a
 swapped pre/post segment in the oracle fails these checks.
 """
 from __future__ import annotations
@@ -24,7 +29,8 @@ import torch
 
 from oracle import brute
 from oracle import mhc_ref as R
-from tests._util import golden_names, load_golden, maxrel, t
+from tests._util import golden_names, load_golden, maxrel, seeded_names, t
+from tests.golden import cases as K
 
 DT = {"bf16": torch.bfloat16, "f32": torch.float32}
 
@@ -269,3 +275,103 @@ def test_planted_dropped_eps_fails_brute():
     ref = torch.tensor(brute.sinkhorn(M.tolist(), 5, 1e-2), dtype=torch.float64)
     assert (R.sinkhorn(M, 5, 1e-2) - ref).abs().max() < 1e-14
     assert (_Mutant("drop_eps").sinkhorn(M, 5, 1e-2) - ref).abs().max() > 1e-4
+
+
+# ------------------------------------------- reference vectors (seeded fixtures)
+
+@pytest.fixture
+def one_thread():
+    """torch's CPU fp32 GEMM splits long reductions (K = n*C = 3072) by thread
+    count, so its last bit depends on it; make_golden.py runs the reference at
+    one thread, and these checks run the oracle the same way."""
+    prev = torch.get_num_threads()
+    torch.set_num_threads(1)
+    yield
+    torch.set_num_threads(prev)
+
+
+_FN_OUTS = {"pre_full": ("sub_in", "h_pre", "h_post", "h_res_raw", "inv_rms", "mixes_raw"),
+            "pre_nohres": ("sub_in", "h_pre", "h_post", "inv_rms", "mixes_raw")}
+
+
+def oracle_function_outputs(case, inp, mod=R):
+    """The oracle function a seeded function-level case pins, on its inputs."""
+    kind, n = case["kind"], case["n"]
+    if kind == "sinkhorn":
+        return {"y": mod.sinkhorn(inp["M"], case["iters"], 1e-6)}
+    C = case["C"]
+    if kind == "pre_full":
+        return dict(zip(_FN_OUTS[kind], mod.pre_full(inp["x"], inp, n, C)))
+    if kind == "pre_nohres":
+        return dict(zip(_FN_OUTS[kind], mod.pre_nohres(inp["x"], inp, n, C)))
+    if kind == "post_full":
+        return {"out": mod.post_full(inp["x"], inp["h_res"], inp["h_post"], inp["f_out"], n, C)}
+    if kind == "post_nohres":
+        return {"out": mod.post_nohres(inp["x"], inp["h_post"], inp["f_out"], n, C)}
+    raise ValueError(kind)
+
+
+@pytest.mark.parametrize("name", [k for k in seeded_names() if k.startswith("fn_")])
+def test_oracle_function_matches_reference_vectors(name, one_thread):
+    """Each per-phase oracle function reproduces the reference function's
+    outputs (every output, its dtype and its bits) on the same inputs."""
+    case, inp, ref = K.load(name)
+    got = oracle_function_outputs(case, inp)
+    assert set(got) == set(ref)
+    for k in ref:
+        assert got[k].dtype == ref[k].dtype, k
+        assert torch.equal(got[k], ref[k].view(got[k].shape)), f"{name}:{k} {maxrel(ref[k], got[k]):.3e}"
+
+
+@pytest.mark.parametrize("name", seeded_names("full"))
+def test_oracle_matches_reference_c768_rows(name, one_thread):
+    """mhc_full_forward at C = 768: config 1 itself (fp32, T = 256, alpha 0.01,
+    biases 0 / I, F = Linear ~ N(0, 0.02)) and bf16 rows with stress gates."""
+    case, inp, ref = K.load(name)
+    fw = inp["f_weight"]
+    got = R.mhc_full_forward(inp["x"], inp, lambda z: z @ fw.t(), case["n"], case["C"],
+                             sinkhorn_iters=case["iters"])["out"]
+    assert got.dtype == ref["out"].dtype
+    assert torch.equal(got, ref["out"]), f"{name}: {maxrel(ref['out'], got):.3e}"
+
+
+class _PhaseMutant:
+    """Per-phase oracle functions with one planted mistake (tests only)."""
+
+    def __init__(self, kind):
+        self.kind = kind
+
+    def pre_full(self, x, p, n, C):
+        q = dict(p)
+        if self.kind == "swap_pre_post":
+            w = p["phi_weight"].clone()
+            w[:, :n], w[:, n:2 * n] = p["phi_weight"][:, n:2 * n], p["phi_weight"][:, :n]
+            q["phi_weight"] = w
+        if self.kind == "skip_xnorm_rounding":
+            inv = R._inv_rms(x, 1e-6)
+            mixes = (x.float() * inv) @ p["phi_weight"].float()
+            q["phi_weight"] = p["phi_weight"]
+            out = list(R.pre_full(x, q, n, C))
+            out[5] = mixes
+            return tuple(out)
+        return R.pre_full(x, q, n, C)
+
+    def post_full(self, x, h_res, h_post, f, n, C):
+        if self.kind == "transpose_hres":
+            h_res = h_res.transpose(-1, -2)
+        return R.post_full(x, h_res, h_post, f, n, C)
+
+    def sinkhorn(self, M, iters, eps):
+        return R.sinkhorn(M, iters, 0.0 if self.kind == "drop_eps" else eps)
+
+
+@pytest.mark.parametrize("kind,name", [
+    ("swap_pre_post", "fn_pre_full_n4_c64_stress_f32"),
+    ("skip_xnorm_rounding", "fn_pre_full_n4_c768_stress_bf16"),
+    ("transpose_hres", "fn_post_full_n4_c64_f32"),
+    ("drop_eps", "fn_sinkhorn_n4_it1_f32"),
+])
+def test_planted_mistakes_fail_function_vectors(kind, name, one_thread):
+    case, inp, ref = K.load(name)
+    got = oracle_function_outputs(case, inp, _PhaseMutant(kind))
+    assert any(not torch.equal(got[k], ref[k].view(got[k].shape)) for k in ref)
