@@ -230,9 +230,11 @@ int mhc_expand_norm_fwd(const void* x, int x_dtype, const void* norm_weight, int
 
 /*
  * Batch size (tokens) at or below which the pre-phase entry points run the
- * one-workgroup-per-token kernel instead of the persistent one (bf16, packed
- * phi, n <= 2, C <= 1024; default 512); max_tokens < 0 only queries.  Returns the previous
- * value.  Process-wide setting, not synchronised with calls in flight.
+ * small-batch kernel (one workgroup per group of up to 16 tokens, phi read
+ * from L2) instead of the large-batch ones (bf16, packed phi, n in {1, 2, 4,
+ * 8}, C <= 1024; default 1024); max_tokens < 0 only queries.  Both sides give
+ * bit-identical results.  Returns the previous value.  Process-wide setting,
+ * not synchronised with calls in flight.
  * No reference counterpart (the reference launches one program per token at
  * every size, model/mhc_fused.py:615-641).
  */

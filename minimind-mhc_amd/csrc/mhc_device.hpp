@@ -194,35 +194,45 @@ __device__ __forceinline__ float dot2_bf16(uint32_t a, uint32_t b, float c) {
                                          __builtin_bit_cast(bf16x2_t, b), c, false);
 }
 
+// One packed column pair: x[i] holds columns (c, c + 1) of stream i.
+template <int N>
+__device__ __forceinline__ uint32_t preagg_pair(const uint32_t (&x)[N], const uint32_t (&hlo)[N],
+                                                const uint32_t (&hhi)[N]) {
+  constexpr uint32_t kOnes = 0x3F803F80u;  // bf16 (1.0, 1.0)
+  float plo[N];
+  float phi_[N];
+#pragma unroll
+  for (int i = 0; i < N; ++i) {
+    plo[i] = dot2_bf16(x[i], hlo[i], 0.f);
+    phi_[i] = dot2_bf16(x[i], hhi[i], 0.f);
+  }
+  float slo;
+  float shi;
+  if constexpr (N == 1) {
+    slo = plo[0];
+    shi = phi_[0];
+  } else {
+    slo = 0.f;
+    shi = 0.f;
+#pragma unroll
+    for (int i = 0; i < N; i += 2) {
+      slo = dot2_bf16(pack_bf16x2(plo[i], plo[i + 1]), kOnes, slo);
+      shi = dot2_bf16(pack_bf16x2(phi_[i], phi_[i + 1]), kOnes, shi);
+    }
+  }
+  return pack_bf16x2(slo, shi);
+}
+
 template <int N>
 __device__ __forceinline__ U32x4 preagg_chunk(const U32x4 (&x)[N], const uint32_t (&hlo)[N],
                                              const uint32_t (&hhi)[N]) {
-  constexpr uint32_t kOnes = 0x3F803F80u;  // bf16 (1.0, 1.0)
   U32x4 out;
 #pragma unroll
   for (int j = 0; j < 4; ++j) {
-    float plo[N];
-    float phi_[N];
+    uint32_t xj[N];
 #pragma unroll
-    for (int i = 0; i < N; ++i) {
-      plo[i] = dot2_bf16(x[i].v[j], hlo[i], 0.f);
-      phi_[i] = dot2_bf16(x[i].v[j], hhi[i], 0.f);
-    }
-    float slo;
-    float shi;
-    if constexpr (N == 1) {
-      slo = plo[0];
-      shi = phi_[0];
-    } else {
-      slo = 0.f;
-      shi = 0.f;
-#pragma unroll
-      for (int i = 0; i < N; i += 2) {
-        slo = dot2_bf16(pack_bf16x2(plo[i], plo[i + 1]), kOnes, slo);
-        shi = dot2_bf16(pack_bf16x2(phi_[i], phi_[i + 1]), kOnes, shi);
-      }
-    }
-    out.v[j] = pack_bf16x2(slo, shi);
+    for (int i = 0; i < N; ++i) xj[i] = x[i].v[j];
+    out.v[j] = preagg_pair<N>(xj, hlo, hhi);
   }
   return out;
 }

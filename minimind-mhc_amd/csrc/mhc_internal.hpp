@@ -131,11 +131,8 @@ struct WeightsArgs {
 // Launchers: return hipSuccess or the launch error.
 hipError_t launch_pre_mfma(const PreArgs& a, hipStream_t s);   // requires mfma_supported()
 hipError_t launch_pre_generic(const PreArgs& a, hipStream_t s);
-// One workgroup per token (small M, n <= 2, bf16, packed phi): see mhc_pre_token.hip.
-bool pre_token_supported(const PreArgs& a);
-hipError_t launch_pre_token(const PreArgs& a, hipStream_t s);
-// Tokens at or below which launch_pre_mfma picks the one-workgroup-per-token
-// kernel (process-wide setting).
+// Tokens at or below which launch_pre_mfma picks the small-batch group kernel
+// (one workgroup per group of up to 16 tokens; process-wide setting).
 int64_t pre_token_max_m();
 void set_pre_token_max_m(int64_t m);
 // Whether the persistent pre kernel stages x tiles through LDS from row-

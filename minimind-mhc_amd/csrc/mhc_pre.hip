@@ -7,7 +7,7 @@
 // are fp32; the gates and the pre-aggregate round where the reference's torch
 // ops round (model/mhc_fused.py:843-859, model/mhc_fused_no_hres.py:364-386,
 // model/mhc_common.py:298-308).
-#include "mhc_pre_kstream.hpp"
+#include "mhc_pre_group.hpp"
 
 namespace mhc {
 
@@ -64,6 +64,23 @@ hipError_t launch_phi_pack(const void* phi, int phi_dtype, void* packed, int n, 
   return hipGetLastError();
 }
 
+// ------------------------------------------------------ process-wide settings
+
+namespace {
+// Batch size up to which the small-batch group kernel runs.  Measured on
+// MI355X at C = 768 (pre launch, four rotating input sets): it is ahead of the
+// large-batch kernels up to 1024 tokens for n = 2, 4 and 8 (n = 4: 9.7 vs
+// 11.0 us at 1024, 7.2 vs 9.7 us at 64; n = 8: 24.9 vs 47.3 us at 1024) and
+// level with them at 2048.
+int64_t g_token_max_m = 1024;
+bool g_row_staging = true;
+}  // namespace
+
+int64_t pre_token_max_m() { return g_token_max_m; }
+void set_pre_token_max_m(int64_t m) { g_token_max_m = m; }
+bool pre_row_staging() { return g_row_staging; }
+void set_pre_row_staging(bool on) { g_row_staging = on; }
+
 // Compute units of the current device (cached; one persistent workgroup each).
 static int device_cus() {
   static int cache[64] = {0};
@@ -78,12 +95,20 @@ static int device_cus() {
 }
 
 hipError_t launch_pre_mfma(const PreArgs& a, hipStream_t s) {
-  // Decode-size batches: one workgroup per token.
-  if (a.M <= pre_token_max_m() && pre_token_supported(a)) return launch_pre_token(a, s);
+  const int cus = device_cus();
+  // Decode-size batches: one workgroup per group of up to 16 tokens.
+  if (a.M <= pre_token_max_m() && a.phi_packed) {
+    switch (a.n) {
+      case 1: return launch_pre_group_n1(a, cus, s);
+      case 2: return launch_pre_group_n2(a, cus, s);
+      case 4: return launch_pre_group_n4(a, cus, s);
+      case 8: return launch_pre_group_n8(a, cus, s);
+      default: break;
+    }
+  }
   // n <= 4: persistent workgroups with the x tile double-buffered in registers.
   if (a.n <= 4) {
     const int kb = persist_kb_needed(a.C);
-    const int cus = device_cus();
     switch (a.n) {
       case 1: return launch_pre_persist_n1(a, kb, cus, s);
       case 2: return launch_pre_persist_n2(a, kb, cus, s);

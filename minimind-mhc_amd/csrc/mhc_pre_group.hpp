@@ -1,0 +1,391 @@
+// Pre phase for small batches on MFMA: one workgroup per group of G tokens
+// (G a power of two, at most 16), phi streamed from L2.  bf16 streams, packed
+// phi, n in {1, 2, 4, 8}, C <= 1024, C % 8 == 0.
+//
+// At decode sizes the large-batch kernels leave most of the chip idle: the
+// persistent kernel (n <= 4) puts one 16-token tile on each of a handful of
+// CUs, each of which first pulls the whole of phi into registers, and the
+// K-streamed kernel (n = 8) one 32-token tile per workgroup.  Here M / G
+// workgroups each run a single MFMA tile with only G of its 16 rows live:
+//   * wave w walks the 32-column blocks the same wave of the large-batch
+//     kernel walks, in the same order (pre_persist_kernel's for n <= 4;
+//     pre_kstream_kernel's, with its per-tile rotation, for n = 8).  The MFMA
+//     accumulation chains, the per-wave sums of squares and the cross-wave
+//     sums are then the large-batch kernel's, so every output is bit for bit
+//     what that kernel writes and the results do not depend on the batch size;
+//   * each block is one A-operand load (lanes of rows past the group read
+//     nothing) and NT B-operand loads of the packed phi image (1 KiB per wave
+//     instruction, padding columns skipped), with P blocks in flight per wave;
+//   * the A operands of the live rows go to LDS as they are consumed, so the
+//     pre-aggregate runs one column pair per lane over the whole workgroup
+//     instead of on the few lanes that hold a live row;
+//   * gates take one (token, feature) per thread; the Sinkhorn runs on the
+//     last waves with the large-batch kernel's lane layout (sinkhorn_lane<N>
+//     for n <= 4, the half-row sk8_* layout for n = 8), before their share of
+//     the pre-aggregate;
+//   * the RMSNorm epilogue sums its squares in the large-batch kernel's order.
+// Rounding points as pre_persist_kernel.
+//
+// Reference semantics: model/mhc_fused.py:163-268, :533-559, :47-56;
+// model/mhc_fused_no_hres.py:48-145; model/mhc_common.py:128-195.
+#pragma once
+
+#include "mhc_pre_kstream.hpp"
+
+namespace mhc {
+
+constexpr int kGrpWaves = 8;
+constexpr int kKsTileTokens = 32;  // tokens of one pre_kstream_kernel tile (its rotation key)
+
+template <int N, int MODE, int KB>
+struct GroupPlan {
+  using S = PreShape<N, MODE>;
+  static constexpr int FD = S::FD;
+  static constexpr int NT = S::NT;
+  static constexpr int NN = N * N;
+  static constexpr int LAST_COLS = FD - 16 * (NT - 1);  // real columns of the last tile
+  static constexpr int NB = N * KB;                     // 32-column blocks per wave, at most
+  // Blocks in flight per wave: one x and NT phi registers (4 VGPRs each) a
+  // block; 48 such registers, 32 for the wide n = 8 projection (whose
+  // accumulators and Sinkhorn need the rest), 24 there at C = 1024.
+  static constexpr int PMAX = (NT >= 4 ? (KB >= 4 ? 24 : 32) : 48) / (1 + NT);
+  static constexpr int P = NB < PMAX ? NB : PMAX;
+  static constexpr bool KS_ORDER = N == 8;
+  static constexpr int CMAX = 256 * KB;
+  static constexpr int ROW = N * CMAX + 8;  // LDS x row in bf16 elements, 16 bytes of pad
+  static constexpr int GFIT = 98304 / (2 * ROW);
+  static constexpr int GMAX = GFIT >= 16 ? 16 : GFIT >= 8 ? 8 : GFIT >= 4 ? 4 : GFIT >= 2 ? 2 : 1;
+  static constexpr int SKL = N == 8 ? 16 : NN;  // Sinkhorn lanes per token
+  static constexpr int SK_TOK = 64 / SKL;       // tokens per Sinkhorn wave
+};
+
+template <int N, int MODE, int KB, bool NORM>
+struct GroupShared {
+  using P = GroupPlan<N, MODE, KB>;
+  float prm[GateParams<N>::kCount];
+  float acc[kGrpWaves][16][P::FD];  // per-wave partial projections of the live rows
+  float ss[kGrpWaves][16];          // per-wave partial sums of squares
+  float hpre[16][N];
+  float hres[16][MODE == kFull ? P::NN : 1];
+  alignas(16) uint16_t xs[P::GMAX][P::ROW];  // the group's x rows
+  // RMSNorm epilogue: rounded pre-aggregate, gain, square-sum partials, scales.
+  uint32_t ys[NORM ? P::GMAX : 1][NORM ? P::CMAX / 2 : 1];
+  float gain[NORM ? P::CMAX : 1];
+  float q2[NORM ? P::GMAX : 1][32];
+  float scale[16];
+};
+
+template <int N, int MODE, int KB, bool NORM>
+__global__ __launch_bounds__(kGrpWaves * 64) void pre_group_kernel(PreArgs a, int G) {
+  using P = GroupPlan<N, MODE, KB>;
+  using GP = GateParams<N>;
+  constexpr int FD = P::FD;
+  constexpr int NT = P::NT;
+  constexpr int NN = P::NN;
+  constexpr int T = kGrpWaves * 64;
+  static_assert(sizeof(GroupShared<N, MODE, KB, NORM>) <= kLdsBytes, "LDS budget");
+  static_assert(P::CMAX <= 2 * T, "two gain columns per thread");
+  __shared__ GroupShared<N, MODE, KB, NORM> sh;
+
+  const int tid = threadIdx.x;
+  const int lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int r = lane & 15;
+  const int g = lane >> 4;
+  const int C = a.C;
+  const int NC = N * C;
+  const int NCB = (C + kCBlock - 1) / kCBlock;
+  const int NCH = N * NCB;                              // 32-column blocks of a row
+  const int NJ = (NCH + kGrpWaves - 1) / kGrpWaves;     // blocks per wave, kstream order
+  const int64_t t0 = wave_uniform((int64_t)blockIdx.x * G);
+  const int valid = (int)(a.M - t0 < G ? a.M - t0 : G);
+  // pre_kstream_kernel rotates each tile's block order by (tile % NJ).
+  const int rot = P::KS_ORDER ? (int)((t0 / kKsTileTokens) % NJ) : 0;
+
+  const RawParam rp = load_gate_param<N, MODE>(a, tid);
+  float gain[2] = {0.f, 0.f};  // norm gain of columns tid and tid + T (branch-free loads)
+  if constexpr (NORM) {
+#pragma unroll
+    for (int h = 0; h < 2; ++h) {
+      const int c = tid + h * T;
+      const float v = ld_any(a.norm_w, c < C ? c : 0, a.norm_dtype);
+      gain[h] = c < C ? v : 0.f;
+    }
+  }
+
+  // ---- projection: MFMA over this wave's blocks, P in flight ---------------
+  const auto rx = make_rsrc(static_cast<const uint16_t*>(a.x) + t0 * NC, (uint32_t)valid * NC * 2u);
+  const auto rw = make_rsrc(a.phi_packed, (uint32_t)(NCH * NT) * 1024u);
+  const uint32_t xrow = (uint32_t)(r * NC) * 2u + (uint32_t)g * 16u;
+  // Block b of this wave: stream i, column block cb; false past the row.
+  auto block_of = [&](int b, int& i, int& cb) -> bool {
+    if constexpr (P::KS_ORDER) {
+      const int jr = b < NJ ? (b + rot < NJ ? b + rot : b + rot - NJ) : b;
+      const int k = wave + kGrpWaves * jr;
+      const bool live = b < NJ && k < NCH;
+      i = live ? k / NCB : 0;
+      cb = live ? k - i * NCB : 0;
+      return live;
+    } else {
+      i = b % N;
+      cb = wave + kGrpWaves * (b / N);
+      return cb < NCB;
+    }
+  };
+  U32x4 xq[P::P];
+  U32x4 wq[P::P][NT];
+  auto issue = [&](int b) {
+    int i, cb;
+    const bool live = block_of(b, i, cb);
+    const int c0 = cb * kCBlock;
+    const bool xl = live && c0 + g * 8 < C;
+    xq[b % P::P] = buf_load16_nt(rx, xl ? xrow + (uint32_t)(i * C + c0) * 2u : kBufOob, 0);
+#pragma unroll
+    for (int nt = 0; nt < NT; ++nt) {
+      const bool pad = nt == NT - 1 && r >= P::LAST_COLS;
+      wq[b % P::P][nt] = buf_load16(
+          rw, live && !pad ? (uint32_t)(((i * NCB + cb) * NT + nt) * 64 + lane) * 16u : kBufOob);
+    }
+  };
+#pragma unroll
+  for (int b = 0; b < P::P; ++b) issue(b);
+
+  f32x4_t acc[NT];
+#pragma unroll
+  for (int nt = 0; nt < NT; ++nt) acc[nt] = f32x4_t{0.f, 0.f, 0.f, 0.f};
+  float ss = 0.f;
+#pragma unroll
+  for (int b = 0; b < P::NB; ++b) {
+    const U32x4 v = xq[b % P::P];
+#pragma unroll
+    for (int j = 0; j < 4; ++j) ss = dot2_bf16(v.v[j], v.v[j], ss);
+    const bf16x8_t av = __builtin_bit_cast(bf16x8_t, v);
+#pragma unroll
+    for (int nt = 0; nt < NT; ++nt)
+      acc[nt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(av, __builtin_bit_cast(bf16x8_t, wq[b % P::P][nt]),
+                                                         acc[nt], 0, 0, 0);
+    int i, cb;
+    const bool live = block_of(b, i, cb);
+    const int c0 = cb * kCBlock;
+    if (live && r < valid && c0 + g * 8 < C)
+      *reinterpret_cast<U32x4*>(&sh.xs[r][i * C + c0 + 8 * g]) = v;
+    if (b + P::P < P::NB) issue(b + P::P);
+  }
+  ss += __shfl_xor(ss, 16, 64);
+  ss += __shfl_xor(ss, 32, 64);
+  // MFMA 16x16 result layout: lane l holds D[4*(l/16) + j][l % 16], j = 0..3.
+#pragma unroll
+  for (int nt = 0; nt < NT; ++nt)
+    if (nt * 16 + r < FD)
+#pragma unroll
+      for (int j = 0; j < 4; ++j)
+        if (4 * g + j < G) sh.acc[wave][4 * g + j][nt * 16 + r] = acc[nt][j];
+  if (g == 0 && r < G) sh.ss[wave][r] = ss;
+  if (tid < GP::kCount) sh.prm[tid] = convert_param(rp, a.param_dtype);
+  if constexpr (NORM) {
+#pragma unroll
+    for (int h = 0; h < 2; ++h)
+      if (tid + h * T < P::CMAX) sh.gain[tid + h * T] = gain[h];
+  }
+  __syncthreads();  // partials, x rows and parameters visible
+
+  // ---- inv_rms and gates: one (token, feature) per thread -------------------
+  const float nc = (float)NC;
+  for (int idx = tid; idx < G * FD; idx += T) {
+    const int tt = idx / FD;
+    const int f = idx - tt * FD;
+    float sq = 0.f;
+#pragma unroll
+    for (int w = 0; w < kGrpWaves; ++w) sq += sh.ss[w][tt];
+    const float inv = 1.0f / sqrtf(sq / nc + a.rms_eps);
+    float sum = 0.f;
+#pragma unroll
+    for (int w = 0; w < kGrpWaves; ++w) sum += sh.acc[w][tt][f];
+    const float m = sum * inv;
+    const int64_t tk = t0 + tt;
+    const bool ok = tt < valid;
+    if (ok && a.mixes_raw) a.mixes_raw[tk * FD + f] = m;
+    if (f < N) {
+      const float h = gate_pre(m, sh.prm[0], sh.prm[GP::kBiasPre + f], a.pre_eps, kBF16);
+      sh.hpre[tt][f] = h;
+      if (ok && a.h_pre) st_any(a.h_pre, tk * N + f, kBF16, h);
+      if (ok && f == 0 && a.inv_rms) a.inv_rms[tk] = inv;
+    } else if (f < 2 * N) {
+      if (ok)
+        st_any(a.h_post, tk * N + (f - N), kBF16,
+               gate_post(m, sh.prm[1], sh.prm[GP::kBiasPost + f - N], a.post_mult, kBF16));
+    } else if constexpr (MODE == kFull) {
+      const int e = f - 2 * N;
+      const float h = gate_res(m, sh.prm[2], sh.prm[GP::kBiasRes + e], kBF16);
+      sh.hres[tt][e] = h;
+      if (ok && a.h_res_raw) st_any(a.h_res_raw, tk * NN + e, kBF16, h);
+    }
+  }
+  __syncthreads();  // h_pre and the h_res logits visible
+
+  // ---- Sinkhorn on the last waves, then the pre-aggregate -------------------
+  if constexpr (MODE == kFull) {
+    const int sk_waves = (G + P::SK_TOK - 1) / P::SK_TOK;
+    const int sw = kGrpWaves - 1 - wave;  // uniform
+    if (a.h_res && sw < sk_waves) {
+      const int tt = sw * P::SK_TOK + lane / P::SKL;
+      const int ts = tt < G ? tt : 0;
+      const bool ok = tt < valid;
+      if constexpr (N == 8) {
+        const int jl = lane & 15;
+        const int e0 = (jl & 7) * N + 4 * (jl >> 3);  // row (jl & 7), columns 4 (jl >> 3) ..
+        float v[4];
+#pragma unroll
+        for (int q = 0; q < 4; ++q) v[q] = sh.hres[ts][e0 + q];
+        sk8_start(v, a.sk_eps);
+        for (int it = 1; it < a.sk_iters; ++it) sk8_iter(v, a.sk_eps);
+        if (ok) {
+#pragma unroll
+          for (int q = 0; q < 4; ++q) st_any(a.h_res, (t0 + tt) * NN + e0 + q, kBF16, v[q]);
+        }
+      } else {
+        const int e = lane % NN;
+        const float v = sinkhorn_lane<N>(sh.hres[ts][e], a.sk_iters, a.sk_eps);
+        if (ok) st_any(a.h_res, (t0 + tt) * NN + e, kBF16, v);
+      }
+    }
+  }
+
+  const int C2 = C / 2;
+  const int items = G * C2;
+  const auto rsub = make_rsrc(static_cast<uint16_t*>(a.sub_in) + t0 * C, (uint32_t)valid * C * 2u);
+  for (int idx = tid; idx < items; idx += T) {
+    const int tt = idx / C2;
+    const int d = idx - tt * C2;
+    uint32_t xd[N];
+    uint32_t hlo[N];
+    uint32_t hhi[N];
+#pragma unroll
+    for (int i = 0; i < N; ++i) {
+      xd[i] = *reinterpret_cast<const uint32_t*>(&sh.xs[tt][i * C + 2 * d]);
+      hlo[i] = pack_lo(sh.hpre[tt][i]);
+      hhi[i] = pack_hi(sh.hpre[tt][i]);
+    }
+    const uint32_t y = preagg_pair<N>(xd, hlo, hhi);
+    if constexpr (NORM) {
+      sh.ys[tt][d] = y;
+    } else {
+      __builtin_amdgcn_raw_buffer_store_b32(y, rsub, tt < valid ? (tt * C + 2 * d) * 2 : (int)kBufOob,
+                                            0, kNt);
+    }
+  }
+
+  // ---- RMSNorm over C: squares summed in the large-batch kernel's order ------
+  if constexpr (NORM) {
+    __syncthreads();  // the rounded pre-aggregate complete
+    if constexpr (!P::KS_ORDER) {
+      // pre_persist_kernel: lane (g, r) of wave w chains the chunks at columns
+      // (w + 8q) * 32 + 8g over q; then (g0 + g1) + (g2 + g3), then over w.
+      for (int idx = tid; idx < G * 32; idx += T) {
+        const int tt = idx >> 5;
+        const int w = (idx >> 2) & 7;
+        const int gg = idx & 3;
+        float q = 0.f;
+#pragma unroll
+        for (int qb = 0; qb < KB; ++qb) {
+          const int c0 = (w + kGrpWaves * qb) * kCBlock + 8 * gg;
+          if (c0 < C) {
+#pragma unroll
+            for (int j = 0; j < 4; ++j) {
+              const uint32_t y = sh.ys[tt][c0 / 2 + j];
+              q = dot2_bf16(y, y, q);
+            }
+          }
+        }
+        sh.q2[tt][idx & 31] = q;
+      }
+      __syncthreads();
+      if (tid < G) {
+        float t = 0.f;
+#pragma unroll
+        for (int w = 0; w < kGrpWaves; ++w)
+          t += (sh.q2[tid][4 * w] + sh.q2[tid][4 * w + 1]) + (sh.q2[tid][4 * w + 2] + sh.q2[tid][4 * w + 3]);
+        sh.scale[tid] = 1.0f / sqrtf(t / (float)C + a.norm_eps);
+      }
+    } else {
+      // pre_kstream_kernel: 16 lanes per token chain the chunks jl, jl + 16, ..,
+      // then an 8-lane butterfly and the row mirror.
+      const int tt = wave * 4 + (lane >> 4);
+      const int ts = tt < G ? tt : 0;
+      const int jl = lane & 15;
+      float q = 0.f;
+      for (int ch = jl; ch < C / 8; ch += 16) {
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+          const uint32_t y = sh.ys[ts][4 * ch + j];
+          q = dot2_bf16(y, y, q);
+        }
+      }
+      q = row_reduce<8, OpAdd>(q);
+      q = q + dpp_f<kDppRowMirror>(q);
+      if (jl == 0 && tt < G) sh.scale[tt] = 1.0f / sqrtf(q / (float)C + a.norm_eps);
+    }
+    __syncthreads();  // token scales visible
+    for (int idx = tid; idx < items; idx += T) {
+      const int tt = idx / C2;
+      const int d = idx - tt * C2;
+      const uint32_t y = sh.ys[tt][d];
+      const float sc = sh.scale[tt];
+      const uint32_t o = pack_bf16x2(bf16lo(y) * sc * sh.gain[2 * d], bf16hi(y) * sc * sh.gain[2 * d + 1]);
+      __builtin_amdgcn_raw_buffer_store_b32(o, rsub, tt < valid ? (tt * C + 2 * d) * 2 : (int)kBufOob,
+                                            0, kNt);
+    }
+  }
+}
+
+// Tokens per workgroup: enough workgroups for one per CU, as a power of two
+// no larger than the LDS allows.
+template <int N, int MODE, int KB>
+int group_tokens(int64_t M, int num_cus) {
+  int G = 1;
+  while (G < GroupPlan<N, MODE, KB>::GMAX && (int64_t)G * num_cus < M) G *= 2;
+  return G;
+}
+
+template <int N, int MODE, int KB>
+hipError_t launch_pre_group_inst(const PreArgs& a, int num_cus, hipStream_t s) {
+  const int G = group_tokens<N, MODE, KB>(a.M, num_cus);
+  const int64_t grid = (a.M + G - 1) / G;
+  if (a.norm_w)
+    hipLaunchKernelGGL((pre_group_kernel<N, MODE, KB, true>), dim3((unsigned)grid),
+                       dim3(kGrpWaves * 64), 0, s, a, G);
+  else
+    hipLaunchKernelGGL((pre_group_kernel<N, MODE, KB, false>), dim3((unsigned)grid),
+                       dim3(kGrpWaves * 64), 0, s, a, G);
+  return hipGetLastError();
+}
+
+template <int N, int MODE, int... KBS>
+hipError_t dispatch_group_kb(const PreArgs& a, int kb, int num_cus, hipStream_t s) {
+  hipError_t r = hipErrorInvalidValue;
+  bool done = false;
+  ((!done && KBS >= kb ? (r = launch_pre_group_inst<N, MODE, KBS>(a, num_cus, s), done = true) : false),
+   ...);
+  return r;
+}
+
+template <int N>
+hipError_t dispatch_group_mode(const PreArgs& a, int num_cus, hipStream_t s) {
+  const int kb = persist_kb_needed(a.C);
+  switch (a.mode) {
+    case kFull: return dispatch_group_kb<N, kFull, 1, 2, 3, 4>(a, kb, num_cus, s);
+    case kNoHres: return dispatch_group_kb<N, kNoHres, 1, 2, 3, 4>(a, kb, num_cus, s);
+    case kHead:
+      if constexpr (N > 1) return dispatch_group_kb<N, kHead, 1, 2, 3, 4>(a, kb, num_cus, s);
+      return hipErrorInvalidValue;
+    default: return hipErrorInvalidValue;
+  }
+}
+
+// Per-n entry points (mhc_pre_group_n*.hip).
+hipError_t launch_pre_group_n1(const PreArgs& a, int num_cus, hipStream_t s);
+hipError_t launch_pre_group_n2(const PreArgs& a, int num_cus, hipStream_t s);
+hipError_t launch_pre_group_n4(const PreArgs& a, int num_cus, hipStream_t s);
+hipError_t launch_pre_group_n8(const PreArgs& a, int num_cus, hipStream_t s);
+
+}  // namespace mhc

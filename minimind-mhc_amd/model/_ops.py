@@ -305,8 +305,8 @@ def expand_norm(x: torch.Tensor, weight: torch.Tensor, eps: float, n: int) -> to
 
 def pre_token_threshold(max_tokens: int = -1) -> int:
     """Set (max_tokens >= 0) or query the batch size at or below which the
-    pre-phase launches use the one-workgroup-per-token kernel; returns the
-    previous value."""
+    pre-phase launches use the small-batch group kernel (bit-identical to the
+    large-batch kernels); returns the previous value."""
     return int(H.load().mhc_pre_token_threshold(int(max_tokens)))
 
 
