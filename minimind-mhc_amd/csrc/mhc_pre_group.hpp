@@ -45,16 +45,20 @@ struct GroupPlan {
   static constexpr int NN = N * N;
   static constexpr int LAST_COLS = FD - 16 * (NT - 1);  // real columns of the last tile
   static constexpr int NB = N * KB;                     // 32-column blocks per wave, at most
-  // Blocks in flight per wave: one x and NT phi registers (4 VGPRs each) a
-  // block; 48 such registers, 32 for the wide n = 8 projection (whose
-  // accumulators and Sinkhorn need the rest), 24 there at C = 1024.
-  static constexpr int PMAX = (NT >= 4 ? (KB >= 4 ? 24 : 32) : 48) / (1 + NT);
+  // phi blocks in flight per wave: NT registers of 4 VGPRs a block, at most
+  // 40 such registers (28 for the wide n = 8 projection at C > 512, whose
+  // accumulators and Sinkhorn need the rest).
+  static constexpr int PMAX = (NT >= 4 && KB >= 3 ? 28 : 40) / NT;
   static constexpr int P = NB < PMAX ? NB : PMAX;
   static constexpr bool KS_ORDER = N == 8;
   static constexpr int CMAX = 256 * KB;
   static constexpr int ROW = N * CMAX + 8;  // LDS x row in bf16 elements, 16 bytes of pad
   static constexpr int GFIT = 98304 / (2 * ROW);
-  static constexpr int GMAX = GFIT >= 16 ? 16 : GFIT >= 8 ? 8 : GFIT >= 4 ? 4 : GFIT >= 2 ? 2 : 1;
+  static constexpr int GLDS = GFIT >= 16 ? 16 : GFIT >= 8 ? 8 : GFIT >= 4 ? 4 : GFIT >= 2 ? 2 : 1;
+  // A group's h_pre fits one wave, one (token, stream) per lane.
+  static constexpr int GMAX = GLDS * N <= 64 ? GLDS : 64 / N;
+  // 16-byte x chunks per lane for the group's rows (row-contiguous loads).
+  static constexpr int XW = (GMAX * N * CMAX / 8 + kGrpWaves * 64 - 1) / (kGrpWaves * 64);
   static constexpr int SKL = N == 8 ? 16 : NN;  // Sinkhorn lanes per token
   static constexpr int SK_TOK = 64 / SKL;       // tokens per Sinkhorn wave
 };
@@ -63,11 +67,11 @@ template <int N, int MODE, int KB, bool NORM>
 struct GroupShared {
   using P = GroupPlan<N, MODE, KB>;
   float prm[GateParams<N>::kCount];
-  float acc[kGrpWaves][16][P::FD];  // per-wave partial projections of the live rows
-  float ss[kGrpWaves][16];          // per-wave partial sums of squares
-  float hpre[16][N];
-  float hres[16][MODE == kFull ? P::NN : 1];
-  alignas(16) uint16_t xs[P::GMAX][P::ROW];  // the group's x rows
+  alignas(16) float acc[kGrpWaves][16][P::FD];  // per-wave partial projections of the live rows
+  float ss[kGrpWaves][16];                      // per-wave partial sums of squares
+  U32x4 zero;                                   // A operand of rows past the group
+  float hw[kGrpWaves][64];                      // each wave's copy of the group's h_pre
+  alignas(16) uint16_t xs[P::GMAX][P::ROW];     // the group's x rows
   // RMSNorm epilogue: rounded pre-aggregate, gain, square-sum partials, scales.
   uint32_t ys[NORM ? P::GMAX : 1][NORM ? P::CMAX / 2 : 1];
   float gain[NORM ? P::CMAX : 1];
@@ -113,10 +117,21 @@ __global__ __launch_bounds__(kGrpWaves * 64) void pre_group_kernel(PreArgs a, in
     }
   }
 
-  // ---- projection: MFMA over this wave's blocks, P in flight ---------------
+  // ---- x rows: row-contiguous loads (1 KiB per wave instruction), first ----
+  // 16-byte chunk j of the group's rows (they are contiguous in memory) is
+  // lane j % 64 of instruction j / 64; instruction (u, wave) = u * 8 + wave.
+  const int NC8 = NC / 8;
+  const int nchunk = G * NC8;
   const auto rx = make_rsrc(static_cast<const uint16_t*>(a.x) + t0 * NC, (uint32_t)valid * NC * 2u);
+  U32x4 xl[P::XW];
+#pragma unroll
+  for (int u = 0; u < P::XW; ++u) {
+    const int j = (u * kGrpWaves + wave) * 64 + lane;
+    xl[u] = buf_load16_nt(rx, j < nchunk ? (uint32_t)j * 16u : kBufOob, 0);
+  }
+
+  // ---- phi blocks, P in flight per wave ---------------------------------------
   const auto rw = make_rsrc(a.phi_packed, (uint32_t)(NCH * NT) * 1024u);
-  const uint32_t xrow = (uint32_t)(r * NC) * 2u + (uint32_t)g * 16u;
   // Block b of this wave: stream i, column block cb; false past the row.
   auto block_of = [&](int b, int& i, int& cb) -> bool {
     if constexpr (P::KS_ORDER) {
@@ -132,14 +147,10 @@ __global__ __launch_bounds__(kGrpWaves * 64) void pre_group_kernel(PreArgs a, in
       return cb < NCB;
     }
   };
-  U32x4 xq[P::P];
   U32x4 wq[P::P][NT];
   auto issue = [&](int b) {
     int i, cb;
     const bool live = block_of(b, i, cb);
-    const int c0 = cb * kCBlock;
-    const bool xl = live && c0 + g * 8 < C;
-    xq[b % P::P] = buf_load16_nt(rx, xl ? xrow + (uint32_t)(i * C + c0) * 2u : kBufOob, 0);
 #pragma unroll
     for (int nt = 0; nt < NT; ++nt) {
       const bool pad = nt == NT - 1 && r >= P::LAST_COLS;
@@ -150,13 +161,40 @@ __global__ __launch_bounds__(kGrpWaves * 64) void pre_group_kernel(PreArgs a, in
 #pragma unroll
   for (int b = 0; b < P::P; ++b) issue(b);
 
+  // x rows into LDS (waits for the x loads only: they were issued first).
+#pragma unroll
+  for (int u = 0; u < P::XW; ++u) {
+    const int j = (u * kGrpWaves + wave) * 64 + lane;
+    if (j < nchunk) {
+      const int t = j / NC8;
+      *reinterpret_cast<U32x4*>(&sh.xs[t][(j - t * NC8) * 8]) = xl[u];
+    }
+  }
+  if (tid == 0) sh.zero = U32x4{{0u, 0u, 0u, 0u}};
+  if (tid < GP::kCount) sh.prm[tid] = convert_param(rp, a.param_dtype);
+  if constexpr (NORM) {
+#pragma unroll
+    for (int h = 0; h < 2; ++h)
+      if (tid + h * T < P::CMAX) sh.gain[tid + h * T] = gain[h];
+  }
+  __syncthreads();  // x rows, zero block and parameters visible
+
+  // ---- projection: MFMA over this wave's blocks --------------------------------
   f32x4_t acc[NT];
 #pragma unroll
   for (int nt = 0; nt < NT; ++nt) acc[nt] = f32x4_t{0.f, 0.f, 0.f, 0.f};
   float ss = 0.f;
 #pragma unroll
   for (int b = 0; b < P::NB; ++b) {
-    const U32x4 v = xq[b % P::P];
+    int i, cb;
+    const bool live = block_of(b, i, cb);
+    const int c0 = cb * kCBlock;
+    // Lane (g, r): row r, columns c0 + 8g .. + 7 of stream i; zeros past the
+    // group's rows or past C.
+    const U32x4* src = live && r < G && c0 + g * 8 < C
+                           ? reinterpret_cast<const U32x4*>(&sh.xs[r][i * C + c0 + 8 * g])
+                           : &sh.zero;
+    const U32x4 v = *src;
 #pragma unroll
     for (int j = 0; j < 4; ++j) ss = dot2_bf16(v.v[j], v.v[j], ss);
     const bf16x8_t av = __builtin_bit_cast(bf16x8_t, v);
@@ -164,11 +202,6 @@ __global__ __launch_bounds__(kGrpWaves * 64) void pre_group_kernel(PreArgs a, in
     for (int nt = 0; nt < NT; ++nt)
       acc[nt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(av, __builtin_bit_cast(bf16x8_t, wq[b % P::P][nt]),
                                                          acc[nt], 0, 0, 0);
-    int i, cb;
-    const bool live = block_of(b, i, cb);
-    const int c0 = cb * kCBlock;
-    if (live && r < valid && c0 + g * 8 < C)
-      *reinterpret_cast<U32x4*>(&sh.xs[r][i * C + c0 + 8 * g]) = v;
     if (b + P::P < P::NB) issue(b + P::P);
   }
   ss += __shfl_xor(ss, 16, 64);
@@ -181,76 +214,108 @@ __global__ __launch_bounds__(kGrpWaves * 64) void pre_group_kernel(PreArgs a, in
       for (int j = 0; j < 4; ++j)
         if (4 * g + j < G) sh.acc[wave][4 * g + j][nt * 16 + r] = acc[nt][j];
   if (g == 0 && r < G) sh.ss[wave][r] = ss;
-  if (tid < GP::kCount) sh.prm[tid] = convert_param(rp, a.param_dtype);
-  if constexpr (NORM) {
-#pragma unroll
-    for (int h = 0; h < 2; ++h)
-      if (tid + h * T < P::CMAX) sh.gain[tid + h * T] = gain[h];
-  }
-  __syncthreads();  // partials, x rows and parameters visible
+  __syncthreads();  // partials visible
 
-  // ---- inv_rms and gates: one (token, feature) per thread -------------------
+  // ---- gates straight from the partials, no further barrier ------------------
   const float nc = (float)NC;
-  for (int idx = tid; idx < G * FD; idx += T) {
-    const int tt = idx / FD;
-    const int f = idx - tt * FD;
+  auto inv_of = [&](int tt) {
     float sq = 0.f;
 #pragma unroll
     for (int w = 0; w < kGrpWaves; ++w) sq += sh.ss[w][tt];
-    const float inv = 1.0f / sqrtf(sq / nc + a.rms_eps);
+    return 1.0f / sqrtf(sq / nc + a.rms_eps);
+  };
+  auto mix_of = [&](int tt, int f, float inv) {
     float sum = 0.f;
 #pragma unroll
     for (int w = 0; w < kGrpWaves; ++w) sum += sh.acc[w][tt][f];
-    const float m = sum * inv;
-    const int64_t tk = t0 + tt;
-    const bool ok = tt < valid;
-    if (ok && a.mixes_raw) a.mixes_raw[tk * FD + f] = m;
-    if (f < N) {
-      const float h = gate_pre(m, sh.prm[0], sh.prm[GP::kBiasPre + f], a.pre_eps, kBF16);
-      sh.hpre[tt][f] = h;
-      if (ok && a.h_pre) st_any(a.h_pre, tk * N + f, kBF16, h);
-      if (ok && f == 0 && a.inv_rms) a.inv_rms[tk] = inv;
-    } else if (f < 2 * N) {
-      if (ok)
-        st_any(a.h_post, tk * N + (f - N), kBF16,
-               gate_post(m, sh.prm[1], sh.prm[GP::kBiasPost + f - N], a.post_mult, kBF16));
-    } else if constexpr (MODE == kFull) {
-      const int e = f - 2 * N;
-      const float h = gate_res(m, sh.prm[2], sh.prm[GP::kBiasRes + e], kBF16);
-      sh.hres[tt][e] = h;
-      if (ok && a.h_res_raw) st_any(a.h_res_raw, tk * NN + e, kBF16, h);
+    return sum * inv;
+  };
+  // Every wave: h_pre of the group's tokens, lane = (token, stream).
+  const int sk_waves = MODE == kFull && a.h_res ? (G + P::SK_TOK - 1) / P::SK_TOK : 0;
+  const int post_wave = kGrpWaves - 1 - sk_waves;  // writes h_pre / h_post / inv / mixes
+  float hp = 0.f;
+  {
+    const int tt = lane / N;
+    const int i = lane % N;
+    if (tt < G) {
+      const float inv = inv_of(tt);
+      const float m = mix_of(tt, i, inv);
+      hp = gate_pre(m, sh.prm[0], sh.prm[GP::kBiasPre + i], a.pre_eps, kBF16);
+      if (wave == post_wave && tt < valid) {
+        const int64_t tk = t0 + tt;
+        if (a.h_pre) st_any(a.h_pre, tk * N + i, kBF16, hp);
+        if (a.inv_rms && i == 0) a.inv_rms[tk] = inv;
+        if (a.mixes_raw) a.mixes_raw[tk * FD + i] = m;
+        if constexpr (MODE != kHead) {
+          const float mp = mix_of(tt, N + i, inv);
+          st_any(a.h_post, tk * N + i, kBF16,
+                 gate_post(mp, sh.prm[1], sh.prm[GP::kBiasPost + i], a.post_mult, kBF16));
+          if (a.mixes_raw) a.mixes_raw[tk * FD + N + i] = mp;
+        }
+      }
     }
   }
-  __syncthreads();  // h_pre and the h_res logits visible
 
-  // ---- Sinkhorn on the last waves, then the pre-aggregate -------------------
+  // The wave's own copy in LDS for the pre-aggregate items (a lane-indexed
+  // shuffle there would read zeros from lanes that ran out of items).  A
+  // wave's LDS accesses complete in order, so no barrier is needed.
+  sh.hw[wave][lane] = hp;
+  __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+  __builtin_amdgcn_wave_barrier();
+  __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+
+  // The last waves: h_res logits of their tokens, then the Sinkhorn, before
+  // their share of the pre-aggregate.
   if constexpr (MODE == kFull) {
-    const int sk_waves = (G + P::SK_TOK - 1) / P::SK_TOK;
     const int sw = kGrpWaves - 1 - wave;  // uniform
-    if (a.h_res && sw < sk_waves) {
+    if (sw < sk_waves) {
       const int tt = sw * P::SK_TOK + lane / P::SKL;
       const int ts = tt < G ? tt : 0;
       const bool ok = tt < valid;
+      const int64_t tk = t0 + tt;
+      const float inv = inv_of(ts);
       if constexpr (N == 8) {
         const int jl = lane & 15;
         const int e0 = (jl & 7) * N + 4 * (jl >> 3);  // row (jl & 7), columns 4 (jl >> 3) ..
         float v[4];
 #pragma unroll
-        for (int q = 0; q < 4; ++q) v[q] = sh.hres[ts][e0 + q];
+        for (int q = 0; q < 4; ++q) {
+          const float m = mix_of(ts, 2 * N + e0 + q, inv);
+          v[q] = gate_res(m, sh.prm[2], sh.prm[GP::kBiasRes + e0 + q], kBF16);
+          if (ok && a.mixes_raw) a.mixes_raw[tk * FD + 2 * N + e0 + q] = m;
+          if (ok && a.h_res_raw) st_any(a.h_res_raw, tk * NN + e0 + q, kBF16, v[q]);
+        }
         sk8_start(v, a.sk_eps);
         for (int it = 1; it < a.sk_iters; ++it) sk8_iter(v, a.sk_eps);
         if (ok) {
 #pragma unroll
-          for (int q = 0; q < 4; ++q) st_any(a.h_res, (t0 + tt) * NN + e0 + q, kBF16, v[q]);
+          for (int q = 0; q < 4; ++q) st_any(a.h_res, tk * NN + e0 + q, kBF16, v[q]);
         }
       } else {
         const int e = lane % NN;
-        const float v = sinkhorn_lane<N>(sh.hres[ts][e], a.sk_iters, a.sk_eps);
-        if (ok) st_any(a.h_res, (t0 + tt) * NN + e, kBF16, v);
+        const float m = mix_of(ts, 2 * N + e, inv);
+        const float h = gate_res(m, sh.prm[2], sh.prm[GP::kBiasRes + e], kBF16);
+        if (ok && a.mixes_raw) a.mixes_raw[tk * FD + 2 * N + e] = m;
+        if (ok && a.h_res_raw) st_any(a.h_res_raw, tk * NN + e, kBF16, h);
+        const float v = sinkhorn_lane<N>(h, a.sk_iters, a.sk_eps);
+        if (ok) st_any(a.h_res, tk * NN + e, kBF16, v);
+      }
+    } else if (!a.h_res && wave == post_wave) {
+      // No Sinkhorn wanted: the raw logits (and their mixes) still go out.
+      for (int idx = lane; idx < G * NN; idx += 64) {
+        const int tt = idx / NN;
+        const int e = idx - tt * NN;
+        if (tt < valid) {
+          const int64_t tk = t0 + tt;
+          const float m = mix_of(tt, 2 * N + e, inv_of(tt));
+          if (a.mixes_raw) a.mixes_raw[tk * FD + 2 * N + e] = m;
+          if (a.h_res_raw) st_any(a.h_res_raw, tk * NN + e, kBF16, gate_res(m, sh.prm[2], sh.prm[GP::kBiasRes + e], kBF16));
+        }
       }
     }
   }
 
+  // ---- pre-aggregate: one column pair per item -------------------------------
   const int C2 = C / 2;
   const int items = G * C2;
   const auto rsub = make_rsrc(static_cast<uint16_t*>(a.sub_in) + t0 * C, (uint32_t)valid * C * 2u);
@@ -263,8 +328,9 @@ __global__ __launch_bounds__(kGrpWaves * 64) void pre_group_kernel(PreArgs a, in
 #pragma unroll
     for (int i = 0; i < N; ++i) {
       xd[i] = *reinterpret_cast<const uint32_t*>(&sh.xs[tt][i * C + 2 * d]);
-      hlo[i] = pack_lo(sh.hpre[tt][i]);
-      hhi[i] = pack_hi(sh.hpre[tt][i]);
+      const float h = sh.hw[wave][tt * N + i];
+      hlo[i] = pack_lo(h);
+      hhi[i] = pack_hi(h);
     }
     const uint32_t y = preagg_pair<N>(xd, hlo, hhi);
     if constexpr (NORM) {
