@@ -260,6 +260,103 @@ def bench_backward(reps: int = 20, sets: int = 4, n: int = N_STREAMS, M: int = T
     return out
 
 
+def layout_bytes(n: int, C: int, M: int, sx: int = 4, sf: int = 2, sp: int = 4):
+    """Compulsory HBM bytes per launch in the reference trainers' layout
+    (trainer/train_pretrain.py:129-130: fp32 model under bf16 autocast): fp32
+    stream, gates, gradients and parameters (sx, sp bytes), bf16 sublayer
+    output F and its gradient (sf).  Same operand lists as algorithmic_bytes
+    and backward_bytes."""
+    fd = 2 * n + n * n
+    h = n + n * n
+    return {
+        "pre": M * (n * C + C + h) * sx + n * C * fd * sp,
+        "post": M * (2 * n * C * sx + C * sf + h * sx),
+        "post_bwd": M * (3 * n * C * sx + 2 * C * sf + 2 * h * sx),
+        "sinkhorn_bwd": M * 3 * n * n * sx,
+        "pre_bwd": M * ((2 * n * C + C + h) * sx + 4 + 8 * fd) + n * C * fd * sp,
+        "pre_bwd_weights": M * (n * C * sx + 4 + 8 * fd) + n * C * fd * sp,
+    }
+
+
+def bench_layout32(reps: int = 10, sets: int = 4, n: int = N_STREAMS, M: int = TOKENS):
+    """The forward and backward launches of one connection at the config-2
+    shape in the reference trainers' layout: fp32 stream x, fp32 phi and gate
+    parameters, bf16 F (what F returns under autocast, model/mhc_fused.py:441),
+    fp32 gradients of the stream.  Timed like bench_backward: `sets` rotating
+    input sets, steady state."""
+    import torch
+    from model import _hip as H, _ops
+
+    dev = torch.device("cuda:0")
+    C = C_DIM
+    f32, bf = torch.float32, torch.bfloat16
+    g = torch.Generator().manual_seed(5)
+    phi = (torch.randn(n * C, 2 * n + n * n, generator=g) * 0.02).to(dev)
+    a = torch.tensor(0.01, dtype=f32, device=dev)
+    b0 = torch.zeros(n, dtype=f32, device=dev)
+    br = torch.eye(n, dtype=f32, device=dev)
+    packed = _ops.PhiPack(H.MODE_FULL).get(phi, n, C)
+    S = []
+    for _ in range(sets):
+        x = torch.randn(M, n * C, generator=g).to(dev)
+        o = _ops.pre_full(x.view(1, M, n * C), phi, packed, a, b0, a, b0, a, br, n, C, 2.0, 1e-6,
+                          1e-6, ITERS, 1e-6, want_raw=True, want_saved=True)
+        f = torch.randn(M, C, generator=g).to(bf).to(dev)
+        gout = torch.randn(M, n * C, generator=g).to(dev)
+        gsub = torch.randn(M, C, generator=g).to(dev)
+        S.append(dict(x=x, o=o, f=f, gout=gout, gsub=gsub))
+    for s in S:
+        _, s["ghr"], s["ghp"], _ = _ops.post_bwd(s["x"], s["o"]["h_res"], s["o"]["h_post"], s["f"],
+                                                 n, C, s["gout"])
+        s["graw_res"] = _ops.sinkhorn_bwd(s["o"]["h_res_raw"], s["ghr"], ITERS, 1e-6, out_dtype=f32)
+        _, s["graw"] = _ops.pre_bwd(s["x"], phi, (a, a, a), (b0, b0, br), s["o"]["inv_rms"],
+                                    s["o"]["mixes_raw"], n, C, H.MODE_FULL, 2.0, 1e-6, s["gsub"],
+                                    None, s["ghp"], s["graw_res"])
+    ops = {
+        "pre": lambda s: _ops.pre_full(s["x"].view(1, M, n * C), phi, packed, a, b0, a, b0, a, br,
+                                       n, C, 2.0, 1e-6, 1e-6, ITERS, 1e-6, want_raw=True,
+                                       want_saved=True),
+        "post": lambda s: _ops.post(s["x"], s["o"]["h_res"], s["o"]["h_post"], s["f"], n, C),
+        "post_bwd": lambda s: _ops.post_bwd(s["x"], s["o"]["h_res"], s["o"]["h_post"], s["f"], n,
+                                            C, s["gout"]),
+        "sinkhorn_bwd": lambda s: _ops.sinkhorn_bwd(s["o"]["h_res_raw"], s["ghr"], ITERS, 1e-6,
+                                                    out_dtype=f32),
+        "pre_bwd": lambda s: _ops.pre_bwd(s["x"], phi, (a, a, a), (b0, b0, br), s["o"]["inv_rms"],
+                                          s["o"]["mixes_raw"], n, C, H.MODE_FULL, 2.0, 1e-6,
+                                          s["gsub"], None, s["ghp"], s["graw_res"]),
+        "pre_bwd_weights": lambda s: _ops.pre_bwd_weights(s["x"], s["o"]["inv_rms"],
+                                                          s["o"]["mixes_raw"], s["graw"], phi,
+                                                          (a, a, a), n, C, H.MODE_FULL),
+    }
+    nbytes = layout_bytes(n, C, M)
+    out = {}
+    for name, fn in ops.items():
+        for s in S:
+            fn(s)
+        _sync()
+        e0 = torch.cuda.Event(enable_timing=True)
+        e1 = torch.cuda.Event(enable_timing=True)
+        _queue_ahead()
+        e0.record()
+        for _ in range(reps):
+            for s in S:
+                fn(s)
+        e1.record()
+        _sync()
+        ms = e0.elapsed_time(e1) / (reps * sets)
+        gbs = nbytes[name] / (ms * 1e-3) / 1e9
+        out[name] = {"ms": round(ms, 5), "GBps": round(gbs, 1), "frac": round(gbs / HBM_PEAK_GBS, 4),
+                     "algorithmic_bytes": nbytes[name]}
+    fwd = out["pre"]["ms"] + out["post"]["ms"]
+    bwd = sum(out[k]["ms"] for k in ("post_bwd", "sinkhorn_bwd", "pre_bwd", "pre_bwd_weights"))
+    out["fwd_ms"] = round(fwd, 5)
+    out["bwd_ms"] = round(bwd, 5)
+    out["fwd_tokens_per_s"] = round(M / (fwd * 1e-3), 1)
+    out["config"] = (f"{M} tokens, n={n}, C={C}: x / phi / gates / stream gradients fp32, "
+                     "F and its gradient bf16 (autocast)")
+    return out
+
+
 TRAFFIC_FILE = ROOT / "profiles" / "traffic_mhc_fwd_c2.txt"
 
 

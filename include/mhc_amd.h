@@ -71,6 +71,24 @@ int mhc_phi_pack(const void* phi, int phi_dtype, void* packed, int n, int C, int
                  hipStream_t stream);
 
 /*
+ * Size in bytes of the split-operand image of an fp32 phi for (n, C, mode), or
+ * 0 when that shape has no fp32 MFMA kernel (n not in {1,2,4}, C % 8 != 0,
+ * C > 1024, or MHCHead with n == 1).  Host-only, no device work.
+ * No reference counterpart: the reference's fused kernel computes the fp32
+ * projection elementwise (model/mhc_fused.py:217-230); this build runs it as
+ * bf16 MFMAs on hi / lo splits of both operands.
+ */
+int64_t mhc_phi_split_bytes(int n, int C, int mode);
+
+/*
+ * Write the split-operand image of phi [n*C, FD] (any dtype; each value is
+ * split into bf16(v) and bf16(v - bf16(v))) into packed (mhc_phi_split_bytes
+ * bytes).  No reference counterpart (see mhc_phi_split_bytes).
+ */
+int mhc_phi_pack_split(const void* phi, int phi_dtype, void* packed, int n, int C, int mode,
+                       hipStream_t stream);
+
+/*
  * Full mHC pre phase fused with Sinkhorn: RMS over the n*C row (no gain),
  * projection x_norm @ phi, gates, Sinkhorn-Knopp of H_res, and the
  * pre-aggregate sublayer_in = sum_i h_pre[i] * x[i].
@@ -82,7 +100,10 @@ int mhc_phi_pack(const void* phi, int phi_dtype, void* packed, int n, int C, int
  *
  *   x            [M, n*C]   x_dtype (f32 / bf16 / f16)
  *   phi          [n*C, FD]  phi_dtype, FD = 2n + n*n, columns [pre | post | res]
- *   phi_packed   mhc_phi_pack image of phi, or NULL (then a VALU kernel runs)
+ *   phi_packed   image of phi for the MFMA kernels, or NULL (then a VALU kernel
+ *                runs): the mhc_phi_pack image for bf16 x and bf16 phi, the
+ *                mhc_phi_pack_split image for fp32 x and fp32 phi; ignored for
+ *                other dtype pairs
  *   alpha_pre/post/res  0-dim scalars, bias_pre/post [n], bias_res [n, n];
  *                all param_dtype
  *   sublayer_in  [M, C]     x_dtype               (required)

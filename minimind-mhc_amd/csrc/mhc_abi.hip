@@ -66,10 +66,12 @@ int check_pre(const mhc::PreArgs& a, const char* fn) {
 int run_pre(mhc::PreArgs& a, hipStream_t stream, const char* fn) {
   if (int rc = check_pre(a, fn)) return rc;
   if (a.M == 0) return 0;
-  const bool mfma = a.phi_packed && a.mode != mhc::kRms &&
-                    mhc::mfma_supported(a.x_dtype, a.phi_dtype, a.n, a.C, a.mode) &&
-                    aligned16(a.x) && aligned16(a.sub_in) && aligned16(a.phi_packed);
-  if (!mfma) a.phi_packed = nullptr;
+  const bool packed_ok = a.phi_packed && a.mode != mhc::kRms && aligned16(a.x) && aligned16(a.sub_in) &&
+                         aligned16(a.phi_packed);
+  const bool mfma = packed_ok && mhc::mfma_supported(a.x_dtype, a.phi_dtype, a.n, a.C, a.mode);
+  const bool split = packed_ok && !a.norm_w && mhc::split_supported(a.x_dtype, a.phi_dtype, a.n, a.C, a.mode);
+  if (!mfma && !split) a.phi_packed = nullptr;
+  if (split) return hip_status(mhc::launch_pre_split(a, mhc::device_cus(), stream), fn);
   return hip_status(mfma ? mhc::launch_pre_mfma(a, stream) : mhc::launch_pre_generic(a, stream), fn);
 }
 
@@ -147,7 +149,7 @@ int scratch_ptr(hipStream_t stream, void** out, const char* fn) {
 
 extern "C" {
 
-int mhc_abi_version(void) { return 4; }
+int mhc_abi_version(void) { return 5; }
 
 const char* mhc_last_error(void) { return g_err; }
 
@@ -160,6 +162,18 @@ int mhc_phi_pack(const void* phi, int phi_dtype, void* packed, int n, int C, int
   if (phi_dtype != mhc::kBF16) return fail(hipErrorInvalidValue, "mhc_phi_pack: phi must be bf16");
   if (!phi || !packed) return fail(hipErrorInvalidValue, "mhc_phi_pack: null pointer");
   return hip_status(mhc::launch_phi_pack(phi, phi_dtype, packed, n, C, mode, stream), "mhc_phi_pack");
+}
+
+int64_t mhc_phi_split_bytes(int n, int C, int mode) { return mhc::split_packed_bytes(n, C, mode); }
+
+int mhc_phi_pack_split(const void* phi, int phi_dtype, void* packed, int n, int C, int mode,
+                       hipStream_t stream) {
+  const int64_t bytes = mhc::split_packed_bytes(n, C, mode);
+  if (bytes <= 0)
+    return fail(hipErrorInvalidValue, "mhc_phi_pack_split: no split layout for n=%d C=%d mode=%d", n, C, mode);
+  if (!dtype_ok(phi_dtype)) return fail(hipErrorInvalidValue, "mhc_phi_pack_split: bad phi dtype %d", phi_dtype);
+  if (!phi || !packed) return fail(hipErrorInvalidValue, "mhc_phi_pack_split: null pointer");
+  return hip_status(mhc::launch_phi_pack_split(phi, phi_dtype, packed, n, C, mode, stream), "mhc_phi_pack_split");
 }
 
 static int pre_full(const void* x, int x_dtype, const void* phi, int phi_dtype,

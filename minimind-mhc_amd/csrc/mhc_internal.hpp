@@ -128,8 +128,17 @@ struct WeightsArgs {
   int max_ranges;
 };
 
+// Compute units of the current device (cached).
+int device_cus();
 // Launchers: return hipSuccess or the launch error.
 hipError_t launch_pre_mfma(const PreArgs& a, hipStream_t s);   // requires mfma_supported()
+// fp32 x and fp32 phi on split bf16 MFMA operands (n in {1, 2, 4}, C <= 1024,
+// C % 8 == 0, no fused norm); phi_packed is the mhc_phi_pack_split image.
+bool split_supported(int x_dtype, int phi_dtype, int n, int C, int mode);
+int64_t split_packed_bytes(int n, int C, int mode);
+hipError_t launch_phi_pack_split(const void* phi, int phi_dtype, void* packed, int n, int C, int mode,
+                                 hipStream_t s);
+hipError_t launch_pre_split(const PreArgs& a, int num_cus, hipStream_t s);
 hipError_t launch_pre_generic(const PreArgs& a, hipStream_t s);
 // Tokens at or below which launch_pre_mfma picks the small-batch group kernel
 // (one workgroup per group of up to 16 tokens; process-wide setting).

@@ -193,6 +193,8 @@ hipError_t launch_post(const PostArgs& a, hipStream_t s) {
   if (vec_ok) {
     if (a.x_dtype == kBF16 && a.f_dtype == kBF16) return launch_vec_n<__bf16, __bf16>(a, s);
     if (a.x_dtype == kF32 && a.f_dtype == kF32) return launch_vec_n<float, float>(a, s);
+    // fp32 stream, bf16 F: the reference trainers' autocast layout.
+    if (a.x_dtype == kF32 && a.f_dtype == kBF16) return launch_vec_n<float, __bf16>(a, s);
     if (a.x_dtype == kF16 && a.f_dtype == kF16) return launch_vec_n<_Float16, _Float16>(a, s);
   }
   const int64_t total = a.M * a.n * (int64_t)a.C;
@@ -211,7 +213,7 @@ hipError_t launch_post(const PostArgs& a, hipStream_t s) {
 // tl.store casts), as one wave per token: lanes stride over the token's
 // 16-byte column chunks, then wave_sum reduces the n^2 + n dot products.
 
-template <typename XT, int N, bool RES>
+template <typename XT, typename FT, int N, bool RES>
 __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(N >= 8 ? 2 : 1))) void post_bwd_vec_kernel(PostBwdArgs a) {
   constexpr int V = 16 / sizeof(XT);
   const int lane = threadIdx.x & 63;
@@ -222,9 +224,9 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(N >= 8 ? 2 
   const int64_t NC = (int64_t)N * C;
   const XT* __restrict__ x = static_cast<const XT*>(a.x) + tok * NC;
   const XT* __restrict__ g = static_cast<const XT*>(a.g_out) + tok * NC;
-  const XT* __restrict__ f = static_cast<const XT*>(a.f_out) + tok * C;
+  const FT* __restrict__ f = static_cast<const FT*>(a.f_out) + tok * C;
   XT* __restrict__ gx = a.g_x ? static_cast<XT*>(a.g_x) + tok * NC : nullptr;
-  XT* __restrict__ gf = static_cast<XT*>(a.g_f) + tok * C;
+  FT* __restrict__ gf = static_cast<FT*>(a.g_f) + tok * C;
 
   float hp[N];
   load_pack<XT, N>(static_cast<const XT*>(a.h_post) + tok * N, hp);
@@ -241,13 +243,13 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(N >= 8 ? 2 
     const int c = cv * V;
     float gv[N][V];
 #pragma unroll
-    for (int i = 0; i < N; ++i) load_pack<XT, V>(g + (int64_t)i * C + c, gv[i]);
+    for (int i = 0; i < N; ++i) load_pack_nt<XT, V>(g + (int64_t)i * C + c, gv[i]);
     float fv[V];
-    load_pack<XT, V>(f + c, fv);
+    load_pack<FT, V>(f + c, fv);
     if constexpr (RES) {
       float xv[N][V];
 #pragma unroll
-      for (int j = 0; j < N; ++j) load_pack<XT, V>(x + (int64_t)j * C + c, xv[j]);
+      for (int j = 0; j < N; ++j) load_pack_nt<XT, V>(x + (int64_t)j * C + c, xv[j]);
 #pragma unroll
       for (int j = 0; j < N; ++j) {
         float o[V];
@@ -258,7 +260,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(N >= 8 ? 2 
           for (int i = 0; i < N; ++i) acc = fmaf(hr[i * N + j], gv[i][v], acc);
           o[v] = acc;
         }
-        store_pack<XT, V>(gx + (int64_t)j * C + c, o);
+        store_pack_nt<XT, V>(gx + (int64_t)j * C + c, o);
       }
 #pragma unroll
       for (int i = 0; i < N; ++i)
@@ -268,7 +270,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(N >= 8 ? 2 
           for (int v = 0; v < V; ++v) ahr[i * N + j] = fmaf(gv[i][v], xv[j][v], ahr[i * N + j]);
     } else if (gx) {
 #pragma unroll
-      for (int j = 0; j < N; ++j) store_pack<XT, V>(gx + (int64_t)j * C + c, gv[j]);
+      for (int j = 0; j < N; ++j) store_pack_nt<XT, V>(gx + (int64_t)j * C + c, gv[j]);
     }
     float o[V];
 #pragma unroll
@@ -278,7 +280,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(N >= 8 ? 2 
       for (int i = 0; i < N; ++i) acc = fmaf(hp[i], gv[i][v], acc);
       o[v] = acc;
     }
-    store_pack<XT, V>(gf + c, o);
+    store_pack<FT, V>(gf + c, o);
 #pragma unroll
     for (int i = 0; i < N; ++i)
 #pragma unroll
@@ -514,13 +516,13 @@ __global__ __launch_bounds__(256) void post_bwd_generic_kernel(PostBwdArgs a) {
   }
 }
 
-template <typename XT, int N>
+template <typename XT, typename FT, int N>
 static hipError_t launch_bwd_vec(const PostBwdArgs& a, hipStream_t s) {
   const int64_t blocks = (a.M + 3) / 4;
   if (a.h_res)
-    hipLaunchKernelGGL((post_bwd_vec_kernel<XT, N, true>), dim3((unsigned)blocks), dim3(256), 0, s, a);
+    hipLaunchKernelGGL((post_bwd_vec_kernel<XT, FT, N, true>), dim3((unsigned)blocks), dim3(256), 0, s, a);
   else
-    hipLaunchKernelGGL((post_bwd_vec_kernel<XT, N, false>), dim3((unsigned)blocks), dim3(256), 0, s, a);
+    hipLaunchKernelGGL((post_bwd_vec_kernel<XT, FT, N, false>), dim3((unsigned)blocks), dim3(256), 0, s, a);
   return hipGetLastError();
 }
 
@@ -537,7 +539,7 @@ static hipError_t launch_bwd_bf16(const PostBwdArgs& a, hipStream_t s) {
 // bf16: the packed dot2 kernel for paired streams, the fp32 form at n = 1.
 static hipError_t launch_bwd_bf16_n(const PostBwdArgs& a, hipStream_t s) {
   switch (a.n) {
-    case 1: return launch_bwd_vec<__bf16, 1>(a, s);
+    case 1: return launch_bwd_vec<__bf16, __bf16, 1>(a, s);
     case 2: return launch_bwd_bf16<2>(a, s);
     case 4: return launch_bwd_bf16<4>(a, s);
     case 8: return launch_bwd_bf16<8>(a, s);
@@ -545,13 +547,13 @@ static hipError_t launch_bwd_bf16_n(const PostBwdArgs& a, hipStream_t s) {
   }
 }
 
-template <typename XT>
+template <typename XT, typename FT>
 static hipError_t launch_bwd_vec_n(const PostBwdArgs& a, hipStream_t s) {
   switch (a.n) {
-    case 1: return launch_bwd_vec<XT, 1>(a, s);
-    case 2: return launch_bwd_vec<XT, 2>(a, s);
-    case 4: return launch_bwd_vec<XT, 4>(a, s);
-    case 8: return launch_bwd_vec<XT, 8>(a, s);
+    case 1: return launch_bwd_vec<XT, FT, 1>(a, s);
+    case 2: return launch_bwd_vec<XT, FT, 2>(a, s);
+    case 4: return launch_bwd_vec<XT, FT, 4>(a, s);
+    case 8: return launch_bwd_vec<XT, FT, 8>(a, s);
     default: return hipErrorInvalidValue;
   }
 }
@@ -564,14 +566,17 @@ hipError_t launch_post_bwd(const PostBwdArgs& a, hipStream_t s) {
     const int al = elems * xb > 16 ? 16 : elems * xb;
     return p == nullptr || (reinterpret_cast<uintptr_t>(p) % al) == 0;
   };
-  const bool vec_ok = pow2n && a.h_dtype == a.x_dtype && a.f_dtype == a.x_dtype && a.C % V == 0 &&
+  // F in the stream dtype, or bf16 F beside an fp32 stream (autocast training).
+  const bool f_ok = a.f_dtype == a.x_dtype || (a.x_dtype == kF32 && a.f_dtype == kBF16);
+  const bool vec_ok = pow2n && a.h_dtype == a.x_dtype && f_ok && a.C % V == 0 &&
                       aligned16(a.x) && aligned16(a.g_out) && aligned16(a.f_out) &&
                       aligned16(a.g_f) && (a.g_x == nullptr || aligned16(a.g_x)) &&
                       small_ok(a.h_post, a.n) && small_ok(a.h_res, a.n * a.n);
   if (vec_ok) {
     if (a.x_dtype == kBF16) return launch_bwd_bf16_n(a, s);
-    if (a.x_dtype == kF32) return launch_bwd_vec_n<float>(a, s);
-    if (a.x_dtype == kF16) return launch_bwd_vec_n<_Float16>(a, s);
+    if (a.x_dtype == kF32 && a.f_dtype == kBF16) return launch_bwd_vec_n<float, __bf16>(a, s);
+    if (a.x_dtype == kF32) return launch_bwd_vec_n<float, float>(a, s);
+    if (a.x_dtype == kF16) return launch_bwd_vec_n<_Float16, _Float16>(a, s);
   }
   hipLaunchKernelGGL(post_bwd_generic_kernel, dim3((unsigned)a.M), dim3(256), 0, s, a);
   return hipGetLastError();

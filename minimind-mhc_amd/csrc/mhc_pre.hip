@@ -82,7 +82,7 @@ bool pre_row_staging() { return g_row_staging; }
 void set_pre_row_staging(bool on) { g_row_staging = on; }
 
 // Compute units of the current device (cached; one persistent workgroup each).
-static int device_cus() {
+int device_cus() {
   static int cache[64] = {0};
   int dev = 0;
   if (hipGetDevice(&dev) != hipSuccess) dev = 0;

@@ -33,6 +33,8 @@ _SIGNATURES = {
     "mhc_last_error": (ctypes.c_char_p, []),
     "mhc_phi_packed_bytes": (_I64, [_I, _I, _I]),
     "mhc_phi_pack": (_I, [_P, _I, _P, _I, _I, _I, _P]),
+    "mhc_phi_split_bytes": (_I64, [_I, _I, _I]),
+    "mhc_phi_pack_split": (_I, [_P, _I, _P, _I, _I, _I, _P]),
     "mhc_pre_fwd": (_I, [_P, _I, _P, _I, _P,              # x, x_dt, phi, phi_dt, packed
                          _P, _P, _P, _P, _P, _P, _I,      # alphas/biases, param_dt
                          _P, _P, _P, _P, _P, _P, _P,      # sub_in, h_pre, h_post, raw, h_res, inv, mixes
@@ -84,7 +86,7 @@ _SIGNATURES = {
     "mhc_sinkhorn_bwd": (_I, [_P, _I, _P, _I, _P, _I, _I64, _I, _I, _F, _P]),
 }
 
-ABI_VERSION = 4
+ABI_VERSION = 5
 _lib: Optional[ctypes.CDLL] = None
 
 

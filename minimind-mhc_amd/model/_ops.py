@@ -53,14 +53,21 @@ class PhiPack:
 
     def get(self, phi: torch.Tensor, n: int, C: int,
             training: Optional[bool] = None) -> Optional[torch.Tensor]:
-        """The image of phi (None when (n, C, dtype) has no MFMA kernel).
+        """The image of phi (None when (n, C, dtype) has no MFMA kernel): the
+        bf16 operand image for a bf16 phi (kernels for bf16 streams), the
+        split hi / lo image for an fp32 phi (kernels for fp32 streams).
         training: whether phi trains in this call; default grad mode and
         phi.requires_grad (inside an autograd Function's forward, where grad
         mode is off, pass ctx.needs_input_grad for phi)."""
         lib = H.load()
-        if phi.dtype != torch.bfloat16:
+        if phi.dtype == torch.bfloat16:
+            nbytes = lib.mhc_phi_packed_bytes(n, C, self.mode)
+            pack = lib.mhc_phi_pack
+        elif phi.dtype == torch.float32:
+            nbytes = lib.mhc_phi_split_bytes(n, C, self.mode)
+            pack = lib.mhc_phi_pack_split
+        else:
             return None
-        nbytes = lib.mhc_phi_packed_bytes(n, C, self.mode)
         if nbytes <= 0:
             return None
         if training is None:
@@ -69,14 +76,14 @@ class PhiPack:
             version = None if training else phi._version
         except RuntimeError:
             version = None
-        key = (phi.data_ptr(), version, phi.device, n, C)
+        key = (phi.data_ptr(), version, phi.device, phi.dtype, n, C)
         src = self._src() if self._src is not None else None
         if version is not None and src is phi and key == self._key and self._buf is not None:
             return self._buf
         w = phi.detach().contiguous()
         buf = torch.empty(nbytes, dtype=torch.uint8, device=phi.device)
-        H.check(lib.mhc_phi_pack(w.data_ptr(), H.DTYPE_BF16, buf.data_ptr(), n, C, self.mode,
-                                 H.stream(phi.device)), "mhc_phi_pack")
+        H.check(pack(w.data_ptr(), H.dtype_tag(w), buf.data_ptr(), n, C, self.mode,
+                     H.stream(phi.device)), "mhc_phi_pack")
         if version is None:
             self.invalidate()
         else:

@@ -56,6 +56,21 @@ def test_packed_sizes(lib):
     assert lib.mhc_phi_packed_bytes(1, 768, 2) == 0                      # head n=1 is RMSNorm
 
 
+def test_split_packed_sizes(lib):
+    # fp32 split image: 16-column tiles of 8 features (hi | lo), n in {1, 2, 4}
+    assert lib.mhc_phi_split_bytes(4, 768, 0) == 4 * 24 * 3 * 64 * 16   # FD 24 -> 3 tiles
+    assert lib.mhc_phi_split_bytes(4, 768, 1) == 4 * 24 * 1 * 64 * 16   # FD 8
+    assert lib.mhc_phi_split_bytes(4, 768, 2) == 4 * 24 * 1 * 64 * 16   # FD 4
+    assert lib.mhc_phi_split_bytes(2, 512, 0) == 2 * 16 * 1 * 64 * 16   # FD 8
+    assert lib.mhc_phi_split_bytes(1, 200, 0) == 1 * 7 * 1 * 64 * 16    # FD 3, ragged C
+    assert lib.mhc_phi_split_bytes(8, 768, 0) == 0                      # no fp32 instance
+    assert lib.mhc_phi_split_bytes(4, 100, 0) == 0                      # C % 8 != 0
+    assert lib.mhc_phi_split_bytes(4, 2048, 0) == 0                     # C > 1024
+    assert lib.mhc_phi_split_bytes(1, 768, 2) == 0                      # head n=1 is RMSNorm
+    rc = lib.mhc_phi_pack_split(None, 0, None, 8, 768, 0, None)
+    assert rc == 1 and b"no split layout" in lib.mhc_last_error()
+
+
 def test_validation_errors_need_no_device(lib):
     # n = 0 is rejected by argument checks, before any HIP call
     rc = lib.mhc_pre_fwd(None, 1, None, 1, None, None, None, None, None, None, None, 1,

@@ -1,0 +1,112 @@
+"""The fp32-stream pre kernel (pre_split_kernel: bf16 MFMA on hi / lo splits of
+x and phi, 8-token tiles) against the fp32 VALU kernel (the same entry point
+without a phi image) and against the CPU oracle, at the BASELINE fp32 bar
+(1e-5 max-norm relative, model/mhc_fused.py:871-876).
+
+This is the layout of the reference's trainers (fp32 model under bf16
+autocast, trainer/train_pretrain.py:129-130): fp32 x, phi and gate
+parameters.  Shapes: n in {1, 2, 4}, the three projection modes, C a multiple
+of 256 and not (640, 200), C = 1024 (phi tiles from LDS and L2), batches with a
+ragged last tile, fewer tiles than CUs and several tiles per CU, Sinkhorn 0 /
+1 / 20 iterations, repeated launches."""
+from __future__ import annotations
+
+import pytest
+import torch
+
+from oracle import mhc_ref as R
+from tests._util import make_params, maxrel
+
+pytestmark = pytest.mark.gpu
+
+from model import _hip as H  # noqa: E402
+from model import _ops  # noqa: E402
+
+F32 = torch.float32
+BAR = 1e-5
+_MODE = {"full": H.MODE_FULL, "nohres": H.MODE_NOHRES, "head": H.MODE_HEAD}
+
+
+def _run(kind, xd, pd, packed, n, C, iters=20):
+    if kind == "full":
+        o = _ops.pre_full(xd, pd["phi_weight"], packed, pd["alpha_pre"], pd["bias_pre"],
+                          pd["alpha_post"], pd["bias_post"], pd["alpha_res"], pd["bias_res"], n, C,
+                          2.0, 1e-6, 1e-6, iters, 1e-6, want_h_pre=True, want_raw=True,
+                          want_saved=True)
+    elif kind == "nohres":
+        o = _ops.pre_nohres(xd, pd["phi_weight"], packed, pd["alpha_pre"], pd["bias_pre"],
+                            pd["alpha_post"], pd["bias_post"], n, C, 2.0, 1e-6, 1e-6,
+                            want_h_pre=True, want_saved=True)
+    else:
+        out, inv, mix = _ops.head(xd, pd["phi_weight"], packed, pd["alpha"], pd["bias"], n, C,
+                                  1e-6, 1e-6, want_saved=True)
+        o = {"sub_in": out, "inv_rms": inv, "mixes_raw": mix}
+    torch.cuda.synchronize()
+    return {k: v.clone() for k, v in o.items() if v is not None}
+
+
+def _case(kind, n, C, M, seed):
+    g = torch.Generator().manual_seed(seed)
+    p = make_params(kind, n, C, F32, g, stress=True)
+    x = torch.randn(1, M, n * C, generator=g) * 2.0
+    dev = torch.device("cuda:0")
+    pd = {k: v.to(dev) for k, v in p.items()}
+    packed = _ops.PhiPack(_MODE[kind]).get(pd["phi_weight"], n, C)
+    assert packed is not None and packed.numel() == H.load().mhc_phi_split_bytes(n, C, _MODE[kind])
+    return x, p, pd, packed, dev
+
+
+@pytest.mark.parametrize("kind", ["full", "nohres", "head"])
+@pytest.mark.parametrize("n,C", [(4, 768), (2, 768), (1, 768), (4, 256), (4, 1024), (2, 512),
+                                 (4, 640), (2, 200), (1, 1024)])
+@pytest.mark.parametrize("M", [1, 9, 4096 + 5])
+def test_split_matches_fp32_valu_kernel(kind, n, C, M):
+    if kind == "head" and n == 1:
+        pytest.skip("MHCHead with n = 1 is an RMSNorm (no projection)")
+    x, p, pd, packed, dev = _case(kind, n, C, M, seed=1000 * n + C + M)
+    print(f"split {kind} n={n} C={C} M={M}", flush=True)
+    xd = x.to(dev)
+    got = _run(kind, xd, pd, packed, n, C)
+    ref = _run(kind, xd, pd, None, n, C)
+    assert got.keys() == ref.keys()
+    for k in ref:
+        assert maxrel(ref[k], got[k]) <= BAR, (k, maxrel(ref[k], got[k]))
+
+
+@pytest.mark.parametrize("n,C", [(4, 768), (2, 512), (1, 256)])
+def test_split_vs_oracle(n, C):
+    M = 8 * 256 * 3 + 5  # several tiles per CU and a ragged last tile
+    x, p, pd, packed, dev = _case("full", n, C, M, seed=3 + n)
+    o = _run("full", x.to(dev), pd, packed, n, C)
+    idx = torch.tensor([0, 1, 7, 8, 9, M // 2, M - 6, M - 1])
+    sub, h_pre, h_post, h_raw, inv, mixes = R.pre_full(x[:, idx], p, n, C)
+    h_res = R.sinkhorn(h_raw.float(), 20, 1e-6)
+    d = idx.to(dev)
+    for ref, key, shape in ((sub, "sub_in", (M, C)), (h_pre, "h_pre", (M, n)),
+                            (h_post, "h_post", (M, n)), (h_raw, "h_res_raw", (M, n * n)),
+                            (h_res, "h_res", (M, n * n)), (inv, "inv_rms", (M,)),
+                            (mixes, "mixes_raw", (M, 2 * n + n * n))):
+        got = o[key].reshape(shape)[d].cpu()
+        assert maxrel(ref[0].reshape(got.shape), got) <= BAR, key
+
+
+@pytest.mark.parametrize("iters", [0, 1, 20])
+def test_split_sinkhorn_iterations(iters):
+    n, C, M = 4, 768, 300
+    x, p, pd, packed, dev = _case("full", n, C, M, seed=iters)
+    xd = x.to(dev)
+    got = _run("full", xd, pd, packed, n, C, iters)
+    ref = _run("full", xd, pd, None, n, C, iters)
+    assert maxrel(ref["h_res"], got["h_res"]) <= BAR
+
+
+def test_split_repeat_launches():
+    """Many workgroups, repeated launches: bit-identical every time."""
+    n, C, M = 4, 768, 8 * 256 * 4 + 3
+    x, p, pd, packed, dev = _case("full", n, C, M, seed=11)
+    xd = x.to(dev)
+    first = _run("full", xd, pd, packed, n, C)
+    for _ in range(4):
+        again = _run("full", xd, pd, packed, n, C)
+        for k in first:
+            assert torch.equal(first[k], again[k]), k
