@@ -136,8 +136,85 @@ __global__ __launch_bounds__(256) void pre_bwd_generic_kernel(PreBwdArgs a) {
 // operands read from L2 as they are used.  That leaves ~90 VGPRs a lane at
 // n = 4 (amdgpu_waves_per_eu(4): two 8-wave workgroups per CU), so one
 // workgroup's loads overlap the other's gates and MFMAs.
-template <int N, int MODE, int NW, int KJ>
-__global__ __launch_bounds__(NW * 64) __attribute__((amdgpu_waves_per_eu(4))) void pre_bwd_mfma_kernel(PreBwdArgs a) {
+// Eight consecutive elements of a bf16 (one 16-byte load) or fp32 (two)
+// tensor, as the MFMA backward kernels hold them.
+template <bool F32>
+struct Chunk8;
+template <>
+struct Chunk8<false> {
+  U32x4 v;
+  __device__ static Chunk8 load(__amdgpu_buffer_rsrc_t r, uint32_t off) {
+    Chunk8 c;
+    c.v = buf_load16(r, off);
+    return c;
+  }
+  __device__ static float get(const Chunk8& c, int i) {
+    return (i & 1) ? bf16hi(c.v.v[i >> 1]) : bf16lo(c.v.v[i >> 1]);
+  }
+  // sum_i a[i] * b[i]: exact bf16 products, fp32 sums (v_dot2)
+  __device__ static float dot(const Chunk8& a, const Chunk8& b) {
+    float acc = 0.f;
+#pragma unroll
+    for (int e = 0; e < 4; ++e) acc = dot2_bf16(a.v.v[e], b.v.v[e], acc);
+    return acc;
+  }
+  __device__ static bf16x8_t hi(const Chunk8& c) { return __builtin_bit_cast(bf16x8_t, c.v); }
+  __device__ static void store(__amdgpu_buffer_rsrc_t r, uint32_t off, const float (&x)[8]) {
+    U32x4 o;
+#pragma unroll
+    for (int e = 0; e < 4; ++e) o.v[e] = pack_bf16x2(x[2 * e], x[2 * e + 1]);
+    buf_store16(r, off, o);
+  }
+};
+template <>
+struct Chunk8<true> {
+  U32x4 v[2];
+  __device__ static Chunk8 load(__amdgpu_buffer_rsrc_t r, uint32_t off) {
+    Chunk8 c;
+    c.v[0] = buf_load16(r, off);
+    c.v[1] = buf_load16(r, off == kBufOob ? kBufOob : off + 16u);
+    return c;
+  }
+  __device__ static float get(const Chunk8& c, int i) { return __uint_as_float(c.v[i >> 2].v[i & 3]); }
+  __device__ static float dot(const Chunk8& a, const Chunk8& b) {
+    float acc = 0.f;
+#pragma unroll
+    for (int i = 0; i < 8; ++i) acc = fmaf(get(a, i), get(b, i), acc);
+    return acc;
+  }
+  // bf16(x) and bf16(x - bf16(x)) of the 8 values, as MFMA operands
+  __device__ static bf16x8_t hi(const Chunk8& c) {
+    U32x4 o;
+#pragma unroll
+    for (int e = 0; e < 4; ++e) o.v[e] = pack_bf16x2(get(c, 2 * e), get(c, 2 * e + 1));
+    return __builtin_bit_cast(bf16x8_t, o);
+  }
+  __device__ static bf16x8_t lo(const Chunk8& c) {
+    U32x4 o;
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+      const float a0 = get(c, 2 * e), a1 = get(c, 2 * e + 1);
+      const uint32_t h = pack_bf16x2(a0, a1);
+      o.v[e] = pack_bf16x2(a0 - bf16lo(h), a1 - bf16hi(h));
+    }
+    return __builtin_bit_cast(bf16x8_t, o);
+  }
+  __device__ static void store(__amdgpu_buffer_rsrc_t r, uint32_t off, const float (&x)[8]) {
+    U32x4 o0, o1;
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+      o0.v[e] = __float_as_uint(x[e]);
+      o1.v[e] = __float_as_uint(x[4 + e]);
+    }
+    buf_store16(r, off, o0);
+    buf_store16(r, off == kBufOob ? kBufOob : off + 16u, o1);
+  }
+};
+
+template <int N, int MODE, int NW, int KJ, bool F32>
+__global__ __launch_bounds__(NW * 64) __attribute__((amdgpu_waves_per_eu(F32 ? 2 : 4))) void pre_bwd_mfma_kernel(PreBwdArgs a) {
+  using XV = Chunk8<F32>;
+  constexpr uint32_t ES = F32 ? 4u : 2u;  // bytes of a stream / gradient / phi element
   constexpr int FD = MODE == kFull ? 2 * N + N * N : (MODE == kNoHres ? 2 * N : N);
   constexpr int KS = (FD + 31) / 32;  // 32-feature K-steps
   constexpr int TM = 16;
@@ -158,10 +235,10 @@ __global__ __launch_bounds__(NW * 64) __attribute__((amdgpu_waves_per_eu(4))) vo
   const int64_t t0 = (int64_t)blockIdx.x * TM;
   const int valid = (int)(a.M - t0 < TM ? a.M - t0 : TM);
 
-  const auto rx = make_rsrc(static_cast<const uint16_t*>(a.x) + t0 * NC, (uint32_t)valid * NC * 2u);
-  const auto rgs = make_rsrc(a.g_sub ? static_cast<const uint16_t*>(a.g_sub) + t0 * C : nullptr,
-                             a.g_sub ? (uint32_t)valid * C * 2u : 0u);
-  const auto rgx = make_rsrc(static_cast<uint16_t*>(a.g_x) + t0 * NC, (uint32_t)valid * NC * 2u);
+  const auto rx = make_rsrc(static_cast<const unsigned char*>(a.x) + t0 * NC * ES, (uint32_t)valid * NC * ES);
+  const auto rgs = make_rsrc(a.g_sub ? static_cast<const unsigned char*>(a.g_sub) + t0 * C * ES : nullptr,
+                             a.g_sub ? (uint32_t)valid * C * ES : 0u);
+  const auto rgx = make_rsrc(static_cast<unsigned char*>(a.g_x) + t0 * NC * ES, (uint32_t)valid * NC * ES);
 
   // chunk j of this wave: stream ci, first column c0; lane column c0 + 8g
   auto chunk = [&](int j, int& ci, int& c0) {
@@ -169,13 +246,13 @@ __global__ __launch_bounds__(NW * 64) __attribute__((amdgpu_waves_per_eu(4))) vo
     ci = k < NCH ? k / NCB : 0;
     c0 = k < NCH ? (k - ci * NCB) * 32 : C;  // C: no columns (loads read zeros)
   };
-  U32x4 xs[KJ];
+  XV xs[KJ];
 #pragma unroll
   for (int j = 0; j < KJ; ++j) {
     int ci, c0;
     chunk(j, ci, c0);
     const bool ok = c0 + 8 * g < C;
-    xs[j] = buf_load16(rx, ok ? (uint32_t)(r * NC + ci * C + c0 + 8 * g) * 2u : kBufOob);
+    xs[j] = XV::load(rx, ok ? (uint32_t)(r * NC + ci * C + c0 + 8 * g) * ES : kBufOob);
   }
   const float inv = r < valid ? a.inv_rms[t0 + r] : 0.f;
 
@@ -210,16 +287,16 @@ __global__ __launch_bounds__(NW * 64) __attribute__((amdgpu_waves_per_eu(4))) vo
     }
   }
 
-  const auto rphi = make_rsrc(a.phi, (uint32_t)NC * FD * 2u);
+  const auto rphi = make_rsrc(a.phi, (uint32_t)NC * FD * ES);
   // phi A operand of chunk j, k-tile h, K-step ks: A-row r is column
   // c0 + 8 (r / 4) + 4 h + r % 4 of the chunk, lane group g features 32 ks + 8g .. + 7
+  // (fp32 phi: those 8 values, to be split into hi and lo operands).
   auto phi_op = [&](int j, int h, int ks) {
     int ci, c0;
     chunk(j, ci, c0);
     const int col = c0 + 8 * (r >> 2) + 4 * h + (r & 3);
     const bool ok = col < C && 32 * ks + 8 * g < FD;
-    return __builtin_bit_cast(
-        bf16x8_t, buf_load16(rphi, ok ? (uint32_t)((ci * C + col) * FD + 32 * ks + 8 * g) * 2u : kBufOob));
+    return XV::load(rphi, ok ? (uint32_t)((ci * C + col) * FD + 32 * ks + 8 * g) * ES : kBufOob);
   };
 
   // ---- gh partials per chunk: sum_c g_sub[c] * x[i][c].  The g_sub loads go
@@ -228,24 +305,22 @@ __global__ __launch_bounds__(NW * 64) __attribute__((amdgpu_waves_per_eu(4))) vo
   constexpr int GB = KJ < 6 ? KJ : 6;
 #pragma unroll
   for (int j0 = 0; j0 < KJ; j0 += GB) {
-    U32x4 gvb[GB];
+    XV gvb[GB];
 #pragma unroll
     for (int u = 0; u < GB; ++u) {
       int ci, c0;
       chunk(j0 + u, ci, c0);
       const bool ok = j0 + u < KJ && c0 + 8 * g < C;
-      gvb[u] = buf_load16(rgs, ok ? (uint32_t)(r * C + c0 + 8 * g) * 2u : kBufOob);
+      gvb[u] = XV::load(rgs, ok ? (uint32_t)(r * C + c0 + 8 * g) * ES : kBufOob);
     }
 #pragma unroll
     for (int u = 0; u < GB; ++u) {
       const int j = j0 + u;
       if (j >= KJ) break;
-      float acc = 0.f;
-#pragma unroll
-      for (int e = 0; e < 4; ++e) acc = dot2_bf16(gvb[u].v[e], xs[j].v[e], acc);
-      acc += xor_lane16(acc);
-      acc += xor_lane32(acc);
-      if (g == 0) s_gp[wave + NW * j][r] = acc;
+      const float acc = XV::dot(gvb[u], xs[j]);
+      const float a16 = acc + xor_lane16(acc);
+      const float a32 = a16 + xor_lane32(a16);
+      if (g == 0) s_gp[wave + NW * j][r] = a32;
     }
   }
   __syncthreads();
@@ -325,8 +400,8 @@ __global__ __launch_bounds__(NW * 64) __attribute__((amdgpu_waves_per_eu(4))) vo
   constexpr bool PF = KS == 1;
   constexpr bool CH = !PF && KJ <= 12;
   struct ChunkIn {
-    bf16x8_t av[2][KS];
-    U32x4 gv;
+    XV av[2][KS];
+    XV gv;
   };
   auto load_chunk = [&](int j, ChunkIn& in) {
     int ci, c0;
@@ -336,7 +411,7 @@ __global__ __launch_bounds__(NW * 64) __attribute__((amdgpu_waves_per_eu(4))) vo
 #pragma unroll
       for (int ks = 0; ks < KS; ++ks) in.av[h][ks] = phi_op(j, h, ks);
     const bool ok = c0 + 8 * g < C;
-    in.gv = buf_load16(rgs, ok ? (uint32_t)(r * C + c0 + 8 * g) * 2u : kBufOob);
+    in.gv = XV::load(rgs, ok ? (uint32_t)(r * C + c0 + 8 * g) * ES : kBufOob);
   };
   ChunkIn cin[PF ? 2 : 1];
   if constexpr (PF) load_chunk(0, cin[0]);
@@ -357,80 +432,83 @@ __global__ __launch_bounds__(NW * 64) __attribute__((amdgpu_waves_per_eu(4))) vo
       f32x4_t d = f32x4_t{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
       for (int ks = 0; ks < KS; ++ks) {
-        const bf16x8_t av = PF || CH ? cur.av[h][ks] : phi_op(j, h, ks);
-        d = __builtin_amdgcn_mfma_f32_16x16x32_bf16(av, bhi[ks], d, 0, 0, 0);
-        d = __builtin_amdgcn_mfma_f32_16x16x32_bf16(av, blo[ks], d, 0, 0, 0);
+        const XV av = PF || CH ? cur.av[h][ks] : phi_op(j, h, ks);
+        if constexpr (F32) {  // phi_hi . (b_hi + b_lo) + phi_lo . b_hi
+          const bf16x8_t ahi = XV::hi(av);
+          const bf16x8_t alo = XV::lo(av);
+          d = __builtin_amdgcn_mfma_f32_16x16x32_bf16(ahi, bhi[ks], d, 0, 0, 0);
+          d = __builtin_amdgcn_mfma_f32_16x16x32_bf16(ahi, blo[ks], d, 0, 0, 0);
+          d = __builtin_amdgcn_mfma_f32_16x16x32_bf16(alo, bhi[ks], d, 0, 0, 0);
+        } else {
+          const bf16x8_t ab = XV::hi(av);  // bf16 phi: the operand itself
+          d = __builtin_amdgcn_mfma_f32_16x16x32_bf16(ab, bhi[ks], d, 0, 0, 0);
+          d = __builtin_amdgcn_mfma_f32_16x16x32_bf16(ab, blo[ks], d, 0, 0, 0);
+        }
       }
       d2[h] = d;
     }
-    const U32x4 gv = PF || CH ? cur.gv : buf_load16(rgs, ok ? (uint32_t)(r * C + c0 + 8 * g) * 2u : kBufOob);
+    const XV gv = PF || CH ? cur.gv : XV::load(rgs, ok ? (uint32_t)(r * C + c0 + 8 * g) * ES : kBufOob);
     const float hp = s_hp[r][ci];
-    U32x4 o;
+    float v[8];
 #pragma unroll
-    for (int e = 0; e < 4; ++e) {
-      float v[2];
-#pragma unroll
-      for (int b = 0; b < 2; ++b) {
-        const int cc = 2 * e + b;  // column 8g + cc
-        const float gx = d2[cc >> 2][cc & 3];
-        const float xv = b ? bf16hi(xs[j].v[e]) : bf16lo(xs[j].v[e]);
-        const float gsv = b ? bf16hi(gv.v[e]) : bf16lo(gv.v[e]);
-        v[b] = inv * (gx - xv * inv * mean) + hp * gsv;
-      }
-      o.v[e] = pack_bf16x2(v[0], v[1]);
+    for (int cc = 0; cc < 8; ++cc) {  // column 8g + cc
+      const float gx = d2[cc >> 2][cc & 3];
+      v[cc] = inv * (gx - XV::get(xs[j], cc) * inv * mean) + hp * XV::get(gv, cc);
     }
     // whole offset in the vector offset, scalar offset the literal 0 (a
     // 128-bit store reads its data registers after issue)
-    buf_store16(rgx, ok ? (uint32_t)(r * NC + ci * C + c0 + 8 * g) * 2u : kBufOob, o);
+    XV::store(rgx, ok ? (uint32_t)(r * NC + ci * C + c0 + 8 * g) * ES : kBufOob, v);
   }
 }
 
-// Chunks per wave instantiated: 2 .. 24 in steps that cover C <= 1024 for
-// n in {2, 4} (8 waves) and n = 8 (16 waves).
-template <int N, int MODE, int NW, int KJ>
+// Chunks per wave instantiated: 2 .. 16 in steps that cover C <= 1024 for
+// n in {2, 4} (8 waves) and n = 8 (16 waves, bf16 only).
+template <int N, int MODE, int NW, int KJ, bool F32>
 static hipError_t launch_pre_bwd_inst(const PreBwdArgs& a, hipStream_t s) {
-  hipLaunchKernelGGL((pre_bwd_mfma_kernel<N, MODE, NW, KJ>), dim3((unsigned)((a.M + 15) / 16)),
+  hipLaunchKernelGGL((pre_bwd_mfma_kernel<N, MODE, NW, KJ, F32>), dim3((unsigned)((a.M + 15) / 16)),
                      dim3(NW * 64), 0, s, a);
   return hipGetLastError();
 }
 
-template <int N, int MODE, int NW, int... KJS>
+template <int N, int MODE, int NW, bool F32, int... KJS>
 static hipError_t launch_pre_bwd_mfma_kj(const PreBwdArgs& a, int kj, hipStream_t s) {
   hipError_t r = hipErrorInvalidValue;
   bool done = false;
-  ((!done && KJS >= kj ? (r = launch_pre_bwd_inst<N, MODE, NW, KJS>(a, s), done = true) : false), ...);
+  ((!done && KJS >= kj ? (r = launch_pre_bwd_inst<N, MODE, NW, KJS, F32>(a, s), done = true) : false), ...);
   return r;
 }
 
-template <int N, int MODE>
+template <int N, int MODE, bool F32>
 static hipError_t launch_pre_bwd_mfma_mode(const PreBwdArgs& a, hipStream_t s) {
   constexpr int NW = N >= 8 ? 16 : 8;
   const int nch = N * ((a.C + 31) / 32);
   const int kj = (nch + NW - 1) / NW;
-  return launch_pre_bwd_mfma_kj<N, MODE, NW, 2, 4, 6, 8, 12, 16>(a, kj, s);
+  return launch_pre_bwd_mfma_kj<N, MODE, NW, F32, 2, 4, 6, 8, 12, 16>(a, kj, s);
 }
 
-// Shapes with an MFMA kernel: bf16 x / phi / gradients, n in {2, 4, 8}, FD a
-// multiple of 8 (16-byte phi rows), C % 8 == 0 and C <= 1024, 16-byte aligned
-// x / g_sub / g_x / phi.
+// Shapes with an MFMA kernel: x / phi / gradients all bf16 (n in {2, 4, 8}) or
+// all fp32 (n in {2, 4}: the fp32 chunks take twice the registers), FD a
+// multiple of 8 (whole 8-feature phi operands), C % 8 == 0 and C <= 1024,
+// 16-byte aligned x / g_sub / g_x / phi.
 static bool pre_bwd_mfma_ok(const PreBwdArgs& a) {
   auto al = [](const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15) == 0; };
   if (a.mode == kRms) return false;
-  if (a.x_dtype != kBF16 || a.phi_dtype != kBF16 || a.grad_dtype != kBF16) return false;
-  if (!(a.n == 2 || a.n == 4 || a.n == 8)) return false;
+  const bool bf = a.x_dtype == kBF16 && a.phi_dtype == kBF16 && a.grad_dtype == kBF16;
+  const bool f32 = a.x_dtype == kF32 && a.phi_dtype == kF32 && a.grad_dtype == kF32;
+  if (!(bf && (a.n == 2 || a.n == 4 || a.n == 8)) && !(f32 && (a.n == 2 || a.n == 4))) return false;
   if (mode_fd(a.mode, a.n) % 8 != 0) return false;
   if (a.C % 8 != 0 || a.C > 32 * kMfmaMaxColBlocks) return false;
-  if ((int64_t)a.n * a.C * mode_fd(a.mode, a.n) * 2 > 0x7fffffffLL) return false;
+  if ((int64_t)a.n * a.C * mode_fd(a.mode, a.n) * dtype_bytes(a.x_dtype) > 0x7fffffffLL) return false;
   return al(a.x) && al(a.phi) && al(a.g_x) && (a.g_sub == nullptr || al(a.g_sub));
 }
 
-template <int N>
+template <int N, bool F32>
 static hipError_t launch_pre_bwd_mfma_n(const PreBwdArgs& a, hipStream_t s) {
   switch (a.mode) {
-    case kFull: return launch_pre_bwd_mfma_mode<N, kFull>(a, s);
-    case kNoHres: return launch_pre_bwd_mfma_mode<N, kNoHres>(a, s);
+    case kFull: return launch_pre_bwd_mfma_mode<N, kFull, F32>(a, s);
+    case kNoHres: return launch_pre_bwd_mfma_mode<N, kNoHres, F32>(a, s);
     case kHead:
-      if constexpr (N == 8) return launch_pre_bwd_mfma_mode<N, kHead>(a, s);
+      if constexpr (N == 8) return launch_pre_bwd_mfma_mode<N, kHead, F32>(a, s);
       return hipErrorInvalidValue;
     default: return hipErrorInvalidValue;
   }
@@ -438,11 +516,19 @@ static hipError_t launch_pre_bwd_mfma_n(const PreBwdArgs& a, hipStream_t s) {
 
 hipError_t launch_pre_bwd(const PreBwdArgs& a, hipStream_t s) {
   if (pre_bwd_mfma_ok(a)) {
-    switch (a.n) {
-      case 2: return launch_pre_bwd_mfma_n<2>(a, s);
-      case 4: return launch_pre_bwd_mfma_n<4>(a, s);
-      case 8: return launch_pre_bwd_mfma_n<8>(a, s);
-      default: break;
+    if (a.x_dtype == kF32) {
+      switch (a.n) {
+        case 2: return launch_pre_bwd_mfma_n<2, true>(a, s);
+        case 4: return launch_pre_bwd_mfma_n<4, true>(a, s);
+        default: break;
+      }
+    } else {
+      switch (a.n) {
+        case 2: return launch_pre_bwd_mfma_n<2, false>(a, s);
+        case 4: return launch_pre_bwd_mfma_n<4, false>(a, s);
+        case 8: return launch_pre_bwd_mfma_n<8, false>(a, s);
+        default: break;
+      }
     }
   }
   hipLaunchKernelGGL(pre_bwd_generic_kernel, dim3((unsigned)a.M), dim3(256), 0, s, a);
@@ -559,23 +645,28 @@ __global__ __launch_bounds__(256) void weights_reduce_kernel(WeightsArgs a, int 
   }
 }
 
-// bf16 x on MFMA.  Workgroup (k-slice of 128 columns, token range): per step
-// of 64 tokens the x tile is written to LDS transposed ([column][token], two
-// tokens per 32-bit write) and u = inv_rms * g_raw ([feature][token]) split
-// into bf16 hi + lo, then wave w accumulates
+// bf16 or fp32 x on MFMA.  Workgroup (k-slice of 128 columns, token range):
+// per step of 64 tokens the x tile is written to LDS transposed ([column]
+// [token], two tokens per 32-bit write) and u = inv_rms * g_raw ([feature]
+// [token]) split into bf16 hi + lo, then wave w accumulates
 //   D[16w + i][f] += sum_t x[t][k0 + 16w + i] * u[t][f]
-// with A = x^T rows (16-byte LDS reads of 8 tokens) and B = u columns.
+// with A = x^T rows (16-byte LDS reads of 8 tokens) and B = u columns.  An
+// fp32 x is split the same way (a second transposed tile holds x_lo) and
+// three products run per step: x_hi u_hi + x_hi u_lo + x_lo u_hi.
 // Workgroups of k-slice 0 also sum g_raw and g_raw * mixes per feature over
 // their range (the alpha / bias partials).
 constexpr int kWTok = 64;                // tokens per step
 constexpr int kWCols = 128;              // columns per workgroup
 constexpr int kWRow = kWTok * 2 + 16;    // LDS row stride in bytes (64 bf16 + pad)
 
-template <int NTF>  // 16-wide feature tiles
+template <int NTF, bool F32>  // 16-wide feature tiles, fp32 x
 __global__ __launch_bounds__(512) void weights_mfma_kernel(WeightsArgs a, int64_t per) {
   constexpr int F16 = NTF * 16;
   constexpr int UPT = F16 / 16;  // (token pair, feature) items per thread: 32 * F16 / 512
+  constexpr int XQ = F32 ? 2 : 1;  // 16-byte loads per 8 columns of one token
+  constexpr uint32_t ES = F32 ? 4u : 2u;
   __shared__ __attribute__((aligned(16))) unsigned char s_x[kWCols * kWRow];
+  __shared__ __attribute__((aligned(16))) unsigned char s_xl[F32 ? kWCols * kWRow : 16];
   __shared__ __attribute__((aligned(16))) unsigned char s_uh[F16 * kWRow];
   __shared__ __attribute__((aligned(16))) unsigned char s_ul[F16 * kWRow];
   __shared__ float s_ab[2][kWTok / 2][F16];
@@ -609,15 +700,18 @@ __global__ __launch_bounds__(512) void weights_mfma_kernel(WeightsArgs a, int64_
   // while the current step's MFMAs run.  x is read non-temporally (its last
   // use in the backward).
   struct Step {
-    U32x4 xa, xb;
+    U32x4 xa[XQ], xb[XQ];
     float ga[UPT], gb[UPT], ia[UPT], ib[UPT], ma[UPT], mb[UPT];
   };
   auto load_step = [&](int64_t t, Step& st) {
     const int valid = t < te ? (int)(te - t < kWTok ? te - t : kWTok) : 0;
-    const auto rs = make_rsrc(static_cast<const uint16_t*>(a.x) + (t < te ? t : 0) * NC,
-                              (uint32_t)valid * NC * 2u);
-    st.xa = buf_load16_nt(rs, okc ? (uint32_t)((2 * tp) * NC + col) * 2u : kBufOob, 0);
-    st.xb = buf_load16_nt(rs, okc ? (uint32_t)((2 * tp + 1) * NC + col) * 2u : kBufOob, 0);
+    const auto rs = make_rsrc(static_cast<const unsigned char*>(a.x) + (t < te ? t : 0) * NC * ES,
+                              (uint32_t)valid * NC * ES);
+#pragma unroll
+    for (int h = 0; h < XQ; ++h) {
+      st.xa[h] = buf_load16_nt(rs, okc ? (uint32_t)((2 * tp) * NC + col) * ES + 16u * h : kBufOob, 0);
+      st.xb[h] = buf_load16_nt(rs, okc ? (uint32_t)((2 * tp + 1) * NC + col) * ES + 16u * h : kBufOob, 0);
+    }
 #pragma unroll
     for (int u = 0; u < UPT; ++u) {
       const int idx = tid + 512 * u;
@@ -663,23 +757,36 @@ __global__ __launch_bounds__(512) void weights_mfma_kernel(WeightsArgs a, int64_
     // x tile transposed: column 8kc + e, tokens (2tp, 2tp + 1) in one dword
 #pragma unroll
     for (int e = 0; e < 8; ++e) {
-      const uint32_t wa = cur.xa.v[e >> 1];
-      const uint32_t wb = cur.xb.v[e >> 1];
-      const uint32_t d = (e & 1) ? ((wa >> 16) | (wb & 0xffff0000u)) : ((wa & 0xffffu) | (wb << 16));
-      *reinterpret_cast<uint32_t*>(s_x + (8 * kc + e) * kWRow + tp_slot(tp, kc) * 4) = d;
+      const uint32_t off = (8 * kc + e) * kWRow + tp_slot(tp, kc) * 4;
+      if constexpr (F32) {
+        const float va = __uint_as_float(cur.xa[e >> 2].v[e & 3]);
+        const float vb = __uint_as_float(cur.xb[e >> 2].v[e & 3]);
+        const uint32_t hi = pack_bf16x2(va, vb);
+        *reinterpret_cast<uint32_t*>(s_x + off) = hi;
+        *reinterpret_cast<uint32_t*>(s_xl + off) = pack_bf16x2(va - bf16lo(hi), vb - bf16hi(hi));
+      } else {
+        const uint32_t wa = cur.xa[0].v[e >> 1];
+        const uint32_t wb = cur.xb[0].v[e >> 1];
+        const uint32_t d = (e & 1) ? ((wa >> 16) | (wb & 0xffff0000u)) : ((wa & 0xffffu) | (wb << 16));
+        *reinterpret_cast<uint32_t*>(s_x + off) = d;
+      }
     }
     __syncthreads();
     load_step(t + kWTok, cur);  // next step's loads fly over the MFMAs
 #pragma unroll
     for (int ks = 0; ks < kWTok / 32; ++ks) {
       const int xc = 16 * wave + r;  // column of the slice
-      const bf16x8_t av = *reinterpret_cast<const bf16x8_t*>(
-          s_x + xc * kWRow + tp_slot(16 * ks + 4 * g, xc >> 3) * 4);
+      const int xoff = xc * kWRow + tp_slot(16 * ks + 4 * g, xc >> 3) * 4;
+      const bf16x8_t av = *reinterpret_cast<const bf16x8_t*>(s_x + xoff);
 #pragma unroll
       for (int ft = 0; ft < NTF; ++ft) {
         const int off = (16 * ft + r) * kWRow + (32 * ks + 8 * g) * 2;
-        acc[ft] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(av, *reinterpret_cast<const bf16x8_t*>(s_uh + off), acc[ft], 0, 0, 0);
+        const bf16x8_t uh = *reinterpret_cast<const bf16x8_t*>(s_uh + off);
+        acc[ft] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(av, uh, acc[ft], 0, 0, 0);
         acc[ft] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(av, *reinterpret_cast<const bf16x8_t*>(s_ul + off), acc[ft], 0, 0, 0);
+        if constexpr (F32)
+          acc[ft] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(*reinterpret_cast<const bf16x8_t*>(s_xl + xoff), uh,
+                                                            acc[ft], 0, 0, 0);
       }
     }
     __syncthreads();
@@ -718,8 +825,11 @@ __global__ __launch_bounds__(512) void weights_mfma_kernel(WeightsArgs a, int64_
 template <int NTF>
 static hipError_t launch_weights_mfma(const WeightsArgs& a, int R, int64_t per, hipStream_t s) {
   const int NC = a.n * a.C;
-  hipLaunchKernelGGL((weights_mfma_kernel<NTF>), dim3((unsigned)((NC + kWCols - 1) / kWCols), (unsigned)R),
-                     dim3(512), 0, s, a, per);
+  const dim3 grid((unsigned)((NC + kWCols - 1) / kWCols), (unsigned)R);
+  if (a.x_dtype == kF32)
+    hipLaunchKernelGGL((weights_mfma_kernel<NTF, true>), grid, dim3(512), 0, s, a, per);
+  else
+    hipLaunchKernelGGL((weights_mfma_kernel<NTF, false>), grid, dim3(512), 0, s, a, per);
   return hipGetLastError();
 }
 
@@ -728,7 +838,7 @@ hipError_t launch_pre_bwd_weights(const WeightsArgs& a, hipStream_t s) {
   const int64_t NC = (int64_t)a.n * a.C;
   const int64_t qb = (NC * FD + 255) / 256;
   const int ntf = (FD + 15) / 16;
-  const bool mfma = a.x_dtype == kBF16 && NC % 8 == 0 &&
+  const bool mfma = (a.x_dtype == kBF16 || a.x_dtype == kF32) && NC % 8 == 0 &&
                     (reinterpret_cast<uintptr_t>(a.x) & 15) == 0 &&
                     (ntf == 1 || ntf == 2 || ntf == 3 || ntf == 5);  // FD <= 80 (LDS)
   int R = weight_ranges(a.M);

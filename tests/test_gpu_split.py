@@ -110,3 +110,102 @@ def test_split_repeat_launches():
         again = _run("full", xd, pd, packed, n, C)
         for k in first:
             assert torch.equal(first[k], again[k]), k
+
+
+# ---------------------------------------------------------------- backward
+
+def _misaligned(t: torch.Tensor) -> torch.Tensor:
+    """The same values at an address 4 bytes past a 16-byte boundary: the MFMA
+    backward kernels need 16-byte aligned rows, so this copy takes the fp32
+    VALU kernels (the comparison's reference)."""
+    buf = torch.empty(t.numel() + 1, dtype=t.dtype, device=t.device)
+    v = buf[1:].view(t.shape)
+    v.copy_(t)
+    return v
+
+
+def _alpha_err(ref, got, g_raw, mixes, lo, hi):
+    terms = (g_raw[:, lo:hi].float() * mixes[:, lo:hi].float()).abs().sum().item()
+    return abs(ref.float().item() - got.float().item()) / max(abs(ref.float().item()), terms, 1e-30)
+
+
+@pytest.mark.parametrize("kind", ["full", "nohres"])
+@pytest.mark.parametrize("n,C,M", [(4, 768, 37), (4, 768, 1100), (2, 768, 300), (4, 256, 64),
+                                   (4, 1024, 50), (2, 200, 33), (4, 640, 17)])
+def test_split_backward_matches_fp32_valu_kernels(kind, n, C, M):
+    """pre_bwd (g_x, g_raw) and pre_bwd_weights (g_phi, g_alpha, g_bias) of
+    fp32 x / phi / gradients on MFMA against the fp32 VALU kernels."""
+    x, p, pd, packed, dev = _case(kind, n, C, M, seed=77 * n + C + M)
+    xd = x.to(dev).view(M, n * C)
+    o = _run(kind, x.to(dev), pd, packed, n, C)
+    inv, mixes = o["inv_rms"], o["mixes_raw"]
+    g = torch.Generator().manual_seed(M)
+    gsub = torch.randn(M, C, generator=g).to(dev)
+    ghp = torch.randn(M, n, generator=g).to(dev)
+    ghpost = torch.randn(M, n, generator=g).to(dev)
+    ghres = torch.randn(M, n * n, generator=g).to(dev) if kind == "full" else None
+    if kind == "full":
+        alphas = (pd["alpha_pre"], pd["alpha_post"], pd["alpha_res"])
+        biases = (pd["bias_pre"], pd["bias_post"], pd["bias_res"])
+        mode = H.MODE_FULL
+    else:
+        alphas = (pd["alpha_pre"], pd["alpha_post"], None)
+        biases = (pd["bias_pre"], pd["bias_post"], None)
+        mode = H.MODE_NOHRES
+    print(f"split bwd {kind} n={n} C={C} M={M}", flush=True)
+    res = []
+    for xin in (xd, _misaligned(xd)):
+        g_x, g_raw = _ops.pre_bwd(xin, pd["phi_weight"], alphas, biases, inv, mixes, n, C, mode,
+                                  2.0, 1e-6, gsub, ghp, ghpost, ghres)
+        g_w, g_a, g_b = _ops.pre_bwd_weights(xin, inv, mixes, g_raw, pd["phi_weight"], alphas, n,
+                                             C, mode)
+        torch.cuda.synchronize()
+        res.append((g_x.clone(), g_raw.clone(), g_w.clone(), g_a, g_b))
+    (gx, graw, gw, ga, gb), (rx, rraw, rw, ra, rb) = res
+    assert maxrel(rx, gx) <= BAR
+    assert maxrel(rraw, graw) <= BAR
+    assert maxrel(rw, gw) <= BAR
+    fd = 2 * n + (n * n if kind == "full" else 0)
+    bounds = ((0, n), (n, 2 * n), (2 * n, fd))
+    for i in range(3 if kind == "full" else 2):
+        assert _alpha_err(ra[i], ga[i], rraw, mixes, *bounds[i]) <= BAR, i
+        assert maxrel(rb[i], gb[i]) <= BAR, i
+
+
+def test_module_fp32_autocast_layout_training_step_matches_oracle():
+    """MHCConnection_Fused in the reference trainers' layout: fp32 parameters
+    and stream, F returning bf16 (autocast).  Forward and backward run the
+    fp32 MFMA kernels; gradients of x, phi and the gate parameters against
+    autograd of the fp32 oracle with the same bf16 F."""
+    from model.mhc_fused import MHCConnection_Fused
+    dev = torch.device("cuda:0")
+    n, C, M = 4, 768, 96
+    g = torch.Generator().manual_seed(23)
+    x = torch.randn(1, M, n * C, generator=g)
+    p = make_params("full", n, C, F32, g)
+    fw = (torch.randn(C, C, generator=g) * 0.03).to(torch.bfloat16)
+    gout = torch.randn(1, M, n * C, generator=g)
+
+    def f_ref(s):  # bf16 matmul of the bf16-cast input, as autocast runs F
+        return (s.to(torch.bfloat16).float() @ fw.float().t()).to(torch.bfloat16).float()
+
+    xr = x.clone().requires_grad_(True)
+    pr = {k: v.clone().requires_grad_(True) for k, v in p.items()}
+    ref = R.mhc_full_forward(xr, pr, f_ref, n, C, sinkhorn_iters=20)["out"]
+    (ref * gout).sum().backward()
+
+    mod = MHCConnection_Fused(n, C, sinkhorn_iters=20).to(dev)
+    with torch.no_grad():
+        for k, v in p.items():
+            getattr(mod, k).copy_(v)
+    fwd_t = fw.t().contiguous().to(dev)
+    xd = x.to(dev).requires_grad_(True)
+    out = mod(xd, lambda s: s.to(torch.bfloat16) @ fwd_t)
+    assert out.dtype == F32
+    (out * gout.to(dev)).sum().backward()
+    # F's bf16 output and input cast bound the agreement to bf16 rounding of F.
+    assert maxrel(ref, out) <= 1e-2
+    assert maxrel(xr.grad, xd.grad) <= 1e-2
+    assert maxrel(pr["phi_weight"].grad, mod.phi_weight.grad) <= 1e-2
+    for k in ("bias_pre", "bias_post", "bias_res"):
+        assert maxrel(pr[k].grad, getattr(mod, k).grad) <= 1e-2, k
