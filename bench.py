@@ -22,7 +22,9 @@ config-2 shape in bf16 on the host cores, with fp32 and config 1 beside it);
 `backward`: the four backward launches of one
 connection at config 2 (post, Sinkhorn, per-token pre phase, weight
 gradients), each against its algorithmic bytes, plus the fwd + bwd tokens/s of
-the connection (F excluded); `other_configs`: the same kernel pair at config
+the connection (F excluded); `fp32_layout`: the forward and backward launches
+at the config-2 shape in the reference trainers' layout (fp32 stream, phi and
+gates, bf16 F under autocast); `other_configs`: the same kernel pair at config
 5's n = 8 shape and config 4's 64-token shape; and the end-to-end model
 figures: `e2e_prefill` (config 3), `e2e_decode` (config 4, eager and
 HIP-graph replay) and `e2e_prefill_moe` (config 5).
@@ -819,6 +821,7 @@ def main():
     bw5 = bench_backward(n=8, M=8192)
     bw5["config"] = "C5 shape: 8192 tokens, n=8, C=768, bf16"
     line["backward_c5"] = bw5
+    line["fp32_layout"] = bench_layout32()
     line["other_configs"] = isolated_configs(max(10, args.steps // 2), max(3, args.warmup // 2))
     if not args.no_e2e:
         line["e2e_prefill"] = e2e_prefill()

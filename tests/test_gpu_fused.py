@@ -5,7 +5,9 @@
   each forced through mhc_pre_token_threshold, against the CPU oracle at the
   BASELINE bars (1e-2 bf16), on the batch sizes either side of the switch.
 * mhc_pre_norm_fwd / mhc_pre_nohres_norm_fwd / mhc_head_norm_fwd: every
-  output but the main one equals the plain entry point's bit for bit, and the
+  output but the main one equals the plain entry point's bit for bit (within
+  1e-5 for fp32 streams, whose plain call takes the split-operand kernel and
+  normed call the VALU kernel), and the
   main output is RMSNorm(plain output) (the reference applies nn.RMSNorm to
   the rounded pre-aggregate, model/model_minimind.py:330, :336, :367-370),
   computed here in fp32 by torch: within one rounding step of the stream
@@ -170,10 +172,20 @@ def test_fused_norm_matches_plain_then_rmsnorm(dev, kind, n, C, M, dtype, gain_f
     print(f"norm {kind} n={n} C={C} M={M} {dtype} gain_f32={gain_f32}", flush=True)
     plain = _run(kind, x, p, n, C, dev)
     fused = _run(kind, x, p, n, C, dev, norm=(w, eps))
+    # fp32 streams: the plain call runs the split-operand MFMA kernel, the normed
+    # call the fp32 VALU kernel (the split kernel has no norm epilogue), so the
+    # two agree at the fp32 bar rather than bit for bit.
+    split = dtype == torch.float32 and kind != "head" and n in (1, 2, 4)
     for k, v in plain.items():
         if k != "sub_in" and v is not None:
-            assert torch.equal(v, fused[k]), k
-    _assert_rounded_close(fused["sub_in"], _norm_ref(plain["sub_in"], w, eps), dtype)
+            if split:
+                assert maxrel(v, fused[k]) <= 1e-5, k
+            else:
+                assert torch.equal(v, fused[k]), k
+    if split:  # different pre-aggregates upstream: the fp32 max-norm bar
+        assert maxrel(_norm_ref(plain["sub_in"], w, eps), fused["sub_in"]) <= 1e-5
+    else:
+        _assert_rounded_close(fused["sub_in"], _norm_ref(plain["sub_in"], w, eps), dtype)
 
 
 @pytest.mark.parametrize("M", [1, 17, 300])
