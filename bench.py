@@ -37,6 +37,7 @@ from profiles/traffic_mhc_fwd_c2.txt (the rocprofv3 summary committed beside
 the kernel-trace summary); traffic is null when that file is absent.
 
 Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--no-e2e] [--no-cpu]
+       python bench.py --section fp32-layout|other-configs   (one section only)
        python bench.py --traffic     (counter passes only; prints nothing)
        python bench.py --e2e-only [prefill|decode|moe]   (end-to-end model figures only)
 """
@@ -730,6 +731,9 @@ def main():
                     choices=["all", "prefill", "decode", "moe"],
                     help="run only the end-to-end model figures (configs 3, 4, 5, or one of "
                          "them) and print them as one JSON line")
+    ap.add_argument("--section", choices=["fp32-layout", "other-configs"], default=None,
+                    help="run only the fp32-layout launches or the isolated config-4 / config-5 "
+                         "kernel pairs and print them as one JSON line (for profiler runs)")
     ap.add_argument("--mfma-kernels", action="store_true",
                     help="with --traffic: also run the config-2 backward MFMA kernels and the "
                          "config-5 (n = 8) pre phase once")
@@ -746,6 +750,13 @@ def main():
 
     if args.traffic:
         traffic_passes(args.vector_pre, args.mfma_kernels)
+        return
+    if args.section == "fp32-layout":
+        print(json.dumps({"fp32_layout": bench_layout32()}), flush=True)
+        return
+    if args.section == "other-configs":
+        print(json.dumps({"other_configs": isolated_configs(max(10, args.steps // 2),
+                                                            max(3, args.warmup // 2))}), flush=True)
         return
     if args.e2e_only:
         runs = {"prefill": ("e2e_prefill", e2e_prefill), "decode": ("e2e_decode", e2e_decode),

@@ -372,6 +372,16 @@ int mhc_pre_bwd_weights_noalloc(const void* x, int x_dtype, const float* inv_rms
                                 hipStream_t stream);
 
 /*
+ * Largest Sinkhorn iteration count mhc_sinkhorn_bwd accepts for n (64 for
+ * n in {2, 4, 8}, 30 otherwise; 0 for n outside [1, 16]).  The forward
+ * kernels take any count; a caller that will need gradients checks this
+ * before the forward.  No reference counterpart: the reference's backward
+ * recomputes the forward under autograd (model/mhc_fused.py:131-137) and has
+ * no limit.
+ */
+int mhc_sinkhorn_bwd_max_iters(int n);
+
+/*
  * Sinkhorn-Knopp backward: g_in = d output / d input of mhc_sinkhorn_fwd's
  * schedule, by recomputing the forward iterates (fp32).  n <= 16;
  * iters <= 64 for n in {2, 4, 8}, <= 30 otherwise (the iterates live in LDS).

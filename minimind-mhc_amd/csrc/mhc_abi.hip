@@ -547,14 +547,19 @@ int mhc_pre_bwd_weights_noalloc(const void* x, int x_dtype, const float* inv_rms
                        ranges > 64 ? 64 : (int)ranges, stream, fn);
 }
 
+int mhc_sinkhorn_bwd_max_iters(int n) {
+  if (n < 1 || n > 16) return 0;
+  return n == 2 || n == 4 || n == 8 ? 64 : 30;  // the trajectory lives in 64 KiB of LDS per wave
+}
+
 int mhc_sinkhorn_bwd(const void* m_in, int in_dtype, const void* g_out, int g_dtype, void* g_in,
                      int gi_dtype, int64_t batch, int n, int iters, float eps, hipStream_t stream) {
   const char* fn = "mhc_sinkhorn_bwd";
   if (batch < 0) return fail(hipErrorInvalidValue, "%s: batch must be >= 0", fn);
   if (n < 1 || n > 16) return fail(hipErrorInvalidValue, "%s: n must be in [1, 16] (got %d)", fn, n);
-  const bool lanes = n == 2 || n == 4 || n == 8;  // trajectory in 64 KiB of LDS per wave
-  if (iters > (lanes ? 64 : 30))
-    return fail(hipErrorInvalidValue, "%s: iters must be <= %d for n = %d (got %d)", fn, lanes ? 64 : 30, n, iters);
+  const int cap = mhc_sinkhorn_bwd_max_iters(n);
+  if (iters > cap)
+    return fail(hipErrorInvalidValue, "%s: iters must be <= %d for n = %d (got %d)", fn, cap, n, iters);
   if (!dtype_ok(in_dtype) || !dtype_ok(g_dtype) || !dtype_ok(gi_dtype)) return fail(hipErrorInvalidValue, "%s: bad dtype", fn);
   if (batch > kMaxBlocks) return fail(hipErrorInvalidValue, "%s: batch too large", fn);
   if (batch == 0) return 0;

@@ -84,6 +84,7 @@ _SIGNATURES = {
                                          _P, _P, _P, _P, _P, _P,
                                          _I64, _I, _I, _I, _P]),
     "mhc_sinkhorn_bwd": (_I, [_P, _I, _P, _I, _P, _I, _I64, _I, _I, _F, _P]),
+    "mhc_sinkhorn_bwd_max_iters": (_I, [_I]),
 }
 
 ABI_VERSION = 5

@@ -7,12 +7,40 @@ current stream.  Inputs are made contiguous, as the reference's Functions do
 """
 from __future__ import annotations
 
+import threading
 import weakref
 from typing import Optional
 
 import torch
 
 from . import _hip as H
+
+_GRAD = threading.local()
+
+
+class GradAwareFunction(torch.autograd.Function):
+    """An autograd Function whose forward can tell whether the caller had grad
+    mode on.  ctx.needs_input_grad follows requires_grad alone, also under
+    torch.no_grad(), so a forward that keys on it alone would save tensors,
+    write backward-only outputs and repack trainable weights on every
+    inference call."""
+
+    @classmethod
+    def apply(cls, *args, **kwargs):
+        prev = getattr(_GRAD, "on", True)
+        _GRAD.on = torch.is_grad_enabled()
+        try:
+            return super().apply(*args, **kwargs)
+        finally:
+            _GRAD.on = prev
+
+
+def grad_wanted(ctx, index: Optional[int] = None) -> bool:
+    """Inside a GradAwareFunction's forward: whether a gradient of any input
+    (or of input `index`) will be asked for."""
+    if not getattr(_GRAD, "on", True):
+        return False
+    return any(ctx.needs_input_grad) if index is None else bool(ctx.needs_input_grad[index])
 
 
 class PhiPack:
@@ -58,7 +86,7 @@ class PhiPack:
         split hi / lo image for an fp32 phi (kernels for fp32 streams).
         training: whether phi trains in this call; default grad mode and
         phi.requires_grad (inside an autograd Function's forward, where grad
-        mode is off, pass ctx.needs_input_grad for phi)."""
+        mode is off, pass grad_wanted(ctx, <phi's index>))."""
         lib = H.load()
         if phi.dtype == torch.bfloat16:
             nbytes = lib.mhc_phi_packed_bytes(n, C, self.mode)
@@ -442,6 +470,16 @@ def pre_bwd_weights(x2, inv_rms, mixes, g_raw, phi, alphas, n, C, mode):
         H.stream(dev))
     H.check(rc, "mhc_pre_bwd_weights")
     return g_phi, g_alpha, g_bias
+
+
+def check_sinkhorn_bwd_iters(n: int, iters: int) -> None:
+    """Raise, before a forward whose Sinkhorn will need a gradient, when the
+    backward kernel cannot take `iters` iterations for n (it would otherwise
+    fail only at backward)."""
+    cap = int(H.load().mhc_sinkhorn_bwd_max_iters(int(n)))
+    if iters > cap:
+        raise ValueError(f"mhc_amd: sinkhorn_iters={iters} exceeds what the Sinkhorn backward "
+                         f"takes for n={n} ({cap}); train with sinkhorn_iters <= {cap}")
 
 
 def sinkhorn_bwd(m: torch.Tensor, g: torch.Tensor, iters: int, eps: float,

@@ -40,7 +40,7 @@ def norm_eps(norm: nn.RMSNorm, x: torch.Tensor) -> float:
     return float(norm.eps) if norm.eps is not None else float(torch.finfo(x.dtype).eps)
 
 
-class _StreamExpandFn(torch.autograd.Function):
+class _StreamExpandFn(_ops.GradAwareFunction):
     @staticmethod
     def forward(ctx, x, n):
         ctx.n = n
@@ -73,15 +73,15 @@ class StreamExpand(nn.Module):
         return self(in_norm(x))
 
 
-class _MHCHeadFn(torch.autograd.Function):
+class _MHCHeadFn(_ops.GradAwareFunction):
     """MHCHead forward on the HIP kernel (model/mhc_common.py:311-400)."""
 
     @staticmethod
     def forward(ctx, x_flat, w_phi, alpha, bias, pre_eps, rms_eps, n, c, packed=None):
         B, L, NC = x_flat.shape
-        train = any(ctx.needs_input_grad)
+        train = _ops.grad_wanted(ctx)
         if packed is None and n > 1:  # called without the module's pack
-            packed = _ops.packed_phi(w_phi, n, c, H.MODE_HEAD, training=ctx.needs_input_grad[1])
+            packed = _ops.packed_phi(w_phi, n, c, H.MODE_HEAD, training=_ops.grad_wanted(ctx, 1))
         out, inv, mix = _ops.head(x_flat, w_phi, packed, alpha, bias, n, c, pre_eps, rms_eps,
                                   want_saved=train)
         if train:
@@ -102,14 +102,14 @@ class _MHCHeadFn(torch.autograd.Function):
                 g_b[0].to(bias.dtype).view(bias.shape), None, None, None, None, None)
 
 
-class _RMSFn(torch.autograd.Function):
+class _RMSFn(_ops.GradAwareFunction):
     """y = x * rsqrt(mean(x^2) + eps), no gain (MHCHead with n == 1)."""
 
     @staticmethod
     def forward(ctx, x_flat, eps):
         B, L, C = x_flat.shape
         out, inv, _ = _ops.head(x_flat, None, None, None, None, 1, C, 0.0, eps,
-                                want_saved=any(ctx.needs_input_grad))
+                                want_saved=_ops.grad_wanted(ctx))
         if inv is not None:
             ctx.save_for_backward(x_flat.detach().contiguous().view(B * L, C), inv)
         return out.view(B, L, C)

@@ -31,12 +31,14 @@ def _is_pow2(n: int) -> bool:
 
 # ---------------------------------------------------------------- Sinkhorn op
 
-class _SinkhornFn(torch.autograd.Function):
+class _SinkhornFn(_ops.GradAwareFunction):
     """Sinkhorn-Knopp forward on the HIP kernel; backward by recompute
     (model/mhc_fused.py:96-137)."""
 
     @staticmethod
     def forward(ctx, M: torch.Tensor, iters: int, eps: float) -> torch.Tensor:
+        if _ops.grad_wanted(ctx, 0):
+            _ops.check_sinkhorn_bwd_iters(M.shape[-1], iters)
         out = _ops.sinkhorn(M, iters, eps)
         ctx.save_for_backward(M)
         ctx.iters, ctx.eps = iters, eps
@@ -74,7 +76,7 @@ def _pre_full_grads(x2, w, alphas, biases, inv, mixes, n, c, post_mult, pre_eps,
     return out
 
 
-class _PrePhaseFullFn(torch.autograd.Function):
+class _PrePhaseFullFn(_ops.GradAwareFunction):
     """Pre phase -> (sublayer_in, h_pre, h_post, h_res_raw), h_res_raw before
     Sinkhorn, as the reference Function (model/mhc_fused.py:571-717)."""
 
@@ -82,13 +84,15 @@ class _PrePhaseFullFn(torch.autograd.Function):
     def forward(ctx, x_flat, w_phi, alpha_pre, bias_pre, alpha_post, bias_post,
                 alpha_res, bias_res, post_mult, pre_eps, rms_eps, n, c):
         B, L, NC = x_flat.shape
-        packed = _ops.packed_phi(w_phi, n, c, H.MODE_FULL, training=ctx.needs_input_grad[1])
+        train = _ops.grad_wanted(ctx)
+        packed = _ops.packed_phi(w_phi, n, c, H.MODE_FULL, training=_ops.grad_wanted(ctx, 1))
         o = _ops.pre_full(x_flat, w_phi, packed, alpha_pre, bias_pre, alpha_post, bias_post,
                           alpha_res, bias_res, n, c, post_mult, pre_eps, rms_eps, 0, 0.0,
-                          sinkhorn=False, want_h_pre=True, want_raw=True, want_saved=True)
-        ctx.save_for_backward(x_flat.detach().contiguous().view(B * L, NC), w_phi, alpha_pre,
-                              bias_pre, alpha_post, bias_post, alpha_res, bias_res,
-                              o["inv_rms"], o["mixes_raw"])
+                          sinkhorn=False, want_h_pre=True, want_raw=True, want_saved=train)
+        if train:
+            ctx.save_for_backward(x_flat.detach().contiguous().view(B * L, NC), w_phi, alpha_pre,
+                                  bias_pre, alpha_post, bias_post, alpha_res, bias_res,
+                                  o["inv_rms"], o["mixes_raw"])
         ctx.cfg = (n, c, float(post_mult), float(pre_eps), (B, L, NC))
         return (o["sub_in"].view(B, L, c), o["h_pre"].view(B, L, n),
                 o["h_post"].view(B, L, n), o["h_res_raw"].view(B, L, n, n))
@@ -103,7 +107,7 @@ class _PrePhaseFullFn(torch.autograd.Function):
                 None, None, None, None, None)
 
 
-class _PreSinkhornFn(torch.autograd.Function):
+class _PreSinkhornFn(_ops.GradAwareFunction):
     """Fused pre phase + Sinkhorn -> (sublayer_in, h_post, h_res): the single
     launch MHCConnection_Fused.forward uses in place of the reference's
     _PrePhaseFullFn + sinkhorn_normalize pair (model/mhc_fused.py:820-830)."""
@@ -112,7 +116,9 @@ class _PreSinkhornFn(torch.autograd.Function):
     def forward(ctx, x_flat, w_phi, packed, alpha_pre, bias_pre, alpha_post, bias_post,
                 alpha_res, bias_res, post_mult, pre_eps, rms_eps, n, c, iters, sk_eps):
         B, L, NC = x_flat.shape
-        train = any(ctx.needs_input_grad)
+        train = _ops.grad_wanted(ctx)
+        if train:
+            _ops.check_sinkhorn_bwd_iters(n, iters)
         o = _ops.pre_full(x_flat, w_phi, packed, alpha_pre, bias_pre, alpha_post, bias_post,
                           alpha_res, bias_res, n, c, post_mult, pre_eps, rms_eps, iters, sk_eps,
                           sinkhorn=True, want_raw=train, want_saved=train)
@@ -139,14 +145,14 @@ class _PreSinkhornFn(torch.autograd.Function):
         return (g[0], g[1], None, *g[2:], None, None, None, None, None, None, None)
 
 
-class _PostPhaseFullFn(torch.autograd.Function):
+class _PostPhaseFullFn(_ops.GradAwareFunction):
     """out = H_res . x + H_post (x) F_out (model/mhc_fused.py:720-772)."""
 
     @staticmethod
     def forward(ctx, x_flat, h_res, h_post, f_out, n, c):
         B, L, NC = x_flat.shape
         out = _ops.post(x_flat, h_res, h_post, f_out, n, c)
-        if any(ctx.needs_input_grad):
+        if _ops.grad_wanted(ctx):
             ctx.save_for_backward(x_flat.detach().contiguous().view(B * L, NC), h_res, h_post,
                                   f_out)
         ctx.cfg = (n, c, (B, L, NC))

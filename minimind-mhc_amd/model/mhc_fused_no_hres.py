@@ -22,16 +22,16 @@ def _is_pow2(n: int) -> bool:
     return n >= 1 and (n & (n - 1)) == 0
 
 
-class _PrePhaseFn(torch.autograd.Function):
+class _PrePhaseFn(_ops.GradAwareFunction):
     """Pre phase -> (sublayer_in, h_pre, h_post) (model/mhc_fused_no_hres.py:397-529)."""
 
     @staticmethod
     def forward(ctx, x_flat, w_phi, alpha_pre, bias_pre, alpha_post, bias_post,
                 post_mult, pre_eps, rms_eps, n, c, packed=None):
         B, L, NC = x_flat.shape
-        train = any(ctx.needs_input_grad)
+        train = _ops.grad_wanted(ctx)
         if packed is None:  # called as the reference's Function, without the module's pack
-            packed = _ops.packed_phi(w_phi, n, c, H.MODE_NOHRES, training=ctx.needs_input_grad[1])
+            packed = _ops.packed_phi(w_phi, n, c, H.MODE_NOHRES, training=_ops.grad_wanted(ctx, 1))
         o = _ops.pre_nohres(x_flat, w_phi, packed, alpha_pre, bias_pre, alpha_post, bias_post,
                             n, c, post_mult, pre_eps, rms_eps, want_h_pre=True, want_saved=train)
         if train:
@@ -56,14 +56,14 @@ class _PrePhaseFn(torch.autograd.Function):
                 None, None, None, None, None, None)
 
 
-class _PostPhaseFn(torch.autograd.Function):
+class _PostPhaseFn(_ops.GradAwareFunction):
     """out = x + H_post (x) F_out (model/mhc_fused_no_hres.py:532-581)."""
 
     @staticmethod
     def forward(ctx, x_flat, h_post, f_out, n, c):
         B, L, NC = x_flat.shape
         out = _ops.post(x_flat, None, h_post, f_out, n, c)
-        if any(ctx.needs_input_grad):
+        if _ops.grad_wanted(ctx):
             ctx.save_for_backward(h_post, f_out)
         ctx.cfg = (n, c, (B, L, NC))
         return out.view(B, L, NC)

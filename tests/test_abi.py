@@ -56,6 +56,15 @@ def test_packed_sizes(lib):
     assert lib.mhc_phi_packed_bytes(1, 768, 2) == 0                      # head n=1 is RMSNorm
 
 
+def test_sinkhorn_bwd_max_iters(lib):
+    assert lib.mhc_sinkhorn_bwd_max_iters(4) == 64
+    assert lib.mhc_sinkhorn_bwd_max_iters(8) == 64
+    assert lib.mhc_sinkhorn_bwd_max_iters(3) == 30
+    assert lib.mhc_sinkhorn_bwd_max_iters(16) == 30
+    assert lib.mhc_sinkhorn_bwd_max_iters(0) == 0
+    assert lib.mhc_sinkhorn_bwd_max_iters(17) == 0
+
+
 def test_split_packed_sizes(lib):
     # fp32 split image: 16-column tiles of 8 features (hi | lo), n in {1, 2, 4}
     assert lib.mhc_phi_split_bytes(4, 768, 0) == 4 * 24 * 3 * 64 * 16   # FD 24 -> 3 tiles

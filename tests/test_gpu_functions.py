@@ -222,3 +222,24 @@ def test_frozen_connection_trainable_sublayer_gets_gradients(dev, kind):
     assert ld.weight.grad is not None
     assert maxrel(lr.weight.grad, ld.weight.grad) <= 1e-4
     assert maxabs(ref, out) <= 1e-5 * ref.abs().max().item()
+
+
+def test_sinkhorn_iterations_beyond_backward_limit(dev):
+    """A Sinkhorn count the backward kernel cannot take fails at the forward that
+    would need it (a clear error instead of one at backward), and runs in
+    inference."""
+    n, C, M = 4, 64, 8
+    cap = H.load().mhc_sinkhorn_bwd_max_iters(n)
+    mod = MHCConnection_Fused(n, C, sinkhorn_iters=cap + 1).to(dev)
+    x = torch.randn(1, M, n * C, device=dev)
+    with torch.no_grad():
+        out = mod(x, lambda z: z)
+    assert torch.isfinite(out).all()
+    with pytest.raises(ValueError, match="sinkhorn_iters"):
+        mod(x, lambda z: z)
+    m = torch.randn(3, n, n, device=dev, requires_grad=True)
+    with pytest.raises(ValueError, match="sinkhorn_iters"):
+        sinkhorn_normalize(m, cap + 1)
+    ok = MHCConnection_Fused(n, C, sinkhorn_iters=cap).to(dev)
+    ok(x, lambda z: z).sum().backward()
+    assert ok.phi_weight.grad is not None
