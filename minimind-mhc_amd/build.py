@@ -2,8 +2,9 @@
 
 Each csrc/*.hip file is compiled separately (in parallel) with hipcc for
 gfx950 only, then linked into one shared object next to this file.  Packed
-FP32 instructions are disabled for device code (-packed-fp32-ops); hipcc's
-host pass prints a harmless "not a recognized feature" warning for it.
+FP32 instructions are disabled for device code (-packed-fp32-ops), and so is
+the accumulate-in-place dot2 encoding (-dot13-insts, see COMMON_FLAGS); hipcc's
+host pass prints a harmless "not a recognized feature" warning for each.
 
 Usage:  python minimind-mhc_amd/build.py [-v]
 """
@@ -31,6 +32,9 @@ COMMON_FLAGS = [
     "-std=c++17",
     "-fPIC",
     "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops",
+    # v_dot2_f32_bf16 (VOP3P) instead of v_dot2c_f32_bf16: a product into a
+    # zero accumulator is one instruction, not a v_mov of 0 plus the dot2c.
+    "-Xclang", "-target-feature", "-Xclang", "-dot13-insts",
     "-Wall",
     "-Wno-unused-function",
     f"-I{REPO_DIR / 'include'}",
@@ -42,9 +46,9 @@ def _compile(src: Path, verbose: bool) -> Path:
     obj = BUILD_DIR / (src.stem + ".o")
     cmd = [HIPCC, *COMMON_FLAGS, "-c", str(src), "-o", str(obj)]
     res = subprocess.run(cmd, capture_output=True, text=True)
-    # hipcc's host pass does not know the packed-fp32 feature name; drop that noise.
-    noise = "'-packed-fp32-ops' is not a recognized feature"
-    err = "\n".join(l for l in res.stderr.splitlines() if noise not in l)
+    # hipcc's host pass does not know these device feature names; drop that noise.
+    noise = ("'-packed-fp32-ops' is not a recognized feature", "'-dot13-insts' is not a recognized feature")
+    err = "\n".join(l for l in res.stderr.splitlines() if not any(n in l for n in noise))
     if res.returncode != 0:
         raise RuntimeError(f"hipcc failed for {src.name}:\n{' '.join(cmd)}\n{err}")
     if verbose and err.strip():

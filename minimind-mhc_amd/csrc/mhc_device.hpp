@@ -90,12 +90,13 @@ __device__ __forceinline__ void buf_store16(__amdgpu_buffer_rsrc_t r, uint32_t o
 __device__ __forceinline__ float bf16lo(uint32_t u) { return __uint_as_float(u << 16); }
 __device__ __forceinline__ float bf16hi(uint32_t u) { return __uint_as_float(u & 0xffff0000u); }
 
-// Round-to-nearest-even fp32 -> bf16 pair (lowers to v_cvt_pk_bf16_f32 on gfx950).
+// Round-to-nearest-even fp32 -> bf16 pair: one v_cvt_pk_bf16_f32 on gfx950.
+// (Two scalar (__bf16) conversions joined by shifts compile to two
+// v_cvt_pk_bf16_f32 with a zero operand, a shift and an SDWA or.)
+typedef float f32x2_t __attribute__((ext_vector_type(2)));
 __device__ __forceinline__ uint32_t pack_bf16x2(float a, float b) {
-  __bf16 x = (__bf16)a;
-  __bf16 y = (__bf16)b;
-  return (uint32_t)__builtin_bit_cast(uint16_t, x) |
-         ((uint32_t)__builtin_bit_cast(uint16_t, y) << 16);
+  const f32x2_t v = {a, b};
+  return __builtin_bit_cast(uint32_t, __builtin_convertvector(v, bf16x2_t));
 }
 
 __device__ __forceinline__ uint16_t f32_to_bf16_bits(float a) {
@@ -178,6 +179,17 @@ __device__ __forceinline__ float gate_post(float m, float alpha, float bias, flo
 // h_res_raw: alpha * m + bias (Sinkhorn then runs in fp32 on this value)
 __device__ __forceinline__ float gate_res(float m, float alpha, float bias, int dt) {
   return round_to(__fadd_rn(round_to(__fmul_rn(round_to(m, dt), alpha), dt), bias), dt);
+}
+
+// ------------------------------------------------------- x_norm on packed bf16
+// bf16(x * inv) for the 8 columns of one 16-byte chunk: the fp32 product
+// rounded to bf16, as the reference's x_norm = (x.float() * inv_rms).to(x.dtype)
+// (model/mhc_fused.py:845) rounds it.
+__device__ __forceinline__ U32x4 x_norm_chunk(const U32x4& v, float inv) {
+  U32x4 o;
+#pragma unroll
+  for (int j = 0; j < 4; ++j) o.v[j] = pack_bf16x2(bf16lo(v.v[j]) * inv, bf16hi(v.v[j]) * inv);
+  return o;
 }
 
 // ------------------------------------------- pre-aggregate on packed bf16

@@ -3,9 +3,10 @@
 // The generic kernel serves every (dtype, n, C) the MFMA instances do not:
 // fp32 / fp16 streams, fp32 phi, n == 16, C > 1024 or C % 8 != 0, and the
 // n == 1 MHCHead (plain RMSNorm).  One 256-thread workgroup per token; it is a
-// correctness path, not a tuned one.  x_norm = x * inv_rms and the projection
-// are fp32; the gates and the pre-aggregate round where the reference's torch
-// ops round (model/mhc_fused.py:843-859, model/mhc_fused_no_hres.py:364-386,
+// correctness path, not a tuned one.  x_norm = x * inv_rms is rounded to the
+// stream dtype and the projection accumulates in fp32; the gates and the
+// pre-aggregate round where the reference's torch ops round
+// (model/mhc_fused.py:843-859, model/mhc_fused_no_hres.py:364-386,
 // model/mhc_common.py:298-308).
 #include "mhc_pre_group.hpp"
 
@@ -206,7 +207,8 @@ __global__ __launch_bounds__(kGenThreads) void pre_generic_kernel(PreArgs a) {
 #pragma unroll
     for (int j = 0; j < kGenChunk; ++j) p[j] = 0.f;
     for (int64_t k = tid; k < NC; k += kGenThreads) {
-      const float xn = ld_any(a.x, xb + k, xdt) * inv;
+      // x_norm rounded to the stream dtype (model/mhc_fused.py:845)
+      const float xn = round_to(ld_any(a.x, xb + k, xdt) * inv, xdt);
       const int64_t wb = k * FD + f0;
 #pragma unroll
       for (int j = 0; j < kGenChunk; ++j)

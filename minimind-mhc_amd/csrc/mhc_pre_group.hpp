@@ -180,43 +180,17 @@ __global__ __launch_bounds__(kGrpWaves * 64) void pre_group_kernel(PreArgs a, in
   __syncthreads();  // x rows, zero block and parameters visible
 
   // ---- projection: MFMA over this wave's blocks --------------------------------
-  f32x4_t acc[NT];
-#pragma unroll
-  for (int nt = 0; nt < NT; ++nt) acc[nt] = f32x4_t{0.f, 0.f, 0.f, 0.f};
-  float ss = 0.f;
-#pragma unroll
-  for (int b = 0; b < P::NB; ++b) {
+  // Lane (g, r) of block b: row r, columns c0 + 8g .. + 7 of stream i; zeros
+  // past the group's rows or past C.
+  auto a_of = [&](int b) -> U32x4 {
     int i, cb;
     const bool live = block_of(b, i, cb);
     const int c0 = cb * kCBlock;
-    // Lane (g, r): row r, columns c0 + 8g .. + 7 of stream i; zeros past the
-    // group's rows or past C.
     const U32x4* src = live && r < G && c0 + g * 8 < C
                            ? reinterpret_cast<const U32x4*>(&sh.xs[r][i * C + c0 + 8 * g])
                            : &sh.zero;
-    const U32x4 v = *src;
-#pragma unroll
-    for (int j = 0; j < 4; ++j) ss = dot2_bf16(v.v[j], v.v[j], ss);
-    const bf16x8_t av = __builtin_bit_cast(bf16x8_t, v);
-#pragma unroll
-    for (int nt = 0; nt < NT; ++nt)
-      acc[nt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(av, __builtin_bit_cast(bf16x8_t, wq[b % P::P][nt]),
-                                                         acc[nt], 0, 0, 0);
-    if (b + P::P < P::NB) issue(b + P::P);
-  }
-  ss += __shfl_xor(ss, 16, 64);
-  ss += __shfl_xor(ss, 32, 64);
-  // MFMA 16x16 result layout: lane l holds D[4*(l/16) + j][l % 16], j = 0..3.
-#pragma unroll
-  for (int nt = 0; nt < NT; ++nt)
-    if (nt * 16 + r < FD)
-#pragma unroll
-      for (int j = 0; j < 4; ++j)
-        if (4 * g + j < G) sh.acc[wave][4 * g + j][nt * 16 + r] = acc[nt][j];
-  if (g == 0 && r < G) sh.ss[wave][r] = ss;
-  __syncthreads();  // partials visible
-
-  // ---- gates straight from the partials, no further barrier ------------------
+    return *src;
+  };
   const float nc = (float)NC;
   auto inv_of = [&](int tt) {
     float sq = 0.f;
@@ -224,11 +198,64 @@ __global__ __launch_bounds__(kGrpWaves * 64) void pre_group_kernel(PreArgs a, in
     for (int w = 0; w < kGrpWaves; ++w) sq += sh.ss[w][tt];
     return 1.0f / sqrtf(sq / nc + a.rms_eps);
   };
+  // n <= 4: the projection runs on x_norm = bf16(x * inv_rms), rounded as the
+  // reference rounds it (model/mhc_fused.py:845), so the sums of squares come
+  // first (in pre_persist_kernel's order), then a barrier, then the MFMAs.
+  // n = 8 keeps pre_kstream_kernel's arithmetic: the MFMAs on x, the sums of
+  // squares beside them, and the fp32 result scaled by inv_rms.
+  constexpr bool XN = N <= 4;
+  float ss = 0.f;
+  if constexpr (XN) {
+#pragma unroll
+    for (int b = 0; b < P::NB; ++b) {
+      const U32x4 v = a_of(b);
+#pragma unroll
+      for (int j = 0; j < 4; ++j) ss = dot2_bf16(v.v[j], v.v[j], ss);
+    }
+    ss += __shfl_xor(ss, 16, 64);
+    ss += __shfl_xor(ss, 32, 64);
+    if (g == 0 && r < G) sh.ss[wave][r] = ss;
+    __syncthreads();  // sums of squares visible
+  }
+  const float inv_r = XN ? inv_of(r < G ? r : 0) : 1.0f;
+  f32x4_t acc[NT];
+#pragma unroll
+  for (int nt = 0; nt < NT; ++nt) acc[nt] = f32x4_t{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+  for (int b = 0; b < P::NB; ++b) {
+    const U32x4 v = a_of(b);
+    if constexpr (!XN) {
+#pragma unroll
+      for (int j = 0; j < 4; ++j) ss = dot2_bf16(v.v[j], v.v[j], ss);
+    }
+    const bf16x8_t av = __builtin_bit_cast(bf16x8_t, XN ? x_norm_chunk(v, inv_r) : v);
+#pragma unroll
+    for (int nt = 0; nt < NT; ++nt)
+      acc[nt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(av, __builtin_bit_cast(bf16x8_t, wq[b % P::P][nt]),
+                                                         acc[nt], 0, 0, 0);
+    if (b + P::P < P::NB) issue(b + P::P);
+  }
+  if constexpr (!XN) {
+    ss += __shfl_xor(ss, 16, 64);
+    ss += __shfl_xor(ss, 32, 64);
+  }
+  // MFMA 16x16 result layout: lane l holds D[4*(l/16) + j][l % 16], j = 0..3.
+#pragma unroll
+  for (int nt = 0; nt < NT; ++nt)
+    if (nt * 16 + r < FD)
+#pragma unroll
+      for (int j = 0; j < 4; ++j)
+        if (4 * g + j < G) sh.acc[wave][4 * g + j][nt * 16 + r] = acc[nt][j];
+  if (!XN && g == 0 && r < G) sh.ss[wave][r] = ss;
+  __syncthreads();  // partials visible
+
+  // ---- gates straight from the partials, no further barrier ------------------
+  // (n <= 4: the partials are already normalised; mix_of's scale is 1.)
   auto mix_of = [&](int tt, int f, float inv) {
     float sum = 0.f;
 #pragma unroll
     for (int w = 0; w < kGrpWaves; ++w) sum += sh.acc[w][tt][f];
-    return sum * inv;
+    return XN ? sum : sum * inv;
   };
   // Every wave: h_pre of the group's tokens, lane = (token, stream).
   const int sk_waves = MODE == kFull && a.h_res ? (G + P::SK_TOK - 1) / P::SK_TOK : 0;

@@ -26,7 +26,12 @@
 //   * with the RMSNorm epilogue the pre-aggregate chunks wait in LDS; after
 //     the rounds 16 lanes per token sum their squares, and a last pass
 //     scales, rounds and stores them.
-// Arithmetic and rounding points as pre_persist_kernel.
+// Arithmetic and rounding points as pre_persist_kernel, except x_norm: the
+// MFMAs run on x and the fp32 result is scaled by inv_rms, the way the
+// reference's fused kernel computes x_norm (model/mhc_fused.py:209-229), where
+// the PyTorch path rounds x * inv_rms to bf16 before its GEMM (:845).  Rounding
+// it here needs each row's sum of squares before the K loop, i.e. a second
+// pass over the tile's 393 KB of x, which the tile cannot hold on chip.
 //
 // Reference semantics: model/mhc_fused.py:163-268, :533-559, :47-56;
 // model/mhc_fused_no_hres.py:48-145; model/mhc_common.py:128-195.

@@ -2,9 +2,10 @@
 //
 // Per token, with x read from HBM exactly once:
 //   ss        = sum_k x[k]^2                    (fp32, bf16 dot2 on the held registers)
-//   acc[f]    = sum_k x[k] * phi[k, f]          (v_mfma_f32_16x16x32_bf16, fp32 accumulate)
 //   inv_rms   = 1 / sqrt(ss / (n*C) + rms_eps)
-//   mixes[f]  = acc[f] * inv_rms                (== (x * inv_rms) @ phi)
+//   xn[k]     = bf16(x[k] * inv_rms)            (the reference's x_norm, rounded to the
+//                                                stream dtype: model/mhc_fused.py:845)
+//   mixes[f]  = sum_k xn[k] * phi[k, f]         (v_mfma_f32_16x16x32_bf16, fp32 accumulate)
 //   gates     h_pre = sigmoid(a_pre*m + b_pre) + pre_eps
 //             h_post = post_mult * sigmoid(a_post*m + b_post)
 //             h_res_raw = a_res*m + b_res
@@ -43,10 +44,12 @@
 //     also wait for the prefetch.  Gate scalars and biases are read once, with
 //     branch-free loads issued before everything else, and kept in LDS as fp32.
 //
-// Per tile, one workgroup barrier (two with row staging):
-//   1. all waves: sum of squares + MFMA partial projections -> LDS (two slots,
-//      alternating per tile, so a fast wave may start the next tile's partials
-//      while others still read this tile's);
+// Per tile, two workgroup barriers (three with row staging):
+//   0. all waves: partial sums of squares of the tile's rows -> LDS;
+//   -- barrier --
+//   1. all waves: inv_rms of each row, x_norm, MFMA partial projections -> LDS
+//      (two slots, alternating per tile, so a fast wave may start the next
+//      tile's partials while others still read this tile's);
 //   -- barrier --
 //   2. waves 0..SK_WAVES-1 first run the Sinkhorn-Knopp iterations of the
 //      PREVIOUS tile (h_res logits from the other LDS slot): a ~20-step
@@ -220,6 +223,29 @@ __device__ __forceinline__ void persist_load_row(U32x4 (&xn)[KB][N], __amdgpu_bu
     xn[p / N][p % N] = buf_load16_nt<kNtSc1>(rsrc, (uint32_t)lane * 16u, (wave * RW::PW + p) * 1024);
 }
 
+// Row pieces [P0, P1) of the next tile, issued a share at a time from inside a
+// compute loop over KB column blocks: at(q) issues the q-th share.  Loads
+// spread through the step keep a steady amount in flight; a batch issued at
+// once stalls the issuing wave on the CU's full request queue, and one
+// issued at the end of a step leaves its latency exposed at the next.
+template <int N, int MODE, int KB, int P0, int P1>
+struct RowIssue {
+  U32x4 (&xn)[KB][N];
+  __amdgpu_buffer_rsrc_t rn;
+  int wave, lane;
+  __device__ __forceinline__ void at(int q) const {
+    using RW = PersistRow<N, MODE, KB>;
+    constexpr int PER = (P1 - P0 + KB - 1) / KB;
+#pragma unroll
+    for (int p = P0; p < P1; ++p)
+      if (p >= P0 + q * PER && p < P0 + (q + 1) * PER)
+        xn[p / N][p % N] = buf_load16_nt<kNtSc1>(rn, (uint32_t)lane * 16u, (wave * RW::PW + p) * 1024);
+  }
+};
+struct NoIssue {
+  __device__ __forceinline__ void at(int) const {}
+};
+
 // This wave's row pieces [P0, P1) of a tile -> LDS.
 template <int N, int MODE, int KB, int P0, int P1>
 __device__ __forceinline__ void persist_row_to_lds(unsigned char* xl, const U32x4 (&xn)[KB][N],
@@ -293,23 +319,48 @@ __device__ __forceinline__ void persist_load_part(U32x4 (&xr)[KB][N], __amdgpu_b
   }
 }
 
-// ---- phase 1: sum of squares (bf16 dot2) + projection partials (MFMA) -> LDS
-template <int N, int MODE, int KB, bool NORM>
-__device__ __forceinline__ void persist_partials(
+// ---- phase 0: this wave's partial sums of squares of the tile's rows -> LDS.
+// Lane (r, g) adds its chunks of row r in (block, stream) order, the four
+// lanes of a row are summed by a butterfly, and the eight waves' partials are
+// added in wave order (persist_inv_rms): every pre kernel that must agree bit
+// for bit with this one (pre_group_kernel) sums in this order.
+template <int N, int FD, int KB>
+__device__ __forceinline__ void persist_sumsq(PersistShared<N, FD>& sh, const U32x4 (&xr)[KB][N], int slot,
+                                              int lane, int wave) {
+  const int r = lane & 15;
+  const int g = lane >> 4;
+  float ss = 0.f;
+#pragma unroll
+  for (int q = 0; q < KB; ++q)
+#pragma unroll
+    for (int i = 0; i < N; ++i)
+#pragma unroll
+      for (int j = 0; j < 4; ++j) ss = dot2_bf16(xr[q][i].v[j], xr[q][i].v[j], ss);
+  ss += __shfl_xor(ss, 16, 64);
+  ss += __shfl_xor(ss, 32, 64);
+  if (g == 0) sh.ss[slot][wave][r] = ss;
+}
+
+// ---- phase 1: projection partials (MFMA) of x_norm -> LDS.  The A operand is
+// the row's x_norm = bf16(x * inv_rms), rounded as the reference's torch op
+// rounds it (model/mhc_fused.py:845: (x.float() * inv_rms).to(x.dtype)), so
+// the projection sums the same bf16 products the reference's GEMM sums.
+template <int N, int MODE, int KB, bool NORM, typename Issue = NoIssue>
+__device__ __forceinline__ void persist_project(
     const PreArgs& a, PersistShared<N, PersistPlan<N, MODE, KB>::FD>& sh, const U32x4 (&xr)[KB][N],
     const bf16x8_t (&wreg)[KB][N][PersistPlan<N, MODE, KB, NORM>::WR], const unsigned char* lds_w,
-    int slot, int lane, int wave) {
+    int slot, int lane, int wave, const Issue& issue = Issue()) {
   using P = PersistPlan<N, MODE, KB, NORM>;
   constexpr int FD = P::FD;
   constexpr int NT = P::NT;
   const int r = lane & 15;
   const int g = lane >> 4;
   const int NCB = (a.C + kCBlock - 1) / kCBlock;
+  const float inv = persist_inv_rms(sh, slot, r, (float)(N * a.C), a.rms_eps);
 
   f32x4_t acc[NT];
 #pragma unroll
   for (int nt = 0; nt < NT; ++nt) acc[nt] = f32x4_t{0.f, 0.f, 0.f, 0.f};
-  float ss = 0.f;
   // Column blocks past C hold zeros in x and in every phi copy (registers, LDS,
   // and the bounded L2 reads below), so every block runs unconditionally: no
   // branch splits the waits on the x buffers.
@@ -319,10 +370,7 @@ __device__ __forceinline__ void persist_partials(
     const int cb = wave + kPersistWaves * q;
 #pragma unroll
     for (int i = 0; i < N; ++i) {
-      const U32x4 v = xr[q][i];
-#pragma unroll
-      for (int j = 0; j < 4; ++j) ss = dot2_bf16(v.v[j], v.v[j], ss);
-      const bf16x8_t av = __builtin_bit_cast(bf16x8_t, v);
+      const bf16x8_t av = __builtin_bit_cast(bf16x8_t, x_norm_chunk(xr[q][i], inv));
 #pragma unroll
       for (int nt = 0; nt < NT; ++nt) {
         bf16x8_t bv;
@@ -343,21 +391,19 @@ __device__ __forceinline__ void persist_partials(
         acc[nt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(av, bv, acc[nt], 0, 0, 0);
       }
     }
+    issue.at(q);
   }
-  ss += __shfl_xor(ss, 16, 64);
-  ss += __shfl_xor(ss, 32, 64);
   // MFMA 16x16 result layout: lane l holds D[4*(l/16) + j][l % 16], j = 0..3.
 #pragma unroll
   for (int nt = 0; nt < NT; ++nt)
     if (nt * 16 + r < FD)
 #pragma unroll
       for (int j = 0; j < 4; ++j) sh.acc[slot][wave][4 * g + j][nt * 16 + r] = acc[nt][j];
-  if (g == 0) sh.ss[slot][wave][r] = ss;
 }
 
 // ---- gates ---------------------------------------------------------------
-// inv_rms of token tt and the reduced projection m = (sum_w partial) * inv of
-// feature f, from partials slot `slot`.
+// inv_rms of token tt and the reduced projection m = sum_w partial of feature
+// f (of x_norm, so already normalised), from partials slot `slot`.
 template <int N, int FD>
 __device__ __forceinline__ float persist_inv_rms(const PersistShared<N, FD>& sh, int slot, int tt,
                                                  float nc, float eps) {
@@ -368,12 +414,11 @@ __device__ __forceinline__ float persist_inv_rms(const PersistShared<N, FD>& sh,
 }
 
 template <int N, int FD>
-__device__ __forceinline__ float persist_mix(const PersistShared<N, FD>& sh, int slot, int tt, int f,
-                                             float inv) {
+__device__ __forceinline__ float persist_mix(const PersistShared<N, FD>& sh, int slot, int tt, int f) {
   float sum = 0.f;
 #pragma unroll
   for (int w = 0; w < kPersistWaves; ++w) sum += sh.acc[slot][w][tt][f];
-  return sum * inv;
+  return sum;
 }
 
 // h_pre of (token lane / N, stream lane % N) for every wave (lanes past TM*N
@@ -390,19 +435,19 @@ __device__ __forceinline__ float persist_pre_post(const PreArgs& a,
   if (lane < kTokTile * N) {
     const int tt = lane / N;
     const int i = lane % N;
-    const float inv = persist_inv_rms(sh, slot, tt, (float)(N * a.C), a.rms_eps);
-    const float m = persist_mix(sh, slot, tt, i, inv);
+    const float m = persist_mix(sh, slot, tt, i);
     hp = gate_pre(m, sh.prm[0], sh.prm[GP::kBiasPre + i], a.pre_eps, kBF16);
     if (wave == P::POST_WAVE) {
       const int64_t tk = tile * kTokTile + tt;
       const bool ok = tk < a.M;
       if (ok) {
         if (a.h_pre) st_any(a.h_pre, tk * N + i, kBF16, hp);
-        if (a.inv_rms && i == 0) a.inv_rms[tk] = inv;
+        if (a.inv_rms && i == 0)
+          a.inv_rms[tk] = persist_inv_rms(sh, slot, tt, (float)(N * a.C), a.rms_eps);
         if (a.mixes_raw) a.mixes_raw[tk * FD + i] = m;
       }
       if constexpr (MODE != kHead) {
-        const float mp = persist_mix(sh, slot, tt, N + i, inv);
+        const float mp = persist_mix(sh, slot, tt, N + i);
         const float hq = gate_post(mp, sh.prm[1], sh.prm[GP::kBiasPost + i], a.post_mult, kBF16);
         if (ok) {
           st_any(a.h_post, tk * N + i, kBF16, hq);
@@ -427,8 +472,7 @@ __device__ __forceinline__ void persist_res_gates(const PreArgs& a,
   for (int idx = idx0; idx < kTokTile * G; idx += P::GATE_LANES) {
     const int tt = idx / G;
     const int e = idx % G;
-    const float inv = persist_inv_rms(sh, slot, tt, (float)(N * a.C), a.rms_eps);
-    const float m = persist_mix(sh, slot, tt, 2 * N + e, inv);
+    const float m = persist_mix(sh, slot, tt, 2 * N + e);
     const float h = gate_res(m, sh.prm[2], sh.prm[GP::kBiasRes + e], kBF16);
     sh.hres[slot][idx] = h;
     const int64_t tk = tile * kTokTile + tt;
@@ -456,11 +500,12 @@ __device__ __forceinline__ void persist_sinkhorn(const PreArgs& a, const float* 
 // ---- phase 3: pre-aggregate from the held x registers.  With the norm the
 // chunks go to the lane's LDS slots and the token's sum of squares (of the
 // bf16-rounded values) to this wave's partial, for persist_norm_store.
-template <int N, int KB, bool NORM>
+template <int N, int KB, bool NORM, typename Issue = NoIssue>
 __device__ __forceinline__ void persist_preagg(const PreArgs& a, const U32x4 (&xr)[KB][N],
                                                const uint32_t (&hlo)[N], const uint32_t (&hhi)[N],
                                                int64_t tile, int lane, int wave,
-                                               PersistNorm<NORM, KB>& nsh, int slot) {
+                                               PersistNorm<NORM, KB>& nsh, int slot,
+                                               const Issue& issue = Issue()) {
   constexpr int TM = kTokTile;
   const int r = lane & 15;
   const int g = lane >> 4;
@@ -473,6 +518,7 @@ __device__ __forceinline__ void persist_preagg(const PreArgs& a, const U32x4 (&x
   float q2 = 0.f;
 #pragma unroll
   for (int q = 0; q < KB; ++q) {
+    issue.at(q);
     const int c0 = (wave + kPersistWaves * q) * kCBlock;
     const uint32_t lo = x_lane_off(q, wave, g, C);
     const U32x4 pk = preagg_chunk<N>(xr[q], hlo, hhi);
@@ -532,8 +578,8 @@ __device__ __forceinline__ void persist_norm_store(const PreArgs& a, const Persi
   }
 }
 
-// One tile (partials slot and h_res slot `slot`); the next tile's loads go
-// into xn in three batches along the way.
+// One tile (sums-of-squares, partials and h_res slot `slot`); the next tile's
+// loads go into xn in three batches along the way.
 template <int N, int MODE, int KB, bool NORM>
 __device__ __forceinline__ void persist_step(
     const PreArgs& a, PersistShared<N, PersistPlan<N, MODE, KB>::FD>& sh, PersistNorm<NORM, KB>& nsh,
@@ -546,9 +592,11 @@ __device__ __forceinline__ void persist_step(
   const auto rn = x_tile_rsrc(static_cast<const uint16_t*>(a.x), tile + gridDim.x, ntiles, a.M,
                               N * a.C);
   persist_load_part<N, KB, 0, P::B1>(xn, rn, a.C, wave, r, g);
-  persist_partials<N, MODE, KB, NORM>(a, sh, xr, wreg, lds_w, slot, lane, wave);
-  __syncthreads();
+  persist_sumsq(sh, xr, slot, lane, wave);
+  __syncthreads();  // sums of squares visible
   persist_load_part<N, KB, P::B1, P::B2>(xn, rn, a.C, wave, r, g);
+  persist_project<N, MODE, KB, NORM>(a, sh, xr, wreg, lds_w, slot, lane, wave);
+  __syncthreads();  // partials visible
   if constexpr (MODE == kFull) {
     if (wave < P::SK_WAVES && prev >= 0 && a.h_res)
       persist_sinkhorn<N>(a, sh.hres[slot ^ 1], prev, tid);
@@ -576,11 +624,11 @@ __device__ __forceinline__ void persist_step(
 
 // One tile with row staging: xn holds the tile in row layout (its loads were
 // issued during the previous step); it goes to LDS, xn takes the next tile's
-// loads in three batches along the step (at its start, after the partials
-// barrier, after the pre-aggregate), and the operand registers xr are read
-// back from LDS.  A second barrier orders the LDS writes before the reads;
-// the previous step's partials barrier orders this step's writes after every
-// wave's previous reads.  (Overlapping two tiles' loads, with the LDS tile
+// loads in three parts along the step (at its start, spread through the
+// projection, spread through the pre-aggregate), and the operand registers xr
+// are read back from LDS.  One more barrier orders the LDS writes before the
+// reads; the previous step's partials barrier orders this step's writes after
+// every wave's previous reads.  (Overlapping two tiles' loads, with the LDS tile
 // taking the next tile's first batch once read, measured slower: the extra
 // loads in flight stall the issuing waves.)
 template <int N, int MODE, int KB>
@@ -598,9 +646,11 @@ __device__ __forceinline__ void persist_step_row(
   persist_load_row<N, MODE, KB, 0, RW::R1>(xn, rn, wave, lane);
   __syncthreads();
   persist_lds_to_operands<N, MODE, KB>(xl, xr, wave, lane);
-  persist_partials<N, MODE, KB, false>(a, sh, xr, wreg, lds_w, slot, lane, wave);
-  __syncthreads();
-  persist_load_row<N, MODE, KB, RW::R1, RW::R2>(xn, rn, wave, lane);
+  persist_sumsq(sh, xr, slot, lane, wave);
+  __syncthreads();  // sums of squares visible
+  persist_project<N, MODE, KB, false>(a, sh, xr, wreg, lds_w, slot, lane, wave,
+                                      RowIssue<N, MODE, KB, RW::R1, RW::R2>{xn, rn, wave, lane});
+  __syncthreads();  // partials visible
   if constexpr (MODE == kFull) {
     if (wave < P::SK_WAVES && prev >= 0 && a.h_res)
       persist_sinkhorn<N>(a, sh.hres[slot ^ 1], prev, tid);
@@ -617,8 +667,8 @@ __device__ __forceinline__ void persist_step_row(
     hlo[i] = pack_lo(h);
     hhi[i] = pack_hi(h);
   }
-  persist_preagg<N, KB, false>(a, xr, hlo, hhi, tile, lane, wave, nsh, slot);
-  persist_load_row<N, MODE, KB, RW::R2, RW::PW>(xn, rn, wave, lane);
+  persist_preagg<N, KB, false>(a, xr, hlo, hhi, tile, lane, wave, nsh, slot,
+                               RowIssue<N, MODE, KB, RW::R2, RW::PW>{xn, rn, wave, lane});
 }
 
 // Gate parameter of thread tid (raw bits; converted once the streaming loads

@@ -51,10 +51,15 @@ def test_pre_full_vs_oracle(dev, dtype, n, C, M):
     assert maxrel(r["sub"], o["sub_in"]) <= bar
     assert maxrel(r["h_pre"], o["h_pre"]) <= bar
     assert maxrel(r["h_post"], o["h_post"]) <= bar
-    assert maxrel(r["h_raw"], o["h_res_raw"]) <= (2e-2 if dtype == torch.bfloat16 else 1e-5)
+    # The kernels project x_norm rounded to bf16, as the oracle does
+    # (model/mhc_fused.py:845): mixes_raw (fp32) lands within half a bf16 step of
+    # the oracle's bf16 mixes and h_res_raw within one step (8e-3 of the largest
+    # entry).  The n = 8 MFMA kernel keeps x_norm in fp32 (the reference's fused
+    # kernel, :209-229), a bf16 rounding of x_norm away: 2e-2.
+    raw_bar = 1e-5 if dtype == torch.float32 else (2e-2 if n == 8 and mfma else 8e-3)
+    assert maxrel(r["h_raw"], o["h_res_raw"]) <= raw_bar
     assert maxrel(r["inv"], o["inv_rms"]) <= 1e-5
-    # The oracle's projection rounds x_norm and mixes to bf16; the kernels keep fp32.
-    assert maxrel(r["mixes"], o["mixes_raw"]) <= (2e-2 if dtype == torch.bfloat16 else 1e-5)
+    assert maxrel(r["mixes"], o["mixes_raw"]) <= raw_bar
     assert maxabs(r["h_res"], o["h_res"]) <= (1e-2 if dtype == torch.bfloat16 else 1e-5)
     if dtype == torch.float32:
         for dim in (-1, -2):
@@ -63,14 +68,19 @@ def test_pre_full_vs_oracle(dev, dtype, n, C, M):
 
 @pytest.mark.parametrize("n,C", [(4, 768), (8, 768), (2, 512)])
 def test_pre_mfma_matches_generic(dev, n, C):
-    """The MFMA kernel and the generic VALU kernel agree on the same bf16 input."""
+    """The MFMA kernel and the generic VALU kernel agree on the same bf16 input.
+    Both project x_norm rounded to bf16 (model/mhc_fused.py:845) for n <= 4, so
+    their fp32 mixes differ only in the order of the fp32 sums.  The n = 8
+    kernel projects the unrounded fp32 x_norm (as the reference's fused kernel
+    does), so at n = 8 its mixes sit a bf16 rounding of x_norm away from the
+    generic kernel's: held to the 2e-2 bar of the oracle comparison above."""
     a, _, packed = _pre_case(dev, n, C, 48, torch.bfloat16, True, 20, use_pack=True, seed=5)
     b, _, _ = _pre_case(dev, n, C, 48, torch.bfloat16, True, 20, use_pack=False, seed=5)
     assert packed is not None
-    assert maxrel(b["mixes_raw"], a["mixes_raw"]) <= 1e-5
+    assert maxrel(b["mixes_raw"], a["mixes_raw"]) <= (1e-5 if n <= 4 else 2e-2)
     assert maxrel(b["inv_rms"], a["inv_rms"]) <= 1e-6
     for k in ("sub_in", "h_post", "h_res"):
-        assert maxrel(b[k], a[k]) <= 1e-2, k
+        assert maxrel(b[k], a[k]) <= (1e-2 if n <= 4 else 2e-2), k
 
 
 @pytest.mark.parametrize("n,C,M", [(4, 768, 4096), (2, 512, 4096), (4, 768, 20000),
@@ -264,11 +274,13 @@ def test_pre_vs_reference_vectors(dev, name):
                             want_h_pre=True, want_saved=True)
     ref = {k: v.reshape(o[k].shape) for k, v in ref.items()}
     bar = tol(dtype)
-    # x_norm and the projection stay fp32 in the kernels (as in the reference's
-    # fused kernel, model/mhc_fused.py:209-229); _pre_phase_full_ref rounds both
-    # to bf16 (:545-546), so the raw projection and h_res_raw carry up to a bf16
-    # step of their largest entry (2**-8 relative).
-    raw_bar = 2e-2 if dtype == torch.bfloat16 else 1e-5
+    # The kernels round x_norm to bf16 before the projection, as
+    # _pre_phase_full_ref does (:541-546), and keep the projection's sum in
+    # fp32 where the reference rounds it to bf16: the raw projection and
+    # h_res_raw carry at most a bf16 step of their largest entry.  The n = 8
+    # MFMA kernel keeps x_norm in fp32 (the reference's fused kernel,
+    # model/mhc_fused.py:209-229): 2e-2.
+    raw_bar = 1e-5 if dtype != torch.bfloat16 else (2e-2 if n == 8 and packed is not None else 8e-3)
     assert maxrel(ref["sub_in"], o["sub_in"]) <= bar
     assert maxrel(ref["h_pre"], o["h_pre"]) <= bar
     assert maxrel(ref["h_post"], o["h_post"]) <= bar
