@@ -54,8 +54,9 @@ const char* mhc_last_error(void);
 
 /*
  * Size in bytes of the MFMA operand image of phi for (n, C, mode), or 0 when
- * that shape has no MFMA kernel (n not in {1,2,4,8}, C % 8 != 0, C > 1024,
- * or MHCHead with n == 1).  Host-only, no device work.
+ * that shape has no MFMA kernel (n not in {1,2,4,8,16}, C % 8 != 0, n == 1
+ * with C > 1024, MHCHead with n == 1, or an image past 2 GiB).  Host-only, no
+ * device work.
  * No reference counterpart: the reference re-reads phi row-major per token
  * (model/mhc_fused.py:217-229); this build re-lays it out once per weight
  * version for MFMA B-operand loads.
@@ -253,7 +254,8 @@ int mhc_expand_norm_fwd(const void* x, int x_dtype, const void* norm_weight, int
  * Batch size (tokens) at or below which the pre-phase entry points run the
  * small-batch kernel (one workgroup per group of up to 16 tokens, phi read
  * from L2) instead of the large-batch ones (bf16, packed phi, n in {1, 2, 4,
- * 8}, C <= 1024; default 1024); max_tokens < 0 only queries.  Both sides give
+ * 8}, C <= 1024; n = 16 and wider rows take the K-streamed kernel at every
+ * size; default 1024); max_tokens < 0 only queries.  Both sides give
  * bit-identical results.  Returns the previous value.  Process-wide setting,
  * not synchronised with calls in flight.
  * No reference counterpart (the reference launches one program per token at

@@ -418,4 +418,50 @@ __device__ __forceinline__ void sk8_iter(float (&v)[4], float eps) {
   sk8_col_norm(v, eps);
 }
 
+// ---------------------------------------- 16 x 16 Sinkhorn, half a row per lane
+// One matrix per 32 lanes (two DPP rows): lane j of the group holds row
+// (j >> 1), columns 8 * (j & 1) .. + 7 in v[0..7].  A row sum is seven in-lane
+// adds and one DPP add with the neighbouring lane (the row's other half).  A
+// column sum runs over the 16 lanes of one parity (j & 1): lane xor 2
+// (quad_perm), xor 8 (row_ror:8), then row_ror:4, which adds lane j + 4 or its
+// xor-8 partner (the value is already symmetric under xor 8), and the other
+// DPP row (lane xor 16); each step adds two bit-identical values, so every
+// lane of a column ends with the bit-identical sum.  Schedule and (sum + eps)
+// divisors as sinkhorn_lane.
+
+__device__ __forceinline__ float sk16_row_sum(const float (&v)[8]) {
+  const float s = ((v[0] + v[1]) + (v[2] + v[3])) + ((v[4] + v[5]) + (v[6] + v[7]));
+  return s + dpp_f<kDppXor1>(s);
+}
+
+__device__ __forceinline__ float sk16_col_sum(float c) {
+  c = c + dpp_f<kDppXor2>(c);
+  c = c + dpp_f<kDppRor8>(c);
+  c = c + dpp_f<kDppRor4>(c);
+  return c + xor_lane16(c);
+}
+
+__device__ __forceinline__ void sk16_col_norm(float (&v)[8], float eps) {
+#pragma unroll
+  for (int q = 0; q < 8; ++q) v[q] = v[q] * __builtin_amdgcn_rcpf(sk16_col_sum(v[q]) + eps);
+}
+
+__device__ __forceinline__ void sk16_start(float (&v)[8], float eps) {
+  float mx = fmaxf(fmaxf(fmaxf(v[0], v[1]), fmaxf(v[2], v[3])), fmaxf(fmaxf(v[4], v[5]), fmaxf(v[6], v[7])));
+  mx = fmaxf(mx, dpp_f<kDppXor1>(mx));
+#pragma unroll
+  for (int q = 0; q < 8; ++q) v[q] = expf(v[q] - mx);
+  const float r = __builtin_amdgcn_rcpf(sk16_row_sum(v));
+#pragma unroll
+  for (int q = 0; q < 8; ++q) v[q] = v[q] * r + eps;
+  sk16_col_norm(v, eps);
+}
+
+__device__ __forceinline__ void sk16_iter(float (&v)[8], float eps) {
+  const float r = __builtin_amdgcn_rcpf(sk16_row_sum(v) + eps);
+#pragma unroll
+  for (int q = 0; q < 8; ++q) v[q] = v[q] * r;
+  sk16_col_norm(v, eps);
+}
+
 }  // namespace mhc

@@ -133,6 +133,8 @@ hipError_t launch_stream_expand(const void* x, void* out, int elem_bytes, int64_
 // then n copies (model/mhc_common.py:115-119), in one pass:
 //   y[c] = round(x[c] * (1 / sqrt(mean_c(x^2) + eps)) * w[c]),  out[t, i*C + c] = y[c].
 // One wave per token; fp32 arithmetic, one rounding to the stream dtype.
+// With n = 1 it is a plain RMSNorm, also in place (out == x): each lane
+// reads its chunks of the row before it writes them.
 
 __device__ __forceinline__ float lo16(uint32_t u, int dt) {
   return dt == kBF16 ? bf16lo(u) : f16_bits_to_f32((uint16_t)(u & 0xffffu));
@@ -146,9 +148,9 @@ __device__ __forceinline__ uint32_t pack16(float a, float b, int dt) {
 }
 
 // 16-bit streams, C % 8 == 0, 16-byte aligned rows: 8 elements per lane step.
-__global__ __launch_bounds__(256) void expand_norm_vec_kernel(const U32x4* __restrict__ x, int xdt,
+__global__ __launch_bounds__(256) void expand_norm_vec_kernel(const U32x4* x, int xdt,
                                                               const void* __restrict__ w, int wdt,
-                                                              U32x4* __restrict__ out, int64_t M,
+                                                              U32x4* out, int64_t M,
                                                               int n, int C, float eps) {
   const int64_t tok = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
   if (tok >= M) return;  // whole waves
@@ -182,9 +184,9 @@ __global__ __launch_bounds__(256) void expand_norm_vec_kernel(const U32x4* __res
   }
 }
 
-__global__ __launch_bounds__(256) void expand_norm_kernel(const void* __restrict__ x, int xdt,
+__global__ __launch_bounds__(256) void expand_norm_kernel(const void* x, int xdt,
                                                           const void* __restrict__ w, int wdt,
-                                                          void* __restrict__ out, int64_t M, int n,
+                                                          void* out, int64_t M, int n,
                                                           int C, float eps) {
   const int64_t tok = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
   if (tok >= M) return;

@@ -127,6 +127,90 @@ __global__ __launch_bounds__(256) void post_vec_kernel(PostArgs a) {
   }
 }
 
+// n = 16, bf16 stream, gates and F.  post_vec_kernel's one thread per column
+// chunk would hold 256 gate values a thread; here one wave takes a token and
+// its lanes stride over 4-column chunks (8 bytes of each stream).  The gates
+// are wave-uniform and come through the scalar cache, h_res one row at a time
+// as bf16 pairs of adjacent streams (h_res[i][2p], h_res[i][2p+1]): the
+// row-major layout already pairs them.  The x chunk is re-packed once into the
+// matching pairs (x[2p][c], x[2p+1][c]) by v_perm, and each res-mix output is
+// eight v_dot2_f32_bf16 (bf16 products are exact in fp32; the fp32 sum runs
+// pairwise rather than in post_vec_kernel's order).  Rounding points as
+// post_vec_kernel.
+typedef unsigned int u32x2_t __attribute__((ext_vector_type(2)));
+
+template <bool RES>
+__global__ __launch_bounds__(256) void post_n16_kernel(PostArgs a) {
+  constexpr int N = 16;
+  constexpr int NP = N / 2;
+  const int lane = threadIdx.x & 63;
+  const int64_t tok = (int64_t)blockIdx.x * 4 + __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  if (tok >= a.M) return;  // whole wave
+  const int C = a.C;
+  const int C4 = C / 4;
+  const int64_t NC = (int64_t)N * C;
+  const uint16_t* __restrict__ x = static_cast<const uint16_t*>(a.x) + tok * NC;
+  const uint16_t* __restrict__ f = static_cast<const uint16_t*>(a.f_out) + tok * C;
+  uint16_t* __restrict__ out = static_cast<uint16_t*>(a.out) + tok * NC;
+  const uint32_t* __restrict__ hp32 =
+      reinterpret_cast<const uint32_t*>(static_cast<const uint16_t*>(a.h_post) + tok * N);
+  const uint32_t* __restrict__ hr32 =
+      RES ? reinterpret_cast<const uint32_t*>(static_cast<const uint16_t*>(a.h_res) + tok * N * N) : nullptr;
+  float hp[N];
+#pragma unroll
+  for (int p = 0; p < NP; ++p) {
+    const uint32_t w = __builtin_amdgcn_readfirstlane(hp32[p]);
+    hp[2 * p] = bf16lo(w);
+    hp[2 * p + 1] = bf16hi(w);
+  }
+  for (int cv = lane; cv < C4; cv += 64) {
+    const int c = cv * 4;
+    u32x2_t xv[N];
+#pragma unroll
+    for (int j = 0; j < N; ++j)
+      xv[j] = __builtin_nontemporal_load(reinterpret_cast<const u32x2_t*>(x + (int64_t)j * C + c));
+    const u32x2_t fv = *reinterpret_cast<const u32x2_t*>(f + c);
+    const float fl[4] = {bf16lo(fv.x), bf16hi(fv.x), bf16lo(fv.y), bf16hi(fv.y)};
+    // xp[p][k] = (x[2p][c + k], x[2p + 1][c + k])
+    uint32_t xp[RES ? NP : 1][4];
+    if constexpr (RES) {
+#pragma unroll
+      for (int p = 0; p < NP; ++p)
+#pragma unroll
+        for (int h = 0; h < 2; ++h) {
+          xp[p][2 * h] = __builtin_amdgcn_perm(xv[2 * p + 1][h], xv[2 * p][h], 0x05040100u);
+          xp[p][2 * h + 1] = __builtin_amdgcn_perm(xv[2 * p + 1][h], xv[2 * p][h], 0x07060302u);
+        }
+    }
+#pragma unroll
+    for (int i = 0; i < N; ++i) {
+      float r[4];
+      if constexpr (RES) {
+        uint32_t hrow[NP];
+#pragma unroll
+        for (int p = 0; p < NP; ++p) hrow[p] = __builtin_amdgcn_readfirstlane(hr32[i * NP + p]);
+#pragma unroll
+        for (int k = 0; k < 4; ++k) {
+          float acc = 0.f;
+#pragma unroll
+          for (int p = 0; p < NP; ++p) acc = dot2_bf16(hrow[p], xp[p][k], acc);
+          r[k] = rnd<__bf16>(acc);
+        }
+      } else {
+        r[0] = bf16lo(xv[i].x);
+        r[1] = bf16hi(xv[i].x);
+        r[2] = bf16lo(xv[i].y);
+        r[3] = bf16hi(xv[i].y);
+      }
+      float o[4];
+#pragma unroll
+      for (int k = 0; k < 4; ++k) o[k] = __fadd_rn(r[k], rnd<__bf16>(__fmul_rn(hp[i], fl[k])));
+      const u32x2_t ov = {pack_bf16x2(o[0], o[1]), pack_bf16x2(o[2], o[3])};
+      __builtin_nontemporal_store(ov, reinterpret_cast<u32x2_t*>(out + (int64_t)i * C + c));
+    }
+  }
+}
+
 // Any dtype mix, any C: one thread per output element.
 __global__ __launch_bounds__(256) void post_generic_kernel(PostArgs a) {
   const int64_t gid = (int64_t)blockIdx.x * 256 + threadIdx.x;
@@ -183,7 +267,18 @@ static bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 
 hipError_t launch_post(const PostArgs& a, hipStream_t s) {
   const int xb = dtype_bytes(a.x_dtype);
   const int V = 16 / xb;
-  // n == 16 would hold 256 gate values per thread; it takes the generic kernel.
+  // n == 16 would hold 256 gate values per thread: one wave per token instead.
+  if (a.n == 16 && a.x_dtype == kBF16 && a.h_dtype == kBF16 && a.f_dtype == kBF16 && a.C % 4 == 0 &&
+      ((reinterpret_cast<uintptr_t>(a.x) | reinterpret_cast<uintptr_t>(a.out) |
+        reinterpret_cast<uintptr_t>(a.f_out)) & 7) == 0 &&
+      ((reinterpret_cast<uintptr_t>(a.h_post) | reinterpret_cast<uintptr_t>(a.h_res)) & 3) == 0) {
+    const int64_t blocks = (a.M + 3) / 4;
+    if (a.h_res)
+      hipLaunchKernelGGL(post_n16_kernel<true>, dim3((unsigned)blocks), dim3(256), 0, s, a);
+    else
+      hipLaunchKernelGGL(post_n16_kernel<false>, dim3((unsigned)blocks), dim3(256), 0, s, a);
+    return hipGetLastError();
+  }
   const bool pow2n = a.n == 1 || a.n == 2 || a.n == 4 || a.n == 8;
   const bool vec_ok = pow2n && a.h_dtype == a.x_dtype && a.C % V == 0 && aligned16(a.x) &&
                       aligned16(a.out) && aligned16(a.f_out) &&

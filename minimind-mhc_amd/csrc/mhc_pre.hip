@@ -1,8 +1,9 @@
 // Pre phase: MFMA dispatch, phi packing, and the generic VALU kernel.
 //
 // The generic kernel serves every (dtype, n, C) the MFMA instances do not:
-// fp32 / fp16 streams, fp32 phi, n == 16, C > 1024 or C % 8 != 0, and the
-// n == 1 MHCHead (plain RMSNorm).  One 256-thread workgroup per token; it is a
+// fp16 streams, mixed stream / phi dtypes, fp32 outside the split kernel's
+// shapes (n <= 4, C <= 1024), C % 8 != 0, and the n == 1 MHCHead (plain
+// RMSNorm) at C > 1024.  One 256-thread workgroup per token; it is a
 // correctness path, not a tuned one.  x_norm = x * inv_rms is rounded to the
 // stream dtype and the projection accumulates in fp32; the gates and the
 // pre-aggregate round where the reference's torch ops round
@@ -37,16 +38,26 @@ __global__ __launch_bounds__(256) void phi_pack_kernel(const void* __restrict__ 
   packed[idx] = f32_to_bf16_bits(v);
 }
 
+// MFMA kernels: n in {1, 2, 4, 8} at C <= 1024 (register-resident phi for
+// n <= 4, the K-streamed kernel for n = 8), and the K-streamed kernel for
+// n in {2, 4, 8, 16} at any wider C.  The image is addressed with 32-bit
+// byte offsets.
 int64_t mfma_packed_bytes(int n, int C, int mode) {
-  if (!(n == 1 || n == 2 || n == 4 || n == 8)) return 0;
+  if (!(n == 1 || n == 2 || n == 4 || n == 8 || n == 16)) return 0;
   if (mode != kFull && mode != kNoHres && mode != kHead) return 0;
   if (mode == kHead && n == 1) return 0;
   if (C <= 0 || C % 8 != 0) return 0;
-  if ((C + kCBlock - 1) / kCBlock > kMfmaMaxColBlocks) return 0;  // C <= 1024
+  const int ncb = (C + kCBlock - 1) / kCBlock;
+  if (n == 1 && ncb > kMfmaMaxColBlocks) return 0;  // C <= 1024
   const int fd = mode_fd(mode, n);
   const int nt = (fd + 15) / 16;
-  const int ncb = (C + kCBlock - 1) / kCBlock;
-  return (int64_t)n * ncb * nt * 64 * 8 * 2;
+  const int64_t bytes = (int64_t)n * ncb * nt * 64 * 8 * 2;
+  return bytes <= 0x7fffffffLL ? bytes : 0;
+}
+
+// Shapes that take the K-streamed kernel at every batch size.
+static bool pre_wide(int n, int C) {
+  return n == 16 || (C + kCBlock - 1) / kCBlock > kMfmaMaxColBlocks;
 }
 
 bool mfma_supported(int x_dtype, int phi_dtype, int n, int C, int mode) {
@@ -97,6 +108,16 @@ int device_cus() {
 
 hipError_t launch_pre_mfma(const PreArgs& a, hipStream_t s) {
   const int cus = device_cus();
+  // n = 16, C > 1024: phi streams from L2 through the K-split MFMA loop.
+  if (pre_wide(a.n, a.C)) {
+    switch (a.n) {
+      case 2: return launch_pre_kstream_n2(a, s);
+      case 4: return launch_pre_kstream_n4(a, s);
+      case 8: return launch_pre_kstream_n8(a, s);
+      case 16: return launch_pre_kstream_n16(a, s);
+      default: return hipErrorInvalidValue;
+    }
+  }
   // Decode-size batches: one workgroup per group of up to 16 tokens.
   if (a.M <= pre_token_max_m() && a.phi_packed) {
     switch (a.n) {

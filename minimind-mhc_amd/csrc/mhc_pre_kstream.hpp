@@ -1,37 +1,43 @@
-// Fused mHC pre phase for wide projections (n = 8): K-streamed MFMA.
+// Fused mHC pre phase for wide projections: K-streamed MFMA.
 //
-// At n = 8, C = 768 the projection phi is [6144, 80] bf16 = 983 KB: it fits
-// neither in a workgroup's registers and LDS (as it does at n = 4) nor does a
-// 16-token x tile (192 KB) fit in registers next to it.  So phi streams from
-// L2 and its cost is spread over a 32-token tile:
-//   * one 8-wave workgroup per 32-token tile; wave w owns every 8th 32-column
-//     chunk of the n*C row (K split 8 ways) for both 16-token M-blocks, so
-//     each phi chunk is read once per tile and feeds two MFMAs;
-//   * the K loop keeps D chunks in flight per wave: each chunk is two 16-byte
-//     x loads (16 tokens x 32 columns per M-block, the MFMA A operands) and
-//     NT 16-byte phi loads (the packed B operands, 16 output columns each);
+// Serves the shapes whose phi does not fit a workgroup's registers: n = 8 and
+// n = 16 at any C, and n in {2, 4} at C > 1024.  At n = 8, C = 768 phi is
+// [6144, 80] bf16 = 983 KB; neither it nor a 16-token x tile (192 KB) fits in
+// registers next to the other.  So phi streams from L2 and its cost is spread
+// over a token tile:
+//   * one 8-wave workgroup per TM-token tile (32; 16 at n = 16).  Wave w owns
+//     every KS-th 32-column chunk of the n*C row (K split KS ways) for all of
+//     the tile's 16-token M-blocks, so each phi chunk is read once per tile and
+//     feeds MB MFMAs.  KS = 8, except at n = 16 with H_res (18 output tiles of
+//     16 columns): there two waves share each chunk, one per half of the output
+//     tiles (KS = 4), so a wave's operands and accumulators stay in registers;
+//   * the K loop keeps D chunks in flight per wave: each chunk is MB 16-byte x
+//     loads (16 tokens x 32 columns per M-block, the MFMA A operands) and NTW
+//     16-byte phi loads (the packed B operands, 16 output columns each);
 //     v_mfma_f32_16x16x32_bf16 accumulates, bf16 dot2 forms the sum of
 //     squares;
-//   * the eight K-split partials meet in LDS.  The pre-aggregate's re-reads
-//     of the tile's x (393 KB, from the Infinity Cache: it has left L2 by
-//     then) need no result of the projection, so its first two rounds go out
-//     before the partials are summed;
-//   * 16 lanes per token then form inv_rms and the gates straight from the
-//     partials: lane j takes mix j (h_pre for j < 8, h_post for 8 <= j < 16)
-//     and the four h_res logits of row (j & 7), columns 4 * (j >> 3) .. + 3,
-//     which is the layout the Sinkhorn iterations (sk8_*) run in, so h_res
+//   * the K-split partials meet in LDS.  The pre-aggregate's re-reads of the
+//     tile's x (from the Infinity Cache: it has left L2 by then) need no
+//     result of the projection, so its first two rounds go out before the
+//     partials are summed;
+//   * LPT = 512 / TM lanes per token (16, or 32 at n = 16) then form inv_rms
+//     and the gates straight from the partials: lane j takes mix j (h_pre for
+//     j < n, h_post for n <= j < 2n) and its share of the n*n h_res logits in
+//     the layout the Sinkhorn iterations run in (one element per lane for
+//     n <= 4, half a row per lane, sk8_* / sk16_*, for n = 8 / 16), so h_res
 //     never passes through LDS;
 //   * the Sinkhorn iterations are spread between the pre-aggregate rounds:
 //     VALU work while the next round's loads are in flight;
-//   * with the RMSNorm epilogue the pre-aggregate chunks wait in LDS; after
-//     the rounds 16 lanes per token sum their squares, and a last pass
-//     scales, rounds and stores them.
-// Arithmetic and rounding points as pre_persist_kernel, except x_norm: the
-// MFMAs run on x and the fp32 result is scaled by inv_rms, the way the
-// reference's fused kernel computes x_norm (model/mhc_fused.py:209-229), where
-// the PyTorch path rounds x * inv_rms to bf16 before its GEMM (:845).  Rounding
-// it here needs each row's sum of squares before the K loop, i.e. a second
-// pass over the tile's 393 KB of x, which the tile cannot hold on chip.
+//   * with the RMSNorm epilogue (C <= 1024) the pre-aggregate chunks wait in
+//     LDS; after the rounds the token's lanes sum their squares, and a last
+//     pass scales, rounds and stores them.  Wider rows take a second launch
+//     (the RMSNorm in place on the written sublayer input).
+// Arithmetic and rounding points as pre_persist_kernel.  For n <= 4 that
+// includes x_norm = bf16(x * inv_rms) (model/mhc_fused.py:845): a first pass
+// over the tile's x forms each row's sum of squares (read again by the K
+// loop).  n = 8 and n = 16 skip that third read of x: their MFMAs run on x and
+// the fp32 result is scaled by inv_rms, the way the reference's fused kernel
+// computes x_norm (model/mhc_fused.py:209-229).
 //
 // Reference semantics: model/mhc_fused.py:163-268, :533-559, :47-56;
 // model/mhc_fused_no_hres.py:48-145; model/mhc_common.py:128-195.
@@ -42,6 +48,7 @@
 namespace mhc {
 
 constexpr int kKsWaves = 8;
+constexpr int kKsNormMaxC = kMfmaMaxColBlocks * kCBlock;  // widest row of the fused RMSNorm
 
 template <int N, int MODE>
 struct KsPlan {
@@ -50,13 +57,24 @@ struct KsPlan {
   static constexpr int NT = S::NT;
   static constexpr int G = N * N;
   static constexpr int WAVES = kKsWaves;
-  static constexpr int MB = 2;             // 16-token M-blocks per tile (every wave)
-  static constexpr int TM = 16 * MB;       // tokens per tile
-  static constexpr int KS = WAVES;         // K split
-  static constexpr int D = 3;              // chunks in flight per wave
-  static constexpr int PB = 2;             // pre-aggregate items per lane per round (two rounds in flight)
-  static_assert(N == 8, "16 lanes per token: mixes 0..2N-1 and half an 8 x 8 row each");
-  static_assert(TM == WAVES * 4, "four tokens per wave");
+  static constexpr int NH = NT > 9 ? 2 : 1;          // output-tile halves
+  static constexpr int NTW = (NT + NH - 1) / NH;     // output tiles per wave
+  static constexpr int KS = WAVES / NH;              // K split
+  static constexpr int TM = N >= 16 ? 16 : 32;       // tokens per tile
+  static constexpr int MB = TM / 16;                 // 16-token M-blocks (every wave)
+  static constexpr int LPT = WAVES * 64 / TM;        // lanes per token in the gate phase
+  static constexpr int TPW = 64 / LPT;               // tokens per wave
+  static constexpr int D = 3;                        // chunks in flight per wave
+  static constexpr int PB = N >= 16 ? 1 : 2;         // pre-aggregate items per lane per round
+  static constexpr bool XN = N <= 4;                 // projection on bf16(x * inv_rms)
+  static constexpr int SD = 4;                       // chunks in flight in the sums-of-squares pass
+  static constexpr int SKV = G > LPT ? G / LPT : 1;  // Sinkhorn values per lane
+  static constexpr int SKL = G / SKV;                // lanes holding distinct h_res values
+  static_assert(N == 2 || N == 4 || N == 8 || N == 16, "n in {2, 4, 8, 16}");
+  static_assert(2 * N <= LPT, "one pre / post mix per lane");
+  static_assert(TM == WAVES * TPW, "whole tokens per wave");
+  static_assert(SKV == 1 || SKV == 4 || SKV == 8, "Sinkhorn lane layouts");
+  static_assert((KS & (KS - 1)) == 0, "power-of-two K split");
 };
 
 template <int N, int MODE>
@@ -73,15 +91,65 @@ struct KsShared {
 template <int N, int MODE, bool NORM>
 struct KsNorm {
   using P = KsPlan<N, MODE>;
-  static constexpr int kChunks = kMfmaMaxColBlocks * 4;  // 8-column chunks of a C <= 1024 row
+  static constexpr int kChunks = kKsNormMaxC / 8;  // 8-column chunks of a row
   U32x4 stash[P::TM * kChunks];
-  float gain[kMfmaMaxColBlocks * kCBlock];
+  float gain[kKsNormMaxC];
   float scale[P::TM];
 };
 template <int N, int MODE>
 struct KsNorm<N, MODE, false> {
   int unused;
 };
+
+// Whether the fused RMSNorm epilogue fits beside the partials.
+template <int N, int MODE>
+constexpr bool ks_norm_fits() {
+  return sizeof(KsShared<N, MODE>) + sizeof(KsNorm<N, MODE, true>) <= (size_t)kLdsBytes;
+}
+
+// First h_res entry of gate-phase lane jl (of P::SKV consecutive ones).
+template <int N, int SKV>
+__device__ __forceinline__ int ks_res_entry(int jl) {
+  if constexpr (SKV == 1) return jl % (N * N);
+  else if constexpr (SKV == 4) return (jl & 7) * N + 4 * (jl >> 3);  // n = 8: half row
+  else return (jl >> 1) * N + 8 * (jl & 1);                           // n = 16: half row
+}
+
+// Sinkhorn on the gate-phase layout: first step (softmax, + eps, first column
+// normalisation) and one more row + column normalisation.
+template <int N, int SKV>
+__device__ __forceinline__ void ks_sk_start(float (&v)[SKV], float eps) {
+  if constexpr (SKV == 1) {
+    const float mx = row_reduce<N, OpMax>(v[0]);
+    const float e = expf(v[0] - mx);
+    v[0] = e * __builtin_amdgcn_rcpf(row_reduce<N, OpAdd>(e)) + eps;
+    v[0] = v[0] * __builtin_amdgcn_rcpf(col_sum<N>(v[0]) + eps);
+  } else if constexpr (SKV == 4) {
+    sk8_start(v, eps);
+  } else {
+    sk16_start(v, eps);
+  }
+}
+template <int N, int SKV>
+__device__ __forceinline__ void ks_sk_iter(float (&v)[SKV], float eps) {
+  if constexpr (SKV == 1) {
+    v[0] = v[0] * __builtin_amdgcn_rcpf(row_reduce<N, OpAdd>(v[0]) + eps);
+    v[0] = v[0] * __builtin_amdgcn_rcpf(col_sum<N>(v[0]) + eps);
+  } else if constexpr (SKV == 4) {
+    sk8_iter(v, eps);
+  } else {
+    sk16_iter(v, eps);
+  }
+}
+
+// Sum over the LPT lanes of one token (16: a DPP row; 32: two).
+template <int LPT>
+__device__ __forceinline__ float ks_token_sum(float q) {
+  q = row_reduce<8, OpAdd>(q);
+  q = q + dpp_f<kDppRowMirror>(q);
+  if constexpr (LPT == 32) q = q + xor_lane16(q);
+  return q;
+}
 
 template <int N, int MODE, bool NORM>
 __global__ __launch_bounds__(kKsWaves * 64) void pre_kstream_kernel(PreArgs a) {
@@ -90,8 +158,11 @@ __global__ __launch_bounds__(kKsWaves * 64) void pre_kstream_kernel(PreArgs a) {
   using NS = KsNorm<N, MODE, NORM>;
   constexpr int FD = P::FD;
   constexpr int NT = P::NT;
+  constexpr int NTW = P::NTW;
   constexpr int TM = P::TM;
   constexpr int D = P::D;
+  constexpr int LPT = P::LPT;
+  constexpr int SKV = P::SKV;
   constexpr int T = P::WAVES * 64;
   static_assert(sizeof(KsShared<N, MODE>) + sizeof(NS) <= kLdsBytes, "LDS budget");
   __shared__ KsShared<N, MODE> sh;
@@ -102,7 +173,8 @@ __global__ __launch_bounds__(kKsWaves * 64) void pre_kstream_kernel(PreArgs a) {
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int r = lane & 15;
   const int g = lane >> 4;
-  const int kq = wave;
+  const int kq = wave & (P::KS - 1);                  // K-split index
+  const int nh = (int)((unsigned)wave / (unsigned)P::KS);  // half of the output tiles
   const int C = a.C;
   const int NC = N * C;
   const int NCB = (C + kCBlock - 1) / kCBlock;
@@ -128,15 +200,8 @@ __global__ __launch_bounds__(kKsWaves * 64) void pre_kstream_kernel(PreArgs a) {
   const auto rw = make_rsrc(a.phi_packed, (uint32_t)(NCH * NT) * 1024u);
   const uint32_t xrow = (uint32_t)(r * NC) * 2u + (uint32_t)g * 16u;
   const uint32_t xblk = (uint32_t)(16 * NC) * 2u;  // offset of M-block 1
-  U32x4 xs[D][P::MB];
-  U32x4 ws[D][NT];
-  // Workgroups walk their chunks in rotated orders, so the CUs of an XCD do
-  // not all read the same few phi lines from the same L2 channels at once.
-  const int rot = (int)(blockIdx.x % (unsigned)NJ);
-  auto issue = [&](int slot_j, U32x4 (&xd)[P::MB], U32x4 (&wd)[NT]) {
-    const int jr = slot_j < NJ ? (slot_j + rot < NJ ? slot_j + rot : slot_j + rot - NJ) : slot_j;
-    const int k = kq + P::KS * jr;              // uniform
-    const bool live = slot_j < NJ && k < NCH;
+  // x chunk k of every M-block (zeros past the row or past C).
+  auto x_chunk = [&](int k, bool live, U32x4 (&xd)[P::MB]) {
     const int i = live ? k / NCB : 0;
     const int cb = live ? k - i * NCB : 0;
     const int c0 = cb * kCBlock;
@@ -145,34 +210,86 @@ __global__ __launch_bounds__(kKsWaves * 64) void pre_kstream_kernel(PreArgs a) {
     for (int m = 0; m < P::MB; ++m)
       xd[m] = __builtin_bit_cast(U32x4, __builtin_amdgcn_raw_buffer_load_b128(
                                             rx, (int)(xl ? xrow + m * xblk : kBufOob), (i * C + c0) * 2, 0));
-    const uint32_t wo = live ? (uint32_t)lane * 16u : kBufOob;
+  };
+  U32x4 xs[D][P::MB];
+  U32x4 ws[D][NTW];
+  // Workgroups walk their chunks in rotated orders, so the CUs of an XCD do
+  // not all read the same few phi lines from the same L2 channels at once.
+  const int rot = (int)(blockIdx.x % (unsigned)NJ);
+  auto issue = [&](int slot_j, U32x4 (&xd)[P::MB], U32x4 (&wd)[NTW]) {
+    const int jr = slot_j < NJ ? (slot_j + rot < NJ ? slot_j + rot : slot_j + rot - NJ) : slot_j;
+    const int k = kq + P::KS * jr;              // uniform
+    const bool live = slot_j < NJ && k < NCH;
+    x_chunk(k, live, xd);
 #pragma unroll
-    for (int nt = 0; nt < NT; ++nt)
-      wd[nt] = __builtin_bit_cast(
-          U32x4, __builtin_amdgcn_raw_buffer_load_b128(rw, (int)wo, (k * NT + nt) * 1024, 0));
+    for (int nt = 0; nt < NTW; ++nt) {
+      const int ntg = nh * NTW + nt;
+      wd[nt] = __builtin_bit_cast(U32x4, __builtin_amdgcn_raw_buffer_load_b128(
+                                             rw, (int)(live && ntg < NT ? (uint32_t)lane * 16u : kBufOob),
+                                             (k * NT + ntg) * 1024, 0));
+    }
   };
 #pragma unroll
   for (int d = 0; d < D; ++d) issue(d, xs[d], ws[d]);
 
-  f32x4_t acc[P::MB][NT];
   float ss[P::MB];
 #pragma unroll
-  for (int m = 0; m < P::MB; ++m) {
-    ss[m] = 0.f;
+  for (int m = 0; m < P::MB; ++m) ss[m] = 0.f;
+  // n <= 4: sums of squares first (this wave's chunks, SD in flight), then
+  // each row's inv_rms for x_norm.  The K loop's first chunks are in flight.
+  float inv_r[P::MB];
 #pragma unroll
-    for (int nt = 0; nt < NT; ++nt) acc[m][nt] = f32x4_t{0.f, 0.f, 0.f, 0.f};
+  for (int m = 0; m < P::MB; ++m) inv_r[m] = 1.0f;
+  if constexpr (P::XN) {
+    for (int j0 = 0; j0 < NJ; j0 += P::SD) {  // uniform trip count
+      U32x4 v[P::SD][P::MB];
+#pragma unroll
+      for (int d = 0; d < P::SD; ++d) {
+        const int k = kq + P::KS * (j0 + d);
+        x_chunk(k, j0 + d < NJ && k < NCH, v[d]);
+      }
+#pragma unroll
+      for (int d = 0; d < P::SD; ++d)
+#pragma unroll
+        for (int m = 0; m < P::MB; ++m)
+#pragma unroll
+          for (int q = 0; q < 4; ++q) ss[m] = dot2_bf16(v[d][m].v[q], v[d][m].v[q], ss[m]);
+    }
+#pragma unroll
+    for (int m = 0; m < P::MB; ++m) {
+      ss[m] += __shfl_xor(ss[m], 16, 64);
+      ss[m] += __shfl_xor(ss[m], 32, 64);
+      if (g == 0) sh.ss[kq][m * 16 + r] = ss[m];
+    }
+    __syncthreads();  // sums of squares visible
+#pragma unroll
+    for (int m = 0; m < P::MB; ++m) {
+      float sq = 0.f;
+#pragma unroll
+      for (int w = 0; w < P::KS; ++w) sq += sh.ss[w][m * 16 + r];
+      inv_r[m] = 1.0f / sqrtf(sq / (float)NC + a.rms_eps);
+    }
   }
+
+  f32x4_t acc[P::MB][NTW];
+#pragma unroll
+  for (int m = 0; m < P::MB; ++m)
+#pragma unroll
+    for (int nt = 0; nt < NTW; ++nt) acc[m][nt] = f32x4_t{0.f, 0.f, 0.f, 0.f};
+  const bool ss_here = !P::XN && (P::NH == 1 || nh == 0);  // uniform
   for (int j0 = 0; j0 < NJ; j0 += D) {   // uniform trip count
 #pragma unroll
     for (int d = 0; d < D; ++d) {
 #pragma unroll
       for (int m = 0; m < P::MB; ++m) {
         const U32x4 v = xs[d][m];
+        if (ss_here) {
 #pragma unroll
-        for (int q = 0; q < 4; ++q) ss[m] = dot2_bf16(v.v[q], v.v[q], ss[m]);
-        const bf16x8_t av = __builtin_bit_cast(bf16x8_t, v);
+          for (int q = 0; q < 4; ++q) ss[m] = dot2_bf16(v.v[q], v.v[q], ss[m]);
+        }
+        const bf16x8_t av = __builtin_bit_cast(bf16x8_t, P::XN ? x_norm_chunk(v, inv_r[m]) : v);
 #pragma unroll
-        for (int nt = 0; nt < NT; ++nt)
+        for (int nt = 0; nt < NTW; ++nt)
           acc[m][nt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(
               av, __builtin_bit_cast(bf16x8_t, ws[d][nt]), acc[m][nt], 0, 0, 0);
       }
@@ -182,14 +299,18 @@ __global__ __launch_bounds__(kKsWaves * 64) void pre_kstream_kernel(PreArgs a) {
   // MFMA 16x16 result layout: lane l holds D[4*(l/16) + j][l % 16], j = 0..3.
 #pragma unroll
   for (int m = 0; m < P::MB; ++m) {
-    ss[m] += __shfl_xor(ss[m], 16, 64);
-    ss[m] += __shfl_xor(ss[m], 32, 64);
+    if (ss_here) {
+      ss[m] += __shfl_xor(ss[m], 16, 64);
+      ss[m] += __shfl_xor(ss[m], 32, 64);
+      if (g == 0) sh.ss[kq][m * 16 + r] = ss[m];
+    }
 #pragma unroll
-    for (int nt = 0; nt < NT; ++nt)
-      if (nt * 16 + r < FD)
+    for (int nt = 0; nt < NTW; ++nt) {
+      const int ntg = nh * NTW + nt;
+      if (ntg * 16 + r < FD)
 #pragma unroll
-        for (int j = 0; j < 4; ++j) sh.acc[kq][m * 16 + 4 * g + j][nt * 16 + r] = acc[m][nt][j];
-    if (g == 0) sh.ss[kq][m * 16 + r] = ss[m];
+        for (int j = 0; j < 4; ++j) sh.acc[kq][m * 16 + 4 * g + j][ntg * 16 + r] = acc[m][nt][j];
+    }
   }
   if (tid < GP::kCount) sh.prm[tid] = convert_param(rp, a.param_dtype);
   if constexpr (NORM) {
@@ -252,22 +373,23 @@ __global__ __launch_bounds__(kKsWaves * 64) void pre_kstream_kernel(PreArgs a) {
   pa_issue(1, xb);
   __syncthreads();  // partials and gate parameters visible
 
-  // ---- inv_rms and gates: 16 lanes per token ----------------------------------
-  const int tt = wave * 4 + (lane >> 4);
-  const int jl = lane & 15;
+  // ---- inv_rms and gates: LPT lanes per token ---------------------------------
+  const int tt = wave * P::TPW + lane / LPT;
+  const int jl = lane % LPT;
   const int64_t tk = t0 + tt;
   const bool ok = tt < valid;
   float sq = 0.f;
 #pragma unroll
   for (int w = 0; w < P::KS; ++w) sq += sh.ss[w][tt];
   const float inv = 1.0f / sqrtf(sq / (float)NC + a.rms_eps);
+  const float msc = P::XN ? 1.0f : inv;  // the n <= 4 partials are already normalised
   if (jl == 0 && ok && a.inv_rms) a.inv_rms[tk] = inv;
   constexpr int NMIX = FD < 2 * N ? FD : 2 * N;  // pre (and post) mixes
   if (jl < NMIX) {
     float sum = 0.f;
 #pragma unroll
     for (int w = 0; w < P::KS; ++w) sum += sh.acc[w][tt][jl];
-    const float m = sum * inv;
+    const float m = sum * msc;
     if (ok && a.mixes_raw) a.mixes_raw[tk * FD + jl] = m;
     // bias_pre[j] and bias_post[j - N] are adjacent: GP::kBiasPre + j for both
     const bool pre = jl < N;
@@ -281,24 +403,36 @@ __global__ __launch_bounds__(kKsWaves * 64) void pre_kstream_kernel(PreArgs a) {
       st_any(a.h_post, tk * N + (jl - N), kBF16, h);
     }
   }
-  float v[4] = {0.f, 0.f, 0.f, 0.f};
-  const int e0 = (jl & 7) * N + 4 * (jl >> 3);  // first of this lane's h_res entries
+  float v[SKV];
+#pragma unroll
+  for (int q = 0; q < SKV; ++q) v[q] = 0.f;
+  const int e0 = ks_res_entry<N, SKV>(jl);  // first of this lane's h_res entries
+  const bool own = jl < P::SKL;             // n = 2: lanes past the 4 entries repeat them
   if constexpr (MODE == kFull) {
-    float s4[4] = {0.f, 0.f, 0.f, 0.f};
+    float s[SKV];
+#pragma unroll
+    for (int q = 0; q < SKV; ++q) s[q] = 0.f;
 #pragma unroll
     for (int w = 0; w < P::KS; ++w) {
-      const float4 pw = *reinterpret_cast<const float4*>(&sh.acc[w][tt][2 * N + e0]);
-      s4[0] += pw.x;
-      s4[1] += pw.y;
-      s4[2] += pw.z;
-      s4[3] += pw.w;
+      if constexpr (SKV == 1) {
+        s[0] += sh.acc[w][tt][2 * N + e0];
+      } else {
+#pragma unroll
+        for (int q4 = 0; q4 < SKV; q4 += 4) {
+          const float4 pw = *reinterpret_cast<const float4*>(&sh.acc[w][tt][2 * N + e0 + q4]);
+          s[q4 + 0] += pw.x;
+          s[q4 + 1] += pw.y;
+          s[q4 + 2] += pw.z;
+          s[q4 + 3] += pw.w;
+        }
+      }
     }
 #pragma unroll
-    for (int q = 0; q < 4; ++q) {
-      const float m = s4[q] * inv;
-      if (ok && a.mixes_raw) a.mixes_raw[tk * FD + 2 * N + e0 + q] = m;
+    for (int q = 0; q < SKV; ++q) {
+      const float m = s[q] * msc;
+      if (ok && own && a.mixes_raw) a.mixes_raw[tk * FD + 2 * N + e0 + q] = m;
       v[q] = gate_res(m, sh.prm[2], sh.prm[GP::kBiasRes + e0 + q], kBF16);
-      if (ok && a.h_res_raw) st_any(a.h_res_raw, tk * P::G + e0 + q, kBF16, v[q]);
+      if (ok && own && a.h_res_raw) st_any(a.h_res_raw, tk * P::G + e0 + q, kBF16, v[q]);
     }
   }
   __syncthreads();  // h_pre visible to every lane's pre-aggregate items
@@ -308,11 +442,11 @@ __global__ __launch_bounds__(kKsWaves * 64) void pre_kstream_kernel(PreArgs a) {
   const int slots = (nrounds + 1) & ~1;  // rounds run in pairs
   const int sk_rest = a.sk_iters > 1 ? a.sk_iters - 1 : 0;
   int sk_done = 0;
-  if (sk) sk8_start(v, a.sk_eps);
+  if (sk) ks_sk_start<N, SKV>(v, a.sk_eps);
   auto sk_share = [&](int slot) {  // iterations due before slot's round is consumed
     if (!sk) return;
     const int target = (sk_rest * (slot + 1) + slots - 1) / slots;
-    for (; sk_done < target; ++sk_done) sk8_iter(v, a.sk_eps);
+    for (; sk_done < target; ++sk_done) ks_sk_iter<N, SKV>(v, a.sk_eps);
   };
   for (int rd = 0; rd < nrounds; rd += 2) {  // uniform trip count, no exit between steps
     sk_share(rd);
@@ -322,23 +456,22 @@ __global__ __launch_bounds__(kKsWaves * 64) void pre_kstream_kernel(PreArgs a) {
     pa_finish(rd + 1, xb);
     pa_issue(rd + 3, xb);
   }
-  if (sk && ok) {
+  if (sk && ok && own) {
 #pragma unroll
-    for (int q = 0; q < 4; ++q) st_any(a.h_res, tk * P::G + e0 + q, kBF16, v[q]);
+    for (int q = 0; q < SKV; ++q) st_any(a.h_res, tk * P::G + e0 + q, kBF16, v[q]);
   }
   if constexpr (NORM) {
-    // RMSNorm over C: 16 lanes per token sum the squares of the stashed
-    // (bf16-rounded) chunks jl, jl + 16, ...; then every item is scaled by
+    // RMSNorm over C: the token's LPT lanes sum the squares of the stashed
+    // (bf16-rounded) chunks jl, jl + LPT, ...; then every item is scaled by
     // its token's 1 / sqrt(mean + norm_eps) and the gain, rounded, stored.
     __syncthreads();  // every chunk stashed
     float q2 = 0.f;
-    for (int ch = jl; ch < C8; ch += 16) {
+    for (int ch = jl; ch < C8; ch += LPT) {
       const U32x4 pk = nsh.stash[tt * NS::kChunks + ch];
 #pragma unroll
       for (int j = 0; j < 4; ++j) q2 = dot2_bf16(pk.v[j], pk.v[j], q2);
     }
-    q2 = row_reduce<8, OpAdd>(q2);
-    q2 = q2 + dpp_f<kDppRowMirror>(q2);
+    q2 = ks_token_sum<LPT>(q2);
     if (jl == 0) nsh.scale[tt] = 1.0f / sqrtf(q2 / (float)C + a.norm_eps);
     __syncthreads();  // token scales visible
     for (int p = tid; p < items; p += T) {
@@ -358,20 +491,48 @@ __global__ __launch_bounds__(kKsWaves * 64) void pre_kstream_kernel(PreArgs a) {
   }
 }
 
+// The RMSNorm over C in place on the written sublayer input (rows wider than
+// the fused epilogue's LDS holds); mhc_misc.hip.
+hipError_t launch_expand_norm(const void* x, int x_dtype, const void* w, int w_dtype, void* out,
+                              int64_t M, int n, int C, float eps, hipStream_t s);
+
 template <int N, int MODE>
 hipError_t launch_pre_kstream_inst(const PreArgs& a, hipStream_t s) {
   constexpr int TM = KsPlan<N, MODE>::TM;
   const int64_t tiles = (a.M + TM - 1) / TM;
-  if (a.norm_w)
-    hipLaunchKernelGGL((pre_kstream_kernel<N, MODE, true>), dim3((unsigned)tiles),
-                       dim3(KsPlan<N, MODE>::WAVES * 64), 0, s, a);
-  else
-    hipLaunchKernelGGL((pre_kstream_kernel<N, MODE, false>), dim3((unsigned)tiles),
-                       dim3(KsPlan<N, MODE>::WAVES * 64), 0, s, a);
-  return hipGetLastError();
+  const dim3 block(KsPlan<N, MODE>::WAVES * 64);
+  if (!a.norm_w) {
+    hipLaunchKernelGGL((pre_kstream_kernel<N, MODE, false>), dim3((unsigned)tiles), block, 0, s, a);
+    return hipGetLastError();
+  }
+  if constexpr (ks_norm_fits<N, MODE>()) {
+    if (a.C <= kKsNormMaxC) {
+      hipLaunchKernelGGL((pre_kstream_kernel<N, MODE, true>), dim3((unsigned)tiles), block, 0, s, a);
+      return hipGetLastError();
+    }
+  }
+  PreArgs plain = a;
+  plain.norm_w = nullptr;
+  hipLaunchKernelGGL((pre_kstream_kernel<N, MODE, false>), dim3((unsigned)tiles), block, 0, s, plain);
+  const hipError_t e = hipGetLastError();
+  if (e != hipSuccess) return e;
+  return launch_expand_norm(a.sub_in, kBF16, a.norm_w, a.norm_dtype, a.sub_in, a.M, 1, a.C, a.norm_eps, s);
 }
 
-// n = 8 instances (mhc_pre_kstream_n8.hip).
+template <int N>
+hipError_t launch_pre_kstream_mode(const PreArgs& a, hipStream_t s) {
+  switch (a.mode) {
+    case kFull: return launch_pre_kstream_inst<N, kFull>(a, s);
+    case kNoHres: return launch_pre_kstream_inst<N, kNoHres>(a, s);
+    case kHead: return launch_pre_kstream_inst<N, kHead>(a, s);
+    default: return hipErrorInvalidValue;
+  }
+}
+
+// Per-n instances (mhc_pre_kstream_n*.hip).
+hipError_t launch_pre_kstream_n2(const PreArgs& a, hipStream_t s);
+hipError_t launch_pre_kstream_n4(const PreArgs& a, hipStream_t s);
 hipError_t launch_pre_kstream_n8(const PreArgs& a, hipStream_t s);
+hipError_t launch_pre_kstream_n16(const PreArgs& a, hipStream_t s);
 
 }  // namespace mhc

@@ -50,10 +50,13 @@ def test_packed_sizes(lib):
     assert lib.mhc_phi_packed_bytes(4, 768, 0) == 4 * 24 * 2 * 64 * 16
     assert lib.mhc_phi_packed_bytes(8, 768, 0) == 8 * 24 * 5 * 64 * 16   # FD 80 -> 5 tiles
     assert lib.mhc_phi_packed_bytes(4, 768, 1) == 4 * 24 * 1 * 64 * 16
-    assert lib.mhc_phi_packed_bytes(16, 768, 0) == 0                     # no MFMA instance
+    # n = 16 and C > 1024 take the K-streamed kernel: FD 288 -> 18 tiles
+    assert lib.mhc_phi_packed_bytes(16, 768, 0) == 16 * 24 * 18 * 64 * 16
+    assert lib.mhc_phi_packed_bytes(4, 2048, 0) == 4 * 64 * 2 * 64 * 16
     assert lib.mhc_phi_packed_bytes(4, 100, 0) == 0                      # C % 8 != 0
-    assert lib.mhc_phi_packed_bytes(4, 2048, 0) == 0                     # C > 1024
-    assert lib.mhc_phi_packed_bytes(1, 768, 2) == 0                      # head n=1 is RMSNorm
+    assert lib.mhc_phi_packed_bytes(3, 768, 0) == 0                      # n not a power of two
+    assert lib.mhc_phi_packed_bytes(1, 2048, 2) == 0                     # head n=1 is RMSNorm
+    assert lib.mhc_phi_packed_bytes(1, 768, 2) == 0
 
 
 def test_sinkhorn_bwd_max_iters(lib):

@@ -15,7 +15,8 @@
 * mhc_expand_norm_fwd against torch's rms_norm + expand
   (model/model_minimind.py:365; model/mhc_common.py:115-119), same bars.
 Shapes cover every kernel: token (M <= threshold), persistent (n <= 4),
-K-streamed (n = 8) and generic (fp32, C > 1024, C % 8 != 0)."""
+K-streamed (n = 8, n = 16, and C > 1024, where the RMSNorm is a second launch
+in place) and generic (fp16, fp32 outside the split kernel, C % 8 != 0)."""
 from __future__ import annotations
 
 import pytest
@@ -163,6 +164,10 @@ CASES = [  # (kind, n, C, M, dtype): token, persistent, K-streamed and generic k
     ("head", 4, 768, 37, torch.bfloat16), ("head", 4, 768, 1000, torch.bfloat16),
     ("head", 8, 768, 100, torch.bfloat16), ("head", 1, 64, 50, torch.bfloat16),
     ("head", 1, 64, 50, torch.float32),
+    # K-streamed n = 16 (fused epilogue) and C > 1024 (RMSNorm as a second launch)
+    ("full", 16, 128, 40, torch.bfloat16), ("nohres", 16, 64, 33, torch.bfloat16),
+    ("head", 16, 64, 20, torch.bfloat16), ("full", 2, 2048, 70, torch.bfloat16),
+    ("full", 8, 1536, 40, torch.bfloat16), ("head", 4, 2048, 9, torch.bfloat16),
 ]
 
 

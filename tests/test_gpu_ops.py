@@ -41,7 +41,7 @@ def _pre_case(dev, n, C, M, dtype, stress, iters, use_pack, seed=0):
 
 @pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float32])
 @pytest.mark.parametrize("n,C", [(4, 768), (4, 64), (8, 768), (2, 256), (1, 128), (16, 64),
-                                 (4, 104), (4, 100), (4, 2048)])
+                                 (4, 104), (4, 100), (4, 2048), (2, 1536), (8, 2048), (16, 256)])
 @pytest.mark.parametrize("M", [1, 17, 64])
 def test_pre_full_vs_oracle(dev, dtype, n, C, M):
     o, r, packed = _pre_case(dev, n, C, M, dtype, stress=True, iters=20, use_pack=True)
@@ -54,9 +54,9 @@ def test_pre_full_vs_oracle(dev, dtype, n, C, M):
     # The kernels project x_norm rounded to bf16, as the oracle does
     # (model/mhc_fused.py:845): mixes_raw (fp32) lands within half a bf16 step of
     # the oracle's bf16 mixes and h_res_raw within one step (8e-3 of the largest
-    # entry).  The n = 8 MFMA kernel keeps x_norm in fp32 (the reference's fused
-    # kernel, :209-229), a bf16 rounding of x_norm away: 2e-2.
-    raw_bar = 1e-5 if dtype == torch.float32 else (2e-2 if n == 8 and mfma else 8e-3)
+    # entry).  The n = 8 and n = 16 MFMA kernels keep x_norm in fp32 (the
+    # reference's fused kernel, :209-229), a bf16 rounding of x_norm away: 2e-2.
+    raw_bar = 1e-5 if dtype == torch.float32 else (2e-2 if n >= 8 and mfma else 8e-3)
     assert maxrel(r["h_raw"], o["h_res_raw"]) <= raw_bar
     assert maxrel(r["inv"], o["inv_rms"]) <= 1e-5
     assert maxrel(r["mixes"], o["mixes_raw"]) <= raw_bar
@@ -66,17 +66,19 @@ def test_pre_full_vs_oracle(dev, dtype, n, C, M):
             assert maxabs(r["h_res"].sum(dim), o["h_res"].sum(dim)) <= 1e-5
 
 
-@pytest.mark.parametrize("n,C", [(4, 768), (8, 768), (2, 512)])
+@pytest.mark.parametrize("n,C", [(4, 768), (8, 768), (2, 512), (4, 2048), (2, 1536), (16, 128),
+                                 (8, 1152)])
 def test_pre_mfma_matches_generic(dev, n, C):
     """The MFMA kernel and the generic VALU kernel agree on the same bf16 input.
     Both project x_norm rounded to bf16 (model/mhc_fused.py:845) for n <= 4, so
-    their fp32 mixes differ only in the order of the fp32 sums.  The n = 8
-    kernel projects the unrounded fp32 x_norm (as the reference's fused kernel
-    does), so at n = 8 its mixes sit a bf16 rounding of x_norm away from the
-    generic kernel's: held to the 2e-2 bar of the oracle comparison above."""
+    their fp32 mixes differ only in the order of the fp32 sums.  The n = 8 and
+    n = 16 kernels project the unrounded fp32 x_norm (as the reference's fused
+    kernel does), so there the mixes sit a bf16 rounding of x_norm away from
+    the generic kernel's: held to the 2e-2 bar of the oracle comparison above."""
     a, _, packed = _pre_case(dev, n, C, 48, torch.bfloat16, True, 20, use_pack=True, seed=5)
     b, _, _ = _pre_case(dev, n, C, 48, torch.bfloat16, True, 20, use_pack=False, seed=5)
     assert packed is not None
+    print(f"mfma vs generic n={n} C={C}", flush=True)
     assert maxrel(b["mixes_raw"], a["mixes_raw"]) <= (1e-5 if n <= 4 else 2e-2)
     assert maxrel(b["inv_rms"], a["inv_rms"]) <= 1e-6
     for k in ("sub_in", "h_post", "h_res"):
@@ -84,13 +86,17 @@ def test_pre_mfma_matches_generic(dev, n, C):
 
 
 @pytest.mark.parametrize("n,C,M", [(4, 768, 4096), (2, 512, 4096), (4, 768, 20000),
-                                   (8, 768, 8192), (8, 768, 8200)])
+                                   (8, 768, 8192), (8, 768, 8200), (4, 2048, 2100),
+                                   (2, 1536, 4100), (16, 256, 3000), (16, 768, 1030)])
 def test_pre_mfma_many_workgroups_repeat(dev, n, C, M):
     """Every CU busy, one or more tiles per workgroup, several launches: the
     persistent kernel's output must equal the generic kernel's within bf16
     rounding on every launch and be bit-identical between launches.  (A store
     whose data registers were overwritten before the store read them left
-    zeros in a few lanes only under this kind of load.)"""
+    zeros in a few lanes only under this kind of load.)  n = 8 and n = 16 keep
+    x_norm in fp32: the 2e-2 bar of the oracle comparison."""
+    print(f"many workgroups n={n} C={C} M={M}", flush=True)
+    bar = 1e-2 if n <= 4 else 2e-2
     g = torch.Generator().manual_seed(7 + n + M)
     x = torch.randn(M, n * C, generator=g).to(torch.bfloat16).to(dev)
     p = _to(make_params("full", n, C, torch.bfloat16, g), dev)
@@ -104,7 +110,7 @@ def test_pre_mfma_many_workgroups_repeat(dev, n, C, M):
         o = _ops.pre_full(x, p["phi_weight"], packed, *args)
         torch.cuda.synchronize()
         for k in ("sub_in", "h_post", "h_res"):
-            assert maxrel(ref[k], o[k]) <= 1e-2, (rep, k)
+            assert maxrel(ref[k], o[k]) <= bar, (rep, k)
             if first is not None:
                 assert torch.equal(first[k], o[k]), (rep, k)
         first = first or o
@@ -117,19 +123,24 @@ def test_pre_sinkhorn_iteration_counts(dev, iters):
 
 
 @pytest.mark.parametrize("iters", [0, 1, 2, 7, 20])
-@pytest.mark.parametrize("M", [32, 45])
-def test_pre_n8_sinkhorn_iteration_counts(dev, iters, M):
-    """n = 8, bf16: the MFMA kernel spreads the Sinkhorn iterations over its
-    pre-aggregate rounds; every count (including 0 and 1) must give the
-    reference schedule."""
-    o, r, packed = _pre_case(dev, 8, 768, M, torch.bfloat16, True, iters, use_pack=True)
+@pytest.mark.parametrize("n,C,M", [(8, 768, 32), (8, 768, 45), (16, 128, 16), (16, 64, 21),
+                                   (4, 1536, 40), (2, 2048, 33)])
+def test_pre_kstream_sinkhorn_iteration_counts(dev, iters, n, C, M):
+    """bf16, K-streamed kernel (n = 8, n = 16, and n <= 4 at C > 1024): the
+    Sinkhorn iterations are spread over the pre-aggregate rounds; every count
+    (including 0 and 1) must give the reference schedule."""
+    print(f"kstream sinkhorn n={n} C={C} M={M} iters={iters}", flush=True)
+    o, r, packed = _pre_case(dev, n, C, M, torch.bfloat16, True, iters, use_pack=True)
     assert packed is not None
     assert maxabs(r["h_res"], o["h_res"]) <= 1e-2
-    assert maxrel(r["sub"], o["sub_in"]) <= 1e-2
+    assert maxrel(r["sub"], o["sub_in"]) <= (1e-2 if n <= 4 else 2e-2)
+    if iters >= 1:  # the schedule ends on a column normalisation (bf16 store)
+        assert maxabs(o["h_res"].float().cpu().sum(-2), torch.ones(())) <= n * 2.0 ** -8
 
 
 @pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float32])
-@pytest.mark.parametrize("n,C", [(4, 768), (8, 768), (2, 64), (1, 96), (4, 100), (16, 32)])
+@pytest.mark.parametrize("n,C", [(4, 768), (8, 768), (2, 64), (1, 96), (4, 100), (16, 32),
+                                 (16, 128), (4, 2048)])
 def test_pre_nohres_vs_oracle(dev, dtype, n, C):
     g = torch.Generator().manual_seed(11 + n + C)
     M = 40
@@ -148,7 +159,8 @@ def test_pre_nohres_vs_oracle(dev, dtype, n, C):
 
 
 @pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float32])
-@pytest.mark.parametrize("n,C", [(4, 768), (8, 768), (2, 64), (1, 768), (4, 100), (16, 32)])
+@pytest.mark.parametrize("n,C", [(4, 768), (8, 768), (2, 64), (1, 768), (4, 100), (16, 32),
+                                 (16, 128), (2, 2048)])
 def test_head_vs_oracle(dev, dtype, n, C):
     g = torch.Generator().manual_seed(17 + n + C)
     M = 33
@@ -163,7 +175,8 @@ def test_head_vs_oracle(dev, dtype, n, C):
 
 
 @pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float32])
-@pytest.mark.parametrize("n,C", [(4, 768), (8, 768), (2, 64), (1, 64), (4, 100), (16, 32)])
+@pytest.mark.parametrize("n,C", [(4, 768), (8, 768), (2, 64), (1, 64), (4, 100), (16, 32),
+                                 (16, 768), (16, 100), (16, 30), (4, 2048)])
 @pytest.mark.parametrize("res", [True, False])
 def test_post_vs_oracle(dev, dtype, n, C, res):
     g = torch.Generator().manual_seed(23 + n + C)

@@ -79,3 +79,27 @@ def test_layer_output_random_seeds_bf16_n8(dev, threshold, seed, path):
     with torch.no_grad():
         out = mod(x, f).cpu()
     assert maxrel(ref, out) <= 2e-2, f"seed {seed}: {maxrel(ref, out):.3e}"
+
+
+@pytest.mark.parametrize("n,C,bar", [(4, 2048, 1e-2), (2, 1536, 1e-2), (16, 256, 2e-2)])
+@pytest.mark.parametrize("seed", range(4))
+def test_layer_output_random_seeds_wide_bf16(dev, n, C, bar, seed):
+    """The shapes only the K-streamed kernel serves (C > 1024, n = 16), at the
+    batch of the seeds above with stress gates: n <= 4 rounds x_norm as the
+    PyTorch path does and holds the 1e-2 bar; n = 16 keeps x_norm in fp32, as
+    n = 8 does, and is held to 2e-2."""
+    g = torch.Generator().manual_seed(2000 + seed)
+    p = make_params("full", n, C, BF, g, stress=True)
+    x = torch.randn(2, 32, n * C, generator=g).to(BF)
+    fw = (torch.randn(C, C, generator=g) * 0.03).to(BF)
+    mod = MHCConnection_Fused(n, C, sinkhorn_iters=20).to(BF)
+    with torch.no_grad():
+        for k, v in p.items():
+            getattr(mod, k).copy_(v)
+    mod = mod.to(dev)
+    ref = R.mhc_full_forward(x, p, lambda z: z @ fw.t(), n, C, sinkhorn_iters=20)["out"]
+    fwd = fw.t().contiguous().to(dev)
+    print(f"wide seeds n={n} C={C} seed={seed}", flush=True)
+    with torch.no_grad():
+        out = mod(x.to(dev), lambda z: z @ fwd).cpu()
+    assert maxrel(ref, out) <= bar, f"seed {seed}: {maxrel(ref, out):.3e}"
