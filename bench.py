@@ -25,7 +25,8 @@ gradients), each against its algorithmic bytes, plus the fwd + bwd tokens/s of
 the connection (F excluded); `fp32_layout`: the forward and backward launches
 at the config-2 shape in the reference trainers' layout (fp32 stream, phi and
 gates, bf16 F under autocast); `other_configs`: the same kernel pair at config
-5's n = 8 shape and config 4's 64-token shape; and the end-to-end model
+5's n = 8 shape, config 4's 64-token shape, and the widest shapes the
+reference's module accepts (dim 2048 at n = 4, n = 16 at dim 768); and the end-to-end model
 figures: `e2e_prefill` (config 3), `e2e_decode` (config 4, eager and
 HIP-graph replay) and `e2e_prefill_moe` (config 5).
 
@@ -599,13 +600,18 @@ def isolated_configs(steps: int, warmup: int):
     """The isolated pre + post kernel pair at the other BASELINE shapes:
     config 5's n = 8 connection (B=4, T=2048: 8192 tokens, phi [6144, 80],
     8x8 Sinkhorn) and config 4's decode shape (64 tokens, n = 4), where the
-    pair is launch-bound; timed as bench_mhc times config 2."""
+    pair is launch-bound; and at the widest shapes the reference's module
+    accepts (model/mhc_fused.py:599-600, :784): dim 2048 at n = 4 and n = 16
+    at dim 768, 16384 tokens each (K-streamed pre kernel; one-wave-per-token
+    post kernel at n = 16).  Timed as bench_mhc times config 2."""
     out = {}
-    for key, n, M, sets in (("c5_n8_M8192", 8, 8192, 4), ("c4_n4_M64", 4, 64, 8)):
-        r, _ = bench_mhc(steps, warmup, sets=sets, n=n, M=M, cold=False)
-        pre_b, post_b = algorithmic_bytes(n, C_DIM, M)
+    for key, n, C, M, sets in (("c5_n8_M8192", 8, C_DIM, 8192, 4), ("c4_n4_M64", 4, C_DIM, 64, 8),
+                               ("wide_n4_C2048_M16384", 4, 2048, TOKENS, 4),
+                               ("wide_n16_C768_M16384", 16, C_DIM, TOKENS, 4)):
+        r, _ = bench_mhc(steps, warmup, sets=sets, n=n, C=C, M=M, cold=False)
+        pre_b, post_b = algorithmic_bytes(n, C, M)
         t = r["t_pre"] + r["t_post"]
-        out[key] = {"n": n, "C": C_DIM, "tokens": M,
+        out[key] = {"n": n, "C": C, "tokens": M,
                     "pre_ms": round(r["t_pre"], 5), "post_ms": round(r["t_post"], 5),
                     "pre_GBps": round(pre_b / (r["t_pre"] * 1e-3) / 1e9, 1),
                     "post_GBps": round(post_b / (r["t_post"] * 1e-3) / 1e9, 1),
