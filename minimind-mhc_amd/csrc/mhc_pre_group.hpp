@@ -198,14 +198,11 @@ __global__ __launch_bounds__(kGrpWaves * 64) void pre_group_kernel(PreArgs a, in
     for (int w = 0; w < kGrpWaves; ++w) sq += sh.ss[w][tt];
     return 1.0f / sqrtf(sq / nc + a.rms_eps);
   };
-  // n <= 4: the projection runs on x_norm = bf16(x * inv_rms), rounded as the
+  // The projection runs on x_norm = bf16(x * inv_rms), rounded as the
   // reference rounds it (model/mhc_fused.py:845), so the sums of squares come
-  // first (in pre_persist_kernel's order), then a barrier, then the MFMAs.
-  // n = 8 keeps pre_kstream_kernel's arithmetic: the MFMAs on x, the sums of
-  // squares beside them, and the fp32 result scaled by inv_rms.
-  constexpr bool XN = N <= 4;
-  float ss = 0.f;
-  if constexpr (XN) {
+  // first (in the large-batch kernel's order), then a barrier, then the MFMAs.
+  {
+    float ss = 0.f;
 #pragma unroll
     for (int b = 0; b < P::NB; ++b) {
       const U32x4 v = a_of(b);
@@ -215,29 +212,20 @@ __global__ __launch_bounds__(kGrpWaves * 64) void pre_group_kernel(PreArgs a, in
     ss += __shfl_xor(ss, 16, 64);
     ss += __shfl_xor(ss, 32, 64);
     if (g == 0 && r < G) sh.ss[wave][r] = ss;
-    __syncthreads();  // sums of squares visible
   }
-  const float inv_r = XN ? inv_of(r < G ? r : 0) : 1.0f;
+  __syncthreads();  // sums of squares visible
+  const float inv_r = inv_of(r < G ? r : 0);
   f32x4_t acc[NT];
 #pragma unroll
   for (int nt = 0; nt < NT; ++nt) acc[nt] = f32x4_t{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
   for (int b = 0; b < P::NB; ++b) {
-    const U32x4 v = a_of(b);
-    if constexpr (!XN) {
-#pragma unroll
-      for (int j = 0; j < 4; ++j) ss = dot2_bf16(v.v[j], v.v[j], ss);
-    }
-    const bf16x8_t av = __builtin_bit_cast(bf16x8_t, XN ? x_norm_chunk(v, inv_r) : v);
+    const bf16x8_t av = __builtin_bit_cast(bf16x8_t, x_norm_chunk(a_of(b), inv_r));
 #pragma unroll
     for (int nt = 0; nt < NT; ++nt)
       acc[nt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(av, __builtin_bit_cast(bf16x8_t, wq[b % P::P][nt]),
                                                          acc[nt], 0, 0, 0);
     if (b + P::P < P::NB) issue(b + P::P);
-  }
-  if constexpr (!XN) {
-    ss += __shfl_xor(ss, 16, 64);
-    ss += __shfl_xor(ss, 32, 64);
   }
   // MFMA 16x16 result layout: lane l holds D[4*(l/16) + j][l % 16], j = 0..3.
 #pragma unroll
@@ -246,16 +234,15 @@ __global__ __launch_bounds__(kGrpWaves * 64) void pre_group_kernel(PreArgs a, in
 #pragma unroll
       for (int j = 0; j < 4; ++j)
         if (4 * g + j < G) sh.acc[wave][4 * g + j][nt * 16 + r] = acc[nt][j];
-  if (!XN && g == 0 && r < G) sh.ss[wave][r] = ss;
   __syncthreads();  // partials visible
 
   // ---- gates straight from the partials, no further barrier ------------------
-  // (n <= 4: the partials are already normalised; mix_of's scale is 1.)
-  auto mix_of = [&](int tt, int f, float inv) {
+  // (the partials are already normalised).
+  auto mix_of = [&](int tt, int f, float) {
     float sum = 0.f;
 #pragma unroll
     for (int w = 0; w < kGrpWaves; ++w) sum += sh.acc[w][tt][f];
-    return XN ? sum : sum * inv;
+    return sum;
   };
   // Every wave: h_pre of the group's tokens, lane = (token, stream).
   const int sk_waves = MODE == kFull && a.h_res ? (G + P::SK_TOK - 1) / P::SK_TOK : 0;

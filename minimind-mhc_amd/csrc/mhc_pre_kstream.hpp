@@ -11,11 +11,13 @@
 //     feeds MB MFMAs.  KS = 8, except at n = 16 with H_res (18 output tiles of
 //     16 columns): there two waves share each chunk, one per half of the output
 //     tiles (KS = 4), so a wave's operands and accumulators stay in registers;
+//   * a first pass over the wave's chunks forms each row's sum of squares
+//     (bf16 dot2), so the projection can run on x_norm = bf16(x * inv_rms),
+//     rounded as the PyTorch path rounds it (model/mhc_fused.py:845);
 //   * the K loop keeps D chunks in flight per wave: each chunk is MB 16-byte x
 //     loads (16 tokens x 32 columns per M-block, the MFMA A operands) and NTW
 //     16-byte phi loads (the packed B operands, 16 output columns each);
-//     v_mfma_f32_16x16x32_bf16 accumulates, bf16 dot2 forms the sum of
-//     squares;
+//     v_mfma_f32_16x16x32_bf16 accumulates;
 //   * the K-split partials meet in LDS.  The pre-aggregate's re-reads of the
 //     tile's x (from the Infinity Cache: it has left L2 by then) need no
 //     result of the projection, so its first two rounds go out before the
@@ -32,12 +34,9 @@
 //     LDS; after the rounds the token's lanes sum their squares, and a last
 //     pass scales, rounds and stores them.  Wider rows take a second launch
 //     (the RMSNorm in place on the written sublayer input).
-// Arithmetic and rounding points as pre_persist_kernel.  For n <= 4 that
-// includes x_norm = bf16(x * inv_rms) (model/mhc_fused.py:845): a first pass
-// over the tile's x forms each row's sum of squares (read again by the K
-// loop).  n = 8 and n = 16 skip that third read of x: their MFMAs run on x and
-// the fp32 result is scaled by inv_rms, the way the reference's fused kernel
-// computes x_norm (model/mhc_fused.py:209-229).
+// Arithmetic and rounding points as pre_persist_kernel.  The tile's x is read
+// three times (sums of squares, K loop, pre-aggregate), the second and third
+// mostly from the Infinity Cache.
 //
 // Reference semantics: model/mhc_fused.py:163-268, :533-559, :47-56;
 // model/mhc_fused_no_hres.py:48-145; model/mhc_common.py:128-195.
@@ -66,7 +65,6 @@ struct KsPlan {
   static constexpr int TPW = 64 / LPT;               // tokens per wave
   static constexpr int D = 3;                        // chunks in flight per wave
   static constexpr int PB = N >= 16 ? 1 : 2;         // pre-aggregate items per lane per round
-  static constexpr bool XN = N <= 4;                 // projection on bf16(x * inv_rms)
   static constexpr int SD = 4;                       // chunks in flight in the sums-of-squares pass
   static constexpr int SKV = G > LPT ? G / LPT : 1;  // Sinkhorn values per lane
   static constexpr int SKL = G / SKV;                // lanes holding distinct h_res values
@@ -215,11 +213,18 @@ __global__ __launch_bounds__(kKsWaves * 64) void pre_kstream_kernel(PreArgs a) {
   U32x4 ws[D][NTW];
   // Workgroups walk their chunks in rotated orders, so the CUs of an XCD do
   // not all read the same few phi lines from the same L2 channels at once.
+  // Slot j of this wave is chunk kq + KS * ((j + rot) mod NJ); slots past NJ
+  // read nothing.
   const int rot = (int)(blockIdx.x % (unsigned)NJ);
-  auto issue = [&](int slot_j, U32x4 (&xd)[P::MB], U32x4 (&wd)[NTW]) {
+  auto chunk_of = [&](int slot_j, bool& live) {
     const int jr = slot_j < NJ ? (slot_j + rot < NJ ? slot_j + rot : slot_j + rot - NJ) : slot_j;
-    const int k = kq + P::KS * jr;              // uniform
-    const bool live = slot_j < NJ && k < NCH;
+    const int k = kq + P::KS * jr;  // uniform
+    live = slot_j < NJ && k < NCH;
+    return k;
+  };
+  auto issue = [&](int slot_j, U32x4 (&xd)[P::MB], U32x4 (&wd)[NTW]) {
+    bool live;
+    const int k = chunk_of(slot_j, live);
     x_chunk(k, live, xd);
 #pragma unroll
     for (int nt = 0; nt < NTW; ++nt) {
@@ -232,34 +237,40 @@ __global__ __launch_bounds__(kKsWaves * 64) void pre_kstream_kernel(PreArgs a) {
 #pragma unroll
   for (int d = 0; d < D; ++d) issue(d, xs[d], ws[d]);
 
-  float ss[P::MB];
-#pragma unroll
-  for (int m = 0; m < P::MB; ++m) ss[m] = 0.f;
-  // n <= 4: sums of squares first (this wave's chunks, SD in flight), then
-  // each row's inv_rms for x_norm.  The K loop's first chunks are in flight.
+  // ---- sums of squares, then each row's inv_rms --------------------------------
+  // A first pass over this wave's chunks in the K loop's order (SD in flight;
+  // the K loop's first chunks are already out): lane (g, r) chains the dot2
+  // squares of its 8 columns of row r, then the 16-lane groups are summed and
+  // the K-split partials meet in LDS.  pre_group_kernel forms the same sums in
+  // the same order.  At n = 16 the waves of the second output-tile half read
+  // the same chunks as the first and skip the pass.
   float inv_r[P::MB];
+  {
+    float ss[P::MB];
 #pragma unroll
-  for (int m = 0; m < P::MB; ++m) inv_r[m] = 1.0f;
-  if constexpr (P::XN) {
-    for (int j0 = 0; j0 < NJ; j0 += P::SD) {  // uniform trip count
-      U32x4 v[P::SD][P::MB];
+    for (int m = 0; m < P::MB; ++m) ss[m] = 0.f;
+    if (P::NH == 1 || nh == 0) {  // uniform
+      for (int j0 = 0; j0 < NJ; j0 += P::SD) {  // uniform trip count
+        U32x4 v[P::SD][P::MB];
 #pragma unroll
-      for (int d = 0; d < P::SD; ++d) {
-        const int k = kq + P::KS * (j0 + d);
-        x_chunk(k, j0 + d < NJ && k < NCH, v[d]);
+        for (int d = 0; d < P::SD; ++d) {
+          bool live;
+          const int k = chunk_of(j0 + d, live);
+          x_chunk(k, live, v[d]);
+        }
+#pragma unroll
+        for (int d = 0; d < P::SD; ++d)
+#pragma unroll
+          for (int m = 0; m < P::MB; ++m)
+#pragma unroll
+            for (int q = 0; q < 4; ++q) ss[m] = dot2_bf16(v[d][m].v[q], v[d][m].v[q], ss[m]);
       }
 #pragma unroll
-      for (int d = 0; d < P::SD; ++d)
-#pragma unroll
-        for (int m = 0; m < P::MB; ++m)
-#pragma unroll
-          for (int q = 0; q < 4; ++q) ss[m] = dot2_bf16(v[d][m].v[q], v[d][m].v[q], ss[m]);
-    }
-#pragma unroll
-    for (int m = 0; m < P::MB; ++m) {
-      ss[m] += __shfl_xor(ss[m], 16, 64);
-      ss[m] += __shfl_xor(ss[m], 32, 64);
-      if (g == 0) sh.ss[kq][m * 16 + r] = ss[m];
+      for (int m = 0; m < P::MB; ++m) {
+        ss[m] += __shfl_xor(ss[m], 16, 64);
+        ss[m] += __shfl_xor(ss[m], 32, 64);
+        if (g == 0) sh.ss[kq][m * 16 + r] = ss[m];
+      }
     }
     __syncthreads();  // sums of squares visible
 #pragma unroll
@@ -271,23 +282,18 @@ __global__ __launch_bounds__(kKsWaves * 64) void pre_kstream_kernel(PreArgs a) {
     }
   }
 
+  // ---- K loop: MFMAs on x_norm = bf16(x * inv_rms) ----------------------------
   f32x4_t acc[P::MB][NTW];
 #pragma unroll
   for (int m = 0; m < P::MB; ++m)
 #pragma unroll
     for (int nt = 0; nt < NTW; ++nt) acc[m][nt] = f32x4_t{0.f, 0.f, 0.f, 0.f};
-  const bool ss_here = !P::XN && (P::NH == 1 || nh == 0);  // uniform
   for (int j0 = 0; j0 < NJ; j0 += D) {   // uniform trip count
 #pragma unroll
     for (int d = 0; d < D; ++d) {
 #pragma unroll
       for (int m = 0; m < P::MB; ++m) {
-        const U32x4 v = xs[d][m];
-        if (ss_here) {
-#pragma unroll
-          for (int q = 0; q < 4; ++q) ss[m] = dot2_bf16(v.v[q], v.v[q], ss[m]);
-        }
-        const bf16x8_t av = __builtin_bit_cast(bf16x8_t, P::XN ? x_norm_chunk(v, inv_r[m]) : v);
+        const bf16x8_t av = __builtin_bit_cast(bf16x8_t, x_norm_chunk(xs[d][m], inv_r[m]));
 #pragma unroll
         for (int nt = 0; nt < NTW; ++nt)
           acc[m][nt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(
@@ -299,11 +305,6 @@ __global__ __launch_bounds__(kKsWaves * 64) void pre_kstream_kernel(PreArgs a) {
   // MFMA 16x16 result layout: lane l holds D[4*(l/16) + j][l % 16], j = 0..3.
 #pragma unroll
   for (int m = 0; m < P::MB; ++m) {
-    if (ss_here) {
-      ss[m] += __shfl_xor(ss[m], 16, 64);
-      ss[m] += __shfl_xor(ss[m], 32, 64);
-      if (g == 0) sh.ss[kq][m * 16 + r] = ss[m];
-    }
 #pragma unroll
     for (int nt = 0; nt < NTW; ++nt) {
       const int ntg = nh * NTW + nt;
@@ -382,14 +383,13 @@ __global__ __launch_bounds__(kKsWaves * 64) void pre_kstream_kernel(PreArgs a) {
 #pragma unroll
   for (int w = 0; w < P::KS; ++w) sq += sh.ss[w][tt];
   const float inv = 1.0f / sqrtf(sq / (float)NC + a.rms_eps);
-  const float msc = P::XN ? 1.0f : inv;  // the n <= 4 partials are already normalised
   if (jl == 0 && ok && a.inv_rms) a.inv_rms[tk] = inv;
   constexpr int NMIX = FD < 2 * N ? FD : 2 * N;  // pre (and post) mixes
   if (jl < NMIX) {
     float sum = 0.f;
 #pragma unroll
     for (int w = 0; w < P::KS; ++w) sum += sh.acc[w][tt][jl];
-    const float m = sum * msc;
+    const float m = sum;  // the partials are already normalised
     if (ok && a.mixes_raw) a.mixes_raw[tk * FD + jl] = m;
     // bias_pre[j] and bias_post[j - N] are adjacent: GP::kBiasPre + j for both
     const bool pre = jl < N;
@@ -429,7 +429,7 @@ __global__ __launch_bounds__(kKsWaves * 64) void pre_kstream_kernel(PreArgs a) {
     }
 #pragma unroll
     for (int q = 0; q < SKV; ++q) {
-      const float m = s[q] * msc;
+      const float m = s[q];
       if (ok && own && a.mixes_raw) a.mixes_raw[tk * FD + 2 * N + e0 + q] = m;
       v[q] = gate_res(m, sh.prm[2], sh.prm[GP::kBiasRes + e0 + q], kBF16);
       if (ok && own && a.h_res_raw) st_any(a.h_res_raw, tk * P::G + e0 + q, kBF16, v[q]);

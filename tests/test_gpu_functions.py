@@ -63,10 +63,10 @@ def test_pre_phase_full_fn_forward(dev, dtype, n, C, M):
     assert maxrel(r_sub, sub) <= bar
     assert maxrel(r_pre, h_pre) <= bar
     assert maxrel(r_post, h_post) <= bar
-    # h_res_raw = alpha_res * m + bias_res: the oracle rounds x_norm and m to bf16,
-    # the kernels keep them fp32 as the reference's fused kernel does
-    # (model/mhc_fused.py:209-245); one bf16 step of the largest entry is 2**-8.
-    assert maxrel(r_raw, h_raw) <= (2e-2 if dtype == torch.bfloat16 else 1e-5)
+    # h_res_raw = alpha_res * m + bias_res: the kernels round x_norm to bf16 as
+    # the oracle does (model/mhc_fused.py:845) but keep m in fp32 where the
+    # oracle rounds it to bf16 (:546); one bf16 step of the largest entry is 2**-8.
+    assert maxrel(r_raw, h_raw) <= (8e-3 if dtype == torch.bfloat16 else 1e-5)
 
 
 @pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float32])

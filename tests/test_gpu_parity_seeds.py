@@ -1,20 +1,16 @@
-"""Layer-output parity on many random seeds at C = 768 with stress gates.
+"""Layer-output parity on many random seeds with stress gates.
 
 The bf16 bar, max|out - ref| / max|ref| <= 1e-2 (the reference's comparator,
 model/mhc_fused.py:871-876), is under two bf16 steps of the largest output
 element, so any intermediate that differs from the PyTorch path in its last
 bit can cost that much.  With the projection run on x_norm rounded to bf16 as
-the PyTorch path rounds it (model/mhc_fused.py:845), the n <= 4 kernels (the
-persistent large-batch kernel and the small-batch group kernel) reproduce its
-mixes, gates and pre-aggregate, and the layer output stays inside the bar on
-every seed; most outputs are bit-identical.
-
-The n = 8 kernels keep x_norm in fp32, as the reference's fused kernel does
-(model/mhc_fused.py:209-229).  Their mixes then differ from the PyTorch path's
-in the last bf16 bit on a sizeable share of entries, and on a few seeds the
-layer output lands above 1e-2 (up to ~1.5e-2); they are held to the 2e-2 bar the
-reference's own end-to-end test uses between its fused and PyTorch paths
-(model/mhc_fused.py:1098).
+the PyTorch path rounds it (model/mhc_fused.py:845), every MFMA kernel (the
+persistent and K-streamed large-batch kernels and the small-batch group
+kernel) reproduces its mixes, gates and pre-aggregate, and the layer output
+stays inside the bar on every seed; most outputs are bit-identical.  (Kept in
+fp32, as the reference's fused kernel keeps it, model/mhc_fused.py:209-229,
+x_norm put the n = 8 layer output above the bar on 2 of 24 seeds, up to
+~1.5e-2.)
 """
 from __future__ import annotations
 
@@ -78,16 +74,18 @@ def test_layer_output_random_seeds_bf16_n8(dev, threshold, seed, path):
     print(f"seeds n=8 seed={seed} path={path}", flush=True)
     with torch.no_grad():
         out = mod(x, f).cpu()
-    assert maxrel(ref, out) <= 2e-2, f"seed {seed}: {maxrel(ref, out):.3e}"
+    err = maxrel(ref, out)
+    differ = (out.float() != ref.float()).float().mean().item()
+    assert err <= tol(BF), f"seed {seed}: {err:.3e}"
+    assert differ <= 1e-2, f"seed {seed}: {differ:.2%} of outputs differ"
 
 
-@pytest.mark.parametrize("n,C,bar", [(4, 2048, 1e-2), (2, 1536, 1e-2), (16, 256, 2e-2)])
+@pytest.mark.parametrize("n,C", [(4, 2048), (2, 1536), (16, 256), (8, 2048)])
 @pytest.mark.parametrize("seed", range(4))
-def test_layer_output_random_seeds_wide_bf16(dev, n, C, bar, seed):
+def test_layer_output_random_seeds_wide_bf16(dev, n, C, seed):
     """The shapes only the K-streamed kernel serves (C > 1024, n = 16), at the
-    batch of the seeds above with stress gates: n <= 4 rounds x_norm as the
-    PyTorch path does and holds the 1e-2 bar; n = 16 keeps x_norm in fp32, as
-    n = 8 does, and is held to 2e-2."""
+    batch of the seeds above with stress gates, at the 1e-2 bar."""
+    bar = tol(BF)
     g = torch.Generator().manual_seed(2000 + seed)
     p = make_params("full", n, C, BF, g, stress=True)
     x = torch.randn(2, 32, n * C, generator=g).to(BF)
