@@ -80,7 +80,7 @@ struct GroupShared {
 };
 
 template <int N, int MODE, int KB, bool NORM>
-__global__ __launch_bounds__(kGrpWaves * 64) void pre_group_kernel(PreArgs a, int G) {
+__global__ __launch_bounds__(kGrpWaves * 64) void pre_group_kernel(PreArgs a, int G, int row_ss) {
   using P = GroupPlan<N, MODE, KB>;
   using GP = GateParams<N>;
   constexpr int FD = P::FD;
@@ -201,7 +201,23 @@ __global__ __launch_bounds__(kGrpWaves * 64) void pre_group_kernel(PreArgs a, in
   // The projection runs on x_norm = bf16(x * inv_rms), rounded as the
   // reference rounds it (model/mhc_fused.py:845), so the sums of squares come
   // first (in the large-batch kernel's order), then a barrier, then the MFMAs.
-  {
+  if (row_ss) {  // uniform
+    // The row-staged persistent kernel's order (persist_row_sumsq): lane l
+    // chains the row's chunks at bytes 16 l + 1024 k (the row is a whole
+    // number of 1 KiB pieces) in k order, then the wave butterfly.  The total
+    // goes to ss[0], the other waves' partials are zero.
+    for (int t = wave; t < G; t += kGrpWaves) {  // uniform
+      float s = 0.f;
+      for (int k = 0; k < NC / 512; ++k) {
+        const U32x4 v = *reinterpret_cast<const U32x4*>(&sh.xs[t][k * 512 + lane * 8]);
+#pragma unroll
+        for (int j = 0; j < 4; ++j) s = dot2_bf16(v.v[j], v.v[j], s);
+      }
+      s = wave_sum(s);
+      if (lane == 0) sh.ss[0][t] = s;
+    }
+    if (wave > 0 && g == 0 && r < G) sh.ss[wave][r] = 0.f;
+  } else {
     float ss = 0.f;
 #pragma unroll
     for (int b = 0; b < P::NB; ++b) {
@@ -431,12 +447,19 @@ template <int N, int MODE, int KB>
 hipError_t launch_pre_group_inst(const PreArgs& a, int num_cus, hipStream_t s) {
   const int G = group_tokens<N, MODE, KB>(a.M, num_cus);
   const int64_t grid = (a.M + G - 1) / G;
+  // Sum the squares in the order of the large-batch kernel this shape would
+  // run: row order where launch_pre_persist_inst picks row staging.
+  int row_ss = 0;
+  if constexpr (N <= 4) {
+    if constexpr (PersistRow<N, MODE, KB>::OK)
+      row_ss = !a.norm_w && a.C == 256 * KB && pre_row_staging() ? 1 : 0;
+  }
   if (a.norm_w)
     hipLaunchKernelGGL((pre_group_kernel<N, MODE, KB, true>), dim3((unsigned)grid),
-                       dim3(kGrpWaves * 64), 0, s, a, G);
+                       dim3(kGrpWaves * 64), 0, s, a, G, row_ss);
   else
     hipLaunchKernelGGL((pre_group_kernel<N, MODE, KB, false>), dim3((unsigned)grid),
-                       dim3(kGrpWaves * 64), 0, s, a, G);
+                       dim3(kGrpWaves * 64), 0, s, a, G, row_ss);
   return hipGetLastError();
 }
 

@@ -44,8 +44,10 @@
 //     also wait for the prefetch.  Gate scalars and biases are read once, with
 //     branch-free loads issued before everything else, and kept in LDS as fp32.
 //
-// Per tile, two workgroup barriers (three with row staging):
-//   0. all waves: partial sums of squares of the tile's rows -> LDS;
+// Per tile, two workgroup barriers:
+//   0. all waves: partial sums of squares of the tile's rows -> LDS (with row
+//      staging: each wave's two whole rows, from the row-layout registers,
+//      beside the tile's copy into LDS);
 //   -- barrier --
 //   1. all waves: inv_rms of each row, x_norm, MFMA partial projections -> LDS
 //      (two slots, alternating per tile, so a fast wave may start the next
@@ -199,7 +201,9 @@ struct PersistRow {
   // 30.0-31.3 to 29.6 us; 4/9, 3/9 and 5/10 measured the same, 4/11 slower.
   static constexpr int R1 = (PW + 2) / 3;
   static constexpr int R2 = 5 * PW / 6;
-  static constexpr bool OK = P::NREG == P::NT && RCH % 16 == 0 &&
+  // A row is a whole number of 1 KiB pieces (n * KB even), so each wave holds
+  // two whole rows and every lane the same columns of both (persist_row_sumsq).
+  static constexpr bool OK = P::NREG == P::NT && RCH % 16 == 0 && (NC * 2) % 1024 == 0 &&
                              P::SHARED + 256 + BYTES <= kLdsBytes;
 };
 
@@ -339,6 +343,36 @@ __device__ __forceinline__ void persist_sumsq(PersistShared<N, FD>& sh, const U3
   ss += __shfl_xor(ss, 16, 64);
   ss += __shfl_xor(ss, 32, 64);
   if (g == 0) sh.ss[slot][wave][r] = ss;
+}
+
+// ---- row staging, phase 0: the sums of squares of this wave's two rows.
+// The tile arrives in row layout: wave w holds rows 2w and 2w + 1 as pieces
+// [0, PW/2) and [PW/2, PW) of 1 KiB, lane l holding bytes 16 l .. 16 l + 15 of
+// each piece.  Lane l chains the dot2 squares of its chunks of each row in
+// piece order, a wave butterfly (wave_sum) adds the lanes, and lane 0 writes
+// the totals to ss[slot][0][row].  ss[slot][1..7] hold zeros (set at launch),
+// so persist_inv_rms adds each total to zeros: exact.  pre_group_kernel sums
+// in this order when the persistent kernel would stage rows.
+template <int N, int MODE, int KB, int FD>
+__device__ __forceinline__ void persist_row_sumsq(PersistShared<N, FD>& sh, const U32x4 (&xn)[KB][N],
+                                                  int slot, int wave, int lane) {
+  using RW = PersistRow<N, MODE, KB>;
+  static_assert(RW::PW % 2 == 0, "whole pieces per row");
+  float s0 = 0.f;
+  float s1 = 0.f;
+#pragma unroll
+  for (int p = 0; p < RW::PW; ++p) {
+    const U32x4 v = xn[p / N][p % N];
+    float& s = p < RW::PW / 2 ? s0 : s1;  // compile-time after unrolling
+#pragma unroll
+    for (int j = 0; j < 4; ++j) s = dot2_bf16(v.v[j], v.v[j], s);
+  }
+  s0 = wave_sum(s0);
+  s1 = wave_sum(s1);
+  if (lane == 0) {
+    sh.ss[slot][0][2 * wave] = s0;
+    sh.ss[slot][0][2 * wave + 1] = s1;
+  }
 }
 
 // ---- phase 1: projection partials (MFMA) of x_norm -> LDS.  The A operand is
@@ -623,12 +657,14 @@ __device__ __forceinline__ void persist_step(
 }
 
 // One tile with row staging: xn holds the tile in row layout (its loads were
-// issued during the previous step); it goes to LDS, xn takes the next tile's
-// loads in three parts along the step (at its start, spread through the
-// projection, spread through the pre-aggregate), and the operand registers xr
-// are read back from LDS.  One more barrier orders the LDS writes before the
-// reads; the previous step's partials barrier orders this step's writes after
-// every wave's previous reads.  (Overlapping two tiles' loads, with the LDS tile
+// issued during the previous step); it goes to LDS, each wave sums the squares
+// of its two rows from xn, xn takes the next tile's loads in three parts along
+// the step (at its start, spread through the projection, spread through the
+// pre-aggregate), and the operand registers xr are read back from LDS.  The
+// first barrier orders the LDS writes (tile and row sums) before the reads;
+// the previous step's partials barrier orders this step's writes after every
+// wave's previous reads.  (The row sums replace the operand-layout partial
+// sums and the barrier after them: C2 pre 31.4 -> 29.9 us on MI355X.)  (Overlapping two tiles' loads, with the LDS tile
 // taking the next tile's first batch once read, measured slower: the extra
 // loads in flight stall the issuing waves.)
 template <int N, int MODE, int KB>
@@ -643,11 +679,10 @@ __device__ __forceinline__ void persist_step_row(
   const auto rn = x_tile_rsrc(static_cast<const uint16_t*>(a.x), tile + gridDim.x, ntiles, a.M,
                               N * a.C);
   persist_row_to_lds<N, MODE, KB, 0, RW::PW>(xl, xn, wave, lane);
+  persist_row_sumsq<N, MODE, KB>(sh, xn, slot, wave, lane);
   persist_load_row<N, MODE, KB, 0, RW::R1>(xn, rn, wave, lane);
-  __syncthreads();
+  __syncthreads();  // the tile in LDS and its row sums of squares visible
   persist_lds_to_operands<N, MODE, KB>(xl, xr, wave, lane);
-  persist_sumsq(sh, xr, slot, lane, wave);
-  __syncthreads();  // sums of squares visible
   persist_project<N, MODE, KB, false>(a, sh, xr, wreg, lds_w, slot, lane, wave,
                                       RowIssue<N, MODE, KB, RW::R1, RW::R2>{xn, rn, wave, lane});
   __syncthreads();  // partials visible
@@ -802,6 +837,11 @@ __global__ __launch_bounds__(kPersistWaves * 64) void pre_persist_kernel(PreArgs
   if constexpr (!P::X_EARLY && !ROW) persist_load_part<N, KB, 0, KB>(xa, r0, C, wave, r, g);
 
   if (tid == 0) sh.zero = U32x4{{0u, 0u, 0u, 0u}};
+  if constexpr (ROW) {  // the row sums live in ss[slot][0]; the other partials stay zero
+    constexpr int kRest = 2 * (kPersistWaves - 1) * kTokTile;
+    if (tid < kRest)
+      sh.ss[tid / ((kPersistWaves - 1) * kTokTile)][1 + (tid / kTokTile) % (kPersistWaves - 1)][tid % kTokTile] = 0.f;
+  }
   if (tid < GateParams<N>::kCount) sh.prm[tid] = convert_param(rp, a.param_dtype);
   if constexpr (NORM) {
 #pragma unroll

@@ -182,16 +182,31 @@ def test_fused_norm_matches_plain_then_rmsnorm(dev, kind, n, C, M, dtype, gain_f
     # call the fp32 VALU kernel (the split kernel has no norm epilogue), so the
     # two agree at the fp32 bar rather than bit for bit.
     split = dtype == torch.float32 and kind != "head" and n in (1, 2, 4)
+    # bf16, n <= 4, C a multiple of 256: the plain call's kernels sum each row's
+    # squares in row order (the persistent kernel's row staging, which has no
+    # norm epilogue), the normed call's in MFMA-operand order.  inv_rms may then
+    # differ in its last bit, and through x_norm a mix or gate by a rounding
+    # step on a few tokens; the other shapes agree bit for bit.
+    row_order = dtype == torch.bfloat16 and n in (1, 2, 4) and C % 256 == 0 and C <= 1024
+    ref = _norm_ref(plain["sub_in"], w, eps).reshape(M, C)
+    got = fused["sub_in"].reshape(M, C)
+    same = torch.ones(M, dtype=torch.bool, device=got.device)  # tokens with bit-identical mixes
     for k, v in plain.items():
         if k != "sub_in" and v is not None:
             if split:
                 assert maxrel(v, fused[k]) <= 1e-5, k
+            elif row_order:  # inv_rms: its last bit; a flipped x_norm element: a bf16 step
+                assert maxrel(v, fused[k]) <= (1e-6 if k == "inv_rms" else 8e-3), k
+                if k != "inv_rms":  # equal mixes: equal gates and pre-aggregate
+                    same &= (v == fused[k]).reshape(M, -1).all(-1)
             else:
                 assert torch.equal(v, fused[k]), k
     if split:  # different pre-aggregates upstream: the fp32 max-norm bar
-        assert maxrel(_norm_ref(plain["sub_in"], w, eps), fused["sub_in"]) <= 1e-5
+        assert maxrel(ref, got) <= 1e-5
     else:
-        _assert_rounded_close(fused["sub_in"], _norm_ref(plain["sub_in"], w, eps), dtype)
+        assert same.float().mean().item() >= 0.5  # the order changes few tokens' gates
+        _assert_rounded_close(got[same], ref[same], dtype)
+        assert maxrel(ref, got) <= tol(dtype)
 
 
 @pytest.mark.parametrize("M", [1, 17, 300])

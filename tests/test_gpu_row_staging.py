@@ -1,14 +1,19 @@
 """The persistent pre kernel with row-staged x tiles (whole-row loads through an
 LDS transpose, mhc_pre_row_staging on) against the same kernel loading the
-MFMA operand layout directly (off): every output bit for bit, since both feed
-the same operands to the same MFMA, dot2 and pre-aggregate sequence.  The
-operand-layout path is itself pinned against the oracle by the other GPU
-tests; here the sampled outputs are also checked against the oracle at the
-BASELINE bars.  Shapes: C a multiple of 256 (the shapes row staging takes:
-n in {1, 2, 4}, C in {256, 512, 768, 1024}, modes full / no-H_res / head),
-batches with a ragged last tile, fewer tiles than CUs, several tiles per CU
-and the C2 size, plus shapes it does not take (C % 256 != 0, fused norm),
-which must be unaffected by the setting."""
+MFMA operand layout directly (off).  Both feed the same operands to the same
+MFMA and pre-aggregate sequence; the row-staged kernel sums each row's squares
+from its whole-row registers, in row order, where the operand-layout kernel
+sums per-wave partials.  So inv_rms may differ in its last bit, and through
+x_norm's rounding a token's mixes and gates by a rounding step: every output
+agrees at rounding level, and tokens whose mixes are bit-identical agree bit
+for bit.  The operand-layout path is itself pinned against the oracle by the
+other GPU tests; here the sampled outputs are also checked against the oracle
+at the BASELINE bars.  Shapes: C a multiple of 256 (the shapes row staging
+takes: n in {2, 4} with C in {256, 512, 768, 1024}, n = 1 with C in {512,
+1024}, modes full / no-H_res / head), batches with a ragged last tile, fewer
+tiles than CUs, several tiles per CU and the C2 size, plus shapes it does not
+take (C % 256 != 0, n * C / 256 odd, fused norm), which must be unaffected by
+the setting, bit for bit."""
 from __future__ import annotations
 
 import pytest
@@ -55,7 +60,7 @@ def _run(kind, xd, pd, packed, n, C, norm=None):
     return {k: v.clone() for k, v in o.items() if v is not None}
 
 
-def _both(staging, kind, n, C, M, seed, norm=None):
+def _both(staging, kind, n, C, M, seed, norm=None, exact=False):
     g = torch.Generator().manual_seed(seed)
     p = make_params(kind, n, C, BF, g, stress=True)
     x = (torch.randn(1, M, n * C, generator=g) * 2.0).to(BF)
@@ -71,16 +76,29 @@ def _both(staging, kind, n, C, M, seed, norm=None):
     staging(1)
     row = _run(kind, xd, pd, packed, n, C, norm)
     assert ref.keys() == row.keys()
+    if exact:
+        for k in ref:
+            assert torch.equal(ref[k], row[k]), k
+        return x, p, row
+    same = torch.ones(M, dtype=torch.bool, device=dev)  # tokens with bit-identical mixes
     for k in ref:
-        assert torch.equal(ref[k], row[k]), k
+        if k != "sub_in":  # inv_rms: its last bit; a flipped x_norm element: a bf16 step
+            assert maxrel(ref[k], row[k]) <= (1e-6 if k == "inv_rms" else 8e-3), k
+        if k not in ("inv_rms", "sub_in"):  # equal mixes: equal gates and pre-aggregate
+            same &= (ref[k] == row[k]).reshape(M, -1).all(-1)
+    assert maxrel(ref["sub_in"], row["sub_in"]) <= tol(BF)
+    assert same.float().mean().item() >= 0.5
+    for k in ref:
+        if k != "inv_rms":
+            assert torch.equal(ref[k].reshape(M, -1)[same], row[k].reshape(M, -1)[same]), k
     return x, p, row
 
 
 @pytest.mark.parametrize("kind", ["full", "nohres", "head"])
-@pytest.mark.parametrize("n,C", [(4, 768), (4, 512), (4, 256), (2, 768), (2, 1024), (1, 768),
+@pytest.mark.parametrize("n,C", [(4, 768), (4, 512), (4, 256), (2, 768), (2, 1024), (1, 512),
                                  (1, 256)])
 @pytest.mark.parametrize("M", [1, 37, 4096 + 5, 16384])
-def test_row_staging_bit_identical(staging, kind, n, C, M):
+def test_row_staging_matches_operand_layout(staging, kind, n, C, M):
     if kind == "head" and n == 1:
         pytest.skip("MHCHead with n = 1 is an RMSNorm (no projection)")
     _both(staging, kind, n, C, M, seed=1000 * n + C + M)
@@ -100,10 +118,11 @@ def test_row_staging_vs_oracle(staging, n, C):
     assert maxrel(inv[0], o["inv_rms"].view(M)[d].cpu()) <= 1e-5
 
 
-@pytest.mark.parametrize("n,C,norm", [(4, 640, False), (2, 200, False), (4, 768, True)])
+@pytest.mark.parametrize("n,C,norm", [(4, 640, False), (2, 200, False), (4, 768, True),
+                                      (1, 768, False)])
 def test_shapes_without_row_staging_unaffected(staging, n, C, norm):
     w = torch.rand(C, generator=torch.Generator().manual_seed(3)).to(BF) + 0.5 if norm else None
-    _both(staging, "full", n, C, 4096 + 9, seed=11, norm=w)
+    _both(staging, "full", n, C, 4096 + 9, seed=11, norm=w, exact=True)
 
 
 def test_row_staging_repeat_launches(staging):
