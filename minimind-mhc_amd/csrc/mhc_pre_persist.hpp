@@ -379,7 +379,7 @@ __device__ __forceinline__ void persist_row_sumsq(PersistShared<N, FD>& sh, cons
 // the row's x_norm = bf16(x * inv_rms), rounded as the reference's torch op
 // rounds it (model/mhc_fused.py:845: (x.float() * inv_rms).to(x.dtype)), so
 // the projection sums the same bf16 products the reference's GEMM sums.
-template <int N, int MODE, int KB, bool NORM, typename Issue = NoIssue>
+template <int N, int MODE, int KB, bool NORM, bool RSS = false, typename Issue = NoIssue>
 __device__ __forceinline__ void persist_project(
     const PreArgs& a, PersistShared<N, PersistPlan<N, MODE, KB>::FD>& sh, const U32x4 (&xr)[KB][N],
     const bf16x8_t (&wreg)[KB][N][PersistPlan<N, MODE, KB, NORM>::WR], const unsigned char* lds_w,
@@ -390,7 +390,7 @@ __device__ __forceinline__ void persist_project(
   const int r = lane & 15;
   const int g = lane >> 4;
   const int NCB = (a.C + kCBlock - 1) / kCBlock;
-  const float inv = persist_inv_rms(sh, slot, r, (float)(N * a.C), a.rms_eps);
+  const float inv = persist_inv_rms<N, FD, RSS>(sh, slot, r, (float)(N * a.C), a.rms_eps);
 
   f32x4_t acc[NT];
 #pragma unroll
@@ -437,13 +437,19 @@ __device__ __forceinline__ void persist_project(
 
 // ---- gates ---------------------------------------------------------------
 // inv_rms of token tt and the reduced projection m = sum_w partial of feature
-// f (of x_norm, so already normalised), from partials slot `slot`.
-template <int N, int FD>
+// f (of x_norm, so already normalised), from partials slot `slot`.  With row
+// sums (RSS) the total sits in ss[slot][0] and the other partials are zero:
+// reading it alone gives the same bits as adding the zeros.
+template <int N, int FD, bool RSS = false>
 __device__ __forceinline__ float persist_inv_rms(const PersistShared<N, FD>& sh, int slot, int tt,
                                                  float nc, float eps) {
   float sq = 0.f;
+  if constexpr (RSS) {
+    sq = sh.ss[slot][0][tt];
+  } else {
 #pragma unroll
-  for (int w = 0; w < kPersistWaves; ++w) sq += sh.ss[slot][w][tt];
+    for (int w = 0; w < kPersistWaves; ++w) sq += sh.ss[slot][w][tt];
+  }
   return 1.0f / sqrtf(sq / nc + eps);
 }
 
@@ -458,7 +464,7 @@ __device__ __forceinline__ float persist_mix(const PersistShared<N, FD>& sh, int
 // h_pre of (token lane / N, stream lane % N) for every wave (lanes past TM*N
 // return 0); wave POST_WAVE also writes h_post, h_pre, inv_rms and the
 // pre/post mixes when asked for.
-template <int N, int MODE, int KB>
+template <int N, int MODE, int KB, bool RSS = false>
 __device__ __forceinline__ float persist_pre_post(const PreArgs& a,
                                                   const PersistShared<N, PersistPlan<N, MODE, KB>::FD>& sh,
                                                   int64_t tile, int slot, int lane, int wave) {
@@ -477,7 +483,7 @@ __device__ __forceinline__ float persist_pre_post(const PreArgs& a,
       if (ok) {
         if (a.h_pre) st_any(a.h_pre, tk * N + i, kBF16, hp);
         if (a.inv_rms && i == 0)
-          a.inv_rms[tk] = persist_inv_rms(sh, slot, tt, (float)(N * a.C), a.rms_eps);
+          a.inv_rms[tk] = persist_inv_rms<N, FD, RSS>(sh, slot, tt, (float)(N * a.C), a.rms_eps);
         if (a.mixes_raw) a.mixes_raw[tk * FD + i] = m;
       }
       if constexpr (MODE != kHead) {
@@ -683,14 +689,14 @@ __device__ __forceinline__ void persist_step_row(
   persist_load_row<N, MODE, KB, 0, RW::R1>(xn, rn, wave, lane);
   __syncthreads();  // the tile in LDS and its row sums of squares visible
   persist_lds_to_operands<N, MODE, KB>(xl, xr, wave, lane);
-  persist_project<N, MODE, KB, false>(a, sh, xr, wreg, lds_w, slot, lane, wave,
+  persist_project<N, MODE, KB, false, true>(a, sh, xr, wreg, lds_w, slot, lane, wave,
                                       RowIssue<N, MODE, KB, RW::R1, RW::R2>{xn, rn, wave, lane});
   __syncthreads();  // partials visible
   if constexpr (MODE == kFull) {
     if (wave < P::SK_WAVES && prev >= 0 && a.h_res)
       persist_sinkhorn<N>(a, sh.hres[slot ^ 1], prev, tid);
   }
-  const float hp = persist_pre_post<N, MODE, KB>(a, sh, tile, slot, lane, wave);
+  const float hp = persist_pre_post<N, MODE, KB, true>(a, sh, tile, slot, lane, wave);
   if constexpr (MODE == kFull) {
     if (wave >= P::SK_WAVES) persist_res_gates<N, MODE, KB>(a, sh, tile, slot, tid - P::SK_WAVES * 64);
   }
