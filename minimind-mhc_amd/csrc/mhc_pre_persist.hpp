@@ -697,9 +697,6 @@ __device__ __forceinline__ void persist_step_row(
       persist_sinkhorn<N>(a, sh.hres[slot ^ 1], prev, tid);
   }
   const float hp = persist_pre_post<N, MODE, KB, true>(a, sh, tile, slot, lane, wave);
-  if constexpr (MODE == kFull) {
-    if (wave >= P::SK_WAVES) persist_res_gates<N, MODE, KB>(a, sh, tile, slot, tid - P::SK_WAVES * 64);
-  }
   uint32_t hlo[N];
   uint32_t hhi[N];
 #pragma unroll
@@ -710,6 +707,12 @@ __device__ __forceinline__ void persist_step_row(
   }
   persist_preagg<N, KB, false>(a, xr, hlo, hhi, tile, lane, wave, nsh, slot,
                                RowIssue<N, MODE, KB, RW::R2, RW::PW>{xn, rn, wave, lane});
+  // The h_res logits feed the next step's Sinkhorn only: after the
+  // pre-aggregate, whose stores and next-tile loads then go out sooner, they
+  // overlap the wait for those loads (C2 pre 29.2 -> 28.9 us).
+  if constexpr (MODE == kFull) {
+    if (wave >= P::SK_WAVES) persist_res_gates<N, MODE, KB>(a, sh, tile, slot, tid - P::SK_WAVES * 64);
+  }
 }
 
 // Gate parameter of thread tid (raw bits; converted once the streaming loads
