@@ -79,13 +79,36 @@ def _sync():
     torch.cuda.synchronize()
 
 
-def _queue_ahead():
-    """Park the GPU on a short spin kernel so the host can enqueue the timed
-    launches ahead of it: HIP events then bracket back-to-back kernels, not
-    host enqueue gaps."""
+_BUSY = {}
+
+
+def _queue_ahead(ms: float = 25.0):
+    """Keep every CU busy for about `ms` while the host enqueues the timed
+    launches behind that work: HIP events then bracket back-to-back kernels,
+    not host enqueue gaps.  The work is bf16 GEMMs (torch.matmul on
+    contiguous 4096 x 4096 operands), heavy enough to hold the clocks at their
+    loaded level: after an idle spell the GPU needs ~15 ms of sustained load
+    before its clocks settle (measured on MI355X: the config-2 pre launch runs
+    at 31-36 us over the first ~15 ms of back-to-back launches and at
+    28.4-28.7 us after; a single-wave spin here left the timed launches inside
+    that ramp).  A training loop runs these kernels at the settled level."""
     import torch
-    if hasattr(torch.cuda, "_sleep"):
-        torch.cuda._sleep(20_000_000)
+    if "a" not in _BUSY:
+        a = torch.randn(4096, 4096, device="cuda").to(torch.bfloat16)
+        o = torch.empty_like(a)
+        for _ in range(3):
+            torch.matmul(a, a, out=o)
+        _sync()
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        e0.record()
+        for _ in range(20):
+            torch.matmul(a, a, out=o)
+        e1.record()
+        _sync()
+        _BUSY.update(a=a, o=o, per_ms=max(e0.elapsed_time(e1) / 20, 1e-3))
+    a, o = _BUSY["a"], _BUSY["o"]
+    for _ in range(int(ms / _BUSY["per_ms"]) + 1):
+        torch.matmul(a, a, out=o)
 
 
 def bench_mhc(steps: int, warmup: int, sets: int = 4, n: int = N_STREAMS, C: int = C_DIM,
