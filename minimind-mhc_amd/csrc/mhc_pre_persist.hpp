@@ -195,6 +195,15 @@ struct PersistRow {
   static constexpr int RCH = NC / 8;                   // 16-byte chunks of a token row
   static constexpr int PW = N * KB;                    // 1 KiB pieces per wave
   static constexpr int BYTES = kTokTile * NC * 2;      // the tile in LDS
+  static constexpr int SCH = KB * 32;                  // 16-byte chunks of a sublayer-input row
+  // The sublayer input goes out through LDS as whole rows (persist_stage_store)
+  // where that measured faster (MI355X, 16384 tokens: n = 1, C = 1024 20.1 ->
+  // 16.5 us; n = 2, C = 768 20.1 -> 19.3; n = 4, C = 256 at 65536 tokens 52.3
+  // -> 50.9).  At n * KB = 8 it measured level (n = 2, C = 1024) or slower
+  // (n = 4, C = 512: 22.5 -> 23.1); at 12 (n = 4, C = 768) the kernel already
+  // holds 192 VGPRs of phi and x tiles and the staging spilled.
+  static constexpr bool STAGE = N * KB <= 6;
+  static constexpr int SUBB = STAGE ? kTokTile * SCH * 16 : 0;  // the tile's sublayer input in LDS
   // Load batches [0,R1) [R1,R2) [R2,PW) at three points of a step.  The
   // second (after the first barrier) carries half the tile: measured on MI355X
   // at C2 (PW = 12), splits 4/8/12 -> 4/10/12 took the pre launch from
@@ -204,7 +213,7 @@ struct PersistRow {
   // A row is a whole number of 1 KiB pieces (n * KB even), so each wave holds
   // two whole rows and every lane the same columns of both (persist_row_sumsq).
   static constexpr bool OK = P::NREG == P::NT && RCH % 16 == 0 && (NC * 2) % 1024 == 0 &&
-                             P::SHARED + 256 + BYTES <= kLdsBytes;
+                             P::SHARED + 256 + BYTES + SUBB <= kLdsBytes;
 };
 
 // LDS byte of 16-byte chunk j of token row t.  The chunk index is XORed with
@@ -545,7 +554,8 @@ __device__ __forceinline__ void persist_preagg(const PreArgs& a, const U32x4 (&x
                                                const uint32_t (&hlo)[N], const uint32_t (&hhi)[N],
                                                int64_t tile, int lane, int wave,
                                                PersistNorm<NORM, KB>& nsh, int slot,
-                                               const Issue& issue = Issue()) {
+                                               const Issue& issue = Issue(),
+                                               unsigned char* stage = nullptr) {
   constexpr int TM = kTokTile;
   const int r = lane & 15;
   const int g = lane >> 4;
@@ -566,6 +576,14 @@ __device__ __forceinline__ void persist_preagg(const PreArgs& a, const U32x4 (&x
 #pragma unroll
       for (int j = 0; j < 4; ++j) q2 = dot2_bf16(pk.v[j], pk.v[j], q2);
       nsh.stash[slot][r * PersistNorm<NORM, KB>::kChunks + (c0 >> 3) + g] = pk;
+      continue;
+    }
+    if (stage) {  // row staging: the tile's rows go out whole at the next step
+      // chunk j = 4 wave + g + 32 q of row r; the XOR with r < 16 touches only
+      // the low 5 bits, so the three chunks are one base 512 bytes apart
+      constexpr int SCH = KB * 32;
+      const uint32_t base = (uint32_t)(r * SCH + ((4 * wave + g) ^ r)) * 16u;
+      *reinterpret_cast<U32x4*>(stage + base + q * 512) = pk;
       continue;
     }
     // The whole offset travels in the vector offset, the scalar offset stays
@@ -615,6 +633,33 @@ __device__ __forceinline__ void persist_norm_store(const PreArgs& a, const Persi
     y.v[3] = pack_bf16x2(bf16lo(pk.v[3]) * sc * w1.z, bf16hi(pk.v[3]) * sc * w1.w);
     // whole offset in the vector offset, scalar offset the literal 0 (see above)
     buf_store16_nt<kNtSc1>(rsub, lo == kBufOob ? kBufOob : sub_row + lo + (uint32_t)c0 * 2u, y);
+  }
+}
+
+// Row staging: the sublayer input of tile `tile`, staged in LDS by its
+// pre-aggregate (chunk j of row r at (r * SCH + (j ^ r)) * 16, the XOR
+// spreading the 16 rows of one column over the banks), stored as whole rows:
+// wave w takes the two-row span of rows 2w and 2w + 1, lane l its chunks l,
+// l + 64, .. (1 KiB per wave instruction), where the pre-aggregate's own
+// layout splits every 128-byte line of sub_in between two waves.
+template <int KB>
+__device__ __forceinline__ void persist_stage_store(const PreArgs& a, const unsigned char* stage,
+                                                    int64_t tile, int lane, int wave) {
+  constexpr int SCH = KB * 32;
+  const int64_t M = a.M;
+  const int C = a.C;
+  const int64_t t0 = wave_uniform(tile * kTokTile);
+  const int valid = (int)(M - t0 < kTokTile ? M - t0 : kTokTile);
+  const auto rsub = make_rsrc(static_cast<uint16_t*>(a.sub_in) + t0 * C, (uint32_t)valid * C * 2u);
+#pragma unroll
+  for (int k = 0; k < KB; ++k) {
+    const int qr = lane + 64 * k;        // chunk of the two-row span of rows 2w, 2w + 1
+    const int second = qr >= SCH ? 1 : 0;
+    const int j = qr - second * SCH;     // chunk of its row
+    const int row = 2 * wave + second;   // < 16: row & 15 == row
+    const U32x4 v = *reinterpret_cast<const U32x4*>(stage + (row * SCH + (j ^ row)) * 16);
+    // whole offset in the vector offset, scalar offset the literal 0 (see persist_preagg)
+    buf_store16_nt<kNtSc1>(rsub, (uint32_t)(2 * wave * SCH + qr) * 16u, v);
   }
 }
 
@@ -676,7 +721,7 @@ __device__ __forceinline__ void persist_step(
 template <int N, int MODE, int KB>
 __device__ __forceinline__ void persist_step_row(
     const PreArgs& a, PersistShared<N, PersistPlan<N, MODE, KB>::FD>& sh, PersistNorm<false, KB>& nsh,
-    unsigned char* xl, U32x4 (&xr)[KB][N], U32x4 (&xn)[KB][N],
+    unsigned char* xl, unsigned char* stage, U32x4 (&xr)[KB][N], U32x4 (&xn)[KB][N],
     const bf16x8_t (&wreg)[KB][N][PersistPlan<N, MODE, KB>::WR], const unsigned char* lds_w,
     int64_t tile, int64_t prev, int64_t ntiles, int slot, int tid, int lane, int wave) {
   using P = PersistPlan<N, MODE, KB>;
@@ -686,8 +731,14 @@ __device__ __forceinline__ void persist_step_row(
                               N * a.C);
   persist_row_to_lds<N, MODE, KB, 0, RW::PW>(xl, xn, wave, lane);
   persist_row_sumsq<N, MODE, KB>(sh, xn, slot, wave, lane);
-  persist_load_row<N, MODE, KB, 0, RW::R1>(xn, rn, wave, lane);
-  __syncthreads();  // the tile in LDS and its row sums of squares visible
+  if constexpr (!RW::STAGE) persist_load_row<N, MODE, KB, 0, RW::R1>(xn, rn, wave, lane);
+  __syncthreads();  // the tile in LDS, its row sums of squares and the previous sub_in visible
+  if constexpr (RW::STAGE) {
+    // The previous tile's sublayer input goes out while neither the operand
+    // registers nor the next tile's loads are live.
+    if (prev >= 0) persist_stage_store<KB>(a, stage, prev, lane, wave);
+    persist_load_row<N, MODE, KB, 0, RW::R1>(xn, rn, wave, lane);
+  }
   persist_lds_to_operands<N, MODE, KB>(xl, xr, wave, lane);
   persist_project<N, MODE, KB, false, true>(a, sh, xr, wreg, lds_w, slot, lane, wave,
                                       RowIssue<N, MODE, KB, RW::R1, RW::R2>{xn, rn, wave, lane});
@@ -706,7 +757,8 @@ __device__ __forceinline__ void persist_step_row(
     hhi[i] = pack_hi(h);
   }
   persist_preagg<N, KB, false>(a, xr, hlo, hhi, tile, lane, wave, nsh, slot,
-                               RowIssue<N, MODE, KB, RW::R2, RW::PW>{xn, rn, wave, lane});
+                               RowIssue<N, MODE, KB, RW::R2, RW::PW>{xn, rn, wave, lane},
+                               RW::STAGE ? stage : nullptr);
   // The h_res logits feed the next step's Sinkhorn only: after the
   // pre-aggregate, whose stores and next-tile loads then go out sooner, they
   // overlap the wait for those loads (C2 pre 29.2 -> 28.9 us).
@@ -769,6 +821,7 @@ __global__ __launch_bounds__(kPersistWaves * 64) void pre_persist_kernel(PreArgs
   __shared__ PersistNorm<NORM, KB> nsh;
   __shared__ __attribute__((aligned(16))) unsigned char lds_w[P::LDS_W];
   __shared__ __attribute__((aligned(16))) unsigned char xl[ROW ? RW::BYTES : 16];
+  __shared__ __attribute__((aligned(16))) unsigned char sub_stage[ROW && RW::STAGE ? RW::SUBB : 16];
 
   const int tid = threadIdx.x;
   const int lane = tid & 63;
@@ -869,8 +922,8 @@ __global__ __launch_bounds__(kPersistWaves * 64) void pre_persist_kernel(PreArgs
   int64_t k = 0;
   if constexpr (ROW) {  // fixed roles: xa in flight (row layout), xb the operands
     for (; k < my_tiles; ++k) {
-      persist_step_row<N, MODE, KB>(a, sh, nsh, xl, xb, xa, wreg, lds_w, tile, prev, ntiles, slot,
-                                    tid, lane, wave);
+      persist_step_row<N, MODE, KB>(a, sh, nsh, xl, sub_stage, xb, xa, wreg, lds_w, tile, prev, ntiles,
+                                    slot, tid, lane, wave);
       prev = tile;
       slot ^= 1;
       tile += step;
@@ -892,8 +945,10 @@ __global__ __launch_bounds__(kPersistWaves * 64) void pre_persist_kernel(PreArgs
     slot ^= 1;
   }
   // The last tile's Sinkhorn, once every gate wave has written its logits,
-  // and its normed stores, once every wave has written its partial.
-  if constexpr (MODE == kFull || NORM) __syncthreads();
+  // its normed stores, once every wave has written its partial, and (row
+  // staging) its staged sublayer input.
+  if constexpr (MODE == kFull || NORM || (ROW && RW::STAGE)) __syncthreads();
+  if constexpr (ROW && RW::STAGE) persist_stage_store<KB>(a, sub_stage, prev, lane, wave);
   if constexpr (NORM) persist_norm_store<N, KB>(a, nsh, prev, slot ^ 1, lane, wave);
   if constexpr (MODE == kFull) {
     if (wave < P::SK_WAVES && a.h_res) persist_sinkhorn<N>(a, sh.hres[slot ^ 1], prev, tid);
