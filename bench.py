@@ -8,9 +8,9 @@ connection: the fused pre phase (RMS + projection + gates + Sinkhorn +
 pre-aggregate) and the post phase (res-mix + post-expand).
 
 Timing: W untimed warmup steps, then K timed steps bracketed by
-torch.cuda.synchronize().  A step runs the pre kernel on 4 distinct input
-sets, then the post kernel on the same 4 sets (see bench_mhc for why); each
-group of 4 back-to-back launches of one kernel is bracketed by HIP events on
+torch.cuda.synchronize().  A step runs the pre kernel on 8 distinct input
+sets, then the post kernel on the same 8 sets (see bench_mhc for why); each
+group of 8 back-to-back launches of one kernel is bracketed by HIP events on
 the stream it runs on; value = tokens / (mean pre + mean post launch time).  A cold-cache measurement (read-only
 flush before each kernel) and plain torch copy / sum kernels over 1 GiB
 (`hbm_calibration`) are reported beside it.
@@ -111,15 +111,18 @@ def _queue_ahead(ms: float = 25.0):
         torch.matmul(a, a, out=o)
 
 
-def bench_mhc(steps: int, warmup: int, sets: int = 4, n: int = N_STREAMS, C: int = C_DIM,
+def bench_mhc(steps: int, warmup: int, sets: int = 8, n: int = N_STREAMS, C: int = C_DIM,
               M: int = TOKENS, cold: bool = True):
     """Steady-state kernel times over `sets` distinct input sets.
 
     Each step runs the pre kernel on every set, then the post kernel on every
-    set, so a set's x is touched again only after 3 other sets' traffic
-    (>= 375 MB, more than the 256 MB Infinity Cache): every launch reads cold
-    data and evicts the dirty lines earlier launches left, i.e. pays for its
-    own reads and (in steady state) its own writes.  Also returns a cold-cache
+    set, so at config 2 (8 sets) a set's x is touched again only after 7 other
+    sets' traffic (>= 875 MB, more than the 256 MB Infinity Cache): every
+    launch reads cold data and evicts the dirty lines earlier launches left,
+    i.e. pays for its own reads and (in steady state) its own writes.  One
+    event pair brackets all `sets` launches of a kernel, so the event packets'
+    own cost is spread over them (at config 2, 4 sets measured ~0.3 us a
+    launch more than 8; 16 sets made the post launch slower, 36.7 us).  Also returns a cold-cache
     measurement (1 GiB read-only flush before each kernel, which leaves clean
     lines, so writes are absorbed by the cache)."""
     import torch
@@ -844,7 +847,7 @@ def main():
                                "16384 tok (B=16,T=1024), n=4, C=768, bf16, F fixed N(0,1)",
                    "tokens": TOKENS, "n": N_STREAMS, "C": C_DIM, "sinkhorn_iters": ITERS,
                    "parallelism": "single GPU",
-                   "timing": "steady state over 4 rotating input sets, HIP events per kernel"},
+                   "timing": "steady state over 8 rotating input sets, HIP events per kernel"},
         "roofline": {"bound": "hbm",
                      "kernel": "one mHC forward step: pre_persist_kernel (RMS + projection + gates "
                                "+ Sinkhorn + pre-aggregate) then post_vec_kernel (res-mix + "

@@ -173,6 +173,7 @@ struct PersistPlan {
   static constexpr int SK_WAVES = MODE == kFull ? (kTokTile * G + 63) / 64 : 0;
   static constexpr int GATE_LANES = (kPersistWaves - SK_WAVES) * 64;
   static_assert(SK_WAVES < kPersistWaves, "gates need at least one wave");
+  static_assert(2 * SK_WAVES <= kPersistWaves, "the last two Sinkhorns run side by side");
   static_assert(kTokTile * N <= 64, "one wave holds a tile's h_pre, one per lane");
   static_assert(kPersistWaves * kTokTile * FD * 4 >= 64 * 16, "partials area doubles as a write sink");
   // Wave that writes h_post (and h_pre / inv_rms when asked for).
@@ -384,6 +385,22 @@ __device__ __forceinline__ void persist_row_sumsq(PersistShared<N, FD>& sh, cons
   }
 }
 
+// inv_rms of token tt from the sums-of-squares partials of slot `slot`.  With
+// row sums (RSS) the total sits in ss[slot][0] and the other partials are
+// zero: reading it alone gives the same bits as adding the zeros.
+template <int N, int FD, bool RSS = false>
+__device__ __forceinline__ float persist_inv_rms(const PersistShared<N, FD>& sh, int slot, int tt,
+                                                 float nc, float eps) {
+  float sq = 0.f;
+  if constexpr (RSS) {
+    sq = sh.ss[slot][0][tt];
+  } else {
+#pragma unroll
+    for (int w = 0; w < kPersistWaves; ++w) sq += sh.ss[slot][w][tt];
+  }
+  return 1.0f / sqrtf(sq / nc + eps);
+}
+
 // ---- phase 1: projection partials (MFMA) of x_norm -> LDS.  The A operand is
 // the row's x_norm = bf16(x * inv_rms), rounded as the reference's torch op
 // rounds it (model/mhc_fused.py:845: (x.float() * inv_rms).to(x.dtype)), so
@@ -445,23 +462,8 @@ __device__ __forceinline__ void persist_project(
 }
 
 // ---- gates ---------------------------------------------------------------
-// inv_rms of token tt and the reduced projection m = sum_w partial of feature
-// f (of x_norm, so already normalised), from partials slot `slot`.  With row
-// sums (RSS) the total sits in ss[slot][0] and the other partials are zero:
-// reading it alone gives the same bits as adding the zeros.
-template <int N, int FD, bool RSS = false>
-__device__ __forceinline__ float persist_inv_rms(const PersistShared<N, FD>& sh, int slot, int tt,
-                                                 float nc, float eps) {
-  float sq = 0.f;
-  if constexpr (RSS) {
-    sq = sh.ss[slot][0][tt];
-  } else {
-#pragma unroll
-    for (int w = 0; w < kPersistWaves; ++w) sq += sh.ss[slot][w][tt];
-  }
-  return 1.0f / sqrtf(sq / nc + eps);
-}
-
+// The reduced projection m = sum_w partial of feature f of token tt (of x_norm,
+// so already normalised), from partials slot `slot`.
 template <int N, int FD>
 __device__ __forceinline__ float persist_mix(const PersistShared<N, FD>& sh, int slot, int tt, int f) {
   float sum = 0.f;
@@ -723,7 +725,7 @@ __device__ __forceinline__ void persist_step_row(
     const PreArgs& a, PersistShared<N, PersistPlan<N, MODE, KB>::FD>& sh, PersistNorm<false, KB>& nsh,
     unsigned char* xl, unsigned char* stage, U32x4 (&xr)[KB][N], U32x4 (&xn)[KB][N],
     const bf16x8_t (&wreg)[KB][N][PersistPlan<N, MODE, KB>::WR], const unsigned char* lds_w,
-    int64_t tile, int64_t prev, int64_t ntiles, int slot, int tid, int lane, int wave) {
+    int64_t tile, int64_t prev, int64_t ntiles, int slot, int tid, int lane, int wave, bool last) {
   using P = PersistPlan<N, MODE, KB>;
   using RW = PersistRow<N, MODE, KB>;
   const int r = lane & 15;
@@ -744,7 +746,9 @@ __device__ __forceinline__ void persist_step_row(
                                       RowIssue<N, MODE, KB, RW::R1, RW::R2>{xn, rn, wave, lane});
   __syncthreads();  // partials visible
   if constexpr (MODE == kFull) {
-    if (wave < P::SK_WAVES && prev >= 0 && a.h_res)
+    // In the last step the previous tile's Sinkhorn waits for the end of the
+    // loop, where it runs on the gate waves beside the last tile's.
+    if (wave < P::SK_WAVES && prev >= 0 && a.h_res && !last)
       persist_sinkhorn<N>(a, sh.hres[slot ^ 1], prev, tid);
   }
   const float hp = persist_pre_post<N, MODE, KB, true>(a, sh, tile, slot, lane, wave);
@@ -918,12 +922,14 @@ __global__ __launch_bounds__(kPersistWaves * 64) void pre_persist_kernel(PreArgs
   // flight.
   const int64_t my_tiles = (ntiles - blockIdx.x + step - 1) / step;
   int64_t prev = -1;
+  int64_t pprev = -1;  // the tile before prev (row staging: its Sinkhorn runs after the loop)
   int slot = 0;
   int64_t k = 0;
   if constexpr (ROW) {  // fixed roles: xa in flight (row layout), xb the operands
     for (; k < my_tiles; ++k) {
       persist_step_row<N, MODE, KB>(a, sh, nsh, xl, sub_stage, xb, xa, wreg, lds_w, tile, prev, ntiles,
-                                    slot, tid, lane, wave);
+                                    slot, tid, lane, wave, k + 1 == my_tiles);
+      pprev = prev;
       prev = tile;
       slot ^= 1;
       tile += step;
@@ -952,6 +958,13 @@ __global__ __launch_bounds__(kPersistWaves * 64) void pre_persist_kernel(PreArgs
   if constexpr (NORM) persist_norm_store<N, KB>(a, nsh, prev, slot ^ 1, lane, wave);
   if constexpr (MODE == kFull) {
     if (wave < P::SK_WAVES && a.h_res) persist_sinkhorn<N>(a, sh.hres[slot ^ 1], prev, tid);
+    // Row staging: the tile before the last, deferred from the last step, on
+    // the gate waves (each SIMD then interleaves two independent Sinkhorn
+    // chains); its logits sit in the other slot, untouched since its step.
+    if constexpr (ROW) {
+      if (wave >= P::SK_WAVES && wave < 2 * P::SK_WAVES && pprev >= 0 && a.h_res)
+        persist_sinkhorn<N>(a, sh.hres[slot], pprev, tid - P::SK_WAVES * 64);
+    }
   }
 }
 
