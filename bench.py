@@ -11,7 +11,9 @@ Timing: W untimed warmup steps, then K timed steps bracketed by
 torch.cuda.synchronize().  A step runs the pre kernel on 8 distinct input
 sets, then the post kernel on the same 8 sets (see bench_mhc for why); each
 group of 8 back-to-back launches of one kernel is bracketed by HIP events on
-the stream it runs on; value = tokens / (mean pre + mean post launch time).  A cold-cache measurement (read-only
+the stream it runs on; value = tokens / (mean pre + mean post launch time).
+After the synchronize and before the first timed step, ~25 ms more of the
+same steps run untimed, so the timed ones meet settled clocks.  A cold-cache measurement (read-only
 flush before each kernel) and plain torch copy / sum kernels over 1 GiB
 (`hbm_calibration`) are reported beside it.
 
@@ -187,11 +189,26 @@ def bench_mhc(steps: int, warmup: int, sets: int = 8, n: int = N_STREAMS, C: int
         rec["pre"].append((e0, e1))
         rec["post"].append((e1, e2))
 
-    for _ in range(warmup):
-        step({"pre": [], "post": []})
+    warm = {"pre": [], "post": []}
+    for _ in range(max(warmup, 2)):
+        step(warm)
     _sync()
+    # Settle: the GPU's clocks need ~15 ms of sustained load after an idle
+    # spell (see _queue_ahead).  Where a launch takes well over the host's
+    # ~10 us to enqueue one, the load is this step itself, enqueued for ~25 ms
+    # ahead of the timed steps, so they run at the operating point their own
+    # work sets (at config 2 that measured ~0.2 us a step faster than settling
+    # on bf16 GEMMs, whose MFMA load leaves other clocks).  Shorter launches
+    # (config 4's 64 tokens) would leave the host behind the GPU: there the
+    # GEMMs of _queue_ahead give the host its head start.
+    per_step = sum(a_.elapsed_time(b_) for a_, b_ in warm["pre"][1:] + warm["post"][1:])
+    per_step /= len(warm["pre"]) - 1
+    if per_step / (2 * sets) > 0.02:
+        for _ in range(int(25.0 / per_step) + 1):
+            step({"pre": [], "post": []})
+    else:
+        _queue_ahead()
     rec = {"pre": [], "post": []}
-    _queue_ahead()
     for _ in range(steps):
         step(rec)
     _sync()
