@@ -391,9 +391,12 @@ __global__ __launch_bounds__(NW * 64) __attribute__((amdgpu_waves_per_eu(F32 ? 2
   // ---- gxn = phi . (alpha * g_raw) on MFMA, and
   //      g_x = inv * (gxn - xn * mean) + h_pre[i] * g_sub.
   // Where phi is one K-step wide (FD <= 32), a chunk's phi A operands and its
-  // g_sub go out one chunk ahead (two register sets), so the MFMAs and the
-  // g_x arithmetic of chunk j run while chunk j + 1's loads are in flight
-  // instead of each load being waited for in turn.  Wider phi (n = 8, full)
+  // g_sub go out three chunks ahead (four register sets: 123 VGPRs at n = 4,
+  // C = 768, within two 8-wave workgroups per CU; one ahead at 16 chunks a
+  // wave), so the MFMAs and the g_x
+  // arithmetic of chunk j run while the loads of chunks j + 1 .. j + 3 are in
+  // flight instead of each load being waited for in turn (C2 68.0 -> 67.3 us
+  // against one chunk ahead).  Wider phi (n = 8, full)
   // keeps one set, loaded at the start of its chunk (CH: one round trip a
   // chunk) up to 12 chunks a wave, and operand by operand beyond that (the
   // whole set would spill).
@@ -413,13 +416,18 @@ __global__ __launch_bounds__(NW * 64) __attribute__((amdgpu_waves_per_eu(F32 ? 2
     const bool ok = c0 + 8 * g < C;
     in.gv = XV::load(rgs, ok ? (uint32_t)(r * C + c0 + 8 * g) * ES : kBufOob);
   };
-  ChunkIn cin[PF ? 2 : 1];
-  if constexpr (PF) load_chunk(0, cin[0]);
+  constexpr int PD = PF ? (KJ <= 12 ? 4 : 2) : 1;  // 16 chunks a wave: four sets would spill
+  ChunkIn cin[PD];
+  if constexpr (PF) {
+#pragma unroll
+    for (int p = 0; p < PD - 1; ++p)
+      if (p < KJ) load_chunk(p, cin[p]);
+  }
 #pragma unroll
   for (int j = 0; j < KJ; ++j) {
-    ChunkIn& cur = cin[PF ? (j & 1) : 0];
+    ChunkIn& cur = cin[PF ? (j % PD) : 0];
     if constexpr (PF) {
-      if (j + 1 < KJ) load_chunk(j + 1, cin[(j + 1) & 1]);
+      if (j + PD - 1 < KJ) load_chunk(j + PD - 1, cin[(j + PD - 1) % PD]);
     } else if constexpr (CH) {
       load_chunk(j, cur);
     }
