@@ -214,8 +214,11 @@ __global__ __launch_bounds__(kKsWaves * 64) void pre_kstream_kernel(PreArgs a) {
   // Workgroups walk their chunks in rotated orders, so the CUs of an XCD do
   // not all read the same few phi lines from the same L2 channels at once.
   // Slot j of this wave is chunk kq + KS * ((j + rot) mod NJ); slots past NJ
-  // read nothing.
-  const int rot = (int)(blockIdx.x % (unsigned)NJ);
+  // read nothing.  At n = 16 phi (7 MB at C = 768) outgrows an XCD's 4 MB L2:
+  // there every workgroup walks the same order, so the CUs of an XCD read each
+  // phi line at about the same time and share its L2 fill (652 -> 553 us at
+  // 16384 tokens; at n = 8 and at C = 2048 the rotation stays faster).
+  const int rot = N == 16 ? 0 : (int)(blockIdx.x % (unsigned)NJ);
   auto chunk_of = [&](int slot_j, bool& live) {
     const int jr = slot_j < NJ ? (slot_j + rot < NJ ? slot_j + rot : slot_j + rot - NJ) : slot_j;
     const int k = kq + P::KS * jr;  // uniform
