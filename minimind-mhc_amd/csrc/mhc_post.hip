@@ -211,6 +211,76 @@ __global__ __launch_bounds__(256) void post_n16_kernel(PostArgs a) {
   }
 }
 
+// n = 8, bf16 stream, gates and F: post_vec_kernel's split (one thread per
+// token and 16-byte column chunk), with x and H_res kept packed.  Unpacked,
+// the 64 x values and 64 H_res values of a thread take 116 VGPRs (four waves
+// a SIMD).  Here the chunk is re-packed once into stream pairs
+// (x[2p][c], x[2p+1][c]) by v_perm and each res-mix output is four
+// v_dot2_f32_bf16 against H_res row i's adjacent pairs, as post_n16_kernel
+// does (the fp32 sum runs pairwise rather than in post_vec_kernel's order).
+template <bool RES>
+__global__ __launch_bounds__(256) void post_n8_kernel(PostArgs a) {
+  constexpr int N = 8;
+  constexpr int NP = N / 2;
+  const int C = a.C;
+  const int CV = C / 8;
+  const int64_t gid = (int64_t)blockIdx.x * 256 + threadIdx.x;
+  const int64_t tok = gid / CV;
+  if (tok >= a.M) return;
+  const int c = (int)(gid - tok * CV) * 8;
+  const int64_t NC = (int64_t)N * C;
+  const uint16_t* __restrict__ x = static_cast<const uint16_t*>(a.x) + tok * NC + c;
+  uint16_t* __restrict__ out = static_cast<uint16_t*>(a.out) + tok * NC + c;
+  u32x4_t xv[N];
+#pragma unroll
+  for (int j = 0; j < N; ++j)
+    xv[j] = __builtin_nontemporal_load(reinterpret_cast<const u32x4_t*>(x + (int64_t)j * C));
+  const u32x4_t fv = *reinterpret_cast<const u32x4_t*>(static_cast<const uint16_t*>(a.f_out) + tok * C + c);
+  const u32x4_t hpv = *reinterpret_cast<const u32x4_t*>(static_cast<const uint16_t*>(a.h_post) + tok * N);
+  float fl[8];
+#pragma unroll
+  for (int e = 0; e < 4; ++e) {
+    fl[2 * e] = bf16lo(fv[e]);
+    fl[2 * e + 1] = bf16hi(fv[e]);
+  }
+  u32x4_t hr[RES ? N : 1];  // row i: its four adjacent pairs (h_res[i][2p], h_res[i][2p + 1])
+  uint32_t xp[RES ? NP : 1][8];     // xp[p][k] = (x[2p][c + k], x[2p + 1][c + k])
+  if constexpr (RES) {
+    const u32x4_t* hr4 = reinterpret_cast<const u32x4_t*>(static_cast<const uint16_t*>(a.h_res) + tok * N * N);
+#pragma unroll
+    for (int i = 0; i < N; ++i) hr[i] = hr4[i];
+#pragma unroll
+    for (int p = 0; p < NP; ++p)
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        xp[p][2 * e] = __builtin_amdgcn_perm(xv[2 * p + 1][e], xv[2 * p][e], 0x05040100u);
+        xp[p][2 * e + 1] = __builtin_amdgcn_perm(xv[2 * p + 1][e], xv[2 * p][e], 0x07060302u);
+      }
+  }
+#pragma unroll
+  for (int i = 0; i < N; ++i) {
+    const float hp = (i & 1) ? bf16hi(hpv[i >> 1]) : bf16lo(hpv[i >> 1]);
+    float o[8];
+#pragma unroll
+    for (int k = 0; k < 8; ++k) {
+      float r;
+      if constexpr (RES) {
+        float acc = 0.f;
+#pragma unroll
+        for (int p = 0; p < NP; ++p) acc = dot2_bf16(hr[i][p], xp[p][k], acc);
+        r = rnd<__bf16>(acc);
+      } else {
+        r = (k & 1) ? bf16hi(xv[i][k >> 1]) : bf16lo(xv[i][k >> 1]);
+      }
+      o[k] = __fadd_rn(r, rnd<__bf16>(__fmul_rn(hp, fl[k])));
+    }
+    u32x4_t ov;
+#pragma unroll
+    for (int e = 0; e < 4; ++e) ov[e] = pack_bf16x2(o[2 * e], o[2 * e + 1]);
+    __builtin_nontemporal_store(ov, reinterpret_cast<u32x4_t*>(out + (int64_t)i * C));
+  }
+}
+
 // Any dtype mix, any C: one thread per output element.
 __global__ __launch_bounds__(256) void post_generic_kernel(PostArgs a) {
   const int64_t gid = (int64_t)blockIdx.x * 256 + threadIdx.x;
@@ -277,6 +347,16 @@ hipError_t launch_post(const PostArgs& a, hipStream_t s) {
       hipLaunchKernelGGL(post_n16_kernel<true>, dim3((unsigned)blocks), dim3(256), 0, s, a);
     else
       hipLaunchKernelGGL(post_n16_kernel<false>, dim3((unsigned)blocks), dim3(256), 0, s, a);
+    return hipGetLastError();
+  }
+  if (a.n == 8 && a.x_dtype == kBF16 && a.h_dtype == kBF16 && a.f_dtype == kBF16 && a.C % 8 == 0 &&
+      aligned16(a.x) && aligned16(a.out) && aligned16(a.f_out) && aligned16(a.h_post) &&
+      (!a.h_res || aligned16(a.h_res))) {
+    const int64_t blocks = (a.M * (a.C / 8) + 255) / 256;
+    if (a.h_res)
+      hipLaunchKernelGGL(post_n8_kernel<true>, dim3((unsigned)blocks), dim3(256), 0, s, a);
+    else
+      hipLaunchKernelGGL(post_n8_kernel<false>, dim3((unsigned)blocks), dim3(256), 0, s, a);
     return hipGetLastError();
   }
   const bool pow2n = a.n == 1 || a.n == 2 || a.n == 4 || a.n == 8;
