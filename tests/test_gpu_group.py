@@ -119,3 +119,13 @@ def test_group_repeat_launches(threshold):
         again = _run("full", x.to(dev), pd, packed, n, C, None, 20)
         for k in first:
             assert torch.equal(first[k], again[k]), k
+
+
+@pytest.mark.parametrize("n,C", [(4, 768), (2, 768), (1, 1024), (8, 768)])
+@pytest.mark.parametrize("M", [16 * 256 * 2 + 16 * 37 + 5, 16 * 256 * 4])
+def test_group_matches_large_batch_kernel_several_tiles_per_workgroup(threshold, n, C, M):
+    """Token counts that give the large-batch kernels two to four tiles a
+    workgroup on a 256-CU part: the persistent kernel's steady steps, its last
+    step (whose Sinkhorn of the tile before it runs after the loop, on the gate
+    waves) and ragged last tiles, bit for bit against the group kernel."""
+    _both(threshold, "full", n, C, M, seed=3 * n + C + M)
