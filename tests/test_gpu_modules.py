@@ -243,3 +243,39 @@ def test_module_matches_reference_c768(dev, name):
         out = mod(inp["x"].to(dev), lambda z: z @ fw)
     err = maxrel(ref["out"], out)
     assert err <= tol(dtype), f"{name}: {err:.3e}"
+
+
+@pytest.mark.parametrize("n,C,M", [(4, 768, 16384), (8, 768, 8192), (16, 768, 4096)])
+def test_full_size_stress_gates_bf16(dev, n, C, M):
+    """Full-size launches with projection-driven (stress) gates on every large-batch
+    kernel: the persistent kernel at config 2's shape, the K-streamed kernel at
+    config 5's (n = 8, with the packed n = 8 post kernel) and at n = 16.  All
+    tokens: finite outputs, a non-negative H_res whose bf16 row and column sums
+    are 1 up to n half-ulps, 0 <= h_post <= 2; 256 random tokens against the
+    oracle at the bf16 bar (mHC is per-token)."""
+    from model import _hip as H, _ops
+    g = torch.Generator().manual_seed(11 + n)
+    x = torch.randn(M, n * C, generator=g).to(torch.bfloat16)
+    f = torch.randn(M, C, generator=g).to(torch.bfloat16)
+    p = make_params("full", n, C, torch.bfloat16, g, stress=True)
+    pd = {k: v.to(dev) for k, v in p.items()}
+    packed = _ops.PhiPack(H.MODE_FULL).get(pd["phi_weight"], n, C)
+    assert packed is not None
+    xd = x.to(dev).view(1, M, n * C)
+    print(f"full-size stress n={n} C={C} M={M}", flush=True)
+    o = _ops.pre_full(xd, pd["phi_weight"], packed, pd["alpha_pre"], pd["bias_pre"], pd["alpha_post"],
+                      pd["bias_post"], pd["alpha_res"], pd["bias_res"], n, C, 2.0, 1e-6, 1e-6, 20, 1e-6)
+    out = _ops.post(xd, o["h_res"], o["h_post"], f.to(dev), n, C)
+    hr = o["h_res"].float()
+    hp = o["h_post"].float()
+    assert torch.isfinite(out.float()).all() and torch.isfinite(o["sub_in"].float()).all()
+    assert (hr >= 0).all()
+    assert (hr.sum(-1) - 1).abs().max().item() <= n * 2 ** -9
+    assert (hr.sum(-2) - 1).abs().max().item() <= n * 2 ** -9
+    assert (hp >= 0).all() and (hp <= 2).all()
+    idx = torch.randperm(M, generator=g)[:256]
+    xs = x[idx].view(1, -1, n * C)
+    fs = f[idx].view(1, -1, C)
+    ref = R.mhc_full_forward(xs, p, lambda z: fs, n, C, sinkhorn_iters=20)
+    assert maxrel(ref["out"][0], out[idx.to(dev)]) <= 1e-2
+    assert maxrel(ref["sub_in"][0], o["sub_in"][idx.to(dev)]) <= 1e-2
