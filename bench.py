@@ -30,7 +30,9 @@ gates, bf16 F under autocast); `other_configs`: the same kernel pair at config
 5's n = 8 shape, config 4's 64-token shape, and the widest shapes the
 reference's module accepts (dim 2048 at n = 4, n = 16 at dim 768); and the end-to-end model
 figures: `e2e_prefill` (config 3), `e2e_decode` (config 4, eager and
-HIP-graph replay) and `e2e_prefill_moe` (config 5).
+HIP-graph replay) and `e2e_prefill_moe` (config 5); `reference_bench_shapes`:
+the reference's own fwd + bwd speed workloads (its `_bench` shapes, one
+connection around an MLP sublayer).
 
 `*roofline.traffic` is the measured HBM traffic per launch (per step for `roofline`):
 FETCH_SIZE + WRITE_SIZE from two rocprofv3 --pmc passes over `--traffic`
@@ -40,7 +42,7 @@ from profiles/traffic_mhc_fwd_c2.txt (the rocprofv3 summary committed beside
 the kernel-trace summary); traffic is null when that file is absent.
 
 Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--no-e2e] [--no-cpu]
-       python bench.py --section fp32-layout|other-configs   (one section only)
+       python bench.py --section fp32-layout|other-configs|reference-shapes   (one section only)
        python bench.py --traffic     (counter passes only; prints nothing)
        python bench.py --e2e-only [prefill|decode|moe]   (end-to-end model figures only)
 """
@@ -663,6 +665,54 @@ def isolated_configs(steps: int, warmup: int):
     return out
 
 
+REFERENCE_BENCH_SHAPES = ((4, 512, 4, 256), (4, 1024, 4, 512), (2, 2048, 8, 512))
+
+
+def reference_bench_shapes(warmup: int = 10, runs: int = 50):
+    """The reference's own speed workloads (model/mhc_fused.py:1028-1077 with
+    the shapes of :1103-1108): one MHCConnection_Fused (bf16, default
+    constructor, so 10 Sinkhorn iterations) around a sublayer MLP
+    C -> 4C -> C (SiLU, no bias), loss out.float().pow(2).mean(), forward +
+    backward, gradients cleared after each step; `runs` steps bracketed by one
+    event pair after `warmup`, as the reference times them.  `mhc_only` is the
+    same step with the identity as the sublayer (the connection's own forward
+    and backward launches, plus the loss).  tokens_per_s = B * L / step."""
+    import torch
+    import torch.nn as nn
+    from model.mhc_fused import MHCConnection_Fused
+
+    dev = torch.device("cuda:0")
+    out = {}
+    for B, L, n, C in REFERENCE_BENCH_SHAPES:
+        torch.manual_seed(0)
+        mlp = nn.Sequential(nn.Linear(C, 4 * C, bias=False), nn.SiLU(),
+                            nn.Linear(4 * C, C, bias=False)).to(dev).to(torch.bfloat16)
+        mhc = MHCConnection_Fused(n, C).to(dev).to(torch.bfloat16)
+        x_t = torch.randn(B, L, n * C, device=dev).to(torch.bfloat16)
+        params = list(mhc.parameters()) + list(mlp.parameters())
+        res = {"B": B, "L": L, "n": n, "C": C}
+        for key, fn in (("with_mlp", mlp), ("mhc_only", lambda z: z)):
+            def one():
+                x = x_t.clone().requires_grad_(True)
+                loss = mhc(x, fn).float().pow(2).mean()
+                loss.backward()
+                for p_ in params:
+                    p_.grad = None
+            for _ in range(warmup):
+                one()
+            _sync()
+            e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+            e0.record()
+            for _ in range(runs):
+                one()
+            e1.record()
+            _sync()
+            ms = e0.elapsed_time(e1) / runs
+            res[key] = {"ms_per_step": round(ms, 4), "tokens_per_s": round(B * L / (ms * 1e-3), 1)}
+        out[f"B{B}_L{L}_n{n}_C{C}"] = res
+    return out
+
+
 def _dense_config(**kw):
     from model.model_minimind import MiniMindConfig
     base = dict(hidden_size=768, num_hidden_layers=8, num_attention_heads=8, num_key_value_heads=4,
@@ -804,7 +854,8 @@ def main():
                     choices=["all", "prefill", "decode", "moe"],
                     help="run only the end-to-end model figures (configs 3, 4, 5, or one of "
                          "them) and print them as one JSON line")
-    ap.add_argument("--section", choices=["fp32-layout", "other-configs"], default=None,
+    ap.add_argument("--section", choices=["fp32-layout", "other-configs", "reference-shapes"],
+                    default=None,
                     help="run only the fp32-layout launches or the isolated config-4 / config-5 "
                          "kernel pairs and print them as one JSON line (for profiler runs)")
     ap.add_argument("--mfma-kernels", action="store_true",
@@ -826,6 +877,9 @@ def main():
         return
     if args.section == "fp32-layout":
         print(json.dumps({"fp32_layout": bench_layout32()}), flush=True)
+        return
+    if args.section == "reference-shapes":
+        print(json.dumps({"reference_bench_shapes": reference_bench_shapes()}), flush=True)
         return
     if args.section == "other-configs":
         print(json.dumps({"other_configs": isolated_configs(max(10, args.steps // 2),
@@ -907,6 +961,7 @@ def main():
     line["backward_c5"] = bw5
     line["fp32_layout"] = bench_layout32()
     line["other_configs"] = isolated_configs(max(10, args.steps // 2), max(3, args.warmup // 2))
+    line["reference_bench_shapes"] = reference_bench_shapes()
     if not args.no_e2e:
         line["e2e_prefill"] = e2e_prefill()
         line["e2e_decode"] = e2e_decode()

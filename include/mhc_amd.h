@@ -4,13 +4,15 @@
  * Every entry point takes raw device pointers, plain sizes and a hipStream_t,
  * enqueues its kernels on that stream and returns without synchronising.
  * The caller allocates every output (as the reference's autograd Functions do
- * with torch.empty); the library never allocates or frees device memory and
- * keeps no state between calls, so calls are re-entrant and capturable.  It has
- * two process-wide settings, both kernel choices: mhc_pre_token_threshold and
- * mhc_pre_row_staging.  One entry point (mhc_pre_bwd_weights) needs scratch
- * for token-range partial sums; the caller passes it as a workspace argument,
- * or calls mhc_pre_bwd_weights_noalloc, which uses a static device array the
- * library holds instead.
+ * with torch.empty); the library never allocates or frees device memory.  It
+ * keeps no per-call state, so calls are re-entrant and capturable, with one
+ * exception below.  It has two process-wide settings, both kernel choices:
+ * mhc_pre_token_threshold and mhc_pre_row_staging.  One entry point
+ * (mhc_pre_bwd_weights) needs scratch for token-range partial sums; the caller
+ * passes it as a workspace argument, or calls mhc_pre_bwd_weights_noalloc,
+ * which uses a 32 MiB static device array the library holds per device
+ * instead.  That array is the exception: calls of the noalloc entry point
+ * that overlap on one device share it and race.
  *
  * Return value: 0 on success.  Otherwise a hipError_t code
  * (hipErrorInvalidValue = 1 for bad arguments); mhc_last_error() then returns a
@@ -51,6 +53,16 @@ int mhc_abi_version(void);
 
 /* Message for the last non-zero status returned on this thread. */
 const char* mhc_last_error(void);
+
+/*
+ * One-time set-up for every visible device: looks up each device's copy of
+ * the scratch array that mhc_pre_bwd_weights_noalloc uses.  Call it once
+ * before capturing that entry point in a HIP graph; the entry point refuses a
+ * device it has not seen while its stream is being captured.  Idempotent,
+ * thread-safe, no device allocation.
+ * No reference counterpart (the reference has no allocation-free path).
+ */
+int mhc_init(void);
 
 /*
  * Size in bytes of the MFMA operand image of phi for (n, C, mode), or 0 when
@@ -360,7 +372,8 @@ int mhc_pre_bwd_weights(const void* x, int x_dtype, const float* inv_rms, const 
  * differently (fp32 rounding only).  Rejects shapes whose one-range partials,
  * (n*C*FD + 2*FD) * 4 bytes, exceed the scratch (e.g. n = 16, C = 2048).
  * Calls that overlap on one device share the scratch and race: serialise
- * them (one stream, or events between streams).
+ * them (one stream, or events between streams).  Call mhc_init() (or this
+ * entry point once, uncaptured) before capturing it in a HIP graph.
  * No reference counterpart: for callers that cannot allocate device memory
  * (code under HIP graph capture, serving loops, harnesses that forbid
  * hipMalloc).

@@ -119,9 +119,28 @@ constexpr int kMaxDevices = 64;
 std::mutex g_scratch_mu;
 void* g_scratch_dev[kMaxDevices] = {};
 
+// Looks up device `dev`'s copy of scratch with that device current (the caller
+// holds g_scratch_mu).  The host-side name `scratch` is not a device address
+// and is never passed to a kernel.
+int resolve_scratch(int dev, int cur, const char* fn) {
+  if (g_scratch_dev[dev]) return 0;
+  if (dev != cur)
+    if (hipError_t e = hipSetDevice(dev); e != hipSuccess) return hip_status(e, fn);
+  void* p = nullptr;
+  const hipError_t e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+  if (dev != cur) (void)hipSetDevice(cur);
+  if (e != hipSuccess || !p)
+    return fail(e != hipSuccess ? (int)e : (int)hipErrorInvalidSymbol,
+                "%s: hipGetSymbolAddress(scratch) on device %d failed: %s", fn, dev, hipGetErrorString(e));
+  g_scratch_dev[dev] = p;
+  return 0;
+}
+
 // Device address of this device's copy of scratch (the device `stream` runs
-// on), looked up once per device with that device current.  The host-side
-// name `scratch` is not a device address and is never passed to a kernel.
+// on).  mhc_init looks it up for every device at set-up; a device it has not
+// seen is looked up here on its first call, which is refused while `stream`
+// is being captured (the lookup may load the code object on that device,
+// which is not a capturable operation).
 int scratch_ptr(hipStream_t stream, void** out, const char* fn) {
   int cur = 0;
   if (hipError_t e = hipGetDevice(&cur); e != hipSuccess) return hip_status(e, fn);
@@ -131,15 +150,13 @@ int scratch_ptr(hipStream_t stream, void** out, const char* fn) {
   if (dev < 0 || dev >= kMaxDevices) return fail(hipErrorInvalidValue, "%s: device %d out of range", fn, dev);
   std::lock_guard<std::mutex> lock(g_scratch_mu);
   if (!g_scratch_dev[dev]) {
-    if (dev != cur)
-      if (hipError_t e = hipSetDevice(dev); e != hipSuccess) return hip_status(e, fn);
-    void* p = nullptr;
-    const hipError_t e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
-    if (dev != cur) (void)hipSetDevice(cur);
-    if (e != hipSuccess || !p)
-      return fail(e != hipSuccess ? (int)e : (int)hipErrorInvalidSymbol,
-                  "%s: hipGetSymbolAddress(scratch) failed: %s", fn, hipGetErrorString(e));
-    g_scratch_dev[dev] = p;
+    hipStreamCaptureStatus cs = hipStreamCaptureStatusNone;
+    if (hipError_t e = hipStreamIsCapturing(stream, &cs); e != hipSuccess) return hip_status(e, fn);
+    if (cs != hipStreamCaptureStatusNone)
+      return fail(hipErrorStreamCaptureUnsupported,
+                  "%s: the scratch of device %d is not set up; call mhc_init() (or this entry "
+                  "point once) before capturing", fn, dev);
+    if (int rc = resolve_scratch(dev, cur, fn)) return rc;
   }
   *out = g_scratch_dev[dev];
   return 0;
@@ -149,7 +166,19 @@ int scratch_ptr(hipStream_t stream, void** out, const char* fn) {
 
 extern "C" {
 
-int mhc_abi_version(void) { return 5; }
+int mhc_abi_version(void) { return 6; }
+
+int mhc_init(void) {
+  const char* fn = "mhc_init";
+  int count = 0;
+  if (hipError_t e = hipGetDeviceCount(&count); e != hipSuccess) return hip_status(e, fn);
+  int cur = 0;
+  if (hipError_t e = hipGetDevice(&cur); e != hipSuccess) return hip_status(e, fn);
+  std::lock_guard<std::mutex> lock(g_scratch_mu);
+  for (int dev = 0; dev < count && dev < kMaxDevices; ++dev)
+    if (int rc = resolve_scratch(dev, cur, fn)) return rc;
+  return 0;
+}
 
 const char* mhc_last_error(void) { return g_err; }
 
@@ -549,7 +578,7 @@ int mhc_pre_bwd_weights_noalloc(const void* x, int x_dtype, const float* inv_rms
 
 int mhc_sinkhorn_bwd_max_iters(int n) {
   if (n < 1 || n > 16) return 0;
-  return n == 2 || n == 4 || n == 8 ? 64 : 30;  // the trajectory lives in 64 KiB of LDS per wave
+  return mhc::kSinkhornBwdMaxIters;  // checkpointed recompute: LDS grows as sqrt(iters)
 }
 
 int mhc_sinkhorn_bwd(const void* m_in, int in_dtype, const void* g_out, int g_dtype, void* g_in,

@@ -74,8 +74,7 @@ __global__ __launch_bounds__(256) void pre_bwd_generic_kernel(PreBwdArgs a) {
     if (tid == 0) s_gh[i] = t + (a.g_hpre ? ld_any(a.g_hpre, tok * n + i, gdt) : 0.f);
   }
   __syncthreads();
-  if (tid < FD) {
-    const int f = tid;
+  for (int f = tid; f < FD; f += 256) {  // FD = 288 at n = 16
     const float m = a.mixes[tok * FD + f];
     const int pdt = a.param_dtype;
     float graw, alpha;
@@ -576,17 +575,18 @@ __global__ __launch_bounds__(256) void weights_partial_generic_kernel(WeightsArg
       acc = fmaf(ld_any(a.x, t * NC + k, a.x_dtype) * a.inv_rms[t], a.g_raw[t * FD + f], acc);
     a.work[(r * NC + k) * FD + f] = acc;
   }
-  if (blockIdx.y == 0 && threadIdx.x < FD) {  // alpha / bias partials of this range
-    const int f = threadIdx.x;
-    float sb = 0.f, sa = 0.f;
-    for (int64_t t = t0; t < t1; ++t) {
-      const float gr = a.g_raw[t * FD + f];
-      sb += gr;
-      sa = fmaf(gr, a.mixes[t * FD + f], sa);
+  if (blockIdx.y == 0) {  // alpha / bias partials of this range (FD = 288 at n = 16)
+    for (int f = threadIdx.x; f < FD; f += 256) {
+      float sb = 0.f, sa = 0.f;
+      for (int64_t t = t0; t < t1; ++t) {
+        const float gr = a.g_raw[t * FD + f];
+        sb += gr;
+        sa = fmaf(gr, a.mixes[t * FD + f], sa);
+      }
+      float* ab = a.work + (int64_t)R * NC * FD + (int64_t)r * 2 * FD;
+      ab[f] = sb;
+      ab[FD + f] = sa;
     }
-    float* ab = a.work + (int64_t)R * NC * FD + (int64_t)r * 2 * FD;
-    ab[f] = sb;
-    ab[FD + f] = sa;
   }
 }
 
@@ -880,14 +880,19 @@ hipError_t launch_pre_bwd_weights(const WeightsArgs& a, hipStream_t s) {
 
 // ------------------------------------------------------- Sinkhorn backward
 // One 256-thread workgroup holds 256 / n^2 matrices, one element per thread.
-// LDS: the softmax P, the 2*iters forward iterates T[s] and a scratch row.
 // Forward T[0] = P + eps, T[1] = T[0] / (colsum + eps), then row / column
 // steps; backward through y = x / (sum(x) + eps):  g_x = (g_y - sum(g_y * y)) / (sum(x) + eps),
 // and through the softmax: g_m = P * (g - rowsum(g * P)).
+// The trajectory is not kept whole: the forward stores every K-th iterate
+// (checkpoints), and the backward walks the segments from the last, first
+// recomputing a segment's K + 1 iterates from its checkpoint with the same
+// operations (so the same bits).  LDS holds the softmax P, J checkpoints, one
+// segment and a scratch row: (J + K + 3) * 1 KiB with K ~ J ~ sqrt(steps).
 __global__ __launch_bounds__(256) void sinkhorn_bwd_kernel(const void* __restrict__ m_in, int in_dt,
                                                            const void* __restrict__ g_out, int g_dt,
                                                            void* __restrict__ g_in, int gi_dt,
-                                                           int64_t batch, int n, int iters, float eps) {
+                                                           int64_t batch, int n, int iters, float eps,
+                                                           int K) {
   extern __shared__ float lds[];
   const int G = n * n;
   const int per = 256 / G;                  // matrices per workgroup
@@ -900,9 +905,11 @@ __global__ __launch_bounds__(256) void sinkhorn_bwd_kernel(const void* __restric
   const bool live = m_loc < per && mat < batch;
   const int64_t idx = mat * G + e;
   const int steps = 2 * (iters > 1 ? iters : 1);
+  const int J = (steps - 1 + K - 1) / K;    // segments of backward steps 1 .. steps - 1
   float* P = lds;                           // [256]
-  float* T = lds + 256;                     // [steps][256]
-  float* S = T + (int64_t)steps * 256;      // [256] scratch
+  float* CK = lds + 256;                    // [J][256] iterate jK
+  float* SEG = CK + (int64_t)J * 256;       // [K + 1][256] iterates jK .. jK + K
+  float* S = SEG + (int64_t)(K + 1) * 256;  // [256] scratch
   // First element of this row / column (stride n).  Threads past the last
   // whole matrix (256 % n^2 of them) read matrix 0 and store nothing.
   const int rb = m_loc < per ? tid - e + r * n : 0;
@@ -917,8 +924,13 @@ __global__ __launch_bounds__(256) void sinkhorn_bwd_kernel(const void* __restric
     for (int i = 0; i < n; ++i) s += A[cb + i * n];
     return s;
   };
+  // One forward step s (odd: column, even: row) from X into Y.
+  auto fwd_step = [&](int s, const float* X, float* Y) {
+    const float den = ((s & 1) ? col_sum(X) : row_sum(X)) + eps;
+    Y[tid] = X[tid] / den;
+  };
 
-  // forward recompute
+  // forward recompute, keeping iterates 0, K, 2K, ... (two SEG rows alternate)
   const float v = live ? ld_any(m_in, idx, in_dt) : 0.f;
   S[tid] = v;
   __syncthreads();
@@ -930,26 +942,39 @@ __global__ __launch_bounds__(256) void sinkhorn_bwd_kernel(const void* __restric
   __syncthreads();
   const float p = ex / row_sum(S);
   P[tid] = p;
-  T[tid] = p + eps;
+  SEG[tid] = p + eps;
+  CK[tid] = p + eps;
   __syncthreads();
-  for (int s = 1; s < steps; ++s) {  // odd s: column step, even s: row step
-    const float* X = T + (int64_t)(s - 1) * 256;
-    const float den = ((s & 1) ? col_sum(X) : row_sum(X)) + eps;
-    T[(int64_t)s * 256 + tid] = X[tid] / den;
+  for (int s = 1; s < (J - 1) * K + 1; ++s) {  // up to the last checkpoint
+    const float* X = SEG + (int64_t)((s - 1) & 1) * 256;
+    float* Y = SEG + (int64_t)(s & 1) * 256;
+    fwd_step(s, X, Y);
+    if (s % K == 0) CK[(int64_t)(s / K) * 256 + tid] = Y[tid];
     __syncthreads();
   }
-  // backward
+  // backward, one segment at a time from the last
   float g = live ? ld_any(g_out, idx, g_dt) : 0.f;
-  for (int s = steps - 1; s >= 1; --s) {
-    const float* X = T + (int64_t)(s - 1) * 256;
-    const float* Y = T + (int64_t)s * 256;
+  for (int j = J - 1; j >= 0; --j) {
+    const int s0 = j * K;
+    const int s1 = s0 + K < steps - 1 ? s0 + K : steps - 1;  // last backward step of the segment
+    __syncthreads();                      // every read of the previous segment done
+    SEG[tid] = CK[(int64_t)j * 256 + tid];
     __syncthreads();
-    S[tid] = g * Y[tid];
-    __syncthreads();
-    const bool col = s & 1;
-    const float dot = col ? col_sum(S) : row_sum(S);
-    const float den = (col ? col_sum(X) : row_sum(X)) + eps;
-    g = (g - dot) / den;
+    for (int s = s0 + 1; s <= s1; ++s) {
+      fwd_step(s, SEG + (int64_t)(s - 1 - s0) * 256, SEG + (int64_t)(s - s0) * 256);
+      __syncthreads();
+    }
+    for (int s = s1; s >= s0 + 1; --s) {
+      const float* X = SEG + (int64_t)(s - 1 - s0) * 256;
+      const float* Y = SEG + (int64_t)(s - s0) * 256;
+      __syncthreads();
+      S[tid] = g * Y[tid];
+      __syncthreads();
+      const bool col = s & 1;
+      const float dot = col ? col_sum(S) : row_sum(S);
+      const float den = (col ? col_sum(X) : row_sum(X)) + eps;
+      g = (g - dot) / den;
+    }
   }
   __syncthreads();
   S[tid] = g * p;
@@ -1045,6 +1070,21 @@ __global__ __launch_bounds__(256) void sinkhorn_bwd_regs_kernel(const void* __re
   if (live) st_any(g_in, idx, gi_dt, gm);
 }
 
+// Segment length K of sinkhorn_bwd_kernel for a schedule of 2 * iters steps
+// (about the square root of the step count) and its LDS bytes.
+int sinkhorn_bwd_segment(int iters) {
+  const int steps = 2 * (iters > 1 ? iters : 1);
+  int K = 1;
+  while (K * K < steps - 1) ++K;
+  return K;
+}
+size_t sinkhorn_bwd_lds_bytes(int iters) {
+  const int steps = 2 * (iters > 1 ? iters : 1);
+  const int K = sinkhorn_bwd_segment(iters);
+  const int J = (steps - 1 + K - 1) / K;
+  return (size_t)(J + K + 3) * 256 * sizeof(float);
+}
+
 hipError_t launch_sinkhorn_bwd(const void* m_in, int in_dtype, const void* g_out, int g_dtype,
                                void* g_in, int gi_dtype, int64_t batch, int n, int iters,
                                float eps, hipStream_t s) {
@@ -1057,7 +1097,7 @@ hipError_t launch_sinkhorn_bwd(const void* m_in, int in_dtype, const void* g_out
     }
     return hipGetLastError();
   }
-  if (n == 2 || n == 4 || n == 8) {
+  if ((n == 2 || n == 4 || n == 8) && iters <= kSinkhornBwdLanesMaxIters) {
     const int steps = 2 * (iters > 1 ? iters : 1);
     const size_t lds = (size_t)2 * steps * 64 * sizeof(float);
     const int64_t blocks = (batch * n * n + 63) / 64;
@@ -1071,10 +1111,10 @@ hipError_t launch_sinkhorn_bwd(const void* m_in, int in_dtype, const void* g_out
   const int G = n * n;
   const int per = 256 / G;
   const int64_t blocks = (batch + per - 1) / per;
-  const int steps = 2 * (iters > 1 ? iters : 1);
-  const size_t lds = (size_t)(steps + 2) * 256 * sizeof(float);
+  const int K = sinkhorn_bwd_segment(iters);
+  const size_t lds = sinkhorn_bwd_lds_bytes(iters);
   hipLaunchKernelGGL(sinkhorn_bwd_kernel, dim3((unsigned)blocks), dim3(256), lds, s, m_in, in_dtype,
-                     g_out, g_dtype, g_in, gi_dtype, batch, n, iters, eps);
+                     g_out, g_dtype, g_in, gi_dtype, batch, n, iters, eps, K);
   return hipGetLastError();
 }
 

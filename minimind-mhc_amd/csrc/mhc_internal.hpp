@@ -159,6 +159,14 @@ int64_t weights_workspace_bytes(int64_t M, int n, int C, int mode);
 // Workspace bytes of one token range (its phi partials and alpha / bias sums).
 int64_t weights_range_bytes(int n, int C, int mode);
 hipError_t launch_pre_bwd_weights(const WeightsArgs& a, hipStream_t s);
+// Sinkhorn backward schedules: n in {2, 4, 8} keep the trajectory per lane up
+// to kSinkhornBwdLanesMaxIters iterations; longer schedules and other n run
+// the checkpointed workgroup kernel, up to kSinkhornBwdMaxIters (its LDS,
+// (J + K + 3) KiB with K ~ J ~ sqrt(2 * iters), stays under 64 KiB).
+constexpr int kSinkhornBwdLanesMaxIters = 64;
+constexpr int kSinkhornBwdMaxIters = 256;
+int sinkhorn_bwd_segment(int iters);
+size_t sinkhorn_bwd_lds_bytes(int iters);
 hipError_t launch_sinkhorn_bwd(const void* m_in, int in_dtype, const void* g_out, int g_dtype,
                                void* g_in, int gi_dtype, int64_t batch, int n, int iters,
                                float eps, hipStream_t s);

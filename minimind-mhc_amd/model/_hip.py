@@ -31,6 +31,7 @@ _F = ctypes.c_float
 _SIGNATURES = {
     "mhc_abi_version": (_I, []),
     "mhc_last_error": (ctypes.c_char_p, []),
+    "mhc_init": (_I, []),
     "mhc_phi_packed_bytes": (_I64, [_I, _I, _I]),
     "mhc_phi_pack": (_I, [_P, _I, _P, _I, _I, _I, _P]),
     "mhc_phi_split_bytes": (_I64, [_I, _I, _I]),
@@ -87,7 +88,7 @@ _SIGNATURES = {
     "mhc_sinkhorn_bwd_max_iters": (_I, [_I]),
 }
 
-ABI_VERSION = 5
+ABI_VERSION = 6
 _lib: Optional[ctypes.CDLL] = None
 
 
@@ -108,6 +109,10 @@ def load() -> ctypes.CDLL:
     if lib.mhc_abi_version() != ABI_VERSION:
         raise RuntimeError(f"mhc_amd: ABI version {lib.mhc_abi_version()} != {ABI_VERSION}")
     _lib = lib
+    if torch.cuda.is_available():
+        # per-device set-up (the noalloc entry point's scratch addresses), done
+        # here so that no later call needs it inside a graph capture
+        check(lib.mhc_init(), "mhc_init")
     return lib
 
 

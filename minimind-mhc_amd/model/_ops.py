@@ -122,8 +122,15 @@ class PhiPack:
 
 
 # Packs of weights that no module owns (the reference-style autograd Functions
-# called directly): id(phi), mode -> (weak reference to phi, PhiPack).
+# called directly): id(phi), mode -> (weak reference to phi, PhiPack).  An entry
+# goes (with its device image) as soon as its weight is freed.
 _PACKS: dict = {}
+
+
+def _drop_pack(key, ref) -> None:
+    ent = _PACKS.get(key)
+    if ent is not None and ent[0] is ref:
+        del _PACKS[key]
 
 
 def packed_phi(phi: torch.Tensor, n: int, C: int, mode: int,
@@ -135,10 +142,7 @@ def packed_phi(phi: torch.Tensor, n: int, C: int, mode: int,
     key = (id(phi), mode)
     ent = _PACKS.get(key)
     if ent is None or ent[0]() is not phi:
-        if len(_PACKS) >= 256:
-            for k in [k for k, (ref, _) in _PACKS.items() if ref() is None]:
-                del _PACKS[k]
-        ent = (weakref.ref(phi), PhiPack(mode))
+        ent = (weakref.ref(phi, lambda ref, key=key: _drop_pack(key, ref)), PhiPack(mode))
         _PACKS[key] = ent
     return ent[1].get(phi, n, C, training)
 

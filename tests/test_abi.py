@@ -60,10 +60,9 @@ def test_packed_sizes(lib):
 
 
 def test_sinkhorn_bwd_max_iters(lib):
-    assert lib.mhc_sinkhorn_bwd_max_iters(4) == 64
-    assert lib.mhc_sinkhorn_bwd_max_iters(8) == 64
-    assert lib.mhc_sinkhorn_bwd_max_iters(3) == 30
-    assert lib.mhc_sinkhorn_bwd_max_iters(16) == 30
+    # checkpointed recompute: one cap for every n
+    for n in (1, 2, 3, 4, 8, 16):
+        assert lib.mhc_sinkhorn_bwd_max_iters(n) == 256
     assert lib.mhc_sinkhorn_bwd_max_iters(0) == 0
     assert lib.mhc_sinkhorn_bwd_max_iters(17) == 0
 

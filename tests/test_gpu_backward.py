@@ -99,7 +99,11 @@ def test_sinkhorn_bwd_vs_autograd(dev, n, iters):
     assert maxrel(mr.grad.float(), got) <= 1e-4
 
 
-@pytest.mark.parametrize("n,iters", [(4, 64), (8, 40), (3, 30)])
+# (4, 64), (8, 40): the per-lane trajectory kernel at its longest; the rest
+# take the checkpointed workgroup kernel (segments recomputed from every K-th
+# iterate), up to the 256-iteration cap, n = 16 included.
+@pytest.mark.parametrize("n,iters", [(4, 64), (8, 40), (3, 30), (16, 31), (16, 100), (4, 65),
+                                     (2, 130), (8, 256), (1, 50), (5, 7)])
 def test_sinkhorn_bwd_long_schedules(dev, n, iters):
     g = torch.Generator().manual_seed(n + iters)
     m = torch.randn(33, n, n, generator=g)
@@ -111,8 +115,11 @@ def test_sinkhorn_bwd_long_schedules(dev, n, iters):
 
 
 def test_sinkhorn_bwd_iteration_limit(dev):
+    cap = H.load().mhc_sinkhorn_bwd_max_iters(3)
+    assert cap == 256
     with pytest.raises(RuntimeError, match="iters must be"):
-        _ops.sinkhorn_bwd(torch.zeros(2, 3, 3, device=dev), torch.zeros(2, 3, 3, device=dev), 31, 1e-6)
+        _ops.sinkhorn_bwd(torch.zeros(2, 3, 3, device=dev), torch.zeros(2, 3, 3, device=dev),
+                          cap + 1, 1e-6)
 
 
 def test_sinkhorn_bwd_bf16_io(dev):
@@ -150,8 +157,9 @@ def _pre_case(dev, kind, n, C, M, dtype, seed):
 
 
 @pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
+# n = 16: FD = 288 features, more than a 256-thread workgroup has threads
 @pytest.mark.parametrize("n,C,M", [(4, 64, 24), (4, 768, 300), (2, 100, 17), (8, 768, 40),
-                                   (1, 64, 9), (4, 256, 1100)])
+                                   (1, 64, 9), (4, 256, 1100), (16, 64, 20), (16, 256, 300)])
 def test_pre_full_bwd_vs_oracle(dev, dtype, n, C, M):
     """g_x, g_phi, alphas and biases of the full pre phase for given upstream
     gradients of (sublayer_in, h_pre, h_post, h_res_raw)."""
@@ -268,8 +276,9 @@ def test_module_bf16_training_step_matches_oracle(dev):
 
     xr = _leaf(x)
     pr = {k: _leaf(v) for k, v in p.items()}
-    ref = R.mhc_full_forward(xr, pr, lambda s: s @ fw.float().t(), n, C, sinkhorn_iters=20)["out"]
-    (ref.float() * gout.float()).sum().backward()
+    d = R.mhc_full_forward(xr, pr, lambda s: s @ fw.float().t(), n, C, sinkhorn_iters=20)
+    d["mixes"].retain_grad()
+    (d["out"].float() * gout.float()).sum().backward()
 
     mod = MHCConnection_Fused(n, C, sinkhorn_iters=20).to(dev).to(torch.bfloat16)
     with torch.no_grad():
@@ -283,3 +292,43 @@ def test_module_bf16_training_step_matches_oracle(dev):
     assert maxrel(pr["phi_weight"].grad, mod.phi_weight.grad) <= 2e-2
     for k in ("bias_pre", "bias_post", "bias_res"):
         assert maxrel(pr[k].grad, getattr(mod, k).grad) <= 2e-2, k
+    # alpha_seg's gradient is sum_t sum_f g_raw[t, f] * mixes[t, f] with
+    # g_raw = d loss / d mixes / alpha_seg; it can cancel far below its terms,
+    # so it is held to 2e-2 of the terms' magnitudes (the oracle's)
+    mixes, g_mixes = d["mixes"].detach(), d["mixes"].grad
+    for seg, (lo, hi) in (("pre", (0, n)), ("post", (n, 2 * n)), ("res", (2 * n, 2 * n + n * n))):
+        ref_a = pr[f"alpha_{seg}"]
+        terms = (g_mixes[..., lo:hi] / ref_a.detach() * mixes[..., lo:hi]).abs().sum().item()
+        got = getattr(mod, f"alpha_{seg}").grad.float().item()
+        err = abs(ref_a.grad.item() - got) / max(abs(ref_a.grad.item()), terms, 1e-30)
+        assert err <= 2e-2, (seg, err)
+
+
+@pytest.mark.parametrize("n,iters", [(16, 40), (4, 100), (16, 20)])
+def test_module_training_long_sinkhorn_matches_oracle(dev, n, iters):
+    """A training step with more Sinkhorn iterations than the per-lane backward
+    kernels keep (n = 16 past 30, n = 4 past 64): the checkpointed backward,
+    fp32, against autograd of the oracle."""
+    from model.mhc_fused import MHCConnection_Fused
+    C, M = 64, 24
+    g = torch.Generator().manual_seed(40 + n)
+    x = torch.randn(1, M, n * C, generator=g)
+    p = make_params("full", n, C, torch.float32, g, stress=True)
+    fw = torch.randn(C, C, generator=g) * 0.1
+    gout = torch.randn(1, M, n * C, generator=g)
+    xr = _leaf(x)
+    pr = {k: _leaf(v) for k, v in p.items()}
+    ref = R.mhc_full_forward(xr, pr, lambda s: s @ fw.t(), n, C, sinkhorn_iters=iters)["out"]
+    (ref * gout).sum().backward()
+    mod = MHCConnection_Fused(n, C, sinkhorn_iters=iters).to(dev)
+    with torch.no_grad():
+        for k, v in p.items():
+            getattr(mod, k).copy_(v)
+    xd = x.to(dev).requires_grad_(True)
+    fwd_t = fw.t().contiguous().to(dev)
+    out = mod(xd, lambda s: s @ fwd_t)
+    (out * gout.to(dev)).sum().backward()
+    assert maxrel(ref.detach(), out.detach().cpu()) <= 1e-5
+    assert maxrel(xr.grad, xd.grad) <= 1e-4
+    assert maxrel(pr["phi_weight"].grad, mod.phi_weight.grad) <= 1e-4
+    assert maxrel(pr["bias_res"].grad, mod.bias_res.grad) <= 1e-4

@@ -128,3 +128,120 @@ def test_reference_fp16_checkpoint_runs_on_hip_model(dev, tmp_path, use_mhc, n, 
         want = ref(ids).logits
         got = model.to(dev)(ids.to(dev)).logits
     assert _rel(got, want) < 1e-4, _rel(got, want)
+
+
+def _hook_mhc(model):
+    """Wrap every mHC piece of a model so that each call records its inputs
+    and outputs: the connections (x, the sublayer's input, the sublayer's
+    output, out), the entry RMSNorm + StreamExpand and the exit MHCHead +
+    final RMSNorm.  Returns the record list (filled in call order)."""
+    from model.mhc_common import MHCHead, StreamExpand
+    from model.mhc_fused import MHCConnection_Fused
+
+    records = []
+    for name, mod in model.named_modules():
+        if isinstance(mod, MHCConnection_Fused):
+            def conn(x, f, in_norm=None, _orig=mod.forward, _mod=mod, _name=name):
+                rec = {"kind": "conn", "name": _name, "mod": _mod, "norm": in_norm,
+                       "x": x.detach().clone()}
+
+                def fw(z):
+                    rec["z"] = z.detach().clone()
+                    o = f(z)
+                    rec["f"] = o.detach().clone()
+                    return o
+                out = _orig(x, fw, in_norm)
+                rec["out"] = out.detach().clone()
+                records.append(rec)
+                return out
+            mod.forward = conn
+        elif isinstance(mod, StreamExpand):
+            def expand(x, norm, _orig=mod.forward_normed, _mod=mod):
+                out = _orig(x, norm)
+                records.append({"kind": "entry", "mod": _mod, "norm": norm,
+                                "x": x.detach().clone(), "out": out.detach().clone()})
+                return out
+            mod.forward_normed = expand
+        elif isinstance(mod, MHCHead):
+            def head(x, out_norm=None, _orig=mod.forward, _mod=mod):
+                out = _orig(x, out_norm)
+                records.append({"kind": "exit", "mod": _mod, "norm": out_norm,
+                                "x": x.detach().clone(), "out": out.detach().clone()})
+                return out
+            mod.forward = head
+    return records
+
+
+def _cpu_norm(norm):
+    """The GPU model's nn.RMSNorm as a bf16 CPU module with the same gain."""
+    c = torch.nn.RMSNorm(norm.normalized_shape, eps=norm.eps).to(torch.bfloat16)
+    with torch.no_grad():
+        c.weight.copy_(norm.weight.detach().cpu())
+    return c
+
+
+def _check_record(rec):
+    """One recorded mHC call against the oracle on its captured inputs (bf16,
+    the reference's rounding points, max-norm 1e-2).  A connection's sublayer
+    returns the captured sublayer output, so the comparison is of the mHC
+    arithmetic alone; its sublayer input (normed) is compared too."""
+    from oracle import mhc_ref as R
+
+    mod, x = rec["mod"], rec["x"].cpu()
+    norm = _cpu_norm(rec["norm"]) if rec["norm"] is not None else (lambda t: t)
+    if rec["kind"] == "conn":
+        seen = {}
+
+        def f(s):
+            seen["z"] = norm(s)
+            return rec["f"].cpu()
+        d = R.mhc_full_forward(x, R.module_params(mod), f, mod.n, mod.dim, eps=mod.eps,
+                               pre_eps=mod.pre_eps, post_mult=mod.post_mult_value,
+                               sinkhorn_iters=mod.sinkhorn_iters, sinkhorn_eps=mod.sinkhorn_eps)
+        return {"out": _rel(rec["out"], d["out"]), "sublayer_in": _rel(rec["z"], seen["z"])}
+    if rec["kind"] == "entry":
+        want = R.stream_expand(norm(x), mod.n)
+    else:
+        want = norm(R.head(x, R.module_params(mod), mod.n, mod.dim, pre_eps=mod.pre_eps,
+                           rms_eps=mod.eps))
+    return {"out": _rel(rec["out"], want)}
+
+
+@pytest.mark.parametrize("config", ["c3", "c5"])
+@pytest.mark.parametrize("kernels", ["small_batch", "large_batch"])
+def test_bf16_model_every_connection_vs_oracle(dev, config, kernels):
+    """The bf16 C3 (n = 4) and C5 (n = 8, MoE) models with stress gates, B = 2,
+    T = 128: every connection, the entry RMSNorm + StreamExpand and the exit
+    MHCHead + final RMSNorm, each against the oracle on the inputs it saw in
+    the model (1e-2, the bf16 layer bar).  256 tokens take the small-batch
+    group kernel; kernels="large_batch" drops the token threshold to 0 so the
+    same model runs the persistent (n = 4) / K-streamed (n = 8) kernels.  The
+    model runs without autograd, so the norms are the fused epilogues."""
+    from model import _ops
+
+    cfg = _c3() if config == "c3" else _c5()
+    model = _build(cfg, "stress").to(torch.bfloat16).to(dev)
+    records = _hook_mhc(model)
+    g = torch.Generator().manual_seed(17)
+    ids = torch.randint(0, cfg.vocab_size, (2, 128), generator=g).to(dev)
+    prev = _ops.pre_token_threshold(0 if kernels == "large_batch" else 1024)
+    try:
+        print(f"bf16 per-connection {config} {kernels}", flush=True)
+        with torch.no_grad():
+            logits = model(ids).logits
+        torch.cuda.synchronize()
+    finally:
+        _ops.pre_token_threshold(prev)
+    assert torch.isfinite(logits.float()).all()
+    kinds = [r["kind"] for r in records]
+    assert kinds.count("entry") == 1 and kinds.count("exit") == 1
+    assert kinds.count("conn") == 2 * cfg.num_hidden_layers
+    worst = {}
+    for rec in records:
+        errs = _check_record(rec)
+        for k, v in errs.items():
+            key = (rec["kind"], rec.get("name", ""), k)
+            worst[key] = v
+    bad = {k: v for k, v in worst.items() if not v <= 1e-2}
+    assert not bad, bad
+    print(f"max per-connection error {max(worst.values()):.2e}", flush=True)

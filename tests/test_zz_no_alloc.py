@@ -97,10 +97,52 @@ def test_noalloc_rejects_oversized_rows(dev):
     lib = H.load()
     n, C = 16, 2048                      # (32768 * 288 + 576) * 4 B > 32 MiB
     assert (n * C * (2 * n + n * n) + 2 * (2 * n + n * n)) * 4 > SCRATCH_BYTES
-    t = torch.zeros(8, device=dev)
-    rc = lib.mhc_pre_bwd_weights_noalloc(t.data_ptr(), H.DTYPE_F32, t.data_ptr(), t.data_ptr(),
-                                         t.data_ptr(), t.data_ptr(), t.data_ptr(), t.data_ptr(),
-                                         H.DTYPE_F32, t.data_ptr(), H.DTYPE_F32, None, None, None,
+    # Null data pointers: should the size check ever regress, the host-side
+    # null check still refuses the call (and the message assertion fails)
+    # instead of a launch on buffers far smaller than the shape.
+    rc = lib.mhc_pre_bwd_weights_noalloc(None, H.DTYPE_F32, None, None, None, None, None, None,
+                                         H.DTYPE_F32, None, H.DTYPE_F32, None, None, None,
                                          None, None, None, 4, n, C, H.MODE_FULL, H.stream(dev))
     assert rc != 0
     assert "scratch" in lib.mhc_last_error().decode()
+
+
+def test_noalloc_captured_in_hip_graph(dev):
+    """The noalloc entry point captured in a HIP graph (the callers it is for)
+    and replayed three times, with eager calls between the replays that
+    overwrite the scratch; every replay equals the workspace entry point's
+    eager result bit for bit."""
+    lib = H.load()                       # runs mhc_init: scratch addresses set up before capture
+    n, C, mode, M = 4, 768, H.MODE_FULL, 4096
+    x, inv, mixes, g_raw, alphas, FD = _inputs(M, n, C, mode, torch.bfloat16, dev, 11)
+    ref = _call(lib, False, x, inv, mixes, g_raw, alphas, n, C, mode, torch.bfloat16, dev)
+    g_phi, g_a, g_b = _outputs(n, C, FD, torch.bfloat16, dev)
+    args = [x.data_ptr(), H.dtype_tag(x), inv.data_ptr(), mixes.data_ptr(), g_raw.data_ptr(),
+            alphas[0].data_ptr(), alphas[1].data_ptr(), alphas[2].data_ptr(), H.DTYPE_F32,
+            g_phi.data_ptr(), H.dtype_tag(g_phi),
+            g_a[0].data_ptr(), g_b[0].data_ptr(), g_a[1].data_ptr(), g_b[1].data_ptr(),
+            g_a[2].data_ptr(), g_b[2].data_ptr(), M, n, C, mode]
+    side = torch.cuda.Stream(dev)
+    side.wait_stream(torch.cuda.current_stream(dev))
+    with torch.cuda.stream(side):        # one uncaptured call first, as torch's capture docs ask
+        H.check(lib.mhc_pre_bwd_weights_noalloc(*args, H.stream(dev)), "noalloc warm-up")
+    torch.cuda.current_stream(dev).wait_stream(side)
+    torch.cuda.synchronize()
+    graph = torch.cuda.CUDAGraph()
+    rcs = []
+    with torch.cuda.graph(graph):
+        rcs.append(lib.mhc_pre_bwd_weights_noalloc(*args, H.stream(dev)))
+    assert rcs == [0], lib.mhc_last_error().decode()
+    other = _inputs(1000, n, C, mode, torch.bfloat16, dev, 12)
+    for rep in range(3):
+        print(f"noalloc graph replay {rep}", flush=True)
+        # eager work between replays: another call fills the scratch with
+        # other partials, and the outputs are reset
+        _call(lib, True, *other[:5], n, C, mode, torch.bfloat16, dev)
+        for t in [g_phi] + g_a + g_b:
+            t.fill_(float("nan"))
+        graph.replay()
+        torch.cuda.synchronize()
+        assert torch.equal(ref[0], g_phi)
+        for r, q in zip(ref[1] + ref[2], g_a + g_b):
+            assert torch.equal(r, q)
