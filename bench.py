@@ -116,7 +116,7 @@ def _queue_ahead(ms: float = 25.0):
 
 
 def bench_mhc(steps: int, warmup: int, sets: int = 8, n: int = N_STREAMS, C: int = C_DIM,
-              M: int = TOKENS, cold: bool = True):
+              M: int = TOKENS, cold: bool = True, chain: bool = True):
     """Steady-state kernel times over `sets` distinct input sets.
 
     Each step runs the pre kernel on every set, then the post kernel on every
@@ -128,7 +128,15 @@ def bench_mhc(steps: int, warmup: int, sets: int = 8, n: int = N_STREAMS, C: int
     own cost is spread over them (at config 2, 4 sets measured ~0.3 us a
     launch more than 8; 16 sets made the post launch slower, 36.7 us).  Also returns a cold-cache
     measurement (1 GiB read-only flush before each kernel, which leaves clean
-    lines, so writes are absorbed by the cache)."""
+    lines, so writes are absorbed by the cache).
+
+    chain: where the shape carries per-row sums of squares from the launch
+    that writes the stream to the pre launch that reads it (n >= 8 or
+    C > 1024, as inside a model, where each connection's post launch writes
+    the next one's input), the post launch writes them for its output and the
+    pre launch takes those of its input (for the rotating inputs, formed once
+    in the set-up, as a previous post launch would have).  chain=False times
+    the pre launch forming them itself."""
     import torch
     from model import _hip as H, _ops
 
@@ -142,6 +150,11 @@ def bench_mhc(steps: int, warmup: int, sets: int = 8, n: int = N_STREAMS, C: int
     br = torch.eye(n, dtype=torch.bfloat16, device=dev)
     packed = _ops.PhiPack(H.MODE_FULL).get(phi, n, C)
     assert packed is not None, "configs 2, 4 and 5 take the MFMA kernels"
+    use_ssq = chain and _ops.ssq_wanted(torch.bfloat16, n, C)
+    ssq_in = [(x.view(M, n, C // _ops.SSQ_COLS, _ops.SSQ_COLS).float().pow(2).sum(dim=(1, 3))
+               .contiguous() if use_ssq else None) for x in xs]
+    ssq_out = [torch.empty(M, C // _ops.SSQ_COLS, dtype=torch.float32, device=dev) if use_ssq
+               else None for _ in range(sets)]
 
     # Outputs are allocated once per input set through the checked op wrappers,
     # and the timed launches call the C ABI on them directly (what a C caller
@@ -160,10 +173,10 @@ def bench_mhc(steps: int, warmup: int, sets: int = 8, n: int = N_STREAMS, C: int
                  b0.data_ptr(), a.data_ptr(), b0.data_ptr(), a.data_ptr(), br.data_ptr(), BF,
                  outs[s]["sub_in"].data_ptr(), None, outs[s]["h_post"].data_ptr(), None,
                  outs[s]["h_res"].data_ptr(), None, None, M_, n, C, 2.0, 1e-6, 1e-6, ITERS, 1e-6,
-                 stream) for s in range(sets)]
+                 H.ptr(ssq_in[s]), stream) for s in range(sets)]
     post_args = [(xs[s].data_ptr(), BF, outs[s]["h_res"].data_ptr(), outs[s]["h_post"].data_ptr(),
-                  BF, fs[s].data_ptr(), BF, finals[s].data_ptr(), M_, n, C, stream)
-                 for s in range(sets)]
+                  BF, fs[s].data_ptr(), BF, finals[s].data_ptr(), M_, n, C, H.ptr(ssq_out[s]),
+                  stream) for s in range(sets)]
     pre_fn, post_fn = lib.mhc_pre_fwd, lib.mhc_post_fwd
 
     def pre(s):
@@ -217,7 +230,7 @@ def bench_mhc(steps: int, warmup: int, sets: int = 8, n: int = N_STREAMS, C: int
     t_pre = [a_.elapsed_time(b_) / sets for a_, b_ in rec["pre"]]
     t_post = [a_.elapsed_time(b_) / sets for a_, b_ in rec["post"]]
     steady = dict(t_pre=sum(t_pre) / len(t_pre), t_post=sum(t_post) / len(t_post),
-                  t_pre_min=min(t_pre), t_post_min=min(t_post))
+                  t_pre_min=min(t_pre), t_post_min=min(t_post), chain=bool(use_ssq))
     if not cold:
         return steady, None
 
@@ -648,15 +661,20 @@ def isolated_configs(steps: int, warmup: int):
     pair is launch-bound; and at the widest shapes the reference's module
     accepts (model/mhc_fused.py:599-600, :784): dim 2048 at n = 4 and n = 16
     at dim 768, 16384 tokens each (K-streamed pre kernel; one-wave-per-token
-    post kernel at n = 16).  Timed as bench_mhc times config 2."""
+    post kernel at n = 16).  Timed as bench_mhc times config 2.  Where the shape
+    carries the rows' sums of squares along the chain (bench_mhc), the entry
+    is timed that way, and config 5 also without it (`_unchained`)."""
     out = {}
-    for key, n, C, M, sets in (("c5_n8_M8192", 8, C_DIM, 8192, 4), ("c4_n4_M64", 4, C_DIM, 64, 8),
-                               ("wide_n4_C2048_M16384", 4, 2048, TOKENS, 4),
-                               ("wide_n16_C768_M16384", 16, C_DIM, TOKENS, 4)):
-        r, _ = bench_mhc(steps, warmup, sets=sets, n=n, C=C, M=M, cold=False)
+    for key, n, C, M, sets, chain in (("c5_n8_M8192", 8, C_DIM, 8192, 4, True),
+                                      ("c5_n8_M8192_unchained", 8, C_DIM, 8192, 4, False),
+                                      ("c4_n4_M64", 4, C_DIM, 64, 8, True),
+                                      ("c4_n8_M64", 8, C_DIM, 64, 8, True),
+                                      ("wide_n4_C2048_M16384", 4, 2048, TOKENS, 4, True),
+                                      ("wide_n16_C768_M16384", 16, C_DIM, TOKENS, 4, True)):
+        r, _ = bench_mhc(steps, warmup, sets=sets, n=n, C=C, M=M, cold=False, chain=chain)
         pre_b, post_b = algorithmic_bytes(n, C, M)
         t = r["t_pre"] + r["t_post"]
-        out[key] = {"n": n, "C": C, "tokens": M,
+        out[key] = {"n": n, "C": C, "tokens": M, "ssq_chain": r["chain"],
                     "pre_ms": round(r["t_pre"], 5), "post_ms": round(r["t_post"], 5),
                     "pre_GBps": round(pre_b / (r["t_pre"] * 1e-3) / 1e9, 1),
                     "post_GBps": round(post_b / (r["t_post"] * 1e-3) / 1e9, 1),

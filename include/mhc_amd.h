@@ -128,6 +128,14 @@ int mhc_phi_pack_split(const void* phi, int phi_dtype, void* packed, int n, int 
  *   mixes_raw    [M, FD]    fp32                  (optional)
  *   sinkhorn_iters: reference count (1 softmax-row pass + iters column passes,
  *                   iters - 1 extra row passes); <= 1 behaves as 1.
+ *   x_ssq        [M, C / 128] fp32 or NULL: per-row partial sums of squares
+ *                of x as mhc_post_fwd / mhc_expand_norm_fwd write them
+ *                (out_ssq), row t's sum of squares = sum_j x_ssq[t][j] in j
+ *                order.  bf16 x with C % 128 == 0 only.  Used where the
+ *                kernel would otherwise read x once more to form the sums
+ *                (n = 8, n = 16, or C > 1024), ignored elsewhere; inv_rms
+ *                then comes from these sums (equal to rounding).  No
+ *                reference counterpart.
  */
 int mhc_pre_fwd(const void* x, int x_dtype, const void* phi, int phi_dtype, const void* phi_packed,
                 const void* alpha_pre, const void* bias_pre, const void* alpha_post,
@@ -135,7 +143,7 @@ int mhc_pre_fwd(const void* x, int x_dtype, const void* phi, int phi_dtype, cons
                 int param_dtype, void* sublayer_in, void* h_pre, void* h_post, void* h_res_raw,
                 void* h_res, float* inv_rms, float* mixes_raw, int64_t M, int n, int C,
                 float post_mult, float pre_eps, float rms_eps, int sinkhorn_iters,
-                float sinkhorn_eps, hipStream_t stream);
+                float sinkhorn_eps, const float* x_ssq, hipStream_t stream);
 
 /*
  * mHC pre phase without H_res (use_mhc = 2): FD = 2n, no Sinkhorn.
@@ -148,7 +156,7 @@ int mhc_pre_nohres_fwd(const void* x, int x_dtype, const void* phi, int phi_dtyp
                        const void* alpha_post, const void* bias_post, int param_dtype,
                        void* sublayer_in, void* h_pre, void* h_post, float* inv_rms,
                        float* mixes_raw, int64_t M, int n, int C, float post_mult, float pre_eps,
-                       float rms_eps, hipStream_t stream);
+                       float rms_eps, const float* x_ssq, hipStream_t stream);
 
 /*
  * Post phase: out[t,i,:] = sum_j h_res[t,i,j] * x[t,j,:] + h_post[t,i] * f_out[t,:].
@@ -156,10 +164,13 @@ int mhc_pre_nohres_fwd(const void* x, int x_dtype, const void* phi, int phi_dtyp
  *          (its kernel               model/mhc_fused.py:416-459).
  *   x [M, n*C] x_dtype; h_res [M, n, n] and h_post [M, n] h_dtype;
  *   f_out [M, C] f_dtype; out [M, n*C] x_dtype (must not alias x).
+ *   out_ssq [M, C / 128] fp32 or NULL: per-row partial sums of the squares
+ *   of out (as stored), for the next pre launch's x_ssq (bf16 x, gates and
+ *   F, C % 128 == 0, 16-byte aligned tensors; no reference counterpart).
  */
 int mhc_post_fwd(const void* x, int x_dtype, const void* h_res, const void* h_post, int h_dtype,
                  const void* f_out, int f_dtype, void* out, int64_t M, int n, int C,
-                 hipStream_t stream);
+                 float* out_ssq, hipStream_t stream);
 
 /*
  * Post phase without H_res: out = x + h_post (x) f_out.
@@ -168,7 +179,7 @@ int mhc_post_fwd(const void* x, int x_dtype, const void* h_res, const void* h_po
  */
 int mhc_post_nohres_fwd(const void* x, int x_dtype, const void* h_post, int h_dtype,
                         const void* f_out, int f_dtype, void* out, int64_t M, int n, int C,
-                        hipStream_t stream);
+                        float* out_ssq, hipStream_t stream);
 
 /*
  * MHCHead exit: out = sum_i (sigmoid(alpha * (x_norm @ phi)_i + bias_i) + pre_eps) * x_i,
@@ -177,12 +188,13 @@ int mhc_post_nohres_fwd(const void* x, int x_dtype, const void* h_post, int h_dt
  * Replaces _MHCHeadFn.forward     model/mhc_common.py:315-357
  *          (its kernel            model/mhc_common.py:128-195)
  *          and MHCHead.forward's n == 1 branch  model/mhc_common.py:438-442.
- *   out [M, C] x_dtype; inv_rms [M], mix_raw [M, n] fp32 optional.
+ *   out [M, C] x_dtype; inv_rms [M], mix_raw [M, n] fp32 optional;
+ *   x_ssq as mhc_pre_fwd.
  */
 int mhc_head_fwd(const void* x, int x_dtype, const void* phi, int phi_dtype,
                  const void* phi_packed, const void* alpha, const void* bias, int param_dtype,
                  void* out, float* inv_rms, float* mix_raw, int64_t M, int n, int C, float pre_eps,
-                 float rms_eps, hipStream_t stream);
+                 float rms_eps, const float* x_ssq, hipStream_t stream);
 
 /*
  * Batched Sinkhorn-Knopp of [batch, n, n] matrices, fp32 arithmetic, output
@@ -225,7 +237,8 @@ int mhc_pre_norm_fwd(const void* x, int x_dtype, const void* phi, int phi_dtype,
                      void* h_post, void* h_res_raw, void* h_res, float* inv_rms,
                      float* mixes_raw, int64_t M, int n, int C, float post_mult, float pre_eps,
                      float rms_eps, int sinkhorn_iters, float sinkhorn_eps,
-                     const void* norm_weight, int norm_dtype, float norm_eps, hipStream_t stream);
+                     const void* norm_weight, int norm_dtype, float norm_eps, const float* x_ssq,
+                     hipStream_t stream);
 
 /*
  * mhc_pre_nohres_fwd + the sublayer's input RMSNorm.
@@ -238,7 +251,7 @@ int mhc_pre_nohres_norm_fwd(const void* x, int x_dtype, const void* phi, int phi
                             void* sublayer_in_normed, void* h_pre, void* h_post, float* inv_rms,
                             float* mixes_raw, int64_t M, int n, int C, float post_mult,
                             float pre_eps, float rms_eps, const void* norm_weight, int norm_dtype,
-                            float norm_eps, hipStream_t stream);
+                            float norm_eps, const float* x_ssq, hipStream_t stream);
 
 /*
  * mhc_head_fwd + the model's final RMSNorm.
@@ -249,7 +262,7 @@ int mhc_head_norm_fwd(const void* x, int x_dtype, const void* phi, int phi_dtype
                       const void* phi_packed, const void* alpha, const void* bias, int param_dtype,
                       void* out_normed, float* inv_rms, float* mix_raw, int64_t M, int n, int C,
                       float pre_eps, float rms_eps, const void* norm_weight, int norm_dtype,
-                      float norm_eps, hipStream_t stream);
+                      float norm_eps, const float* x_ssq, hipStream_t stream);
 
 /*
  * The model's entry: RMSNorm over C with gain norm_weight, then n copies:
@@ -257,10 +270,13 @@ int mhc_head_norm_fwd(const void* x, int x_dtype, const void* phi, int phi_dtype
  * Replaces self.embed_up_norm = Sequential(RMSNorm, StreamExpand)
  *          model/model_minimind.py:365, applied at :385
  *          (StreamExpand.forward model/mhc_common.py:115-119).
- *   x [M, C] x_dtype; out [M, n*C] x_dtype.
+ *   x [M, C] x_dtype; out [M, n*C] x_dtype; out_ssq [M, C / 128] fp32 or
+ *   NULL: the written row's sum of squares in out_ssq[t][0], the other
+ *   partials zero (the next pre launch's x_ssq; bf16, C % 128 == 0).
  */
 int mhc_expand_norm_fwd(const void* x, int x_dtype, const void* norm_weight, int norm_dtype,
-                        void* out, int64_t M, int n, int C, float eps, hipStream_t stream);
+                        void* out, int64_t M, int n, int C, float eps, float* out_ssq,
+                        hipStream_t stream);
 
 /*
  * Batch size (tokens) at or below which the pre-phase entry points run the

@@ -60,6 +60,8 @@ int check_pre(const mhc::PreArgs& a, const char* fn) {
     return fail(hipErrorInvalidValue, "%s: alpha_res and bias_res are required", fn);
   if (a.norm_w && !dtype_ok(a.norm_dtype)) return fail(hipErrorInvalidValue, "%s: bad norm dtype %d", fn, a.norm_dtype);
   if (a.norm_w && !(a.norm_eps >= 0.f)) return fail(hipErrorInvalidValue, "%s: norm_eps must be >= 0", fn);
+  if (a.x_ssq && !mhc::ssq_supported(a.x_dtype, a.C))
+    return fail(hipErrorInvalidValue, "%s: x_ssq needs a bf16 stream with C %% %d == 0", fn, mhc::kSsqCols);
   return 0;
 }
 
@@ -71,6 +73,7 @@ int run_pre(mhc::PreArgs& a, hipStream_t stream, const char* fn) {
   const bool mfma = packed_ok && mhc::mfma_supported(a.x_dtype, a.phi_dtype, a.n, a.C, a.mode);
   const bool split = packed_ok && !a.norm_w && mhc::split_supported(a.x_dtype, a.phi_dtype, a.n, a.C, a.mode);
   if (!mfma && !split) a.phi_packed = nullptr;
+  if (!mfma || !mhc::ssq_used(a.n, a.C)) a.x_ssq = nullptr;
   if (split) return hip_status(mhc::launch_pre_split(a, mhc::device_cus(), stream), fn);
   return hip_status(mfma ? mhc::launch_pre_mfma(a, stream) : mhc::launch_pre_generic(a, stream), fn);
 }
@@ -166,7 +169,7 @@ int scratch_ptr(hipStream_t stream, void** out, const char* fn) {
 
 extern "C" {
 
-int mhc_abi_version(void) { return 6; }
+int mhc_abi_version(void) { return 7; }
 
 int mhc_init(void) {
   const char* fn = "mhc_init";
@@ -212,8 +215,9 @@ static int pre_full(const void* x, int x_dtype, const void* phi, int phi_dtype,
                     void* h_post, void* h_res_raw, void* h_res, float* inv_rms, float* mixes_raw,
                     int64_t M, int n, int C, float post_mult, float pre_eps, float rms_eps,
                     int sinkhorn_iters, float sinkhorn_eps, const void* norm_w, int norm_dtype,
-                    float norm_eps, hipStream_t stream, const char* fn) {
+                    float norm_eps, const float* x_ssq, hipStream_t stream, const char* fn) {
   mhc::PreArgs a{};
+  a.x_ssq = x_ssq;
   a.norm_w = norm_w;
   a.norm_dtype = norm_dtype;
   a.norm_eps = norm_eps;
@@ -254,11 +258,11 @@ int mhc_pre_fwd(const void* x, int x_dtype, const void* phi, int phi_dtype, cons
                 int param_dtype, void* sublayer_in, void* h_pre, void* h_post, void* h_res_raw,
                 void* h_res, float* inv_rms, float* mixes_raw, int64_t M, int n, int C,
                 float post_mult, float pre_eps, float rms_eps, int sinkhorn_iters,
-                float sinkhorn_eps, hipStream_t stream) {
+                float sinkhorn_eps, const float* x_ssq, hipStream_t stream) {
   return pre_full(x, x_dtype, phi, phi_dtype, phi_packed, alpha_pre, bias_pre, alpha_post,
                   bias_post, alpha_res, bias_res, param_dtype, sublayer_in, h_pre, h_post,
                   h_res_raw, h_res, inv_rms, mixes_raw, M, n, C, post_mult, pre_eps, rms_eps,
-                  sinkhorn_iters, sinkhorn_eps, nullptr, 0, 0.f, stream, "mhc_pre_fwd");
+                  sinkhorn_iters, sinkhorn_eps, nullptr, 0, 0.f, x_ssq, stream, "mhc_pre_fwd");
 }
 
 int mhc_pre_norm_fwd(const void* x, int x_dtype, const void* phi, int phi_dtype,
@@ -268,12 +272,13 @@ int mhc_pre_norm_fwd(const void* x, int x_dtype, const void* phi, int phi_dtype,
                      void* h_post, void* h_res_raw, void* h_res, float* inv_rms,
                      float* mixes_raw, int64_t M, int n, int C, float post_mult, float pre_eps,
                      float rms_eps, int sinkhorn_iters, float sinkhorn_eps,
-                     const void* norm_weight, int norm_dtype, float norm_eps, hipStream_t stream) {
+                     const void* norm_weight, int norm_dtype, float norm_eps,
+                     const float* x_ssq, hipStream_t stream) {
   if (!norm_weight && M != 0) return fail(hipErrorInvalidValue, "mhc_pre_norm_fwd: norm_weight is required");
   return pre_full(x, x_dtype, phi, phi_dtype, phi_packed, alpha_pre, bias_pre, alpha_post,
                   bias_post, alpha_res, bias_res, param_dtype, sublayer_in_normed, h_pre, h_post,
                   h_res_raw, h_res, inv_rms, mixes_raw, M, n, C, post_mult, pre_eps, rms_eps,
-                  sinkhorn_iters, sinkhorn_eps, norm_weight, norm_dtype, norm_eps, stream,
+                  sinkhorn_iters, sinkhorn_eps, norm_weight, norm_dtype, norm_eps, x_ssq, stream,
                   "mhc_pre_norm_fwd");
 }
 
@@ -283,8 +288,9 @@ static int pre_nohres(const void* x, int x_dtype, const void* phi, int phi_dtype
                       void* sublayer_in, void* h_pre, void* h_post, float* inv_rms,
                       float* mixes_raw, int64_t M, int n, int C, float post_mult, float pre_eps,
                       float rms_eps, const void* norm_w, int norm_dtype, float norm_eps,
-                      hipStream_t stream, const char* fn) {
+                      const float* x_ssq, hipStream_t stream, const char* fn) {
   mhc::PreArgs a{};
+  a.x_ssq = x_ssq;
   a.norm_w = norm_w;
   a.norm_dtype = norm_dtype;
   a.norm_eps = norm_eps;
@@ -318,10 +324,11 @@ int mhc_pre_nohres_fwd(const void* x, int x_dtype, const void* phi, int phi_dtyp
                        const void* alpha_post, const void* bias_post, int param_dtype,
                        void* sublayer_in, void* h_pre, void* h_post, float* inv_rms,
                        float* mixes_raw, int64_t M, int n, int C, float post_mult, float pre_eps,
-                       float rms_eps, hipStream_t stream) {
+                       float rms_eps, const float* x_ssq, hipStream_t stream) {
   return pre_nohres(x, x_dtype, phi, phi_dtype, phi_packed, alpha_pre, bias_pre, alpha_post,
                     bias_post, param_dtype, sublayer_in, h_pre, h_post, inv_rms, mixes_raw, M, n,
-                    C, post_mult, pre_eps, rms_eps, nullptr, 0, 0.f, stream, "mhc_pre_nohres_fwd");
+                    C, post_mult, pre_eps, rms_eps, nullptr, 0, 0.f, x_ssq, stream,
+                    "mhc_pre_nohres_fwd");
 }
 
 int mhc_pre_nohres_norm_fwd(const void* x, int x_dtype, const void* phi, int phi_dtype,
@@ -330,20 +337,21 @@ int mhc_pre_nohres_norm_fwd(const void* x, int x_dtype, const void* phi, int phi
                             void* sublayer_in_normed, void* h_pre, void* h_post, float* inv_rms,
                             float* mixes_raw, int64_t M, int n, int C, float post_mult,
                             float pre_eps, float rms_eps, const void* norm_weight, int norm_dtype,
-                            float norm_eps, hipStream_t stream) {
+                            float norm_eps, const float* x_ssq, hipStream_t stream) {
   if (!norm_weight && M != 0) return fail(hipErrorInvalidValue, "mhc_pre_nohres_norm_fwd: norm_weight is required");
   return pre_nohres(x, x_dtype, phi, phi_dtype, phi_packed, alpha_pre, bias_pre, alpha_post,
                     bias_post, param_dtype, sublayer_in_normed, h_pre, h_post, inv_rms, mixes_raw,
                     M, n, C, post_mult, pre_eps, rms_eps, norm_weight, norm_dtype, norm_eps,
-                    stream, "mhc_pre_nohres_norm_fwd");
+                    x_ssq, stream, "mhc_pre_nohres_norm_fwd");
 }
 
 static int head(const void* x, int x_dtype, const void* phi, int phi_dtype,
                 const void* phi_packed, const void* alpha, const void* bias, int param_dtype,
                 void* out, float* inv_rms, float* mix_raw, int64_t M, int n, int C, float pre_eps,
                 float rms_eps, const void* norm_w, int norm_dtype, float norm_eps,
-                hipStream_t stream, const char* fn) {
+                const float* x_ssq, hipStream_t stream, const char* fn) {
   mhc::PreArgs a{};
+  a.x_ssq = x_ssq;
   a.norm_w = norm_w;
   a.norm_dtype = norm_dtype;
   a.norm_eps = norm_eps;
@@ -370,20 +378,20 @@ static int head(const void* x, int x_dtype, const void* phi, int phi_dtype,
 int mhc_head_fwd(const void* x, int x_dtype, const void* phi, int phi_dtype,
                  const void* phi_packed, const void* alpha, const void* bias, int param_dtype,
                  void* out, float* inv_rms, float* mix_raw, int64_t M, int n, int C, float pre_eps,
-                 float rms_eps, hipStream_t stream) {
+                 float rms_eps, const float* x_ssq, hipStream_t stream) {
   return head(x, x_dtype, phi, phi_dtype, phi_packed, alpha, bias, param_dtype, out, inv_rms,
-              mix_raw, M, n, C, pre_eps, rms_eps, nullptr, 0, 0.f, stream, "mhc_head_fwd");
+              mix_raw, M, n, C, pre_eps, rms_eps, nullptr, 0, 0.f, x_ssq, stream, "mhc_head_fwd");
 }
 
 int mhc_head_norm_fwd(const void* x, int x_dtype, const void* phi, int phi_dtype,
                       const void* phi_packed, const void* alpha, const void* bias, int param_dtype,
                       void* out_normed, float* inv_rms, float* mix_raw, int64_t M, int n, int C,
                       float pre_eps, float rms_eps, const void* norm_weight, int norm_dtype,
-                      float norm_eps, hipStream_t stream) {
+                      float norm_eps, const float* x_ssq, hipStream_t stream) {
   if (!norm_weight && M != 0) return fail(hipErrorInvalidValue, "mhc_head_norm_fwd: norm_weight is required");
   return head(x, x_dtype, phi, phi_dtype, phi_packed, alpha, bias, param_dtype, out_normed,
               inv_rms, mix_raw, M, n, C, pre_eps, rms_eps, norm_weight, norm_dtype, norm_eps,
-              stream, "mhc_head_norm_fwd");
+              x_ssq, stream, "mhc_head_norm_fwd");
 }
 
 static int run_post(mhc::PostArgs& a, hipStream_t stream, const char* fn) {
@@ -396,21 +404,26 @@ static int run_post(mhc::PostArgs& a, hipStream_t stream, const char* fn) {
   if (a.M == 0) return 0;
   if (!a.x || !a.h_post || !a.f_out || !a.out) return fail(hipErrorInvalidValue, "%s: null pointer", fn);
   if (a.out == a.x) return fail(hipErrorInvalidValue, "%s: out must not alias x", fn);
-  return hip_status(mhc::launch_post(a, stream), fn);
+  if (a.out_ssq && !mhc::ssq_supported(a.x_dtype, a.C))
+    return fail(hipErrorInvalidValue, "%s: out_ssq needs a bf16 stream with C %% %d == 0", fn, mhc::kSsqCols);
+  const hipError_t e = mhc::launch_post(a, stream);
+  if (e == hipErrorInvalidValue && a.out_ssq)
+    return fail(e, "%s: out_ssq needs bf16 gates and F and 16-byte aligned tensors", fn);
+  return hip_status(e, fn);
 }
 
 int mhc_post_fwd(const void* x, int x_dtype, const void* h_res, const void* h_post, int h_dtype,
                  const void* f_out, int f_dtype, void* out, int64_t M, int n, int C,
-                 hipStream_t stream) {
+                 float* out_ssq, hipStream_t stream) {
   if (!h_res && M != 0) return fail(hipErrorInvalidValue, "mhc_post_fwd: h_res is required");
-  mhc::PostArgs a{x, h_res, h_post, f_out, out, M, n, C, x_dtype, h_dtype, f_dtype};
+  mhc::PostArgs a{x, h_res, h_post, f_out, out, out_ssq, M, n, C, x_dtype, h_dtype, f_dtype};
   return run_post(a, stream, "mhc_post_fwd");
 }
 
 int mhc_post_nohres_fwd(const void* x, int x_dtype, const void* h_post, int h_dtype,
                         const void* f_out, int f_dtype, void* out, int64_t M, int n, int C,
-                        hipStream_t stream) {
-  mhc::PostArgs a{x, nullptr, h_post, f_out, out, M, n, C, x_dtype, h_dtype, f_dtype};
+                        float* out_ssq, hipStream_t stream) {
+  mhc::PostArgs a{x, nullptr, h_post, f_out, out, out_ssq, M, n, C, x_dtype, h_dtype, f_dtype};
   return run_post(a, stream, "mhc_post_nohres_fwd");
 }
 
@@ -440,7 +453,8 @@ int mhc_stream_expand_fwd(const void* x, void* out, int elem_bytes, int64_t M, i
 }
 
 int mhc_expand_norm_fwd(const void* x, int x_dtype, const void* norm_weight, int norm_dtype,
-                        void* out, int64_t M, int n, int C, float eps, hipStream_t stream) {
+                        void* out, int64_t M, int n, int C, float eps, float* out_ssq,
+                        hipStream_t stream) {
   const char* fn = "mhc_expand_norm_fwd";
   if (M < 0 || n < 1 || n > kMaxN || C < 1) return fail(hipErrorInvalidValue, "%s: bad shape (M=%lld n=%d C=%d)", fn, (long long)M, n, C);
   if (!dtype_ok(x_dtype) || !dtype_ok(norm_dtype)) return fail(hipErrorInvalidValue, "%s: bad dtype", fn);
@@ -448,8 +462,12 @@ int mhc_expand_norm_fwd(const void* x, int x_dtype, const void* norm_weight, int
   if (M > kMaxBlocks) return fail(hipErrorInvalidValue, "%s: M too large", fn);
   if (M == 0) return 0;
   if (!x || !norm_weight || !out) return fail(hipErrorInvalidValue, "%s: null pointer", fn);
-  return hip_status(mhc::launch_expand_norm(x, x_dtype, norm_weight, norm_dtype, out, M, n, C, eps,
-                                            stream), fn);
+  if (out_ssq && !mhc::ssq_supported(x_dtype, C))
+    return fail(hipErrorInvalidValue, "%s: out_ssq needs a bf16 stream with C %% %d == 0", fn, mhc::kSsqCols);
+  const hipError_t e = mhc::launch_expand_norm(x, x_dtype, norm_weight, norm_dtype, out, M, n, C,
+                                               eps, stream, out_ssq);
+  if (e == hipErrorInvalidValue && out_ssq) return fail(e, "%s: out_ssq needs 16-byte aligned rows", fn);
+  return hip_status(e, fn);
 }
 
 int64_t mhc_pre_token_threshold(int64_t max_tokens) {

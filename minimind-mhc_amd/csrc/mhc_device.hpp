@@ -313,6 +313,13 @@ __device__ __forceinline__ float xor_lane32(float v) {
   return __builtin_bit_cast(float, upper ? r[0] : r[1]);
 }
 
+// Sum over the 16 lanes of a DPP row (both halves, then the mirror): every
+// lane of the row ends with the bit-identical total.
+__device__ __forceinline__ float row16_sum(float v) {
+  v = row_reduce<8, OpAdd>(v);
+  return v + dpp_f<kDppRowMirror>(v);
+}
+
 // Sum over all 64 lanes of the wave; every lane ends with the bit-identical
 // total (each step adds a value and its partner's, a commutative pair).
 __device__ __forceinline__ float wave_sum(float v) {

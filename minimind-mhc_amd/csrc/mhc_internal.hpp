@@ -46,6 +46,12 @@ struct PreArgs {
   float post_mult, pre_eps, rms_eps;
   int sk_iters;
   float sk_eps;
+  // Partial sums of squares of each x row from the kernel that wrote x
+  // (mhc_post_fwd / mhc_expand_norm_fwd): [M, C / kSsqCols] fp32, row t's
+  // sum of squares = sum_j x_ssq[t][j] in j order.  Optional; the kernels that
+  // would otherwise need a pass over x of their own to form it (the
+  // K-streamed kernel and the n = 8 group kernel) use it, the others ignore it.
+  const float* x_ssq;
   // RMSNorm over C applied to the main output before it is stored (the
   // sublayer's input norm, or the model's final norm after MHCHead):
   //   out = bf16(s * (1 / sqrt(mean_c(s^2) + norm_eps)) * norm_w),  s the
@@ -61,6 +67,7 @@ struct PostArgs {
   const void* h_post;  // [M, n]
   const void* f_out;   // [M, C]
   void* out;           // [M, n*C]
+  float* out_ssq;      // [M, C / kSsqCols] partial sums of squares of out, or null
   int64_t M;
   int n, C;
   int x_dtype, h_dtype, f_dtype;
@@ -151,7 +158,8 @@ bool pre_row_staging();
 void set_pre_row_staging(bool on);
 // RMSNorm of each C row followed by n copies (StreamExpand): out[t, i*C + c].
 hipError_t launch_expand_norm(const void* x, int x_dtype, const void* w, int w_dtype, void* out,
-                              int64_t M, int n, int C, float eps, hipStream_t s);
+                              int64_t M, int n, int C, float eps, hipStream_t s,
+                              float* out_ssq = nullptr);
 hipError_t launch_post(const PostArgs& a, hipStream_t s);
 hipError_t launch_post_bwd(const PostBwdArgs& a, hipStream_t s);
 hipError_t launch_pre_bwd(const PreBwdArgs& a, hipStream_t s);
@@ -176,6 +184,20 @@ hipError_t launch_stream_expand(const void* x, void* out, int elem_bytes, int64_
                                 int C, hipStream_t s);
 hipError_t launch_phi_pack(const void* phi, int phi_dtype, void* packed, int n, int C, int mode,
                            hipStream_t s);
+
+// Per-row sums of squares handed from the kernel that writes a stream to the
+// pre kernel that reads it: one fp32 partial per kSsqCols columns of C (for
+// every stream together), bf16 streams with C % kSsqCols == 0 only.
+constexpr int kSsqCols = 128;
+__host__ __device__ inline bool ssq_supported(int x_dtype, int C) {
+  return x_dtype == kBF16 && C > 0 && C % kSsqCols == 0;
+}
+// Whether a pre launch of this shape uses x_ssq (the kernels that would read x
+// once more to form the sums themselves): n = 8 and n = 16 at any C, n <= 4
+// past C = 1024.
+__host__ __device__ inline bool ssq_used(int n, int C) {
+  return n == 8 || n == 16 || (n >= 2 && C > 1024);
+}
 
 // MFMA pre-phase geometry: 16-token tiles, c-blocks of 32 columns.
 constexpr int kTokTile = 16;

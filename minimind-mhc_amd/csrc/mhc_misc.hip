@@ -148,10 +148,14 @@ __device__ __forceinline__ uint32_t pack16(float a, float b, int dt) {
 }
 
 // 16-bit streams, C % 8 == 0, 16-byte aligned rows: 8 elements per lane step.
+// out_ssq (optional, bf16, C % 128 == 0): the sum of the squares of the
+// written row (n times that of one normed copy) in out_ssq[token][0], the
+// token's other C / 128 - 1 partials zero (see PreArgs::x_ssq).
 __global__ __launch_bounds__(256) void expand_norm_vec_kernel(const U32x4* x, int xdt,
                                                               const void* __restrict__ w, int wdt,
                                                               U32x4* out, int64_t M,
-                                                              int n, int C, float eps) {
+                                                              int n, int C, float eps,
+                                                              float* __restrict__ out_ssq) {
   const int64_t tok = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
   if (tok >= M) return;  // whole waves
   const int lane = threadIdx.x & 63;
@@ -171,6 +175,7 @@ __global__ __launch_bounds__(256) void expand_norm_vec_kernel(const U32x4* x, in
   ss = wave_sum(ss);
   const float r = 1.0f / sqrtf(ss / (float)C + eps);
   U32x4* orow = out + tok * n * C8;
+  float q = 0.f;
   for (int ch = lane; ch < C8; ch += 64) {
     const U32x4 v = xr[ch];
     U32x4 y;
@@ -181,6 +186,15 @@ __global__ __launch_bounds__(256) void expand_norm_vec_kernel(const U32x4* x, in
                       hi16(v.v[j], xdt) * r * ld_any(w, c + 1, wdt), xdt);
     }
     for (int i = 0; i < n; ++i) orow[(int64_t)i * C8 + ch] = y;
+    if (out_ssq) {  // uniform
+#pragma unroll
+      for (int j = 0; j < 4; ++j) q = dot2_bf16(y.v[j], y.v[j], q);
+    }
+  }
+  if (out_ssq) {  // uniform
+    q = wave_sum(q) * (float)n;
+    const int P = C / kSsqCols;
+    for (int j = lane; j < P; j += 64) out_ssq[tok * P + j] = j == 0 ? q : 0.f;
   }
 }
 
@@ -207,16 +221,19 @@ __global__ __launch_bounds__(256) void expand_norm_kernel(const void* x, int xdt
 }
 
 hipError_t launch_expand_norm(const void* x, int x_dtype, const void* w, int w_dtype, void* out,
-                              int64_t M, int n, int C, float eps, hipStream_t s) {
+                              int64_t M, int n, int C, float eps, hipStream_t s, float* out_ssq) {
   const unsigned blocks = (unsigned)((M + 3) / 4);
   const uintptr_t align = reinterpret_cast<uintptr_t>(x) | reinterpret_cast<uintptr_t>(out);
-  if (x_dtype != kF32 && C % 8 == 0 && align % 16 == 0)
+  if (x_dtype != kF32 && C % 8 == 0 && align % 16 == 0) {
+    if (out_ssq && !ssq_supported(x_dtype, C)) return hipErrorInvalidValue;
     hipLaunchKernelGGL(expand_norm_vec_kernel, dim3(blocks), dim3(256), 0, s,
                        static_cast<const U32x4*>(x), x_dtype, w, w_dtype, static_cast<U32x4*>(out),
-                       M, n, C, eps);
-  else
+                       M, n, C, eps, out_ssq);
+  } else {
+    if (out_ssq) return hipErrorInvalidValue;  // sums of squares: the vector kernel only
     hipLaunchKernelGGL(expand_norm_kernel, dim3(blocks), dim3(256), 0, s, x, x_dtype, w, w_dtype,
                        out, M, n, C, eps);
+  }
   return hipGetLastError();
 }
 

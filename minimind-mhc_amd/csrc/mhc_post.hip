@@ -84,9 +84,15 @@ __device__ __forceinline__ float rnd(float v) {
 // the einsum result, the H_post * F product and their sum are each a tensor of
 // the stream dtype.  x reads and out writes are non-temporal (each byte once per
 // launch); F keeps the default policy (measured slower non-temporal).
-template <typename XT, typename FT, int N, bool RES>
+// SSQ (bf16 streams, C % 128 == 0): each DPP row of 16 threads covers 128
+// columns of one token (C / 8 threads a token, a multiple of 16, rows aligned
+// to tokens); its sum of the squares of the stored outputs over every stream
+// goes to out_ssq[token][column / 128], the sums of squares the next pre
+// launch would otherwise form with a pass over the row of its own.
+template <typename XT, typename FT, int N, bool RES, bool SSQ>
 __global__ __launch_bounds__(256) void post_vec_kernel(PostArgs a) {
   constexpr int V = 16 / sizeof(XT);
+  static_assert(!SSQ || V == 8, "sums of squares for 16-bit streams");
   const int C = a.C;
   const int CV = C / V;
   const int64_t gid = (int64_t)blockIdx.x * 256 + threadIdx.x;
@@ -107,6 +113,7 @@ __global__ __launch_bounds__(256) void post_vec_kernel(PostArgs a) {
   float hr[RES ? N * N : 1];
   if constexpr (RES) load_pack<XT, N * N>(static_cast<const XT*>(a.h_res) + tok * N * N, hr);
 
+  float q = 0.f;
 #pragma unroll
   for (int i = 0; i < N; ++i) {
     float o[V];
@@ -122,8 +129,17 @@ __global__ __launch_bounds__(256) void post_vec_kernel(PostArgs a) {
         acc = xv[i][v];
       }
       o[v] = __fadd_rn(acc, rnd<XT>(__fmul_rn(hp[i], fv[v])));
+      if constexpr (SSQ) {
+        const float st = rnd<XT>(o[v]);
+        q = fmaf(st, st, q);
+      }
     }
     store_pack_nt<XT, V>(out + (int64_t)i * C, o);
+  }
+  if constexpr (SSQ) {
+    q = row16_sum(q);
+    const int ch = (int)(gid - tok * CV);
+    if ((ch & 15) == 0) a.out_ssq[tok * (CV / 16) + (ch >> 4)] = q;
   }
 }
 
@@ -139,7 +155,9 @@ __global__ __launch_bounds__(256) void post_vec_kernel(PostArgs a) {
 // post_vec_kernel.
 typedef unsigned int u32x2_t __attribute__((ext_vector_type(2)));
 
-template <bool RES>
+// SSQ: the wave's sum of the squares of the token's stored outputs goes to
+// out_ssq[token][0], the token's other C / 128 - 1 partials are zero.
+template <bool RES, bool SSQ>
 __global__ __launch_bounds__(256) void post_n16_kernel(PostArgs a) {
   constexpr int N = 16;
   constexpr int NP = N / 2;
@@ -163,6 +181,7 @@ __global__ __launch_bounds__(256) void post_n16_kernel(PostArgs a) {
     hp[2 * p] = bf16lo(w);
     hp[2 * p + 1] = bf16hi(w);
   }
+  float q = 0.f;
   for (int cv = lane; cv < C4; cv += 64) {
     const int c = cv * 4;
     u32x2_t xv[N];
@@ -207,7 +226,19 @@ __global__ __launch_bounds__(256) void post_n16_kernel(PostArgs a) {
       for (int k = 0; k < 4; ++k) o[k] = __fadd_rn(r[k], rnd<__bf16>(__fmul_rn(hp[i], fl[k])));
       const u32x2_t ov = {pack_bf16x2(o[0], o[1]), pack_bf16x2(o[2], o[3])};
       __builtin_nontemporal_store(ov, reinterpret_cast<u32x2_t*>(out + (int64_t)i * C + c));
+      if constexpr (SSQ) {
+#pragma unroll
+        for (int k = 0; k < 4; ++k) {
+          const float st = rnd<__bf16>(o[k]);
+          q = fmaf(st, st, q);
+        }
+      }
     }
+  }
+  if constexpr (SSQ) {
+    q = wave_sum(q);
+    const int P = C / kSsqCols;
+    for (int j = lane; j < P; j += 64) a.out_ssq[tok * P + j] = j == 0 ? q : 0.f;
   }
 }
 
@@ -218,7 +249,8 @@ __global__ __launch_bounds__(256) void post_n16_kernel(PostArgs a) {
 // (x[2p][c], x[2p+1][c]) by v_perm and each res-mix output is four
 // v_dot2_f32_bf16 against H_res row i's adjacent pairs, as post_n16_kernel
 // does (the fp32 sum runs pairwise rather than in post_vec_kernel's order).
-template <bool RES>
+// SSQ as post_vec_kernel.
+template <bool RES, bool SSQ>
 __global__ __launch_bounds__(256) void post_n8_kernel(PostArgs a) {
   constexpr int N = 8;
   constexpr int NP = N / 2;
@@ -257,6 +289,7 @@ __global__ __launch_bounds__(256) void post_n8_kernel(PostArgs a) {
         xp[p][2 * e + 1] = __builtin_amdgcn_perm(xv[2 * p + 1][e], xv[2 * p][e], 0x07060302u);
       }
   }
+  float q = 0.f;
 #pragma unroll
   for (int i = 0; i < N; ++i) {
     const float hp = (i & 1) ? bf16hi(hpv[i >> 1]) : bf16lo(hpv[i >> 1]);
@@ -273,11 +306,20 @@ __global__ __launch_bounds__(256) void post_n8_kernel(PostArgs a) {
         r = (k & 1) ? bf16hi(xv[i][k >> 1]) : bf16lo(xv[i][k >> 1]);
       }
       o[k] = __fadd_rn(r, rnd<__bf16>(__fmul_rn(hp, fl[k])));
+      if constexpr (SSQ) {
+        const float st = rnd<__bf16>(o[k]);
+        q = fmaf(st, st, q);
+      }
     }
     u32x4_t ov;
 #pragma unroll
     for (int e = 0; e < 4; ++e) ov[e] = pack_bf16x2(o[2 * e], o[2 * e + 1]);
     __builtin_nontemporal_store(ov, reinterpret_cast<u32x4_t*>(out + (int64_t)i * C));
+  }
+  if constexpr (SSQ) {
+    q = row16_sum(q);
+    const int ch = (int)(gid - tok * CV);
+    if ((ch & 15) == 0) a.out_ssq[tok * (CV / 16) + (ch >> 4)] = q;
   }
 }
 
@@ -313,11 +355,21 @@ template <typename XT, typename FT, int N>
 static hipError_t launch_vec(const PostArgs& a, hipStream_t s) {
   constexpr int V = 16 / sizeof(XT);
   const int64_t threads = a.M * (a.C / V);
-  const int64_t blocks = (threads + 255) / 256;
+  const dim3 grid((unsigned)((threads + 255) / 256));
+  if constexpr (V == 8 && N <= 4) {
+    if (a.out_ssq) {
+      if (a.h_res)
+        hipLaunchKernelGGL((post_vec_kernel<XT, FT, N, true, true>), grid, dim3(256), 0, s, a);
+      else
+        hipLaunchKernelGGL((post_vec_kernel<XT, FT, N, false, true>), grid, dim3(256), 0, s, a);
+      return hipGetLastError();
+    }
+  }
+  if (a.out_ssq) return hipErrorInvalidValue;  // no sums-of-squares form of this kernel
   if (a.h_res)
-    hipLaunchKernelGGL((post_vec_kernel<XT, FT, N, true>), dim3((unsigned)blocks), dim3(256), 0, s, a);
+    hipLaunchKernelGGL((post_vec_kernel<XT, FT, N, true, false>), grid, dim3(256), 0, s, a);
   else
-    hipLaunchKernelGGL((post_vec_kernel<XT, FT, N, false>), dim3((unsigned)blocks), dim3(256), 0, s, a);
+    hipLaunchKernelGGL((post_vec_kernel<XT, FT, N, false, false>), grid, dim3(256), 0, s, a);
   return hipGetLastError();
 }
 
@@ -342,21 +394,35 @@ hipError_t launch_post(const PostArgs& a, hipStream_t s) {
       ((reinterpret_cast<uintptr_t>(a.x) | reinterpret_cast<uintptr_t>(a.out) |
         reinterpret_cast<uintptr_t>(a.f_out)) & 7) == 0 &&
       ((reinterpret_cast<uintptr_t>(a.h_post) | reinterpret_cast<uintptr_t>(a.h_res)) & 3) == 0) {
-    const int64_t blocks = (a.M + 3) / 4;
-    if (a.h_res)
-      hipLaunchKernelGGL(post_n16_kernel<true>, dim3((unsigned)blocks), dim3(256), 0, s, a);
-    else
-      hipLaunchKernelGGL(post_n16_kernel<false>, dim3((unsigned)blocks), dim3(256), 0, s, a);
+    const dim3 grid((unsigned)((a.M + 3) / 4));
+    if (a.out_ssq) {
+      if (a.h_res)
+        hipLaunchKernelGGL((post_n16_kernel<true, true>), grid, dim3(256), 0, s, a);
+      else
+        hipLaunchKernelGGL((post_n16_kernel<false, true>), grid, dim3(256), 0, s, a);
+    } else {
+      if (a.h_res)
+        hipLaunchKernelGGL((post_n16_kernel<true, false>), grid, dim3(256), 0, s, a);
+      else
+        hipLaunchKernelGGL((post_n16_kernel<false, false>), grid, dim3(256), 0, s, a);
+    }
     return hipGetLastError();
   }
   if (a.n == 8 && a.x_dtype == kBF16 && a.h_dtype == kBF16 && a.f_dtype == kBF16 && a.C % 8 == 0 &&
       aligned16(a.x) && aligned16(a.out) && aligned16(a.f_out) && aligned16(a.h_post) &&
       (!a.h_res || aligned16(a.h_res))) {
-    const int64_t blocks = (a.M * (a.C / 8) + 255) / 256;
-    if (a.h_res)
-      hipLaunchKernelGGL(post_n8_kernel<true>, dim3((unsigned)blocks), dim3(256), 0, s, a);
-    else
-      hipLaunchKernelGGL(post_n8_kernel<false>, dim3((unsigned)blocks), dim3(256), 0, s, a);
+    const dim3 grid((unsigned)((a.M * (a.C / 8) + 255) / 256));
+    if (a.out_ssq) {
+      if (a.h_res)
+        hipLaunchKernelGGL((post_n8_kernel<true, true>), grid, dim3(256), 0, s, a);
+      else
+        hipLaunchKernelGGL((post_n8_kernel<false, true>), grid, dim3(256), 0, s, a);
+    } else {
+      if (a.h_res)
+        hipLaunchKernelGGL((post_n8_kernel<true, false>), grid, dim3(256), 0, s, a);
+      else
+        hipLaunchKernelGGL((post_n8_kernel<false, false>), grid, dim3(256), 0, s, a);
+    }
     return hipGetLastError();
   }
   const bool pow2n = a.n == 1 || a.n == 2 || a.n == 4 || a.n == 8;
@@ -372,6 +438,7 @@ hipError_t launch_post(const PostArgs& a, hipStream_t s) {
     if (a.x_dtype == kF32 && a.f_dtype == kBF16) return launch_vec_n<float, __bf16>(a, s);
     if (a.x_dtype == kF16 && a.f_dtype == kF16) return launch_vec_n<_Float16, _Float16>(a, s);
   }
+  if (a.out_ssq) return hipErrorInvalidValue;  // sums of squares: bf16 vector kernels only
   const int64_t total = a.M * a.n * (int64_t)a.C;
   const int64_t blocks = (total + 255) / 256;
   hipLaunchKernelGGL(post_generic_kernel, dim3((unsigned)blocks), dim3(256), 0, s, a);

@@ -107,6 +107,16 @@ __global__ __launch_bounds__(kGrpWaves * 64) void pre_group_kernel(PreArgs a, in
   const int rot = P::KS_ORDER ? (int)((t0 / kKsTileTokens) % NJ) : 0;
 
   const RawParam rp = load_gate_param<N, MODE>(a, tid);
+  // Sums of squares handed over by the kernel that wrote x, used where the
+  // large-batch kernel uses them (n = 8: pre_kstream_kernel), summed in the
+  // same order, so the two stay bit-identical.
+  const bool given = P::KS_ORDER && a.x_ssq != nullptr;  // uniform
+  float ss_given = 0.f;
+  if (given && tid < G && tid < valid) {
+    const int PS = C / kSsqCols;
+    const float* src = a.x_ssq + (t0 + tid) * PS;
+    for (int j = 0; j < PS; ++j) ss_given += src[j];
+  }
   float gain[2] = {0.f, 0.f};  // norm gain of columns tid and tid + T (branch-free loads)
   if constexpr (NORM) {
 #pragma unroll
@@ -201,7 +211,10 @@ __global__ __launch_bounds__(kGrpWaves * 64) void pre_group_kernel(PreArgs a, in
   // The projection runs on x_norm = bf16(x * inv_rms), rounded as the
   // reference rounds it (model/mhc_fused.py:845), so the sums of squares come
   // first (in the large-batch kernel's order), then a barrier, then the MFMAs.
-  if (row_ss) {  // uniform
+  if (given) {  // uniform: the totals in slot 0, the other waves' slots zero
+    if (tid < G) sh.ss[0][tid] = ss_given;
+    else if (tid < kGrpWaves * 16 && tid % 16 < G && tid >= 16) sh.ss[tid / 16][tid % 16] = 0.f;
+  } else if (row_ss) {  // uniform
     // The row-staged persistent kernel's order (persist_row_sumsq): lane l
     // chains the row's chunks at bytes 16 l + 1024 k (the row is a whole
     // number of 1 KiB pieces) in k order, then the wave butterfly.  The total

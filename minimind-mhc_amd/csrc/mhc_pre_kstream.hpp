@@ -13,7 +13,9 @@
 //     tiles (KS = 4), so a wave's operands and accumulators stay in registers;
 //   * a first pass over the wave's chunks forms each row's sum of squares
 //     (bf16 dot2), so the projection can run on x_norm = bf16(x * inv_rms),
-//     rounded as the PyTorch path rounds it (model/mhc_fused.py:845);
+//     rounded as the PyTorch path rounds it (model/mhc_fused.py:845).  When
+//     the kernel that wrote x handed its rows' sums over (PreArgs::x_ssq),
+//     the pass is skipped and x is read twice, not three times;
 //   * the K loop keeps D chunks in flight per wave: each chunk is MB 16-byte x
 //     loads (16 tokens x 32 columns per M-block, the MFMA A operands) and NTW
 //     16-byte phi loads (the packed B operands, 16 output columns each);
@@ -35,8 +37,8 @@
 //     pass scales, rounds and stores them.  Wider rows take a second launch
 //     (the RMSNorm in place on the written sublayer input).
 // Arithmetic and rounding points as pre_persist_kernel.  The tile's x is read
-// three times (sums of squares, K loop, pre-aggregate), the second and third
-// mostly from the Infinity Cache.
+// three times (sums of squares, K loop, pre-aggregate; twice with x_ssq), the
+// later reads mostly from the Infinity Cache.
 //
 // Reference semantics: model/mhc_fused.py:163-268, :533-559, :47-56;
 // model/mhc_fused_no_hres.py:48-145; model/mhc_common.py:128-195.
@@ -183,6 +185,16 @@ __global__ __launch_bounds__(kKsWaves * 64) void pre_kstream_kernel(PreArgs a) {
   const int valid = (int)(M - t0 < TM ? M - t0 : TM);
 
   const RawParam rp = load_gate_param<N, MODE>(a, tid);
+  // Sums of squares handed over by the kernel that wrote x (see PreArgs::
+  // x_ssq): thread tt < TM sums row tt's partials in order.  Loaded before
+  // the K loop's first chunks, so no wait on them.
+  const bool given = a.x_ssq != nullptr;  // uniform
+  float ss_given = 0.f;
+  if (given && tid < TM && tid < valid) {
+    const int P = C / kSsqCols;
+    const float* src = a.x_ssq + (t0 + tid) * P;
+    for (int j = 0; j < P; ++j) ss_given += src[j];
+  }
   float gain[2] = {0.f, 0.f};  // norm gain of columns tid and tid + 512 (branch-free loads)
   if constexpr (NORM) {
 #pragma unroll
@@ -252,7 +264,10 @@ __global__ __launch_bounds__(kKsWaves * 64) void pre_kstream_kernel(PreArgs a) {
     float ss[P::MB];
 #pragma unroll
     for (int m = 0; m < P::MB; ++m) ss[m] = 0.f;
-    if (P::NH == 1 || nh == 0) {  // uniform
+    if (given) {  // uniform: the totals in slot 0, the other K-split slots zero
+      if (tid < TM) sh.ss[0][tid] = ss_given;
+      else if (tid < P::KS * TM) sh.ss[tid / TM][tid % TM] = 0.f;
+    } else if (P::NH == 1 || nh == 0) {  // uniform
       for (int j0 = 0; j0 < NJ; j0 += P::SD) {  // uniform trip count
         U32x4 v[P::SD][P::MB];
 #pragma unroll
@@ -493,11 +508,6 @@ __global__ __launch_bounds__(kKsWaves * 64) void pre_kstream_kernel(PreArgs a) {
     }
   }
 }
-
-// The RMSNorm over C in place on the written sublayer input (rows wider than
-// the fused epilogue's LDS holds); mhc_misc.hip.
-hipError_t launch_expand_norm(const void* x, int x_dtype, const void* w, int w_dtype, void* out,
-                              int64_t M, int n, int C, float eps, hipStream_t s);
 
 template <int N, int MODE>
 hipError_t launch_pre_kstream_inst(const PreArgs& a, hipStream_t s) {

@@ -39,27 +39,29 @@ _SIGNATURES = {
     "mhc_pre_fwd": (_I, [_P, _I, _P, _I, _P,              # x, x_dt, phi, phi_dt, packed
                          _P, _P, _P, _P, _P, _P, _I,      # alphas/biases, param_dt
                          _P, _P, _P, _P, _P, _P, _P,      # sub_in, h_pre, h_post, raw, h_res, inv, mixes
-                         _I64, _I, _I, _F, _F, _F, _I, _F, _P]),
+                         _I64, _I, _I, _F, _F, _F, _I, _F,
+                         _P, _P]),                        # x_ssq, stream
     "mhc_pre_nohres_fwd": (_I, [_P, _I, _P, _I, _P,
                                 _P, _P, _P, _P, _I,
                                 _P, _P, _P, _P, _P,
-                                _I64, _I, _I, _F, _F, _F, _P]),
-    "mhc_post_fwd": (_I, [_P, _I, _P, _P, _I, _P, _I, _P, _I64, _I, _I, _P]),
-    "mhc_post_nohres_fwd": (_I, [_P, _I, _P, _I, _P, _I, _P, _I64, _I, _I, _P]),
-    "mhc_head_fwd": (_I, [_P, _I, _P, _I, _P, _P, _P, _I, _P, _P, _P, _I64, _I, _I, _F, _F, _P]),
+                                _I64, _I, _I, _F, _F, _F, _P, _P]),
+    "mhc_post_fwd": (_I, [_P, _I, _P, _P, _I, _P, _I, _P, _I64, _I, _I, _P, _P]),
+    "mhc_post_nohres_fwd": (_I, [_P, _I, _P, _I, _P, _I, _P, _I64, _I, _I, _P, _P]),
+    "mhc_head_fwd": (_I, [_P, _I, _P, _I, _P, _P, _P, _I, _P, _P, _P, _I64, _I, _I, _F, _F,
+                          _P, _P]),
     "mhc_pre_norm_fwd": (_I, [_P, _I, _P, _I, _P,
                               _P, _P, _P, _P, _P, _P, _I,
                               _P, _P, _P, _P, _P, _P, _P,
                               _I64, _I, _I, _F, _F, _F, _I, _F,
-                              _P, _I, _F, _P]),                # norm weight, dtype, eps, stream
+                              _P, _I, _F, _P, _P]),            # norm weight, dtype, eps, x_ssq, stream
     "mhc_pre_nohres_norm_fwd": (_I, [_P, _I, _P, _I, _P,
                                      _P, _P, _P, _P, _I,
                                      _P, _P, _P, _P, _P,
                                      _I64, _I, _I, _F, _F, _F,
-                                     _P, _I, _F, _P]),
+                                     _P, _I, _F, _P, _P]),
     "mhc_head_norm_fwd": (_I, [_P, _I, _P, _I, _P, _P, _P, _I, _P, _P, _P, _I64, _I, _I, _F, _F,
-                               _P, _I, _F, _P]),
-    "mhc_expand_norm_fwd": (_I, [_P, _I, _P, _I, _P, _I64, _I, _I, _F, _P]),
+                               _P, _I, _F, _P, _P]),
+    "mhc_expand_norm_fwd": (_I, [_P, _I, _P, _I, _P, _I64, _I, _I, _F, _P, _P]),
     "mhc_pre_token_threshold": (_I64, [_I64]),
     "mhc_pre_row_staging": (_I, [_I]),
     "mhc_sinkhorn_fwd": (_I, [_P, _P, _I, _I64, _I, _I, _F, _P]),
@@ -88,7 +90,7 @@ _SIGNATURES = {
     "mhc_sinkhorn_bwd_max_iters": (_I, [_I]),
 }
 
-ABI_VERSION = 6
+ABI_VERSION = 7
 _lib: Optional[ctypes.CDLL] = None
 
 

@@ -147,6 +147,66 @@ def packed_phi(phi: torch.Tensor, n: int, C: int, mode: int,
     return ent[1].get(phi, n, C, training)
 
 
+# ---------------------------------------------- sums of squares along a chain
+SSQ_COLS = 128  # one fp32 partial per 128 columns of C (kSsqCols)
+
+
+def ssq_wanted(dtype: torch.dtype, n: int, C: int) -> bool:
+    """Whether a stream of this shape carries its rows' sums of squares from the
+    launch that writes it to the pre launch that reads it: bf16, C a multiple
+    of 128, and a pre kernel that would otherwise read the stream once more
+    to form them (n = 8, n = 16, or C > 1024)."""
+    return (dtype == torch.bfloat16 and C % SSQ_COLS == 0
+            and (n in (8, 16) or (n >= 2 and C > 1024)))
+
+
+class StreamChain:
+    """Carries per-row sums of squares along a chain of mHC calls.
+
+    The launch that writes a stream (the post phase, or the entry RMSNorm +
+    StreamExpand) also writes its rows' partial sums of squares
+    ([M, C / 128] fp32); the next pre launch that reads that exact tensor
+    takes them instead of a pass over x of its own.  A caller that hands
+    each call's output unchanged to the next call (as the MiniMind blocks do)
+    creates one chain per forward and passes it to every mHC call; the sums
+    are used only when the next call's input is the very tensor object the
+    previous call returned.  Writing into that tensor in place between the
+    calls is the caller's to avoid (the chain cannot see it).
+    No reference counterpart."""
+
+    __slots__ = ("src", "ssq")
+
+    def __init__(self):
+        self.src = None
+        self.ssq = None
+
+    def take(self, x: torch.Tensor, n: int, C: int) -> Optional[torch.Tensor]:
+        """The sums of squares of x's rows, or None when x is not the tensor the
+        chain last recorded (or the shape carries none)."""
+        if self.ssq is None or self.src is not x:
+            return None
+        M = x.numel() // (n * C) if n * C else 0
+        if tuple(self.ssq.shape) != (M, C // SSQ_COLS) or self.ssq.device != x.device:
+            return None
+        return self.ssq
+
+    def buffer(self, like: torch.Tensor, n: int, C: int,
+               rows: Optional[int] = None) -> Optional[torch.Tensor]:
+        """A buffer for the sums of squares of an n-stream of `rows` tokens
+        (default: `like` is such a stream, [..., n*C]) with like's dtype and
+        device, or None when that shape carries none."""
+        if not like.is_cuda or not ssq_wanted(like.dtype, n, C):
+            return None
+        M = like.numel() // (n * C) if rows is None else rows
+        return torch.empty(M, C // SSQ_COLS, dtype=torch.float32, device=like.device)
+
+    def put(self, out: torch.Tensor, ssq: Optional[torch.Tensor]) -> torch.Tensor:
+        """Record out (the tensor handed to the next call) and its sums."""
+        self.src = out
+        self.ssq = ssq
+        return out
+
+
 def _check_numel(name: str, t: torch.Tensor, want: int) -> None:
     # The kernels index biases by stream / matrix element; a short tensor would be
     # read out of bounds, so sizes are enforced here (the C ABI sees only pointers).
@@ -174,11 +234,21 @@ def _norm_args(norm, C: int, dev):
     return wc.data_ptr(), H.dtype_tag(wc), float(eps), wc
 
 
+def _ssq_ptr(ssq, M: int, C: int):
+    if ssq is None:
+        return None
+    if ssq.dtype != torch.float32 or tuple(ssq.shape) != (M, C // SSQ_COLS) or not ssq.is_contiguous():
+        raise ValueError(f"mhc_amd: sums of squares must be contiguous fp32 [{M}, {C // SSQ_COLS}]")
+    return ssq.data_ptr()
+
+
 def pre_full(x_flat, phi, packed, a_pre, b_pre, a_post, b_post, a_res, b_res, n, C,
              post_mult, pre_eps, rms_eps, sk_iters, sk_eps, *, sinkhorn=True,
-             want_h_pre=False, want_raw=False, want_saved=False, norm=None):
+             want_h_pre=False, want_raw=False, want_saved=False, norm=None, ssq=None):
     """Fused pre phase (+ Sinkhorn).  Returns a dict of [M, ...] tensors.
-    norm=(weight [C], eps): "sub_in" is RMSNorm(pre-aggregate) instead."""
+    norm=(weight [C], eps): "sub_in" is RMSNorm(pre-aggregate) instead.
+    ssq: x's per-row partial sums of squares ([M, C / 128] fp32, from the
+    launch that wrote x), or None."""
     dev = H.require_device(x_flat, phi, a_pre, b_pre, a_post, b_post, a_res, b_res)
     NC = n * C
     FD = 2 * n + n * n
@@ -209,16 +279,18 @@ def pre_full(x_flat, phi, packed, a_pre, b_pre, a_post, b_post, a_res, b_res, n,
             H.ptr(out["h_res_raw"]), H.ptr(out["h_res"]), H.ptr(out["inv_rms"]),
             H.ptr(out["mixes_raw"]), M, n, C, float(post_mult), float(pre_eps), float(rms_eps),
             int(sk_iters), float(sk_eps))
+    sp = _ssq_ptr(ssq, M, C)
     if norm is None:
-        H.check(H.load().mhc_pre_fwd(*args, H.stream(dev)), "mhc_pre_fwd")
+        H.check(H.load().mhc_pre_fwd(*args, sp, H.stream(dev)), "mhc_pre_fwd")
     else:
         wp, wdt, weps, _keep = _norm_args(norm, C, dev)
-        H.check(H.load().mhc_pre_norm_fwd(*args, wp, wdt, weps, H.stream(dev)), "mhc_pre_norm_fwd")
+        H.check(H.load().mhc_pre_norm_fwd(*args, wp, wdt, weps, sp, H.stream(dev)),
+                "mhc_pre_norm_fwd")
     return out
 
 
 def pre_nohres(x_flat, phi, packed, a_pre, b_pre, a_post, b_post, n, C, post_mult, pre_eps,
-               rms_eps, *, want_h_pre=False, want_saved=False, norm=None):
+               rms_eps, *, want_h_pre=False, want_saved=False, norm=None, ssq=None):
     dev = H.require_device(x_flat, phi, a_pre, b_pre, a_post, b_post)
     NC = n * C
     FD = 2 * n
@@ -244,17 +316,18 @@ def pre_nohres(x_flat, phi, packed, a_pre, b_pre, a_post, b_post, n, C, post_mul
             H.dtype_tag(a_pre), out["sub_in"].data_ptr(), H.ptr(out["h_pre"]),
             out["h_post"].data_ptr(), H.ptr(out["inv_rms"]), H.ptr(out["mixes_raw"]),
             M, n, C, float(post_mult), float(pre_eps), float(rms_eps))
+    sp = _ssq_ptr(ssq, M, C)
     if norm is None:
-        H.check(H.load().mhc_pre_nohres_fwd(*args, H.stream(dev)), "mhc_pre_nohres_fwd")
+        H.check(H.load().mhc_pre_nohres_fwd(*args, sp, H.stream(dev)), "mhc_pre_nohres_fwd")
     else:
         wp, wdt, weps, _keep = _norm_args(norm, C, dev)
-        H.check(H.load().mhc_pre_nohres_norm_fwd(*args, wp, wdt, weps, H.stream(dev)),
+        H.check(H.load().mhc_pre_nohres_norm_fwd(*args, wp, wdt, weps, sp, H.stream(dev)),
                 "mhc_pre_nohres_norm_fwd")
     return out
 
 
 def head(x_flat, phi, packed, alpha, bias, n, C, pre_eps, rms_eps, *, want_saved=False,
-         norm=None):
+         norm=None, ssq=None):
     """MHCHead forward; n == 1 is the plain RMSNorm (phi/alpha/bias unused).
     norm=(weight [C], eps): the model's final RMSNorm applied in the same launch."""
     NC = n * C
@@ -279,17 +352,20 @@ def head(x_flat, phi, packed, alpha, bias, n, C, pre_eps, rms_eps, *, want_saved
     mix = torch.empty(M, n, dtype=torch.float32, device=dev) if (want_saved and n > 1) else None
     args = (x2.data_ptr(), H.dtype_tag(x2), phi_p, phi_dt, H.ptr(packed), a_p, b_p, pdt,
             out.data_ptr(), H.ptr(inv), H.ptr(mix), M, n, C, float(pre_eps), float(rms_eps))
+    sp = _ssq_ptr(ssq, M, C) if n > 1 else None
     if norm is None:
-        H.check(H.load().mhc_head_fwd(*args, H.stream(dev)), "mhc_head_fwd")
+        H.check(H.load().mhc_head_fwd(*args, sp, H.stream(dev)), "mhc_head_fwd")
     else:
         wp, wdt, weps, _keep = _norm_args(norm, C, dev)
-        H.check(H.load().mhc_head_norm_fwd(*args, wp, wdt, weps, H.stream(dev)),
+        H.check(H.load().mhc_head_norm_fwd(*args, wp, wdt, weps, sp, H.stream(dev)),
                 "mhc_head_norm_fwd")
     return out, inv, mix
 
 
-def post(x_flat, h_res, h_post, f_out, n, C):
-    """out = H_res . x + H_post (x) F; h_res None means identity (use_mhc = 2)."""
+def post(x_flat, h_res, h_post, f_out, n, C, ssq_out=None):
+    """out = H_res . x + H_post (x) F; h_res None means identity (use_mhc = 2).
+    ssq_out: an [M, C / 128] fp32 buffer that receives out's per-row partial
+    sums of squares (for the next pre launch), or None."""
     dev = H.require_device(x_flat, h_res, h_post, f_out)
     NC = n * C
     x2 = _rows(x_flat, NC)
@@ -300,16 +376,17 @@ def post(x_flat, h_res, h_post, f_out, n, C):
         raise TypeError("mhc_amd: h_res and h_post must share a dtype")
     out = torch.empty_like(x2)
     lib = H.load()
+    sp = _ssq_ptr(ssq_out, M, C)
     if h_res is not None:
         hr = h_res.contiguous().view(M, n, n)
         rc = lib.mhc_post_fwd(x2.data_ptr(), H.dtype_tag(x2), hr.data_ptr(), hp.data_ptr(),
                               H.dtype_tag(hp), f2.data_ptr(), H.dtype_tag(f2), out.data_ptr(),
-                              M, n, C, H.stream(dev))
+                              M, n, C, sp, H.stream(dev))
         H.check(rc, "mhc_post_fwd")
     else:
         rc = lib.mhc_post_nohres_fwd(x2.data_ptr(), H.dtype_tag(x2), hp.data_ptr(),
                                      H.dtype_tag(hp), f2.data_ptr(), H.dtype_tag(f2),
-                                     out.data_ptr(), M, n, C, H.stream(dev))
+                                     out.data_ptr(), M, n, C, sp, H.stream(dev))
         H.check(rc, "mhc_post_nohres_fwd")
     return out
 
@@ -328,16 +405,18 @@ def sinkhorn(m: torch.Tensor, iters: int, eps: float) -> torch.Tensor:
     return out
 
 
-def expand_norm(x: torch.Tensor, weight: torch.Tensor, eps: float, n: int) -> torch.Tensor:
+def expand_norm(x: torch.Tensor, weight: torch.Tensor, eps: float, n: int,
+                ssq_out=None) -> torch.Tensor:
     """RMSNorm over the last dim (gain weight) followed by StreamExpand to n
-    copies, one launch: [B, L, C] -> [B, L, n*C]."""
+    copies, one launch: [B, L, C] -> [B, L, n*C].  ssq_out as in post."""
     dev = H.require_device(x, weight)
     B, L, C = x.shape
     xc = x.contiguous()
     wp, wdt, weps, _keep = _norm_args((weight, eps), C, dev)
     out = torch.empty(B, L, n * C, dtype=x.dtype, device=dev)
     rc = H.load().mhc_expand_norm_fwd(xc.data_ptr(), H.dtype_tag(xc), wp, wdt, out.data_ptr(),
-                                      B * L, n, C, weps, H.stream(dev))
+                                      B * L, n, C, weps, _ssq_ptr(ssq_out, B * L, C),
+                                      H.stream(dev))
     H.check(rc, "mhc_expand_norm_fwd")
     return out
 

@@ -65,25 +65,32 @@ class StreamExpand(nn.Module):
             return x
         return _StreamExpandFn.apply(x, self.n)
 
-    def forward_normed(self, x: torch.Tensor, in_norm: nn.Module) -> torch.Tensor:
+    def forward_normed(self, x: torch.Tensor, in_norm: nn.Module,
+                       chain: _ops.StreamChain = None) -> torch.Tensor:
         """self(in_norm(x)), the model's entry (model/model_minimind.py:365):
-        one HIP launch (RMSNorm + n copies) when no autograd is needed."""
+        one HIP launch (RMSNorm + n copies) when no autograd is needed.  With a
+        chain (see MHCConnection_Fused.forward) that launch also writes the
+        stream's per-row sums of squares for the first connection."""
         if fusable_norm(in_norm, self.dim, x):
-            return _ops.expand_norm(x, in_norm.weight, norm_eps(in_norm, x), self.n)
-        return self(in_norm(x))
+            ssq = (chain.buffer(x, self.n, self.dim, rows=x.numel() // self.dim)
+                   if chain is not None and self.n > 1 else None)
+            out = _ops.expand_norm(x, in_norm.weight, norm_eps(in_norm, x), self.n, ssq_out=ssq)
+            return chain.put(out, ssq) if chain is not None else out
+        out = self(in_norm(x))
+        return chain.put(out, None) if chain is not None else out
 
 
 class _MHCHeadFn(_ops.GradAwareFunction):
     """MHCHead forward on the HIP kernel (model/mhc_common.py:311-400)."""
 
     @staticmethod
-    def forward(ctx, x_flat, w_phi, alpha, bias, pre_eps, rms_eps, n, c, packed=None):
+    def forward(ctx, x_flat, w_phi, alpha, bias, pre_eps, rms_eps, n, c, packed=None, ssq=None):
         B, L, NC = x_flat.shape
         train = _ops.grad_wanted(ctx)
         if packed is None and n > 1:  # called without the module's pack
             packed = _ops.packed_phi(w_phi, n, c, H.MODE_HEAD, training=_ops.grad_wanted(ctx, 1))
         out, inv, mix = _ops.head(x_flat, w_phi, packed, alpha, bias, n, c, pre_eps, rms_eps,
-                                  want_saved=train)
+                                  want_saved=train, ssq=ssq)
         if train:
             ctx.save_for_backward(x_flat.detach().contiguous().view(B * L, NC), w_phi, alpha,
                                   bias, inv, mix)
@@ -99,7 +106,7 @@ class _MHCHeadFn(_ops.GradAwareFunction):
                                   pre_eps, g_sub=g_out)
         g_w, g_a, g_b = _ops.pre_bwd_weights(x2, inv, mix, g_raw, w, alphas, n, c, H.MODE_HEAD)
         return (g_x.view(shape), g_w, g_a[0].to(alpha.dtype).reshape(alpha.shape),
-                g_b[0].to(bias.dtype).view(bias.shape), None, None, None, None, None)
+                g_b[0].to(bias.dtype).view(bias.shape), None, None, None, None, None, None)
 
 
 class _RMSFn(_ops.GradAwareFunction):
@@ -148,21 +155,24 @@ class MHCHead(nn.Module):
     def extra_repr(self) -> str:
         return f"n={self.n}, dim={self.dim}, backend=hip-gfx950"
 
-    def forward(self, x_flat: torch.Tensor, out_norm: nn.Module = None) -> torch.Tensor:
+    def forward(self, x_flat: torch.Tensor, out_norm: nn.Module = None,
+                chain: _ops.StreamChain = None) -> torch.Tensor:
         """out_norm: an nn.RMSNorm over dim applied to the head output (the
         model's final norm, model/model_minimind.py:367-370); without autograd
-        it runs inside the head launch."""
+        it runs inside the head launch.  chain: as MHCConnection_Fused.forward
+        (the head takes the last connection's sums of squares)."""
+        ssq = chain.take(x_flat, self.n, self.dim) if chain is not None and self.n > 1 else None
         if out_norm is not None:
             if fusable_norm(out_norm, self.dim, x_flat):
                 packed = (self._phi_pack.get(self.phi_weight, self.n, self.dim)
                           if self.n > 1 else None)
                 out, _, _ = _ops.head(x_flat, self.phi_weight, packed, self.alpha, self.bias,
                                       self.n, self.dim, self.pre_eps, self.eps,
-                                      norm=(out_norm.weight, norm_eps(out_norm, x_flat)))
+                                      norm=(out_norm.weight, norm_eps(out_norm, x_flat)), ssq=ssq)
                 return out.view(*x_flat.shape[:-1], self.dim)
-            return out_norm(self(x_flat))
+            return out_norm(self(x_flat, chain=chain))
         if self.n == 1:
             return _RMSFn.apply(x_flat, self.eps)
         packed = self._phi_pack.get(self.phi_weight, self.n, self.dim) if x_flat.is_cuda else None
         return _MHCHeadFn.apply(x_flat, self.phi_weight, self.alpha, self.bias,
-                                self.pre_eps, self.eps, self.n, self.dim, packed)
+                                self.pre_eps, self.eps, self.n, self.dim, packed, ssq)

@@ -114,14 +114,14 @@ class _PreSinkhornFn(_ops.GradAwareFunction):
 
     @staticmethod
     def forward(ctx, x_flat, w_phi, packed, alpha_pre, bias_pre, alpha_post, bias_post,
-                alpha_res, bias_res, post_mult, pre_eps, rms_eps, n, c, iters, sk_eps):
+                alpha_res, bias_res, post_mult, pre_eps, rms_eps, n, c, iters, sk_eps, ssq=None):
         B, L, NC = x_flat.shape
         train = _ops.grad_wanted(ctx)
         if train:
             _ops.check_sinkhorn_bwd_iters(n, iters)
         o = _ops.pre_full(x_flat, w_phi, packed, alpha_pre, bias_pre, alpha_post, bias_post,
                           alpha_res, bias_res, n, c, post_mult, pre_eps, rms_eps, iters, sk_eps,
-                          sinkhorn=True, want_raw=train, want_saved=train)
+                          sinkhorn=True, want_raw=train, want_saved=train, ssq=ssq)
         if train:
             ctx.save_for_backward(x_flat.detach().contiguous().view(B * L, NC), w_phi,
                                   alpha_pre, bias_pre, alpha_post, bias_post, alpha_res,
@@ -142,16 +142,16 @@ class _PreSinkhornFn(_ops.GradAwareFunction):
                                       out_dtype=x2.dtype)
         g = _pre_full_grads(x2, w, (a_pre, a_post, a_res), (b_pre, b_post, b_res), inv, mixes,
                             n, c, post_mult, pre_eps, shape, g_sub, None, g_hpost, g_raw)
-        return (g[0], g[1], None, *g[2:], None, None, None, None, None, None, None)
+        return (g[0], g[1], None, *g[2:], None, None, None, None, None, None, None, None)
 
 
 class _PostPhaseFullFn(_ops.GradAwareFunction):
     """out = H_res . x + H_post (x) F_out (model/mhc_fused.py:720-772)."""
 
     @staticmethod
-    def forward(ctx, x_flat, h_res, h_post, f_out, n, c):
+    def forward(ctx, x_flat, h_res, h_post, f_out, n, c, ssq_out=None):
         B, L, NC = x_flat.shape
-        out = _ops.post(x_flat, h_res, h_post, f_out, n, c)
+        out = _ops.post(x_flat, h_res, h_post, f_out, n, c, ssq_out=ssq_out)
         if _ops.grad_wanted(ctx):
             ctx.save_for_backward(x_flat.detach().contiguous().view(B * L, NC), h_res, h_post,
                                   f_out)
@@ -164,7 +164,7 @@ class _PostPhaseFullFn(_ops.GradAwareFunction):
         n, c, shape = ctx.cfg
         g_x, g_hr, g_hp, g_f = _ops.post_bwd(x2, h_res, h_post, f_out, n, c, g_out)
         return (g_x.view(shape), g_hr.view(h_res.shape), g_hp.view(h_post.shape),
-                g_f.to(f_out.dtype).view(f_out.shape), None, None)
+                g_f.to(f_out.dtype).view(f_out.shape), None, None, None)
 
 
 # ------------------------------------------------------------------- module
@@ -210,25 +210,33 @@ class MHCConnection_Fused(nn.Module):
                 f"backend=hip-gfx950")
 
     def forward(self, x_flat: torch.Tensor, sublayer_fn: Callable,
-                in_norm: nn.Module = None) -> torch.Tensor:
+                in_norm: nn.Module = None, chain: _ops.StreamChain = None) -> torch.Tensor:
         """PRE (+Sinkhorn, one HIP launch) -> sublayer F -> POST (one HIP launch).
 
         in_norm (optional, not in the reference signature): an nn.RMSNorm over
         dim that F applies to its input first, i.e. F(z) = sublayer_fn(in_norm(z)).
         Without autograd it runs inside the pre launch; otherwise it is applied
-        as a separate op, as when F contains it."""
+        as a separate op, as when F contains it.
+        chain (optional, not in the reference signature): a _ops.StreamChain
+        shared by consecutive mHC calls.  The post launch then also writes the
+        output rows' sums of squares, and the next call's pre launch takes
+        them instead of a pass over its input of its own (shapes where that
+        pass exists: n >= 8 or dim > 1024)."""
         packed = self._phi_pack.get(self.phi_weight, self.n, self.dim) if x_flat.is_cuda else None
+        ssq = chain.take(x_flat, self.n, self.dim) if chain is not None else None
+        ssq_out = chain.buffer(x_flat, self.n, self.dim) if chain is not None else None
         if in_norm is not None:
             if fusable_norm(in_norm, self.dim, x_flat):
                 o = _ops.pre_full(x_flat, self.phi_weight, packed, self.alpha_pre, self.bias_pre,
                                   self.alpha_post, self.bias_post, self.alpha_res, self.bias_res,
                                   self.n, self.dim, self.post_mult_value, self.pre_eps, self.eps,
                                   self.sinkhorn_iters, self.sinkhorn_eps,
-                                  norm=(in_norm.weight, norm_eps(in_norm, x_flat)))
+                                  norm=(in_norm.weight, norm_eps(in_norm, x_flat)), ssq=ssq)
                 B, L, NC = x_flat.shape
                 f_out = sublayer_fn(o["sub_in"].view(B, L, self.dim))
-                out = _ops.post(x_flat, o["h_res"], o["h_post"], f_out, self.n, self.dim)
-                return out.view(B, L, NC)
+                out = _ops.post(x_flat, o["h_res"], o["h_post"], f_out, self.n, self.dim,
+                                ssq_out=ssq_out).view(B, L, NC)
+                return chain.put(out, ssq_out) if chain is not None else out
             fn = sublayer_fn
             sublayer_fn = lambda z: fn(in_norm(z))  # noqa: E731
         sublayer_in, h_post, h_res = _PreSinkhornFn.apply(
@@ -236,6 +244,7 @@ class MHCConnection_Fused(nn.Module):
             self.alpha_pre, self.bias_pre, self.alpha_post, self.bias_post,
             self.alpha_res, self.bias_res,
             self.post_mult_value, self.pre_eps, self.eps, self.n, self.dim,
-            self.sinkhorn_iters, self.sinkhorn_eps)
+            self.sinkhorn_iters, self.sinkhorn_eps, ssq)
         f_out = sublayer_fn(sublayer_in)
-        return _PostPhaseFullFn.apply(x_flat, h_res, h_post, f_out, self.n, self.dim)
+        out = _PostPhaseFullFn.apply(x_flat, h_res, h_post, f_out, self.n, self.dim, ssq_out)
+        return chain.put(out, ssq_out) if chain is not None else out

@@ -27,13 +27,14 @@ class _PrePhaseFn(_ops.GradAwareFunction):
 
     @staticmethod
     def forward(ctx, x_flat, w_phi, alpha_pre, bias_pre, alpha_post, bias_post,
-                post_mult, pre_eps, rms_eps, n, c, packed=None):
+                post_mult, pre_eps, rms_eps, n, c, packed=None, ssq=None):
         B, L, NC = x_flat.shape
         train = _ops.grad_wanted(ctx)
         if packed is None:  # called as the reference's Function, without the module's pack
             packed = _ops.packed_phi(w_phi, n, c, H.MODE_NOHRES, training=_ops.grad_wanted(ctx, 1))
         o = _ops.pre_nohres(x_flat, w_phi, packed, alpha_pre, bias_pre, alpha_post, bias_post,
-                            n, c, post_mult, pre_eps, rms_eps, want_h_pre=True, want_saved=train)
+                            n, c, post_mult, pre_eps, rms_eps, want_h_pre=True, want_saved=train,
+                            ssq=ssq)
         if train:
             ctx.save_for_backward(x_flat.detach().contiguous().view(B * L, NC), w_phi,
                                   alpha_pre, bias_pre, alpha_post, bias_post,
@@ -53,16 +54,16 @@ class _PrePhaseFn(_ops.GradAwareFunction):
         return (g_x.view(shape), g_w,
                 g_a[0].to(a_pre.dtype).reshape(a_pre.shape), g_b[0].to(b_pre.dtype).view(b_pre.shape),
                 g_a[1].to(a_post.dtype).reshape(a_post.shape), g_b[1].to(b_post.dtype).view(b_post.shape),
-                None, None, None, None, None, None)
+                None, None, None, None, None, None, None)
 
 
 class _PostPhaseFn(_ops.GradAwareFunction):
     """out = x + H_post (x) F_out (model/mhc_fused_no_hres.py:532-581)."""
 
     @staticmethod
-    def forward(ctx, x_flat, h_post, f_out, n, c):
+    def forward(ctx, x_flat, h_post, f_out, n, c, ssq_out=None):
         B, L, NC = x_flat.shape
-        out = _ops.post(x_flat, None, h_post, f_out, n, c)
+        out = _ops.post(x_flat, None, h_post, f_out, n, c, ssq_out=ssq_out)
         if _ops.grad_wanted(ctx):
             ctx.save_for_backward(h_post, f_out)
         ctx.cfg = (n, c, (B, L, NC))
@@ -73,7 +74,7 @@ class _PostPhaseFn(_ops.GradAwareFunction):
         h_post, f_out = ctx.saved_tensors
         n, c, shape = ctx.cfg
         g_x, _, g_hp, g_f = _ops.post_bwd(None, None, h_post, f_out, n, c, g_out)
-        return (g_x.view(shape), g_hp.view(h_post.shape), g_f.view(f_out.shape), None, None)
+        return (g_x.view(shape), g_hp.view(h_post.shape), g_f.view(f_out.shape), None, None, None)
 
 
 class MHCConnection_FusedNoHres(nn.Module):
@@ -111,25 +112,30 @@ class MHCConnection_FusedNoHres(nn.Module):
                 f"post_mult_value={self.post_mult_value}, backend=hip-gfx950")
 
     def forward(self, x_flat: torch.Tensor, sublayer_fn: Callable,
-                in_norm: nn.Module = None) -> torch.Tensor:
-        """in_norm: as MHCConnection_Fused.forward (F(z) = sublayer_fn(in_norm(z)),
-        fused into the pre launch when no autograd is needed)."""
+                in_norm: nn.Module = None, chain: _ops.StreamChain = None) -> torch.Tensor:
+        """in_norm, chain: as MHCConnection_Fused.forward (F(z) =
+        sublayer_fn(in_norm(z)), fused into the pre launch when no autograd is
+        needed; the rows' sums of squares handed along the chain)."""
         packed = self._phi_pack.get(self.phi_weight, self.n, self.dim) if x_flat.is_cuda else None
+        ssq = chain.take(x_flat, self.n, self.dim) if chain is not None else None
+        ssq_out = chain.buffer(x_flat, self.n, self.dim) if chain is not None else None
         if in_norm is not None:
             if fusable_norm(in_norm, self.dim, x_flat):
                 o = _ops.pre_nohres(x_flat, self.phi_weight, packed, self.alpha_pre, self.bias_pre,
                                     self.alpha_post, self.bias_post, self.n, self.dim,
                                     self.post_mult_value, self.pre_eps, self.eps,
-                                    norm=(in_norm.weight, norm_eps(in_norm, x_flat)))
+                                    norm=(in_norm.weight, norm_eps(in_norm, x_flat)), ssq=ssq)
                 B, L, NC = x_flat.shape
                 f_out = sublayer_fn(o["sub_in"].view(B, L, self.dim))
-                out = _ops.post(x_flat, None, o["h_post"], f_out, self.n, self.dim)
-                return out.view(B, L, NC)
+                out = _ops.post(x_flat, None, o["h_post"], f_out, self.n, self.dim,
+                                ssq_out=ssq_out).view(B, L, NC)
+                return chain.put(out, ssq_out) if chain is not None else out
             fn = sublayer_fn
             sublayer_fn = lambda z: fn(in_norm(z))  # noqa: E731
         sublayer_in, _h_pre, h_post = _PrePhaseFn.apply(
             x_flat, self.phi_weight, self.alpha_pre, self.bias_pre,
             self.alpha_post, self.bias_post,
-            self.post_mult_value, self.pre_eps, self.eps, self.n, self.dim, packed)
+            self.post_mult_value, self.pre_eps, self.eps, self.n, self.dim, packed, ssq)
         f_out = sublayer_fn(sublayer_in)
-        return _PostPhaseFn.apply(x_flat, h_post, f_out, self.n, self.dim)
+        out = _PostPhaseFn.apply(x_flat, h_post, f_out, self.n, self.dim, ssq_out)
+        return chain.put(out, ssq_out) if chain is not None else out

@@ -19,7 +19,10 @@ Differences from the reference, all outside the mHC path:
     (in_norm), the entry RMSNorm to StreamExpand.forward_normed and the final
     RMSNorm to MHCHead (out_norm).  Without autograd each runs inside the
     neighbouring HIP launch; with autograd they run as separate ops in the
-    reference's order (model/model_minimind.py:326-336, :365-370).
+    reference's order (model/model_minimind.py:326-336, :365-370);
+  * one StreamChain per forward is passed to every mHC call, so each launch
+    that writes the residual stream hands its rows' sums of squares to the
+    next pre launch (used at n >= 8 or hidden > 1024).
 """
 from __future__ import annotations
 
@@ -30,6 +33,7 @@ import torch
 import torch.nn.functional as F
 from torch import nn
 
+from ._ops import StreamChain
 from .mhc_common import MHCHead, StreamExpand
 from .mhc_fused import MHCConnection_Fused
 from .mhc_fused_no_hres import MHCConnection_FusedNoHres
@@ -242,7 +246,7 @@ class MiniMindBlock(nn.Module):
             self.mlp_mhc = cls(n, D, eps=eps)
 
     def forward(self, hidden_states, position_embeddings, past_key_value=None, use_cache=False,
-                attention_mask=None):
+                attention_mask=None, chain=None):
         if self.use_mhc:
             holder = [None]
 
@@ -254,8 +258,10 @@ class MiniMindBlock(nn.Module):
                 holder[0] = kv
                 return out
 
-            hidden_states = self.attn_mhc(hidden_states, attn_fn, in_norm=self.attn_in_norm)
-            hidden_states = self.mlp_mhc(hidden_states, self.mlp, in_norm=self.ffn_in_norm)
+            hidden_states = self.attn_mhc(hidden_states, attn_fn, in_norm=self.attn_in_norm,
+                                          chain=chain)
+            hidden_states = self.mlp_mhc(hidden_states, self.mlp, in_norm=self.ffn_in_norm,
+                                         chain=chain)
             return hidden_states, holder[0]
         attn_out, kv = self.self_attn(self.attn_in_norm(hidden_states), position_embeddings,
                                       past_key_value, use_cache, attention_mask)
@@ -295,18 +301,22 @@ class MiniMindModel(nn.Module):
         past_key_values = past_key_values or [None] * len(self.layers)
         start = past_key_values[0][0].shape[1] if past_key_values[0] is not None else 0
         h = self.dropout(self.embed_tokens(input_ids))
+        # Each mHC launch that writes the stream hands its rows' sums of squares
+        # to the next one that reads it (the stream passes from call to call
+        # unchanged): a chain per forward.
+        chain = StreamChain() if self.config.use_mhc else None
         if self.config.use_mhc:  # RMSNorm + StreamExpand, one launch without autograd
-            h = self.embed_up_norm[1].forward_normed(h, self.embed_up_norm[0])
+            h = self.embed_up_norm[1].forward_normed(h, self.embed_up_norm[0], chain=chain)
         else:
             h = self.embed_up_norm(h)
         pos = (self.freqs_cos[start:start + seq_len], self.freqs_sin[start:start + seq_len])
         presents = []
         for layer, pkv in zip(self.layers, past_key_values):
             h, present = layer(h, pos, past_key_value=pkv, use_cache=use_cache,
-                               attention_mask=attention_mask)
+                               attention_mask=attention_mask, chain=chain)
             presents.append(present)
         if self.config.use_mhc:  # MHCHead + final RMSNorm, one launch without autograd
-            h = self.norm[0](h, out_norm=self.norm[1])
+            h = self.norm[0](h, out_norm=self.norm[1], chain=chain)
         else:
             h = self.norm(h)
         aux = sum([l.mlp.aux_loss for l in self.layers if isinstance(l.mlp, MOEFeedForward)],

@@ -86,10 +86,10 @@ def test_validation_errors_need_no_device(lib):
     # n = 0 is rejected by argument checks, before any HIP call
     rc = lib.mhc_pre_fwd(None, 1, None, 1, None, None, None, None, None, None, None, 1,
                          None, None, None, None, None, None, None, 16, 0, 768,
-                         2.0, 1e-6, 1e-6, 20, 1e-6, None)
+                         2.0, 1e-6, 1e-6, 20, 1e-6, None, None)
     assert rc == 1
     assert b"n must be in" in lib.mhc_last_error()
-    rc = lib.mhc_post_fwd(None, 1, None, None, 1, None, 1, None, 16, 4, 768, None)
+    rc = lib.mhc_post_fwd(None, 1, None, None, 1, None, 1, None, 16, 4, 768, None, None)
     assert rc == 1
     rc = lib.mhc_sinkhorn_fwd(ctypes.c_void_p(16), ctypes.c_void_p(32), 0, 4, 64, 20, 1e-6, None)
     assert rc == 1 and b"n must be" in lib.mhc_last_error()
@@ -104,19 +104,35 @@ def test_norm_entry_points_validate_without_device(lib):
     p = ctypes.c_void_p(256)
     # the *_norm_fwd variants require the gain
     rc = lib.mhc_pre_norm_fwd(p, 1, p, 1, None, p, p, p, p, p, p, 1, p, None, p, None, p, None,
-                              None, 16, 4, 64, 2.0, 1e-6, 1e-6, 20, 1e-6, None, 1, 1e-6, None)
+                              None, 16, 4, 64, 2.0, 1e-6, 1e-6, 20, 1e-6, None, 1, 1e-6, None, None)
     assert rc == 1 and b"norm_weight is required" in lib.mhc_last_error()
     rc = lib.mhc_pre_nohres_norm_fwd(p, 1, p, 1, None, p, p, p, p, 1, p, None, p, None, None,
-                                     16, 4, 64, 2.0, 1e-6, 1e-6, None, 1, 1e-6, None)
+                                     16, 4, 64, 2.0, 1e-6, 1e-6, None, 1, 1e-6, None, None)
     assert rc == 1 and b"norm_weight is required" in lib.mhc_last_error()
     rc = lib.mhc_head_norm_fwd(p, 1, p, 1, None, p, p, 1, p, None, None, 16, 4, 64, 1e-6, 1e-6,
-                               p, 7, 1e-6, None)
+                               p, 7, 1e-6, None, None)
     assert rc == 1 and b"bad norm dtype" in lib.mhc_last_error()
-    rc = lib.mhc_expand_norm_fwd(p, 1, p, 1, p, 16, 4, 64, -1.0, None)
+    rc = lib.mhc_expand_norm_fwd(p, 1, p, 1, p, 16, 4, 64, -1.0, None, None)
     assert rc == 1 and b"eps" in lib.mhc_last_error()
-    rc = lib.mhc_expand_norm_fwd(p, 1, p, 1, p, 16, 0, 64, 1e-6, None)
+    rc = lib.mhc_expand_norm_fwd(p, 1, p, 1, p, 16, 0, 64, 1e-6, None, None)
     assert rc == 1 and b"bad shape" in lib.mhc_last_error()
-    assert lib.mhc_expand_norm_fwd(None, 1, None, 1, None, 0, 4, 64, 1e-6, None) == 0  # empty
+    assert lib.mhc_expand_norm_fwd(None, 1, None, 1, None, 0, 4, 64, 1e-6, None, None) == 0
+
+
+def test_sums_of_squares_argument_checks(lib):
+    """x_ssq / out_ssq are defined for bf16 streams with C % 128 == 0 only;
+    other shapes are refused before any device work."""
+    p = ctypes.c_void_p(256)
+    f = ctypes.c_void_p(512)
+    # pre with x_ssq at C = 100 (not a multiple of 128), and with an fp32 stream
+    for dt, C in ((1, 100), (0, 768)):
+        rc = lib.mhc_pre_fwd(p, dt, p, dt, None, p, p, p, p, p, p, dt, p, None, p, None, p, None,
+                             None, 16, 8, C, 2.0, 1e-6, 1e-6, 20, 1e-6, f, None)
+        assert rc == 1 and b"x_ssq" in lib.mhc_last_error(), (dt, C)
+    rc = lib.mhc_post_fwd(p, 1, p, p, 1, p, 1, ctypes.c_void_p(4096), 16, 8, 96, f, None)
+    assert rc == 1 and b"out_ssq" in lib.mhc_last_error()
+    rc = lib.mhc_expand_norm_fwd(p, 0, p, 0, ctypes.c_void_p(4096), 16, 8, 256, 1e-6, f, None)
+    assert rc == 1 and b"out_ssq" in lib.mhc_last_error()
 
 
 def test_row_staging_round_trip(lib):
@@ -135,3 +151,21 @@ def test_token_threshold_round_trip(lib):
     assert lib.mhc_pre_token_threshold(-1) == 17
     assert lib.mhc_pre_token_threshold(old) == 17
     assert lib.mhc_pre_token_threshold(-1) == old
+
+
+def test_integration_stub_matches_the_header(lib, monkeypatch):
+    """The ctypes binding INTEGRATION.md shows declares every entry point it
+    binds with the argument list this package's binding (and so the header)
+    has: a stale stub would pass the stream in another argument's place."""
+    from model import _hip as H
+    text = (ROOT / "INTEGRATION.md").read_text()
+    sec = text[text.index("## 2."):]
+    code = re.search(r"```python\n(.*?)```", sec, re.S).group(1)
+    monkeypatch.setenv("MHC_AMD_LIB", str(H.LIB_PATH))
+    ns = {}
+    exec(compile(code, "INTEGRATION.md", "exec"), ns)
+    stub = ns["_lib"]
+    bound = [name for name in H._SIGNATURES if getattr(getattr(stub, name), "argtypes", None)]
+    assert "mhc_pre_fwd" in bound and "mhc_post_fwd" in bound
+    for name in bound:
+        assert list(getattr(stub, name).argtypes) == list(H._SIGNATURES[name][1]), name

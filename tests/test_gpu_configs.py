@@ -141,7 +141,7 @@ def _hook_mhc(model):
     records = []
     for name, mod in model.named_modules():
         if isinstance(mod, MHCConnection_Fused):
-            def conn(x, f, in_norm=None, _orig=mod.forward, _mod=mod, _name=name):
+            def conn(x, f, in_norm=None, chain=None, _orig=mod.forward, _mod=mod, _name=name):
                 rec = {"kind": "conn", "name": _name, "mod": _mod, "norm": in_norm,
                        "x": x.detach().clone()}
 
@@ -150,21 +150,21 @@ def _hook_mhc(model):
                     o = f(z)
                     rec["f"] = o.detach().clone()
                     return o
-                out = _orig(x, fw, in_norm)
+                out = _orig(x, fw, in_norm, chain=chain)
                 rec["out"] = out.detach().clone()
                 records.append(rec)
                 return out
             mod.forward = conn
         elif isinstance(mod, StreamExpand):
-            def expand(x, norm, _orig=mod.forward_normed, _mod=mod):
-                out = _orig(x, norm)
+            def expand(x, norm, chain=None, _orig=mod.forward_normed, _mod=mod):
+                out = _orig(x, norm, chain=chain)
                 records.append({"kind": "entry", "mod": _mod, "norm": norm,
                                 "x": x.detach().clone(), "out": out.detach().clone()})
                 return out
             mod.forward_normed = expand
         elif isinstance(mod, MHCHead):
-            def head(x, out_norm=None, _orig=mod.forward, _mod=mod):
-                out = _orig(x, out_norm)
+            def head(x, out_norm=None, chain=None, _orig=mod.forward, _mod=mod):
+                out = _orig(x, out_norm, chain=chain)
                 records.append({"kind": "exit", "mod": _mod, "norm": out_norm,
                                 "x": x.detach().clone(), "out": out.detach().clone()})
                 return out

@@ -58,7 +58,7 @@ def _oracle_copy(model: MiniMindForCausalLM) -> MiniMindForCausalLM:
     ref.load_state_dict({k: v.detach().float().cpu() for k, v in model.state_dict().items()})
     for mod in ref.modules():
         if isinstance(mod, MHCConnection_Fused):
-            def fwd(self, x, f, in_norm=None):
+            def fwd(self, x, f, in_norm=None, chain=None):
                 return R.mhc_full_forward(x, R.module_params(self), _with_norm(f, in_norm), self.n,
                                           self.dim, eps=self.eps, pre_eps=self.pre_eps,
                                           post_mult=self.post_mult_value,
@@ -66,13 +66,13 @@ def _oracle_copy(model: MiniMindForCausalLM) -> MiniMindForCausalLM:
                                           sinkhorn_eps=self.sinkhorn_eps)["out"]
             mod.forward = types.MethodType(fwd, mod)
         elif isinstance(mod, MHCConnection_FusedNoHres):
-            def fwd(self, x, f, in_norm=None):
+            def fwd(self, x, f, in_norm=None, chain=None):
                 return R.mhc_nohres_forward(x, R.module_params(self), _with_norm(f, in_norm),
                                             self.n, self.dim, eps=self.eps, pre_eps=self.pre_eps,
                                             post_mult=self.post_mult_value)["out"]
             mod.forward = types.MethodType(fwd, mod)
         elif isinstance(mod, MHCHead):
-            def fwd(self, x, out_norm=None):
+            def fwd(self, x, out_norm=None, chain=None):
                 out = R.head(x, R.module_params(self), self.n, self.dim, pre_eps=self.pre_eps,
                              rms_eps=self.eps)
                 return out if out_norm is None else out_norm(out)

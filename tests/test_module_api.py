@@ -34,12 +34,15 @@ def test_constructor_signatures_match_reference():
                                            ("dim", inspect._empty)]
     # model/mhc_fused.py:141
     assert _sig(sinkhorn_normalize) == [("M", inspect._empty), ("iters", 10), ("eps", 1e-6)]
-    # reference forward(x_flat, sublayer_fn) (model/mhc_fused.py:817); the one
-    # addition is an optional trailing in_norm (default None: the reference call)
+    # reference forward(x_flat, sublayer_fn) (model/mhc_fused.py:817); the
+    # additions are optional trailing in_norm / chain (default None: the
+    # reference call)
     for cls in (MHCConnection_Fused, MHCConnection_FusedNoHres):
         assert _sig(cls.forward)[1:] == [("x_flat", inspect._empty),
-                                         ("sublayer_fn", inspect._empty), ("in_norm", None)]
-    assert _sig(MHCHead.forward)[1:] == [("x_flat", inspect._empty), ("out_norm", None)]
+                                         ("sublayer_fn", inspect._empty), ("in_norm", None),
+                                         ("chain", None)]
+    assert _sig(MHCHead.forward)[1:] == [("x_flat", inspect._empty), ("out_norm", None),
+                                         ("chain", None)]
 
 
 def test_parameters_match_reference():
