@@ -42,7 +42,8 @@ from profiles/traffic_mhc_fwd_c2.txt (the rocprofv3 summary committed beside
 the kernel-trace summary); traffic is null when that file is absent.
 
 Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--no-e2e] [--no-cpu]
-       python bench.py --section fp32-layout|other-configs|reference-shapes   (one section only)
+       python bench.py --section fp32-layout|other-configs|reference-shapes|backward
+                                                           (one section only)
        python bench.py --traffic     (counter passes only; prints nothing)
        python bench.py --e2e-only [prefill|decode|moe]   (end-to-end model figures only)
 """
@@ -872,7 +873,8 @@ def main():
                     choices=["all", "prefill", "decode", "moe"],
                     help="run only the end-to-end model figures (configs 3, 4, 5, or one of "
                          "them) and print them as one JSON line")
-    ap.add_argument("--section", choices=["fp32-layout", "other-configs", "reference-shapes"],
+    ap.add_argument("--section", choices=["fp32-layout", "other-configs", "reference-shapes",
+                                          "backward"],
                     default=None,
                     help="run only the fp32-layout launches or the isolated config-4 / config-5 "
                          "kernel pairs and print them as one JSON line (for profiler runs)")
@@ -895,6 +897,11 @@ def main():
         return
     if args.section == "fp32-layout":
         print(json.dumps({"fp32_layout": bench_layout32()}), flush=True)
+        return
+    if args.section == "backward":
+        bw5 = bench_backward(n=8, M=8192)
+        bw5["config"] = "C5 shape: 8192 tokens, n=8, C=768, bf16"
+        print(json.dumps({"backward": bench_backward(), "backward_c5": bw5}), flush=True)
         return
     if args.section == "reference-shapes":
         print(json.dumps({"reference_bench_shapes": reference_bench_shapes()}), flush=True)

@@ -667,8 +667,13 @@ constexpr int kWTok = 64;                // tokens per step
 constexpr int kWCols = 128;              // columns per workgroup
 constexpr int kWRow = kWTok * 2 + 16;    // LDS row stride in bytes (64 bf16 + pad)
 
-template <int NTF, bool F32>  // 16-wide feature tiles, fp32 x
-__global__ __launch_bounds__(512) void weights_mfma_kernel(WeightsArgs a, int64_t per) {
+// x is loaded PF steps ahead (2 where the registers allow: the x of step t + 2
+// goes out while step t's MFMAs run, so a workgroup keeps 32 KB of x in
+// flight); the per-token values of step t + 1 go out as soon as step t has
+// consumed its own.
+template <int NTF, bool F32, int PF>  // 16-wide feature tiles, fp32 x, steps in flight
+__global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(PF == 2 ? 4 : 1)))
+void weights_mfma_kernel(WeightsArgs a, int64_t per) {
   constexpr int F16 = NTF * 16;
   constexpr int UPT = F16 / 16;  // (token pair, feature) items per thread: 32 * F16 / 512
   constexpr int XQ = F32 ? 2 : 1;  // 16-byte loads per 8 columns of one token
@@ -707,11 +712,13 @@ __global__ __launch_bounds__(512) void weights_mfma_kernel(WeightsArgs a, int64_
   // Everything one step reads from memory; the next step's copy is loaded
   // while the current step's MFMAs run.  x is read non-temporally (its last
   // use in the backward).
-  struct Step {
+  struct XStep {  // a step's x, PF steps ahead
     U32x4 xa[XQ], xb[XQ];
+  };
+  struct Step {     // a step's per-token values, one step ahead
     float ga[UPT], gb[UPT], ia[UPT], ib[UPT], ma[UPT], mb[UPT];
   };
-  auto load_step = [&](int64_t t, Step& st) {
+  auto load_x = [&](int64_t t, XStep& st) {
     const int valid = t < te ? (int)(te - t < kWTok ? te - t : kWTok) : 0;
     const auto rs = make_rsrc(static_cast<const unsigned char*>(a.x) + (t < te ? t : 0) * NC * ES,
                               (uint32_t)valid * NC * ES);
@@ -720,6 +727,8 @@ __global__ __launch_bounds__(512) void weights_mfma_kernel(WeightsArgs a, int64_
       st.xa[h] = buf_load16_nt(rs, okc ? (uint32_t)((2 * tp) * NC + col) * ES + 16u * h : kBufOob, 0);
       st.xb[h] = buf_load16_nt(rs, okc ? (uint32_t)((2 * tp + 1) * NC + col) * ES + 16u * h : kBufOob, 0);
     }
+  };
+  auto load_step = [&](int64_t t, Step& st) {
 #pragma unroll
     for (int u = 0; u < UPT; ++u) {
       const int idx = tid + 512 * u;
@@ -743,9 +752,9 @@ __global__ __launch_bounds__(512) void weights_mfma_kernel(WeightsArgs a, int64_
 #pragma unroll
   for (int ft = 0; ft < NTF; ++ft) acc[ft] = f32x4_t{0.f, 0.f, 0.f, 0.f};
 
+  // One step: the staged loads to LDS, then the MFMAs while later steps load.
   Step cur;
-  load_step(tb, cur);
-  for (int64_t t = tb; t < te; t += kWTok) {
+  auto run_step = [&](int64_t t, XStep& xc) {
     // u = inv * g_raw as hi / lo bf16 token pairs, [feature][token]
 #pragma unroll
     for (int u = 0; u < UPT; ++u) {
@@ -762,25 +771,30 @@ __global__ __launch_bounds__(512) void weights_mfma_kernel(WeightsArgs a, int64_
         sa[u] = fmaf(cur.gb[u], cur.mb[u], fmaf(cur.ga[u], cur.ma[u], sa[u]));
       }
     }
+    // The next step's per-token values go out as soon as these are consumed:
+    // they then have this step's transposes, barriers and MFMAs to arrive.
+    load_step(t + kWTok, cur);
     // x tile transposed: column 8kc + e, tokens (2tp, 2tp + 1) in one dword
 #pragma unroll
     for (int e = 0; e < 8; ++e) {
       const uint32_t off = (8 * kc + e) * kWRow + tp_slot(tp, kc) * 4;
       if constexpr (F32) {
-        const float va = __uint_as_float(cur.xa[e >> 2].v[e & 3]);
-        const float vb = __uint_as_float(cur.xb[e >> 2].v[e & 3]);
+        const float va = __uint_as_float(xc.xa[e >> 2].v[e & 3]);
+        const float vb = __uint_as_float(xc.xb[e >> 2].v[e & 3]);
         const uint32_t hi = pack_bf16x2(va, vb);
         *reinterpret_cast<uint32_t*>(s_x + off) = hi;
         *reinterpret_cast<uint32_t*>(s_xl + off) = pack_bf16x2(va - bf16lo(hi), vb - bf16hi(hi));
       } else {
-        const uint32_t wa = cur.xa[0].v[e >> 1];
-        const uint32_t wb = cur.xb[0].v[e >> 1];
+        const uint32_t wa = xc.xa[0].v[e >> 1];
+        const uint32_t wb = xc.xb[0].v[e >> 1];
         const uint32_t d = (e & 1) ? ((wa >> 16) | (wb & 0xffff0000u)) : ((wa & 0xffffu) | (wb << 16));
         *reinterpret_cast<uint32_t*>(s_x + off) = d;
       }
     }
     __syncthreads();
-    load_step(t + kWTok, cur);  // next step's loads fly over the MFMAs
+    // x of step t + PF flies over the MFMAs (issued after the per-token values
+    // of step t + 1: the vector-memory counter retires in order).
+    load_x(t + PF * kWTok, xc);
 #pragma unroll
     for (int ks = 0; ks < kWTok / 32; ++ks) {
       const int xc = 16 * wave + r;  // column of the slice
@@ -798,6 +812,15 @@ __global__ __launch_bounds__(512) void weights_mfma_kernel(WeightsArgs a, int64_
       }
     }
     __syncthreads();
+  };
+  XStep st[PF];
+  load_step(tb, cur);
+#pragma unroll
+  for (int q = 0; q < PF; ++q) load_x(tb + q * kWTok, st[q]);
+  for (int64_t t = tb; t < te; t += PF * kWTok) {  // uniform; steps past te read nothing
+#pragma unroll
+    for (int q = 0; q < PF; ++q)
+      if (t + q * kWTok < te) run_step(t + q * kWTok, st[q]);
   }
   // partial W of this range: lane (feature column r, g) holds rows 4g .. 4g + 3
   float* W = a.work + (int64_t)rng * NC * FD;
@@ -830,14 +853,44 @@ __global__ __launch_bounds__(512) void weights_mfma_kernel(WeightsArgs a, int64_
   }
 }
 
+// Two steps of x in flight where that keeps four waves a SIMD without spills
+// (bf16, FD <= 32: 128 VGPRs); wider features and fp32 x keep one.
+template <int NTF, bool F32>
+constexpr int weights_pf() {
+  return !F32 && NTF <= 2 ? 2 : 1;
+}
+
+// Workgroups of weights_mfma_kernel<NTF, F32> one CU holds at once (from its
+// registers and LDS; cached per instance).
+template <int NTF, bool F32>
+static int weights_wg_per_cu() {
+  static int cached = 0;
+  if (cached == 0) {
+    int blocks = 0;
+    if (hipOccupancyMaxActiveBlocksPerMultiprocessor(
+            &blocks, weights_mfma_kernel<NTF, F32, weights_pf<NTF, F32>()>, 512, 0) != hipSuccess ||
+        blocks < 1)
+      blocks = 1;
+    cached = blocks;
+  }
+  return cached;
+}
+
+template <int NTF>
+static int weights_wg_per_cu(const WeightsArgs& a) {
+  return a.x_dtype == kF32 ? weights_wg_per_cu<NTF, true>() : weights_wg_per_cu<NTF, false>();
+}
+
 template <int NTF>
 static hipError_t launch_weights_mfma(const WeightsArgs& a, int R, int64_t per, hipStream_t s) {
   const int NC = a.n * a.C;
   const dim3 grid((unsigned)((NC + kWCols - 1) / kWCols), (unsigned)R);
   if (a.x_dtype == kF32)
-    hipLaunchKernelGGL((weights_mfma_kernel<NTF, true>), grid, dim3(512), 0, s, a, per);
+    hipLaunchKernelGGL((weights_mfma_kernel<NTF, true, weights_pf<NTF, true>()>), grid, dim3(512), 0,
+                       s, a, per);
   else
-    hipLaunchKernelGGL((weights_mfma_kernel<NTF, false>), grid, dim3(512), 0, s, a, per);
+    hipLaunchKernelGGL((weights_mfma_kernel<NTF, false, weights_pf<NTF, false>()>), grid, dim3(512),
+                       0, s, a, per);
   return hipGetLastError();
 }
 
@@ -853,9 +906,22 @@ hipError_t launch_pre_bwd_weights(const WeightsArgs& a, hipStream_t s) {
   if (a.max_ranges > 0 && R > a.max_ranges) R = a.max_ranges;  // smaller workspace
   hipError_t e;
   if (mfma) {
-    // about two workgroups per CU, token ranges of whole 64-token steps
+    // Token ranges of whole 64-token steps, as many as one round of
+    // workgroups holds (every CU as full as the kernel's registers and LDS
+    // allow; two rounds if one round leaves fewer than four ranges), so no
+    // short last round of stragglers follows the full ones.
+    int wpc = 1;
+    switch (ntf) {
+      case 1: wpc = weights_wg_per_cu<1>(a); break;
+      case 2: wpc = weights_wg_per_cu<2>(a); break;
+      case 3: wpc = weights_wg_per_cu<3>(a); break;
+      default: wpc = weights_wg_per_cu<5>(a); break;
+    }
     const int64_t slices = (NC + kWCols - 1) / kWCols;
-    int64_t want = (512 + slices - 1) / slices;
+    const int64_t cap = (int64_t)wpc * device_cus();
+    int64_t want = cap / slices;
+    if (want < 4) want = 2 * cap / slices;
+    if (want < 1) want = 1;
     if (want < R) R = (int)want;
     int64_t per = (a.M + R - 1) / R;
     per = (per + kWTok - 1) / kWTok * kWTok;

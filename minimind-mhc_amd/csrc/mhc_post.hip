@@ -11,6 +11,8 @@
 // thread reads the n chunks of x at that column, the F chunk, and the token's
 // n*n + n gate values (broadcast within the token's threads), and writes n
 // chunks of out.  Every byte of x, F and out moves exactly once.
+#include <type_traits>
+
 #include "mhc_internal.hpp"
 
 namespace mhc {
@@ -92,7 +94,7 @@ __device__ __forceinline__ float rnd(float v) {
 template <typename XT, typename FT, int N, bool RES, bool SSQ>
 __global__ __launch_bounds__(256) void post_vec_kernel(PostArgs a) {
   constexpr int V = 16 / sizeof(XT);
-  static_assert(!SSQ || V == 8, "sums of squares for 16-bit streams");
+  static_assert(!SSQ || std::is_same_v<XT, __bf16>, "sums of squares for bf16 streams");
   const int C = a.C;
   const int CV = C / V;
   const int64_t gid = (int64_t)blockIdx.x * 256 + threadIdx.x;
@@ -129,12 +131,17 @@ __global__ __launch_bounds__(256) void post_vec_kernel(PostArgs a) {
         acc = xv[i][v];
       }
       o[v] = __fadd_rn(acc, rnd<XT>(__fmul_rn(hp[i], fv[v])));
-      if constexpr (SSQ) {
-        const float st = rnd<XT>(o[v]);
-        q = fmaf(st, st, q);
-      }
     }
-    store_pack_nt<XT, V>(out + (int64_t)i * C, o);
+    if constexpr (SSQ) {  // the stored pairs, squared on dot2 (exact products, fp32 sum)
+      u32x4_t ov;
+#pragma unroll
+      for (int e = 0; e < 4; ++e) ov[e] = pack_bf16x2(o[2 * e], o[2 * e + 1]);
+      __builtin_nontemporal_store(ov, reinterpret_cast<u32x4_t*>(out + (int64_t)i * C));
+#pragma unroll
+      for (int e = 0; e < 4; ++e) q = dot2_bf16(ov[e], ov[e], q);
+    } else {
+      store_pack_nt<XT, V>(out + (int64_t)i * C, o);
+    }
   }
   if constexpr (SSQ) {
     q = row16_sum(q);
@@ -226,13 +233,7 @@ __global__ __launch_bounds__(256) void post_n16_kernel(PostArgs a) {
       for (int k = 0; k < 4; ++k) o[k] = __fadd_rn(r[k], rnd<__bf16>(__fmul_rn(hp[i], fl[k])));
       const u32x2_t ov = {pack_bf16x2(o[0], o[1]), pack_bf16x2(o[2], o[3])};
       __builtin_nontemporal_store(ov, reinterpret_cast<u32x2_t*>(out + (int64_t)i * C + c));
-      if constexpr (SSQ) {
-#pragma unroll
-        for (int k = 0; k < 4; ++k) {
-          const float st = rnd<__bf16>(o[k]);
-          q = fmaf(st, st, q);
-        }
-      }
+      if constexpr (SSQ) q = dot2_bf16(ov.y, ov.y, dot2_bf16(ov.x, ov.x, q));
     }
   }
   if constexpr (SSQ) {
@@ -306,15 +307,15 @@ __global__ __launch_bounds__(256) void post_n8_kernel(PostArgs a) {
         r = (k & 1) ? bf16hi(xv[i][k >> 1]) : bf16lo(xv[i][k >> 1]);
       }
       o[k] = __fadd_rn(r, rnd<__bf16>(__fmul_rn(hp, fl[k])));
-      if constexpr (SSQ) {
-        const float st = rnd<__bf16>(o[k]);
-        q = fmaf(st, st, q);
-      }
     }
     u32x4_t ov;
 #pragma unroll
     for (int e = 0; e < 4; ++e) ov[e] = pack_bf16x2(o[2 * e], o[2 * e + 1]);
     __builtin_nontemporal_store(ov, reinterpret_cast<u32x4_t*>(out + (int64_t)i * C));
+    if constexpr (SSQ) {  // squares of the stored pairs, exact products, fp32 sum
+#pragma unroll
+      for (int e = 0; e < 4; ++e) q = dot2_bf16(ov[e], ov[e], q);
+    }
   }
   if constexpr (SSQ) {
     q = row16_sum(q);
@@ -356,7 +357,7 @@ static hipError_t launch_vec(const PostArgs& a, hipStream_t s) {
   constexpr int V = 16 / sizeof(XT);
   const int64_t threads = a.M * (a.C / V);
   const dim3 grid((unsigned)((threads + 255) / 256));
-  if constexpr (V == 8 && N <= 4) {
+  if constexpr (std::is_same_v<XT, __bf16> && N <= 4) {
     if (a.out_ssq) {
       if (a.h_res)
         hipLaunchKernelGGL((post_vec_kernel<XT, FT, N, true, true>), grid, dim3(256), 0, s, a);
