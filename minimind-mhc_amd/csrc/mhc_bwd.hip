@@ -147,6 +147,13 @@ struct Chunk8<false> {
     c.v = buf_load16(r, off);
     return c;
   }
+  // The first K (4 or 2) elements at off, the others zero.
+  template <int K>
+  __device__ static Chunk8 load_first(__amdgpu_buffer_rsrc_t r, uint32_t off) {
+    Chunk8 c;
+    c.v = K == 4 ? buf_load8z(r, off) : buf_load4z(r, off);
+    return c;
+  }
   __device__ static float get(const Chunk8& c, int i) {
     return (i & 1) ? bf16hi(c.v.v[i >> 1]) : bf16lo(c.v.v[i >> 1]);
   }
@@ -172,6 +179,13 @@ struct Chunk8<true> {
     Chunk8 c;
     c.v[0] = buf_load16(r, off);
     c.v[1] = buf_load16(r, off == kBufOob ? kBufOob : off + 16u);
+    return c;
+  }
+  template <int K>
+  __device__ static Chunk8 load_first(__amdgpu_buffer_rsrc_t r, uint32_t off) {
+    Chunk8 c;
+    c.v[0] = K == 4 ? buf_load16(r, off) : buf_load8z(r, off);
+    c.v[1] = U32x4{{0u, 0u, 0u, 0u}};
     return c;
   }
   __device__ static float get(const Chunk8& c, int i) { return __uint_as_float(c.v[i >> 2].v[i & 3]); }
@@ -213,6 +227,11 @@ struct Chunk8<true> {
 template <int N, int MODE, int NW, int KJ, bool F32>
 __global__ __launch_bounds__(NW * 64) __attribute__((amdgpu_waves_per_eu(F32 ? 2 : 4))) void pre_bwd_mfma_kernel(PreBwdArgs a) {
   using XV = Chunk8<F32>;
+  // The tile's x chunks stay in registers from the gh sums to the g_x stores,
+  // except for fp32 at n = 8: 16-wave workgroups hold 128 VGPRs a lane and
+  // 12 fp32 chunks alone take 96 of them, so there each chunk is loaded where
+  // it is used (for its gh sum, and again with its phi operands for g_x).
+  constexpr bool XRES = !(F32 && N >= 8);
   constexpr uint32_t ES = F32 ? 4u : 2u;  // bytes of a stream / gradient / phi element
   constexpr int FD = MODE == kFull ? 2 * N + N * N : (MODE == kNoHres ? 2 * N : N);
   constexpr int KS = (FD + 31) / 32;  // 32-feature K-steps
@@ -245,13 +264,16 @@ __global__ __launch_bounds__(NW * 64) __attribute__((amdgpu_waves_per_eu(F32 ? 2
     ci = k < NCH ? k / NCB : 0;
     c0 = k < NCH ? (k - ci * NCB) * 32 : C;  // C: no columns (loads read zeros)
   };
-  XV xs[KJ];
-#pragma unroll
-  for (int j = 0; j < KJ; ++j) {
+  auto x_chunk = [&](int j) {
     int ci, c0;
     chunk(j, ci, c0);
     const bool ok = c0 + 8 * g < C;
-    xs[j] = XV::load(rx, ok ? (uint32_t)(r * NC + ci * C + c0 + 8 * g) * ES : kBufOob);
+    return XV::load(rx, ok ? (uint32_t)(r * NC + ci * C + c0 + 8 * g) * ES : kBufOob);
+  };
+  XV xs[XRES ? KJ : 1];
+  if constexpr (XRES) {
+#pragma unroll
+    for (int j = 0; j < KJ; ++j) xs[j] = x_chunk(j);
   }
   const float inv = r < valid ? a.inv_rms[t0 + r] : 0.f;
 
@@ -294,8 +316,14 @@ __global__ __launch_bounds__(NW * 64) __attribute__((amdgpu_waves_per_eu(F32 ? 2
     int ci, c0;
     chunk(j, ci, c0);
     const int col = c0 + 8 * (r >> 2) + 4 * h + (r & 3);
-    const bool ok = col < C && 32 * ks + 8 * g < FD;
-    return XV::load(rphi, ok ? (uint32_t)((ci * C + col) * FD + 32 * ks + 8 * g) * ES : kBufOob);
+    if constexpr (FD % 8 == 0) {
+      const bool ok = col < C && 32 * ks + 8 * g < FD;
+      return XV::load(rphi, ok ? (uint32_t)((ci * C + col) * FD + 32 * ks + 8 * g) * ES : kBufOob);
+    } else {  // FD in {2, 4} (MHCHead at n = 2, 4; no H_res at n = 2): the row's
+              // FD features go to lane group 0, zeros elsewhere
+      const bool ok = col < C && g == 0;
+      return XV::template load_first<FD>(rphi, ok ? (uint32_t)((ci * C + col) * FD) * ES : kBufOob);
+    }
   };
 
   // ---- gh partials per chunk: sum_c g_sub[c] * x[i][c].  The g_sub loads go
@@ -305,18 +333,20 @@ __global__ __launch_bounds__(NW * 64) __attribute__((amdgpu_waves_per_eu(F32 ? 2
 #pragma unroll
   for (int j0 = 0; j0 < KJ; j0 += GB) {
     XV gvb[GB];
+    XV xvb[XRES ? 1 : GB];
 #pragma unroll
     for (int u = 0; u < GB; ++u) {
       int ci, c0;
       chunk(j0 + u, ci, c0);
       const bool ok = j0 + u < KJ && c0 + 8 * g < C;
       gvb[u] = XV::load(rgs, ok ? (uint32_t)(r * C + c0 + 8 * g) * ES : kBufOob);
+      if constexpr (!XRES) xvb[u] = j0 + u < KJ ? x_chunk(j0 + u) : XV::load(rx, kBufOob);
     }
 #pragma unroll
     for (int u = 0; u < GB; ++u) {
       const int j = j0 + u;
       if (j >= KJ) break;
-      const float acc = XV::dot(gvb[u], xs[j]);
+      const float acc = XV::dot(gvb[u], XRES ? xs[j] : xvb[u]);
       const float a16 = acc + xor_lane16(acc);
       const float a32 = a16 + xor_lane32(a16);
       if (g == 0) s_gp[wave + NW * j][r] = a32;
@@ -404,6 +434,7 @@ __global__ __launch_bounds__(NW * 64) __attribute__((amdgpu_waves_per_eu(F32 ? 2
   struct ChunkIn {
     XV av[2][KS];
     XV gv;
+    XV xv[XRES ? 1 : 1];  // the chunk's x when it is not held from the start
   };
   auto load_chunk = [&](int j, ChunkIn& in) {
     int ci, c0;
@@ -414,8 +445,10 @@ __global__ __launch_bounds__(NW * 64) __attribute__((amdgpu_waves_per_eu(F32 ? 2
       for (int ks = 0; ks < KS; ++ks) in.av[h][ks] = phi_op(j, h, ks);
     const bool ok = c0 + 8 * g < C;
     in.gv = XV::load(rgs, ok ? (uint32_t)(r * C + c0 + 8 * g) * ES : kBufOob);
+    if constexpr (!XRES) in.xv[0] = x_chunk(j);
   };
-  constexpr int PD = PF ? (KJ <= 12 ? 4 : 2) : 1;  // 16 chunks a wave: four sets would spill
+  // 16 chunks a wave, or x streamed with the chunk: four sets would spill
+  constexpr int PD = PF ? (KJ <= 12 && XRES ? 4 : 2) : 1;
   ChunkIn cin[PD];
   if constexpr (PF) {
 #pragma unroll
@@ -455,12 +488,15 @@ __global__ __launch_bounds__(NW * 64) __attribute__((amdgpu_waves_per_eu(F32 ? 2
       d2[h] = d;
     }
     const XV gv = PF || CH ? cur.gv : XV::load(rgs, ok ? (uint32_t)(r * C + c0 + 8 * g) * ES : kBufOob);
+    XV xj;
+    if constexpr (XRES) xj = xs[j];
+    else xj = PF || CH ? cur.xv[0] : x_chunk(j);
     const float hp = s_hp[r][ci];
     float v[8];
 #pragma unroll
     for (int cc = 0; cc < 8; ++cc) {  // column 8g + cc
       const float gx = d2[cc >> 2][cc & 3];
-      v[cc] = inv * (gx - XV::get(xs[j], cc) * inv * mean) + hp * XV::get(gv, cc);
+      v[cc] = inv * (gx - XV::get(xj, cc) * inv * mean) + hp * XV::get(gv, cc);
     }
     // whole offset in the vector offset, scalar offset the literal 0 (a
     // 128-bit store reads its data registers after issue)
@@ -502,8 +538,9 @@ static bool pre_bwd_mfma_ok(const PreBwdArgs& a) {
   if (a.mode == kRms) return false;
   const bool bf = a.x_dtype == kBF16 && a.phi_dtype == kBF16 && a.grad_dtype == kBF16;
   const bool f32 = a.x_dtype == kF32 && a.phi_dtype == kF32 && a.grad_dtype == kF32;
-  if (!(bf && (a.n == 2 || a.n == 4 || a.n == 8)) && !(f32 && (a.n == 2 || a.n == 4))) return false;
-  if (mode_fd(a.mode, a.n) % 8 != 0) return false;
+  if (!((bf || f32) && (a.n == 2 || a.n == 4 || a.n == 8))) return false;
+  const int fd = mode_fd(a.mode, a.n);
+  if (fd % 8 != 0 && fd != 4 && fd != 2) return false;  // whole 8-feature operands, or one short one
   if (a.C % 8 != 0 || a.C > 32 * kMfmaMaxColBlocks) return false;
   if ((int64_t)a.n * a.C * mode_fd(a.mode, a.n) * dtype_bytes(a.x_dtype) > 0x7fffffffLL) return false;
   return al(a.x) && al(a.phi) && al(a.g_x) && (a.g_sub == nullptr || al(a.g_sub));
@@ -514,9 +551,7 @@ static hipError_t launch_pre_bwd_mfma_n(const PreBwdArgs& a, hipStream_t s) {
   switch (a.mode) {
     case kFull: return launch_pre_bwd_mfma_mode<N, kFull, F32>(a, s);
     case kNoHres: return launch_pre_bwd_mfma_mode<N, kNoHres, F32>(a, s);
-    case kHead:
-      if constexpr (N == 8) return launch_pre_bwd_mfma_mode<N, kHead, F32>(a, s);
-      return hipErrorInvalidValue;
+    case kHead: return launch_pre_bwd_mfma_mode<N, kHead, F32>(a, s);
     default: return hipErrorInvalidValue;
   }
 }
@@ -527,6 +562,7 @@ hipError_t launch_pre_bwd(const PreBwdArgs& a, hipStream_t s) {
       switch (a.n) {
         case 2: return launch_pre_bwd_mfma_n<2, true>(a, s);
         case 4: return launch_pre_bwd_mfma_n<4, true>(a, s);
+        case 8: return launch_pre_bwd_mfma_n<8, true>(a, s);
         default: break;
       }
     } else {

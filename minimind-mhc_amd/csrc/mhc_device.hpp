@@ -80,6 +80,15 @@ __device__ __forceinline__ void st16_nt(void* p, const U32x4& v) {
 __device__ __forceinline__ U32x4 buf_load16(__amdgpu_buffer_rsrc_t r, uint32_t off) {
   return __builtin_bit_cast(U32x4, __builtin_amdgcn_raw_buffer_load_b128(r, (int)off, 0, 0));
 }
+// 8 / 4 bytes at off into the first dwords of a 16-byte value, the rest zero.
+__device__ __forceinline__ U32x4 buf_load8z(__amdgpu_buffer_rsrc_t r, uint32_t off) {
+  typedef unsigned int u32x2_v __attribute__((ext_vector_type(2)));
+  const u32x2_v v = __builtin_bit_cast(u32x2_v, __builtin_amdgcn_raw_buffer_load_b64(r, (int)off, 0, 0));
+  return U32x4{{v.x, v.y, 0u, 0u}};
+}
+__device__ __forceinline__ U32x4 buf_load4z(__amdgpu_buffer_rsrc_t r, uint32_t off) {
+  return U32x4{{__builtin_amdgcn_raw_buffer_load_b32(r, (int)off, 0, 0), 0u, 0u, 0u}};
+}
 
 __device__ __forceinline__ void buf_store16(__amdgpu_buffer_rsrc_t r, uint32_t off, const U32x4& v) {
   __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(u32x4_t, v), r, (int)off, 0, 0);

@@ -157,9 +157,11 @@ def _pre_case(dev, kind, n, C, M, dtype, seed):
 
 
 @pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
-# n = 16: FD = 288 features, more than a 256-thread workgroup has threads
+# n = 16: FD = 288 features, more than a 256-thread workgroup has threads;
+# n = 8 fp32: the MFMA kernel with x streamed per chunk (C = 768, 1024)
 @pytest.mark.parametrize("n,C,M", [(4, 64, 24), (4, 768, 300), (2, 100, 17), (8, 768, 40),
-                                   (1, 64, 9), (4, 256, 1100), (16, 64, 20), (16, 256, 300)])
+                                   (1, 64, 9), (4, 256, 1100), (16, 64, 20), (16, 256, 300),
+                                   (8, 1024, 70)])
 def test_pre_full_bwd_vs_oracle(dev, dtype, n, C, M):
     """g_x, g_phi, alphas and biases of the full pre phase for given upstream
     gradients of (sublayer_in, h_pre, h_post, h_res_raw)."""
@@ -190,8 +192,10 @@ def test_pre_full_bwd_vs_oracle(dev, dtype, n, C, M):
         assert maxrel(pr[f"bias_{seg}"].grad.reshape(-1), g_b[i]) <= bar, seg
 
 
+# n = 2: FD = 4 (one short phi operand on the MFMA kernel); n = 8 fp32: x
+# streamed per chunk
 @pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
-@pytest.mark.parametrize("n,C,M", [(4, 64, 24), (8, 768, 33), (2, 96, 700)])
+@pytest.mark.parametrize("n,C,M", [(4, 64, 24), (8, 768, 33), (2, 96, 700), (8, 512, 300)])
 def test_pre_nohres_bwd_vs_oracle(dev, dtype, n, C, M):
     x, p, pd, inv, mixes, g = _pre_case(dev, "nohres", n, C, M, dtype, 5 * n + C + M)
     ups = [torch.randn(1, M, C, generator=g).to(dtype), None,
@@ -217,8 +221,10 @@ def test_pre_nohres_bwd_vs_oracle(dev, dtype, n, C, M):
         assert maxrel(pr[f"bias_{seg}"].grad, g_b[i]) <= bar, seg
 
 
+# n = 4 / 2: FD = 4 / 2 (a short phi operand on the MFMA kernel)
 @pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
-@pytest.mark.parametrize("n,C,M", [(4, 64, 24), (1, 768, 50), (8, 768, 300)])
+@pytest.mark.parametrize("n,C,M", [(4, 64, 24), (1, 768, 50), (8, 768, 300), (4, 768, 300),
+                                   (2, 256, 70), (4, 200, 33)])
 def test_head_bwd_vs_oracle(dev, dtype, n, C, M):
     kind = "head"
     x, p, pd, inv, mixes, g = _pre_case(dev, kind, n, C, M, dtype, 3 * n + C + M)
