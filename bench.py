@@ -338,9 +338,9 @@ def bench_backward(reps: int = 20, sets: int = 4, n: int = N_STREAMS, M: int = T
         e1.record()
         _sync()
         ms = e0.elapsed_time(e1) / (reps * sets)
-        gbs = nbytes[name] / (ms * 1e-3) / 1e9
+        gbs = nbytes["pre" if name == "pre_valu" else name] / (ms * 1e-3) / 1e9
         out[name] = {"ms": round(ms, 5), "GBps": round(gbs, 1), "frac": round(gbs / HBM_PEAK_GBS, 4),
-                     "algorithmic_bytes": nbytes[name]}
+                     "algorithmic_bytes": nbytes["pre" if name == "pre_valu" else name]}
     out["total_ms"] = round(sum(v["ms"] for v in out.values()), 5)
     out["note"] = ("timings include each launch's own small torch allocations (outputs, "
                    "workspace); the weights entry is two launches (partials + reduction)")
@@ -403,6 +403,11 @@ def bench_layout32(reps: int = 10, sets: int = 4, n: int = N_STREAMS, M: int = T
         "pre": lambda s: _ops.pre_full(s["x"].view(1, M, n * C), phi, packed, a, b0, a, b0, a, br,
                                        n, C, 2.0, 1e-6, 1e-6, ITERS, 1e-6, want_raw=True,
                                        want_saved=True),
+        # the same launch without the phi image: the VALU kernel (one workgroup
+        # per token) the MFMA kernels replace for fp32 streams
+        "pre_valu": lambda s: _ops.pre_full(s["x"].view(1, M, n * C), phi, None, a, b0, a, b0, a,
+                                            br, n, C, 2.0, 1e-6, 1e-6, ITERS, 1e-6, want_raw=True,
+                                            want_saved=True),
         "post": lambda s: _ops.post(s["x"], s["o"]["h_res"], s["o"]["h_post"], s["f"], n, C),
         "post_bwd": lambda s: _ops.post_bwd(s["x"], s["o"]["h_res"], s["o"]["h_post"], s["f"], n,
                                             C, s["gout"]),
@@ -431,9 +436,9 @@ def bench_layout32(reps: int = 10, sets: int = 4, n: int = N_STREAMS, M: int = T
         e1.record()
         _sync()
         ms = e0.elapsed_time(e1) / (reps * sets)
-        gbs = nbytes[name] / (ms * 1e-3) / 1e9
+        gbs = nbytes["pre" if name == "pre_valu" else name] / (ms * 1e-3) / 1e9
         out[name] = {"ms": round(ms, 5), "GBps": round(gbs, 1), "frac": round(gbs / HBM_PEAK_GBS, 4),
-                     "algorithmic_bytes": nbytes[name]}
+                     "algorithmic_bytes": nbytes["pre" if name == "pre_valu" else name]}
     fwd = out["pre"]["ms"] + out["post"]["ms"]
     bwd = sum(out[k]["ms"] for k in ("post_bwd", "sinkhorn_bwd", "pre_bwd", "pre_bwd_weights"))
     out["fwd_ms"] = round(fwd, 5)
@@ -441,6 +446,14 @@ def bench_layout32(reps: int = 10, sets: int = 4, n: int = N_STREAMS, M: int = T
     out["fwd_tokens_per_s"] = round(M / (fwd * 1e-3), 1)
     out["config"] = (f"{M} tokens, n={n}, C={C}: x / phi / gates / stream gradients fp32, "
                      "F and its gradient bf16 (autocast)")
+    return out
+
+
+def layout32_c5():
+    """bench_layout32 at config 5's connection shape (n = 8, 8192 tokens)."""
+    out = bench_layout32(n=8, M=8192)
+    out["config"] = ("C5 shape: 8192 tokens, n=8, C=768: x / phi / gates / stream gradients "
+                     "fp32, F and its gradient bf16 (autocast)")
     return out
 
 
@@ -896,7 +909,8 @@ def main():
         traffic_passes(args.vector_pre, args.mfma_kernels)
         return
     if args.section == "fp32-layout":
-        print(json.dumps({"fp32_layout": bench_layout32()}), flush=True)
+        print(json.dumps({"fp32_layout": bench_layout32(), "fp32_layout_c5": layout32_c5()}),
+              flush=True)
         return
     if args.section == "backward":
         bw5 = bench_backward(n=8, M=8192)
@@ -985,6 +999,7 @@ def main():
     bw5["config"] = "C5 shape: 8192 tokens, n=8, C=768, bf16"
     line["backward_c5"] = bw5
     line["fp32_layout"] = bench_layout32()
+    line["fp32_layout_c5"] = layout32_c5()
     line["other_configs"] = isolated_configs(max(10, args.steps // 2), max(3, args.warmup // 2))
     line["reference_bench_shapes"] = reference_bench_shapes()
     if not args.no_e2e:

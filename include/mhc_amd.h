@@ -85,8 +85,11 @@ int mhc_phi_pack(const void* phi, int phi_dtype, void* packed, int n, int C, int
 
 /*
  * Size in bytes of the split-operand image of an fp32 phi for (n, C, mode), or
- * 0 when that shape has no fp32 MFMA kernel (n not in {1,2,4}, C % 8 != 0,
- * C > 1024, or MHCHead with n == 1).  Host-only, no device work.
+ * 0 when that shape has no fp32 MFMA kernel.  Shapes with one: n in {1,2,4}
+ * with C <= 1024 (16-column tiles of hi | lo pairs, one-workgroup-per-tile
+ * kernel), n == 8 at any C and n in {2,4} with C > 1024 (the bf16 K-streamed
+ * image twice, hi then lo); C % 8 == 0 and not MHCHead with n == 1 for all.
+ * n == 16 has none.  Host-only, no device work.
  * No reference counterpart: the reference's fused kernel computes the fp32
  * projection elementwise (model/mhc_fused.py:217-230); this build runs it as
  * bf16 MFMAs on hi / lo splits of both operands.

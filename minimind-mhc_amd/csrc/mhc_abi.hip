@@ -72,9 +72,11 @@ int run_pre(mhc::PreArgs& a, hipStream_t stream, const char* fn) {
                          aligned16(a.phi_packed);
   const bool mfma = packed_ok && mhc::mfma_supported(a.x_dtype, a.phi_dtype, a.n, a.C, a.mode);
   const bool split = packed_ok && !a.norm_w && mhc::split_supported(a.x_dtype, a.phi_dtype, a.n, a.C, a.mode);
-  if (!mfma && !split) a.phi_packed = nullptr;
+  const bool ks32 = packed_ok && mhc::ks32_supported(a.x_dtype, a.phi_dtype, a.n, a.C, a.mode);
+  if (!mfma && !split && !ks32) a.phi_packed = nullptr;
   if (!mfma || !mhc::ssq_used(a.n, a.C)) a.x_ssq = nullptr;
   if (split) return hip_status(mhc::launch_pre_split(a, mhc::device_cus(), stream), fn);
+  if (ks32) return hip_status(mhc::launch_pre_kstream_f32(a, stream), fn);
   return hip_status(mfma ? mhc::launch_pre_mfma(a, stream) : mhc::launch_pre_generic(a, stream), fn);
 }
 
@@ -196,16 +198,21 @@ int mhc_phi_pack(const void* phi, int phi_dtype, void* packed, int n, int C, int
   return hip_status(mhc::launch_phi_pack(phi, phi_dtype, packed, n, C, mode, stream), "mhc_phi_pack");
 }
 
-int64_t mhc_phi_split_bytes(int n, int C, int mode) { return mhc::split_packed_bytes(n, C, mode); }
+int64_t mhc_phi_split_bytes(int n, int C, int mode) {
+  const int64_t b = mhc::split_packed_bytes(n, C, mode);
+  return b > 0 ? b : mhc::ks32_packed_bytes(n, C, mode);
+}
 
 int mhc_phi_pack_split(const void* phi, int phi_dtype, void* packed, int n, int C, int mode,
                        hipStream_t stream) {
-  const int64_t bytes = mhc::split_packed_bytes(n, C, mode);
-  if (bytes <= 0)
+  const bool split = mhc::split_packed_bytes(n, C, mode) > 0;
+  if (!split && mhc::ks32_packed_bytes(n, C, mode) <= 0)
     return fail(hipErrorInvalidValue, "mhc_phi_pack_split: no split layout for n=%d C=%d mode=%d", n, C, mode);
   if (!dtype_ok(phi_dtype)) return fail(hipErrorInvalidValue, "mhc_phi_pack_split: bad phi dtype %d", phi_dtype);
   if (!phi || !packed) return fail(hipErrorInvalidValue, "mhc_phi_pack_split: null pointer");
-  return hip_status(mhc::launch_phi_pack_split(phi, phi_dtype, packed, n, C, mode, stream), "mhc_phi_pack_split");
+  return hip_status(split ? mhc::launch_phi_pack_split(phi, phi_dtype, packed, n, C, mode, stream)
+                          : mhc::launch_phi_pack_ks32(phi, phi_dtype, packed, n, C, mode, stream),
+                    "mhc_phi_pack_split");
 }
 
 static int pre_full(const void* x, int x_dtype, const void* phi, int phi_dtype,

@@ -183,7 +183,14 @@ hipError_t launch_sinkhorn(const void* in, void* out, int dtype, int64_t batch, 
 hipError_t launch_stream_expand(const void* x, void* out, int elem_bytes, int64_t M, int n,
                                 int C, hipStream_t s);
 hipError_t launch_phi_pack(const void* phi, int phi_dtype, void* packed, int n, int C, int mode,
-                           hipStream_t s);
+                           hipStream_t s, int lo = 0);
+// fp32 stream and phi on the K-streamed kernel (n = 8; n in {2, 4} past
+// C = 1024): image = packed bf16(phi), then packed phi - bf16(phi).
+int64_t ks32_packed_bytes(int n, int C, int mode);
+bool ks32_supported(int x_dtype, int phi_dtype, int n, int C, int mode);
+hipError_t launch_phi_pack_ks32(const void* phi, int phi_dtype, void* packed, int n, int C, int mode,
+                                hipStream_t s);
+hipError_t launch_pre_kstream_f32(const PreArgs& a, hipStream_t s);
 
 // Per-row sums of squares handed from the kernel that writes a stream to the
 // pre kernel that reads it: one fp32 partial per kSsqCols columns of C (for

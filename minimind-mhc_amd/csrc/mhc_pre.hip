@@ -19,9 +19,12 @@ namespace mhc {
 //     phi[i*C + cb*32 + (lane/16)*8 + s, nt*16 + lane%16]   (0 outside [C, FD))
 // so that lane `lane` of the wave reading column block cb of stream i finds its
 // MFMA B operand (8 consecutive k for output column lane%16) as one 16-byte load.
+// lo: the image of phi - bf16(phi) instead (the low half of an fp32 phi split
+// into bf16 hi + lo operands for the fp32 K-streamed kernel).
 __global__ __launch_bounds__(256) void phi_pack_kernel(const void* __restrict__ phi, int dt,
                                                        uint16_t* __restrict__ packed, int C,
-                                                       int FD, int NCB, int NT, int64_t total) {
+                                                       int FD, int NCB, int NT, int64_t total,
+                                                       int lo) {
   const int64_t idx = (int64_t)blockIdx.x * 256 + threadIdx.x;
   if (idx >= total) return;
   const int s = (int)(idx & 7);
@@ -35,7 +38,8 @@ __global__ __launch_bounds__(256) void phi_pack_kernel(const void* __restrict__ 
   const int f = nt * 16 + (lane & 15);
   float v = 0.f;
   if (c < C && f < FD) v = ld_any(phi, ((int64_t)i * C + c) * FD + f, dt);
-  packed[idx] = f32_to_bf16_bits(v);
+  const uint16_t hi = f32_to_bf16_bits(v);
+  packed[idx] = lo ? f32_to_bf16_bits(v - bf16_bits_to_f32(hi)) : hi;
 }
 
 // MFMA kernels: n in {1, 2, 4, 8} at C <= 1024 (register-resident phi for
@@ -65,15 +69,46 @@ bool mfma_supported(int x_dtype, int phi_dtype, int n, int C, int mode) {
 }
 
 hipError_t launch_phi_pack(const void* phi, int phi_dtype, void* packed, int n, int C, int mode,
-                           hipStream_t s) {
+                           hipStream_t s, int lo) {
   const int fd = mode_fd(mode, n);
   const int nt = (fd + 15) / 16;
   const int ncb = (C + kCBlock - 1) / kCBlock;
   const int64_t total = (int64_t)n * ncb * nt * 64 * 8;
   const int64_t blocks = (total + 255) / 256;
   hipLaunchKernelGGL(phi_pack_kernel, dim3((unsigned)blocks), dim3(256), 0, s, phi, phi_dtype,
-                     static_cast<uint16_t*>(packed), C, fd, ncb, nt, total);
+                     static_cast<uint16_t*>(packed), C, fd, ncb, nt, total, lo);
   return hipGetLastError();
+}
+
+// fp32 stream and phi on the K-streamed kernel: n = 8 at any C and n in {2, 4}
+// past C = 1024 (narrower fp32 rows at n <= 4 take the split kernel).  Its
+// image is the packed bf16 layout of bf16(phi) followed by that of
+// phi - bf16(phi).
+int64_t ks32_packed_bytes(int n, int C, int mode) {
+  if (!(n == 8 || ((n == 2 || n == 4) && (C + kCBlock - 1) / kCBlock > kMfmaMaxColBlocks))) return 0;
+  const int64_t one = mfma_packed_bytes(n, C, mode);
+  return one > 0 && 2 * one <= 0x7fffffffLL ? 2 * one : 0;
+}
+
+bool ks32_supported(int x_dtype, int phi_dtype, int n, int C, int mode) {
+  return x_dtype == kF32 && phi_dtype == kF32 && ks32_packed_bytes(n, C, mode) > 0;
+}
+
+hipError_t launch_phi_pack_ks32(const void* phi, int phi_dtype, void* packed, int n, int C, int mode,
+                                hipStream_t s) {
+  const hipError_t e = launch_phi_pack(phi, phi_dtype, packed, n, C, mode, s, 0);
+  if (e != hipSuccess) return e;
+  return launch_phi_pack(phi, phi_dtype, static_cast<unsigned char*>(packed) + mfma_packed_bytes(n, C, mode),
+                         n, C, mode, s, 1);
+}
+
+hipError_t launch_pre_kstream_f32(const PreArgs& a, hipStream_t s) {
+  switch (a.n) {
+    case 2: return launch_pre_kstream_n2(a, s);
+    case 4: return launch_pre_kstream_n4(a, s);
+    case 8: return launch_pre_kstream_n8(a, s);
+    default: return hipErrorInvalidValue;
+  }
 }
 
 // ------------------------------------------------------ process-wide settings

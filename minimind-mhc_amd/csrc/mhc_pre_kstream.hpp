@@ -151,16 +151,28 @@ __device__ __forceinline__ float ks_token_sum(float q) {
   return q;
 }
 
-template <int N, int MODE, bool NORM>
+// F32: fp32 stream and phi (the reference trainers' layout).  x_norm = x *
+// inv_rms stays fp32 (the reference rounds it to the stream dtype) and is split
+// into bf16 hi + lo MFMA operands, phi likewise (phi_packed holds the hi image
+// of the packed layout, then the lo image); three products per pair (hi.hi,
+// hi.lo, lo.hi) keep ~16 significant bits of each operand.  Gates, Sinkhorn
+// output and the pre-aggregate are fp32 (products rounded, summed in stream
+// order); the pre-aggregate items are 4-column chunks.  No fused norm (a
+// second launch normalises in place).
+template <int N, int MODE, bool NORM, bool F32 = false>
 __global__ __launch_bounds__(kKsWaves * 64) void pre_kstream_kernel(PreArgs a) {
   using P = KsPlan<N, MODE>;
   using GP = GateParams<N>;
   using NS = KsNorm<N, MODE, NORM>;
+  static_assert(!(F32 && NORM), "fp32 streams: the norm runs as a second launch");
   constexpr int FD = P::FD;
   constexpr int NT = P::NT;
   constexpr int NTW = P::NTW;
   constexpr int TM = P::TM;
-  constexpr int D = P::D;
+  constexpr int D = F32 ? 2 : P::D;      // chunks in flight (fp32: hi and lo phi operands)
+  constexpr int XQ = F32 ? 2 : 1;        // 16-byte loads per 8 columns of a row
+  constexpr uint32_t ES = F32 ? 4u : 2u; // bytes per stream element
+  constexpr int XDT = F32 ? kF32 : kBF16;
   constexpr int LPT = P::LPT;
   constexpr int SKV = P::SKV;
   constexpr int T = P::WAVES * 64;
@@ -206,23 +218,29 @@ __global__ __launch_bounds__(kKsWaves * 64) void pre_kstream_kernel(PreArgs a) {
   }
 
   // ---- K loop -----------------------------------------------------------
-  const auto rx = make_rsrc(static_cast<const uint16_t*>(a.x) + t0 * NC, (uint32_t)valid * NC * 2u);
-  const auto rw = make_rsrc(a.phi_packed, (uint32_t)(NCH * NT) * 1024u);
-  const uint32_t xrow = (uint32_t)(r * NC) * 2u + (uint32_t)g * 16u;
-  const uint32_t xblk = (uint32_t)(16 * NC) * 2u;  // offset of M-block 1
+  const auto rx = make_rsrc(static_cast<const unsigned char*>(a.x) + t0 * NC * ES,
+                            (uint32_t)valid * NC * ES);
+  const uint32_t wimg = (uint32_t)(NCH * NT) * 1024u;  // bytes of one packed image
+  const auto rw = make_rsrc(a.phi_packed, F32 ? 2u * wimg : wimg);
+  const uint32_t xrow = (uint32_t)(r * NC) * ES + (uint32_t)g * 8u * ES;
+  const uint32_t xblk = (uint32_t)(16 * NC) * ES;  // offset of M-block 1
   // x chunk k of every M-block (zeros past the row or past C).
-  auto x_chunk = [&](int k, bool live, U32x4 (&xd)[P::MB]) {
+  auto x_chunk = [&](int k, bool live, U32x4 (&xd)[P::MB][XQ]) {
     const int i = live ? k / NCB : 0;
     const int cb = live ? k - i * NCB : 0;
     const int c0 = cb * kCBlock;
     const bool xl = live && c0 + g * 8 < C;
 #pragma unroll
     for (int m = 0; m < P::MB; ++m)
-      xd[m] = __builtin_bit_cast(U32x4, __builtin_amdgcn_raw_buffer_load_b128(
-                                            rx, (int)(xl ? xrow + m * xblk : kBufOob), (i * C + c0) * 2, 0));
+#pragma unroll
+      for (int q = 0; q < XQ; ++q)
+        xd[m][q] = __builtin_bit_cast(U32x4, __builtin_amdgcn_raw_buffer_load_b128(
+                                                 rx, (int)(xl ? xrow + m * xblk + 16u * q : kBufOob),
+                                                 (int)((i * C + c0) * ES), 0));
   };
-  U32x4 xs[D][P::MB];
+  U32x4 xs[D][P::MB][XQ];
   U32x4 ws[D][NTW];
+  U32x4 wl[F32 ? D : 1][NTW];  // lo phi operands (fp32)
   // Workgroups walk their chunks in rotated orders, so the CUs of an XCD do
   // not all read the same few phi lines from the same L2 channels at once.
   // Slot j of this wave is chunk kq + KS * ((j + rot) mod NJ); slots past NJ
@@ -237,20 +255,23 @@ __global__ __launch_bounds__(kKsWaves * 64) void pre_kstream_kernel(PreArgs a) {
     live = slot_j < NJ && k < NCH;
     return k;
   };
-  auto issue = [&](int slot_j, U32x4 (&xd)[P::MB], U32x4 (&wd)[NTW]) {
+  auto issue = [&](int slot_j, U32x4 (&xd)[P::MB][XQ], U32x4 (&wd)[NTW], U32x4 (&wdl)[NTW]) {
     bool live;
     const int k = chunk_of(slot_j, live);
     x_chunk(k, live, xd);
 #pragma unroll
     for (int nt = 0; nt < NTW; ++nt) {
       const int ntg = nh * NTW + nt;
+      const int voff = (int)(live && ntg < NT ? (uint32_t)lane * 16u : kBufOob);
       wd[nt] = __builtin_bit_cast(U32x4, __builtin_amdgcn_raw_buffer_load_b128(
-                                             rw, (int)(live && ntg < NT ? (uint32_t)lane * 16u : kBufOob),
-                                             (k * NT + ntg) * 1024, 0));
+                                             rw, voff, (k * NT + ntg) * 1024, 0));
+      if constexpr (F32)
+        wdl[nt] = __builtin_bit_cast(U32x4, __builtin_amdgcn_raw_buffer_load_b128(
+                                                rw, voff, (int)(wimg + (uint32_t)(k * NT + ntg) * 1024u), 0));
     }
   };
 #pragma unroll
-  for (int d = 0; d < D; ++d) issue(d, xs[d], ws[d]);
+  for (int d = 0; d < D; ++d) issue(d, xs[d], ws[d], wl[F32 ? d : 0]);
 
   // ---- sums of squares, then each row's inv_rms --------------------------------
   // A first pass over this wave's chunks in the K loop's order (SD in flight;
@@ -269,7 +290,7 @@ __global__ __launch_bounds__(kKsWaves * 64) void pre_kstream_kernel(PreArgs a) {
       else if (tid < P::KS * TM) sh.ss[tid / TM][tid % TM] = 0.f;
     } else if (P::NH == 1 || nh == 0) {  // uniform
       for (int j0 = 0; j0 < NJ; j0 += P::SD) {  // uniform trip count
-        U32x4 v[P::SD][P::MB];
+        U32x4 v[P::SD][P::MB][XQ];
 #pragma unroll
         for (int d = 0; d < P::SD; ++d) {
           bool live;
@@ -281,7 +302,16 @@ __global__ __launch_bounds__(kKsWaves * 64) void pre_kstream_kernel(PreArgs a) {
 #pragma unroll
           for (int m = 0; m < P::MB; ++m)
 #pragma unroll
-            for (int q = 0; q < 4; ++q) ss[m] = dot2_bf16(v[d][m].v[q], v[d][m].v[q], ss[m]);
+            for (int xq = 0; xq < XQ; ++xq)
+#pragma unroll
+              for (int q = 0; q < 4; ++q) {
+                if constexpr (F32) {
+                  const float f = __uint_as_float(v[d][m][xq].v[q]);
+                  ss[m] = fmaf(f, f, ss[m]);
+                } else {
+                  ss[m] = dot2_bf16(v[d][m][xq].v[q], v[d][m][xq].v[q], ss[m]);
+                }
+              }
       }
 #pragma unroll
       for (int m = 0; m < P::MB; ++m) {
@@ -311,13 +341,35 @@ __global__ __launch_bounds__(kKsWaves * 64) void pre_kstream_kernel(PreArgs a) {
     for (int d = 0; d < D; ++d) {
 #pragma unroll
       for (int m = 0; m < P::MB; ++m) {
-        const bf16x8_t av = __builtin_bit_cast(bf16x8_t, x_norm_chunk(xs[d][m], inv_r[m]));
+        if constexpr (F32) {  // fp32 x_norm split into hi + lo bf16 operands
+          U32x4 h4, l4;
 #pragma unroll
-        for (int nt = 0; nt < NTW; ++nt)
-          acc[m][nt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(
-              av, __builtin_bit_cast(bf16x8_t, ws[d][nt]), acc[m][nt], 0, 0, 0);
+          for (int e = 0; e < 4; ++e) {
+            const float x0 = __uint_as_float(xs[d][m][e >> 1].v[2 * (e & 1)]) * inv_r[m];
+            const float x1 = __uint_as_float(xs[d][m][e >> 1].v[2 * (e & 1) + 1]) * inv_r[m];
+            const uint32_t hp = pack_bf16x2(x0, x1);
+            h4.v[e] = hp;
+            l4.v[e] = pack_bf16x2(x0 - bf16lo(hp), x1 - bf16hi(hp));
+          }
+          const bf16x8_t ah = __builtin_bit_cast(bf16x8_t, h4);
+          const bf16x8_t al = __builtin_bit_cast(bf16x8_t, l4);
+#pragma unroll
+          for (int nt = 0; nt < NTW; ++nt) {
+            const bf16x8_t bh = __builtin_bit_cast(bf16x8_t, ws[d][nt]);
+            acc[m][nt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(ah, bh, acc[m][nt], 0, 0, 0);
+            acc[m][nt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(
+                ah, __builtin_bit_cast(bf16x8_t, wl[F32 ? d : 0][nt]), acc[m][nt], 0, 0, 0);
+            acc[m][nt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(al, bh, acc[m][nt], 0, 0, 0);
+          }
+        } else {
+          const bf16x8_t av = __builtin_bit_cast(bf16x8_t, x_norm_chunk(xs[d][m][0], inv_r[m]));
+#pragma unroll
+          for (int nt = 0; nt < NTW; ++nt)
+            acc[m][nt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(
+                av, __builtin_bit_cast(bf16x8_t, ws[d][nt]), acc[m][nt], 0, 0, 0);
+        }
       }
-      issue(j0 + d + D, xs[d], ws[d]);
+      issue(j0 + d + D, xs[d], ws[d], wl[F32 ? d : 0]);
     }
   }
   // MFMA 16x16 result layout: lane l holds D[4*(l/16) + j][l % 16], j = 0..3.
@@ -342,25 +394,28 @@ __global__ __launch_bounds__(kKsWaves * 64) void pre_kstream_kernel(PreArgs a) {
   // two register buffers: rounds 0 and 1 are issued here, round r + 2 as soon
   // as round r is consumed.  A round past the end reads nothing (offsets out
   // of the descriptor) and stores nothing.
+  // (fp32: 4-column items, the same 16 bytes of each stream per item)
   constexpr int PB = P::PB;
-  const int C8 = C / 8;
+  constexpr int CW = F32 ? 4 : 8;  // columns per item
+  const int C8 = C / CW;
   const int items = TM * C8;
   const int nrounds = (items + PB * T - 1) / (PB * T);
-  const auto rsub = make_rsrc(static_cast<uint16_t*>(a.sub_in) + t0 * C, (uint32_t)valid * C * 2u);
+  const auto rsub = make_rsrc(static_cast<unsigned char*>(a.sub_in) + t0 * C * ES,
+                              (uint32_t)valid * C * ES);
   auto pa_item = [&](int round, int b, int& tt, int& c) {
     const int p = (round * PB + b) * T + tid;
     tt = p < items ? p / C8 : TM;
-    c = tt < TM ? (p - tt * C8) * 8 : 0;
+    c = tt < TM ? (p - tt * C8) * CW : 0;
   };
   auto pa_issue = [&](int round, U32x4 (&xv)[PB][N]) {
 #pragma unroll
     for (int b = 0; b < PB; ++b) {
       int tt, c;
       pa_item(round, b, tt, c);
-      const uint32_t xo = tt < valid ? (uint32_t)(tt * NC + c) * 2u : kBufOob;
+      const uint32_t xo = tt < valid ? (uint32_t)(tt * NC + c) * ES : kBufOob;
 #pragma unroll
       for (int i = 0; i < N; ++i)
-        xv[b][i] = buf_load16_nt(rx, xo, i * C * 2);  // x's last use in this launch
+        xv[b][i] = buf_load16_nt(rx, xo, (int)(i * C * ES));  // x's last use in this launch
     }
   };
   auto pa_finish = [&](int round, const U32x4 (&xv)[PB][N]) {
@@ -369,6 +424,19 @@ __global__ __launch_bounds__(kKsWaves * 64) void pre_kstream_kernel(PreArgs a) {
       int tt, c;
       pa_item(round, b, tt, c);
       const int ts = tt < TM ? tt : 0;
+      if constexpr (F32) {  // products rounded to fp32, summed in stream order
+        U32x4 o;
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+          float acc = 0.f;
+#pragma unroll
+          for (int i = 0; i < N; ++i)
+            acc = __fadd_rn(acc, __fmul_rn(sh.hpre[ts][i], __uint_as_float(xv[b][i].v[e])));
+          o.v[e] = __float_as_uint(acc);
+        }
+        buf_store16_nt(rsub, tt < valid ? (uint32_t)(tt * C + c) * ES : kBufOob, o);
+        continue;
+      }
       uint32_t hlo[N];
       uint32_t hhi[N];
 #pragma unroll
@@ -383,7 +451,7 @@ __global__ __launch_bounds__(kKsWaves * 64) void pre_kstream_kernel(PreArgs a) {
       }
       // whole offset in the vector offset, scalar offset the literal 0 (see
       // persist_preagg: a 128-bit store reads its data registers after issue)
-      buf_store16_nt(rsub, tt < valid ? (uint32_t)(tt * C + c) * 2u : kBufOob, pk);
+      buf_store16_nt(rsub, tt < valid ? (uint32_t)(tt * C + c) * ES : kBufOob, pk);
     }
   };
   U32x4 xa[PB][N];
@@ -411,14 +479,14 @@ __global__ __launch_bounds__(kKsWaves * 64) void pre_kstream_kernel(PreArgs a) {
     if (ok && a.mixes_raw) a.mixes_raw[tk * FD + jl] = m;
     // bias_pre[j] and bias_post[j - N] are adjacent: GP::kBiasPre + j for both
     const bool pre = jl < N;
-    const float gs = gate_sigmoid(m, sh.prm[pre ? 0 : 1], sh.prm[GP::kBiasPre + jl], kBF16);
-    const float h = pre ? round_to(__fadd_rn(gs, a.pre_eps), kBF16)   // gate_pre
-                        : round_to(__fmul_rn(gs, a.post_mult), kBF16);  // gate_post
+    const float gs = gate_sigmoid(m, sh.prm[pre ? 0 : 1], sh.prm[GP::kBiasPre + jl], XDT);
+    const float h = pre ? round_to(__fadd_rn(gs, a.pre_eps), XDT)   // gate_pre
+                        : round_to(__fmul_rn(gs, a.post_mult), XDT);  // gate_post
     if (pre) {
       sh.hpre[tt][jl] = h;
-      if (ok && a.h_pre) st_any(a.h_pre, tk * N + jl, kBF16, h);
+      if (ok && a.h_pre) st_any(a.h_pre, tk * N + jl, XDT, h);
     } else if (ok) {
-      st_any(a.h_post, tk * N + (jl - N), kBF16, h);
+      st_any(a.h_post, tk * N + (jl - N), XDT, h);
     }
   }
   float v[SKV];
@@ -449,8 +517,8 @@ __global__ __launch_bounds__(kKsWaves * 64) void pre_kstream_kernel(PreArgs a) {
     for (int q = 0; q < SKV; ++q) {
       const float m = s[q];
       if (ok && own && a.mixes_raw) a.mixes_raw[tk * FD + 2 * N + e0 + q] = m;
-      v[q] = gate_res(m, sh.prm[2], sh.prm[GP::kBiasRes + e0 + q], kBF16);
-      if (ok && own && a.h_res_raw) st_any(a.h_res_raw, tk * P::G + e0 + q, kBF16, v[q]);
+      v[q] = gate_res(m, sh.prm[2], sh.prm[GP::kBiasRes + e0 + q], XDT);
+      if (ok && own && a.h_res_raw) st_any(a.h_res_raw, tk * P::G + e0 + q, XDT, v[q]);
     }
   }
   __syncthreads();  // h_pre visible to every lane's pre-aggregate items
@@ -476,7 +544,7 @@ __global__ __launch_bounds__(kKsWaves * 64) void pre_kstream_kernel(PreArgs a) {
   }
   if (sk && ok && own) {
 #pragma unroll
-    for (int q = 0; q < SKV; ++q) st_any(a.h_res, tk * P::G + e0 + q, kBF16, v[q]);
+    for (int q = 0; q < SKV; ++q) st_any(a.h_res, tk * P::G + e0 + q, XDT, v[q]);
   }
   if constexpr (NORM) {
     // RMSNorm over C: the token's LPT lanes sum the squares of the stashed
@@ -514,6 +582,19 @@ hipError_t launch_pre_kstream_inst(const PreArgs& a, hipStream_t s) {
   constexpr int TM = KsPlan<N, MODE>::TM;
   const int64_t tiles = (a.M + TM - 1) / TM;
   const dim3 block(KsPlan<N, MODE>::WAVES * 64);
+  if (a.x_dtype == kF32) {  // fp32 stream and phi: hi / lo operands, norm as a second launch
+    if constexpr (N != 16) {
+      PreArgs plain = a;
+      plain.norm_w = nullptr;
+      hipLaunchKernelGGL((pre_kstream_kernel<N, MODE, false, true>), dim3((unsigned)tiles), block, 0, s,
+                         plain);
+      const hipError_t e = hipGetLastError();
+      if (e != hipSuccess || !a.norm_w) return e;
+      return launch_expand_norm(a.sub_in, kF32, a.norm_w, a.norm_dtype, a.sub_in, a.M, 1, a.C,
+                                a.norm_eps, s);
+    }
+    return hipErrorInvalidValue;
+  }
   if (!a.norm_w) {
     hipLaunchKernelGGL((pre_kstream_kernel<N, MODE, false>), dim3((unsigned)tiles), block, 0, s, a);
     return hipGetLastError();

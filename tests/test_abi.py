@@ -74,11 +74,18 @@ def test_split_packed_sizes(lib):
     assert lib.mhc_phi_split_bytes(4, 768, 2) == 4 * 24 * 1 * 64 * 16   # FD 4
     assert lib.mhc_phi_split_bytes(2, 512, 0) == 2 * 16 * 1 * 64 * 16   # FD 8
     assert lib.mhc_phi_split_bytes(1, 200, 0) == 1 * 7 * 1 * 64 * 16    # FD 3, ragged C
-    assert lib.mhc_phi_split_bytes(8, 768, 0) == 0                      # no fp32 instance
+    # K-streamed fp32: the bf16 K-streamed image twice (hi, then lo)
+    assert lib.mhc_phi_split_bytes(8, 768, 0) == 2 * lib.mhc_phi_packed_bytes(8, 768, 0)
+    assert lib.mhc_phi_split_bytes(8, 768, 0) == 2 * 8 * 24 * 5 * 64 * 16   # FD 80 -> 5 tiles
+    assert lib.mhc_phi_split_bytes(8, 200, 2) == 2 * 8 * 7 * 1 * 64 * 16    # head FD 8
+    assert lib.mhc_phi_split_bytes(4, 2048, 0) == 2 * 4 * 64 * 2 * 64 * 16  # C > 1024
+    assert lib.mhc_phi_split_bytes(2, 1536, 1) == 2 * 2 * 48 * 1 * 64 * 16
+    assert lib.mhc_phi_split_bytes(16, 768, 0) == 0                     # no fp32 instance
+    assert lib.mhc_phi_split_bytes(1, 2048, 0) == 0
     assert lib.mhc_phi_split_bytes(4, 100, 0) == 0                      # C % 8 != 0
-    assert lib.mhc_phi_split_bytes(4, 2048, 0) == 0                     # C > 1024
+    assert lib.mhc_phi_split_bytes(8, 100, 0) == 0
     assert lib.mhc_phi_split_bytes(1, 768, 2) == 0                      # head n=1 is RMSNorm
-    rc = lib.mhc_phi_pack_split(None, 0, None, 8, 768, 0, None)
+    rc = lib.mhc_phi_pack_split(None, 0, None, 16, 768, 0, None)
     assert rc == 1 and b"no split layout" in lib.mhc_last_error()
 
 

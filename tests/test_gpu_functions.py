@@ -49,8 +49,9 @@ def test_pre_phase_full_fn_forward(dev, dtype, n, C, M):
         sub, h_pre, h_post, h_raw = _PrePhaseFullFn.apply(
             xd, pd["phi_weight"], *[pd[k] for k in ARGS], 2.0, 1e-6, 1e-6, n, C)
     packed = _ops.PhiPack(H.MODE_FULL).get(pd["phi_weight"], n, C)
-    # MFMA images: bf16 phi (any n), fp32 phi for n in {1, 2, 4} (the split kernel)
-    assert (packed is not None) == (dtype == torch.bfloat16 or n in (1, 2, 4))
+    # MFMA images: bf16 phi (any n), fp32 phi for n in {1, 2, 4} (the split
+    # kernel) and n = 8 (the K-streamed kernel on hi / lo images)
+    assert (packed is not None) == (dtype == torch.bfloat16 or n in (1, 2, 4, 8))
     o = _ops.pre_full(xd, pd["phi_weight"], packed, *[pd[k] for k in ARGS], n, C, 2.0, 1e-6,
                       1e-6, 0, 0.0, sinkhorn=False, want_h_pre=True, want_raw=True)
     # the same launch the modules make: bit for bit

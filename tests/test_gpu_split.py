@@ -90,6 +90,61 @@ def test_split_vs_oracle(n, C):
         assert maxrel(ref[0].reshape(got.shape), got) <= BAR, key
 
 
+# fp32 on the K-streamed kernel (hi / lo operands of x_norm and of phi, three
+# MFMA products): n = 8 at any C, n in {2, 4} past C = 1024; one tile, many
+# tiles per CU, ragged tiles, C not a multiple of 32 (200)
+KS32 = [(8, 768), (8, 512), (8, 200), (4, 2048), (2, 1536)]
+
+
+@pytest.mark.parametrize("kind", ["full", "nohres", "head"])
+@pytest.mark.parametrize("n,C", KS32)
+@pytest.mark.parametrize("M", [1, 33, 8192 + 7])
+def test_ks32_matches_fp32_valu_kernel(kind, n, C, M):
+    if M > 4096 and C > 768:
+        M = 3000  # the VALU reference takes one workgroup per token
+    x, p, pd, packed, dev = _case(kind, n, C, M, seed=77 * n + C + M)
+    print(f"ks32 {kind} n={n} C={C} M={M}", flush=True)
+    xd = x.to(dev)
+    got = _run(kind, xd, pd, packed, n, C)
+    ref = _run(kind, xd, pd, None, n, C)
+    assert got.keys() == ref.keys()
+    for k in ref:
+        assert maxrel(ref[k], got[k]) <= BAR, (k, maxrel(ref[k], got[k]))
+
+
+@pytest.mark.parametrize("n,C", [(8, 768), (4, 2048)])
+def test_ks32_vs_oracle(n, C):
+    M = 32 * 256 + 11
+    x, p, pd, packed, dev = _case("full", n, C, M, seed=5 + n)
+    o = _run("full", x.to(dev), pd, packed, n, C)
+    idx = torch.tensor([0, 1, 31, 32, 33, M // 2, M - 12, M - 1])
+    sub, h_pre, h_post, h_raw, inv, mixes = R.pre_full(x[:, idx], p, n, C)
+    h_res = R.sinkhorn(h_raw.float(), 20, 1e-6)
+    d = idx.to(dev)
+    for ref, key, shape in ((sub, "sub_in", (M, C)), (h_pre, "h_pre", (M, n)),
+                            (h_post, "h_post", (M, n)), (h_raw, "h_res_raw", (M, n * n)),
+                            (h_res, "h_res", (M, n * n)), (inv, "inv_rms", (M,)),
+                            (mixes, "mixes_raw", (M, 2 * n + n * n))):
+        got = o[key].reshape(shape)[d].cpu()
+        assert maxrel(ref[0].reshape(got.shape), got) <= BAR, key
+
+
+def test_ks32_norm_second_launch():
+    """The fused-norm entry point at fp32 n = 8: the K-streamed launch and an
+    in-place RMSNorm launch, against the plain launch normed by torch."""
+    n, C, M = 8, 768, 100
+    x, p, pd, packed, dev = _case("full", n, C, M, seed=9)
+    xd = x.to(dev)
+    w = (1 + 0.1 * torch.randn(C, generator=torch.Generator().manual_seed(1))).to(dev)
+    args = (pd["phi_weight"], packed, pd["alpha_pre"], pd["bias_pre"], pd["alpha_post"],
+            pd["bias_post"], pd["alpha_res"], pd["bias_res"], n, C, 2.0, 1e-6, 1e-6, 20, 1e-6)
+    plain = _ops.pre_full(xd, *args)
+    normed = _ops.pre_full(xd, *args, norm=(w, 1e-6))
+    ref = torch.nn.functional.rms_norm(plain["sub_in"], (C,), w, 1e-6)
+    assert maxrel(ref, normed["sub_in"]) <= 2e-6
+    assert torch.equal(plain["h_res"], normed["h_res"])
+
+
 @pytest.mark.parametrize("iters", [0, 1, 20])
 def test_split_sinkhorn_iterations(iters):
     n, C, M = 4, 768, 300
