@@ -347,6 +347,71 @@ def bench_backward(reps: int = 20, sets: int = 4, n: int = N_STREAMS, M: int = T
     return out
 
 
+def bench_head_backward(reps: int = 20, sets: int = 4, n: int = N_STREAMS, M: int = TOKENS):
+    """The MHCHead (the model's exit, FD = n) forward and its two backward
+    launches at C = 768, in bf16 and in the fp32 trainer layout (model/
+    mhc_common.py:311-400 forward; its autograd backward).  Bytes: forward
+    reads x (n*C), writes out (C) and the saved inv_rms / mixes; pre_bwd reads
+    x, g_out (C), inv_rms, mixes, phi, writes g_x (n*C) and g_raw; weights
+    reads x, inv_rms, mixes, g_raw, writes g_phi."""
+    import torch
+    from model import _hip as H, _ops
+
+    dev = torch.device("cuda:0")
+    C = C_DIM
+    out = {}
+    for tag, dt in (("bf16", torch.bfloat16), ("fp32", torch.float32)):
+        es = 2 if dt == torch.bfloat16 else 4
+        g = torch.Generator().manual_seed(7)
+        phi = (torch.randn(n * C, n, generator=g) * 0.02).to(dt).to(dev)
+        a = torch.tensor(0.01, dtype=dt, device=dev)
+        b = torch.zeros(n, dtype=dt, device=dev)
+        packed = _ops.PhiPack(H.MODE_HEAD).get(phi, n, C)
+        alphas, biases = (a, None, None), (b, None, None)
+        S = []
+        for _ in range(sets):
+            x = torch.randn(M, n * C, generator=g).to(dt).to(dev)
+            o, inv, mix = _ops.head(x.view(1, M, n * C), phi, packed, a, b, n, C, 1e-6, 1e-6,
+                                    want_saved=True)
+            go = torch.randn(M, C, generator=g).to(dt).to(dev)
+            _, graw = _ops.pre_bwd(x, phi, alphas, biases, inv, mix, n, C, H.MODE_HEAD, 0.0, 1e-6,
+                                   g_sub=go)
+            S.append(dict(x=x, inv=inv, mix=mix, go=go, graw=graw))
+        ops = {
+            "head_fwd": lambda s: _ops.head(s["x"].view(1, M, n * C), phi, packed, a, b, n, C, 1e-6,
+                                            1e-6, want_saved=True),
+            "pre_bwd": lambda s: _ops.pre_bwd(s["x"], phi, alphas, biases, s["inv"], s["mix"], n, C,
+                                              H.MODE_HEAD, 0.0, 1e-6, g_sub=s["go"]),
+            "pre_bwd_weights": lambda s: _ops.pre_bwd_weights(s["x"], s["inv"], s["mix"], s["graw"],
+                                                              phi, alphas, n, C, H.MODE_HEAD),
+        }
+        fd = n
+        nbytes = {"head_fwd": M * ((n * C + C) * es + 4 + 4 * fd) + n * C * fd * es,
+                  "pre_bwd": M * ((2 * n * C + C) * es + 4 + 8 * fd) + n * C * fd * es,
+                  "pre_bwd_weights": M * (n * C * es + 4 + 8 * fd) + n * C * fd * es}
+        res = {}
+        for name, fn in ops.items():
+            for s in S:
+                fn(s)
+            _sync()
+            e0 = torch.cuda.Event(enable_timing=True)
+            e1 = torch.cuda.Event(enable_timing=True)
+            _queue_ahead()
+            e0.record()
+            for _ in range(reps):
+                for s in S:
+                    fn(s)
+            e1.record()
+            _sync()
+            ms = e0.elapsed_time(e1) / (reps * sets)
+            gbs = nbytes[name] / (ms * 1e-3) / 1e9
+            res[name] = {"ms": round(ms, 5), "GBps": round(gbs, 1),
+                         "frac": round(gbs / HBM_PEAK_GBS, 4), "algorithmic_bytes": nbytes[name]}
+        res["config"] = f"MHCHead n={n} (FD={fd}), C={C}, {M} tokens, {tag} x / phi / gradients"
+        out[tag] = res
+    return out
+
+
 def layout_bytes(n: int, C: int, M: int, sx: int = 4, sf: int = 2, sp: int = 4):
     """Compulsory HBM bytes per launch in the reference trainers' layout
     (trainer/train_pretrain.py:129-130: fp32 model under bf16 autocast): fp32
@@ -915,7 +980,8 @@ def main():
     if args.section == "backward":
         bw5 = bench_backward(n=8, M=8192)
         bw5["config"] = "C5 shape: 8192 tokens, n=8, C=768, bf16"
-        print(json.dumps({"backward": bench_backward(), "backward_c5": bw5}), flush=True)
+        print(json.dumps({"backward": bench_backward(), "backward_c5": bw5,
+                          "head_backward": bench_head_backward()}), flush=True)
         return
     if args.section == "reference-shapes":
         print(json.dumps({"reference_bench_shapes": reference_bench_shapes()}), flush=True)
@@ -998,6 +1064,7 @@ def main():
     bw5 = bench_backward(n=8, M=8192)
     bw5["config"] = "C5 shape: 8192 tokens, n=8, C=768, bf16"
     line["backward_c5"] = bw5
+    line["head_backward"] = bench_head_backward()
     line["fp32_layout"] = bench_layout32()
     line["fp32_layout_c5"] = layout32_c5()
     line["other_configs"] = isolated_configs(max(10, args.steps // 2), max(3, args.warmup // 2))

@@ -298,7 +298,13 @@ int64_t mhc_pre_token_threshold(int64_t max_tokens);
  * Whether the persistent pre kernel loads x tiles as whole rows and stages
  * them through LDS (C a multiple of 256, phi resident in registers, no fused
  * norm; on by default) rather than loading the MFMA operand layout directly.
- * Both give bit-identical results; the row loads stream faster on MI355X.
+ * The row-staged kernel sums each row's squares in row order, so inv_rms may
+ * differ in its last bit from the operand-layout kernel's and, through
+ * x_norm's bf16 rounding, a token's gates by a rounding step (rounding-level
+ * agreement; tokens whose mixes agree match bit for bit).  The small-batch
+ * kernel sums in whichever order the persistent kernel would use, so the
+ * token threshold stays bit-identical under either setting.  The row loads
+ * stream faster on MI355X.
  * on < 0 only queries; returns the previous setting (0 or 1).  Process-wide,
  * not synchronised with calls in flight.  No reference counterpart (a
  * scheduling choice of this implementation).

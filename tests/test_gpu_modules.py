@@ -225,10 +225,10 @@ def test_module_matches_reference_c768(dev, name):
     itself (fp32, T = 256) at the 1e-5 bar, and bf16 rows of the config-2
     (n = 4) and config-5 (n = 8) shapes with stress gates (alphas 0.6 / 0.4 /
     0.8, random biases, so every gate follows the projection) at the 1e-2 bar.
-    The n = 4 kernels round x_norm to bf16 before the projection as
-    _forward_ref does (:845); the n = 8 kernel keeps it in fp32, as the
-    reference's fused kernel does (model/mhc_fused.py:209-229).  Many more
-    seeds: tests/test_gpu_parity_seeds.py."""
+    Every bf16 kernel (n = 4 and n = 8) rounds x_norm to bf16 before the
+    projection, as _forward_ref does (:845), not fp32 as the reference's fused
+    kernel keeps it (model/mhc_fused.py:209-229).  Many more seeds:
+    tests/test_gpu_parity_seeds.py."""
     from tests.golden import cases as K
     case, inp, ref = K.load(name)
     assert name in seeded_names("full")
