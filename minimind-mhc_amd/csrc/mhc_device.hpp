@@ -270,6 +270,15 @@ __device__ __forceinline__ uint32_t pack_hi(float h) { return (uint32_t)f32_to_b
 // under xor 8 / within quads (so every lane of a group ends with the
 // bit-identical sum).  Partners 16 and 32 lanes apart use ds_swizzle/bpermute.
 
+// A rounded multiply the compiler may not fuse with a later add into an fma.
+// HIP's __fmul_rn is the plain operator, which -ffp-contract=fast-honor-pragmas
+// (hipcc's default) contracts; the pragma clears the contract flag on this
+// multiply only.
+__device__ __forceinline__ float mul_nc(float a, float b) {
+#pragma clang fp contract(off)
+  return a * b;
+}
+
 template <int CTRL>
 __device__ __forceinline__ float dpp_f(float v) {
   return __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, v), CTRL,
