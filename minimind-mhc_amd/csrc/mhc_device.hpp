@@ -127,6 +127,15 @@ __device__ __forceinline__ float f16_bits_to_f32(uint16_t b) {
 }
 
 // Load element i of a tensor whose dtype is only known at run time.
+// A rounded multiply the compiler may not fuse with a later add into an fma.
+// HIP's __fmul_rn is the plain operator, which -ffp-contract=fast-honor-pragmas
+// (hipcc's default) contracts; the pragma clears the contract flag on this
+// multiply only.
+__device__ __forceinline__ float mul_nc(float a, float b) {
+#pragma clang fp contract(off)
+  return a * b;
+}
+
 __device__ __forceinline__ float ld_any(const void* p, int64_t i, int dt) {
   if (dt == kF32) return static_cast<const float*>(p)[i];
   uint16_t b = static_cast<const uint16_t*>(p)[i];
@@ -158,7 +167,7 @@ __device__ __forceinline__ float sigmoid_f(float z) {
 }
 
 __device__ __forceinline__ float affine_rn(float s, float alpha, float beta) {
-  return __fadd_rn(__fmul_rn(s, alpha), beta);
+  return __fadd_rn(mul_nc(s, alpha), beta);
 }
 
 // ---------------------------------------------- reference rounding points
@@ -171,7 +180,7 @@ __device__ __forceinline__ float affine_rn(float s, float alpha, float beta) {
 // sigmoid(alpha * m + bias) with the reference's roundings.
 __device__ __forceinline__ float gate_sigmoid(float m, float alpha, float bias, int dt) {
   const float mq = round_to(m, dt);
-  const float z = round_to(__fadd_rn(round_to(__fmul_rn(mq, alpha), dt), bias), dt);
+  const float z = round_to(__fadd_rn(round_to(mul_nc(mq, alpha), dt), bias), dt);
   return round_to(sigmoid_f(z), dt);
 }
 
@@ -182,12 +191,12 @@ __device__ __forceinline__ float gate_pre(float m, float alpha, float bias, floa
 
 // h_post: sigmoid(...) * post_mult
 __device__ __forceinline__ float gate_post(float m, float alpha, float bias, float post_mult, int dt) {
-  return round_to(__fmul_rn(gate_sigmoid(m, alpha, bias, dt), post_mult), dt);
+  return round_to(mul_nc(gate_sigmoid(m, alpha, bias, dt), post_mult), dt);
 }
 
 // h_res_raw: alpha * m + bias (Sinkhorn then runs in fp32 on this value)
 __device__ __forceinline__ float gate_res(float m, float alpha, float bias, int dt) {
-  return round_to(__fadd_rn(round_to(__fmul_rn(round_to(m, dt), alpha), dt), bias), dt);
+  return round_to(__fadd_rn(round_to(mul_nc(round_to(m, dt), alpha), dt), bias), dt);
 }
 
 // ------------------------------------------------------- x_norm on packed bf16
@@ -269,15 +278,6 @@ __device__ __forceinline__ uint32_t pack_hi(float h) { return (uint32_t)f32_to_b
 // row_ror:4 / row_half_mirror for xor 4 once the value is already symmetric
 // under xor 8 / within quads (so every lane of a group ends with the
 // bit-identical sum).  Partners 16 and 32 lanes apart use ds_swizzle/bpermute.
-
-// A rounded multiply the compiler may not fuse with a later add into an fma.
-// HIP's __fmul_rn is the plain operator, which -ffp-contract=fast-honor-pragmas
-// (hipcc's default) contracts; the pragma clears the contract flag on this
-// multiply only.
-__device__ __forceinline__ float mul_nc(float a, float b) {
-#pragma clang fp contract(off)
-  return a * b;
-}
 
 template <int CTRL>
 __device__ __forceinline__ float dpp_f(float v) {

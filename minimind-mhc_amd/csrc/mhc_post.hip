@@ -130,7 +130,7 @@ __global__ __launch_bounds__(256) void post_vec_kernel(PostArgs a) {
       } else {
         acc = xv[i][v];
       }
-      o[v] = __fadd_rn(acc, rnd<XT>(__fmul_rn(hp[i], fv[v])));
+      o[v] = __fadd_rn(acc, rnd<XT>(mul_nc(hp[i], fv[v])));
     }
     if constexpr (SSQ) {  // the stored pairs, squared on dot2 (exact products, fp32 sum)
       u32x4_t ov;
@@ -230,7 +230,7 @@ __global__ __launch_bounds__(256) void post_n16_kernel(PostArgs a) {
       }
       float o[4];
 #pragma unroll
-      for (int k = 0; k < 4; ++k) o[k] = __fadd_rn(r[k], rnd<__bf16>(__fmul_rn(hp[i], fl[k])));
+      for (int k = 0; k < 4; ++k) o[k] = __fadd_rn(r[k], rnd<__bf16>(mul_nc(hp[i], fl[k])));
       const u32x2_t ov = {pack_bf16x2(o[0], o[1]), pack_bf16x2(o[2], o[3])};
       __builtin_nontemporal_store(ov, reinterpret_cast<u32x2_t*>(out + (int64_t)i * C + c));
       if constexpr (SSQ) q = dot2_bf16(ov.y, ov.y, dot2_bf16(ov.x, ov.x, q));
@@ -306,7 +306,7 @@ __global__ __launch_bounds__(256) void post_n8_kernel(PostArgs a) {
       } else {
         r = (k & 1) ? bf16hi(xv[i][k >> 1]) : bf16lo(xv[i][k >> 1]);
       }
-      o[k] = __fadd_rn(r, rnd<__bf16>(__fmul_rn(hp, fl[k])));
+      o[k] = __fadd_rn(r, rnd<__bf16>(mul_nc(hp, fl[k])));
     }
     u32x4_t ov;
 #pragma unroll
@@ -347,7 +347,7 @@ __global__ __launch_bounds__(256) void post_generic_kernel(PostArgs a) {
   } else {
     acc = ld_any(a.x, xb + (int64_t)i * C + c, xdt);
   }
-  const float wb = round_to(__fmul_rn(ld_any(a.h_post, tok * n + i, a.h_dtype),
+  const float wb = round_to(mul_nc(ld_any(a.h_post, tok * n + i, a.h_dtype),
                                       ld_any(a.f_out, tok * C + c, a.f_dtype)), xdt);
   st_any(a.out, xb + (int64_t)i * C + c, xdt, __fadd_rn(acc, wb));
 }

@@ -431,7 +431,7 @@ __global__ __launch_bounds__(kKsWaves * 64) void pre_kstream_kernel(PreArgs a) {
           float acc = 0.f;
 #pragma unroll
           for (int i = 0; i < N; ++i)
-            acc = __fadd_rn(acc, __fmul_rn(sh.hpre[ts][i], __uint_as_float(xv[b][i].v[e])));
+            acc = __fadd_rn(acc, mul_nc(sh.hpre[ts][i], __uint_as_float(xv[b][i].v[e])));
           o.v[e] = __float_as_uint(acc);
         }
         buf_store16_nt(rsub, tt < valid ? (uint32_t)(tt * C + c) * ES : kBufOob, o);
@@ -481,7 +481,7 @@ __global__ __launch_bounds__(kKsWaves * 64) void pre_kstream_kernel(PreArgs a) {
     const bool pre = jl < N;
     const float gs = gate_sigmoid(m, sh.prm[pre ? 0 : 1], sh.prm[GP::kBiasPre + jl], XDT);
     const float h = pre ? round_to(__fadd_rn(gs, a.pre_eps), XDT)   // gate_pre
-                        : round_to(__fmul_rn(gs, a.post_mult), XDT);  // gate_post
+                        : round_to(mul_nc(gs, a.post_mult), XDT);  // gate_post
     if (pre) {
       sh.hpre[tt][jl] = h;
       if (ok && a.h_pre) st_any(a.h_pre, tk * N + jl, XDT, h);

@@ -307,9 +307,9 @@ __device__ __forceinline__ void split_preagg(const PreArgs& a, const U32x4 (&xr)
     U32x4 o;
 #pragma unroll
     for (int j = 0; j < 4; ++j) {
-      float s = __fmul_rn(h[0], __uint_as_float(xr[q][0].v[j]));
+      float s = mul_nc(h[0], __uint_as_float(xr[q][0].v[j]));
 #pragma unroll
-      for (int i = 1; i < N; ++i) s = __fadd_rn(s, __fmul_rn(h[i], __uint_as_float(xr[q][i].v[j])));
+      for (int i = 1; i < N; ++i) s = __fadd_rn(s, mul_nc(h[i], __uint_as_float(xr[q][i].v[j])));
       o.v[j] = __float_as_uint(s);
     }
     // The whole offset in the vector offset, the scalar offset the literal 0:
