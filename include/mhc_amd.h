@@ -6,8 +6,9 @@
  * The caller allocates every output (as the reference's autograd Functions do
  * with torch.empty); the library never allocates or frees device memory.  It
  * keeps no per-call state, so calls are re-entrant and capturable, with one
- * exception below.  It has two process-wide settings, both kernel choices:
- * mhc_pre_token_threshold and mhc_pre_row_staging.  One entry point
+ * exception below.  It has three process-wide settings, all kernel choices:
+ * mhc_pre_token_threshold, mhc_pre_group_split_tokens and
+ * mhc_pre_row_staging.  One entry point
  * (mhc_pre_bwd_weights) needs scratch for token-range partial sums; the caller
  * passes it as a workspace argument, or calls mhc_pre_bwd_weights_noalloc,
  * which uses a 32 MiB static device array the library holds per device
@@ -310,6 +311,19 @@ int64_t mhc_pre_token_threshold(int64_t max_tokens);
  * scheduling choice of this implementation).
  */
 int mhc_pre_row_staging(int on);
+
+/*
+ * Batch size (tokens) at or below which the n = 8 small-batch pre phase (bf16,
+ * packed phi, 4 * FD <= 2 * C) runs as two launches: the projection with each
+ * group's 16-column output tiles on workgroups of their own (each reads 1 / NT
+ * of phi instead of all of it), the finished mixes parked as fp32 in the
+ * sublayer-input rows, then the gates, Sinkhorn, pre-aggregate and norm.  The
+ * same MFMA chains and sums as the one-launch kernel: bit-identical results.
+ * Default 128; max_tokens < 0 only queries; returns the previous value.
+ * Process-wide, not synchronised with calls in flight.  No reference
+ * counterpart (a scheduling choice of this implementation).
+ */
+int64_t mhc_pre_group_split_tokens(int64_t max_tokens);
 
 /* ------------------------------------------------------------------ backward
  * Gradients are computed in fp32 and rounded once at the store, as the

@@ -171,7 +171,7 @@ int scratch_ptr(hipStream_t stream, void** out, const char* fn) {
 
 extern "C" {
 
-int mhc_abi_version(void) { return 7; }
+int mhc_abi_version(void) { return 8; }
 
 int mhc_init(void) {
   const char* fn = "mhc_init";
@@ -486,6 +486,12 @@ int64_t mhc_pre_token_threshold(int64_t max_tokens) {
 int mhc_pre_row_staging(int on) {
   const int prev = mhc::pre_row_staging() ? 1 : 0;
   if (on >= 0) mhc::set_pre_row_staging(on != 0);
+  return prev;
+}
+
+int64_t mhc_pre_group_split_tokens(int64_t max_tokens) {
+  const int64_t prev = mhc::pre_group_split_tokens();
+  if (max_tokens >= 0) mhc::set_pre_group_split_tokens(max_tokens);
   return prev;
 }
 

@@ -156,6 +156,10 @@ void set_pre_token_max_m(int64_t m);
 // default).
 bool pre_row_staging();
 void set_pre_row_staging(bool on);
+// Tokens at or below which the n = 8 small-batch pre phase runs in its split
+// form (two launches, bit-identical; process-wide setting, default 128).
+int64_t pre_group_split_tokens();
+void set_pre_group_split_tokens(int64_t m);
 // RMSNorm of each C row followed by n copies (StreamExpand): out[t, i*C + c].
 hipError_t launch_expand_norm(const void* x, int x_dtype, const void* w, int w_dtype, void* out,
                               int64_t M, int n, int C, float eps, hipStream_t s,

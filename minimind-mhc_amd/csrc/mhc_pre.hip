@@ -121,12 +121,17 @@ namespace {
 // level with them at 2048.
 int64_t g_token_max_m = 1024;
 bool g_row_staging = true;
+// Batch size up to which the n = 8 small-batch pre phase runs as two launches
+// (projection split over the output tiles, then the rest).
+int64_t g_group_split_m = 128;
 }  // namespace
 
 int64_t pre_token_max_m() { return g_token_max_m; }
 void set_pre_token_max_m(int64_t m) { g_token_max_m = m; }
 bool pre_row_staging() { return g_row_staging; }
 void set_pre_row_staging(bool on) { g_row_staging = on; }
+int64_t pre_group_split_tokens() { return g_group_split_m; }
+void set_pre_group_split_tokens(int64_t m) { g_group_split_m = m; }
 
 // Compute units of the current device (cached; one persistent workgroup each).
 int device_cus() {

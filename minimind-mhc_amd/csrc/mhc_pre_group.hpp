@@ -79,12 +79,20 @@ struct GroupShared {
   float scale[16];
 };
 
-template <int N, int MODE, int KB, bool NORM>
+// PH: 0 = the whole pre phase; 1 and 2 = the two launches of the split form
+// (launch_pre_group_split): 1 = the projection of output tile blockIdx.y only,
+// its finished mixes (the cross-wave sums) parked as fp32 in the first FD * 4
+// bytes of each token's sublayer-input row; 2 = everything else, the mixes
+// read back from there (before any sublayer input is stored).
+template <int N, int MODE, int KB, bool NORM, int PH = 0>
 __global__ __launch_bounds__(kGrpWaves * 64) void pre_group_kernel(PreArgs a, int G, int row_ss) {
   using P = GroupPlan<N, MODE, KB>;
   using GP = GateParams<N>;
+  static_assert(PH != 1 || !NORM, "the projection launch has no norm");
   constexpr int FD = P::FD;
   constexpr int NT = P::NT;
+  constexpr int NTL = PH == 1 ? 1 : NT;     // output tiles this launch projects
+  constexpr int PB = PH == 1 ? (P::NB < 24 ? P::NB : 24) : P::P;  // blocks in flight per wave
   constexpr int NN = P::NN;
   constexpr int T = kGrpWaves * 64;
   static_assert(sizeof(GroupShared<N, MODE, KB, NORM>) <= kLdsBytes, "LDS budget");
@@ -103,6 +111,10 @@ __global__ __launch_bounds__(kGrpWaves * 64) void pre_group_kernel(PreArgs a, in
   const int NJ = (NCH + kGrpWaves - 1) / kGrpWaves;     // blocks per wave, kstream order
   const int64_t t0 = wave_uniform((int64_t)blockIdx.x * G);
   const int valid = (int)(a.M - t0 < G ? a.M - t0 : G);
+  const int nt0 = PH == 1 ? (int)blockIdx.y : 0;  // first output tile projected here
+  // Mixes parked in the sublayer-input rows between the two split launches.
+  float* const park = static_cast<float*>(a.sub_in);
+  const int64_t park_row = (int64_t)C / 2;  // floats per sublayer-input row
   // pre_kstream_kernel rotates each tile's block order by (tile % NJ).
   const int rot = P::KS_ORDER ? (int)((t0 / kKsTileTokens) % NJ) : 0;
 
@@ -157,19 +169,29 @@ __global__ __launch_bounds__(kGrpWaves * 64) void pre_group_kernel(PreArgs a, in
       return cb < NCB;
     }
   };
-  U32x4 wq[P::P][NT];
+  U32x4 wq[PH == 2 ? 1 : PB][NTL];
   auto issue = [&](int b) {
     int i, cb;
     const bool live = block_of(b, i, cb);
 #pragma unroll
-    for (int nt = 0; nt < NT; ++nt) {
+    for (int u = 0; u < NTL; ++u) {
+      const int nt = nt0 + u;
       const bool pad = nt == NT - 1 && r >= P::LAST_COLS;
-      wq[b % P::P][nt] = buf_load16(
+      wq[b % PB][u] = buf_load16(
           rw, live && !pad ? (uint32_t)(((i * NCB + cb) * NT + nt) * 64 + lane) * 16u : kBufOob);
     }
   };
+  if constexpr (PH != 2) {
 #pragma unroll
-  for (int b = 0; b < P::P; ++b) issue(b);
+    for (int b = 0; b < PB; ++b) issue(b);
+  } else {
+    // The parked mixes into partial slot 0 (the other slots are not read).
+    for (int idx = tid; idx < G * FD; idx += T) {
+      const int tt = idx / FD;
+      const int f = idx - tt * FD;
+      sh.acc[0][tt][f] = tt < valid ? park[(t0 + tt) * park_row + f] : 0.f;
+    }
+  }
 
   // x rows into LDS (waits for the x loads only: they were issued first).
 #pragma unroll
@@ -242,32 +264,52 @@ __global__ __launch_bounds__(kGrpWaves * 64) void pre_group_kernel(PreArgs a, in
     ss += __shfl_xor(ss, 32, 64);
     if (g == 0 && r < G) sh.ss[wave][r] = ss;
   }
-  __syncthreads();  // sums of squares visible
-  const float inv_r = inv_of(r < G ? r : 0);
-  f32x4_t acc[NT];
+  __syncthreads();  // sums of squares (and parked mixes) visible
+  if constexpr (PH != 2) {
+    const float inv_r = inv_of(r < G ? r : 0);
+    f32x4_t acc[NTL];
 #pragma unroll
-  for (int nt = 0; nt < NT; ++nt) acc[nt] = f32x4_t{0.f, 0.f, 0.f, 0.f};
+    for (int u = 0; u < NTL; ++u) acc[u] = f32x4_t{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-  for (int b = 0; b < P::NB; ++b) {
-    const bf16x8_t av = __builtin_bit_cast(bf16x8_t, x_norm_chunk(a_of(b), inv_r));
+    for (int b = 0; b < P::NB; ++b) {
+      const bf16x8_t av = __builtin_bit_cast(bf16x8_t, x_norm_chunk(a_of(b), inv_r));
 #pragma unroll
-    for (int nt = 0; nt < NT; ++nt)
-      acc[nt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(av, __builtin_bit_cast(bf16x8_t, wq[b % P::P][nt]),
-                                                         acc[nt], 0, 0, 0);
-    if (b + P::P < P::NB) issue(b + P::P);
+      for (int u = 0; u < NTL; ++u)
+        acc[u] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(av, __builtin_bit_cast(bf16x8_t, wq[b % PB][u]),
+                                                         acc[u], 0, 0, 0);
+      if (b + PB < P::NB) issue(b + PB);
+    }
+    // MFMA 16x16 result layout: lane l holds D[4*(l/16) + j][l % 16], j = 0..3.
+#pragma unroll
+    for (int u = 0; u < NTL; ++u) {
+      const int nt = nt0 + u;
+      if (nt * 16 + r < FD)
+#pragma unroll
+        for (int j = 0; j < 4; ++j)
+          if (4 * g + j < G) sh.acc[wave][4 * g + j][nt * 16 + r] = acc[u][j];
+    }
+    __syncthreads();  // partials visible
   }
-  // MFMA 16x16 result layout: lane l holds D[4*(l/16) + j][l % 16], j = 0..3.
+  if constexpr (PH == 1) {
+    // The cross-wave sums of this tile's 16 columns, in wave order from zero
+    // (the sum the gates below form), parked for the second launch.
+    for (int idx = tid; idx < G * 16; idx += T) {
+      const int tt = idx >> 4;
+      const int f = nt0 * 16 + (idx & 15);
+      if (tt < valid && f < FD) {
+        float sum = 0.f;
 #pragma unroll
-  for (int nt = 0; nt < NT; ++nt)
-    if (nt * 16 + r < FD)
-#pragma unroll
-      for (int j = 0; j < 4; ++j)
-        if (4 * g + j < G) sh.acc[wave][4 * g + j][nt * 16 + r] = acc[nt][j];
-  __syncthreads();  // partials visible
+        for (int w = 0; w < kGrpWaves; ++w) sum += sh.acc[w][tt][f];
+        park[(t0 + tt) * park_row + f] = sum;
+      }
+    }
+    return;
+  }
 
   // ---- gates straight from the partials, no further barrier ------------------
   // (the partials are already normalised).
   auto mix_of = [&](int tt, int f, float) {
+    if constexpr (PH == 2) return sh.acc[0][tt][f];  // parked: the same sum
     float sum = 0.f;
 #pragma unroll
     for (int w = 0; w < kGrpWaves; ++w) sum += sh.acc[w][tt][f];
@@ -476,10 +518,47 @@ hipError_t launch_pre_group_inst(const PreArgs& a, int num_cus, hipStream_t s) {
   return hipGetLastError();
 }
 
+// The split form (n = 8, bf16): the projection of each group's 16-column
+// output tiles on NT workgroups of their own (each streams 1 / NT of phi from
+// L2 instead of all of it: one workgroup's phi stream is bound by its CU's
+// vector-memory path), the mixes parked in the sublayer-input rows, then a
+// second launch for the gates, the Sinkhorn, the pre-aggregate and the norm.
+// The same MFMA chains and cross-wave sums as the one-launch kernel, so the
+// results are bit for bit the same.  Needs FD fp32 values to fit a bf16 row
+// of C (4 FD <= 2 C).
+template <int N, int MODE, int KB>
+hipError_t launch_pre_group_split_inst(const PreArgs& a, int num_cus, hipStream_t s) {
+  using P = GroupPlan<N, MODE, KB>;
+  int G1 = 1;  // projection groups: enough workgroups (groups x NT) for one per CU
+  while (G1 < P::GMAX && ((a.M + G1 - 1) / G1) * P::NT > num_cus) G1 *= 2;
+  const int64_t grid1 = (a.M + G1 - 1) / G1;
+  hipLaunchKernelGGL((pre_group_kernel<N, MODE, KB, false, 1>), dim3((unsigned)grid1, P::NT),
+                     dim3(kGrpWaves * 64), 0, s, a, G1, 0);
+  hipError_t e = hipGetLastError();
+  if (e != hipSuccess) return e;
+  const int G = group_tokens<N, MODE, KB>(a.M, num_cus);
+  const int64_t grid = (a.M + G - 1) / G;
+  if (a.norm_w)
+    hipLaunchKernelGGL((pre_group_kernel<N, MODE, KB, true, 2>), dim3((unsigned)grid),
+                       dim3(kGrpWaves * 64), 0, s, a, G, 0);
+  else
+    hipLaunchKernelGGL((pre_group_kernel<N, MODE, KB, false, 2>), dim3((unsigned)grid),
+                       dim3(kGrpWaves * 64), 0, s, a, G, 0);
+  return hipGetLastError();
+}
+
 template <int N, int MODE, int... KBS>
 hipError_t dispatch_group_kb(const PreArgs& a, int kb, int num_cus, hipStream_t s) {
   hipError_t r = hipErrorInvalidValue;
   bool done = false;
+  const bool split = N == 8 && a.M <= pre_group_split_tokens() &&
+                     4 * PreShape<N, MODE>::FD <= 2 * a.C;
+  if (split) {
+    ((!done && KBS >= kb ? (r = launch_pre_group_split_inst<N, MODE, KBS>(a, num_cus, s), done = true)
+                         : false),
+     ...);
+    return r;
+  }
   ((!done && KBS >= kb ? (r = launch_pre_group_inst<N, MODE, KBS>(a, num_cus, s), done = true) : false),
    ...);
   return r;

@@ -64,6 +64,7 @@ _SIGNATURES = {
     "mhc_expand_norm_fwd": (_I, [_P, _I, _P, _I, _P, _I64, _I, _I, _F, _P, _P]),
     "mhc_pre_token_threshold": (_I64, [_I64]),
     "mhc_pre_row_staging": (_I, [_I]),
+    "mhc_pre_group_split_tokens": (_I64, [_I64]),
     "mhc_sinkhorn_fwd": (_I, [_P, _P, _I, _I64, _I, _I, _F, _P]),
     "mhc_stream_expand_fwd": (_I, [_P, _P, _I, _I64, _I, _I, _P]),
     "mhc_post_bwd": (_I, [_P, _I, _P, _P, _I, _P, _I, _P, _P, _P, _P, _P, _I64, _I, _I, _P]),
@@ -90,7 +91,7 @@ _SIGNATURES = {
     "mhc_sinkhorn_bwd_max_iters": (_I, [_I]),
 }
 
-ABI_VERSION = 7
+ABI_VERSION = 8
 _lib: Optional[ctypes.CDLL] = None
 
 

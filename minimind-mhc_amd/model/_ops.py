@@ -431,8 +431,16 @@ def pre_token_threshold(max_tokens: int = -1) -> int:
 def pre_row_staging(on: int = -1) -> int:
     """Set (on >= 0) or query whether the persistent pre kernel loads x tiles
     as whole rows staged through LDS where the shape allows; returns the
-    previous setting (0 or 1).  Results are bit-identical either way."""
+    previous setting (0 or 1).  The two agree to rounding (the row sums of
+    squares are added in another order)."""
     return int(H.load().mhc_pre_row_staging(int(on)))
+
+
+def pre_group_split_tokens(max_tokens: int = -1) -> int:
+    """Set (max_tokens >= 0) or query the batch size at or below which the
+    n = 8 small-batch pre phase runs as two launches (the projection split
+    over the output tiles; bit-identical); returns the previous value."""
+    return int(H.load().mhc_pre_group_split_tokens(int(max_tokens)))
 
 
 def stream_expand(x: torch.Tensor, n: int) -> torch.Tensor:

@@ -10,7 +10,10 @@ oracle by tests/test_gpu_fused.py and tests/test_gpu_ops.py.
 Shapes: group sizes 1, 2, 4 and 8 (M = 1, 37, 300, 700, 1100 on a 256-CU
 MI355X), a ragged last group, C a multiple of 256 and not (640, 200), n in
 {1, 2, 4, 8}, the three projection modes, with and without the fused RMSNorm,
-Sinkhorn iteration counts 20, 1 and 0."""
+Sinkhorn iteration counts 20, 1 and 0.  At n = 8 up to
+mhc_pre_group_split_tokens (128) the small-batch side is the split form (two
+launches); test_group_split_matches_one_launch pins it against the one-launch
+kernel directly, with and without handed-over sums of squares."""
 from __future__ import annotations
 
 import pytest
@@ -129,3 +132,59 @@ def test_group_matches_large_batch_kernel_several_tiles_per_workgroup(threshold,
     step (whose Sinkhorn of the tile before it runs after the loop, on the gate
     waves) and ragged last tiles, bit for bit against the group kernel."""
     _both(threshold, "full", n, C, M, seed=3 * n + C + M)
+
+
+@pytest.fixture
+def split():
+    old = _ops.pre_group_split_tokens(-1)
+    yield _ops.pre_group_split_tokens
+    _ops.pre_group_split_tokens(old)
+
+
+@pytest.mark.parametrize("kind", ["full", "nohres", "head"])
+@pytest.mark.parametrize("M", [1, 16, 37, 64, 128, 300])
+@pytest.mark.parametrize("use_norm,use_ssq", [(False, False), (True, False), (False, True),
+                                               (True, True)])
+def test_group_split_matches_one_launch(threshold, split, kind, M, use_norm, use_ssq):
+    """n = 8: the split form (projection per 16-column output tile on its own
+    workgroups, mixes parked in the sublayer-input rows, then the rest) against
+    the one-launch small-batch kernel, bit for bit, every output."""
+    n, C = 8, 768
+    g = torch.Generator().manual_seed(11 * M + (kind == "head") + 2 * use_norm + 4 * use_ssq)
+    p = make_params(kind, n, C, BF, g, stress=True)
+    x = (torch.randn(1, M, n * C, generator=g) * 2.0).to(BF)
+    dev = torch.device("cuda:0")
+    pd = {k: v.to(dev) for k, v in p.items()}
+    packed = _ops.PhiPack(_MODE[kind]).get(pd["phi_weight"], n, C)
+    xd = x.to(dev)
+    norm = ((torch.rand(C, generator=g) + 0.5).to(BF).to(dev), 1e-6) if use_norm else None
+    ssq = None
+    if use_ssq:  # per-row partials per 128 columns (any values: both sides read the same)
+        ssq = (x.float().view(M, n, C // 128, 128) ** 2).sum(dim=(1, 3)).to(dev).contiguous()
+    print(f"group split {kind} M={M} norm={use_norm} ssq={use_ssq}", flush=True)
+    threshold(1 << 40)
+
+    def run():
+        if kind == "full":
+            o = _ops.pre_full(xd, pd["phi_weight"], packed, pd["alpha_pre"], pd["bias_pre"],
+                              pd["alpha_post"], pd["bias_post"], pd["alpha_res"], pd["bias_res"],
+                              n, C, 2.0, 1e-6, 1e-6, 20, 1e-6, want_h_pre=True, want_raw=True,
+                              want_saved=True, norm=norm, ssq=ssq)
+        elif kind == "nohres":
+            o = _ops.pre_nohres(xd, pd["phi_weight"], packed, pd["alpha_pre"], pd["bias_pre"],
+                                pd["alpha_post"], pd["bias_post"], n, C, 2.0, 1e-6, 1e-6,
+                                want_h_pre=True, want_saved=True, norm=norm, ssq=ssq)
+        else:
+            out, inv, mix = _ops.head(xd, pd["phi_weight"], packed, pd["alpha"], pd["bias"], n, C,
+                                      1e-6, 1e-6, want_saved=True, norm=norm, ssq=ssq)
+            o = {"sub_in": out, "inv_rms": inv, "mixes_raw": mix}
+        torch.cuda.synchronize()
+        return {k: v.clone() for k, v in o.items() if v is not None}
+
+    split(0)
+    one = run()
+    split(1 << 40)
+    two = run()
+    assert one.keys() == two.keys()
+    for k in one:
+        assert torch.equal(one[k], two[k]), k
