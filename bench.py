@@ -598,6 +598,13 @@ def traffic_passes(vector_pre: bool = False, extra: bool = False):
         b08 = torch.zeros(n8, dtype=torch.bfloat16, device=dev)
         br8 = torch.eye(n8, dtype=torch.bfloat16, device=dev)
         pk8 = _ops.PhiPack(H.MODE_FULL).get(phi8, n8, C)
+        # the model's launch (the rows' sums of squares handed over, as the
+        # previous post launch writes them), then the same without them
+        ssq8 = (x8.view(M8, n8, C // _ops.SSQ_COLS, _ops.SSQ_COLS).float().pow(2).sum(dim=(1, 3))
+                .contiguous())
+        _sync()
+        _ops.pre_full(x8, phi8, pk8, a, b08, a, b08, a, br8, n8, C, 2.0, 1e-6, 1e-6, ITERS, 1e-6,
+                      ssq=ssq8)
         _sync()
         _ops.pre_full(x8, phi8, pk8, a, b08, a, b08, a, br8, n8, C, 2.0, 1e-6, 1e-6, ITERS, 1e-6)
         _sync()
@@ -958,7 +965,8 @@ def main():
                          "kernel pairs and print them as one JSON line (for profiler runs)")
     ap.add_argument("--mfma-kernels", action="store_true",
                     help="with --traffic: also run the config-2 backward MFMA kernels and the "
-                         "config-5 (n = 8) pre phase once")
+                         "config-5 (n = 8) pre phase, with and without the handed-over sums "
+                         "of squares")
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py: this build measures one GPU only (the mHC forward is per-token and "
