@@ -22,8 +22,8 @@
 //     v_mfma_f32_16x16x32_bf16 accumulates;
 //   * the K-split partials meet in LDS.  The pre-aggregate's re-reads of the
 //     tile's x (from the Infinity Cache: it has left L2 by then) need no
-//     result of the projection, so its first two rounds go out before the
-//     partials are summed;
+//     result of the projection, so its first round goes out before the
+//     partials are summed (and, but for bf16 at n >= 8, the second as well);
 //   * LPT = 512 / TM lanes per token (16, or 32 at n = 16) then form inv_rms
 //     and the gates straight from the partials: lane j takes mix j (h_pre for
 //     j < n, h_post for n <= j < 2n) and its share of the n*n h_res logits in
@@ -66,7 +66,11 @@ struct KsPlan {
   static constexpr int LPT = WAVES * 64 / TM;        // lanes per token in the gate phase
   static constexpr int TPW = 64 / LPT;               // tokens per wave
   static constexpr int D = 3;                        // chunks in flight per wave
-  static constexpr int PB = N >= 16 ? 1 : 2;         // pre-aggregate items per lane per round
+  // pre-aggregate items per lane per round: one at n >= 8, where a round of
+  // two (128 KB a workgroup at n = 8) issued at once held up the loop's tail
+  // (C5 pre 52.5 -> 49.0 us with one, 48.6 us with the second round issued
+  // after the gates); two at n <= 4 (C > 1024), where one measured level.
+  static constexpr int PB = N >= 8 ? 1 : 2;
   static constexpr int SD = 4;                       // chunks in flight in the sums-of-squares pass
   static constexpr int SKV = G > LPT ? G / LPT : 1;  // Sinkhorn values per lane
   static constexpr int SKL = G / SKV;                // lanes holding distinct h_res values
@@ -391,11 +395,14 @@ __global__ __launch_bounds__(kKsWaves * 64) void pre_kstream_kernel(PreArgs a) {
 
   // ---- pre-aggregate rounds --------------------------------------------------
   // Items are (token, 16-byte column chunk) pairs, PB per lane per round, in
-  // two register buffers: rounds 0 and 1 are issued here, round r + 2 as soon
-  // as round r is consumed.  A round past the end reads nothing (offsets out
-  // of the descriptor) and stores nothing.
-  // (fp32: 4-column items, the same 16 bytes of each stream per item)
-  constexpr int PB = P::PB;
+  // two register buffers: round 0 is issued here, round 1 here as well or,
+  // with one item a round (bf16 at n >= 8), after the gates; round r + 2 as
+  // soon as round r is consumed.  A round past the end reads nothing (offsets
+  // out of the descriptor) and stores nothing.
+  // (fp32: 4-column items, the same 16 bytes of each stream per item; two a
+  // round, both rounds up front: C5 110.1 us against 112.0 us with one)
+  constexpr int PB = F32 ? 2 : P::PB;
+  constexpr bool kLateRound1 = PB == 1;
   constexpr int CW = F32 ? 4 : 8;  // columns per item
   const int C8 = C / CW;
   const int items = TM * C8;
@@ -457,7 +464,7 @@ __global__ __launch_bounds__(kKsWaves * 64) void pre_kstream_kernel(PreArgs a) {
   U32x4 xa[PB][N];
   U32x4 xb[PB][N];
   pa_issue(0, xa);
-  pa_issue(1, xb);
+  if constexpr (!kLateRound1) pa_issue(1, xb);
   __syncthreads();  // partials and gate parameters visible
 
   // ---- inv_rms and gates: LPT lanes per token ---------------------------------
@@ -522,6 +529,7 @@ __global__ __launch_bounds__(kKsWaves * 64) void pre_kstream_kernel(PreArgs a) {
     }
   }
   __syncthreads();  // h_pre visible to every lane's pre-aggregate items
+  if constexpr (kLateRound1) pa_issue(1, xb);
 
   // ---- Sinkhorn iterations between the pre-aggregate rounds ------------------
   const bool sk = MODE == kFull && a.h_res != nullptr;
