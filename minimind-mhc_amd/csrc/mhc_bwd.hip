@@ -689,36 +689,94 @@ __global__ __launch_bounds__(256) void weights_reduce_kernel(WeightsArgs a, int 
   }
 }
 
-// bf16 or fp32 x on MFMA.  Workgroup (k-slice of 128 columns, token range):
-// per step of 64 tokens the x tile is written to LDS transposed ([column]
-// [token], two tokens per 32-bit write) and u = inv_rms * g_raw ([feature]
-// [token]) split into bf16 hi + lo, then wave w accumulates
-//   D[16w + i][f] += sum_t x[t][k0 + 16w + i] * u[t][f]
-// with A = x^T rows (16-byte LDS reads of 8 tokens) and B = u columns.  An
+// bf16 or fp32 x on MFMA.  Workgroup (k-slice of 128 MT columns, token
+// range): per step of 64 tokens the x tile is written to LDS transposed
+// ([column][token], two tokens per 32-bit write) and u = inv_rms * g_raw
+// ([feature][token]) split into bf16 hi + lo, then wave w accumulates, for
+// its MT 16-column tiles m (columns 16 (w + 8m) + i),
+//   D[16(w + 8m) + i][f] += sum_t x[t][k0 + 16(w + 8m) + i] * u[t][f]
+// with A = x^T rows (16-byte LDS reads of 8 tokens) and B = u columns, each
+// B operand read once for the MT tiles (the per-step u work and its LDS
+// reads are per workgroup, so wider slices spend less of them per column).  An
 // fp32 x is split the same way (a second transposed tile holds x_lo) and
 // three products run per step: x_hi u_hi + x_hi u_lo + x_lo u_hi.
-// Workgroups of k-slice 0 also sum g_raw and g_raw * mixes per feature over
-// their range (the alpha / bias partials).
+// One more workgroup per token range (blockIdx.x == the slice count) sums
+// g_raw and g_raw * mixes per feature over the range: the alpha / bias
+// partials, kept off the slices' registers.
 constexpr int kWTok = 64;                // tokens per step
-constexpr int kWCols = 128;              // columns per workgroup
+constexpr int kWCols = 128;              // columns per workgroup and 16-column tile per wave
 constexpr int kWRow = kWTok * 2 + 16;    // LDS row stride in bytes (64 bf16 + pad)
 
-// x is loaded PF steps ahead (2 where the registers allow: the x of step t + 2
-// goes out while step t's MFMAs run, so a workgroup keeps 32 KB of x in
-// flight); the per-token values of step t + 1 go out as soon as step t has
-// consumed its own.
-template <int NTF, bool F32, int PF>  // 16-wide feature tiles, fp32 x, steps in flight
-__global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(PF == 2 ? 4 : 1)))
-void weights_mfma_kernel(WeightsArgs a, int64_t per) {
+// The alpha / bias partials of one token range [tb, te): thread (row, quad)
+// sums features 4 quad .. 4 quad + 3 over tokens tb + row, tb + row + rows,
+// ..., four tokens in flight; the rows are then summed in order.
+__device__ __forceinline__ void weights_ab_range(const WeightsArgs& a, int FD, int64_t tb, int64_t te,
+                                                 float* ab, float (*s_red)[2][4]) {
+  const int tid = threadIdx.x;
+  const int Q = (FD + 3) / 4;
+  const int rows = 512 / Q;
+  const int row = tid / Q;
+  const int q = tid % Q;
+  const uint32_t span = (uint32_t)((te - tb) * FD * 4);
+  const auto rg = make_rsrc(a.g_raw + tb * FD, span);
+  const auto rm = make_rsrc(a.mixes + tb * FD, span);
+  float sb[4] = {0.f, 0.f, 0.f, 0.f}, sa[4] = {0.f, 0.f, 0.f, 0.f};
+  auto quad = [&](__amdgpu_buffer_rsrc_t r, int64_t t) -> U32x4 {  // FD % 4 == 0
+    return buf_load16(r, t < te - tb ? (uint32_t)(t * FD * 4) + 16u * q : kBufOob);
+  };
+  if (row < rows) {
+    for (int64_t t = row; t < te - tb; t += 4 * (int64_t)rows) {  // uniform per thread
+      U32x4 g[4], m[4];
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        g[j] = quad(rg, t + (int64_t)j * rows);
+        m[j] = quad(rm, t + (int64_t)j * rows);
+      }
+#pragma unroll
+      for (int j = 0; j < 4; ++j)
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+          const float gv = __uint_as_float(g[j].v[e]);
+          sb[e] += gv;
+          sa[e] = fmaf(gv, __uint_as_float(m[j].v[e]), sa[e]);
+        }
+    }
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+      s_red[tid][0][e] = sb[e];
+      s_red[tid][1][e] = sa[e];
+    }
+  }
+  __syncthreads();
+  for (int f = tid; f < FD; f += 512) {
+    float b = 0.f, al = 0.f;
+    for (int r = 0; r < rows; ++r) {
+      b += s_red[r * Q + f / 4][0][f % 4];
+      al += s_red[r * Q + f / 4][1][f % 4];
+    }
+    ab[f] = b;
+    ab[FD + f] = al;
+  }
+}
+
+// x is loaded PF steps ahead and the per-token values TD steps ahead (step
+// t + TD's go out as soon as step t has consumed its own).  Per-token items
+// are (token pair, feature quad): 16-byte loads of both tokens' g_raw quads
+// and one inv_rms each, token pairs along the lanes so the u writes to LDS
+// fill whole rows.
+template <int NTF, bool F32, int MT, int PF, int TD, int WPE>  // feature tiles, fp32 x, column tiles a wave,
+__global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(WPE)))  // x / per-token steps in flight,
+void weights_mfma_kernel(WeightsArgs a, int64_t per) {                       // waves / SIMD
   constexpr int F16 = NTF * 16;
-  constexpr int UPT = F16 / 16;  // (token pair, feature) items per thread: 32 * F16 / 512
+  constexpr int QT = F16 / 4;                   // feature quads of the tile
+  constexpr int NI = (32 * QT + 511) / 512;     // (token pair, quad) items per thread
   constexpr int XQ = F32 ? 2 : 1;  // 16-byte loads per 8 columns of one token
   constexpr uint32_t ES = F32 ? 4u : 2u;
-  __shared__ __attribute__((aligned(16))) unsigned char s_x[kWCols * kWRow];
-  __shared__ __attribute__((aligned(16))) unsigned char s_xl[F32 ? kWCols * kWRow : 16];
+  constexpr int WC = kWCols * MT;  // columns of the slice
+  __shared__ __attribute__((aligned(16))) unsigned char s_x[WC * kWRow];
+  __shared__ __attribute__((aligned(16))) unsigned char s_xl[F32 ? WC * kWRow : 16];
   __shared__ __attribute__((aligned(16))) unsigned char s_uh[F16 * kWRow];
   __shared__ __attribute__((aligned(16))) unsigned char s_ul[F16 * kWRow];
-  __shared__ float s_ab[2][kWTok / 2][F16];
   const int FD = mode_fd(a.mode, a.n);
   const int NC = a.n * a.C;
   const int tid = threadIdx.x;
@@ -726,175 +784,208 @@ void weights_mfma_kernel(WeightsArgs a, int64_t per) {
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int r = lane & 15;
   const int g = lane >> 4;
-  const int k0 = blockIdx.x * kWCols;
   const int rng = blockIdx.y;
   const int64_t tb = (int64_t)rng * per;
   const int64_t te = tb + per < a.M ? tb + per : a.M;
-  const bool ab_slice = blockIdx.x == 0;
+  if (blockIdx.x + 1 == gridDim.x) {  // the range's alpha / bias partials
+    static_assert(512 * 2 * 4 * 4 <= kWCols * kWRow, "reduction rows fit s_x");
+    weights_ab_range(a, FD, tb, te, a.work + (int64_t)gridDim.y * NC * FD + (int64_t)rng * 2 * FD,
+                     reinterpret_cast<float (*)[2][4]>(s_x));
+    return;
+  }
+  const int k0 = blockIdx.x * WC;
 
-  // x: 8-column group kc (columns k0 + 8kc .. + 7) of token pair tp (tokens
-  // 2tp, 2tp + 1 of the step).  Sixteen consecutive lanes cover a token's 256
-  // bytes of the slice, so each wave load reads whole 128-byte lines.
+  // x: 8-column groups kc + 16m (columns k0 + 8 (kc + 16m) .. + 7) of token
+  // pair tp (tokens 2tp, 2tp + 1 of the step).  Sixteen consecutive lanes
+  // cover 256 bytes of a token's row, so each wave load reads whole 128-byte
+  // lines.
   const int kc = tid & 15;
   const int tp = tid >> 4;
-  const int col = k0 + 8 * kc;
-  const bool okc = col < NC;
   // In s_x the 16-byte groups of token pairs (4 pairs = 8 tokens) of column
   // group kc are XOR-permuted by kc & 7: the transposed writes of 16 column
   // groups at one token pair then spread over 8 bank groups instead of one,
   // and an MFMA read of 8 consecutive tokens stays one aligned 16-byte read.
   auto tp_slot = [](int pair, int group) { return pair ^ (4 * (group & 7)); };
 
-  // Everything one step reads from memory; the next step's copy is loaded
-  // while the current step's MFMAs run.  x is read non-temporally (its last
-  // use in the backward).
+  // Per-token items: item i of this thread is token pair pp = idx % 32 and
+  // feature quad fq = idx / 32 (idx = tid + 512 i; fq < QT), read through
+  // descriptors over the range (tokens past te read zeros).
+  const auto rg = make_rsrc(a.g_raw + tb * FD, (uint32_t)((te - tb) * FD * 4));
+  const auto ri = make_rsrc(a.inv_rms + tb, (uint32_t)((te - tb) * 4));
   struct XStep {  // a step's x, PF steps ahead
-    U32x4 xa[XQ], xb[XQ];
+    U32x4 xa[MT][XQ], xb[MT][XQ];
   };
-  struct Step {     // a step's per-token values, one step ahead
-    float ga[UPT], gb[UPT], ia[UPT], ib[UPT], ma[UPT], mb[UPT];
+  struct Step {  // a step's per-token values, one step ahead
+    U32x4 ga[NI], gb[NI];
+    float ia[NI], ib[NI];
   };
   auto load_x = [&](int64_t t, XStep& st) {
     const int valid = t < te ? (int)(te - t < kWTok ? te - t : kWTok) : 0;
     const auto rs = make_rsrc(static_cast<const unsigned char*>(a.x) + (t < te ? t : 0) * NC * ES,
                               (uint32_t)valid * NC * ES);
 #pragma unroll
-    for (int h = 0; h < XQ; ++h) {
-      st.xa[h] = buf_load16_nt(rs, okc ? (uint32_t)((2 * tp) * NC + col) * ES + 16u * h : kBufOob, 0);
-      st.xb[h] = buf_load16_nt(rs, okc ? (uint32_t)((2 * tp + 1) * NC + col) * ES + 16u * h : kBufOob, 0);
+    for (int m = 0; m < MT; ++m) {
+      const int col = k0 + 8 * (kc + 16 * m);
+      const bool okc = col < NC;
+#pragma unroll
+      for (int h = 0; h < XQ; ++h) {
+        st.xa[m][h] = buf_load16_nt(rs, okc ? (uint32_t)((2 * tp) * NC + col) * ES + 16u * h : kBufOob, 0);
+        st.xb[m][h] = buf_load16_nt(rs, okc ? (uint32_t)((2 * tp + 1) * NC + col) * ES + 16u * h : kBufOob, 0);
+      }
     }
+  };
+  // Quad fq of token tok (relative to tb; FD % 4 == 0, the launcher keeps
+  // (per + 64) * FD * 4 below 2^31, and tokens past te land past the descriptor).
+  auto g_quad = [&](bool live, uint32_t tok, int fq) -> U32x4 {
+    return buf_load16(rg, live && 4 * fq < FD ? tok * (uint32_t)FD * 4u + 16u * fq : kBufOob);
   };
   auto load_step = [&](int64_t t, Step& st) {
 #pragma unroll
-    for (int u = 0; u < UPT; ++u) {
-      const int idx = tid + 512 * u;
-      const int f = idx % F16;  // feature-major: consecutive threads read consecutive features
-      const int pp = idx / F16;
-      const int64_t ta = t + 2 * pp;
-      const bool fa = f < FD && ta < te;
-      const bool fb = f < FD && ta + 1 < te;
-      st.ga[u] = fa ? a.g_raw[ta * FD + f] : 0.f;
-      st.gb[u] = fb ? a.g_raw[(ta + 1) * FD + f] : 0.f;
-      st.ia[u] = fa ? a.inv_rms[ta] : 0.f;
-      st.ib[u] = fb ? a.inv_rms[ta + 1] : 0.f;
-      st.ma[u] = fa && ab_slice ? a.mixes[ta * FD + f] : 0.f;
-      st.mb[u] = fb && ab_slice ? a.mixes[(ta + 1) * FD + f] : 0.f;
+    for (int i = 0; i < NI; ++i) {
+      const int idx = tid + 512 * i;
+      const int pp = idx & 31;
+      const int fq = idx >> 5;
+      const uint32_t ta = (uint32_t)(t - tb) + 2u * pp;
+      const bool live = fq < QT && t < te;
+      st.ga[i] = g_quad(live, ta, fq);
+      st.gb[i] = g_quad(live, ta + 1, fq);
+      st.ia[i] = __uint_as_float(__builtin_amdgcn_raw_buffer_load_b32(ri, (int)(live ? 4u * ta : kBufOob), 0, 0));
+      st.ib[i] = __uint_as_float(__builtin_amdgcn_raw_buffer_load_b32(ri, (int)(live ? 4u * ta + 4u : kBufOob), 0, 0));
     }
   };
-  float sb[UPT], sa[UPT];
+  f32x4_t acc[MT][NTF];
 #pragma unroll
-  for (int u = 0; u < UPT; ++u) { sb[u] = 0.f; sa[u] = 0.f; }
-  f32x4_t acc[NTF];
+  for (int m = 0; m < MT; ++m)
 #pragma unroll
-  for (int ft = 0; ft < NTF; ++ft) acc[ft] = f32x4_t{0.f, 0.f, 0.f, 0.f};
+    for (int ft = 0; ft < NTF; ++ft) acc[m][ft] = f32x4_t{0.f, 0.f, 0.f, 0.f};
 
   // One step: the staged loads to LDS, then the MFMAs while later steps load.
-  Step cur;
-  auto run_step = [&](int64_t t, XStep& xc) {
+  auto run_step = [&](int64_t t, XStep& xc, Step& cur) {
     // u = inv * g_raw as hi / lo bf16 token pairs, [feature][token]
 #pragma unroll
-    for (int u = 0; u < UPT; ++u) {
-      const int idx = tid + 512 * u;
-      const int f = idx % F16;
-      const int pp = idx / F16;
-      const float va = cur.ia[u] * cur.ga[u];
-      const float vb = cur.ib[u] * cur.gb[u];
-      const uint32_t hi = pack_bf16x2(va, vb);
-      *reinterpret_cast<uint32_t*>(s_uh + f * kWRow + pp * 4) = hi;
-      *reinterpret_cast<uint32_t*>(s_ul + f * kWRow + pp * 4) = pack_bf16x2(va - bf16lo(hi), vb - bf16hi(hi));
-      if (ab_slice) {
-        sb[u] += cur.ga[u] + cur.gb[u];
-        sa[u] = fmaf(cur.gb[u], cur.mb[u], fmaf(cur.ga[u], cur.ma[u], sa[u]));
-      }
-    }
-    // The next step's per-token values go out as soon as these are consumed:
-    // they then have this step's transposes, barriers and MFMAs to arrive.
-    load_step(t + kWTok, cur);
-    // x tile transposed: column 8kc + e, tokens (2tp, 2tp + 1) in one dword
+    for (int i = 0; i < NI; ++i) {
+      const int idx = tid + 512 * i;
+      const int pp = idx & 31;
+      const int fq = idx >> 5;
+      if (fq < QT) {
 #pragma unroll
-    for (int e = 0; e < 8; ++e) {
-      const uint32_t off = (8 * kc + e) * kWRow + tp_slot(tp, kc) * 4;
-      if constexpr (F32) {
-        const float va = __uint_as_float(xc.xa[e >> 2].v[e & 3]);
-        const float vb = __uint_as_float(xc.xb[e >> 2].v[e & 3]);
-        const uint32_t hi = pack_bf16x2(va, vb);
-        *reinterpret_cast<uint32_t*>(s_x + off) = hi;
-        *reinterpret_cast<uint32_t*>(s_xl + off) = pack_bf16x2(va - bf16lo(hi), vb - bf16hi(hi));
-      } else {
-        const uint32_t wa = xc.xa[0].v[e >> 1];
-        const uint32_t wb = xc.xb[0].v[e >> 1];
-        const uint32_t d = (e & 1) ? ((wa >> 16) | (wb & 0xffff0000u)) : ((wa & 0xffffu) | (wb << 16));
-        *reinterpret_cast<uint32_t*>(s_x + off) = d;
+        for (int e = 0; e < 4; ++e) {
+          const float va = cur.ia[i] * __uint_as_float(cur.ga[i].v[e]);
+          const float vb = cur.ib[i] * __uint_as_float(cur.gb[i].v[e]);
+          const uint32_t hi = pack_bf16x2(va, vb);
+          const int off = (4 * fq + e) * kWRow + pp * 4;
+          *reinterpret_cast<uint32_t*>(s_uh + off) = hi;
+          *reinterpret_cast<uint32_t*>(s_ul + off) = pack_bf16x2(va - bf16lo(hi), vb - bf16hi(hi));
+        }
       }
     }
+    // Step t + TD's per-token values go out as soon as these are consumed.
+    load_step(t + TD * kWTok, cur);
+    // x tile transposed: column 8 (kc + 16m) + e, tokens (2tp, 2tp + 1) in one dword
+#pragma unroll
+    for (int m = 0; m < MT; ++m)
+#pragma unroll
+      for (int e = 0; e < 8; ++e) {
+        const uint32_t off = (8 * (kc + 16 * m) + e) * kWRow + tp_slot(tp, kc) * 4;
+        if constexpr (F32) {
+          const float va = __uint_as_float(xc.xa[m][e >> 2].v[e & 3]);
+          const float vb = __uint_as_float(xc.xb[m][e >> 2].v[e & 3]);
+          const uint32_t hi = pack_bf16x2(va, vb);
+          *reinterpret_cast<uint32_t*>(s_x + off) = hi;
+          *reinterpret_cast<uint32_t*>(s_xl + off) = pack_bf16x2(va - bf16lo(hi), vb - bf16hi(hi));
+        } else {
+          const uint32_t wa = xc.xa[m][0].v[e >> 1];
+          const uint32_t wb = xc.xb[m][0].v[e >> 1];
+          const uint32_t d = (e & 1) ? ((wa >> 16) | (wb & 0xffff0000u)) : ((wa & 0xffffu) | (wb << 16));
+          *reinterpret_cast<uint32_t*>(s_x + off) = d;
+        }
+      }
     __syncthreads();
     // x of step t + PF flies over the MFMAs (issued after the per-token values
     // of step t + 1: the vector-memory counter retires in order).
     load_x(t + PF * kWTok, xc);
 #pragma unroll
     for (int ks = 0; ks < kWTok / 32; ++ks) {
-      const int xc = 16 * wave + r;  // column of the slice
-      const int xoff = xc * kWRow + tp_slot(16 * ks + 4 * g, xc >> 3) * 4;
-      const bf16x8_t av = *reinterpret_cast<const bf16x8_t*>(s_x + xoff);
+      bf16x8_t av[MT];
+      int xoff[MT];
+#pragma unroll
+      for (int m = 0; m < MT; ++m) {
+        const int xc = 16 * (wave + 8 * m) + r;  // column of the slice
+        xoff[m] = xc * kWRow + tp_slot(16 * ks + 4 * g, xc >> 3) * 4;
+        av[m] = *reinterpret_cast<const bf16x8_t*>(s_x + xoff[m]);
+      }
 #pragma unroll
       for (int ft = 0; ft < NTF; ++ft) {
         const int off = (16 * ft + r) * kWRow + (32 * ks + 8 * g) * 2;
         const bf16x8_t uh = *reinterpret_cast<const bf16x8_t*>(s_uh + off);
-        acc[ft] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(av, uh, acc[ft], 0, 0, 0);
-        acc[ft] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(av, *reinterpret_cast<const bf16x8_t*>(s_ul + off), acc[ft], 0, 0, 0);
-        if constexpr (F32)
-          acc[ft] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(*reinterpret_cast<const bf16x8_t*>(s_xl + xoff), uh,
-                                                            acc[ft], 0, 0, 0);
+        const bf16x8_t ul = *reinterpret_cast<const bf16x8_t*>(s_ul + off);
+#pragma unroll
+        for (int m = 0; m < MT; ++m) {
+          acc[m][ft] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(av[m], uh, acc[m][ft], 0, 0, 0);
+          acc[m][ft] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(av[m], ul, acc[m][ft], 0, 0, 0);
+          if constexpr (F32)
+            acc[m][ft] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(
+                *reinterpret_cast<const bf16x8_t*>(s_xl + xoff[m]), uh, acc[m][ft], 0, 0, 0);
+        }
       }
     }
     __syncthreads();
   };
+  constexpr int U = PF * TD / (PF % TD == 0 || TD % PF == 0 ? (PF < TD ? PF : TD) : 1);  // lcm
   XStep st[PF];
-  load_step(tb, cur);
+  Step tk[TD];
+#pragma unroll
+  for (int q = 0; q < TD; ++q) load_step(tb + q * kWTok, tk[q]);
 #pragma unroll
   for (int q = 0; q < PF; ++q) load_x(tb + q * kWTok, st[q]);
-  for (int64_t t = tb; t < te; t += PF * kWTok) {  // uniform; steps past te read nothing
+  for (int64_t t = tb; t < te; t += U * kWTok) {  // uniform; steps past te read nothing
 #pragma unroll
-    for (int q = 0; q < PF; ++q)
-      if (t + q * kWTok < te) run_step(t + q * kWTok, st[q]);
+    for (int q = 0; q < U; ++q)
+      if (t + q * kWTok < te) run_step(t + q * kWTok, st[q % PF], tk[q % TD]);
   }
   // partial W of this range: lane (feature column r, g) holds rows 4g .. 4g + 3
+  // of each of its column tiles
   float* W = a.work + (int64_t)rng * NC * FD;
 #pragma unroll
-  for (int ft = 0; ft < NTF; ++ft)
+  for (int m = 0; m < MT; ++m)
 #pragma unroll
-    for (int j = 0; j < 4; ++j) {
-      const int k = k0 + 16 * wave + 4 * g + j;
-      const int f = 16 * ft + r;
-      if (k < NC && f < FD) W[(int64_t)k * FD + f] = acc[ft][j];
-    }
-  if (ab_slice) {  // alpha / bias partials: sum the 32 token-pair slots of each feature
+    for (int ft = 0; ft < NTF; ++ft)
 #pragma unroll
-    for (int u = 0; u < UPT; ++u) {
-      const int idx = tid + 512 * u;
-      s_ab[0][idx / F16][idx % F16] = sb[u];
-      s_ab[1][idx / F16][idx % F16] = sa[u];
-    }
-    __syncthreads();
-    float* ab = a.work + (int64_t)gridDim.y * NC * FD + (int64_t)rng * 2 * FD;
-    for (int f = tid; f < FD; f += 512) {
-      float b = 0.f, al = 0.f;
-      for (int q = 0; q < kWTok / 2; ++q) {
-        b += s_ab[0][q][f];
-        al += s_ab[1][q][f];
+      for (int j = 0; j < 4; ++j) {
+        const int k = k0 + 16 * (wave + 8 * m) + 4 * g + j;
+        const int f = 16 * ft + r;
+        if (k < NC && f < FD) W[(int64_t)k * FD + f] = acc[m][ft][j];
       }
-      ab[f] = b;
-      ab[FD + f] = al;
-    }
-  }
 }
 
-// Two steps of x in flight where that keeps four waves a SIMD without spills
-// (bf16, FD <= 32: 128 VGPRs); wider features and fp32 x keep one.
+// Column tiles a wave (MT), steps of x (PF) and of the per-token values (TD)
+// in flight, and the waves per SIMD each instance is held to.  Measured at
+// 16384 tokens, n = 4 and 8192 tokens, n = 8 (C = 768; partials + reduction):
+//   bf16, FD <= 32: MT 1, PF 2, TD 2 at two workgroups a CU (29.2 us; 256-column
+//     slices 31.2 us: the step's chain of waits and barriers bounds it, not
+//     the per-column work they halve);
+//   bf16, FD > 32: MT 2, PF 2, TD 2 at one workgroup a CU (41.0 us; MT 1 at two
+//     a CU 50.3 us, with x one step ahead 65.8 us);
+//   fp32 x: PF 2, TD 1, and MT 2 with PF 1 where FD > 32 (C2 54.3 us, C5 67.7 us).
+template <int NTF, bool F32>
+constexpr int weights_mt() {
+  return NTF >= 3 ? 2 : 1;
+}
 template <int NTF, bool F32>
 constexpr int weights_pf() {
-  return !F32 && NTF <= 2 ? 2 : 1;
+  return F32 && NTF >= 3 ? 1 : 2;
 }
+template <int NTF, bool F32>
+constexpr int weights_td() {
+  return !F32 ? 2 : 1;
+}
+template <int NTF, bool F32>
+constexpr int weights_wpe() {
+  return NTF >= 3 ? 2 : 4;
+}
+#define WEIGHTS_INST(NTF, F32)                                                                           \
+  weights_mfma_kernel<NTF, F32, weights_mt<NTF, F32>(), weights_pf<NTF, F32>(), weights_td<NTF, F32>(), \
+                      weights_wpe<NTF, F32>()>
 
 // Workgroups of weights_mfma_kernel<NTF, F32> one CU holds at once (from its
 // registers and LDS; cached per instance).
@@ -903,8 +994,7 @@ static int weights_wg_per_cu() {
   static int cached = 0;
   if (cached == 0) {
     int blocks = 0;
-    if (hipOccupancyMaxActiveBlocksPerMultiprocessor(
-            &blocks, weights_mfma_kernel<NTF, F32, weights_pf<NTF, F32>()>, 512, 0) != hipSuccess ||
+    if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&blocks, WEIGHTS_INST(NTF, F32), 512, 0) != hipSuccess ||
         blocks < 1)
       blocks = 1;
     cached = blocks;
@@ -917,16 +1007,21 @@ static int weights_wg_per_cu(const WeightsArgs& a) {
   return a.x_dtype == kF32 ? weights_wg_per_cu<NTF, true>() : weights_wg_per_cu<NTF, false>();
 }
 
+// Columns of one workgroup's slice for the instance a launch takes.
+template <int NTF>
+static int weights_slice_cols(const WeightsArgs& a) {
+  return kWCols * (a.x_dtype == kF32 ? weights_mt<NTF, true>() : weights_mt<NTF, false>());
+}
+
 template <int NTF>
 static hipError_t launch_weights_mfma(const WeightsArgs& a, int R, int64_t per, hipStream_t s) {
   const int NC = a.n * a.C;
-  const dim3 grid((unsigned)((NC + kWCols - 1) / kWCols), (unsigned)R);
+  const int wc = weights_slice_cols<NTF>(a);
+  const dim3 grid((unsigned)((NC + wc - 1) / wc + 1), (unsigned)R);  // + the alpha / bias workgroup
   if (a.x_dtype == kF32)
-    hipLaunchKernelGGL((weights_mfma_kernel<NTF, true, weights_pf<NTF, true>()>), grid, dim3(512), 0,
-                       s, a, per);
+    hipLaunchKernelGGL((WEIGHTS_INST(NTF, true)), grid, dim3(512), 0, s, a, per);
   else
-    hipLaunchKernelGGL((weights_mfma_kernel<NTF, false, weights_pf<NTF, false>()>), grid, dim3(512),
-                       0, s, a, per);
+    hipLaunchKernelGGL((WEIGHTS_INST(NTF, false)), grid, dim3(512), 0, s, a, per);
   return hipGetLastError();
 }
 
@@ -935,8 +1030,13 @@ hipError_t launch_pre_bwd_weights(const WeightsArgs& a, hipStream_t s) {
   const int64_t NC = (int64_t)a.n * a.C;
   const int64_t qb = (NC * FD + 255) / 256;
   const int ntf = (FD + 15) / 16;
+  // The MFMA kernel reads g_raw and mixes as 16-byte feature quads (FD % 4 == 0:
+  // every mode but MHCHead at n = 2) at 32-bit per-range offsets: (per + 64) * FD
+  // * 4 < 2^31 with per <= M (up to 6.7 M tokens at FD = 80 in one range).
   const bool mfma = (a.x_dtype == kBF16 || a.x_dtype == kF32) && NC % 8 == 0 &&
                     (reinterpret_cast<uintptr_t>(a.x) & 15) == 0 &&
+                    ((reinterpret_cast<uintptr_t>(a.g_raw) | reinterpret_cast<uintptr_t>(a.mixes)) & 15) == 0 &&
+                    FD % 4 == 0 && (a.M + kWTok) * FD * 4 < ((int64_t)1 << 31) &&
                     (ntf == 1 || ntf == 2 || ntf == 3 || ntf == 5);  // FD <= 80 (LDS)
   int R = weight_ranges(a.M);
   if (a.max_ranges > 0 && R > a.max_ranges) R = a.max_ranges;  // smaller workspace
@@ -946,14 +1046,14 @@ hipError_t launch_pre_bwd_weights(const WeightsArgs& a, hipStream_t s) {
     // workgroups holds (every CU as full as the kernel's registers and LDS
     // allow; two rounds if one round leaves fewer than four ranges), so no
     // short last round of stragglers follows the full ones.
-    int wpc = 1;
+    int wpc = 1, wc = kWCols;
     switch (ntf) {
-      case 1: wpc = weights_wg_per_cu<1>(a); break;
-      case 2: wpc = weights_wg_per_cu<2>(a); break;
-      case 3: wpc = weights_wg_per_cu<3>(a); break;
-      default: wpc = weights_wg_per_cu<5>(a); break;
+      case 1: wpc = weights_wg_per_cu<1>(a); wc = weights_slice_cols<1>(a); break;
+      case 2: wpc = weights_wg_per_cu<2>(a); wc = weights_slice_cols<2>(a); break;
+      case 3: wpc = weights_wg_per_cu<3>(a); wc = weights_slice_cols<3>(a); break;
+      default: wpc = weights_wg_per_cu<5>(a); wc = weights_slice_cols<5>(a); break;
     }
-    const int64_t slices = (NC + kWCols - 1) / kWCols;
+    const int64_t slices = (NC + wc - 1) / wc + 1;  // + the alpha / bias workgroup
     const int64_t cap = (int64_t)wpc * device_cus();
     int64_t want = cap / slices;
     if (want < 4) want = 2 * cap / slices;
