@@ -158,10 +158,13 @@ def _pre_case(dev, kind, n, C, M, dtype, seed):
 
 @pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
 # n = 16: FD = 288 features, more than a 256-thread workgroup has threads;
-# n = 8 fp32: the MFMA kernel with x streamed per chunk (C = 768, 1024)
+# n = 8 fp32: the MFMA kernel with x streamed per chunk (C = 768, 1024);
+# n = 8, C = 200: the weight kernel's 256-column slices with a partial last
+# slice (n*C = 1600) and a ragged last token range; n = 6: FD = 48, three
+# feature tiles (two column tiles a wave as well)
 @pytest.mark.parametrize("n,C,M", [(4, 64, 24), (4, 768, 300), (2, 100, 17), (8, 768, 40),
                                    (1, 64, 9), (4, 256, 1100), (16, 64, 20), (16, 256, 300),
-                                   (8, 1024, 70)])
+                                   (8, 1024, 70), (8, 200, 130), (6, 64, 77)])
 def test_pre_full_bwd_vs_oracle(dev, dtype, n, C, M):
     """g_x, g_phi, alphas and biases of the full pre phase for given upstream
     gradients of (sublayer_in, h_pre, h_post, h_res_raw)."""
