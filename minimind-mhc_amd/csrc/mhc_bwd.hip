@@ -224,9 +224,19 @@ struct Chunk8<true> {
   }
 };
 
-template <int N, int MODE, int NW, int KJ, bool F32>
+// Row pieces for bf16 x / g_x where C % 32 == 0: C2 pre backward 68.1-69.0 ->
+// 64.6-65.4 us, MHCHead 62.9-63.7 -> 60.6-61.1 us; n = 8 (C5) unchanged.
+constexpr bool kPreBwdRowPieces = true;
+// RS (bf16, C % 32 == 0): each wave takes pairs of adjacent chunks (64
+// columns, contiguous in a token's row) and moves the tile's x in and g_x out
+// as whole 128-byte row pieces, regrouped between that layout and the MFMA
+// one through a 2 KiB LDS block of its own (no barrier: one wave writes and
+// reads it, in order).  The MFMA layout alone covers 16 rows x 64 bytes per
+// load or store, half of each 128-byte line.
+template <int N, int MODE, int NW, int KJ, bool F32, bool RS = false>
 __global__ __launch_bounds__(NW * 64) __attribute__((amdgpu_waves_per_eu(F32 ? 2 : 4))) void pre_bwd_mfma_kernel(PreBwdArgs a) {
   using XV = Chunk8<F32>;
+  static_assert(!RS || (!F32 && KJ % 2 == 0), "row pieces: bf16, whole chunk pairs");
   // The tile's x chunks stay in registers from the gh sums to the g_x stores,
   // except for fp32 at n = 8: 16-wave workgroups hold 128 VGPRs a lane and
   // 12 fp32 chunks alone take 96 of them, so there each chunk is loaded where
@@ -240,6 +250,7 @@ __global__ __launch_bounds__(NW * 64) __attribute__((amdgpu_waves_per_eu(F32 ? 2
   __shared__ float s_mx[TM][KS * 32];    // mixes_raw, zero padded
   __shared__ float s_gm[TM][KS * 32];    // alpha * g_raw, zero padded
   __shared__ float s_hp[TM][N];          // h_pre = sigmoid + pre_eps (fp32 recompute)
+  __shared__ __attribute__((aligned(16))) U32x4 s_rs[RS ? NW : 1][TM][8];  // per-wave regroup block
 
   const int tid = threadIdx.x;
   const int lane = tid & 63;
@@ -259,8 +270,10 @@ __global__ __launch_bounds__(NW * 64) __attribute__((amdgpu_waves_per_eu(F32 ? 2
   const auto rgx = make_rsrc(static_cast<unsigned char*>(a.g_x) + t0 * NC * ES, (uint32_t)valid * NC * ES);
 
   // chunk j of this wave: stream ci, first column c0; lane column c0 + 8g
+  // (RS: chunks 2 (wave + NW j/2) + j % 2, pairs of adjacent ones)
+  auto kidx = [&](int j) { return RS ? 2 * (wave + NW * (j >> 1)) + (j & 1) : wave + NW * j; };
   auto chunk = [&](int j, int& ci, int& c0) {
-    const int k = wave + NW * j;
+    const int k = kidx(j);
     ci = k < NCH ? k / NCB : 0;
     c0 = k < NCH ? (k - ci * NCB) * 32 : C;  // C: no columns (loads read zeros)
   };
@@ -272,8 +285,36 @@ __global__ __launch_bounds__(NW * 64) __attribute__((amdgpu_waves_per_eu(F32 ? 2
   };
   XV xs[XRES ? KJ : 1];
   if constexpr (XRES) {
+    if constexpr (RS) {
+      // pair p: row pieces (token 8i + l/8, 16-byte piece l % 8 of the pair's
+      // 128 bytes) into xs[2p + i], then through LDS into the MFMA layout;
+      // piece q of row t sits in slot q ^ (t & 7) (conflict-free both ways)
 #pragma unroll
-    for (int j = 0; j < KJ; ++j) xs[j] = x_chunk(j);
+      for (int p = 0; p < KJ / 2; ++p) {
+        const int col = 64 * (wave + NW * p);
+#pragma unroll
+        for (int i = 0; i < 2; ++i) {
+          const int tt = 8 * i + (lane >> 3);
+          const int pc = lane & 7;
+          xs[2 * p + i] = XV::load(rx, col + 8 * pc < NC ? (uint32_t)(tt * NC + col + 8 * pc) * ES : kBufOob);
+        }
+      }
+#pragma unroll
+      for (int p = 0; p < KJ / 2; ++p) {
+#pragma unroll
+        for (int i = 0; i < 2; ++i) {
+          const int tt = 8 * i + (lane >> 3);
+          s_rs[wave][tt][(lane & 7) ^ (tt & 7)] = xs[2 * p + i].v;
+        }
+        __builtin_amdgcn_fence(__ATOMIC_ACQ_REL, "wavefront");
+#pragma unroll
+        for (int h = 0; h < 2; ++h) xs[2 * p + h].v = s_rs[wave][r][(4 * h + g) ^ (r & 7)];
+        __builtin_amdgcn_fence(__ATOMIC_ACQ_REL, "wavefront");
+      }
+    } else {
+#pragma unroll
+      for (int j = 0; j < KJ; ++j) xs[j] = x_chunk(j);
+    }
   }
   const float inv = r < valid ? a.inv_rms[t0 + r] : 0.f;
 
@@ -349,7 +390,7 @@ __global__ __launch_bounds__(NW * 64) __attribute__((amdgpu_waves_per_eu(F32 ? 2
       const float acc = XV::dot(gvb[u], XRES ? xs[j] : xvb[u]);
       const float a16 = acc + xor_lane16(acc);
       const float a32 = a16 + xor_lane32(a16);
-      if (g == 0) s_gp[wave + NW * j][r] = a32;
+      if (g == 0) s_gp[kidx(j)][r] = a32;
     }
   }
   __syncthreads();
@@ -500,7 +541,26 @@ __global__ __launch_bounds__(NW * 64) __attribute__((amdgpu_waves_per_eu(F32 ? 2
     }
     // whole offset in the vector offset, scalar offset the literal 0 (a
     // 128-bit store reads its data registers after issue)
-    XV::store(rgx, ok ? (uint32_t)(r * NC + ci * C + c0 + 8 * g) * ES : kBufOob, v);
+    if constexpr (RS) {  // both chunks of the pair through LDS, then two row stores
+      U32x4 o;
+#pragma unroll
+      for (int e = 0; e < 4; ++e) o.v[e] = pack_bf16x2(v[2 * e], v[2 * e + 1]);
+      s_rs[wave][r][(4 * (j & 1) + g) ^ (r & 7)] = o;
+      if (j & 1) {
+        __builtin_amdgcn_fence(__ATOMIC_ACQ_REL, "wavefront");
+        const int col = 64 * (wave + NW * (j >> 1));
+#pragma unroll
+        for (int i = 0; i < 2; ++i) {
+          const int tt = 8 * i + (lane >> 3);
+          const int pc = lane & 7;
+          buf_store16(rgx, col + 8 * pc < NC ? (uint32_t)(tt * NC + col + 8 * pc) * ES : kBufOob,
+                      s_rs[wave][tt][pc ^ (tt & 7)]);
+        }
+        __builtin_amdgcn_fence(__ATOMIC_ACQ_REL, "wavefront");
+      }
+    } else {
+      XV::store(rgx, ok ? (uint32_t)(r * NC + ci * C + c0 + 8 * g) * ES : kBufOob, v);
+    }
   }
 }
 
@@ -508,6 +568,13 @@ __global__ __launch_bounds__(NW * 64) __attribute__((amdgpu_waves_per_eu(F32 ? 2
 // n in {2, 4} (8 waves) and n = 8 (16 waves, bf16 only).
 template <int N, int MODE, int NW, int KJ, bool F32>
 static hipError_t launch_pre_bwd_inst(const PreBwdArgs& a, hipStream_t s) {
+  if constexpr (kPreBwdRowPieces && !F32 && KJ % 2 == 0) {
+    if (a.C % 32 == 0) {  // a chunk pair's 64 columns contiguous in the row
+      hipLaunchKernelGGL((pre_bwd_mfma_kernel<N, MODE, NW, KJ, F32, true>), dim3((unsigned)((a.M + 15) / 16)),
+                         dim3(NW * 64), 0, s, a);
+      return hipGetLastError();
+    }
+  }
   hipLaunchKernelGGL((pre_bwd_mfma_kernel<N, MODE, NW, KJ, F32>), dim3((unsigned)((a.M + 15) / 16)),
                      dim3(NW * 64), 0, s, a);
   return hipGetLastError();
