@@ -224,15 +224,18 @@ struct Chunk8<true> {
   }
 };
 
-// Row pieces for bf16 x / g_x where C % 32 == 0: C2 pre backward 68.1-69.0 ->
-// 64.6-65.4 us, MHCHead 62.9-63.7 -> 60.6-61.1 us; n = 8 (C5) unchanged.
+// Row pieces for bf16 x / g_x where C % 64 == 0: C2 pre backward 68.1-69.0 ->
+// 64.6-65.4 us, MHCHead 62.9-63.7 -> 60.6-61.1 us, n = 8 (C5) unchanged; with
+// the gh sums' g_sub as row pieces too: C2 63.3 -> 60.5 us, C5 97.5 -> 92.4 us,
+// MHCHead 59.2 -> 57.2 us (one box).
 constexpr bool kPreBwdRowPieces = true;
-// RS (bf16, C % 32 == 0): each wave takes pairs of adjacent chunks (64
-// columns, contiguous in a token's row) and moves the tile's x in and g_x out
-// as whole 128-byte row pieces, regrouped between that layout and the MFMA
-// one through a 2 KiB LDS block of its own (no barrier: one wave writes and
-// reads it, in order).  The MFMA layout alone covers 16 rows x 64 bytes per
-// load or store, half of each 128-byte line.
+// RS (bf16, C % 64 == 0): each wave takes pairs of adjacent chunks (64
+// columns of one stream, contiguous in a token's row) and moves the tile's x
+// in, g_sub in (for the gh sums) and g_x out as whole 128-byte row pieces,
+// regrouped between that layout and the MFMA one through a 2 KiB LDS block of
+// its own (no barrier: one wave writes and reads it, in order).  The MFMA
+// layout alone covers 16 rows x 64 bytes per load or store, half of each
+// 128-byte line.
 template <int N, int MODE, int NW, int KJ, bool F32, bool RS = false>
 __global__ __launch_bounds__(NW * 64) __attribute__((amdgpu_waves_per_eu(F32 ? 2 : 4))) void pre_bwd_mfma_kernel(PreBwdArgs a) {
   using XV = Chunk8<F32>;
@@ -375,13 +378,39 @@ __global__ __launch_bounds__(NW * 64) __attribute__((amdgpu_waves_per_eu(F32 ? 2
   for (int j0 = 0; j0 < KJ; j0 += GB) {
     XV gvb[GB];
     XV xvb[XRES ? 1 : GB];
+    if constexpr (RS) {  // a pair's g_sub: 64 columns of one stream's row (C % 64 == 0)
 #pragma unroll
-    for (int u = 0; u < GB; ++u) {
-      int ci, c0;
-      chunk(j0 + u, ci, c0);
-      const bool ok = j0 + u < KJ && c0 + 8 * g < C;
-      gvb[u] = XV::load(rgs, ok ? (uint32_t)(r * C + c0 + 8 * g) * ES : kBufOob);
-      if constexpr (!XRES) xvb[u] = j0 + u < KJ ? x_chunk(j0 + u) : XV::load(rx, kBufOob);
+      for (int u = 0; u < GB; u += 2) {
+        int ci, c0;
+        chunk(j0 + u, ci, c0);
+#pragma unroll
+        for (int i = 0; i < 2; ++i) {
+          const int tt = 8 * i + (lane >> 3);
+          const int pc = lane & 7;
+          gvb[u + i] = XV::load(rgs, j0 + u < KJ && c0 + 8 * pc < C ? (uint32_t)(tt * C + c0 + 8 * pc) * ES : kBufOob);
+        }
+      }
+#pragma unroll
+      for (int u = 0; u < GB; u += 2) {
+#pragma unroll
+        for (int i = 0; i < 2; ++i) {
+          const int tt = 8 * i + (lane >> 3);
+          s_rs[wave][tt][(lane & 7) ^ (tt & 7)] = gvb[u + i].v;
+        }
+        __builtin_amdgcn_fence(__ATOMIC_ACQ_REL, "wavefront");
+#pragma unroll
+        for (int h = 0; h < 2; ++h) gvb[u + h].v = s_rs[wave][r][(4 * h + g) ^ (r & 7)];
+        __builtin_amdgcn_fence(__ATOMIC_ACQ_REL, "wavefront");
+      }
+    } else {
+#pragma unroll
+      for (int u = 0; u < GB; ++u) {
+        int ci, c0;
+        chunk(j0 + u, ci, c0);
+        const bool ok = j0 + u < KJ && c0 + 8 * g < C;
+        gvb[u] = XV::load(rgs, ok ? (uint32_t)(r * C + c0 + 8 * g) * ES : kBufOob);
+        if constexpr (!XRES) xvb[u] = j0 + u < KJ ? x_chunk(j0 + u) : XV::load(rx, kBufOob);
+      }
     }
 #pragma unroll
     for (int u = 0; u < GB; ++u) {
@@ -569,7 +598,7 @@ __global__ __launch_bounds__(NW * 64) __attribute__((amdgpu_waves_per_eu(F32 ? 2
 template <int N, int MODE, int NW, int KJ, bool F32>
 static hipError_t launch_pre_bwd_inst(const PreBwdArgs& a, hipStream_t s) {
   if constexpr (kPreBwdRowPieces && !F32 && KJ % 2 == 0) {
-    if (a.C % 32 == 0) {  // a chunk pair's 64 columns contiguous in the row
+    if (a.C % 64 == 0) {  // a chunk pair's 64 columns in one stream's row
       hipLaunchKernelGGL((pre_bwd_mfma_kernel<N, MODE, NW, KJ, F32, true>), dim3((unsigned)((a.M + 15) / 16)),
                          dim3(NW * 64), 0, s, a);
       return hipGetLastError();
