@@ -229,6 +229,10 @@ struct Chunk8<true> {
 // the gh sums' g_sub as row pieces too: C2 63.3 -> 60.5 us, C5 97.5 -> 92.4 us,
 // MHCHead 59.2 -> 57.2 us (one box).
 constexpr bool kPreBwdRowPieces = true;
+// Phi operands from contiguous 16-byte pieces of each chunk's phi block,
+// regrouped through LDS, instead of 16 phi rows x 64 bytes an instruction:
+// C5 pre backward 94.5 -> 76.7 us, C2 61.7 -> 59.7 us (one box).
+constexpr bool kPreBwdPhiBlock = true;
 // RS (bf16, C % 64 == 0): each wave takes pairs of adjacent chunks (64
 // columns of one stream, contiguous in a token's row) and moves the tile's x
 // in, g_sub in (for the gh sums) and g_x out as whole 128-byte row pieces,
@@ -254,6 +258,14 @@ __global__ __launch_bounds__(NW * 64) __attribute__((amdgpu_waves_per_eu(F32 ? 2
   __shared__ float s_gm[TM][KS * 32];    // alpha * g_raw, zero padded
   __shared__ float s_hp[TM][N];          // h_pre = sigmoid + pre_eps (fp32 recompute)
   __shared__ __attribute__((aligned(16))) U32x4 s_rs[RS ? NW : 1][TM][8];  // per-wave regroup block
+  // PB: a chunk's phi operands are one contiguous block of phi (its 32 rows x
+  // FD features), read with whole 16-byte pieces along the lanes and regrouped
+  // into the A layout through a block of LDS per wave.
+  // (the shapes whose chunk loop loads a chunk's operand set: KS == 1 or at
+  // most 12 chunks a wave)
+  constexpr bool PB = RS && FD % 8 == 0 && kPreBwdPhiBlock && (KS == 1 || KJ <= 12);
+  constexpr int NPB = (4 * FD + 63) / 64;  // 64-lane loads of a chunk's 4 * FD pieces
+  __shared__ __attribute__((aligned(16))) U32x4 s_pb[PB ? NW : 1][PB ? 4 * FD : 1];
 
   const int tid = threadIdx.x;
   const int lane = tid & 63;
@@ -502,17 +514,27 @@ __global__ __launch_bounds__(NW * 64) __attribute__((amdgpu_waves_per_eu(F32 ? 2
   constexpr bool PF = KS == 1;
   constexpr bool CH = !PF && KJ <= 12;
   struct ChunkIn {
-    XV av[2][KS];
+    XV av[PB ? 1 : 2][PB ? 1 : KS];
+    U32x4 pb[PB ? NPB : 1];  // PB: the chunk's phi block, 16-byte pieces along the lanes
     XV gv;
     XV xv[XRES ? 1 : 1];  // the chunk's x when it is not held from the start
   };
   auto load_chunk = [&](int j, ChunkIn& in) {
     int ci, c0;
     chunk(j, ci, c0);
+    if constexpr (PB) {
+      const uint32_t base = (uint32_t)((ci * C + c0) * FD) * ES;
 #pragma unroll
-    for (int h = 0; h < 2; ++h)
+      for (int i = 0; i < NPB; ++i) {
+        const int pc = 64 * i + lane;
+        in.pb[i] = buf_load16(rphi, c0 < C && pc < 4 * FD ? base + 16u * pc : kBufOob);
+      }
+    } else {
 #pragma unroll
-      for (int ks = 0; ks < KS; ++ks) in.av[h][ks] = phi_op(j, h, ks);
+      for (int h = 0; h < 2; ++h)
+#pragma unroll
+        for (int ks = 0; ks < KS; ++ks) in.av[h][ks] = phi_op(j, h, ks);
+    }
     const bool ok = c0 + 8 * g < C;
     in.gv = XV::load(rgs, ok ? (uint32_t)(r * C + c0 + 8 * g) * ES : kBufOob);
     if constexpr (!XRES) in.xv[0] = x_chunk(j);
@@ -536,13 +558,30 @@ __global__ __launch_bounds__(NW * 64) __attribute__((amdgpu_waves_per_eu(F32 ? 2
     int ci, c0;
     chunk(j, ci, c0);
     const bool ok = c0 + 8 * g < C;
+    // PB: A-row r of half h is row 8 (r / 4) + 4h + r % 4 of the block, lane
+    // group g features 32 ks + 8g .. + 7: piece row * FD / 8 + 4 ks + g
+    XV avb[PB ? 2 : 1][PB ? KS : 1];
+    if constexpr (PB) {
+#pragma unroll
+      for (int i = 0; i < NPB; ++i)
+        if (64 * i + lane < 4 * FD) s_pb[wave][64 * i + lane] = cur.pb[i];
+      __builtin_amdgcn_fence(__ATOMIC_ACQ_REL, "wavefront");
+#pragma unroll
+      for (int h = 0; h < 2; ++h)
+#pragma unroll
+        for (int ks = 0; ks < KS; ++ks) {
+          const int rr = 8 * (r >> 2) + 4 * h + (r & 3);
+          avb[h][ks].v = 32 * ks + 8 * g < FD ? s_pb[wave][rr * (FD / 8) + 4 * ks + g] : U32x4{{0u, 0u, 0u, 0u}};
+        }
+      __builtin_amdgcn_fence(__ATOMIC_ACQ_REL, "wavefront");
+    }
     f32x4_t d2[2];
 #pragma unroll
     for (int h = 0; h < 2; ++h) {
       f32x4_t d = f32x4_t{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
       for (int ks = 0; ks < KS; ++ks) {
-        const XV av = PF || CH ? cur.av[h][ks] : phi_op(j, h, ks);
+        const XV av = PB ? avb[PB ? h : 0][PB ? ks : 0] : (PF || CH ? cur.av[PB ? 0 : h][PB ? 0 : ks] : phi_op(j, h, ks));
         if constexpr (F32) {  // phi_hi . (b_hi + b_lo) + phi_lo . b_hi
           const bf16x8_t ahi = XV::hi(av);
           const bf16x8_t alo = XV::lo(av);
