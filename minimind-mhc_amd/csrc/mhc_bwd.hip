@@ -233,7 +233,8 @@ constexpr bool kPreBwdRowPieces = true;
 // regrouped through LDS, instead of 16 phi rows x 64 bytes an instruction:
 // C5 pre backward 94.5 -> 76.7 us, C2 61.7 -> 59.7 us (one box).
 constexpr bool kPreBwdPhiBlock = true;
-// RS (bf16, C % 64 == 0): each wave takes pairs of adjacent chunks (64
+// RS (bf16, or fp32 at n <= 4 where x stays resident; C % 64 == 0; fp32 C2
+// 144.4 -> 128.6 us): each wave takes pairs of adjacent chunks (64
 // columns of one stream, contiguous in a token's row) and moves the tile's x
 // in, g_sub in (for the gh sums) and g_x out as whole 128-byte row pieces,
 // regrouped between that layout and the MFMA one through a 2 KiB LDS block of
@@ -243,7 +244,7 @@ constexpr bool kPreBwdPhiBlock = true;
 template <int N, int MODE, int NW, int KJ, bool F32, bool RS = false>
 __global__ __launch_bounds__(NW * 64) __attribute__((amdgpu_waves_per_eu(F32 ? 2 : 4))) void pre_bwd_mfma_kernel(PreBwdArgs a) {
   using XV = Chunk8<F32>;
-  static_assert(!RS || (!F32 && KJ % 2 == 0), "row pieces: bf16, whole chunk pairs");
+  static_assert(!RS || ((!F32 || N <= 4) && KJ % 2 == 0), "row pieces: x resident, whole chunk pairs");
   // The tile's x chunks stay in registers from the gh sums to the g_x stores,
   // except for fp32 at n = 8: 16-wave workgroups hold 128 VGPRs a lane and
   // 12 fp32 chunks alone take 96 of them, so there each chunk is loaded where
@@ -257,15 +258,22 @@ __global__ __launch_bounds__(NW * 64) __attribute__((amdgpu_waves_per_eu(F32 ? 2
   __shared__ float s_mx[TM][KS * 32];    // mixes_raw, zero padded
   __shared__ float s_gm[TM][KS * 32];    // alpha * g_raw, zero padded
   __shared__ float s_hp[TM][N];          // h_pre = sigmoid + pre_eps (fp32 recompute)
-  __shared__ __attribute__((aligned(16))) U32x4 s_rs[RS ? NW : 1][TM][8];  // per-wave regroup block
+  // 16-byte pieces: XP per 8 columns, PPR in a chunk pair's row, RPI rows and
+  // NRI row-piece loads per pair
+  constexpr int XP = F32 ? 2 : 1;
+  constexpr int PPR = 8 * XP;
+  constexpr int RPI = 64 / PPR;
+  constexpr int NRI = TM / RPI;
+  __shared__ __attribute__((aligned(16))) U32x4 s_rs[RS ? NW : 1][TM][PPR];  // per-wave regroup block
   // PB: a chunk's phi operands are one contiguous block of phi (its 32 rows x
   // FD features), read with whole 16-byte pieces along the lanes and regrouped
   // into the A layout through a block of LDS per wave.
   // (the shapes whose chunk loop loads a chunk's operand set: KS == 1 or at
   // most 12 chunks a wave)
   constexpr bool PB = RS && FD % 8 == 0 && kPreBwdPhiBlock && (KS == 1 || KJ <= 12);
-  constexpr int NPB = (4 * FD + 63) / 64;  // 64-lane loads of a chunk's 4 * FD pieces
-  __shared__ __attribute__((aligned(16))) U32x4 s_pb[PB ? NW : 1][PB ? 4 * FD : 1];
+  constexpr int NPC = 4 * FD * XP;         // 16-byte pieces of a chunk's phi block
+  constexpr int NPB = (NPC + 63) / 64;     // 64-lane loads of them
+  __shared__ __attribute__((aligned(16))) U32x4 s_pb[PB ? NW : 1][PB ? NPC : 1];
 
   const int tid = threadIdx.x;
   const int lane = tid & 63;
@@ -287,6 +295,11 @@ __global__ __launch_bounds__(NW * 64) __attribute__((amdgpu_waves_per_eu(F32 ? 2
   // chunk j of this wave: stream ci, first column c0; lane column c0 + 8g
   // (RS: chunks 2 (wave + NW j/2) + j % 2, pairs of adjacent ones)
   auto kidx = [&](int j) { return RS ? 2 * (wave + NW * (j >> 1)) + (j & 1) : wave + NW * j; };
+  // 16-byte piece e of an 8-column chunk slice (bf16: the one; fp32: two)
+  auto piece = [](XV& c, int e) -> U32x4& {
+    if constexpr (F32) return c.v[e];
+    else { (void)e; return c.v; }
+  };
   auto chunk = [&](int j, int& ci, int& c0) {
     const int k = kidx(j);
     ci = k < NCH ? k / NCB : 0;
@@ -301,29 +314,33 @@ __global__ __launch_bounds__(NW * 64) __attribute__((amdgpu_waves_per_eu(F32 ? 2
   XV xs[XRES ? KJ : 1];
   if constexpr (XRES) {
     if constexpr (RS) {
-      // pair p: row pieces (token 8i + l/8, 16-byte piece l % 8 of the pair's
-      // 128 bytes) into xs[2p + i], then through LDS into the MFMA layout;
-      // piece q of row t sits in slot q ^ (t & 7) (conflict-free both ways)
+      // pair p: row pieces (token RPI i + l / PPR, 16-byte piece l % PPR of the
+      // pair's row) into the pair's XV registers, then through LDS into the
+      // MFMA layout; piece q of row t sits in slot q ^ (t & 7) (conflict-free
+      // both ways)
 #pragma unroll
       for (int p = 0; p < KJ / 2; ++p) {
         const int col = 64 * (wave + NW * p);
 #pragma unroll
-        for (int i = 0; i < 2; ++i) {
-          const int tt = 8 * i + (lane >> 3);
-          const int pc = lane & 7;
-          xs[2 * p + i] = XV::load(rx, col + 8 * pc < NC ? (uint32_t)(tt * NC + col + 8 * pc) * ES : kBufOob);
+        for (int i = 0; i < NRI; ++i) {
+          const int tt = RPI * i + lane / PPR;
+          const int pc = lane % PPR;
+          piece(xs[2 * p + i / XP], i % XP) =
+              buf_load16(rx, col + pc * (16 / (int)ES) < NC ? (uint32_t)(tt * NC + col) * ES + 16u * pc : kBufOob);
         }
       }
 #pragma unroll
       for (int p = 0; p < KJ / 2; ++p) {
 #pragma unroll
-        for (int i = 0; i < 2; ++i) {
-          const int tt = 8 * i + (lane >> 3);
-          s_rs[wave][tt][(lane & 7) ^ (tt & 7)] = xs[2 * p + i].v;
+        for (int i = 0; i < NRI; ++i) {
+          const int tt = RPI * i + lane / PPR;
+          s_rs[wave][tt][(lane % PPR) ^ (tt & 7)] = piece(xs[2 * p + i / XP], i % XP);
         }
         __builtin_amdgcn_fence(__ATOMIC_ACQ_REL, "wavefront");
 #pragma unroll
-        for (int h = 0; h < 2; ++h) xs[2 * p + h].v = s_rs[wave][r][(4 * h + g) ^ (r & 7)];
+        for (int h = 0; h < 2; ++h)
+#pragma unroll
+          for (int e = 0; e < XP; ++e) piece(xs[2 * p + h], e) = s_rs[wave][r][(PPR / 2 * h + XP * g + e) ^ (r & 7)];
         __builtin_amdgcn_fence(__ATOMIC_ACQ_REL, "wavefront");
       }
     } else {
@@ -396,22 +413,26 @@ __global__ __launch_bounds__(NW * 64) __attribute__((amdgpu_waves_per_eu(F32 ? 2
         int ci, c0;
         chunk(j0 + u, ci, c0);
 #pragma unroll
-        for (int i = 0; i < 2; ++i) {
-          const int tt = 8 * i + (lane >> 3);
-          const int pc = lane & 7;
-          gvb[u + i] = XV::load(rgs, j0 + u < KJ && c0 + 8 * pc < C ? (uint32_t)(tt * C + c0 + 8 * pc) * ES : kBufOob);
+        for (int i = 0; i < NRI; ++i) {
+          const int tt = RPI * i + lane / PPR;
+          const int pc = lane % PPR;
+          piece(gvb[u + i / XP], i % XP) =
+              buf_load16(rgs, j0 + u < KJ && c0 + pc * (16 / (int)ES) < C ? (uint32_t)(tt * C + c0) * ES + 16u * pc
+                                                                          : kBufOob);
         }
       }
 #pragma unroll
       for (int u = 0; u < GB; u += 2) {
 #pragma unroll
-        for (int i = 0; i < 2; ++i) {
-          const int tt = 8 * i + (lane >> 3);
-          s_rs[wave][tt][(lane & 7) ^ (tt & 7)] = gvb[u + i].v;
+        for (int i = 0; i < NRI; ++i) {
+          const int tt = RPI * i + lane / PPR;
+          s_rs[wave][tt][(lane % PPR) ^ (tt & 7)] = piece(gvb[u + i / XP], i % XP);
         }
         __builtin_amdgcn_fence(__ATOMIC_ACQ_REL, "wavefront");
 #pragma unroll
-        for (int h = 0; h < 2; ++h) gvb[u + h].v = s_rs[wave][r][(4 * h + g) ^ (r & 7)];
+        for (int h = 0; h < 2; ++h)
+#pragma unroll
+          for (int e = 0; e < XP; ++e) piece(gvb[u + h], e) = s_rs[wave][r][(PPR / 2 * h + XP * g + e) ^ (r & 7)];
         __builtin_amdgcn_fence(__ATOMIC_ACQ_REL, "wavefront");
       }
     } else {
@@ -527,7 +548,7 @@ __global__ __launch_bounds__(NW * 64) __attribute__((amdgpu_waves_per_eu(F32 ? 2
 #pragma unroll
       for (int i = 0; i < NPB; ++i) {
         const int pc = 64 * i + lane;
-        in.pb[i] = buf_load16(rphi, c0 < C && pc < 4 * FD ? base + 16u * pc : kBufOob);
+        in.pb[i] = buf_load16(rphi, c0 < C && pc < NPC ? base + 16u * pc : kBufOob);
       }
     } else {
 #pragma unroll
@@ -559,19 +580,23 @@ __global__ __launch_bounds__(NW * 64) __attribute__((amdgpu_waves_per_eu(F32 ? 2
     chunk(j, ci, c0);
     const bool ok = c0 + 8 * g < C;
     // PB: A-row r of half h is row 8 (r / 4) + 4h + r % 4 of the block, lane
-    // group g features 32 ks + 8g .. + 7: piece row * FD / 8 + 4 ks + g
+    // group g features 32 ks + 8g .. + 7: pieces (row * FD + 32 ks + 8g) XP / 8
+    // .. + XP - 1
     XV avb[PB ? 2 : 1][PB ? KS : 1];
     if constexpr (PB) {
 #pragma unroll
       for (int i = 0; i < NPB; ++i)
-        if (64 * i + lane < 4 * FD) s_pb[wave][64 * i + lane] = cur.pb[i];
+        if (64 * i + lane < NPC) s_pb[wave][64 * i + lane] = cur.pb[i];
       __builtin_amdgcn_fence(__ATOMIC_ACQ_REL, "wavefront");
 #pragma unroll
       for (int h = 0; h < 2; ++h)
 #pragma unroll
         for (int ks = 0; ks < KS; ++ks) {
           const int rr = 8 * (r >> 2) + 4 * h + (r & 3);
-          avb[h][ks].v = 32 * ks + 8 * g < FD ? s_pb[wave][rr * (FD / 8) + 4 * ks + g] : U32x4{{0u, 0u, 0u, 0u}};
+          const int p0 = rr * (FD * XP / 8) + 4 * XP * ks + XP * g;  // FD % 8 == 0
+#pragma unroll
+          for (int e = 0; e < XP; ++e)
+            piece(avb[h][ks], e) = 32 * ks + 8 * g < FD ? s_pb[wave][p0 + e] : U32x4{{0u, 0u, 0u, 0u}};
         }
       __builtin_amdgcn_fence(__ATOMIC_ACQ_REL, "wavefront");
     }
@@ -609,19 +634,23 @@ __global__ __launch_bounds__(NW * 64) __attribute__((amdgpu_waves_per_eu(F32 ? 2
     }
     // whole offset in the vector offset, scalar offset the literal 0 (a
     // 128-bit store reads its data registers after issue)
-    if constexpr (RS) {  // both chunks of the pair through LDS, then two row stores
-      U32x4 o;
+    if constexpr (RS) {  // both chunks of the pair through LDS, then NRI row stores
+      U32x4 o[XP];
 #pragma unroll
-      for (int e = 0; e < 4; ++e) o.v[e] = pack_bf16x2(v[2 * e], v[2 * e + 1]);
-      s_rs[wave][r][(4 * (j & 1) + g) ^ (r & 7)] = o;
+      for (int e = 0; e < 4 * XP; ++e) {
+        if constexpr (F32) o[e >> 2].v[e & 3] = __float_as_uint(v[e]);
+        else o[0].v[e] = pack_bf16x2(v[2 * e], v[2 * e + 1]);
+      }
+#pragma unroll
+      for (int e = 0; e < XP; ++e) s_rs[wave][r][(PPR / 2 * (j & 1) + XP * g + e) ^ (r & 7)] = o[e];
       if (j & 1) {
         __builtin_amdgcn_fence(__ATOMIC_ACQ_REL, "wavefront");
         const int col = 64 * (wave + NW * (j >> 1));
 #pragma unroll
-        for (int i = 0; i < 2; ++i) {
-          const int tt = 8 * i + (lane >> 3);
-          const int pc = lane & 7;
-          buf_store16(rgx, col + 8 * pc < NC ? (uint32_t)(tt * NC + col + 8 * pc) * ES : kBufOob,
+        for (int i = 0; i < NRI; ++i) {
+          const int tt = RPI * i + lane / PPR;
+          const int pc = lane % PPR;
+          buf_store16(rgx, col + pc * (16 / (int)ES) < NC ? (uint32_t)(tt * NC + col) * ES + 16u * pc : kBufOob,
                       s_rs[wave][tt][pc ^ (tt & 7)]);
         }
         __builtin_amdgcn_fence(__ATOMIC_ACQ_REL, "wavefront");
@@ -636,7 +665,7 @@ __global__ __launch_bounds__(NW * 64) __attribute__((amdgpu_waves_per_eu(F32 ? 2
 // n in {2, 4} (8 waves) and n = 8 (16 waves, bf16 only).
 template <int N, int MODE, int NW, int KJ, bool F32>
 static hipError_t launch_pre_bwd_inst(const PreBwdArgs& a, hipStream_t s) {
-  if constexpr (kPreBwdRowPieces && !F32 && KJ % 2 == 0) {
+  if constexpr (kPreBwdRowPieces && (!F32 || N <= 4) && KJ % 2 == 0) {
     if (a.C % 64 == 0) {  // a chunk pair's 64 columns in one stream's row
       hipLaunchKernelGGL((pre_bwd_mfma_kernel<N, MODE, NW, KJ, F32, true>), dim3((unsigned)((a.M + 15) / 16)),
                          dim3(NW * 64), 0, s, a);
