@@ -231,7 +231,8 @@ struct Chunk8<true> {
 constexpr bool kPreBwdRowPieces = true;
 // Phi operands from contiguous 16-byte pieces of each chunk's phi block,
 // regrouped through LDS, instead of 16 phi rows x 64 bytes an instruction:
-// C5 pre backward 94.5 -> 76.7 us, C2 61.7 -> 59.7 us (one box).
+// C5 pre backward 94.5 -> 76.7 us, C2 61.7 -> 59.7 us (one box); fp32 at
+// n = 8, one half of the block at a time: C5 fp32 208.5-210.1 -> 177.6-181.3 us.
 constexpr bool kPreBwdPhiBlock = true;
 // RS (bf16, or fp32 at n <= 4 where x stays resident; C % 64 == 0; fp32 C2
 // 144.4 -> 128.6 us): each wave takes pairs of adjacent chunks (64
@@ -270,10 +271,16 @@ __global__ __launch_bounds__(NW * 64) __attribute__((amdgpu_waves_per_eu(F32 ? 2
   // into the A layout through a block of LDS per wave.
   // (the shapes whose chunk loop loads a chunk's operand set: KS == 1 or at
   // most 12 chunks a wave)
-  constexpr bool PB = RS && FD % 8 == 0 && kPreBwdPhiBlock && (KS == 1 || KJ <= 12);
-  constexpr int NPC = 4 * FD * XP;         // 16-byte pieces of a chunk's phi block
-  constexpr int NPB = (NPC + 63) / 64;     // 64-lane loads of them
-  __shared__ __attribute__((aligned(16))) U32x4 s_pb[PB ? NW : 1][PB ? NPC : 1];
+  // The block is read in half-major order: half h (the A rows of MFMA half h)
+  // is the four 4-row groups 8q + 4h .. 8q + 4h + 3, each contiguous in phi.
+  // fp32 at n = 8 (x streamed, no row pieces) takes it too, one half in LDS at
+  // a time (16 waves x a whole 10 KiB block would not fit).
+  constexpr bool PB = FD % 8 == 0 && kPreBwdPhiBlock && (KS == 1 || KJ <= 12) && (RS || (F32 && N >= 8));
+  constexpr bool PBH = F32 && N >= 8;      // one half in LDS at a time
+  constexpr int GPC = FD * XP / 2;         // 16-byte pieces of a 4-row group
+  constexpr int NPH = 4 * GPC;             // of a half
+  constexpr int NPBH = (NPH + 63) / 64;    // 64-lane loads of a half
+  __shared__ __attribute__((aligned(16))) U32x4 s_pb[PB ? NW : 1][PB ? (PBH ? 1 : 2) * NPH : 1];
 
   const int tid = threadIdx.x;
   const int lane = tid & 63;
@@ -536,7 +543,7 @@ __global__ __launch_bounds__(NW * 64) __attribute__((amdgpu_waves_per_eu(F32 ? 2
   constexpr bool CH = !PF && KJ <= 12;
   struct ChunkIn {
     XV av[PB ? 1 : 2][PB ? 1 : KS];
-    U32x4 pb[PB ? NPB : 1];  // PB: the chunk's phi block, 16-byte pieces along the lanes
+    U32x4 pb[PB ? 2 : 1][PB ? NPBH : 1];  // PB: the chunk's phi block, 16-byte pieces along the lanes
     XV gv;
     XV xv[XRES ? 1 : 1];  // the chunk's x when it is not held from the start
   };
@@ -546,10 +553,15 @@ __global__ __launch_bounds__(NW * 64) __attribute__((amdgpu_waves_per_eu(F32 ? 2
     if constexpr (PB) {
       const uint32_t base = (uint32_t)((ci * C + c0) * FD) * ES;
 #pragma unroll
-      for (int i = 0; i < NPB; ++i) {
-        const int pc = 64 * i + lane;
-        in.pb[i] = buf_load16(rphi, c0 < C && pc < NPC ? base + 16u * pc : kBufOob);
-      }
+      for (int h = 0; h < 2; ++h)
+#pragma unroll
+        for (int i = 0; i < NPBH; ++i) {
+          const int ph = 64 * i + lane;
+          const int q = ph / GPC;
+          const uint32_t off = base + (uint32_t)((8 * q + 4 * h) * FD) * ES + 16u * (ph - q * GPC);
+          // C % 8 == 0: a 4-row group lies wholly inside or wholly past C
+          in.pb[h][i] = buf_load16(rphi, c0 + 8 * q < C && ph < NPH ? off : kBufOob);
+        }
     } else {
 #pragma unroll
       for (int h = 0; h < 2; ++h)
@@ -579,30 +591,41 @@ __global__ __launch_bounds__(NW * 64) __attribute__((amdgpu_waves_per_eu(F32 ? 2
     int ci, c0;
     chunk(j, ci, c0);
     const bool ok = c0 + 8 * g < C;
-    // PB: A-row r of half h is row 8 (r / 4) + 4h + r % 4 of the block, lane
-    // group g features 32 ks + 8g .. + 7: pieces (row * FD + 32 ks + 8g) XP / 8
-    // .. + XP - 1
+    // PB: A-row r of half h is row r % 4 of group r / 4 of that half; lane
+    // group g takes features 32 ks + 8g .. + 7, pieces (4 ks + g) XP .. + XP - 1
+    // of the row
     XV avb[PB ? 2 : 1][PB ? KS : 1];
-    if constexpr (PB) {
+    auto pb_stage = [&](int h) {
 #pragma unroll
-      for (int i = 0; i < NPB; ++i)
-        if (64 * i + lane < NPC) s_pb[wave][64 * i + lane] = cur.pb[i];
+      for (int i = 0; i < NPBH; ++i)
+        if (64 * i + lane < NPH) s_pb[wave][(PBH ? 0 : h) * NPH + 64 * i + lane] = cur.pb[h][i];
+    };
+    auto pb_fetch = [&](int h) {
+#pragma unroll
+      for (int ks = 0; ks < KS; ++ks) {
+        const int p0 = (PBH ? 0 : h) * NPH + (r >> 2) * GPC + (r & 3) * (FD * XP / 8) + 4 * XP * ks + XP * g;
+#pragma unroll
+        for (int e = 0; e < XP; ++e)
+          piece(avb[h][ks], e) = 32 * ks + 8 * g < FD ? s_pb[wave][p0 + e] : U32x4{{0u, 0u, 0u, 0u}};
+      }
+    };
+    if constexpr (PB && !PBH) {
+      pb_stage(0);
+      pb_stage(1);
       __builtin_amdgcn_fence(__ATOMIC_ACQ_REL, "wavefront");
-#pragma unroll
-      for (int h = 0; h < 2; ++h)
-#pragma unroll
-        for (int ks = 0; ks < KS; ++ks) {
-          const int rr = 8 * (r >> 2) + 4 * h + (r & 3);
-          const int p0 = rr * (FD * XP / 8) + 4 * XP * ks + XP * g;  // FD % 8 == 0
-#pragma unroll
-          for (int e = 0; e < XP; ++e)
-            piece(avb[h][ks], e) = 32 * ks + 8 * g < FD ? s_pb[wave][p0 + e] : U32x4{{0u, 0u, 0u, 0u}};
-        }
+      pb_fetch(0);
+      pb_fetch(1);
       __builtin_amdgcn_fence(__ATOMIC_ACQ_REL, "wavefront");
     }
     f32x4_t d2[2];
 #pragma unroll
     for (int h = 0; h < 2; ++h) {
+      if constexpr (PB && PBH) {
+        pb_stage(h);
+        __builtin_amdgcn_fence(__ATOMIC_ACQ_REL, "wavefront");
+        pb_fetch(h);
+        __builtin_amdgcn_fence(__ATOMIC_ACQ_REL, "wavefront");
+      }
       f32x4_t d = f32x4_t{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
       for (int ks = 0; ks < KS; ++ks) {
