@@ -1371,7 +1371,10 @@ __global__ __launch_bounds__(256) void sinkhorn_bwd_kernel(const void* __restric
   };
 
   // forward recompute, keeping iterates 0, K, 2K, ... (two SEG rows alternate)
-  const float v = live ? ld_any(m_in, idx, in_dt) : 0.f;
+  // both inputs' loads issue before either is waited for
+  const uint32_t mb = live ? ld_raw(m_in, idx, in_dt) : 0u;
+  const uint32_t gb = live ? ld_raw(g_out, idx, g_dt) : 0u;
+  const float v = raw_to_f32(mb, in_dt);
   S[tid] = v;
   __syncthreads();
   float mx = -INFINITY;
@@ -1393,7 +1396,7 @@ __global__ __launch_bounds__(256) void sinkhorn_bwd_kernel(const void* __restric
     __syncthreads();
   }
   // backward, one segment at a time from the last
-  float g = live ? ld_any(g_out, idx, g_dt) : 0.f;
+  float g = raw_to_f32(gb, g_dt);
   for (int j = J - 1; j >= 0; --j) {
     const int s0 = j * K;
     const int s1 = s0 + K < steps - 1 ? s0 + K : steps - 1;  // last backward step of the segment
@@ -1443,7 +1446,10 @@ __global__ __launch_bounds__(64) void sinkhorn_bwd_lanes_kernel(const void* __re
   float* Y = lds;                 // [steps][64] iterate after step s
   float* D = lds + steps * 64;    // [steps][64] divisor of step s (1 for the softmax step)
 
-  const float v = live ? ld_any(m_in, idx, in_dt) : 0.f;
+  // both inputs' loads issue before either is waited for
+  const uint32_t mb = live ? ld_raw(m_in, idx, in_dt) : 0u;
+  const uint32_t gb = live ? ld_raw(g_out, idx, g_dt) : 0u;
+  const float v = raw_to_f32(mb, in_dt);
   const float mx = row_reduce<N, OpMax>(v);
   const float ex = expf(v - mx);
   const float p = ex * __builtin_amdgcn_rcpf(row_reduce<N, OpAdd>(ex));
@@ -1455,7 +1461,7 @@ __global__ __launch_bounds__(64) void sinkhorn_bwd_lanes_kernel(const void* __re
     Y[st * 64 + lane] = t;
     D[st * 64 + lane] = den;
   }
-  float gr = live ? ld_any(g_out, idx, g_dt) : 0.f;
+  float gr = raw_to_f32(gb, g_dt);
   for (int st = steps - 1; st >= 1; --st) {
     const float y = Y[st * 64 + lane];
     const float gy = gr * y;
@@ -1484,7 +1490,14 @@ __global__ __launch_bounds__(256) void sinkhorn_bwd_regs_kernel(const void* __re
   const int steps = EXACT ? MAXS : 2 * (iters > 1 ? iters : 1);
   float Y[MAXS];
   float R[MAXS];  // 1 / divisor of each step
-  const float v = live ? ld_any(m_in, idx, in_dt) : 0.f;
+  // Both inputs' elements load together, as the 4-byte words that hold them
+  // (descriptors of the exact sizes; n^2 is even, so a 16-bit element's word
+  // lies inside its tensor): the per-dtype branches of ld_any made each load
+  // wait for the one before it.
+  const int es_m = in_dt == kF32 ? 4 : 2, es_g = g_dt == kF32 ? 4 : 2;
+  const uint32_t mw = buf_load4z(make_rsrc(m_in, (uint32_t)(batch * G * es_m)), live ? word_off(idx, in_dt) : kBufOob).v[0];
+  const uint32_t gw = buf_load4z(make_rsrc(g_out, (uint32_t)(batch * G * es_g)), live ? word_off(idx, g_dt) : kBufOob).v[0];
+  const float v = word_elem(mw, idx, in_dt);
   const float mx = row_reduce<N, OpMax>(v);
   const float ex = expf(v - mx);
   const float p = ex * __builtin_amdgcn_rcpf(row_reduce<N, OpAdd>(ex));
@@ -1500,7 +1513,7 @@ __global__ __launch_bounds__(256) void sinkhorn_bwd_regs_kernel(const void* __re
       Y[st] = t;
     }
   }
-  float gr = live ? ld_any(g_out, idx, g_dt) : 0.f;
+  float gr = word_elem(gw, idx, g_dt);
 #pragma unroll
   for (int st = MAXS - 1; st >= 1; --st) {
     if (st < steps) {
@@ -1538,9 +1551,17 @@ __global__ __launch_bounds__(256) void sinkhorn_bwd_sk8_kernel(const void* __res
   const int j = threadIdx.x & 15;
   const bool live = mi < batch;
   const int64_t e0 = mi * 64 + (j & 7) * 8 + 4 * (j >> 3);  // first of this lane's elements
+  // This lane's four elements of both inputs, one 16-byte buffer load each
+  // (a 16-bit input's four are its first 8 bytes), issued together: with a
+  // per-dtype branch and conversion around each element, the eight loads were
+  // eight round trips in turn (C5 shape 9.1-9.2 -> 8.5-8.9 us).  The
+  // descriptors hold the exact sizes, so bytes past the end read zero.
+  const int es_m = in_dt == kF32 ? 4 : 2, es_g = g_dt == kF32 ? 4 : 2;
+  const U32x4 mw = buf_load16(make_rsrc(m_in, (uint32_t)(batch * 64 * es_m)), live ? (uint32_t)e0 * es_m : kBufOob);
+  const U32x4 gw = buf_load16(make_rsrc(g_out, (uint32_t)(batch * 64 * es_g)), live ? (uint32_t)e0 * es_g : kBufOob);
   float t[4];
 #pragma unroll
-  for (int q = 0; q < 4; ++q) t[q] = live ? ld_any(m_in, e0 + q, in_dt) : 0.f;
+  for (int q = 0; q < 4; ++q) t[q] = word4_elem(mw, q, in_dt);
   // softmax over the row, + eps
   float mx = fmaxf(fmaxf(t[0], t[1]), fmaxf(t[2], t[3]));
   mx = fmaxf(mx, dpp_f<kDppRor8>(mx));
@@ -1579,7 +1600,7 @@ __global__ __launch_bounds__(256) void sinkhorn_bwd_sk8_kernel(const void* __res
   }
   float gr[4];
 #pragma unroll
-  for (int q = 0; q < 4; ++q) gr[q] = live ? ld_any(g_out, e0 + q, g_dt) : 0.f;
+  for (int q = 0; q < 4; ++q) gr[q] = word4_elem(gw, q, g_dt);
 #pragma unroll
   for (int k = K - 1; k >= 0; --k) {
     // column step k: y = Y[k], per-column reciprocal
@@ -1628,13 +1649,17 @@ size_t sinkhorn_bwd_lds_bytes(int iters) {
 hipError_t launch_sinkhorn_bwd(const void* m_in, int in_dtype, const void* g_out, int g_dtype,
                                void* g_in, int gi_dtype, int64_t batch, int n, int iters,
                                float eps, hipStream_t s) {
-  if (n == 8 && iters == 20) {  // the reference's default schedule: half-row layout
+  // The register kernels read both inputs through buffer descriptors: 32-bit
+  // byte offsets, 4-byte aligned bases.  Anything else takes the kernels below.
+  const bool buf_ok = batch * n * n * 4 < (int64_t)kBufOob && ((uintptr_t)m_in & 3) == 0 &&
+                      ((uintptr_t)g_out & 3) == 0;
+  if (buf_ok && n == 8 && iters == 20) {  // the reference's default schedule: half-row layout
     const int64_t blocks = (batch * 16 + 255) / 256;
     hipLaunchKernelGGL((sinkhorn_bwd_sk8_kernel<20>), dim3((unsigned)blocks), dim3(256), 0, s, m_in,
                        in_dtype, g_out, g_dtype, g_in, gi_dtype, batch, eps);
     return hipGetLastError();
   }
-  if ((n == 2 || n == 4) && iters == 20) {
+  if (buf_ok && (n == 2 || n == 4) && iters == 20) {
     const int64_t blocks = (batch * n * n + 255) / 256;
     if (n == 2)
       hipLaunchKernelGGL((sinkhorn_bwd_regs_kernel<2, 40, true>), dim3((unsigned)blocks), dim3(256), 0, s, m_in, in_dtype, g_out, g_dtype, g_in, gi_dtype, batch, iters, eps);
@@ -1642,7 +1667,7 @@ hipError_t launch_sinkhorn_bwd(const void* m_in, int in_dtype, const void* g_out
       hipLaunchKernelGGL((sinkhorn_bwd_regs_kernel<4, 40, true>), dim3((unsigned)blocks), dim3(256), 0, s, m_in, in_dtype, g_out, g_dtype, g_in, gi_dtype, batch, iters, eps);
     return hipGetLastError();
   }
-  if ((n == 2 || n == 4 || n == 8) && iters <= 20) {
+  if (buf_ok && (n == 2 || n == 4 || n == 8) && iters <= 20) {
     const int64_t blocks = (batch * n * n + 255) / 256;
     switch (n) {
       case 2: hipLaunchKernelGGL((sinkhorn_bwd_regs_kernel<2, 40>), dim3((unsigned)blocks), dim3(256), 0, s, m_in, in_dtype, g_out, g_dtype, g_in, gi_dtype, batch, iters, eps); break;

@@ -142,6 +142,41 @@ __device__ __forceinline__ float ld_any(const void* p, int64_t i, int dt) {
   return dt == kBF16 ? bf16_bits_to_f32(b) : f16_bits_to_f32(b);
 }
 
+// Raw bits of element i of a tensor whose dtype is only known at run time
+// (fp32 bits, or the 16-bit value zero-extended), and the value they hold.
+// ld_any converts inside its per-dtype branch, right after the load, so each
+// ld_any waits for its own load before the next one issues; raw loads carry no
+// conversion, so a kernel can put all of its loads in flight first.
+__device__ __forceinline__ uint32_t ld_raw(const void* p, int64_t i, int dt) {
+  if (dt == kF32) return static_cast<const uint32_t*>(p)[i];
+  return static_cast<const uint16_t*>(p)[i];
+}
+__device__ __forceinline__ float raw_to_f32(uint32_t b, int dt) {
+  if (dt == kF32) return __builtin_bit_cast(float, b);
+  return dt == kBF16 ? bf16_bits_to_f32((uint16_t)b) : f16_bits_to_f32((uint16_t)b);
+}
+
+// Element q (0..3) of four consecutive elements loaded as one 16-byte buffer
+// word group (buf_load16 at the first element's byte offset): fp32 takes word
+// q, a 16-bit dtype the half q & 1 of word q >> 1.  One unconditional load per
+// lane instead of a per-dtype branch around each element.
+__device__ __forceinline__ float word4_elem(const U32x4& w, int q, int dt) {
+  if (dt == kF32) return __builtin_bit_cast(float, w.v[q]);
+  const uint32_t h = (q & 1) ? w.v[q >> 1] >> 16 : w.v[q >> 1] & 0xffffu;
+  return dt == kBF16 ? bf16_bits_to_f32((uint16_t)h) : f16_bits_to_f32((uint16_t)h);
+}
+// Element i of a run-time-dtype tensor from the 4-byte word that holds it (a
+// 16-bit element's word starts at (2i) & ~3; for tensors of an even count of
+// 16-bit elements that word lies inside the tensor).
+__device__ __forceinline__ uint32_t word_off(int64_t i, int dt) {
+  return dt == kF32 ? (uint32_t)i * 4u : ((uint32_t)i * 2u) & ~3u;
+}
+__device__ __forceinline__ float word_elem(uint32_t w, int64_t i, int dt) {
+  if (dt == kF32) return __builtin_bit_cast(float, w);
+  const uint32_t h = (i & 1) ? w >> 16 : w & 0xffffu;
+  return dt == kBF16 ? bf16_bits_to_f32((uint16_t)h) : f16_bits_to_f32((uint16_t)h);
+}
+
 __device__ __forceinline__ void st_any(void* p, int64_t i, int dt, float v) {
   if (dt == kF32) {
     static_cast<float*>(p)[i] = v;
