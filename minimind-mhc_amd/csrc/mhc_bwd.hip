@@ -1526,108 +1526,116 @@ __global__ __launch_bounds__(256) void sinkhorn_bwd_regs_kernel(const void* __re
   if (live) st_any(g_in, idx, gi_dt, gm);
 }
 
-// n = 8 on the half-row layout of the forward's sk8_* Sinkhorn: one matrix per
-// 16 lanes, lane j holding row (j & 7), columns 4 (j >> 3) .. + 3, four
-// matrices per wave.  A row sum is three in-lane adds and one DPP add with the
-// lane 8 away; a column sum is the 8-lane butterfly over one half's lanes,
-// four columns at a time; each lane takes the reciprocal of only column
-// (j & 3) of its half and quad_perm broadcasts hand every lane the four it
-// needs.  So a step costs a quarter of the reductions of the one-element-per-
-// lane kernel per element (n = 8, 20 iterations: ~2.5x fewer VALU
-// instructions in all).  The trajectory: the iterate after each column step
-// (4 values), its column reciprocal (the lane's own one) and each row step's
-// reciprocal; the iterate after a row step is recomputed from the column
-// iterate before it with the forward's own multiply.  Products that feed a
-// sum are non-contracting multiplies (mul_nc): contracted into the DPP adds
-// they cost a DPP move and an fma each instead of one fused v_add_f32_dpp.  K column steps (the
-// reference's iters; the schedule: softmax + eps, a column step, then K - 1
-// row + column steps), K fixed so every step is unrolled.
+// n = 8 on 2 x 2 blocks: one matrix per 16 lanes (a DPP row), lane j holding
+// rows 2 (j >> 2) .. + 1 and columns 2 (j & 3) .. + 1.  A row sum is one
+// in-lane add and the quad butterfly (lane xor 1, 2); a column sum one in-lane
+// add and the two rotations of col_sum<4> (lanes j + 4, 8, 12): so both steps
+// cost what only the row step cost in the half-row layout of the forward's
+// sk8_* Sinkhorn (lane j: row j & 7, columns 4 (j >> 3) .. + 3), whose column
+// step took a 3-stage butterfly for each of four columns and DPP broadcasts of
+// the reciprocals: 1429 instead of 1690 VALU instructions a wave, C5 shape
+// (8192 matrices) 8.1-8.2 -> 6.9-7.0 us.  Each lane keeps its two rows' and
+// two columns' reciprocals of every step (244 VGPRs, two waves a SIMD as
+// before: the grid has two waves per SIMD).
+// The trajectory: the iterate after each column step (4 values) and both
+// reciprocals; the iterate after a row step is recomputed from the column
+// iterate before it with the forward's own multiply.
 template <int K>
-__global__ __launch_bounds__(256) void sinkhorn_bwd_sk8_kernel(const void* __restrict__ m_in, int in_dt,
+__global__ __launch_bounds__(256) void sinkhorn_bwd_b22_kernel(const void* __restrict__ m_in, int in_dt,
                                                                const void* __restrict__ g_out, int g_dt,
                                                                void* __restrict__ g_in, int gi_dt,
                                                                int64_t batch, float eps) {
   const int64_t mi = ((int64_t)blockIdx.x * 256 + threadIdx.x) >> 4;  // matrix
   const int j = threadIdx.x & 15;
   const bool live = mi < batch;
-  const int64_t e0 = mi * 64 + (j & 7) * 8 + 4 * (j >> 3);  // first of this lane's elements
-  // This lane's four elements of both inputs, one 16-byte buffer load each
-  // (a 16-bit input's four are its first 8 bytes), issued together: with a
-  // per-dtype branch and conversion around each element, the eight loads were
-  // eight round trips in turn (C5 shape 9.1-9.2 -> 8.5-8.9 us).  The
-  // descriptors hold the exact sizes, so bytes past the end read zero.
+  // element (a, b) of this lane's block: row 2 (j >> 2) + a, column 2 (j & 3) + b
+  const int64_t e0 = mi * 64 + (j >> 2) * 16 + (j & 3) * 2;  // (0, 0); (1, 0) is 8 further
+  // Both inputs' two row pairs, one 8-byte buffer load each, issued together
+  // (a 16-bit input's pair is the first half of its 8 bytes); the descriptors
+  // hold the exact sizes, so bytes past the end read zero.
   const int es_m = in_dt == kF32 ? 4 : 2, es_g = g_dt == kF32 ? 4 : 2;
-  const U32x4 mw = buf_load16(make_rsrc(m_in, (uint32_t)(batch * 64 * es_m)), live ? (uint32_t)e0 * es_m : kBufOob);
-  const U32x4 gw = buf_load16(make_rsrc(g_out, (uint32_t)(batch * 64 * es_g)), live ? (uint32_t)e0 * es_g : kBufOob);
-  float t[4];
+  const auto rm = make_rsrc(m_in, (uint32_t)(batch * 64 * es_m));
+  const auto rg = make_rsrc(g_out, (uint32_t)(batch * 64 * es_g));
+  U32x4 mw[2], gw[2];
 #pragma unroll
-  for (int q = 0; q < 4; ++q) t[q] = word4_elem(mw, q, in_dt);
-  // softmax over the row, + eps
-  float mx = fmaxf(fmaxf(t[0], t[1]), fmaxf(t[2], t[3]));
-  mx = fmaxf(mx, dpp_f<kDppRor8>(mx));
-  float p[4];
+  for (int a = 0; a < 2; ++a) mw[a] = buf_load8z(rm, live ? (uint32_t)(e0 + 8 * a) * es_m : kBufOob);
 #pragma unroll
-  for (int q = 0; q < 4; ++q) p[q] = expf(t[q] - mx);
-  const float rs = __builtin_amdgcn_rcpf(sk8_row_sum(p));
+  for (int a = 0; a < 2; ++a) gw[a] = buf_load8z(rg, live ? (uint32_t)(e0 + 8 * a) * es_g : kBufOob);
+  float t[2][2];
 #pragma unroll
-  for (int q = 0; q < 4; ++q) {
-    p[q] = mul_nc(p[q], rs);
-    t[q] = p[q] + eps;
+  for (int a = 0; a < 2; ++a)
+#pragma unroll
+    for (int b = 0; b < 2; ++b) t[a][b] = word4_elem(mw[a], b, in_dt);
+  // softmax over each row, + eps
+  float p[2][2];
+#pragma unroll
+  for (int a = 0; a < 2; ++a) {
+    const float mx = row_reduce<4, OpMax>(fmaxf(t[a][0], t[a][1]));
+    p[a][0] = expf(t[a][0] - mx);
+    p[a][1] = expf(t[a][1] - mx);
+    const float rs = __builtin_amdgcn_rcpf(row_reduce<4, OpAdd>(p[a][0] + p[a][1]));
+#pragma unroll
+    for (int b = 0; b < 2; ++b) {
+      p[a][b] = mul_nc(p[a][b], rs);
+      t[a][b] = p[a][b] + eps;
+    }
   }
-  float Y[K][4];  // iterate after column step k
-  float RC[K];    // column step k: reciprocal of this lane's column (j & 3)
-  float RR[K];    // row step k (before column step k, k >= 1): the row's reciprocal
-  const int l = __lane_id();
+  float Y[K][2][2];  // iterate after column step k
+  float RC[K][2];    // column step k: reciprocals of this lane's two columns
+  float RR[K][2];    // row step k (before column step k, k >= 1): of its two rows
 #pragma unroll
   for (int k = 0; k < K; ++k) {
     if (k > 0) {
-      RR[k] = __builtin_amdgcn_rcpf(sk8_row_sum(t) + eps);
 #pragma unroll
-      for (int q = 0; q < 4; ++q) t[q] = mul_nc(t[q], RR[k]);
+      for (int a = 0; a < 2; ++a) {
+        RR[k][a] = __builtin_amdgcn_rcpf(row_reduce<4, OpAdd>(t[a][0] + t[a][1]) + eps);
+        t[a][0] = mul_nc(t[a][0], RR[k][a]);
+        t[a][1] = mul_nc(t[a][1], RR[k][a]);
+      }
     }
-    float c[4];
 #pragma unroll
-    for (int q = 0; q < 4; ++q) c[q] = row_reduce<8, OpAdd>(t[q]);
-    const float lo = (l & 1) ? c[1] : c[0];
-    const float hi = (l & 1) ? c[3] : c[2];
-    RC[k] = __builtin_amdgcn_rcpf(((l & 2) ? hi : lo) + eps);
-    t[0] = mul_nc(t[0], dpp_f<0x00>(RC[k]));  // quad_perm [0,0,0,0]
-    t[1] = mul_nc(t[1], dpp_f<0x55>(RC[k]));  // quad_perm [1,1,1,1]
-    t[2] = mul_nc(t[2], dpp_f<0xAA>(RC[k]));  // quad_perm [2,2,2,2]
-    t[3] = mul_nc(t[3], dpp_f<0xFF>(RC[k]));  // quad_perm [3,3,3,3]
+    for (int b = 0; b < 2; ++b) {
+      RC[k][b] = __builtin_amdgcn_rcpf(col_sum<4>(t[0][b] + t[1][b]) + eps);
+      t[0][b] = mul_nc(t[0][b], RC[k][b]);
+      t[1][b] = mul_nc(t[1][b], RC[k][b]);
+    }
 #pragma unroll
-    for (int q = 0; q < 4; ++q) Y[k][q] = t[q];
+    for (int a = 0; a < 2; ++a)
+#pragma unroll
+      for (int b = 0; b < 2; ++b) Y[k][a][b] = t[a][b];
   }
-  float gr[4];
+  float gr[2][2];
 #pragma unroll
-  for (int q = 0; q < 4; ++q) gr[q] = word4_elem(gw, q, g_dt);
+  for (int a = 0; a < 2; ++a)
+#pragma unroll
+    for (int b = 0; b < 2; ++b) gr[a][b] = word4_elem(gw[a], b, g_dt);
 #pragma unroll
   for (int k = K - 1; k >= 0; --k) {
-    // column step k: y = Y[k], per-column reciprocal
-    float d[4];
+    // column step k: y = Y[k]
 #pragma unroll
-    for (int q = 0; q < 4; ++q) d[q] = row_reduce<8, OpAdd>(mul_nc(gr[q], Y[k][q]));
-    gr[0] = (gr[0] - d[0]) * dpp_f<0x00>(RC[k]);
-    gr[1] = (gr[1] - d[1]) * dpp_f<0x55>(RC[k]);
-    gr[2] = (gr[2] - d[2]) * dpp_f<0xAA>(RC[k]);
-    gr[3] = (gr[3] - d[3]) * dpp_f<0xFF>(RC[k]);
+    for (int b = 0; b < 2; ++b) {
+      const float d = col_sum<4>(mul_nc(gr[0][b], Y[k][0][b]) + mul_nc(gr[1][b], Y[k][1][b]));
+      gr[0][b] = (gr[0][b] - d) * RC[k][b];
+      gr[1][b] = (gr[1][b] - d) * RC[k][b];
+    }
     if (k > 0) {  // row step k: y = Y[k - 1] * RR[k], as the forward formed it
-      float gy[4];
 #pragma unroll
-      for (int q = 0; q < 4; ++q) gy[q] = mul_nc(gr[q], mul_nc(Y[k - 1][q], RR[k]));
-      const float dr = sk8_row_sum(gy);
-#pragma unroll
-      for (int q = 0; q < 4; ++q) gr[q] = (gr[q] - dr) * RR[k];
+      for (int a = 0; a < 2; ++a) {
+        const float d = row_reduce<4, OpAdd>(mul_nc(gr[a][0], mul_nc(Y[k - 1][a][0], RR[k][a])) +
+                                             mul_nc(gr[a][1], mul_nc(Y[k - 1][a][1], RR[k][a])));
+        gr[a][0] = (gr[a][0] - d) * RR[k][a];
+        gr[a][1] = (gr[a][1] - d) * RR[k][a];
+      }
     }
   }
   // softmax: t0 = p + eps, so the gradient of p is gr
-  float gp[4];
 #pragma unroll
-  for (int q = 0; q < 4; ++q) gp[q] = mul_nc(gr[q], p[q]);
-  const float dp = sk8_row_sum(gp);
-  if (live) {
+  for (int a = 0; a < 2; ++a) {
+    const float dp = row_reduce<4, OpAdd>(mul_nc(gr[a][0], p[a][0]) + mul_nc(gr[a][1], p[a][1]));
+    if (live) {
 #pragma unroll
-    for (int q = 0; q < 4; ++q) st_any(g_in, e0 + q, gi_dt, p[q] * (gr[q] - dp));
+      for (int b = 0; b < 2; ++b) st_any(g_in, e0 + 8 * a + b, gi_dt, p[a][b] * (gr[a][b] - dp));
+    }
   }
 }
 
@@ -1653,9 +1661,9 @@ hipError_t launch_sinkhorn_bwd(const void* m_in, int in_dtype, const void* g_out
   // byte offsets, 4-byte aligned bases.  Anything else takes the kernels below.
   const bool buf_ok = batch * n * n * 4 < (int64_t)kBufOob && ((uintptr_t)m_in & 3) == 0 &&
                       ((uintptr_t)g_out & 3) == 0;
-  if (buf_ok && n == 8 && iters == 20) {  // the reference's default schedule: half-row layout
+  if (buf_ok && n == 8 && iters == 20) {  // the reference's default schedule: 16 lanes a matrix
     const int64_t blocks = (batch * 16 + 255) / 256;
-    hipLaunchKernelGGL((sinkhorn_bwd_sk8_kernel<20>), dim3((unsigned)blocks), dim3(256), 0, s, m_in,
+    hipLaunchKernelGGL((sinkhorn_bwd_b22_kernel<20>), dim3((unsigned)blocks), dim3(256), 0, s, m_in,
                        in_dtype, g_out, g_dtype, g_in, gi_dtype, batch, eps);
     return hipGetLastError();
   }
