@@ -379,14 +379,22 @@ __global__ __launch_bounds__(kPersistWaves * 64) void pre_split_kernel(PreArgs a
   U32x4 xa[KB][N];
   U32x4 xb[KB][N];
   split_load<N, KB, 0, KB>(xa, split_rsrc(a.x, tile, a.M, N * C), C, wave, lane);
+  // Each LDS tile's blocks are loaded into registers together before any is
+  // written: stored straight from each load, the writes made every load wait
+  // for the one before (one register set reused: KB * N round trips a tile).
 #pragma unroll
-  for (int t = 0; t < P::NLDS; ++t)
+  for (int t = 0; t < P::NLDS; ++t) {
+    U32x4 st[KB][N];
+#pragma unroll
+    for (int q = 0; q < KB; ++q)
+#pragma unroll
+      for (int i = 0; i < N; ++i) st[q][i] = buf_load16(wr, phi_off(P::NREG + t, q, i));
 #pragma unroll
     for (int q = 0; q < KB; ++q)
 #pragma unroll
       for (int i = 0; i < N; ++i)
-        *reinterpret_cast<U32x4*>(lds_w + t * P::TILE_LDS + (((wave * KB + q) * N + i) * 64 + lane) * 16) =
-            buf_load16(wr, phi_off(P::NREG + t, q, i));
+        *reinterpret_cast<U32x4*>(lds_w + t * P::TILE_LDS + (((wave * KB + q) * N + i) * 64 + lane) * 16) = st[q][i];
+  }
   if (tid < GateParams<N>::kCount) sh.prm[tid] = convert_param(rp, a.param_dtype);
   __syncthreads();  // gate parameters and LDS phi tiles visible
 
