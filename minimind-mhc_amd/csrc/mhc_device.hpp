@@ -177,6 +177,15 @@ __device__ __forceinline__ float word_elem(uint32_t w, int64_t i, int dt) {
   return dt == kBF16 ? bf16_bits_to_f32((uint16_t)h) : f16_bits_to_f32((uint16_t)h);
 }
 
+// The 4-byte word holding element i of a run-time-dtype vector of `count`
+// elements (count even for a 16-bit dtype), through a buffer descriptor: one
+// unconditional load and no per-dtype branch, so later loads do not wait for
+// it; word_elem converts it where the value is first needed.
+__device__ __forceinline__ uint32_t ld_word(const void* p, int64_t count, int64_t i, int dt) {
+  const uint32_t bytes = (uint32_t)count * (dt == kF32 ? 4u : 2u);
+  return buf_load4z(make_rsrc(p, bytes), word_off(i, dt)).v[0];
+}
+
 __device__ __forceinline__ void st_any(void* p, int64_t i, int dt, float v) {
   if (dt == kF32) {
     static_cast<float*>(p)[i] = v;

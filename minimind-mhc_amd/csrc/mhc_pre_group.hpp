@@ -129,13 +129,14 @@ __global__ __launch_bounds__(kGrpWaves * 64) void pre_group_kernel(PreArgs a, in
     const float* src = a.x_ssq + (t0 + tid) * PS;
     for (int j = 0; j < PS; ++j) ss_given += src[j];
   }
-  float gain[2] = {0.f, 0.f};  // norm gain of columns tid and tid + T (branch-free loads)
+  // norm gain words of columns tid and tid + T, converted where they are
+  // stored to LDS (ld_any's per-dtype branch made the prologue's loads wait)
+  uint32_t gain_w[2] = {0u, 0u};
   if constexpr (NORM) {
 #pragma unroll
     for (int h = 0; h < 2; ++h) {
       const int c = tid + h * T;
-      const float v = ld_any(a.norm_w, c < C ? c : 0, a.norm_dtype);
-      gain[h] = c < C ? v : 0.f;
+      gain_w[h] = ld_word(a.norm_w, C, c < C ? c : 0, a.norm_dtype);
     }
   }
 
@@ -207,7 +208,10 @@ __global__ __launch_bounds__(kGrpWaves * 64) void pre_group_kernel(PreArgs a, in
   if constexpr (NORM) {
 #pragma unroll
     for (int h = 0; h < 2; ++h)
-      if (tid + h * T < P::CMAX) sh.gain[tid + h * T] = gain[h];
+      if (tid + h * T < P::CMAX) {
+        const int c = tid + h * T;
+        sh.gain[c] = c < C ? word_elem(gain_w[h], c, a.norm_dtype) : 0.f;
+      }
   }
   __syncthreads();  // x rows, zero block and parameters visible
 

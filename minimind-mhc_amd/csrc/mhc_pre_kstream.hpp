@@ -211,13 +211,14 @@ __global__ __launch_bounds__(kKsWaves * 64) void pre_kstream_kernel(PreArgs a) {
     const float* src = a.x_ssq + (t0 + tid) * P;
     for (int j = 0; j < P; ++j) ss_given += src[j];
   }
-  float gain[2] = {0.f, 0.f};  // norm gain of columns tid and tid + 512 (branch-free loads)
+  // norm gain words of columns tid and tid + T, converted where they are
+  // stored to LDS (ld_any's per-dtype branch made the prologue's loads wait)
+  uint32_t gain_w[2] = {0u, 0u};
   if constexpr (NORM) {
 #pragma unroll
     for (int h = 0; h < 2; ++h) {
       const int c = tid + h * T;
-      const float v = ld_any(a.norm_w, c < C ? c : 0, a.norm_dtype);
-      gain[h] = c < C ? v : 0.f;
+      gain_w[h] = ld_word(a.norm_w, C, c < C ? c : 0, a.norm_dtype);
     }
   }
 
@@ -390,7 +391,10 @@ __global__ __launch_bounds__(kKsWaves * 64) void pre_kstream_kernel(PreArgs a) {
   if (tid < GP::kCount) sh.prm[tid] = convert_param(rp, a.param_dtype);
   if constexpr (NORM) {
 #pragma unroll
-    for (int h = 0; h < 2; ++h) nsh.gain[tid + h * T] = gain[h];
+    for (int h = 0; h < 2; ++h) {
+      const int c = tid + h * T;
+      nsh.gain[c] = c < C ? word_elem(gain_w[h], c, a.norm_dtype) : 0.f;
+    }
   }
 
   // ---- pre-aggregate rounds --------------------------------------------------

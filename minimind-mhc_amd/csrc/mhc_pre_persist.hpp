@@ -844,13 +844,14 @@ __global__ __launch_bounds__(kPersistWaves * 64) void pre_persist_kernel(PreArgs
   // phi tile write into the (not yet used) partials area.  The second tile's
   // loads go out during the first step.
   const RawParam rp = load_gate_param<N, MODE>(a, tid);
-  float gain[2] = {0.f, 0.f};  // norm gain of columns tid and tid + 512 (branch-free loads)
+  // norm gain words of columns tid and tid + 512, converted where they are
+  // stored to LDS (ld_any's per-dtype branch made the prologue's loads wait)
+  uint32_t gain_w[2] = {0u, 0u};
   if constexpr (NORM) {
 #pragma unroll
     for (int h = 0; h < 2; ++h) {
       const int c = tid + h * kPersistWaves * 64;
-      const float v = ld_any(a.norm_w, c < C ? c : 0, a.norm_dtype);
-      gain[h] = c < C ? v : 0.f;
+      gain_w[h] = ld_word(a.norm_w, C, c < C ? c : 0, a.norm_dtype);
     }
   }
 
@@ -911,7 +912,10 @@ __global__ __launch_bounds__(kPersistWaves * 64) void pre_persist_kernel(PreArgs
   if (tid < GateParams<N>::kCount) sh.prm[tid] = convert_param(rp, a.param_dtype);
   if constexpr (NORM) {
 #pragma unroll
-    for (int h = 0; h < 2; ++h) nsh.gain[tid + h * kPersistWaves * 64] = gain[h];
+    for (int h = 0; h < 2; ++h) {
+      const int c = tid + h * kPersistWaves * 64;
+      nsh.gain[c] = c < C ? word_elem(gain_w[h], c, a.norm_dtype) : 0.f;
+    }
   }
   __syncthreads();  // gate parameters, zero block and phi tiles visible
 
