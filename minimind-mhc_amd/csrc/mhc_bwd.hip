@@ -1475,11 +1475,9 @@ __global__ __launch_bounds__(64) void sinkhorn_bwd_lanes_kernel(const void* __re
 // The same recurrence with the trajectory in registers, for schedules of at
 // most MAXS steps (2 * iters): no LDS, so occupancy is set by registers alone
 // and every access is a register read.  The steps run fully unrolled behind a
-// uniform bound on the real step count; EXACT instances (the schedule is MAXS
-// steps) drop the bound, and with it the per-step branches and the selects
-// that merged the guarded values (n = 8, 20 iterations: 1000 -> 924 VALU
-// instructions a wave).
-template <int N, int MAXS, bool EXACT = false>
+// uniform bound on the real step count.  (The reference's 20 iterations take
+// the 2 x 2-block kernel above at n in {2, 4, 8}.)
+template <int N, int MAXS>
 __global__ __launch_bounds__(256) void sinkhorn_bwd_regs_kernel(const void* __restrict__ m_in, int in_dt,
                                                                 const void* __restrict__ g_out, int g_dt,
                                                                 void* __restrict__ g_in, int gi_dt,
@@ -1487,7 +1485,7 @@ __global__ __launch_bounds__(256) void sinkhorn_bwd_regs_kernel(const void* __re
   constexpr int G = N * N;
   const int64_t idx = (int64_t)blockIdx.x * 256 + threadIdx.x;  // element index
   const bool live = idx < batch * G;
-  const int steps = EXACT ? MAXS : 2 * (iters > 1 ? iters : 1);
+  const int steps = 2 * (iters > 1 ? iters : 1);
   float Y[MAXS];
   float R[MAXS];  // 1 / divisor of each step
   // Both inputs' elements load together, as the 4-byte words that hold them
@@ -1526,41 +1524,46 @@ __global__ __launch_bounds__(256) void sinkhorn_bwd_regs_kernel(const void* __re
   if (live) st_any(g_in, idx, gi_dt, gm);
 }
 
-// n = 8 on 2 x 2 blocks: one matrix per 16 lanes (a DPP row), lane j holding
-// rows 2 (j >> 2) .. + 1 and columns 2 (j & 3) .. + 1.  A row sum is one
-// in-lane add and the quad butterfly (lane xor 1, 2); a column sum one in-lane
-// add and the two rotations of col_sum<4> (lanes j + 4, 8, 12): so both steps
-// cost what only the row step cost in the half-row layout of the forward's
-// sk8_* Sinkhorn (lane j: row j & 7, columns 4 (j >> 3) .. + 3), whose column
-// step took a 3-stage butterfly for each of four columns and DPP broadcasts of
-// the reciprocals: 1429 instead of 1690 VALU instructions a wave, C5 shape
-// (8192 matrices) 8.1-8.2 -> 6.9-7.0 us.  Each lane keeps its two rows' and
-// two columns' reciprocals of every step (244 VGPRs, two waves a SIMD as
-// before: the grid has two waves per SIMD).
-// The trajectory: the iterate after each column step (4 values) and both
-// reciprocals; the iterate after a row step is recomputed from the column
-// iterate before it with the forward's own multiply.
-template <int K>
+// 2 x 2 blocks per lane: one n x n matrix per (n/2)^2 lanes (n = 8: 16 lanes,
+// a DPP row; n = 4: a quad; n = 2: one lane), lane j holding rows
+// 2 (j / (n/2)) .. + 1 and columns 2 (j % (n/2)) .. + 1.  A row sum is one
+// in-lane add and row_reduce<n/2> (lane xor 1, 2); a column sum one in-lane
+// add and col_sum<n/2> (n = 8: lanes j + 4, 8, 12 by two rotations; n = 4:
+// lane xor 2), so both steps cost the same.  At n = 8 this replaced the
+// half-row layout of the forward's sk8_* Sinkhorn (lane j: row j & 7, columns
+// 4 (j >> 3) .. + 3), whose column step took a 3-stage butterfly for each of
+// four columns and DPP broadcasts of the reciprocals: 1690 -> 1429 VALU
+// instructions a wave, C5 shape (8192 matrices) 8.1-8.2 -> 6.9-7.0 us; at
+// n = 4 it replaced one element a lane (531 VALU instructions a wave for 4
+// matrices, 1263 now for 16), C2 shape (16384 matrices) 6.0-6.4 -> 4.8-4.9
+// us, though the grid now fills one wave a SIMD.  Each lane keeps its two
+// rows' and two columns' reciprocals of every step (~244 VGPRs).  The trajectory: the iterate after each column step (4 values) and
+// both reciprocals; the iterate after a row step is recomputed from the
+// column iterate before it with the forward's own multiply.
+template <int N, int K>
 __global__ __launch_bounds__(256) void sinkhorn_bwd_b22_kernel(const void* __restrict__ m_in, int in_dt,
                                                                const void* __restrict__ g_out, int g_dt,
                                                                void* __restrict__ g_in, int gi_dt,
                                                                int64_t batch, float eps) {
-  const int64_t mi = ((int64_t)blockIdx.x * 256 + threadIdx.x) >> 4;  // matrix
-  const int j = threadIdx.x & 15;
+  static_assert(N == 2 || N == 4 || N == 8, "2 x 2 blocks: n in {2, 4, 8}");
+  constexpr int H = N / 2;                                             // blocks a row
+  constexpr int L = H * H;                                             // lanes a matrix
+  const int64_t mi = ((int64_t)blockIdx.x * 256 + threadIdx.x) / L;  // matrix
+  const int j = threadIdx.x % L;
   const bool live = mi < batch;
-  // element (a, b) of this lane's block: row 2 (j >> 2) + a, column 2 (j & 3) + b
-  const int64_t e0 = mi * 64 + (j >> 2) * 16 + (j & 3) * 2;  // (0, 0); (1, 0) is 8 further
+  // element (a, b) of this lane's block: row 2 (j / H) + a, column 2 (j % H) + b
+  const int64_t e0 = mi * N * N + (j / H) * 2 * N + (j % H) * 2;  // (0, 0); (1, 0) is N further
   // Both inputs' two row pairs, one 8-byte buffer load each, issued together
   // (a 16-bit input's pair is the first half of its 8 bytes); the descriptors
   // hold the exact sizes, so bytes past the end read zero.
   const int es_m = in_dt == kF32 ? 4 : 2, es_g = g_dt == kF32 ? 4 : 2;
-  const auto rm = make_rsrc(m_in, (uint32_t)(batch * 64 * es_m));
-  const auto rg = make_rsrc(g_out, (uint32_t)(batch * 64 * es_g));
+  const auto rm = make_rsrc(m_in, (uint32_t)(batch * N * N * es_m));
+  const auto rg = make_rsrc(g_out, (uint32_t)(batch * N * N * es_g));
   U32x4 mw[2], gw[2];
 #pragma unroll
-  for (int a = 0; a < 2; ++a) mw[a] = buf_load8z(rm, live ? (uint32_t)(e0 + 8 * a) * es_m : kBufOob);
+  for (int a = 0; a < 2; ++a) mw[a] = buf_load8z(rm, live ? (uint32_t)(e0 + N * a) * es_m : kBufOob);
 #pragma unroll
-  for (int a = 0; a < 2; ++a) gw[a] = buf_load8z(rg, live ? (uint32_t)(e0 + 8 * a) * es_g : kBufOob);
+  for (int a = 0; a < 2; ++a) gw[a] = buf_load8z(rg, live ? (uint32_t)(e0 + N * a) * es_g : kBufOob);
   float t[2][2];
 #pragma unroll
   for (int a = 0; a < 2; ++a)
@@ -1570,10 +1573,10 @@ __global__ __launch_bounds__(256) void sinkhorn_bwd_b22_kernel(const void* __res
   float p[2][2];
 #pragma unroll
   for (int a = 0; a < 2; ++a) {
-    const float mx = row_reduce<4, OpMax>(fmaxf(t[a][0], t[a][1]));
+    const float mx = row_reduce<H, OpMax>(fmaxf(t[a][0], t[a][1]));
     p[a][0] = expf(t[a][0] - mx);
     p[a][1] = expf(t[a][1] - mx);
-    const float rs = __builtin_amdgcn_rcpf(row_reduce<4, OpAdd>(p[a][0] + p[a][1]));
+    const float rs = __builtin_amdgcn_rcpf(row_reduce<H, OpAdd>(p[a][0] + p[a][1]));
 #pragma unroll
     for (int b = 0; b < 2; ++b) {
       p[a][b] = mul_nc(p[a][b], rs);
@@ -1588,14 +1591,14 @@ __global__ __launch_bounds__(256) void sinkhorn_bwd_b22_kernel(const void* __res
     if (k > 0) {
 #pragma unroll
       for (int a = 0; a < 2; ++a) {
-        RR[k][a] = __builtin_amdgcn_rcpf(row_reduce<4, OpAdd>(t[a][0] + t[a][1]) + eps);
+        RR[k][a] = __builtin_amdgcn_rcpf(row_reduce<H, OpAdd>(t[a][0] + t[a][1]) + eps);
         t[a][0] = mul_nc(t[a][0], RR[k][a]);
         t[a][1] = mul_nc(t[a][1], RR[k][a]);
       }
     }
 #pragma unroll
     for (int b = 0; b < 2; ++b) {
-      RC[k][b] = __builtin_amdgcn_rcpf(col_sum<4>(t[0][b] + t[1][b]) + eps);
+      RC[k][b] = __builtin_amdgcn_rcpf(col_sum<H>(t[0][b] + t[1][b]) + eps);
       t[0][b] = mul_nc(t[0][b], RC[k][b]);
       t[1][b] = mul_nc(t[1][b], RC[k][b]);
     }
@@ -1614,14 +1617,14 @@ __global__ __launch_bounds__(256) void sinkhorn_bwd_b22_kernel(const void* __res
     // column step k: y = Y[k]
 #pragma unroll
     for (int b = 0; b < 2; ++b) {
-      const float d = col_sum<4>(mul_nc(gr[0][b], Y[k][0][b]) + mul_nc(gr[1][b], Y[k][1][b]));
+      const float d = col_sum<H>(mul_nc(gr[0][b], Y[k][0][b]) + mul_nc(gr[1][b], Y[k][1][b]));
       gr[0][b] = (gr[0][b] - d) * RC[k][b];
       gr[1][b] = (gr[1][b] - d) * RC[k][b];
     }
     if (k > 0) {  // row step k: y = Y[k - 1] * RR[k], as the forward formed it
 #pragma unroll
       for (int a = 0; a < 2; ++a) {
-        const float d = row_reduce<4, OpAdd>(mul_nc(gr[a][0], mul_nc(Y[k - 1][a][0], RR[k][a])) +
+        const float d = row_reduce<H, OpAdd>(mul_nc(gr[a][0], mul_nc(Y[k - 1][a][0], RR[k][a])) +
                                              mul_nc(gr[a][1], mul_nc(Y[k - 1][a][1], RR[k][a])));
         gr[a][0] = (gr[a][0] - d) * RR[k][a];
         gr[a][1] = (gr[a][1] - d) * RR[k][a];
@@ -1631,10 +1634,10 @@ __global__ __launch_bounds__(256) void sinkhorn_bwd_b22_kernel(const void* __res
   // softmax: t0 = p + eps, so the gradient of p is gr
 #pragma unroll
   for (int a = 0; a < 2; ++a) {
-    const float dp = row_reduce<4, OpAdd>(mul_nc(gr[a][0], p[a][0]) + mul_nc(gr[a][1], p[a][1]));
+    const float dp = row_reduce<H, OpAdd>(mul_nc(gr[a][0], p[a][0]) + mul_nc(gr[a][1], p[a][1]));
     if (live) {
 #pragma unroll
-      for (int b = 0; b < 2; ++b) st_any(g_in, e0 + 8 * a + b, gi_dt, p[a][b] * (gr[a][b] - dp));
+      for (int b = 0; b < 2; ++b) st_any(g_in, e0 + N * a + b, gi_dt, p[a][b] * (gr[a][b] - dp));
     }
   }
 }
@@ -1661,18 +1664,13 @@ hipError_t launch_sinkhorn_bwd(const void* m_in, int in_dtype, const void* g_out
   // byte offsets, 4-byte aligned bases.  Anything else takes the kernels below.
   const bool buf_ok = batch * n * n * 4 < (int64_t)kBufOob && ((uintptr_t)m_in & 3) == 0 &&
                       ((uintptr_t)g_out & 3) == 0;
-  if (buf_ok && n == 8 && iters == 20) {  // the reference's default schedule: 16 lanes a matrix
-    const int64_t blocks = (batch * 16 + 255) / 256;
-    hipLaunchKernelGGL((sinkhorn_bwd_b22_kernel<20>), dim3((unsigned)blocks), dim3(256), 0, s, m_in,
-                       in_dtype, g_out, g_dtype, g_in, gi_dtype, batch, eps);
-    return hipGetLastError();
-  }
-  if (buf_ok && (n == 2 || n == 4) && iters == 20) {
-    const int64_t blocks = (batch * n * n + 255) / 256;
-    if (n == 2)
-      hipLaunchKernelGGL((sinkhorn_bwd_regs_kernel<2, 40, true>), dim3((unsigned)blocks), dim3(256), 0, s, m_in, in_dtype, g_out, g_dtype, g_in, gi_dtype, batch, iters, eps);
-    else
-      hipLaunchKernelGGL((sinkhorn_bwd_regs_kernel<4, 40, true>), dim3((unsigned)blocks), dim3(256), 0, s, m_in, in_dtype, g_out, g_dtype, g_in, gi_dtype, batch, iters, eps);
+  if (buf_ok && (n == 2 || n == 4 || n == 8) && iters == 20) {  // the reference's default schedule
+    const int64_t blocks = (batch * (n / 2) * (n / 2) + 255) / 256;  // (n/2)^2 lanes a matrix
+    switch (n) {
+      case 2: hipLaunchKernelGGL((sinkhorn_bwd_b22_kernel<2, 20>), dim3((unsigned)blocks), dim3(256), 0, s, m_in, in_dtype, g_out, g_dtype, g_in, gi_dtype, batch, eps); break;
+      case 4: hipLaunchKernelGGL((sinkhorn_bwd_b22_kernel<4, 20>), dim3((unsigned)blocks), dim3(256), 0, s, m_in, in_dtype, g_out, g_dtype, g_in, gi_dtype, batch, eps); break;
+      default: hipLaunchKernelGGL((sinkhorn_bwd_b22_kernel<8, 20>), dim3((unsigned)blocks), dim3(256), 0, s, m_in, in_dtype, g_out, g_dtype, g_in, gi_dtype, batch, eps); break;
+    }
     return hipGetLastError();
   }
   if (buf_ok && (n == 2 || n == 4 || n == 8) && iters <= 20) {
