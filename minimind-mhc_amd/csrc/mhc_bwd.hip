@@ -1664,13 +1664,19 @@ hipError_t launch_sinkhorn_bwd(const void* m_in, int in_dtype, const void* g_out
   // byte offsets, 4-byte aligned bases.  Anything else takes the kernels below.
   const bool buf_ok = batch * n * n * 4 < (int64_t)kBufOob && ((uintptr_t)m_in & 3) == 0 &&
                       ((uintptr_t)g_out & 3) == 0;
-  if (buf_ok && (n == 2 || n == 4 || n == 8) && iters == 20) {  // the reference's default schedule
+  // The 2 x 2-block kernel at the two schedules in use: 20 iterations (the
+  // models' configs) and 10 (MHCConnection_Fused's default).
+  if (buf_ok && (n == 2 || n == 4 || n == 8) && (iters == 20 || iters == 10)) {
     const int64_t blocks = (batch * (n / 2) * (n / 2) + 255) / 256;  // (n/2)^2 lanes a matrix
-    switch (n) {
-      case 2: hipLaunchKernelGGL((sinkhorn_bwd_b22_kernel<2, 20>), dim3((unsigned)blocks), dim3(256), 0, s, m_in, in_dtype, g_out, g_dtype, g_in, gi_dtype, batch, eps); break;
-      case 4: hipLaunchKernelGGL((sinkhorn_bwd_b22_kernel<4, 20>), dim3((unsigned)blocks), dim3(256), 0, s, m_in, in_dtype, g_out, g_dtype, g_in, gi_dtype, batch, eps); break;
-      default: hipLaunchKernelGGL((sinkhorn_bwd_b22_kernel<8, 20>), dim3((unsigned)blocks), dim3(256), 0, s, m_in, in_dtype, g_out, g_dtype, g_in, gi_dtype, batch, eps); break;
+#define MHC_SK_B22(NN, KK)                                                                      \
+  hipLaunchKernelGGL((sinkhorn_bwd_b22_kernel<NN, KK>), dim3((unsigned)blocks), dim3(256), 0, s, \
+                     m_in, in_dtype, g_out, g_dtype, g_in, gi_dtype, batch, eps)
+    if (iters == 20) {
+      if (n == 2) MHC_SK_B22(2, 20); else if (n == 4) MHC_SK_B22(4, 20); else MHC_SK_B22(8, 20);
+    } else {
+      if (n == 2) MHC_SK_B22(2, 10); else if (n == 4) MHC_SK_B22(4, 10); else MHC_SK_B22(8, 10);
     }
+#undef MHC_SK_B22
     return hipGetLastError();
   }
   if (buf_ok && (n == 2 || n == 4 || n == 8) && iters <= 20) {

@@ -122,19 +122,20 @@ def test_sinkhorn_bwd_iteration_limit(dev):
                           cap + 1, 1e-6)
 
 
-# The 20-iteration kernels (n = 8: 2 x 2 blocks a lane; n = 2, 4: one element
-# a lane) read both inputs through buffer descriptors, one load per tensor and
-# lane, whatever their dtypes; a base that is not 4-byte aligned (a 16-bit
-# view starting one element into its buffer) takes the other kernels.  37
-# matrices: the last workgroup is part-filled.
+# The 10- and 20-iteration kernels (2 x 2 blocks a lane) read both inputs
+# through buffer descriptors, one load per tensor and row pair, whatever their
+# dtypes; a base that is not 4-byte aligned (a 16-bit view starting one
+# element into its buffer) takes the other kernels.  37 matrices: the last
+# workgroup is part-filled.
 @pytest.mark.parametrize("n", [2, 4, 8])
 @pytest.mark.parametrize("in_dt,g_dt,out_dt", [
     (torch.bfloat16, torch.bfloat16, torch.bfloat16), (torch.float16, torch.float32, torch.float32),
     (torch.float32, torch.bfloat16, torch.float32), (torch.bfloat16, torch.float32, torch.float16)])
 @pytest.mark.parametrize("offset", [0, 1])
-def test_sinkhorn_bwd_dtypes_and_offsets(dev, n, in_dt, g_dt, out_dt, offset):
+@pytest.mark.parametrize("iters", [10, 20])
+def test_sinkhorn_bwd_dtypes_and_offsets(dev, n, in_dt, g_dt, out_dt, offset, iters):
     batch = 37
-    g = torch.Generator().manual_seed(100 * n + 10 * offset + int(in_dt == torch.float32))
+    g = torch.Generator().manual_seed(100 * n + 10 * offset + int(in_dt == torch.float32) + iters)
     m = (torch.randn(batch, n, n, generator=g) * 1.5).to(in_dt)
     gy = torch.randn(batch, n, n, generator=g).to(g_dt)
 
@@ -144,11 +145,11 @@ def test_sinkhorn_bwd_dtypes_and_offsets(dev, n, in_dt, g_dt, out_dt, offset):
         v.copy_(t.to(dev))
         return v
 
-    print(f"sinkhorn_bwd n={n} {in_dt} {g_dt} -> {out_dt} offset={offset}", flush=True)
-    got = _ops.sinkhorn_bwd(place(m), place(gy), 20, 1e-6, out_dtype=out_dt)
+    print(f"sinkhorn_bwd n={n} iters={iters} {in_dt} {g_dt} -> {out_dt} offset={offset}", flush=True)
+    got = _ops.sinkhorn_bwd(place(m), place(gy), iters, 1e-6, out_dtype=out_dt)
     torch.cuda.synchronize()
     mr = m.double().requires_grad_(True)
-    R.sinkhorn(mr, 20, 1e-6).backward(gy.double())
+    R.sinkhorn(mr, iters, 1e-6).backward(gy.double())
     assert got.dtype == out_dt
     bar = {torch.float32: 1e-4, torch.float16: 2e-3, torch.bfloat16: 1e-2}[out_dt]
     assert maxrel(mr.grad.float(), got.float()) <= bar
