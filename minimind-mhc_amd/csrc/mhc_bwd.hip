@@ -864,13 +864,23 @@ __global__ __launch_bounds__(256) void weights_reduce_kernel(WeightsArgs a, int 
   const int64_t NC = (int64_t)n * a.C;
   const int64_t q = ((int64_t)blockIdx.x * blockDim.x + threadIdx.x) * (V4 ? 4 : 1);
   if (blockIdx.x + 1 < gridDim.x) {
+    // The three segments' alphas, loaded before the partials with no branch
+    // and converted after the sums: read per element after the sums (a
+    // per-lane alpha pointer, then a per-dtype branch), they were a chain of
+    // round trips at the end of every thread.
+    uint32_t alw[3];
+#pragma unroll
+    for (int k = 0; k < 3; ++k) alw[k] = ld_bits(a.alpha[k], 1, 0, a.param_dtype, a.alpha[k] != nullptr);
+    auto alpha_of = [&](int f) {
+      const int sg = seg_of(f, n);
+      return bits_to_f32(sg == 0 ? alw[0] : (sg == 1 ? alw[1] : alw[2]), a.param_dtype);
+    };
     if (q < NC * FD) {
       if constexpr (V4) {
         const f32x4_t acc = sum_ranges4(a.work + q, NC * FD, R);
         float v[4];
 #pragma unroll
-        for (int e = 0; e < 4; ++e)
-          v[e] = acc[e] * ld_any(a.alpha[seg_of((int)((q + e) % FD), n)], 0, a.param_dtype);
+        for (int e = 0; e < 4; ++e) v[e] = acc[e] * alpha_of((int)((q + e) % FD));
         if (a.phi_dtype == kF32) {
           *reinterpret_cast<f32x4_t*>(static_cast<float*>(a.g_phi) + q) = f32x4_t{v[0], v[1], v[2], v[3]};
         } else {
@@ -885,7 +895,7 @@ __global__ __launch_bounds__(256) void weights_reduce_kernel(WeightsArgs a, int 
       } else {
         const int f = (int)(q % FD);
         const float acc = sum_ranges(a.work + q, NC * FD, R);
-        st_any(a.g_phi, q, a.phi_dtype, acc * ld_any(a.alpha[seg_of(f, n)], 0, a.param_dtype));
+        st_any(a.g_phi, q, a.phi_dtype, acc * alpha_of(f));
       }
     }
   } else {

@@ -186,6 +186,25 @@ __device__ __forceinline__ uint32_t ld_word(const void* p, int64_t count, int64_
   return buf_load4z(make_rsrc(p, bytes), word_off(i, dt)).v[0];
 }
 
+// Bits of element i of a run-time-dtype tensor of `count` elements (0 when
+// !ok or p is null), with no branch: two 2-byte buffer loads, the element's
+// low and high halves for fp32, and for a 16-bit dtype the element and an
+// out-of-range offset (reads zero, touches no memory).  Every byte read lies
+// inside the tensor, and with no per-dtype branch later loads do not wait for
+// these; bits_to_f32 converts where the value is needed.
+__device__ __forceinline__ uint32_t ld_bits(const void* p, int64_t count, int64_t i, int dt, bool ok) {
+  const bool f32 = dt == kF32;
+  const auto r = make_rsrc(p, p ? (uint32_t)count * (f32 ? 4u : 2u) : 0u);
+  const uint32_t lo = ok ? (uint32_t)i * (f32 ? 4u : 2u) : kBufOob;
+  const uint32_t hi = ok && f32 ? (uint32_t)i * 4u + 2u : kBufOob;
+  return (uint32_t)__builtin_amdgcn_raw_buffer_load_b16(r, (int)lo, 0, 0) |
+         ((uint32_t)__builtin_amdgcn_raw_buffer_load_b16(r, (int)hi, 0, 0) << 16);
+}
+__device__ __forceinline__ float bits_to_f32(uint32_t b, int dt) {
+  if (dt == kF32) return __builtin_bit_cast(float, b);
+  return dt == kBF16 ? bf16_bits_to_f32((uint16_t)b) : f16_bits_to_f32((uint16_t)b);
+}
+
 __device__ __forceinline__ void st_any(void* p, int64_t i, int dt, float v) {
   if (dt == kF32) {
     static_cast<float*>(p)[i] = v;
