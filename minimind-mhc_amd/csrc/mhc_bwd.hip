@@ -1074,7 +1074,7 @@ void weights_mfma_kernel(WeightsArgs a, int64_t per) {                       // 
   // Quad fq of token tok (relative to tb; FD % 4 == 0, the launcher keeps
   // (per + 64) * FD * 4 below 2^31, and tokens past te land past the descriptor).
   auto g_quad = [&](bool live, uint32_t tok, int fq) -> U32x4 {
-    return buf_load16(rg, live && 4 * fq < FD ? tok * (uint32_t)FD * 4u + 16u * fq : kBufOob);
+    return buf_load16(rg, oob_unless(live && 4 * fq < FD, tok * (uint32_t)FD * 4u + 16u * fq));
   };
   auto load_step = [&](int64_t t, Step& st) {
 #pragma unroll
@@ -1086,8 +1086,8 @@ void weights_mfma_kernel(WeightsArgs a, int64_t per) {                       // 
       const bool live = fq < QT && t < te;
       st.ga[i] = g_quad(live, ta, fq);
       st.gb[i] = g_quad(live, ta + 1, fq);
-      st.ia[i] = __uint_as_float(__builtin_amdgcn_raw_buffer_load_b32(ri, (int)(live ? 4u * ta : kBufOob), 0, 0));
-      st.ib[i] = __uint_as_float(__builtin_amdgcn_raw_buffer_load_b32(ri, (int)(live ? 4u * ta + 4u : kBufOob), 0, 0));
+      st.ia[i] = __uint_as_float(__builtin_amdgcn_raw_buffer_load_b32(ri, (int)oob_unless(live, 4u * ta), 0, 0));
+      st.ib[i] = __uint_as_float(__builtin_amdgcn_raw_buffer_load_b32(ri, (int)oob_unless(live, 4u * ta + 4u), 0, 0));
     }
   };
   f32x4_t acc[MT][NTF];

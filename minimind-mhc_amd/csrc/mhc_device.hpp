@@ -32,6 +32,14 @@ typedef unsigned int u32x4_t __attribute__((ext_vector_type(4)));
 constexpr int kBufDword3 = 0x00020000;   // raw buffer, gfx9-family dword 3
 constexpr uint32_t kBufOob = 0x7FFFFFF0u; // an offset past any descriptor used here
 
+// ok ? off : kBufOob, as arithmetic.  Written as a ternary on a per-lane
+// condition, the compiler may branch and put the load in both arms; the second
+// arm's load into the same registers then waits for every load in flight.
+__device__ __forceinline__ uint32_t oob_unless(bool ok, uint32_t off) {
+  const uint32_t m = 0u - (uint32_t)ok;
+  return (off & m) | (kBufOob & ~m);
+}
+
 __device__ __forceinline__ __amdgpu_buffer_rsrc_t make_rsrc(const void* base, uint32_t bytes) {
   return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), (short)0, (int)bytes,
                                            kBufDword3);
