@@ -115,8 +115,11 @@ __global__ __launch_bounds__(kGrpWaves * 64) void pre_group_kernel(PreArgs a, in
   // Mixes parked in the sublayer-input rows between the two split launches.
   float* const park = static_cast<float*>(a.sub_in);
   const int64_t park_row = (int64_t)C / 2;  // floats per sublayer-input row
-  // pre_kstream_kernel rotates each tile's block order by (tile % NJ).
-  const int rot = P::KS_ORDER ? (int)((t0 / kKsTileTokens) % NJ) : 0;
+  // pre_kstream_kernel rotates each tile's block order by (tile % NJ), or,
+  // with its chunk pairs (C % 64 == 0), the pair slots by (tile % (NJ / 2)).
+  const bool pairs = P::KS_ORDER && ks_pairs<N, MODE>() && C % 64 == 0;  // uniform
+  const int NJP = NJ / 2;  // pair slots per wave (NJ = C / 32 is even then)
+  const int rot = P::KS_ORDER ? (int)((t0 / kKsTileTokens) % (pairs ? NJP : NJ)) : 0;
 
   const RawParam rp = load_gate_param<N, MODE>(a, tid);
   // Sums of squares handed over by the kernel that wrote x, used where the
@@ -158,9 +161,19 @@ __global__ __launch_bounds__(kGrpWaves * 64) void pre_group_kernel(PreArgs a, in
   // Block b of this wave: stream i, column block cb; false past the row.
   auto block_of = [&](int b, int& i, int& cb) -> bool {
     if constexpr (P::KS_ORDER) {
-      const int jr = b < NJ ? (b + rot < NJ ? b + rot : b + rot - NJ) : b;
-      const int k = wave + kGrpWaves * jr;
-      const bool live = b < NJ && k < NCH;
+      int k;
+      bool live;
+      if (pairs) {  // chunks 2p, 2p + 1 of the rotated pair slots, p = wave + 8 jr
+        const int ps = b >> 1;
+        const int jr = ps < NJP ? (ps + rot < NJP ? ps + rot : ps + rot - NJP) : ps;
+        const int pp = wave + kGrpWaves * jr;
+        k = 2 * pp + (b & 1);
+        live = ps < NJP && 2 * pp < NCH;
+      } else {
+        const int jr = b < NJ ? (b + rot < NJ ? b + rot : b + rot - NJ) : b;
+        k = wave + kGrpWaves * jr;
+        live = b < NJ && k < NCH;
+      }
       i = live ? k / NCB : 0;
       cb = live ? k - i * NCB : 0;
       return live;

@@ -163,12 +163,39 @@ __device__ __forceinline__ float ks_token_sum(float q) {
 // output and the pre-aggregate are fp32 (products rounded, summed in stream
 // order); the pre-aggregate items are 4-column chunks.  No fused norm (a
 // second launch normalises in place).
-template <int N, int MODE, bool NORM, bool F32 = false>
+constexpr bool kKsPairs = true;
+// Chunk pairs where a wave's partials slot (TM x FD fp32) holds its 4 KiB
+// regroup block: n = 8 with the full projection (FD = 80; the no-H_res and
+// head projections, FD = 16 and 8, have 2 and 1 KiB slots).  pre_group_kernel
+// follows the same choice.
+template <int N, int MODE>
+constexpr bool ks_pairs() {
+  if constexpr (N == 8) {
+    using P = KsPlan<N, MODE>;
+    return kKsPairs && P::TM * P::FD * 4 >= P::MB * 16 * 128;
+  } else {
+    return false;
+  }
+}
+
+// PAIRS (bf16, n = 8, full projection, C % 64 == 0): wave kq owns chunk
+// pairs (2p, 2p + 1), p = kq + KS jr, 64 columns of one stream, contiguous in
+// a token's row; each pair's x moves as whole 128-byte row pieces (8 rows x
+// 128 B an instruction) and is regrouped into the MFMA A layout through the
+// wave's own partials slot in LDS (sh.acc[kq], unused until the wave's K loop
+// ends), where the operand layout reads 16 rows x 64 B, half of each line.
+// The chunk order is 2p, 2p + 1 for the pair slots in rotated order;
+// pre_group_kernel walks the same order.  C5 shape (8192 tokens, sums of
+// squares handed over) 48.6 -> 43.3 us; the 64-token n = 8 group projection,
+// which must follow the order, 12.7 -> 13.9 us (one box).  Wave kq taking a
+// contiguous range of pairs instead measured the same at C5, slower at 64.
+template <int N, int MODE, bool NORM, bool F32 = false, bool PAIRS = false>
 __global__ __launch_bounds__(kKsWaves * 64) void pre_kstream_kernel(PreArgs a) {
   using P = KsPlan<N, MODE>;
   using GP = GateParams<N>;
   using NS = KsNorm<N, MODE, NORM>;
   static_assert(!(F32 && NORM), "fp32 streams: the norm runs as a second launch");
+  static_assert(!PAIRS || (!F32 && ks_pairs<N, MODE>() && P::NH == 1), "chunk pairs: bf16, n = 8, full");
   constexpr int FD = P::FD;
   constexpr int NT = P::NT;
   constexpr int NTW = P::NTW;
@@ -195,7 +222,8 @@ __global__ __launch_bounds__(kKsWaves * 64) void pre_kstream_kernel(PreArgs a) {
   const int NC = N * C;
   const int NCB = (C + kCBlock - 1) / kCBlock;
   const int NCH = N * NCB;                      // 32-column chunks in a row
-  const int NJ = (NCH + P::KS - 1) / P::KS;     // chunks per wave (last ones may be empty)
+  const int NJP = (NCH / 2 + P::KS - 1) / P::KS;  // PAIRS: pair slots per wave
+  const int NJ = PAIRS ? 2 * NJP : (NCH + P::KS - 1) / P::KS;  // chunks per wave (last ones may be empty)
   const int64_t M = a.M;
   const int64_t t0 = (int64_t)blockIdx.x * TM;
   const int valid = (int)(M - t0 < TM ? M - t0 : TM);
@@ -253,8 +281,16 @@ __global__ __launch_bounds__(kKsWaves * 64) void pre_kstream_kernel(PreArgs a) {
   // there every workgroup walks the same order, so the CUs of an XCD read each
   // phi line at about the same time and share its L2 fill (652 -> 553 us at
   // 16384 tokens; at n = 8 and at C = 2048 the rotation stays faster).
-  const int rot = N == 16 ? 0 : (int)(blockIdx.x % (unsigned)NJ);
+  const int NR = PAIRS ? NJP : NJ;  // slots the rotation turns (pair slots with PAIRS)
+  const int rot = N == 16 ? 0 : (int)(blockIdx.x % (unsigned)NR);
   auto chunk_of = [&](int slot_j, bool& live) {
+    if constexpr (PAIRS) {  // chunk slot_j of the sequence 2p, 2p + 1 over the rotated pair slots
+      const int ps = slot_j >> 1;
+      const int jr = ps < NJP ? (ps + rot < NJP ? ps + rot : ps + rot - NJP) : ps;
+      const int pp = kq + P::KS * jr;  // uniform
+      live = ps < NJP && 2 * pp < NCH;
+      return 2 * pp + (slot_j & 1);
+    }
     const int jr = slot_j < NJ ? (slot_j + rot < NJ ? slot_j + rot : slot_j + rot - NJ) : slot_j;
     const int k = kq + P::KS * jr;  // uniform
     live = slot_j < NJ && k < NCH;
@@ -275,8 +311,42 @@ __global__ __launch_bounds__(kKsWaves * 64) void pre_kstream_kernel(PreArgs a) {
                                                 rw, voff, (int)(wimg + (uint32_t)(k * NT + ntg) * 1024u), 0));
     }
   };
+  // PAIRS: pair slot ps loads both chunks' phi operands and, per M-block,
+  // the pair's 16 rows x 128 bytes as two instructions (lane: row l / 8 of 8,
+  // 16-byte piece l % 8).
+  constexpr int DP = 2;  // pairs in flight
+  U32x4 xp[PAIRS ? DP : 1][PAIRS ? P::MB : 1][2];
+  U32x4 wp[PAIRS ? DP : 1][2][PAIRS ? NTW : 1];
+  auto issue_pair = [&](int ps, U32x4 (&xd)[PAIRS ? P::MB : 1][2], U32x4 (&wd)[2][PAIRS ? NTW : 1]) {
+    bool live;
+    const int k = chunk_of(2 * ps, live);  // the pair's first chunk
+    const int i = live ? k / NCB : 0;
+    const int c0 = live ? (k - i * NCB) * kCBlock : 0;
 #pragma unroll
-  for (int d = 0; d < D; ++d) issue(d, xs[d], ws[d], wl[F32 ? d : 0]);
+    for (int m = 0; m < (PAIRS ? P::MB : 1); ++m)
+#pragma unroll
+      for (int u = 0; u < 2; ++u)
+        xd[m][u] = __builtin_bit_cast(U32x4, __builtin_amdgcn_raw_buffer_load_b128(
+                                                 rx,
+                                                 (int)(live ? (uint32_t)((16 * m + 8 * u + (lane >> 3)) * NC) * ES +
+                                                                  16u * (lane & 7)
+                                                            : kBufOob),
+                                                 (int)((i * C + c0) * ES), 0));
+#pragma unroll
+    for (int h = 0; h < 2; ++h)
+#pragma unroll
+      for (int nt = 0; nt < (PAIRS ? NTW : 1); ++nt)
+        wd[h][nt] = __builtin_bit_cast(U32x4, __builtin_amdgcn_raw_buffer_load_b128(
+                                                  rw, (int)(live ? (uint32_t)lane * 16u : kBufOob),
+                                                  ((k + h) * NT + nt) * 1024, 0));
+  };
+  if constexpr (PAIRS) {
+#pragma unroll
+    for (int d = 0; d < DP; ++d) issue_pair(d, xp[d], wp[d]);
+  } else {
+#pragma unroll
+    for (int d = 0; d < D; ++d) issue(d, xs[d], ws[d], wl[F32 ? d : 0]);
+  }
 
   // ---- sums of squares, then each row's inv_rms --------------------------------
   // A first pass over this wave's chunks in the K loop's order (SD in flight;
@@ -341,7 +411,38 @@ __global__ __launch_bounds__(kKsWaves * 64) void pre_kstream_kernel(PreArgs a) {
   for (int m = 0; m < P::MB; ++m)
 #pragma unroll
     for (int nt = 0; nt < NTW; ++nt) acc[m][nt] = f32x4_t{0.f, 0.f, 0.f, 0.f};
-  for (int j0 = 0; j0 < NJ; j0 += D) {   // uniform trip count
+  if constexpr (PAIRS) {
+    // the wave's regroup block, [M-block][row 16][16-byte slot 8], slots
+    // swizzled by the row's low bits (conflict-free both ways)
+    U32x4* const rsb = reinterpret_cast<U32x4*>(&sh.acc[kq][0][0]);
+    for (int j0 = 0; j0 < NJP; j0 += DP) {  // uniform trip count
+#pragma unroll
+      for (int d = 0; d < DP; ++d) {
+#pragma unroll
+        for (int m = 0; m < P::MB; ++m)
+#pragma unroll
+          for (int u = 0; u < 2; ++u) {
+            const int rr = 8 * u + (lane >> 3);
+            rsb[(m * 16 + rr) * 8 + ((lane & 7) ^ (rr & 7))] = xp[d][m][u];
+          }
+        __builtin_amdgcn_fence(__ATOMIC_ACQ_REL, "wavefront");
+#pragma unroll
+        for (int h = 0; h < 2; ++h)
+#pragma unroll
+          for (int m = 0; m < P::MB; ++m) {
+            const U32x4 xv = rsb[(m * 16 + r) * 8 + ((4 * h + g) ^ (r & 7))];
+            const bf16x8_t av = __builtin_bit_cast(bf16x8_t, x_norm_chunk(xv, inv_r[m]));
+#pragma unroll
+            for (int nt = 0; nt < NTW; ++nt)
+              acc[m][nt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(
+                  av, __builtin_bit_cast(bf16x8_t, wp[d][h][nt]), acc[m][nt], 0, 0, 0);
+          }
+        __builtin_amdgcn_fence(__ATOMIC_ACQ_REL, "wavefront");
+        issue_pair(j0 + d + DP, xp[d], wp[d]);
+      }
+    }
+  }
+  for (int j0 = 0; !PAIRS && j0 < NJ; j0 += D) {   // uniform trip count
 #pragma unroll
     for (int d = 0; d < D; ++d) {
 #pragma unroll
@@ -607,19 +708,38 @@ hipError_t launch_pre_kstream_inst(const PreArgs& a, hipStream_t s) {
     }
     return hipErrorInvalidValue;
   }
+  // chunk pairs where a pair's 64 columns lie in one stream (C % 64 == 0)
+  const bool pairs = ks_pairs<N, MODE>() && a.C % 64 == 0;
   if (!a.norm_w) {
+    if constexpr (ks_pairs<N, MODE>()) {
+      if (pairs) {
+        hipLaunchKernelGGL((pre_kstream_kernel<N, MODE, false, false, true>), dim3((unsigned)tiles), block, 0, s, a);
+        return hipGetLastError();
+      }
+    }
     hipLaunchKernelGGL((pre_kstream_kernel<N, MODE, false>), dim3((unsigned)tiles), block, 0, s, a);
     return hipGetLastError();
   }
   if constexpr (ks_norm_fits<N, MODE>()) {
     if (a.C <= kKsNormMaxC) {
+      if constexpr (ks_pairs<N, MODE>()) {
+        if (pairs) {
+          hipLaunchKernelGGL((pre_kstream_kernel<N, MODE, true, false, true>), dim3((unsigned)tiles), block, 0, s, a);
+          return hipGetLastError();
+        }
+      }
       hipLaunchKernelGGL((pre_kstream_kernel<N, MODE, true>), dim3((unsigned)tiles), block, 0, s, a);
       return hipGetLastError();
     }
   }
   PreArgs plain = a;
   plain.norm_w = nullptr;
-  hipLaunchKernelGGL((pre_kstream_kernel<N, MODE, false>), dim3((unsigned)tiles), block, 0, s, plain);
+  if constexpr (ks_pairs<N, MODE>()) {
+    if (pairs) hipLaunchKernelGGL((pre_kstream_kernel<N, MODE, false, false, true>), dim3((unsigned)tiles), block, 0, s, plain);
+    else hipLaunchKernelGGL((pre_kstream_kernel<N, MODE, false>), dim3((unsigned)tiles), block, 0, s, plain);
+  } else {
+    hipLaunchKernelGGL((pre_kstream_kernel<N, MODE, false>), dim3((unsigned)tiles), block, 0, s, plain);
+  }
   const hipError_t e = hipGetLastError();
   if (e != hipSuccess) return e;
   return launch_expand_norm(a.sub_in, kBF16, a.norm_w, a.norm_dtype, a.sub_in, a.M, 1, a.C, a.norm_eps, s);
