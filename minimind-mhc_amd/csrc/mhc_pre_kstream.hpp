@@ -296,10 +296,35 @@ __global__ __launch_bounds__(kKsWaves * 64) void pre_kstream_kernel(PreArgs a) {
     live = slot_j < NJ && k < NCH;
     return k;
   };
+  // XROWS (fp32, n = 8, full projection): a chunk's 32 fp32 columns are one
+  // 128-byte line of each row, loaded as whole lines (8 rows x 128 B an
+  // instruction, XQ = 2 per M-block: lane row l / 8, 16-byte piece l % 8) and
+  // regrouped into the operand layout through the wave's partials slot
+  // (sh.acc[kq]), as the bf16 chunk pairs do; the operand layout's two loads
+  // each read 16 rows x 64 B, half of every line.  The chunks, their order
+  // and the MFMA inputs are unchanged.  fp32 C5 shape 107.4-109.3 -> 102.0-
+  // 102.2 us (one box).
+  constexpr bool XROWS = F32 && ks_pairs<N, MODE>() && XQ == 2;
+  auto x_rows = [&](int k, bool live, U32x4 (&xd)[P::MB][XQ]) {
+    const int i = live ? k / NCB : 0;
+    const int c0 = live ? (k - i * NCB) * kCBlock : 0;
+    const bool xl = live && c0 + 4 * (lane & 7) < C;
+#pragma unroll
+    for (int m = 0; m < P::MB; ++m)
+#pragma unroll
+      for (int u = 0; u < XQ; ++u)
+        xd[m][u] = __builtin_bit_cast(U32x4, __builtin_amdgcn_raw_buffer_load_b128(
+                                                 rx,
+                                                 (int)(xl ? (uint32_t)((16 * m + 8 * u + (lane >> 3)) * NC) * ES +
+                                                                16u * (lane & 7)
+                                                          : kBufOob),
+                                                 (int)((i * C + c0) * ES), 0));
+  };
   auto issue = [&](int slot_j, U32x4 (&xd)[P::MB][XQ], U32x4 (&wd)[NTW], U32x4 (&wdl)[NTW]) {
     bool live;
     const int k = chunk_of(slot_j, live);
-    x_chunk(k, live, xd);
+    if constexpr (XROWS) x_rows(k, live, xd);
+    else x_chunk(k, live, xd);
 #pragma unroll
     for (int nt = 0; nt < NTW; ++nt) {
       const int ntg = nh * NTW + nt;
@@ -445,6 +470,20 @@ __global__ __launch_bounds__(kKsWaves * 64) void pre_kstream_kernel(PreArgs a) {
   for (int j0 = 0; !PAIRS && j0 < NJ; j0 += D) {   // uniform trip count
 #pragma unroll
     for (int d = 0; d < D; ++d) {
+      if constexpr (XROWS) {  // regroup the chunk's rows into the operand layout, in place
+        U32x4* const rsb = reinterpret_cast<U32x4*>(&sh.acc[kq][0][0]);
+#pragma unroll
+        for (int m = 0; m < P::MB; ++m)
+#pragma unroll
+          for (int u = 0; u < XQ; ++u)
+            rsb[(m * 16 + 8 * u + (lane >> 3)) * 8 + ((lane & 7) ^ ((lane >> 3) & 7))] = xs[d][m][u];
+        __builtin_amdgcn_fence(__ATOMIC_ACQ_REL, "wavefront");
+#pragma unroll
+        for (int m = 0; m < P::MB; ++m)
+#pragma unroll
+          for (int q = 0; q < XQ; ++q) xs[d][m][q] = rsb[(m * 16 + r) * 8 + ((2 * g + q) ^ (r & 7))];
+        __builtin_amdgcn_fence(__ATOMIC_ACQ_REL, "wavefront");
+      }
 #pragma unroll
       for (int m = 0; m < P::MB; ++m) {
         if constexpr (F32) {  // fp32 x_norm split into hi + lo bf16 operands
