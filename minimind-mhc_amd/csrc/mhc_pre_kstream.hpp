@@ -342,7 +342,7 @@ __global__ __launch_bounds__(kKsWaves * 64) void pre_kstream_kernel(PreArgs a) {
   constexpr int DP = 2;  // pairs in flight
   U32x4 xp[PAIRS ? DP : 1][PAIRS ? P::MB : 1][2];
   U32x4 wp[PAIRS ? DP : 1][2][PAIRS ? NTW : 1];
-  auto issue_pair = [&](int ps, U32x4 (&xd)[PAIRS ? P::MB : 1][2], U32x4 (&wd)[2][PAIRS ? NTW : 1]) {
+  auto load_pair_x = [&](int ps, U32x4 (&xd)[PAIRS ? P::MB : 1][2]) {
     bool live;
     const int k = chunk_of(2 * ps, live);  // the pair's first chunk
     const int i = live ? k / NCB : 0;
@@ -357,6 +357,29 @@ __global__ __launch_bounds__(kKsWaves * 64) void pre_kstream_kernel(PreArgs a) {
                                                                   16u * (lane & 7)
                                                             : kBufOob),
                                                  (int)((i * C + c0) * ES), 0));
+  };
+  // The pair's rows into the wave's regroup block, and back in the operand
+  // layout: chunk h of M-block m for this lane (row r, columns 8g .. + 7).
+  auto pair_regroup = [&](const U32x4 (&xd)[PAIRS ? P::MB : 1][2], U32x4 (&ov)[2][PAIRS ? P::MB : 1]) {
+    U32x4* const rsb = reinterpret_cast<U32x4*>(&sh.acc[kq][0][0]);
+#pragma unroll
+    for (int m = 0; m < (PAIRS ? P::MB : 1); ++m)
+#pragma unroll
+      for (int u = 0; u < 2; ++u) {
+        const int rr = 8 * u + (lane >> 3);
+        rsb[(m * 16 + rr) * 8 + ((lane & 7) ^ (rr & 7))] = xd[m][u];
+      }
+    __builtin_amdgcn_fence(__ATOMIC_ACQ_REL, "wavefront");
+#pragma unroll
+    for (int h = 0; h < 2; ++h)
+#pragma unroll
+      for (int m = 0; m < (PAIRS ? P::MB : 1); ++m) ov[h][m] = rsb[(m * 16 + r) * 8 + ((4 * h + g) ^ (r & 7))];
+    __builtin_amdgcn_fence(__ATOMIC_ACQ_REL, "wavefront");
+  };
+  auto issue_pair = [&](int ps, U32x4 (&xd)[PAIRS ? P::MB : 1][2], U32x4 (&wd)[2][PAIRS ? NTW : 1]) {
+    bool live;
+    const int k = chunk_of(2 * ps, live);  // the pair's first chunk
+    load_pair_x(ps, xd);
 #pragma unroll
     for (int h = 0; h < 2; ++h)
 #pragma unroll
@@ -388,6 +411,29 @@ __global__ __launch_bounds__(kKsWaves * 64) void pre_kstream_kernel(PreArgs a) {
     if (given) {  // uniform: the totals in slot 0, the other K-split slots zero
       if (tid < TM) sh.ss[0][tid] = ss_given;
       else if (tid < P::KS * TM) sh.ss[tid / TM][tid % TM] = 0.f;
+    } else if constexpr (PAIRS) {  // the same chains, the pairs' x as row pieces (pair_regroup)
+      for (int j0 = 0; j0 < NJP; j0 += P::SD / 2) {  // uniform trip count
+        U32x4 xv[P::SD / 2][PAIRS ? P::MB : 1][2];
+#pragma unroll
+        for (int e = 0; e < P::SD / 2; ++e) load_pair_x(j0 + e, xv[e]);
+#pragma unroll
+        for (int e = 0; e < P::SD / 2; ++e) {
+          U32x4 ov[2][PAIRS ? P::MB : 1];
+          pair_regroup(xv[e], ov);
+#pragma unroll
+          for (int h = 0; h < 2; ++h)
+#pragma unroll
+            for (int m = 0; m < P::MB; ++m)
+#pragma unroll
+              for (int q = 0; q < 4; ++q) ss[m] = dot2_bf16(ov[h][m].v[q], ov[h][m].v[q], ss[m]);
+        }
+      }
+#pragma unroll
+      for (int m = 0; m < P::MB; ++m) {
+        ss[m] += __shfl_xor(ss[m], 16, 64);
+        ss[m] += __shfl_xor(ss[m], 32, 64);
+        if (g == 0) sh.ss[kq][m * 16 + r] = ss[m];
+      }
     } else if (P::NH == 1 || nh == 0) {  // uniform
       for (int j0 = 0; j0 < NJ; j0 += P::SD) {  // uniform trip count
         U32x4 v[P::SD][P::MB][XQ];
@@ -438,31 +484,22 @@ __global__ __launch_bounds__(kKsWaves * 64) void pre_kstream_kernel(PreArgs a) {
     for (int nt = 0; nt < NTW; ++nt) acc[m][nt] = f32x4_t{0.f, 0.f, 0.f, 0.f};
   if constexpr (PAIRS) {
     // the wave's regroup block, [M-block][row 16][16-byte slot 8], slots
-    // swizzled by the row's low bits (conflict-free both ways)
-    U32x4* const rsb = reinterpret_cast<U32x4*>(&sh.acc[kq][0][0]);
+    // swizzled by the row's low bits (conflict-free both ways): pair_regroup
     for (int j0 = 0; j0 < NJP; j0 += DP) {  // uniform trip count
 #pragma unroll
       for (int d = 0; d < DP; ++d) {
-#pragma unroll
-        for (int m = 0; m < P::MB; ++m)
-#pragma unroll
-          for (int u = 0; u < 2; ++u) {
-            const int rr = 8 * u + (lane >> 3);
-            rsb[(m * 16 + rr) * 8 + ((lane & 7) ^ (rr & 7))] = xp[d][m][u];
-          }
-        __builtin_amdgcn_fence(__ATOMIC_ACQ_REL, "wavefront");
+        U32x4 ov[2][P::MB];
+        pair_regroup(xp[d], ov);
 #pragma unroll
         for (int h = 0; h < 2; ++h)
 #pragma unroll
           for (int m = 0; m < P::MB; ++m) {
-            const U32x4 xv = rsb[(m * 16 + r) * 8 + ((4 * h + g) ^ (r & 7))];
-            const bf16x8_t av = __builtin_bit_cast(bf16x8_t, x_norm_chunk(xv, inv_r[m]));
+            const bf16x8_t av = __builtin_bit_cast(bf16x8_t, x_norm_chunk(ov[h][m], inv_r[m]));
 #pragma unroll
             for (int nt = 0; nt < NTW; ++nt)
               acc[m][nt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(
                   av, __builtin_bit_cast(bf16x8_t, wp[d][h][nt]), acc[m][nt], 0, 0, 0);
           }
-        __builtin_amdgcn_fence(__ATOMIC_ACQ_REL, "wavefront");
         issue_pair(j0 + d + DP, xp[d], wp[d]);
       }
     }
