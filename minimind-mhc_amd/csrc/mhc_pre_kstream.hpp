@@ -320,6 +320,22 @@ __global__ __launch_bounds__(kKsWaves * 64) void pre_kstream_kernel(PreArgs a) {
                                                           : kBufOob),
                                                  (int)((i * C + c0) * ES), 0));
   };
+  // XROWS: a chunk's rows into the wave's regroup block and back, in place,
+  // in the operand layout (xq: 16-byte piece 2g + xq of row r).
+  auto rows_regroup = [&](U32x4 (&xd)[P::MB][XQ]) {
+    U32x4* const rsb = reinterpret_cast<U32x4*>(&sh.acc[kq][0][0]);
+#pragma unroll
+    for (int m = 0; m < P::MB; ++m)
+#pragma unroll
+      for (int u = 0; u < XQ; ++u)
+        rsb[(m * 16 + 8 * u + (lane >> 3)) * 8 + ((lane & 7) ^ ((lane >> 3) & 7))] = xd[m][u];
+    __builtin_amdgcn_fence(__ATOMIC_ACQ_REL, "wavefront");
+#pragma unroll
+    for (int m = 0; m < P::MB; ++m)
+#pragma unroll
+      for (int q = 0; q < XQ; ++q) xd[m][q] = rsb[(m * 16 + r) * 8 + ((2 * g + q) ^ (r & 7))];
+    __builtin_amdgcn_fence(__ATOMIC_ACQ_REL, "wavefront");
+  };
   auto issue = [&](int slot_j, U32x4 (&xd)[P::MB][XQ], U32x4 (&wd)[NTW], U32x4 (&wdl)[NTW]) {
     bool live;
     const int k = chunk_of(slot_j, live);
@@ -441,7 +457,12 @@ __global__ __launch_bounds__(kKsWaves * 64) void pre_kstream_kernel(PreArgs a) {
         for (int d = 0; d < P::SD; ++d) {
           bool live;
           const int k = chunk_of(j0 + d, live);
-          x_chunk(k, live, v[d]);
+          if constexpr (XROWS) x_rows(k, live, v[d]);
+          else x_chunk(k, live, v[d]);
+        }
+        if constexpr (XROWS) {
+#pragma unroll
+          for (int d = 0; d < P::SD; ++d) rows_regroup(v[d]);
         }
 #pragma unroll
         for (int d = 0; d < P::SD; ++d)
@@ -507,20 +528,7 @@ __global__ __launch_bounds__(kKsWaves * 64) void pre_kstream_kernel(PreArgs a) {
   for (int j0 = 0; !PAIRS && j0 < NJ; j0 += D) {   // uniform trip count
 #pragma unroll
     for (int d = 0; d < D; ++d) {
-      if constexpr (XROWS) {  // regroup the chunk's rows into the operand layout, in place
-        U32x4* const rsb = reinterpret_cast<U32x4*>(&sh.acc[kq][0][0]);
-#pragma unroll
-        for (int m = 0; m < P::MB; ++m)
-#pragma unroll
-          for (int u = 0; u < XQ; ++u)
-            rsb[(m * 16 + 8 * u + (lane >> 3)) * 8 + ((lane & 7) ^ ((lane >> 3) & 7))] = xs[d][m][u];
-        __builtin_amdgcn_fence(__ATOMIC_ACQ_REL, "wavefront");
-#pragma unroll
-        for (int m = 0; m < P::MB; ++m)
-#pragma unroll
-          for (int q = 0; q < XQ; ++q) xs[d][m][q] = rsb[(m * 16 + r) * 8 + ((2 * g + q) ^ (r & 7))];
-        __builtin_amdgcn_fence(__ATOMIC_ACQ_REL, "wavefront");
-      }
+      if constexpr (XROWS) rows_regroup(xs[d]);  // the chunk's rows into the operand layout
 #pragma unroll
       for (int m = 0; m < P::MB; ++m) {
         if constexpr (F32) {  // fp32 x_norm split into hi + lo bf16 operands
