@@ -164,26 +164,34 @@ __device__ __forceinline__ float ks_token_sum(float q) {
 // order); the pre-aggregate items are 4-column chunks.  No fused norm (a
 // second launch normalises in place).
 constexpr bool kKsPairs = true;
-// Chunk pairs where a wave's partials slot (TM x FD fp32) holds its 4 KiB
-// regroup block: n = 8 with the full projection (FD = 80; the no-H_res and
-// head projections, FD = 16 and 8, have 2 and 1 KiB slots).  pre_group_kernel
-// follows the same choice.
+// Chunk pairs (and fp32 whole-line x) at n in {2, 4, 8}; n = 16 splits the
+// output tiles over two wave halves (several waves a K-split slot).
+// pre_group_kernel follows the same chunk order at n = 8 (n <= 4 at
+// C > 1024, the only n <= 4 shapes this kernel serves, have no group form).
 template <int N, int MODE>
 constexpr bool ks_pairs() {
-  if constexpr (N == 8) {
+  return kKsPairs && (N == 2 || N == 4 || N == 8);
+}
+// The wave's 4 KiB regroup block: its own partials slot (TM x FD fp32) where
+// that is large enough (n = 8, full projection), else an LDS block of its own.
+template <int N, int MODE>
+constexpr bool ks_regroup_in_slot() {
+  if constexpr (N == 2 || N == 4 || N == 8) {
     using P = KsPlan<N, MODE>;
-    return kKsPairs && P::TM * P::FD * 4 >= P::MB * 16 * 128;
+    return P::TM * P::FD * 4 >= P::MB * 16 * 128;
   } else {
     return false;
   }
 }
 
-// PAIRS (bf16, n = 8, full projection, C % 64 == 0): wave kq owns chunk
-// pairs (2p, 2p + 1), p = kq + KS jr, 64 columns of one stream, contiguous in
-// a token's row; each pair's x moves as whole 128-byte row pieces (8 rows x
-// 128 B an instruction) and is regrouped into the MFMA A layout through the
-// wave's own partials slot in LDS (sh.acc[kq], unused until the wave's K loop
-// ends), where the operand layout reads 16 rows x 64 B, half of each line.
+// PAIRS (bf16, n in {2, 4, 8}, C % 64 == 0): wave kq owns chunk pairs
+// (2p, 2p + 1), p = kq + KS jr, 64 columns of one stream, contiguous in a
+// token's row; each pair's x moves as whole 128-byte row pieces (8 rows x
+// 128 B an instruction) and is regrouped into the MFMA A layout through a
+// 4 KiB LDS block of the wave (its own partials slot sh.acc[kq], unused until
+// the wave's K loop ends, at n = 8 with the full projection; else the norm
+// stash or LDS of its own), where the operand layout reads 16 rows x 64 B,
+// half of each line.
 // The chunk order is 2p, 2p + 1 for the pair slots in rotated order;
 // pre_group_kernel walks the same order.  C5 shape (8192 tokens, sums of
 // squares handed over) 48.6 -> 43.3 us; the 64-token n = 8 group projection,
@@ -195,7 +203,7 @@ __global__ __launch_bounds__(kKsWaves * 64) void pre_kstream_kernel(PreArgs a) {
   using GP = GateParams<N>;
   using NS = KsNorm<N, MODE, NORM>;
   static_assert(!(F32 && NORM), "fp32 streams: the norm runs as a second launch");
-  static_assert(!PAIRS || (!F32 && ks_pairs<N, MODE>() && P::NH == 1), "chunk pairs: bf16, n = 8, full");
+  static_assert(!PAIRS || (!F32 && ks_pairs<N, MODE>() && P::NH == 1), "chunk pairs: bf16, n in {2, 4, 8}");
   constexpr int FD = P::FD;
   constexpr int NT = P::NT;
   constexpr int NTW = P::NTW;
@@ -210,6 +218,14 @@ __global__ __launch_bounds__(kKsWaves * 64) void pre_kstream_kernel(PreArgs a) {
   static_assert(sizeof(KsShared<N, MODE>) + sizeof(NS) <= kLdsBytes, "LDS budget");
   __shared__ KsShared<N, MODE> sh;
   __shared__ NS nsh;
+  // Regroup blocks (4 KiB a wave) of the chunk pairs / whole-line fp32 x where
+  // the partials slots are too small: the norm stash when there is one (it is
+  // first written after the barrier that follows every wave's K loop), else
+  // LDS of their own.
+  constexpr bool kRgOut = (PAIRS || (F32 && N == 8)) && !ks_regroup_in_slot<N, MODE>();
+  constexpr bool kRgOwn = kRgOut && !NORM;
+  __shared__ __attribute__((aligned(16))) U32x4 s_rg[kRgOwn ? P::WAVES * P::MB * 128 : 1];
+  static_assert(sizeof(KsShared<N, MODE>) + sizeof(NS) + sizeof(s_rg) <= kLdsBytes, "LDS budget (regroup)");
 
   const int tid = threadIdx.x;
   const int lane = tid & 63;
@@ -296,15 +312,24 @@ __global__ __launch_bounds__(kKsWaves * 64) void pre_kstream_kernel(PreArgs a) {
     live = slot_j < NJ && k < NCH;
     return k;
   };
-  // XROWS (fp32, n = 8, full projection): a chunk's 32 fp32 columns are one
+  auto rg_block = [&]() -> U32x4* {
+    if constexpr (kRgOwn) return &s_rg[wave * P::MB * 128];
+    else if constexpr (kRgOut) {
+      static_assert(!NORM || sizeof(nsh.stash) >= sizeof(U32x4) * P::WAVES * P::MB * 128, "regroup blocks in the stash");
+      return &nsh.stash[wave * P::MB * 128];
+    } else {
+      return reinterpret_cast<U32x4*>(&sh.acc[kq][0][0]);
+    }
+  };
+  // XROWS (fp32, n = 8): a chunk's 32 fp32 columns are one
   // 128-byte line of each row, loaded as whole lines (8 rows x 128 B an
   // instruction, XQ = 2 per M-block: lane row l / 8, 16-byte piece l % 8) and
-  // regrouped into the operand layout through the wave's partials slot
-  // (sh.acc[kq]), as the bf16 chunk pairs do; the operand layout's two loads
+  // regrouped into the operand layout through the wave's regroup block, as
+  // the bf16 chunk pairs are; the operand layout's two loads
   // each read 16 rows x 64 B, half of every line.  The chunks, their order
   // and the MFMA inputs are unchanged.  fp32 C5 shape 107.4-109.3 -> 102.0-
   // 102.2 us (one box).
-  constexpr bool XROWS = F32 && ks_pairs<N, MODE>() && XQ == 2;
+  constexpr bool XROWS = F32 && N == 8 && XQ == 2;  // n <= 4: 8 more VGPRs, one workgroup a CU fewer
   auto x_rows = [&](int k, bool live, U32x4 (&xd)[P::MB][XQ]) {
     const int i = live ? k / NCB : 0;
     const int c0 = live ? (k - i * NCB) * kCBlock : 0;
@@ -323,7 +348,7 @@ __global__ __launch_bounds__(kKsWaves * 64) void pre_kstream_kernel(PreArgs a) {
   // XROWS: a chunk's rows into the wave's regroup block and back, in place,
   // in the operand layout (xq: 16-byte piece 2g + xq of row r).
   auto rows_regroup = [&](U32x4 (&xd)[P::MB][XQ]) {
-    U32x4* const rsb = reinterpret_cast<U32x4*>(&sh.acc[kq][0][0]);
+    U32x4* const rsb = rg_block();
 #pragma unroll
     for (int m = 0; m < P::MB; ++m)
 #pragma unroll
@@ -377,7 +402,7 @@ __global__ __launch_bounds__(kKsWaves * 64) void pre_kstream_kernel(PreArgs a) {
   // The pair's rows into the wave's regroup block, and back in the operand
   // layout: chunk h of M-block m for this lane (row r, columns 8g .. + 7).
   auto pair_regroup = [&](const U32x4 (&xd)[PAIRS ? P::MB : 1][2], U32x4 (&ov)[2][PAIRS ? P::MB : 1]) {
-    U32x4* const rsb = reinterpret_cast<U32x4*>(&sh.acc[kq][0][0]);
+    U32x4* const rsb = rg_block();
 #pragma unroll
     for (int m = 0; m < (PAIRS ? P::MB : 1); ++m)
 #pragma unroll
