@@ -79,9 +79,10 @@ def _both(threshold, kind, n, C, M, seed, use_norm=False, iters=20):
 
 @pytest.mark.parametrize("kind", ["full", "nohres", "head"])
 @pytest.mark.parametrize("n,C", [(4, 768), (8, 768), (2, 768), (1, 768), (4, 256), (2, 1024),
-                                 (8, 512)])
+                                 (8, 512), (8, 520)])
 @pytest.mark.parametrize("M", [1, 37, 300, 1100])
 def test_group_matches_large_batch_kernel(threshold, kind, n, C, M):
+    # n = 8: C % 64 == 0 walks chunk pairs in both kernels, C = 520 single chunks
     if kind == "head" and n == 1:
         pytest.skip("MHCHead with n = 1 is an RMSNorm (no projection)")
     _both(threshold, kind, n, C, M, seed=100 * n + C + M)

@@ -84,11 +84,14 @@ def test_pre_mfma_matches_generic(dev, n, C):
 
 @pytest.mark.parametrize("n,C,M", [(4, 768, 4096), (2, 512, 4096), (4, 768, 20000),
                                    (8, 768, 8192), (8, 768, 8200), (4, 2048, 2100),
-                                   (2, 1536, 4100), (16, 256, 3000), (16, 768, 1030)])
+                                   (2, 1536, 4100), (16, 256, 3000), (16, 768, 1030),
+                                   (4, 1064, 2100), (2, 1032, 4100), (8, 520, 4100)])
 def test_pre_mfma_many_workgroups_repeat(dev, n, C, M):
     """Every CU busy, one or more tiles per workgroup, several launches: the
     persistent kernel's output must equal the generic kernel's within bf16
-    rounding on every launch and be bit-identical between launches.  (A store
+    rounding on every launch and be bit-identical between launches.  C % 64 != 0
+    (1064, 1032, 520) keeps the K-streamed kernel on single 32-column chunks
+    instead of chunk pairs.  (A store
     whose data registers were overwritten before the store read them left
     zeros in a few lanes only under this kind of load.)"""
     print(f"many workgroups n={n} C={C} M={M}", flush=True)
